@@ -1,0 +1,273 @@
+"""ctypes bindings for the CPU oracle and the reference build (test infrastructure).
+
+Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg import
+this package; the product (hikoboshi_amd) never does.
+
+- ``Oracle``: oracle/liboracle.so, the plain-C restatement (pmpnn_oracle.c).
+- ``Reference``: oracle/_ref/libhkbs_ref.so, the reference's own sources built
+  by oracle/ref.mk (present only when it was built where the reference
+  checkout exists; the file then travels with the tree).
+"""
+from __future__ import annotations
+
+import ctypes as C
+from pathlib import Path
+
+import numpy as np
+
+HERE = Path(__file__).resolve().parent
+ORACLE_SO = HERE / "liboracle.so"
+REF_SO = HERE / "_ref" / "libhkbs_ref.so"
+V = 21
+H = 128
+
+_f32p = C.POINTER(C.c_float)
+_i32p = C.POINTER(C.c_int32)
+_u8p = C.POINTER(C.c_uint8)
+_f64p = C.POINTER(C.c_double)
+
+
+def _p(a, ctype):
+    if a is None:
+        return None
+    return a.ctypes.data_as(ctype)
+
+
+def _f32(a):
+    return None if a is None else np.ascontiguousarray(a, dtype=np.float32)
+
+
+def _i32(a):
+    return None if a is None else np.ascontiguousarray(a, dtype=np.int32)
+
+
+def _u8(a):
+    return None if a is None else np.ascontiguousarray(a, dtype=np.uint8)
+
+
+def k_of(L: int) -> int:
+    return min(48, L)
+
+
+class _TensorTable:
+    def __init__(self, tensors):
+        self.keep = [np.ascontiguousarray(t, dtype=np.float32) for t in tensors]
+        self.table = (C.POINTER(C.c_float) * len(self.keep))(*[t.ctypes.data_as(_f32p) for t in self.keep])
+
+
+class Oracle:
+    """The C restatement of the reference path."""
+
+    def __init__(self, tensors, path: Path = ORACLE_SO):
+        if not Path(path).exists():
+            raise FileNotFoundError(f"{path} not built (run make -C oracle)")
+        lib = C.CDLL(str(path))
+        lib.pmo_model_create.restype = C.c_void_p
+        lib.pmo_model_create.argtypes = [C.c_void_p]
+        lib.pmo_model_destroy.argtypes = [C.c_void_p]
+        lib.pmo_fast_exp_neg.restype = C.c_float
+        lib.pmo_fast_exp_neg.argtypes = [C.c_float]
+        lib.pmo_gelu.restype = C.c_float
+        lib.pmo_gelu.argtypes = [C.c_float]
+        for name in ("pmo_edge_features", "pmo_encode", "pmo_decode_order", "pmo_decode",
+                     "pmo_teacher_forced_decode", "pmo_inverse_fold", "pmo_teacher_forced",
+                     "pmo_algorithm_inverse_fold"):
+            getattr(lib, name).restype = C.c_int
+        self.lib = lib
+        self._t = _TensorTable(tensors)
+        self.model = C.c_void_p(lib.pmo_model_create(C.cast(self._t.table, C.c_void_p)))
+
+    def __del__(self):
+        try:
+            self.lib.pmo_model_destroy(self.model)
+        except Exception:
+            pass
+
+    def fast_exp_neg(self, x: float) -> float:
+        return float(self.lib.pmo_fast_exp_neg(C.c_float(x)))
+
+    def gelu(self, x: float) -> float:
+        return float(self.lib.pmo_gelu(C.c_float(x)))
+
+    def knn(self, ca, valid, K):
+        ca = _f32(ca)
+        valid = _u8(valid)
+        L = ca.shape[0]
+        idx = np.empty((L, K), np.int32)
+        d2 = np.empty((L, K), np.float32)
+        self.lib.pmo_knn(_p(ca, _f32p), _p(valid, _u8p), C.c_int32(L), C.c_int32(K), _p(idx, _i32p), _p(d2, _f32p))
+        return idx, d2
+
+    def edge_features(self, bb):
+        L = bb.L
+        K = k_of(L)
+        idx = np.empty((L, K), np.int32)
+        feat = np.empty((L, K, 416), np.float32)
+        c, s, r, ch = _f32(bb.coords), _u8(bb.atom_sources), _i32(bb.residue_indices), _i32(bb.chain_labels)
+        st = self.lib.pmo_edge_features(self.model, _p(c, _f32p), _p(s, _u8p), _p(r, _i32p), _p(ch, _i32p),
+                                        C.c_int32(L), _p(idx, _i32p), _p(feat, _f32p))
+        assert st == 0
+        return idx, feat
+
+    def encode(self, bb):
+        L = bb.L
+        K = k_of(L)
+        mask = np.empty(L, np.float32)
+        idx = np.empty((L, K), np.int32)
+        hv = np.empty((L, H), np.float32)
+        he = np.empty((L, K, H), np.float32)
+        c, s, r, ch = _f32(bb.coords), _u8(bb.atom_sources), _i32(bb.residue_indices), _i32(bb.chain_labels)
+        st = self.lib.pmo_encode(self.model, _p(c, _f32p), _p(s, _u8p), _p(r, _i32p), _p(ch, _i32p),
+                                 C.c_int32(L), _p(mask, _f32p), _p(idx, _i32p), _p(hv, _f32p), _p(he, _f32p))
+        assert st == 0
+        return mask, idx, hv, he
+
+    def decode_order(self, L, seed, chain_mask=None, residue_mask=None, input_order=None, use_input=False):
+        order = np.empty(L, np.int32)
+        cm, rm, io = _f32(chain_mask), _f32(residue_mask), _i32(input_order)
+        st = self.lib.pmo_decode_order(_p(cm, _f32p), _p(rm, _f32p), C.c_int32(L), C.c_uint64(seed),
+                                       _p(io, _i32p), C.c_int(int(use_input)), _p(order, _i32p))
+        if st != 0:
+            raise ValueError("invalid decoding order")
+        return order
+
+    def decode(self, enc, order, seed, temperature, greedy=False, chain_mask=None, true_tokens=None,
+               forced_tokens=None):
+        mask, idx, hv, he = enc
+        L = hv.shape[0]
+        tokens = np.empty(L, np.int32)
+        lp = np.empty((L, V), np.float32)
+        score = C.c_float(0)
+        sampled = np.empty(L, np.int32)
+        gap = np.empty(L, np.float64)
+        cm, tt, ft, od = _f32(chain_mask), _i32(true_tokens), _i32(forced_tokens), _i32(order)
+        st = self.lib.pmo_decode(self.model, _p(mask, _f32p), _p(idx, _i32p), _p(hv, _f32p), _p(he, _f32p),
+                                 C.c_int32(L), _p(cm, _f32p), _p(tt, _i32p), _p(od, _i32p), C.c_uint64(seed),
+                                 C.c_float(temperature), C.c_int(int(greedy)), _p(ft, _i32p), _p(tokens, _i32p),
+                                 _p(lp, _f32p), C.byref(score), _p(sampled, _i32p), _p(gap, _f64p))
+        assert st == 0
+        return dict(tokens=tokens, log_probs=lp, score=score.value, sampled=sampled, cdf_gap=gap)
+
+    def teacher_forced_decode(self, enc, tokens, order, chain_mask=None):
+        mask, idx, hv, he = enc
+        L = hv.shape[0]
+        lp = np.empty((L, V), np.float32)
+        score = C.c_float(0)
+        cm, tk, od = _f32(chain_mask), _i32(tokens), _i32(order)
+        st = self.lib.pmo_teacher_forced_decode(self.model, _p(mask, _f32p), _p(idx, _i32p), _p(hv, _f32p),
+                                                _p(he, _f32p), C.c_int32(L), _p(cm, _f32p), _p(tk, _i32p),
+                                                _p(od, _i32p), _p(lp, _f32p), C.byref(score))
+        if st != 0:
+            raise ValueError("invalid teacher-forced request")
+        return lp, score.value
+
+    def inverse_fold(self, bb, seed, order_seed, temperature, greedy=False, input_order=None,
+                     use_input_order=False, chain_mask=None, true_tokens=None):
+        L = bb.L
+        tokens = np.empty(L, np.int32)
+        lp = np.empty((L, V), np.float32)
+        order = np.empty(L, np.int32)
+        score = C.c_float(0)
+        c, s, r, ch = _f32(bb.coords), _u8(bb.atom_sources), _i32(bb.residue_indices), _i32(bb.chain_labels)
+        cm, io, tt = _f32(chain_mask), _i32(input_order), _i32(true_tokens)
+        st = self.lib.pmo_inverse_fold(self.model, _p(c, _f32p), _p(s, _u8p), C.c_int32(L), _p(r, _i32p),
+                                       _p(ch, _i32p), _p(cm, _f32p), _p(io, _i32p), _p(tt, _i32p),
+                                       C.c_uint64(seed), C.c_uint64(order_seed), C.c_float(temperature),
+                                       C.c_int(int(greedy)), C.c_int(int(use_input_order)), _p(tokens, _i32p),
+                                       _p(lp, _f32p), _p(order, _i32p), C.byref(score))
+        assert st == 0
+        return dict(tokens=tokens, log_probs=lp, order=order, score=score.value)
+
+    def teacher_forced(self, bb, tokens, input_order=None, chain_mask=None):
+        L = bb.L
+        lp = np.empty((L, V), np.float32)
+        score = C.c_float(0)
+        c, s, r, ch = _f32(bb.coords), _u8(bb.atom_sources), _i32(bb.residue_indices), _i32(bb.chain_labels)
+        cm, tk, io = _f32(chain_mask), _i32(tokens), _i32(input_order)
+        st = self.lib.pmo_teacher_forced(self.model, _p(c, _f32p), _p(s, _u8p), C.c_int32(L), _p(r, _i32p),
+                                         _p(ch, _i32p), _p(cm, _f32p), _p(tk, _i32p), _p(io, _i32p),
+                                         _p(lp, _f32p), C.byref(score))
+        assert st == 0
+        return lp, score.value
+
+    def algorithm_inverse_fold(self, bb, num_seqs, seed, temperature, n_to_c=False):
+        L = bb.L
+        tokens = np.empty((num_seqs, L), np.int32)
+        lp = np.empty((num_seqs, L, V), np.float32)
+        scores = np.empty(num_seqs, np.float32)
+        c, s = _f32(bb.coords), _u8(bb.atom_sources)
+        st = self.lib.pmo_algorithm_inverse_fold(self.model, _p(c, _f32p), _p(s, _u8p), C.c_int32(L),
+                                                 C.c_int32(num_seqs), C.c_uint64(seed), C.c_float(temperature),
+                                                 C.c_int(int(n_to_c)), _p(tokens, _i32p), _p(lp, _f32p),
+                                                 _p(scores, _f32p))
+        assert st == 0
+        return dict(tokens=tokens, log_probs=lp, scores=scores)
+
+
+class Reference:
+    """The reference's own sources compiled by oracle/ref.mk."""
+
+    def __init__(self, tensors, path: Path = REF_SO):
+        if not Path(path).exists():
+            raise FileNotFoundError(f"{path} not built")
+        lib = C.CDLL(str(path))
+        lib.ref_set_weights.argtypes = [C.c_void_p]
+        for name in ("ref_inverse_fold", "ref_teacher_forced", "ref_algorithm_inverse_fold"):
+            getattr(lib, name).restype = C.c_int
+        self.lib = lib
+        self._t = _TensorTable(tensors)
+        lib.ref_set_weights(C.cast(self._t.table, C.c_void_p))
+
+    @staticmethod
+    def available() -> bool:
+        return REF_SO.exists()
+
+    def knn(self, ca, valid, K):
+        ca = _f32(ca)
+        valid = _u8(valid)
+        L = ca.shape[0]
+        idx = np.empty((L, K), np.int32)
+        d2 = np.empty((L, K), np.float32)
+        self.lib.ref_knn(_p(ca, _f32p), _p(valid, _u8p), C.c_int32(L), C.c_int32(K), _p(idx, _i32p), _p(d2, _f32p))
+        return idx, d2
+
+    def inverse_fold(self, bb, seed, order_seed, temperature, greedy=False, input_order=None,
+                     use_input_order=False, chain_mask=None, true_tokens=None):
+        L = bb.L
+        tokens = np.empty(L, np.int32)
+        lp = np.empty((L, V), np.float32)
+        order = np.empty(L, np.int32)
+        score = C.c_float(0)
+        c, s, r, ch = _f32(bb.coords), _u8(bb.atom_sources), _i32(bb.residue_indices), _i32(bb.chain_labels)
+        cm, io, tt = _f32(chain_mask), _i32(input_order), _i32(true_tokens)
+        st = self.lib.ref_inverse_fold(_p(c, _f32p), _p(s, _u8p), C.c_int32(L), _p(r, _i32p), _p(ch, _i32p),
+                                       _p(cm, _f32p), _p(io, _i32p), _p(tt, _i32p), C.c_uint64(seed),
+                                       C.c_uint64(order_seed), C.c_float(temperature), C.c_int(int(greedy)),
+                                       C.c_int(int(use_input_order)), _p(tokens, _i32p), _p(lp, _f32p),
+                                       _p(order, _i32p), C.byref(score))
+        assert st == 0, st
+        return dict(tokens=tokens, log_probs=lp, order=order, score=score.value)
+
+    def teacher_forced(self, bb, tokens, input_order=None, chain_mask=None):
+        L = bb.L
+        lp = np.empty((L, V), np.float32)
+        score = C.c_float(0)
+        c, s, r, ch = _f32(bb.coords), _u8(bb.atom_sources), _i32(bb.residue_indices), _i32(bb.chain_labels)
+        cm, tk, io = _f32(chain_mask), _i32(tokens), _i32(input_order)
+        st = self.lib.ref_teacher_forced(_p(c, _f32p), _p(s, _u8p), C.c_int32(L), _p(r, _i32p), _p(ch, _i32p),
+                                         _p(cm, _f32p), _p(tk, _i32p), _p(io, _i32p), _p(lp, _f32p),
+                                         C.byref(score))
+        assert st == 0, st
+        return lp, score.value
+
+    def algorithm_inverse_fold(self, bb, num_seqs, seed, temperature, n_to_c=False):
+        L = bb.L
+        tokens = np.empty((num_seqs, L), np.int32)
+        lp = np.empty((num_seqs, L, V), np.float32)
+        scores = np.empty(num_seqs, np.float32)
+        c, s = _f32(bb.coords), _u8(bb.atom_sources)
+        st = self.lib.ref_algorithm_inverse_fold(_p(c, _f32p), _p(s, _u8p), C.c_int32(L), C.c_int32(num_seqs),
+                                                 C.c_uint64(seed), C.c_float(temperature), C.c_int(int(n_to_c)),
+                                                 _p(tokens, _i32p), _p(lp, _f32p), _p(scores, _f32p))
+        assert st == 0, st
+        return dict(tokens=tokens, log_probs=lp, scores=scores)

@@ -1,0 +1,274 @@
+// C entry points around the reference's own ProteinMPNN v_48_020 functions.
+//
+// TEST INFRASTRUCTURE ONLY. oracle/ref.mk compiles this file together with
+// the reference's unmodified sources (read in place under the reference
+// checkout) into oracle/_ref/libhkbs_ref.so. Tests use it to pin the C
+// oracle bit-for-bit; bench.py times ref_algorithm_inverse_fold as the CPU
+// baseline ("kind": "reference"). Nothing in the product links it.
+//
+// The weight view is filled from 118 caller-owned float arrays in the
+// canonical order of hikoboshi_amd/weights.py, mirroring how the reference
+// binds its embedded blob (cpp/weights/embedded_proteinmpnn_v48_eps020.cpp:
+// 136-286) without needing the generated blob translation unit.
+
+#include <hikoboshi/algorithms/inverse_fold.hpp>
+#include <hikoboshi/modules/detail/mpnn_workspace.hpp>
+#include <hikoboshi/modules/mpnn/inverse_fold.hpp>
+#include <hikoboshi/modules/mpnn/proteinmpnn_decoder.hpp>
+#include <hikoboshi/primitives/compute/knn.hpp>
+#include <hikoboshi/universal/detail/proteinmpnn_v48_020_weights.hpp>
+
+#include <algorithm>
+#include <cstdint>
+#include <cstring>
+#include <vector>
+
+namespace {
+
+namespace hd = hikoboshi::modules::detail;
+namespace hm = hikoboshi::modules::mpnn;
+namespace hu = hikoboshi::universal;
+namespace pmp = hikoboshi::universal::detail;
+
+constexpr std::size_t kH = pmp::kProteinMpnnV48020Hidden;
+
+pmp::ProteinMpnnV48020Weights g_weights{};
+
+hu::Span<const float> sp(const float* p, std::size_t n) { return {p, n}; }
+
+void bind_linear(pmp::ProteinMpnnV48020LinearWeights& l, const float* w, const float* b,
+                 std::size_t out, std::size_t in) {
+  l.weight = sp(w, out * in);
+  l.bias = sp(b, out);
+}
+
+void bind_norm(pmp::ProteinMpnnV48020NormWeights& n, const float* g, const float* b) {
+  n.weight = sp(g, kH);
+  n.bias = sp(b, kH);
+}
+
+template <typename T>
+hu::Span<T> span_of(std::vector<T>& v) {
+  return {v.empty() ? nullptr : v.data(), v.size()};
+}
+
+// Workspace sizing follows cpp/algorithms/inverse_fold.cpp:39-124.
+struct EncoderStorage {
+  EncoderStorage(std::size_t L, std::size_t K)
+      : plan{L, kH, K, pmp::kProteinMpnnV48020RbfCount, pmp::kProteinMpnnV48020NumEncoderLayers},
+        ca(hd::mpnn64_ca_coordinate_count(plan)),
+        features(std::max(hd::mpnn64_residue_feature_count(plan),
+                          hd::mpnn64_neighbor_slot_count(plan) * 3U * kH)),
+        idx(hd::mpnn64_neighbor_slot_count(plan)),
+        d2(hd::mpnn64_neighbor_slot_count(plan)),
+        rbf(hd::mpnn64_neighbor_rbf_count(plan)),
+        residue(hd::mpnn64_residue_hidden_count(plan)),
+        gathered(hd::mpnn64_neighbor_hidden_count(plan)),
+        edge(hd::mpnn64_neighbor_hidden_count(plan)),
+        message(hd::mpnn64_neighbor_hidden_count(plan)),
+        projected(hd::mpnn64_neighbor_hidden_count(plan)),
+        scratch(hd::mpnn64_residue_hidden_count(plan)),
+        ffn(hd::mpnn64_ffn_hidden_count(plan)) {}
+  hd::Mpnn64Workspace view() {
+    return {plan, span_of(ca), span_of(features), span_of(idx), span_of(d2), span_of(rbf),
+            span_of(residue), span_of(gathered), span_of(edge), span_of(message),
+            span_of(projected), span_of(scratch), span_of(ffn)};
+  }
+  hd::Mpnn64MemoryPlan plan;
+  std::vector<float> ca, features;
+  std::vector<std::int32_t> idx;
+  std::vector<float> d2, rbf, residue, gathered, edge, message, projected, scratch, ffn;
+};
+
+struct DecoderStorage {
+  DecoderStorage(std::size_t L, std::size_t K)
+      : plan{std::max<std::size_t>(L, 1U), kH, K, pmp::kProteinMpnnV48020DecoderNumInDimension,
+             pmp::kProteinMpnnV48020FfnHidden},
+        input(hm::proteinmpnn_decoder_message_input_count(plan)),
+        message(hm::proteinmpnn_decoder_neighbor_hidden_count(plan)),
+        projected(hm::proteinmpnn_decoder_neighbor_hidden_count(plan)),
+        scratch(hm::proteinmpnn_decoder_residue_hidden_count(plan)),
+        ffn(hm::proteinmpnn_decoder_ffn_hidden_count(plan)) {}
+  hm::ProteinMpnnDecoderWorkspace view() {
+    return {plan, span_of(input), span_of(message), span_of(projected), span_of(scratch),
+            span_of(ffn)};
+  }
+  hm::ProteinMpnnDecoderMemoryPlan plan;
+  std::vector<float> input, message, projected, scratch, ffn;
+};
+
+int code(hu::Status s) { return static_cast<int>(s.code); }
+
+}  // namespace
+
+extern "C" {
+
+void ref_set_weights(const float* const* t) {
+  auto& w = g_weights;
+  w.features.embeddings.linear.weight = sp(t[0], 16 * 66);
+  w.features.embeddings.linear.bias = sp(t[1], 16);
+  w.features.edge_embedding.weight = sp(t[2], kH * 416);
+  bind_norm(w.features.norm_edges, t[3], t[4]);
+  bind_linear(w.W_e, t[5], t[6], kH, kH);
+  w.W_s.weight = sp(t[7], 21 * kH);
+  for (int l = 0; l < 3; ++l) {
+    const float* const* e = t + 8 + 22 * l;
+    auto& L = w.encoder_layers[l];
+    bind_linear(L.W1, e[0], e[1], kH, 3 * kH);
+    bind_linear(L.W2, e[2], e[3], kH, kH);
+    bind_linear(L.W3, e[4], e[5], kH, kH);
+    bind_linear(L.W11, e[6], e[7], kH, 3 * kH);
+    bind_linear(L.W12, e[8], e[9], kH, kH);
+    bind_linear(L.W13, e[10], e[11], kH, kH);
+    bind_norm(L.norm1, e[12], e[13]);
+    bind_norm(L.norm2, e[14], e[15]);
+    bind_norm(L.norm3, e[16], e[17]);
+    bind_linear(L.dense.W_in, e[18], e[19], 4 * kH, kH);
+    bind_linear(L.dense.W_out, e[20], e[21], kH, 4 * kH);
+  }
+  for (int l = 0; l < 3; ++l) {
+    const float* const* d = t + 74 + 14 * l;
+    auto& L = w.decoder_layers[l];
+    bind_linear(L.W1, d[0], d[1], kH, 4 * kH);
+    bind_linear(L.W2, d[2], d[3], kH, kH);
+    bind_linear(L.W3, d[4], d[5], kH, kH);
+    bind_norm(L.norm1, d[6], d[7]);
+    bind_norm(L.norm2, d[8], d[9]);
+    bind_linear(L.dense.W_in, d[10], d[11], 4 * kH, kH);
+    bind_linear(L.dense.W_out, d[12], d[13], kH, 4 * kH);
+  }
+  bind_linear(w.W_out, t[116], t[117], 21, kH);
+}
+
+void ref_knn(const float* ca, const std::uint8_t* valid, std::int32_t L, std::int32_t K,
+             std::int32_t* idx, float* d2) {
+  hikoboshi::primitives::compute::KnnScalarRequest r{};
+  r.query_coordinates = ca;
+  r.target_coordinates = ca;
+  r.query_validity_mask = valid;
+  r.target_validity_mask = valid;
+  r.query_count = static_cast<std::size_t>(L);
+  r.target_count = static_cast<std::size_t>(L);
+  r.k = static_cast<std::size_t>(K);
+  r.include_self = true;
+  r.treat_zero_coords_as_invalid = false;
+  hikoboshi::primitives::compute::KnnScalarOutput o{idx, d2};
+  hikoboshi::primitives::compute::knn_scalar(r, o);
+}
+
+int ref_inverse_fold(const float* coords, const std::uint8_t* atom_src, std::int32_t L,
+                     const std::int32_t* resid, const std::int32_t* chain,
+                     const float* chain_mask, const std::int32_t* input_order,
+                     const std::int32_t* true_tokens, std::uint64_t seed,
+                     std::uint64_t order_seed, float temperature, int greedy,
+                     int use_input_order, std::int32_t* tokens, float* log_probs,
+                     std::int32_t* order_out, float* score) {
+  const std::size_t n = static_cast<std::size_t>(L);
+  const std::size_t K = hm::proteinmpnn_v48_020_effective_neighbor_count(n);
+  EncoderStorage es(n, K);
+  DecoderStorage ds(n, K);
+  hd::Mpnn64Workspace ew = es.view();
+  hm::ProteinMpnnDecoderWorkspace dw = ds.view();
+  std::vector<char> seq(n + 1U, '\0');
+  hm::ProteinMpnnInverseFoldRequest req{};
+  req.coordinates = coords;
+  req.atom_sources = reinterpret_cast<const hu::AtomSource*>(atom_src);
+  req.weights = &g_weights;
+  req.encoder_workspace = &ew;
+  req.decoder_workspace = &dw;
+  req.residue_count = n;
+  req.residue_indices = resid;
+  req.chain_labels = chain;
+  req.chain_mask = chain_mask;
+  req.input_decoding_order = input_order;
+  req.true_token_ids = true_tokens;
+  req.options.seed = seed;
+  req.options.decode_order_seed = order_seed;
+  req.options.temperature = temperature;
+  req.options.greedy = greedy != 0;
+  req.options.use_input_decoding_order = use_input_order != 0;
+  hm::ProteinMpnnInverseFoldOutput out{};
+  out.token_ids = tokens;
+  out.sequence = seq.data();
+  out.log_probs = log_probs;
+  out.decoding_order = order_out;
+  out.sequence_score = score;
+  out.residue_count = n;
+  out.vocab_size = 21;
+  return code(hm::proteinmpnn_inverse_fold_scalar(req, out));
+}
+
+int ref_teacher_forced(const float* coords, const std::uint8_t* atom_src, std::int32_t L,
+                       const std::int32_t* resid, const std::int32_t* chain,
+                       const float* chain_mask, const std::int32_t* tokens,
+                       const std::int32_t* input_order, float* log_probs, float* score) {
+  const std::size_t n = static_cast<std::size_t>(L);
+  const std::size_t K = hm::proteinmpnn_v48_020_effective_neighbor_count(n);
+  EncoderStorage es(n, K);
+  DecoderStorage ds(n, K);
+  hd::Mpnn64Workspace ew = es.view();
+  hm::ProteinMpnnDecoderWorkspace dw = ds.view();
+  std::vector<std::int32_t> iota(n);
+  for (std::size_t i = 0; i < n; ++i) iota[i] = static_cast<std::int32_t>(i);
+  std::vector<std::int32_t> order(n, -1);
+  hm::ProteinMpnnTeacherForcedRequest req{};
+  req.coordinates = coords;
+  req.atom_sources = reinterpret_cast<const hu::AtomSource*>(atom_src);
+  req.token_ids = tokens;
+  req.weights = &g_weights;
+  req.encoder_workspace = &ew;
+  req.decoder_workspace = &dw;
+  req.residue_count = n;
+  req.residue_indices = resid;
+  req.chain_labels = chain;
+  req.chain_mask = chain_mask;
+  req.input_decoding_order = input_order != nullptr ? input_order : iota.data();
+  req.options.use_input_decoding_order = true;
+  hm::ProteinMpnnTeacherForcedOutput out{};
+  out.log_probs = log_probs;
+  out.decoding_order = order.data();
+  out.sequence_score = score;
+  out.residue_count = n;
+  out.vocab_size = 21;
+  return code(hm::proteinmpnn_teacher_forced_forward_scalar(req, out));
+}
+
+// cpp/algorithms/inverse_fold.cpp:221-356 called as the API does, for the
+// CPU baseline. tokens [N,L] and log_probs [N,L,21] are written from the
+// result's sequences / log-prob block.
+int ref_algorithm_inverse_fold(const float* coords, const std::uint8_t* atom_src,
+                               std::int32_t L, std::int32_t num_seqs, std::uint64_t seed,
+                               float temperature, int n_to_c, std::int32_t* tokens,
+                               float* log_probs, float* scores) {
+  const std::size_t n = static_cast<std::size_t>(L);
+  std::vector<char> codes(n, 'X');
+  hikoboshi::algorithms::InverseFoldRequest req{};
+  req.structure.residue_count = n;
+  req.structure.coordinates = sp(coords, n * 15U);
+  req.structure.atom_sources = {reinterpret_cast<const hu::AtomSource*>(atom_src), n * 5U};
+  req.structure.residue_codes = {codes.data(), n};
+  req.structure.residues = {nullptr, 0};
+  req.weights = &g_weights;
+  req.options.sampling_temp = temperature;
+  req.options.num_seqs = static_cast<std::size_t>(num_seqs);
+  req.options.seed = seed;
+  req.options.decode_order = n_to_c ? hikoboshi::algorithms::InverseFoldDecodeOrder::NToC
+                                    : hikoboshi::algorithms::InverseFoldDecodeOrder::Random;
+  req.options.keep_log_probs = true;
+  const auto result = hikoboshi::algorithms::inverse_fold_proteinmpnn_v48_020(req);
+  if (!result.status.ok()) return code(result.status);
+  static const char kAlphabet[] = "ACDEFGHIKLMNPQRSTVWYX";
+  for (std::size_t i = 0; i < result.value.sequences.size(); ++i) {
+    const auto& s = result.value.sequences[i];
+    scores[i] = static_cast<float>(s.score);
+    for (std::size_t r = 0; r < n; ++r) {
+      const char* hit = std::strchr(kAlphabet, s.sequence[r]);
+      tokens[i * n + r] = hit ? static_cast<std::int32_t>(hit - kAlphabet) : 20;
+    }
+  }
+  std::memcpy(log_probs, result.value.logprobs.values.data(),
+              result.value.logprobs.values.size() * sizeof(float));
+  return 0;
+}
+
+}  // extern "C"
