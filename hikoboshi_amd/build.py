@@ -1,0 +1,57 @@
+"""Builds the HIP library hikoboshi_amd/libhkbs_pmpnn.so for gfx950 (in-tree).
+
+    python -m hikoboshi_amd.build
+
+hipcc compiles the kernels and the C-ABI layer in one shared object. Packed
+FP32 instruction selection is disabled on the device side.
+"""
+from __future__ import annotations
+
+import os
+import shutil
+import subprocess
+import sys
+from pathlib import Path
+
+HERE = Path(__file__).resolve().parent
+CSRC = HERE / "csrc"
+LIB = HERE / "libhkbs_pmpnn.so"
+ARCH = os.environ.get("HKBS_OFFLOAD_ARCH", "gfx950")
+SOURCES = ["knn.hip", "features.hip", "encoder.hip", "decoder.hip", "capi.hip"]
+
+
+def hipcc() -> str:
+    for cand in (os.environ.get("HIPCC"), "/opt/rocm/bin/hipcc", shutil.which("hipcc")):
+        if cand and Path(cand).exists():
+            return cand
+    raise RuntimeError("hipcc not found")
+
+
+def build(verbose: bool = False) -> Path:
+    objs = []
+    obj_dir = HERE / "_build"
+    obj_dir.mkdir(exist_ok=True)
+    common = [
+        hipcc(), "-std=c++17", "-O3", "-fPIC", f"--offload-arch={ARCH}",
+        "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+        "-Wno-unused-command-line-argument", "-I", str(HERE.parent / "include"),
+    ]
+    for src in SOURCES:
+        obj = obj_dir / (Path(src).stem + ".o")
+        cmd = common + ["-c", str(CSRC / src), "-o", str(obj)]
+        if verbose:
+            print(" ".join(cmd), flush=True)
+        subprocess.run(cmd, check=True)
+        objs.append(str(obj))
+    tmp = LIB.with_suffix(".so.tmp")
+    cmd = [hipcc(), "-shared", "-fPIC", f"--offload-arch={ARCH}", "-o", str(tmp)] + objs
+    if verbose:
+        print(" ".join(cmd), flush=True)
+    subprocess.run(cmd, check=True)
+    tmp.replace(LIB)
+    return LIB
+
+
+if __name__ == "__main__":
+    build(verbose="-v" in sys.argv)
+    print(LIB)

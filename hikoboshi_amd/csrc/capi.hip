@@ -1,0 +1,947 @@
+// C ABI of the MI355X ProteinMPNN v_48_020 design path (include/hkbs_pmpnn.h).
+//
+// Host responsibilities: parse the safetensors weight package, pack the
+// weights into the device layouts the kernels read (one upload per context),
+// validate requests with the reference's rules, compute decoding orders on
+// the host (bit-exact with the reference's libm-based routine), manage a
+// grow-only device workspace and enqueue the kernels on the context stream.
+#include "../../include/hkbs_pmpnn.h"
+#include "pmpnn_internal.hpp"
+
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cmath>
+#include <cstdio>
+#include <cstring>
+#include <map>
+#include <numeric>
+#include <string>
+#include <vector>
+
+namespace hkbs {
+hipError_t launch_knn(const float* coords, const uint8_t* atom_src, int L, int K, int32_t* idx, float* d2,
+                      float* mask, float4* ca_scratch, hipStream_t stream);
+hipError_t launch_positions(const int32_t* orders, int L, int B, int shared, int32_t* pos, hipStream_t stream);
+}  // namespace hkbs
+
+namespace {
+
+using namespace hkbs;
+
+thread_local const char* g_last_error = "";
+
+hkbs_status fail(hkbs_status code, const char* detail) {
+  g_last_error = detail;
+  return code;
+}
+
+// ---------------------------------------------------------------- JSON ----
+// Minimal JSON reader for the safetensors header.
+struct Json {
+  enum Kind { Null, Bool, Num, Str, Arr, Obj } kind = Null;
+  double num = 0;
+  std::string str;
+  std::vector<Json> arr;
+  std::map<std::string, Json> obj;
+};
+
+struct JsonParser {
+  const char* p;
+  const char* end;
+  bool ok = true;
+  void ws() {
+    while (p < end && (*p == ' ' || *p == '\n' || *p == '\r' || *p == '\t')) ++p;
+  }
+  bool lit(const char* s) {
+    const size_t n = std::strlen(s);
+    if ((size_t)(end - p) < n || std::strncmp(p, s, n) != 0) return false;
+    p += n;
+    return true;
+  }
+  std::string string() {
+    std::string out;
+    if (p >= end || *p != '"') {
+      ok = false;
+      return out;
+    }
+    ++p;
+    while (p < end && *p != '"') {
+      if (*p == '\\') {
+        ++p;
+        if (p >= end) break;
+        switch (*p) {
+          case 'n': out += '\n'; break;
+          case 't': out += '\t'; break;
+          case 'u': p += 4; out += '?'; break;
+          default: out += *p; break;
+        }
+        ++p;
+      } else {
+        out += *p++;
+      }
+    }
+    if (p >= end) {
+      ok = false;
+      return out;
+    }
+    ++p;
+    return out;
+  }
+  Json value(int depth = 0) {
+    Json v;
+    ws();
+    if (p >= end || depth > 16) {
+      ok = false;
+      return v;
+    }
+    if (*p == '{') {
+      v.kind = Json::Obj;
+      ++p;
+      ws();
+      if (p < end && *p == '}') {
+        ++p;
+        return v;
+      }
+      while (ok) {
+        ws();
+        std::string k = string();
+        ws();
+        if (p >= end || *p != ':') {
+          ok = false;
+          break;
+        }
+        ++p;
+        v.obj[k] = value(depth + 1);
+        ws();
+        if (p < end && *p == ',') {
+          ++p;
+          continue;
+        }
+        if (p < end && *p == '}') {
+          ++p;
+          break;
+        }
+        ok = false;
+      }
+    } else if (*p == '[') {
+      v.kind = Json::Arr;
+      ++p;
+      ws();
+      if (p < end && *p == ']') {
+        ++p;
+        return v;
+      }
+      while (ok) {
+        v.arr.push_back(value(depth + 1));
+        ws();
+        if (p < end && *p == ',') {
+          ++p;
+          continue;
+        }
+        if (p < end && *p == ']') {
+          ++p;
+          break;
+        }
+        ok = false;
+      }
+    } else if (*p == '"') {
+      v.kind = Json::Str;
+      v.str = string();
+    } else if (lit("true")) {
+      v.kind = Json::Bool;
+      v.num = 1;
+    } else if (lit("false")) {
+      v.kind = Json::Bool;
+    } else if (lit("null")) {
+      v.kind = Json::Null;
+    } else {
+      char* e = nullptr;
+      v.kind = Json::Num;
+      v.num = std::strtod(p, &e);
+      if (e == p) ok = false;
+      p = e;
+    }
+    return v;
+  }
+};
+
+// ------------------------------------------------------------- weights ----
+const char* const kNames[kTensors] = {
+#define ENC(l)                                                                                          \
+  "encoder_layers." #l ".W1.weight", "encoder_layers." #l ".W1.bias", "encoder_layers." #l ".W2.weight", \
+      "encoder_layers." #l ".W2.bias", "encoder_layers." #l ".W3.weight", "encoder_layers." #l ".W3.bias",  \
+      "encoder_layers." #l ".W11.weight", "encoder_layers." #l ".W11.bias",                              \
+      "encoder_layers." #l ".W12.weight", "encoder_layers." #l ".W12.bias",                              \
+      "encoder_layers." #l ".W13.weight", "encoder_layers." #l ".W13.bias",                              \
+      "encoder_layers." #l ".norm1.weight", "encoder_layers." #l ".norm1.bias",                          \
+      "encoder_layers." #l ".norm2.weight", "encoder_layers." #l ".norm2.bias",                          \
+      "encoder_layers." #l ".norm3.weight", "encoder_layers." #l ".norm3.bias",                          \
+      "encoder_layers." #l ".dense.W_in.weight", "encoder_layers." #l ".dense.W_in.bias",                \
+      "encoder_layers." #l ".dense.W_out.weight", "encoder_layers." #l ".dense.W_out.bias"
+#define DEC(l)                                                                                          \
+  "decoder_layers." #l ".W1.weight", "decoder_layers." #l ".W1.bias", "decoder_layers." #l ".W2.weight", \
+      "decoder_layers." #l ".W2.bias", "decoder_layers." #l ".W3.weight", "decoder_layers." #l ".W3.bias",  \
+      "decoder_layers." #l ".norm1.weight", "decoder_layers." #l ".norm1.bias",                          \
+      "decoder_layers." #l ".norm2.weight", "decoder_layers." #l ".norm2.bias",                          \
+      "decoder_layers." #l ".dense.W_in.weight", "decoder_layers." #l ".dense.W_in.bias",                \
+      "decoder_layers." #l ".dense.W_out.weight", "decoder_layers." #l ".dense.W_out.bias"
+    "features.embeddings.linear.weight",
+    "features.embeddings.linear.bias",
+    "features.edge_embedding.weight",
+    "features.norm_edges.weight",
+    "features.norm_edges.bias",
+    "W_e.weight",
+    "W_e.bias",
+    "W_s.weight",
+    ENC(0),
+    ENC(1),
+    ENC(2),
+    DEC(0),
+    DEC(1),
+    DEC(2),
+    "W_out.weight",
+    "W_out.bias",
+#undef ENC
+#undef DEC
+};
+
+size_t expected_count(int i) {
+  const std::string n = kNames[i];
+  auto ends = [&](const char* s) {
+    const size_t k = std::strlen(s);
+    return n.size() >= k && n.compare(n.size() - k, k, s) == 0;
+  };
+  if (i == 0) return 16 * 66;
+  if (i == 1) return 16;
+  if (i == 2) return 128 * 416;
+  if (i == 5) return 128 * 128;
+  if (i == 7 || i == 116) return 21 * 128;
+  if (i == 117) return 21;
+  if (ends("W_in.weight") || ends("W_out.weight")) return 512 * 128;
+  if (ends("W_in.bias")) return 512;
+  if (n.rfind("encoder", 0) == 0 && (ends("W1.weight") || ends("W11.weight"))) return 128 * 384;
+  if (n.rfind("decoder", 0) == 0 && ends("W1.weight")) return 128 * 512;
+  if (ends(".weight") && (n.find(".W") != std::string::npos)) return 128 * 128;
+  return 128;
+}
+
+struct HostArena {
+  std::vector<float> data;
+  size_t add(size_t n) {
+    const size_t off = data.size();
+    data.resize(off + ((n + 63) / 64) * 64, 0.0F);
+    return off;
+  }
+};
+
+// kpack16: rows [N][kin] (row-major), columns [c0, c0 + kd) -> [kd/16][N][16].
+size_t pack_k16(HostArena& ar, const std::vector<const float*>& row_blocks, int rows_per_block, int kin, int c0,
+                int kd) {
+  const int N = static_cast<int>(row_blocks.size()) * rows_per_block;
+  const size_t off = ar.add((size_t)N * kd);
+  for (int n = 0; n < N; ++n) {
+    const float* src = row_blocks[n / rows_per_block];
+    const int rr = n % rows_per_block;
+    for (int k = 0; k < kd; ++k) {
+      const float v = src ? src[(size_t)rr * kin + c0 + k] : 0.0F;
+      ar.data[off + ((size_t)(k / 16) * N + n) * 16 + (k % 16)] = v;
+    }
+  }
+  return off;
+}
+
+// Transposed: W [N][kin] columns [c0, c0 + kd) -> [kd][ldo] (first N columns used).
+size_t pack_t(HostArena& ar, const float* W, int N, int kin, int c0, int kd, int ldo) {
+  const size_t off = ar.add((size_t)kd * ldo);
+  for (int n = 0; n < N; ++n)
+    for (int k = 0; k < kd; ++k) ar.data[off + (size_t)k * ldo + n] = W[(size_t)n * kin + c0 + k];
+  return off;
+}
+
+size_t copy_raw(HostArena& ar, const float* src, size_t n, size_t pad_to = 0) {
+  const size_t off = ar.add(std::max(n, pad_to));
+  std::memcpy(ar.data.data() + off, src, n * sizeof(float));
+  return off;
+}
+
+// --------------------------------------------------------- workspace ----
+struct DeviceArena {
+  char* base = nullptr;
+  size_t cap = 0;
+  size_t used = 0;
+  hipError_t reserve(size_t bytes) {
+    if (bytes <= cap) return hipSuccess;
+    if (base) (void)hipFree(base);
+    base = nullptr;
+    cap = 0;
+    hipError_t e = hipMalloc(&base, bytes);
+    if (e != hipSuccess) return e;
+    cap = bytes;
+    return hipSuccess;
+  }
+  void reset() { used = 0; }
+  template <typename T>
+  T* take(size_t n) {
+    const size_t bytes = ((n * sizeof(T) + 255) / 256) * 256;
+    T* p = reinterpret_cast<T*>(base + used);
+    used += bytes;
+    return p;
+  }
+};
+
+template <typename T>
+size_t aligned_bytes(size_t n) {
+  return ((n * sizeof(T) + 255) / 256) * 256;
+}
+
+// ------------------------------------------------------- decode order ----
+// cpp/modules/mpnn/decode_order_scalar.cpp:21-42,89-115
+uint64_t splitmix64(uint64_t& state) {
+  state += 0x9E3779B97F4A7C15ull;
+  uint64_t z = state;
+  z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+  z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+  return z ^ (z >> 31);
+}
+
+double uniform01(uint64_t& state) { return static_cast<double>(splitmix64(state) >> 11) * (1.0 / 9007199254740992.0); }
+
+float normal_abs(uint64_t& state) {
+  double u1 = uniform01(state);
+  if (u1 <= 0.0) u1 = 1.0 / 9007199254740992.0;
+  const double u2 = uniform01(state);
+  const double radius = std::sqrt(-2.0 * std::log(u1));
+  return static_cast<float>(std::fabs(radius * std::cos(6.283185307179586476925286766559 * u2)));
+}
+
+void random_order(const float* chain_mask, const float* residue_mask, int L, uint64_t seed, int32_t* order) {
+  std::vector<float> scores(L);
+  uint64_t state = seed;
+  for (int r = 0; r < L; ++r) {
+    const float c = chain_mask ? chain_mask[r] : 1.0F;
+    const float mk = residue_mask ? residue_mask[r] : 1.0F;
+    order[r] = r;
+    scores[r] = (c * mk + 0.0001F) * normal_abs(state);
+  }
+  std::stable_sort(order, order + L, [&](int32_t l, int32_t r) {
+    const float ls = scores[l], rs = scores[r];
+    if (ls == rs) return l < r;
+    return ls < rs;
+  });
+}
+
+bool is_permutation(const int32_t* order, int L) {
+  std::vector<unsigned char> seen(L, 0);
+  for (int p = 0; p < L; ++p) {
+    const int32_t r = order[p];
+    if (r < 0 || r >= L || seen[r]) return false;
+    seen[r] = 1;
+  }
+  return true;
+}
+
+void residue_mask_host(const uint8_t* src, int L, std::vector<float>& mask) {
+  mask.assign(L, 0.0F);
+  for (int r = 0; r < L; ++r) {
+    const uint8_t* s = src + (size_t)r * 5;
+    mask[r] = (s[0] && s[1] && s[2] && s[3]) ? 1.0F : 0.0F;
+  }
+}
+
+}  // namespace
+
+struct hkbs_pmpnn {
+  int device = 0;
+  hipStream_t stream = nullptr;
+  float* weights = nullptr;
+  ModelDev model{};
+  DeviceArena arena;
+};
+
+namespace {
+
+hkbs_status hip_fail(hipError_t e, const char* what) {
+  (void)e;
+  return fail(HKBS_INTERNAL_ERROR, what);
+}
+
+#define HK_CHECK(expr, what)                      \
+  do {                                            \
+    hipError_t _e = (expr);                       \
+    if (_e != hipSuccess) return hip_fail(_e, what); \
+  } while (0)
+
+hkbs_status build_model(hkbs_pmpnn* ctx, const float* const* t) {
+  HostArena ar;
+  struct Off {
+    size_t pos_w, pos_b, edge_t, ne_g, ne_b, We_t, We_b, Ws;
+    size_t W1b_dec_p, W1d_dec_p, Wlog_t, blog;
+    size_t enc[kLayers][22];
+    size_t dec[kLayers][20];
+  } o{};
+  o.pos_w = copy_raw(ar, t[0], 16 * 66);
+  o.pos_b = copy_raw(ar, t[1], 16);
+  o.edge_t = pack_t(ar, t[2], 128, 416, 0, 416, 128);
+  o.ne_g = copy_raw(ar, t[3], 128);
+  o.ne_b = copy_raw(ar, t[4], 128);
+  o.We_t = pack_t(ar, t[5], 128, 128, 0, 128, 128);
+  o.We_b = copy_raw(ar, t[6], 128);
+  o.Ws = copy_raw(ar, t[7], 21 * 128);
+  for (int l = 0; l < kLayers; ++l) {
+    const float* const* e = t + 8 + 22 * l;
+    size_t* q = o.enc[l];
+    q[0] = pack_t(ar, e[0], 128, 384, 0, 384, 128);   // W1_t
+    q[1] = pack_t(ar, e[2], 128, 128, 0, 128, 128);   // W2_t
+    q[2] = pack_t(ar, e[4], 128, 128, 0, 128, 128);   // W3_t
+    q[3] = pack_t(ar, e[6], 128, 384, 0, 384, 128);   // W11_t
+    q[4] = pack_t(ar, e[8], 128, 128, 0, 128, 128);   // W12_t
+    q[5] = pack_t(ar, e[10], 128, 128, 0, 128, 128);  // W13_t
+    q[6] = pack_t(ar, e[18], 512, 128, 0, 128, 512);  // Win_t
+    q[7] = pack_t(ar, e[20], 128, 512, 0, 512, 128);  // Wout_t
+    q[8] = copy_raw(ar, e[1], 128);                   // b1
+    q[9] = copy_raw(ar, e[3], 128);                   // b2
+    q[10] = copy_raw(ar, e[5], 128);                  // b3
+    q[11] = copy_raw(ar, e[7], 128);                  // b11
+    q[12] = copy_raw(ar, e[9], 128);                  // b12
+    q[13] = copy_raw(ar, e[11], 128);                 // b13
+    q[14] = copy_raw(ar, e[19], 512);                 // bin
+    q[15] = copy_raw(ar, e[21], 128);                 // bout
+    for (int i = 0; i < 6; ++i) q[16 + i] = copy_raw(ar, e[12 + i], 128);  // n1g n1b n2g n2b n3g n3b
+  }
+  {
+    std::vector<float> w1b(384 * 128), w1d(384 * 128);
+    for (int l = 0; l < kLayers; ++l) {
+      const float* W1 = t[74 + 14 * l];
+      for (int n = 0; n < 128; ++n)
+        for (int k = 0; k < 128; ++k) {
+          w1b[(size_t)(l * 128 + n) * 128 + k] = W1[(size_t)n * 512 + 128 + k];
+          w1d[(size_t)(l * 128 + n) * 128 + k] = W1[(size_t)n * 512 + 384 + k];
+        }
+    }
+    o.W1b_dec_p = pack_k16(ar, {w1b.data()}, 384, 128, 0, 128);
+    o.W1d_dec_p = pack_k16(ar, {w1d.data()}, 384, 128, 0, 128);
+  }
+  for (int l = 0; l < kLayers; ++l) {
+    const float* const* d = t + 74 + 14 * l;
+    size_t* q = o.dec[l];
+    q[0] = pack_t(ar, d[0], 128, 512, 0, 128, 128);    // W1a_t
+    q[1] = pack_k16(ar, {d[2]}, 128, 128, 0, 128);     // W2_p
+    q[2] = pack_t(ar, d[4], 128, 128, 0, 128, 128);    // W3_t
+    q[3] = pack_t(ar, d[10], 512, 128, 0, 128, 512);   // Win_t [128][512]
+    q[4] = pack_t(ar, d[12], 128, 512, 0, 512, 128);   // Wout_t [512][128]
+    q[5] = pack_t(ar, d[0], 128, 512, 384, 128, 128);  // W1d_t
+    {
+      // T[v][o] = sum_p W1c[o][p] W_s[v][p], in double then rounded.
+      std::vector<float> T(21 * 128);
+      for (int v = 0; v < 21; ++v)
+        for (int oo = 0; oo < 128; ++oo) {
+          double s = 0.0;
+          for (int p = 0; p < 128; ++p) s += (double)d[0][(size_t)oo * 512 + 256 + p] * (double)t[7][(size_t)v * 128 + p];
+          T[(size_t)v * 128 + oo] = static_cast<float>(s);
+        }
+      q[6] = copy_raw(ar, T.data(), T.size());
+    }
+    q[7] = copy_raw(ar, d[1], 128);    // b1
+    q[8] = copy_raw(ar, d[3], 128);    // b2
+    q[9] = copy_raw(ar, d[5], 128);    // b3
+    q[10] = copy_raw(ar, d[11], 512);  // bin
+    q[11] = copy_raw(ar, d[13], 128);  // bout
+    for (int i = 0; i < 4; ++i) q[12 + i] = copy_raw(ar, d[6 + i], 128);  // n1g n1b n2g n2b
+  }
+  o.Wlog_t = pack_t(ar, t[116], 21, 128, 0, 128, 32);
+  o.blog = copy_raw(ar, t[117], 21, 32);
+
+  HK_CHECK(hipMalloc(&ctx->weights, ar.data.size() * sizeof(float)), "device allocation of weights failed");
+  HK_CHECK(hipMemcpy(ctx->weights, ar.data.data(), ar.data.size() * sizeof(float), hipMemcpyHostToDevice),
+           "weight upload failed");
+  const float* B = ctx->weights;
+  ModelDev& m = ctx->model;
+  m.pos_w = B + o.pos_w;
+  m.pos_b = B + o.pos_b;
+  m.edge_t = B + o.edge_t;
+  m.ne_g = B + o.ne_g;
+  m.ne_b = B + o.ne_b;
+  m.We_t = B + o.We_t;
+  m.We_b = B + o.We_b;
+  m.Ws = B + o.Ws;
+  for (int l = 0; l < kLayers; ++l) {
+    const size_t* q = o.enc[l];
+    EncLayerDev& w = m.enc[l];
+    w.W1_t = B + q[0];
+    w.W2_t = B + q[1];
+    w.W3_t = B + q[2];
+    w.W11_t = B + q[3];
+    w.W12_t = B + q[4];
+    w.W13_t = B + q[5];
+    w.Win_t = B + q[6];
+    w.Wout_t = B + q[7];
+    w.b1 = B + q[8];
+    w.b2 = B + q[9];
+    w.b3 = B + q[10];
+    w.b11 = B + q[11];
+    w.b12 = B + q[12];
+    w.b13 = B + q[13];
+    w.bin = B + q[14];
+    w.bout = B + q[15];
+    w.n1g = B + q[16];
+    w.n1b = B + q[17];
+    w.n2g = B + q[18];
+    w.n2b = B + q[19];
+    w.n3g = B + q[20];
+    w.n3b = B + q[21];
+  }
+  for (int l = 0; l < kLayers; ++l) {
+    const size_t* q = o.dec[l];
+    DecLayerDev& w = m.dec[l];
+    w.W1a_t = B + q[0];
+    w.W2_p = B + q[1];
+    w.W3_t = B + q[2];
+    w.Win_t = B + q[3];
+    w.Wout_t = B + q[4];
+    w.W1d_t = B + q[5];
+    w.T = B + q[6];
+    w.b1 = B + q[7];
+    w.b2 = B + q[8];
+    w.b3 = B + q[9];
+    w.bin = B + q[10];
+    w.bout = B + q[11];
+    w.n1g = B + q[12];
+    w.n1b = B + q[13];
+    w.n2g = B + q[14];
+    w.n2b = B + q[15];
+  }
+  m.W1b_dec_p = B + o.W1b_dec_p;
+  m.W1d_dec_p = B + o.W1d_dec_p;
+  m.Wlog_t = B + o.Wlog_t;
+  m.blog = B + o.blog;
+  return HKBS_OK;
+}
+
+// Device pointers of one request's encoder state.
+struct EncodeBuffers {
+  float* mask;
+  float4* ca;
+  int32_t* idx;
+  float* d2;
+  float* h_v;
+  float* h_e;
+  EncoderScratch scratch;
+};
+
+size_t encode_bytes(int L, int K) {
+  const size_t S = (size_t)L * K;
+  return aligned_bytes<float>(L) + aligned_bytes<float4>(L) + aligned_bytes<int32_t>(S) + aligned_bytes<float>(S) +
+         aligned_bytes<float>((size_t)L * kH) + aligned_bytes<float>(S * kH) + aligned_bytes<float>((size_t)L * 256) +
+         aligned_bytes<float>((size_t)L * kH);
+}
+
+EncodeBuffers take_encode(DeviceArena& ar, int L, int K) {
+  const size_t S = (size_t)L * K;
+  EncodeBuffers e{};
+  e.mask = ar.take<float>(L);
+  e.ca = ar.take<float4>(L);
+  e.idx = ar.take<int32_t>(S);
+  e.d2 = ar.take<float>(S);
+  e.h_v = ar.take<float>((size_t)L * kH);
+  e.h_e = ar.take<float>(S * kH);
+  e.scratch.prefix = ar.take<float>((size_t)L * 256);
+  e.scratch.msg_sum = ar.take<float>((size_t)L * kH);
+  return e;
+}
+
+hipError_t run_encode(hkbs_pmpnn* ctx, const float* coords, const uint8_t* src, const int32_t* resid,
+                      const int32_t* chain, int L, int K, const EncodeBuffers& e) {
+  hipError_t err = launch_knn(coords, src, L, K, e.idx, e.d2, e.mask, e.ca, ctx->stream);
+  if (err != hipSuccess) return err;
+  err = launch_edge_embed(ctx->model, coords, src, resid, chain, e.idx, L, K, e.h_e, ctx->stream);
+  if (err != hipSuccess) return err;
+  return launch_encoder(ctx->model, e.idx, e.mask, L, K, e.h_v, e.h_e, e.scratch, ctx->stream);
+}
+
+struct Inputs {
+  float* coords;
+  uint8_t* src;
+  int32_t* resid;
+  int32_t* chain;
+  float* chain_mask;
+  int32_t* true_tokens;
+};
+
+size_t input_bytes(int L) {
+  return aligned_bytes<float>((size_t)L * 15) + aligned_bytes<uint8_t>((size_t)L * 5) + 2 * aligned_bytes<int32_t>(L) +
+         aligned_bytes<float>(L) + aligned_bytes<int32_t>(L);
+}
+
+hkbs_status upload_inputs(hkbs_pmpnn* ctx, DeviceArena& ar, const float* coords, const uint8_t* src,
+                          const int32_t* resid, const int32_t* chain, const float* chain_mask,
+                          const int32_t* true_tokens, int L, Inputs& in) {
+  in.coords = ar.take<float>((size_t)L * 15);
+  in.src = ar.take<uint8_t>((size_t)L * 5);
+  in.resid = ar.take<int32_t>(L);
+  in.chain = ar.take<int32_t>(L);
+  in.chain_mask = ar.take<float>(L);
+  in.true_tokens = ar.take<int32_t>(L);
+  hipStream_t s = ctx->stream;
+  HK_CHECK(hipMemcpyAsync(in.coords, coords, (size_t)L * 15 * sizeof(float), hipMemcpyHostToDevice, s), "H2D failed");
+  HK_CHECK(hipMemcpyAsync(in.src, src, (size_t)L * 5, hipMemcpyHostToDevice, s), "H2D failed");
+  if (resid) HK_CHECK(hipMemcpyAsync(in.resid, resid, (size_t)L * 4, hipMemcpyHostToDevice, s), "H2D failed");
+  else in.resid = nullptr;
+  if (chain) HK_CHECK(hipMemcpyAsync(in.chain, chain, (size_t)L * 4, hipMemcpyHostToDevice, s), "H2D failed");
+  else in.chain = nullptr;
+  if (chain_mask) HK_CHECK(hipMemcpyAsync(in.chain_mask, chain_mask, (size_t)L * 4, hipMemcpyHostToDevice, s), "H2D failed");
+  else in.chain_mask = nullptr;
+  if (true_tokens) HK_CHECK(hipMemcpyAsync(in.true_tokens, true_tokens, (size_t)L * 4, hipMemcpyHostToDevice, s), "H2D failed");
+  else in.true_tokens = nullptr;
+  return HKBS_OK;
+}
+
+size_t decode_bytes(int L, int K, int B) {
+  const size_t S = (size_t)L * K;
+  return aligned_bytes<float>(kLayers * S * kH) + aligned_bytes<float>((size_t)kLayers * L * kH) +
+         2 * aligned_bytes<int32_t>((size_t)B * L) + aligned_bytes<uint64_t>(B) +
+         aligned_bytes<float>((size_t)B * kLayers * L * kH) + aligned_bytes<int32_t>((size_t)B * L) +
+         aligned_bytes<float>((size_t)B * L * kV) + aligned_bytes<float>((size_t)B * L) + aligned_bytes<float>(B);
+}
+
+hkbs_status enter(hkbs_pmpnn* ctx) {
+  if (!ctx) return fail(HKBS_INVALID_ARGUMENT, "hkbs_pmpnn context is null");
+  if (hipSetDevice(ctx->device) != hipSuccess) return fail(HKBS_UNAVAILABLE, "HIP device is not available");
+  return HKBS_OK;
+}
+
+hkbs_status check_temperature(float temperature) {
+  if (!std::isfinite(temperature) || temperature < 0.0F)
+    return fail(HKBS_INVALID_ARGUMENT, "inverse-fold sampling_temp must be finite and >= 0");
+  return HKBS_OK;
+}
+
+// Shared implementation of the device design path. All pointers device.
+hkbs_status design_on_device(hkbs_pmpnn* ctx, const float* coords, const uint8_t* src, const int32_t* resid,
+                             const int32_t* chain, const float* chain_mask, const int32_t* true_tokens, int L, int B,
+                             const int32_t* orders, int shared, const uint64_t* seeds, float temperature, int greedy,
+                             int32_t* tokens, float* log_probs, float* scores, DeviceArena& ar, float* chosen) {
+  const int K = std::min(kKmax, L);
+  const size_t S = (size_t)L * K;
+  EncodeBuffers e = take_encode(ar, L, K);
+  float* E1 = ar.take<float>(kLayers * S * kH);
+  float* Q = ar.take<float>((size_t)kLayers * L * kH);
+  int32_t* pos = ar.take<int32_t>((size_t)B * L);
+  float* R = ar.take<float>((size_t)B * kLayers * L * kH);
+  HK_CHECK(run_encode(ctx, coords, src, resid, chain, L, K, e), "encoder launch failed");
+  HK_CHECK(launch_decoder_precompute(ctx->model, e.h_v, e.h_e, L, K, E1, Q, ctx->stream), "decoder precompute failed");
+  HK_CHECK(launch_positions(orders, L, shared ? 1 : B, shared, pos, ctx->stream), "position kernel failed");
+  DecodeArgs a{};
+  a.idx = e.idx;
+  a.mask = e.mask;
+  a.h_v = e.h_v;
+  a.E1 = E1;
+  a.Q = Q;
+  a.orders = orders;
+  a.shared_order = shared;
+  a.pos = pos;
+  a.chain_mask = chain_mask;
+  a.true_tokens = true_tokens;
+  a.seeds = seeds;
+  a.temperature = temperature;
+  a.greedy = greedy || temperature <= 0.0F;
+  a.L = L;
+  a.K = K;
+  a.B = B;
+  a.R = R;
+  a.tokens = tokens;
+  a.log_probs = log_probs;
+  a.scores = scores;
+  a.chosen_lp = chosen;
+  HK_CHECK(launch_decode(ctx->model, a, ctx->stream), "decode launch failed");
+  return HKBS_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* hkbs_last_error(void) { return g_last_error; }
+
+const char* hkbs_version(void) { return "hikoboshi-amd 0.1.0 (gfx950, ProteinMPNN v_48_020)"; }
+
+int32_t hkbs_device_count(void) {
+  int n = 0;
+  if (hipGetDeviceCount(&n) != hipSuccess) return 0;
+  return n;
+}
+
+hkbs_status hkbs_pmpnn_create(const uint8_t* data, size_t nbytes, int32_t device, hkbs_pmpnn** out) {
+  if (!out) return fail(HKBS_INVALID_ARGUMENT, "output context pointer is null");
+  *out = nullptr;
+  if (!data || nbytes < 8) return fail(HKBS_INVALID_ARGUMENT, "weight package is empty");
+  uint64_t hlen = 0;
+  std::memcpy(&hlen, data, 8);
+  if (hlen > nbytes - 8) return fail(HKBS_INVALID_ARGUMENT, "safetensors header length exceeds the package");
+  JsonParser jp{reinterpret_cast<const char*>(data) + 8, reinterpret_cast<const char*>(data) + 8 + hlen};
+  Json header = jp.value();
+  if (!jp.ok || header.kind != Json::Obj) return fail(HKBS_INVALID_ARGUMENT, "safetensors header is not valid JSON");
+  const size_t base = 8 + hlen;
+  std::vector<std::vector<float>> storage(kTensors);
+  std::vector<const float*> ptrs(kTensors);
+  for (int i = 0; i < kTensors; ++i) {
+    auto it = header.obj.find(kNames[i]);
+    if (it == header.obj.end()) return fail(HKBS_INVALID_ARGUMENT, "weight package is missing a v_48_020 tensor");
+    const Json& t = it->second;
+    auto dt = t.obj.find("dtype");
+    auto offs = t.obj.find("data_offsets");
+    if (dt == t.obj.end() || dt->second.str != "F32" || offs == t.obj.end() || offs->second.arr.size() != 2)
+      return fail(HKBS_INVALID_ARGUMENT, "weight package tensor is not F32 with data offsets");
+    const size_t s = static_cast<size_t>(offs->second.arr[0].num);
+    const size_t e = static_cast<size_t>(offs->second.arr[1].num);
+    const size_t count = expected_count(i);
+    if (e < s || e - s != count * 4 || base + e > nbytes)
+      return fail(HKBS_INVALID_ARGUMENT, "weight package tensor has the wrong size for v_48_020");
+    storage[i].resize(count);
+    std::memcpy(storage[i].data(), data + base + s, count * 4);
+    ptrs[i] = storage[i].data();
+  }
+  int ndev = 0;
+  if (hipGetDeviceCount(&ndev) != hipSuccess || ndev <= 0) return fail(HKBS_UNAVAILABLE, "no HIP device is available");
+  if (device < 0 || device >= ndev) return fail(HKBS_INVALID_ARGUMENT, "HIP device index is out of range");
+  if (hipSetDevice(device) != hipSuccess) return fail(HKBS_UNAVAILABLE, "HIP device is not available");
+  hkbs_pmpnn* ctx = new hkbs_pmpnn();
+  ctx->device = device;
+  if (hipStreamCreateWithFlags(&ctx->stream, hipStreamNonBlocking) != hipSuccess) {
+    delete ctx;
+    return fail(HKBS_UNAVAILABLE, "HIP stream creation failed");
+  }
+  const hkbs_status st = build_model(ctx, ptrs.data());
+  if (st != HKBS_OK) {
+    hkbs_pmpnn_destroy(ctx);
+    return st;
+  }
+  *out = ctx;
+  return HKBS_OK;
+}
+
+void hkbs_pmpnn_destroy(hkbs_pmpnn* ctx) {
+  if (!ctx) return;
+  (void)hipSetDevice(ctx->device);
+  if (ctx->stream) (void)hipStreamSynchronize(ctx->stream);
+  if (ctx->arena.base) (void)hipFree(ctx->arena.base);
+  if (ctx->weights) (void)hipFree(ctx->weights);
+  if (ctx->stream) (void)hipStreamDestroy(ctx->stream);
+  delete ctx;
+}
+
+hkbs_status hkbs_pmpnn_decode_order(const float* chain_mask, const uint8_t* atom_sources, int32_t L, uint64_t seed,
+                                    int32_t* order) {
+  if (L < 0) return fail(HKBS_INVALID_ARGUMENT, "residue count is negative");
+  if (L > 0 && (!atom_sources || !order)) return fail(HKBS_INVALID_ARGUMENT, "decode order pointers must be non-null");
+  std::vector<float> mask;
+  residue_mask_host(atom_sources, L, mask);
+  random_order(chain_mask, mask.data(), L, seed, order);
+  return HKBS_OK;
+}
+
+hkbs_status hkbs_pmpnn_design(hkbs_pmpnn* ctx, const float* coords, const uint8_t* atom_sources,
+                              const int32_t* residue_indices, const int32_t* chain_labels, const float* chain_mask,
+                              const int32_t* true_tokens, int32_t L, int32_t B, int32_t order_mode,
+                              const int32_t* orders, const uint64_t* order_seeds, const uint64_t* sampler_seeds,
+                              float temperature, int32_t greedy, int32_t* tokens, float* log_probs,
+                              int32_t* orders_out, float* scores) {
+  hkbs_status st = enter(ctx);
+  if (st != HKBS_OK) return st;
+  if (L < 0) return fail(HKBS_INVALID_ARGUMENT, "residue count is negative");
+  if (B <= 0) return fail(HKBS_INVALID_ARGUMENT, "inverse-fold num_seqs must be greater than zero");
+  if ((st = check_temperature(temperature)) != HKBS_OK) return st;
+  if (L == 0) return HKBS_OK;
+  if (!coords || !atom_sources) return fail(HKBS_INVALID_ARGUMENT, "inverse-fold structure must provide canonical backbone atoms");
+  if (!sampler_seeds || !tokens) return fail(HKBS_INVALID_ARGUMENT, "sampler seeds and token output must be non-null");
+
+  // Decoding orders on the host (bit-exact reference routine).
+  int shared = 0;
+  std::vector<int32_t> host_orders;
+  std::vector<float> rmask;
+  residue_mask_host(atom_sources, L, rmask);
+  switch (order_mode) {
+    case HKBS_ORDER_RANDOM:
+      if (!order_seeds) return fail(HKBS_INVALID_ARGUMENT, "random decode order needs order seeds");
+      host_orders.resize((size_t)B * L);
+      for (int b = 0; b < B; ++b) random_order(chain_mask, rmask.data(), L, order_seeds[b], host_orders.data() + (size_t)b * L);
+      break;
+    case HKBS_ORDER_INPUT_PER_SEQUENCE:
+      if (!orders) return fail(HKBS_INVALID_ARGUMENT, "input decode orders are null");
+      host_orders.assign(orders, orders + (size_t)B * L);
+      for (int b = 0; b < B; ++b)
+        if (!is_permutation(orders + (size_t)b * L, L))
+          return fail(HKBS_INVALID_ARGUMENT, "ProteinMPNN input decoding_order must be a permutation");
+      break;
+    case HKBS_ORDER_INPUT_SHARED:
+      if (!orders) return fail(HKBS_INVALID_ARGUMENT, "input decode order is null");
+      if (!is_permutation(orders, L)) return fail(HKBS_INVALID_ARGUMENT, "ProteinMPNN input decoding_order must be a permutation");
+      host_orders.assign(orders, orders + L);
+      shared = 1;
+      break;
+    case HKBS_ORDER_N_TO_C:
+      host_orders.resize(L);
+      std::iota(host_orders.begin(), host_orders.end(), 0);
+      shared = 1;
+      break;
+    default:
+      return fail(HKBS_INVALID_ARGUMENT, "unknown decode order mode");
+  }
+
+  const int K = std::min(kKmax, L);
+  const size_t norders = shared ? (size_t)L : (size_t)B * L;
+  const size_t need = input_bytes(L) + encode_bytes(L, K) + decode_bytes(L, K, B) + aligned_bytes<int32_t>(norders) +
+                      aligned_bytes<uint64_t>(B) + aligned_bytes<int32_t>((size_t)B * L) +
+                      aligned_bytes<float>((size_t)B * L * kV) + aligned_bytes<float>(B) + aligned_bytes<float>((size_t)B * L) +
+                      (64u << 10);
+  DeviceArena& ar = ctx->arena;
+  if (ar.reserve(need) != hipSuccess) return fail(HKBS_INTERNAL_ERROR, "device workspace allocation failed");
+  ar.reset();
+  Inputs in{};
+  if ((st = upload_inputs(ctx, ar, coords, atom_sources, residue_indices, chain_labels, chain_mask, true_tokens, L, in)) != HKBS_OK)
+    return st;
+  int32_t* d_orders = ar.take<int32_t>(norders);
+  uint64_t* d_seeds = ar.take<uint64_t>(B);
+  int32_t* d_tokens = ar.take<int32_t>((size_t)B * L);
+  float* d_lp = ar.take<float>((size_t)B * L * kV);
+  float* d_scores = ar.take<float>(B);
+  float* d_chosen = ar.take<float>((size_t)B * L);
+  hipStream_t s = ctx->stream;
+  HK_CHECK(hipMemcpyAsync(d_orders, host_orders.data(), norders * 4, hipMemcpyHostToDevice, s), "H2D failed");
+  HK_CHECK(hipMemcpyAsync(d_seeds, sampler_seeds, (size_t)B * 8, hipMemcpyHostToDevice, s), "H2D failed");
+  if ((st = design_on_device(ctx, in.coords, in.src, in.resid, in.chain, in.chain_mask, in.true_tokens, L, B, d_orders,
+                             shared, d_seeds, temperature, greedy, d_tokens, log_probs ? d_lp : nullptr,
+                             d_scores, ar, d_chosen)) != HKBS_OK)
+    return st;
+  HK_CHECK(hipMemcpyAsync(tokens, d_tokens, (size_t)B * L * 4, hipMemcpyDeviceToHost, s), "D2H failed");
+  if (log_probs) HK_CHECK(hipMemcpyAsync(log_probs, d_lp, (size_t)B * L * kV * 4, hipMemcpyDeviceToHost, s), "D2H failed");
+  if (scores) HK_CHECK(hipMemcpyAsync(scores, d_scores, (size_t)B * 4, hipMemcpyDeviceToHost, s), "D2H failed");
+  HK_CHECK(hipStreamSynchronize(s), "design kernels failed");
+  if (orders_out) {
+    for (int b = 0; b < B; ++b)
+      std::memcpy(orders_out + (size_t)b * L, host_orders.data() + (shared ? 0 : (size_t)b * L), (size_t)L * 4);
+  }
+  return HKBS_OK;
+}
+
+hkbs_status hkbs_pmpnn_design_device(hkbs_pmpnn* ctx, const float* coords, const uint8_t* atom_sources,
+                                     const int32_t* residue_indices, const int32_t* chain_labels, const float* chain_mask,
+                                     const int32_t* true_tokens, int32_t L, int32_t B, const int32_t* orders,
+                                     int32_t shared_order, const uint64_t* sampler_seeds, float temperature,
+                                     int32_t greedy, int32_t* tokens, float* log_probs, float* scores, void* stream) {
+  hkbs_status st = enter(ctx);
+  if (st != HKBS_OK) return st;
+  if (L < 0) return fail(HKBS_INVALID_ARGUMENT, "residue count is negative");
+  if (B <= 0) return fail(HKBS_INVALID_ARGUMENT, "inverse-fold num_seqs must be greater than zero");
+  if ((st = check_temperature(temperature)) != HKBS_OK) return st;
+  if (L == 0) return HKBS_OK;
+  if (!coords || !atom_sources || !orders || !sampler_seeds || !tokens)
+    return fail(HKBS_INVALID_ARGUMENT, "device design pointers must be non-null");
+  const int K = std::min(kKmax, L);
+  const size_t need = encode_bytes(L, K) + decode_bytes(L, K, B) + aligned_bytes<float>((size_t)B * L) + (64u << 10);
+  DeviceArena& ar = ctx->arena;
+  hipStream_t saved = ctx->stream;
+  if (stream) {
+    // Work on the caller's stream: wait for anything pending on ours first.
+    HK_CHECK(hipStreamSynchronize(saved), "context stream failed");
+    ctx->stream = static_cast<hipStream_t>(stream);
+  }
+  if (ar.reserve(need) != hipSuccess) {
+    ctx->stream = saved;
+    return fail(HKBS_INTERNAL_ERROR, "device workspace allocation failed");
+  }
+  ar.reset();
+  float* chosen = ar.take<float>((size_t)B * L);
+  st = design_on_device(ctx, coords, atom_sources, residue_indices, chain_labels, chain_mask, true_tokens, L, B, orders,
+                        shared_order != 0, sampler_seeds, temperature, greedy, tokens, log_probs, scores, ar, chosen);
+  ctx->stream = saved;
+  return st;
+}
+
+hkbs_status hkbs_pmpnn_score(hkbs_pmpnn* ctx, const float* coords, const uint8_t* atom_sources,
+                             const int32_t* residue_indices, const int32_t* chain_labels, const float* chain_mask,
+                             const int32_t* tokens, const int32_t* order, int32_t L, float* log_probs, float* score) {
+  (void)ctx; (void)coords; (void)atom_sources; (void)residue_indices; (void)chain_labels; (void)chain_mask;
+  (void)tokens; (void)order; (void)L; (void)log_probs; (void)score;
+  return fail(HKBS_UNIMPLEMENTED, "teacher-forced scoring is not implemented yet");
+}
+
+hkbs_status hkbs_pmpnn_knn(hkbs_pmpnn* ctx, const float* coords, const uint8_t* atom_sources, int32_t L, int32_t* idx,
+                           float* d2) {
+  hkbs_status st = enter(ctx);
+  if (st != HKBS_OK) return st;
+  if (L < 0) return fail(HKBS_INVALID_ARGUMENT, "residue count is negative");
+  if (L == 0) return HKBS_OK;
+  if (!coords || !atom_sources || !idx || !d2) return fail(HKBS_INVALID_ARGUMENT, "kNN pointers must be non-null");
+  const int K = std::min(kKmax, L);
+  const size_t S = (size_t)L * K;
+  DeviceArena& ar = ctx->arena;
+  if (ar.reserve(input_bytes(L) + encode_bytes(L, K) + (64u << 10)) != hipSuccess)
+    return fail(HKBS_INTERNAL_ERROR, "device workspace allocation failed");
+  ar.reset();
+  Inputs in{};
+  if ((st = upload_inputs(ctx, ar, coords, atom_sources, nullptr, nullptr, nullptr, nullptr, L, in)) != HKBS_OK) return st;
+  EncodeBuffers e = take_encode(ar, L, K);
+  HK_CHECK(launch_knn(in.coords, in.src, L, K, e.idx, e.d2, e.mask, e.ca, ctx->stream), "kNN launch failed");
+  HK_CHECK(hipMemcpyAsync(idx, e.idx, S * 4, hipMemcpyDeviceToHost, ctx->stream), "D2H failed");
+  HK_CHECK(hipMemcpyAsync(d2, e.d2, S * 4, hipMemcpyDeviceToHost, ctx->stream), "D2H failed");
+  HK_CHECK(hipStreamSynchronize(ctx->stream), "kNN kernel failed");
+  return HKBS_OK;
+}
+
+hkbs_status hkbs_pmpnn_encode(hkbs_pmpnn* ctx, const float* coords, const uint8_t* atom_sources,
+                              const int32_t* residue_indices, const int32_t* chain_labels, int32_t L, float* mask,
+                              int32_t* idx, float* h_v, float* h_e) {
+  hkbs_status st = enter(ctx);
+  if (st != HKBS_OK) return st;
+  if (L < 0) return fail(HKBS_INVALID_ARGUMENT, "residue count is negative");
+  if (L == 0) return HKBS_OK;
+  if (!coords || !atom_sources) return fail(HKBS_INVALID_ARGUMENT, "encoder structure pointers must be non-null");
+  const int K = std::min(kKmax, L);
+  const size_t S = (size_t)L * K;
+  DeviceArena& ar = ctx->arena;
+  if (ar.reserve(input_bytes(L) + encode_bytes(L, K) + (64u << 10)) != hipSuccess)
+    return fail(HKBS_INTERNAL_ERROR, "device workspace allocation failed");
+  ar.reset();
+  Inputs in{};
+  if ((st = upload_inputs(ctx, ar, coords, atom_sources, residue_indices, chain_labels, nullptr, nullptr, L, in)) != HKBS_OK)
+    return st;
+  EncodeBuffers e = take_encode(ar, L, K);
+  HK_CHECK(run_encode(ctx, in.coords, in.src, in.resid, in.chain, L, K, e), "encoder launch failed");
+  hipStream_t s = ctx->stream;
+  if (mask) HK_CHECK(hipMemcpyAsync(mask, e.mask, (size_t)L * 4, hipMemcpyDeviceToHost, s), "D2H failed");
+  if (idx) HK_CHECK(hipMemcpyAsync(idx, e.idx, S * 4, hipMemcpyDeviceToHost, s), "D2H failed");
+  if (h_v) HK_CHECK(hipMemcpyAsync(h_v, e.h_v, (size_t)L * kH * 4, hipMemcpyDeviceToHost, s), "D2H failed");
+  if (h_e) HK_CHECK(hipMemcpyAsync(h_e, e.h_e, S * kH * 4, hipMemcpyDeviceToHost, s), "D2H failed");
+  HK_CHECK(hipStreamSynchronize(s), "encoder kernels failed");
+  return HKBS_OK;
+}
+
+hkbs_status hkbs_pmpnn_edge_features(hkbs_pmpnn* ctx, const float* coords, const uint8_t* atom_sources,
+                                     const int32_t* residue_indices, const int32_t* chain_labels, int32_t L,
+                                     float* features) {
+  hkbs_status st = enter(ctx);
+  if (st != HKBS_OK) return st;
+  if (L < 0) return fail(HKBS_INVALID_ARGUMENT, "residue count is negative");
+  if (L == 0) return HKBS_OK;
+  if (!coords || !atom_sources || !features) return fail(HKBS_INVALID_ARGUMENT, "feature pointers must be non-null");
+  const int K = std::min(kKmax, L);
+  const size_t S = (size_t)L * K;
+  DeviceArena& ar = ctx->arena;
+  if (ar.reserve(input_bytes(L) + encode_bytes(L, K) + aligned_bytes<float>(S * kEdgeIn) + (64u << 10)) != hipSuccess)
+    return fail(HKBS_INTERNAL_ERROR, "device workspace allocation failed");
+  ar.reset();
+  Inputs in{};
+  if ((st = upload_inputs(ctx, ar, coords, atom_sources, residue_indices, chain_labels, nullptr, nullptr, L, in)) != HKBS_OK)
+    return st;
+  EncodeBuffers e = take_encode(ar, L, K);
+  float* f = ar.take<float>(S * kEdgeIn);
+  HK_CHECK(launch_knn(in.coords, in.src, L, K, e.idx, e.d2, e.mask, e.ca, ctx->stream), "kNN launch failed");
+  HK_CHECK(launch_edge_features(ctx->model, in.coords, in.src, in.resid, in.chain, e.idx, L, K, f, ctx->stream),
+           "feature launch failed");
+  HK_CHECK(hipMemcpyAsync(features, f, S * kEdgeIn * 4, hipMemcpyDeviceToHost, ctx->stream), "D2H failed");
+  HK_CHECK(hipStreamSynchronize(ctx->stream), "feature kernels failed");
+  return HKBS_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,243 @@
+// Device numerics shared by the kernels.
+//
+// fast_exp_neg and gelu restate the reference's approximations with the same
+// operation order (cpp/include/hikoboshi/primitives/detail/fast_exp_neg.hpp:12-55,
+// cpp/include/hikoboshi/primitives/compute/gelu.hpp:22-51) so that features
+// and activations agree with the CPU path to float rounding.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+namespace hkbs {
+
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+
+__device__ __constant__ static const float kExpNegTable[17] = {
+    1.0F,
+    0.36787944117144232F,
+    0.13533528323661270F,
+    0.04978706836786394F,
+    0.01831563888873418F,
+    0.00673794699908547F,
+    0.00247875217666636F,
+    0.00091188196555452F,
+    0.00033546262790251F,
+    0.00012340980408668F,
+    0.00004539992976248F,
+    0.00001670170079024F,
+    0.00000614421235333F,
+    0.00000226032940698F,
+    0.00000083152871910F,
+    0.00000030590232050F,
+    0.00000011253517471F,
+};
+
+// Table + degree-6 Taylor approximation of exp(x) on [-16, 0].
+__device__ inline float fast_exp_neg(float x) {
+#pragma clang fp contract(off)
+  if (x != x) return x;
+  float neg_x = -x;
+  if (neg_x > 16.0F) return 0.0F;
+  if (neg_x < 0.0F) neg_x = 0.0F;
+  int n = static_cast<int>(neg_x + 0.5F);
+  if (n > 16) n = 16;
+  const float r = -(neg_x - static_cast<float>(n));
+  const float e =
+      1.0F +
+      r * (1.0F +
+           r * (0.5F +
+                r * (1.0F / 6.0F +
+                     r * (1.0F / 24.0F + r * (1.0F / 120.0F + r * (1.0F / 720.0F))))));
+  return kExpNegTable[n] * e;
+}
+
+// GELU with the Abramowitz-Stegun 7.1.26 erf used by the reference.
+__device__ inline float gelu(float x) {
+#pragma clang fp contract(off)
+  float v = x * 0.7071067811865475F;
+  float sign = 1.0F;
+  if (v < 0.0F) {
+    sign = -1.0F;
+    v = -v;
+  }
+  float erfv;
+  if (v > 4.0F) {
+    erfv = sign;
+  } else {
+    const float t = 1.0F / (1.0F + 0.3275911F * v);
+    const float poly =
+        (((((1.061405429F * t + -1.453152027F) * t) + 1.421413741F) * t + -0.284496736F) * t +
+         0.254829592F) *
+        t;
+    erfv = sign * (1.0F - poly * fast_exp_neg(-(v * v)));
+  }
+  return 0.5F * x * (1.0F + erfv);
+}
+
+__device__ inline floatx4 mfma16(float a, float b, floatx4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
+}
+
+// One wave computes an (16 MB) x (16 NB) tile of A . W^T with fp32 MFMA.
+//   A : LDS, row-major with leading dimension lda (floats, multiple of 4).
+//   Wp: kpack16 weights of a layer with N output columns.
+//   n0: first output column of the wave's tile.
+// acc[mb][nb][i] holds D[row = 16 mb + 4 (lane / 16) + i][col = n0 + 16 nb + lane % 16].
+template <int MB, int NB>
+__device__ inline void mfma_tile(const float* __restrict__ A, int lda,
+                                 const float* __restrict__ Wp, int N, int n0, int kdim,
+                                 floatx4 (&acc)[MB][NB]) {
+  const int lane = threadIdx.x & 63;
+  const int r = lane & 15;
+  const int g = lane >> 4;
+  for (int kb = 0; kb < kdim / 16; ++kb) {
+    float4 a[MB];
+    float4 b[NB];
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb)
+      b[nb] = *reinterpret_cast<const float4*>(Wp + ((size_t)kb * N + n0 + nb * 16 + r) * 16 + 4 * g);
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb)
+      a[mb] = *reinterpret_cast<const float4*>(A + (mb * 16 + r) * lda + kb * 16 + 4 * g);
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+      for (int nb = 0; nb < NB; ++nb) {
+        acc[mb][nb] = mfma16(a[mb].x, b[nb].x, acc[mb][nb]);
+        acc[mb][nb] = mfma16(a[mb].y, b[nb].y, acc[mb][nb]);
+        acc[mb][nb] = mfma16(a[mb].z, b[nb].z, acc[mb][nb]);
+        acc[mb][nb] = mfma16(a[mb].w, b[nb].w, acc[mb][nb]);
+      }
+  }
+}
+
+template <int MB, int NB>
+__device__ inline void zero_acc(floatx4 (&acc)[MB][NB]) {
+#pragma unroll
+  for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb) acc[mb][nb] = floatx4{0.F, 0.F, 0.F, 0.F};
+}
+
+// Writes an accumulator tile to LDS C (leading dimension ldc) at column n0.
+template <int MB, int NB>
+__device__ inline void store_acc(const floatx4 (&acc)[MB][NB], float* C, int ldc, int n0) {
+  const int lane = threadIdx.x & 63;
+  const int r = lane & 15;
+  const int g = lane >> 4;
+#pragma unroll
+  for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) C[(mb * 16 + 4 * g + i) * ldc + n0 + nb * 16 + r] = acc[mb][nb][i];
+}
+
+// ---------------------------------------------------------------------------
+// Reference-order arithmetic.
+//
+// The reference's default linear layer accumulates every output element as
+// one sequential float sum over k starting from 0.0f, each product rounded
+// before the add (no FMA), then adds the bias
+// (cpp/primitives/linalg/gemm_scalar_fast.cpp:107-176,249-314;
+// cpp/include/hikoboshi/modules/mpnn/detail/mpnn_inner_inline.hpp:319-339).
+// seq_gemm reproduces that rounding bit for bit: each thread owns an RM x CN
+// block of outputs and walks k in order; parallelism comes from the outputs.
+//   A   : LDS, k-major: A[k * lda + row].
+//   W   : global, transposed weights W[k * ldw + col] (col < NC).
+//   Wbuf: LDS staging for KC x NC floats.
+// The thread's block is rows [r0, r0 + RM), cols [c0, c0 + CN). Every thread
+// of the block must call it (it contains barriers); it starts with a barrier,
+// so LDS writes made before the call are visible.
+template <int RM, int CN, int NC, int KC>
+__device__ inline void seq_gemm(float (&acc)[RM][CN], const float* A, int lda, int r0,
+                                const float* __restrict__ W, int ldw, int kd, float* Wbuf, int c0) {
+#pragma clang fp contract(off)
+  for (int k0 = 0; k0 < kd; k0 += KC) {
+    __syncthreads();
+    for (int i = threadIdx.x; i < KC * (NC / 4); i += blockDim.x) {
+      const int kk = i / (NC / 4);
+      const int c4 = i % (NC / 4);
+      float4 v = make_float4(0.F, 0.F, 0.F, 0.F);
+      if (k0 + kk < kd) v = *reinterpret_cast<const float4*>(W + (size_t)(k0 + kk) * ldw + 4 * c4);
+      *reinterpret_cast<float4*>(Wbuf + kk * NC + 4 * c4) = v;
+    }
+    __syncthreads();
+    const int kn = (kd - k0) < KC ? (kd - k0) : KC;
+    for (int kk = 0; kk < kn; ++kk) {
+      float a[RM];
+      float w[CN];
+      const float* ap = A + (size_t)(k0 + kk) * lda + r0;
+      if constexpr (RM % 4 == 0) {
+#pragma unroll
+        for (int i = 0; i < RM; i += 4) {
+          const float4 v = *reinterpret_cast<const float4*>(ap + i);
+          a[i] = v.x; a[i + 1] = v.y; a[i + 2] = v.z; a[i + 3] = v.w;
+        }
+      } else {
+#pragma unroll
+        for (int i = 0; i < RM; i += 2) {
+          const float2 v = *reinterpret_cast<const float2*>(ap + i);
+          a[i] = v.x; a[i + 1] = v.y;
+        }
+      }
+      const float* wp = Wbuf + kk * NC + c0;
+#pragma unroll
+      for (int j = 0; j < CN; j += 4) {
+        const float4 v = *reinterpret_cast<const float4*>(wp + j);
+        w[j] = v.x; w[j + 1] = v.y; w[j + 2] = v.z; w[j + 3] = v.w;
+      }
+#pragma unroll
+      for (int i = 0; i < RM; ++i)
+#pragma unroll
+        for (int j = 0; j < CN; ++j) acc[i][j] = acc[i][j] + a[i] * w[j];
+    }
+  }
+}
+
+// Welford LayerNorm of one 128-wide row read from a k-major LDS column
+// (x[d * ld]), written to out[d * ld] (may alias). Reference order of
+// cpp/primitives/compute/layer_norm_scalar.cpp:8-40, eps 1e-5.
+__device__ inline void welford_ln_col(const float* x, float* out, int ld, const float* __restrict__ g,
+                                      const float* __restrict__ b) {
+#pragma clang fp contract(off)
+  float mean = 0.0F, m2 = 0.0F;
+  for (int d = 0; d < 128; ++d) {
+    const float v = x[d * ld];
+    const float count = static_cast<float>(d + 1);
+    const float delta = v - mean;
+    mean += delta / count;
+    const float delta2 = v - mean;
+    m2 += delta * delta2;
+  }
+  const float var = m2 / 128.0F;
+  const float inv_std = 1.0F / sqrtf(var + 1.0e-5F);
+  for (int d = 0; d < 128; ++d) {
+    const float normalized = (x[d * ld] - mean) * inv_std;
+    out[d * ld] = normalized * g[d] + b[d];
+  }
+}
+
+// Two-pass LayerNorm statistics of a 128-float row held as 2 floats per lane
+// of one wave (lane holds elements lane and lane + 64). eps = 1e-5
+// (cpp/include/hikoboshi/universal/detail/mpnn_d64_weights.hpp:27).
+__device__ inline float wave_sum(float v) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+  return v;
+}
+
+__device__ inline void ln_row_wave(const float* in, const float* g, const float* b, float* out) {
+  const int lane = threadIdx.x & 63;
+  const float x0 = in[lane], x1 = in[lane + 64];
+  const float mean = wave_sum(x0 + x1) * (1.0F / 128.0F);
+  const float d0 = x0 - mean, d1 = x1 - mean;
+  const float var = wave_sum(d0 * d0 + d1 * d1) * (1.0F / 128.0F);
+  const float inv = 1.0F / sqrtf(var + 1.0e-5F);
+  out[lane] = d0 * inv * g[lane] + b[lane];
+  out[lane + 64] = d1 * inv * g[lane + 64] + b[lane + 64];
+}
+
+}  // namespace hkbs

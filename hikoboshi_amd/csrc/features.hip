@@ -1,0 +1,194 @@
+// Edge featurisation and edge embedding.
+//
+// Features per edge slot (residue r, neighbour j = idx[r,k]):
+//   [0,16)    positional one-hot linear: W_pos[d, class] + b_pos[d],
+//             class = 65 across chains, else clamp(res_r - res_j, +-32) + 32
+//             (cpp/modules/mpnn/edge_rbf_features_scalar.cpp:45-76);
+//   [16,416)  for each of the 25 atom pairs (query atom of r, neighbour atom
+//             of j; cpp/primitives/compute/atom_pair_distance_scalar.cpp:21-72)
+//             16 Gaussian RBFs of D = sqrt(sum (n - q)^2 + 1e-6) with centres
+//             2 + f * 20/15 and 2 sigma^2 from sigma = 20 / (16 / 0.70710678)
+//             (rbf_scalar.cpp:10-35, edge_rbf_features_scalar.cpp:135-137);
+//             zero when either atom is missing; the whole row is zero for an
+//             invalid neighbour. Float operations follow the reference order
+//             with contraction disabled, so features are bit-identical to
+//             the CPU path.
+// Edge embedding (inverse_fold_scalar.cpp:236-279):
+//   h_E = W_e . LayerNorm(W_edge . f) + b_e  (W_edge has no bias),
+// fused in one kernel: a 32-slot tile of features is built in LDS (k-major),
+// multiplied by W_edge, normalised and multiplied by W_e without leaving the
+// CU, all in the reference's rounding order (h_E is bit-identical).
+#include "device_math.hpp"
+#include "pmpnn_internal.hpp"
+
+namespace hkbs {
+namespace {
+
+__device__ __constant__ static const int8_t kPairQ[25] = {1, 0, 2, 3, 4, 1, 1, 1, 1, 0, 0, 0, 4,
+                                                          4, 3, 0, 2, 3, 4, 2, 3, 4, 2, 3, 2};
+__device__ __constant__ static const int8_t kPairN[25] = {1, 0, 2, 3, 4, 0, 2, 3, 4, 2, 3, 4, 2,
+                                                          3, 2, 1, 1, 1, 1, 0, 0, 0, 4, 4, 3};
+
+// Writes the 16 features of chunk c (0 = positional, 1..25 = atom pair c-1)
+// of edge slot (r, j) to out[0..16).
+__device__ inline void edge_chunk(const ModelDev& m, const float* __restrict__ coords,
+                                  const uint8_t* __restrict__ src, const int32_t* __restrict__ resid,
+                                  const int32_t* __restrict__ chain, int L, int r, int j, int c,
+                                  float* out) {
+#pragma clang fp contract(off)
+  if (j < 0 || j >= L) {
+#pragma unroll
+    for (int f = 0; f < 16; ++f) out[f] = 0.0F;
+    return;
+  }
+  if (c == 0) {
+    int cls;
+    const int ci = chain ? chain[r] : 0;
+    const int cj = chain ? chain[j] : 0;
+    if (ci != cj) {
+      cls = kPosClasses - 1;
+    } else {
+      int off = (resid ? resid[r] : r) - (resid ? resid[j] : j);
+      off = off < -32 ? -32 : (off > 32 ? 32 : off);
+      cls = off + 32;
+    }
+#pragma unroll
+    for (int d = 0; d < 16; ++d) out[d] = m.pos_w[d * kPosClasses + cls] + m.pos_b[d];
+    return;
+  }
+  const int p = c - 1;
+  const int qa = kPairQ[p], na = kPairN[p];
+  if (src[(size_t)r * 5 + qa] == 0 || src[(size_t)j * 5 + na] == 0) {
+#pragma unroll
+    for (int f = 0; f < 16; ++f) out[f] = 0.0F;
+    return;
+  }
+  const float* qx = coords + ((size_t)r * 5 + qa) * 3;
+  const float* nx = coords + ((size_t)j * 5 + na) * 3;
+  float sq = 0.0F;
+#pragma unroll
+  for (int ax = 0; ax < 3; ++ax) {
+    const float delta = nx[ax] - qx[ax];
+    sq += delta * delta;
+  }
+  sq = sq + 1.0e-6F;
+  const float dist = sqrtf(sq);
+  const float center_step = (22.0F - 2.0F) / static_cast<float>(kRbf - 1);
+  const float sigma = (22.0F - 2.0F) / (static_cast<float>(kRbf) / 0.7071067811865475F);
+  const float two_sigma_sq = 2.0F * sigma * sigma;
+#pragma unroll
+  for (int f = 0; f < 16; ++f) {
+    const float center = 2.0F + static_cast<float>(f) * center_step;
+    const float delta = dist - center;
+    out[f] = fast_exp_neg(-(delta * delta) / two_sigma_sq);
+  }
+}
+
+__global__ __launch_bounds__(256) void edge_features_kernel(ModelDev m, const float* __restrict__ coords,
+                                                            const uint8_t* __restrict__ src,
+                                                            const int32_t* __restrict__ resid,
+                                                            const int32_t* __restrict__ chain,
+                                                            const int32_t* __restrict__ idx, int L, int K,
+                                                            float* __restrict__ features) {
+  const size_t task = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const size_t S = (size_t)L * K;
+  if (task >= S * 26) return;
+  const size_t slot = task / 26;
+  const int c = static_cast<int>(task % 26);
+  const int r = static_cast<int>(slot / K);
+  float out[16];
+  edge_chunk(m, coords, src, resid, chain, L, r, idx[slot], c, out);
+  float* dst = features + slot * kEdgeIn + c * 16;
+#pragma unroll
+  for (int f = 0; f < 16; ++f) dst[f] = out[f];
+}
+
+constexpr int kTile = 32;  // edge slots per workgroup
+constexpr int kLdT = 36;   // k-major leading dimension
+
+// h_E = W_e . LN(W_edge . f) + b_e in the reference's rounding order
+// (sequential sums without FMA, Welford LayerNorm).
+__global__ __launch_bounds__(256) void edge_embed_kernel(ModelDev m, const float* __restrict__ coords,
+                                                         const uint8_t* __restrict__ src,
+                                                         const int32_t* __restrict__ resid,
+                                                         const int32_t* __restrict__ chain,
+                                                         const int32_t* __restrict__ idx, int L, int K,
+                                                         float* __restrict__ h_e) {
+#pragma clang fp contract(off)
+  __shared__ __attribute__((aligned(16))) float A[kEdgeIn * kLdT];
+  __shared__ __attribute__((aligned(16))) float X[kH * kLdT];
+  __shared__ __attribute__((aligned(16))) float Wbuf[32 * kH];
+  const size_t S = (size_t)L * K;
+  const size_t slot0 = (size_t)blockIdx.x * kTile;
+  const int rg = threadIdx.x / 32, cg = threadIdx.x % 32;
+  const int row0 = rg * 4, col0 = cg * 4;
+
+  for (int task = threadIdx.x; task < kTile * 26; task += 256) {
+    const int row = task % kTile;
+    const int c = task / kTile;
+    const size_t slot = slot0 + row;
+    float out[16];
+    if (slot < S) {
+      const int r = static_cast<int>(slot / K);
+      edge_chunk(m, coords, src, resid, chain, L, r, idx[slot], c, out);
+    } else {
+#pragma unroll
+      for (int f = 0; f < 16; ++f) out[f] = 0.0F;
+    }
+#pragma unroll
+    for (int f = 0; f < 16; ++f) A[(c * 16 + f) * kLdT + row] = out[f];
+  }
+  float acc[4][4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc[i][j] = 0.0F;
+  seq_gemm<4, 4, kH, 32>(acc, A, kLdT, row0, m.edge_t, kH, kEdgeIn, Wbuf, col0);
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) X[(col0 + j) * kLdT + row0 + i] = acc[i][j];
+  __syncthreads();
+  if (threadIdx.x < kTile) welford_ln_col(X + threadIdx.x, A + threadIdx.x, kLdT, m.ne_g, m.ne_b);
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc[i][j] = 0.0F;
+  seq_gemm<4, 4, kH, 32>(acc, A, kLdT, row0, m.We_t, kH, kH, Wbuf, col0);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const size_t slot = slot0 + row0 + i;
+    if (slot < S) {
+      float4 v;
+      v.x = acc[i][0] + m.We_b[col0 + 0];
+      v.y = acc[i][1] + m.We_b[col0 + 1];
+      v.z = acc[i][2] + m.We_b[col0 + 2];
+      v.w = acc[i][3] + m.We_b[col0 + 3];
+      *reinterpret_cast<float4*>(h_e + slot * kH + col0) = v;
+    }
+  }
+}
+
+}  // namespace
+
+hipError_t launch_edge_features(const ModelDev& m, const float* coords, const uint8_t* atom_src,
+                                const int32_t* resid, const int32_t* chain, const int32_t* idx, int L, int K,
+                                float* features, hipStream_t stream) {
+  const size_t tasks = (size_t)L * K * 26;
+  if (tasks == 0) return hipSuccess;
+  edge_features_kernel<<<(unsigned)((tasks + 255) / 256), 256, 0, stream>>>(m, coords, atom_src, resid, chain,
+                                                                           idx, L, K, features);
+  return hipGetLastError();
+}
+
+hipError_t launch_edge_embed(const ModelDev& m, const float* coords, const uint8_t* atom_src,
+                             const int32_t* resid, const int32_t* chain, const int32_t* idx, int L, int K,
+                             float* h_e, hipStream_t stream) {
+  const size_t S = (size_t)L * K;
+  if (S == 0) return hipSuccess;
+  edge_embed_kernel<<<(unsigned)((S + kTile - 1) / kTile), 256, 0, stream>>>(m, coords, atom_src, resid, chain,
+                                                                            idx, L, K, h_e);
+  return hipGetLastError();
+}
+
+}  // namespace hkbs

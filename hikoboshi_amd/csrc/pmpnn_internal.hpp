@@ -1,0 +1,114 @@
+// Internal declarations shared by the HIP kernels and the C-ABI layer.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstddef>
+#include <cstdint>
+
+namespace hkbs {
+
+constexpr int kH = 128;        // hidden width
+constexpr int kV = 21;         // vocabulary
+constexpr int kKmax = 48;      // neighbours
+constexpr int kRbf = 16;       // RBF centres
+constexpr int kPairs = 25;     // atom pairs
+constexpr int kPos = 16;       // positional features
+constexpr int kPosClasses = 66;
+constexpr int kEdgeIn = 416;   // 16 + 25 * 16
+constexpr int kFF = 512;       // FFN hidden
+constexpr int kLayers = 3;
+constexpr int kTensors = 118;
+
+// Packed-weight layouts used on the device.
+//  * "kpack16" for MFMA B operands: W [N][K] (row-major, out x in) stored as
+//    Wp[K/16][N][16] with Wp[kb][n][j] = W[n][16 kb + j]. One float4 load per
+//    lane per four MFMA k-steps, 1 KiB contiguous per 16 columns.
+//  * "t" (transposed) for GEMVs: Wt[K][N] = W[n][k].
+struct EncLayerDev {
+  const float* W1_t;    // [384][128]  input order [h_i | e_ij | h_j]
+  const float* W2_t;    // [128][128]
+  const float* W3_t;    // [128][128]
+  const float* W11_t;   // [384][128]
+  const float* W12_t;   // [128][128]
+  const float* W13_t;   // [128][128]
+  const float* Win_t;   // [128][512]
+  const float* Wout_t;  // [512][128]
+  const float *b1, *b2, *b3, *b11, *b12, *b13, *bin, *bout;
+  const float *n1g, *n1b, *n2g, *n2b, *n3g, *n3b;
+};
+
+struct DecLayerDev {
+  const float* W1a_t;  // [128][128]
+  const float* W2_p;   // kpack16 128 -> 128
+  const float* W3_t;   // [128][128]
+  const float* Win_t;  // [128][512]
+  const float* Wout_t; // [512][128]
+  const float* W1d_t;  // [128][128]
+  const float* T;      // [21][128]: W1c . W_s[v]
+  const float *b1, *b2, *b3, *bin, *bout;
+  const float *n1g, *n1b, *n2g, *n2b;
+};
+
+struct ModelDev {
+  const float* pos_w;  // [16][66]
+  const float* pos_b;  // [16]
+  const float* edge_t; // [416][128]
+  const float *ne_g, *ne_b;
+  const float* We_t;   // [128][128]
+  const float* We_b;
+  const float* Ws;     // [21][128]
+  EncLayerDev enc[kLayers];
+  DecLayerDev dec[kLayers];
+  const float* W1b_dec_p;  // kpack16 128 -> 384: rows = [W1b_0; W1b_1; W1b_2] (decoder)
+  const float* W1d_dec_p;  // kpack16 128 -> 384: rows = [W1d_0; W1d_1; W1d_2]
+  const float* Wlog_t;     // [128][21]
+  const float* blog;       // [21]
+};
+
+// Launchers (each enqueues on `stream`; shapes are validated by the caller).
+hipError_t launch_knn(const float* coords, const uint8_t* atom_src, int L, int K, int32_t* idx,
+                      float* d2, float* mask, float4* ca_scratch, hipStream_t stream);
+// pos[b][orders[b][s]] = s for each of n_orders orders of length L.
+hipError_t launch_positions(const int32_t* orders, int L, int n_orders, int shared, int32_t* pos,
+                            hipStream_t stream);
+hipError_t launch_edge_features(const ModelDev& m, const float* coords, const uint8_t* atom_src,
+                                const int32_t* resid, const int32_t* chain, const int32_t* idx,
+                                int L, int K, float* features, hipStream_t stream);
+hipError_t launch_edge_embed(const ModelDev& m, const float* coords, const uint8_t* atom_src,
+                             const int32_t* resid, const int32_t* chain, const int32_t* idx, int L,
+                             int K, float* h_e, hipStream_t stream);
+struct EncoderScratch {
+  float* prefix;   // [L][256]: sequential partial sums over the h_i inputs of [W11 | next W1]
+  float* msg_sum;  // [L][128]
+};
+// Fills n floats with zero (a kernel, so it can sit inside a captured graph).
+hipError_t launch_zero(float* p, size_t n, hipStream_t stream);
+hipError_t launch_encoder(const ModelDev& m, const int32_t* idx, const float* mask, int L, int K,
+                          float* h_v, float* h_e, const EncoderScratch& ws, hipStream_t stream);
+hipError_t launch_decoder_precompute(const ModelDev& m, const float* h_v, const float* h_e, int L,
+                                     int K, float* E1, float* Q, hipStream_t stream);
+struct DecodeArgs {
+  const int32_t* idx;     // [L][K]
+  const float* mask;      // [L]
+  const float* h_v;       // [L][128] encoder output
+  const float* E1;        // [3][S][128]
+  const float* Q;         // [3][L][128]
+  const int32_t* orders;  // [B][L] or [L]
+  int shared_order;
+  const int32_t* pos;     // [B][L] or [L]: position of residue r in the order
+  const float* chain_mask;   // [L] or null
+  const int32_t* true_tokens; // [L] or null
+  const uint64_t* seeds;  // [B]
+  float temperature;
+  int greedy;
+  int L, K, B;
+  float* R;               // [B][3][L][128] workspace
+  int32_t* tokens;        // [B][L]
+  float* log_probs;       // [B][L][21] or null
+  float* scores;          // [B] or null
+  float* chosen_lp;       // [B][L] workspace: log-prob of the written token
+};
+hipError_t launch_decode(const ModelDev& m, const DecodeArgs& a, hipStream_t stream);
+
+}  // namespace hkbs

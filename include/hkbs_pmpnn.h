@@ -1,0 +1,152 @@
+/*
+ * hkbs_pmpnn.h - C ABI of the MI355X-native ProteinMPNN v_48_020 design path.
+ *
+ * The library replaces, for one GPU, the reference's scalar module seam
+ *   hikoboshi::modules::mpnn::proteinmpnn_inverse_fold_scalar
+ *     (cpp/include/hikoboshi/modules/mpnn/inverse_fold.hpp:113-115)
+ *   hikoboshi::modules::mpnn::proteinmpnn_teacher_forced_forward_scalar
+ *     (cpp/include/hikoboshi/modules/mpnn/inverse_fold.hpp:140-142)
+ * and the per-sample loop of
+ *   hikoboshi::algorithms::inverse_fold_proteinmpnn_v48_020
+ *     (cpp/algorithms/inverse_fold.cpp:292-337)
+ * by one batched call that encodes the backbone once and decodes all
+ * sequences together. Everything crosses the boundary as plain pointers and
+ * sizes; no C++ or framework types.
+ *
+ * Conventions (mirroring the reference):
+ *  - Status codes are the reference's StatusCode values
+ *    (cpp/include/hikoboshi/universal/status.hpp:12-19). HIP failures map to
+ *    HKBS_UNAVAILABLE (no device) or HKBS_INTERNAL_ERROR. hkbs_last_error()
+ *    returns a static detail string for the calling thread's last failure.
+ *  - Arrays are row-major. coords is [L,5,3] float in the atom order
+ *    N, CA, C, O, CB; atom_sources is [L,5] uint8 with the reference's
+ *    AtomSource codes (0 Missing, 1 Observed, 2 Inferred, 3 Virtual;
+ *    cpp/include/hikoboshi/universal/structure.hpp:21-38).
+ *  - Optional inputs may be NULL: residue_indices (default 0..L-1),
+ *    chain_labels (default one chain), chain_mask (default ones),
+ *    true_tokens (default: fallback token 20 for residues not designed).
+ *  - Calls on one context are serialised by the caller (a context owns one
+ *    HIP stream and its workspace). Distinct contexts are independent.
+ */
+#ifndef HKBS_PMPNN_H
+#define HKBS_PMPNN_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef int32_t hkbs_status;
+enum {
+  HKBS_OK = 0,
+  HKBS_INVALID_ARGUMENT = 1,
+  HKBS_FAILED_PRECONDITION = 2,
+  HKBS_UNAVAILABLE = 3,
+  HKBS_UNIMPLEMENTED = 4,
+  HKBS_INTERNAL_ERROR = 5
+};
+
+/* Decode-order modes for hkbs_pmpnn_design. */
+enum {
+  /* Per sequence b: the reference's random order seeded by order_seeds[b]
+   * (cpp/modules/mpnn/decode_order_scalar.cpp:89-115). */
+  HKBS_ORDER_RANDOM = 0,
+  /* orders holds one permutation per sequence, [B,L]
+   * (use_input_decoding_order, decode_order_scalar.cpp:68-87). */
+  HKBS_ORDER_INPUT_PER_SEQUENCE = 1,
+  /* orders holds one permutation [L] shared by every sequence. */
+  HKBS_ORDER_INPUT_SHARED = 2,
+  /* N-to-C order 0..L-1 (cpp/algorithms/inverse_fold.cpp:273-276). */
+  HKBS_ORDER_N_TO_C = 3
+};
+
+typedef struct hkbs_pmpnn hkbs_pmpnn;
+
+/* Static detail text of the calling thread's last non-OK status. */
+const char* hkbs_last_error(void);
+
+/* Library version string. */
+const char* hkbs_version(void);
+
+/* Number of visible HIP devices (0 when none; never fails). */
+int32_t hkbs_device_count(void);
+
+/* Creates a context on HIP device `device` from the v_48_020 weight package
+ * bytes (safetensors, 118 F32 tensors). Replaces the embedded weight view
+ * binding of cpp/weights/embedded_proteinmpnn_v48_eps020.cpp:136-286.
+ * Returns HKBS_INVALID_ARGUMENT for a malformed package and
+ * HKBS_UNAVAILABLE when the device cannot be used. */
+hkbs_status hkbs_pmpnn_create(const uint8_t* safetensors, size_t nbytes, int32_t device,
+                              hkbs_pmpnn** out);
+
+void hkbs_pmpnn_destroy(hkbs_pmpnn* ctx);
+
+/* Batched autoregressive design: B sequences on one backbone of L residues.
+ * Sequence b follows proteinmpnn_inverse_fold_scalar with
+ * options.seed = sampler_seeds[b] and, for HKBS_ORDER_RANDOM,
+ * options.decode_order_seed = order_seeds[b]; greedy != 0 or
+ * temperature <= 0 selects argmax (cpp/modules/mpnn/sampler_scalar.cpp:106-131).
+ * Outputs (host memory): tokens [B,L]; log_probs [B,L,21] temperature-scaled
+ * (or NULL); orders_out [B,L] (or NULL); scores [B] mean NLL (or NULL).
+ * Synchronous. */
+hkbs_status hkbs_pmpnn_design(hkbs_pmpnn* ctx, const float* coords, const uint8_t* atom_sources,
+                              const int32_t* residue_indices, const int32_t* chain_labels,
+                              const float* chain_mask, const int32_t* true_tokens, int32_t L,
+                              int32_t B, int32_t order_mode, const int32_t* orders,
+                              const uint64_t* order_seeds, const uint64_t* sampler_seeds,
+                              float temperature, int32_t greedy, int32_t* tokens,
+                              float* log_probs, int32_t* orders_out, float* scores);
+
+/* Device-resident variant: every pointer argument is device memory, orders
+ * is [B,L] or [L] (shared != 0), and the call is enqueued on `stream`
+ * (a hipStream_t; NULL = the context's stream) without synchronising.
+ * residue_indices / chain_labels / chain_mask / true_tokens may be NULL. */
+hkbs_status hkbs_pmpnn_design_device(hkbs_pmpnn* ctx, const float* coords,
+                                     const uint8_t* atom_sources, const int32_t* residue_indices,
+                                     const int32_t* chain_labels, const float* chain_mask,
+                                     const int32_t* true_tokens, int32_t L, int32_t B,
+                                     const int32_t* orders, int32_t shared_order,
+                                     const uint64_t* sampler_seeds, float temperature,
+                                     int32_t greedy, int32_t* tokens, float* log_probs,
+                                     float* scores, void* stream);
+
+/* Teacher-forced scoring of one protein (proteinmpnn_teacher_forced_forward_scalar,
+ * cpp/modules/mpnn/inverse_fold_scalar.cpp:905-952): plain log_softmax
+ * log-probs [L,21] and mean NLL. order may be NULL (N-to-C). Host memory. */
+hkbs_status hkbs_pmpnn_score(hkbs_pmpnn* ctx, const float* coords, const uint8_t* atom_sources,
+                             const int32_t* residue_indices, const int32_t* chain_labels,
+                             const float* chain_mask, const int32_t* tokens,
+                             const int32_t* order, int32_t L, float* log_probs, float* score);
+
+/* Host helper: the reference's decoding order (decode_order_scalar.cpp:61-116)
+ * for one sequence; chain_mask may be NULL. Bit-exact on the same libm. */
+hkbs_status hkbs_pmpnn_decode_order(const float* chain_mask, const uint8_t* atom_sources,
+                                    int32_t L, uint64_t seed, int32_t* order);
+
+/* Unit-parity entry points (host memory in/out). */
+
+/* CA kNN graph: idx [L,K] and squared distances d2 [L,K], K = min(48, L)
+ * (knn_scalar, cpp/primitives/compute/knn_scalar.cpp:72-168). */
+hkbs_status hkbs_pmpnn_knn(hkbs_pmpnn* ctx, const float* coords, const uint8_t* atom_sources,
+                           int32_t L, int32_t* idx, float* d2);
+
+/* Featurise + encode (inverse_fold_scalar.cpp:300-352): residue mask [L],
+ * neighbour idx [L,K], node states h_V [L,128], edge states h_E [L,K,128].
+ * Any output may be NULL. */
+hkbs_status hkbs_pmpnn_encode(hkbs_pmpnn* ctx, const float* coords, const uint8_t* atom_sources,
+                              const int32_t* residue_indices, const int32_t* chain_labels,
+                              int32_t L, float* mask, int32_t* idx, float* h_v, float* h_e);
+
+/* Edge features [L,K,416] = [positional 16 | 25 atom pairs x 16 RBF]
+ * (edge_rbf_features_scalar, cpp/modules/mpnn/edge_rbf_features_scalar.cpp:117-152). */
+hkbs_status hkbs_pmpnn_edge_features(hkbs_pmpnn* ctx, const float* coords,
+                                     const uint8_t* atom_sources, const int32_t* residue_indices,
+                                     const int32_t* chain_labels, int32_t L, float* features);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* HKBS_PMPNN_H */

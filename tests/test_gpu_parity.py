@@ -1,0 +1,218 @@
+"""GPU parity: the HIP library through its C ABI against the CPU oracle.
+
+Bars (from the design-path contract): kNN neighbour indices and decoding
+orders bit-exact; per-position log-probs within 1e-4 absolute in fp32;
+sampled sequences identical except at positions whose CDF gap is below
+CDF_TOL (forced replay: the oracle re-runs the GPU's token trajectory through
+the reference arithmetic and reports its own draw at every position).
+"""
+import numpy as np
+import pytest
+
+from hikoboshi_amd import _lib, backbone, pdb
+
+from .conftest import FIXTURES, golden_cases
+
+pytestmark = pytest.mark.gpu
+
+LP_TOL = 1e-4  # fp32 per-position log-prob tolerance
+CDF_TOL = 1e-4  # a token may differ only where the draw is this close to a CDF boundary
+
+
+def _say(msg):
+    print(msg, flush=True)
+
+
+# ------------------------------------------------------------------- kNN --
+
+def _knn_cases():
+    bb = backbone.single_chain(300, 11)
+    src = bb.atom_sources.copy()
+    src[[0, 42, 299], 3] = 0  # invalid residues
+    cases = [("L300", bb), ("L300_invalid", backbone.Backbone(bb.coords, src)),
+             ("complex4x256", backbone.tetrahedral_complex(256, 7)), ("L7", backbone.single_chain(7, 1)),
+             ("L1", backbone.single_chain(1, 1)), ("L4000", backbone.single_chain(4000, 3))]
+    grid = backbone.single_chain(90, 2)
+    g = grid.coords.copy()
+    g[:, 1] = np.round(g[:, 1])  # integer CA grid -> exact distance ties
+    cases.append(("ties", backbone.Backbone(g, grid.atom_sources)))
+    return cases
+
+
+@pytest.mark.parametrize("name,bb", _knn_cases(), ids=lambda v: v if isinstance(v, str) else "")
+def test_knn_bit_exact(gpu_ctx, oracle, name, bb):
+    _say(f"knn {name} L={bb.L}")
+    idx, d2 = gpu_ctx.knn(bb.coords, bb.atom_sources)
+    valid = (bb.atom_sources[:, :4] != 0).all(1).astype(np.uint8)
+    ca = np.where(bb.atom_sources[:, 1:2] != 0, bb.coords[:, 1], 0).astype(np.float32)
+    oidx, od2 = oracle.knn(ca, valid, min(48, bb.L))
+    np.testing.assert_array_equal(idx, oidx)
+    np.testing.assert_array_equal(d2, od2)
+
+
+# -------------------------------------------------------------- features --
+
+@pytest.mark.parametrize("which", ["single", "complex", "missing"])
+def test_edge_features(gpu_ctx, oracle, which):
+    if which == "single":
+        bb = backbone.single_chain(120, 7)
+    elif which == "complex":
+        bb = backbone.tetrahedral_complex(40, 3)
+    else:
+        bb = backbone.single_chain(60, 5)
+        src = bb.atom_sources.copy()
+        src[[3, 9], 4] = 0
+        src[20, 2] = 0
+        bb = backbone.Backbone(bb.coords, src)
+    _say(f"features {which}")
+    f = gpu_ctx.edge_features(bb.coords, bb.atom_sources, bb.residue_indices, bb.chain_labels)
+    _, of = oracle.edge_features(bb)
+    np.testing.assert_array_equal(f, of)  # same float operations in the same order
+
+
+@pytest.mark.parametrize("L", [120, 300, 30])
+def test_encoder(gpu_ctx, oracle, L):
+    bb = backbone.single_chain(L, 7)
+    if L == 30:  # masked residues and a missing CB
+        src = bb.atom_sources.copy()
+        src[[2, 17], 3] = 0
+        src[9, 4] = 0
+        bb = backbone.Backbone(bb.coords, src)
+    _say(f"encode L={L}")
+    mask, idx, hv, he = gpu_ctx.encode(bb.coords, bb.atom_sources)
+    omask, oidx, ohv, ohe = oracle.encode(bb)
+    np.testing.assert_array_equal(idx, oidx)
+    np.testing.assert_array_equal(mask, omask)
+    dv, de = np.abs(hv - ohv).max(), np.abs(he - ohe).max()
+    _say(f"  h_V max|d|={dv:.3g} h_E max|d|={de:.3g}")
+    # the encoder reproduces the reference's rounding order: bit-identical
+    np.testing.assert_array_equal(hv, ohv)
+    np.testing.assert_array_equal(he, ohe)
+
+
+# ---------------------------------------------------------------- design --
+
+def replay(oracle, enc, order, seed, temperature, tokens, log_probs, greedy=False, chain_mask=None,
+           true_tokens=None):
+    """Forced replay of one GPU sequence; returns (max |dlogp|, mismatches, unexplained)."""
+    out = oracle.decode(enc, order, seed, temperature, greedy=greedy, chain_mask=chain_mask,
+                        true_tokens=true_tokens, forced_tokens=tokens)
+    dlp = float(np.abs(out["log_probs"] - log_probs).max())
+    mism = np.nonzero(out["sampled"] != tokens)[0]
+    unexplained = [int(r) for r in mism if not (out["cdf_gap"][r] < CDF_TOL)]
+    return dlp, len(mism), unexplained
+
+
+def check_design(oracle, bb, res, seeds, temperature, greedy=False, chain_mask=None, true_tokens=None):
+    enc = oracle.encode(bb)
+    worst = 0.0
+    total_mism = 0
+    for b in range(res["tokens"].shape[0]):
+        dlp, nm, bad = replay(oracle, enc, res["orders"][b], seeds[b], temperature, res["tokens"][b],
+                              res["log_probs"][b], greedy, chain_mask, true_tokens)
+        worst = max(worst, dlp)
+        total_mism += nm
+        assert not bad, f"sequence {b}: token differs at {bad} with a clear CDF margin"
+    _say(f"  max|dlogp|={worst:.3g} near-tie flips={total_mism}")
+    assert worst <= LP_TOL
+    return worst
+
+
+def test_design_random_orders_per_sequence(gpu_ctx, oracle):
+    # L=120, 8 sequences, seed 7+i for both order and sampler (cpp/algorithms/inverse_fold.cpp:186-189,304-310)
+    bb = backbone.single_chain(120, 7)
+    seeds = np.arange(7, 15, dtype=np.uint64)
+    _say("design L=120 B=8 random per-sequence orders")
+    res = gpu_ctx.design(bb.coords, bb.atom_sources, 8, seeds, order_seeds=seeds, temperature=0.1)
+    mask = np.ones(120, np.float32)
+    for b in range(8):
+        np.testing.assert_array_equal(res["orders"][b], oracle.decode_order(120, int(seeds[b]), residue_mask=mask))
+    check_design(oracle, bb, res, seeds, 0.1)
+    # scores: mean NLL of the written tokens
+    for b in range(8):
+        lp = res["log_probs"][b][np.arange(120), res["tokens"][b]]
+        assert res["scores"][b] == pytest.approx(-lp.mean(), abs=1e-5)
+
+
+def test_design_shared_order_L300(gpu_ctx, oracle):
+    bb = backbone.single_chain(300, 7)
+    order = _lib.decode_order(bb.atom_sources, 7)
+    seeds = 7 + np.arange(6, dtype=np.uint64)
+    _say("design L=300 B=6 shared order")
+    res = gpu_ctx.design(bb.coords, bb.atom_sources, 6, seeds, order_mode=_lib.ORDER_INPUT_SHARED, orders=order,
+                         temperature=0.1)
+    assert (res["orders"] == order).all()
+    check_design(oracle, bb, res, seeds, 0.1)
+
+
+def test_design_multichain(gpu_ctx, oracle):
+    cx = backbone.tetrahedral_complex(48, 5)
+    seeds = np.arange(3, dtype=np.uint64) + 100
+    order = _lib.decode_order(cx.atom_sources, 11)
+    _say("design complex 4x48 B=3")
+    res = gpu_ctx.design(cx.coords, cx.atom_sources, 3, seeds, order_mode=_lib.ORDER_INPUT_SHARED, orders=order,
+                         temperature=0.2, residue_indices=cx.residue_indices, chain_labels=cx.chain_labels)
+    check_design(oracle, cx, res, seeds, 0.2)
+
+
+def test_design_chain_mask_missing_atoms_greedy(gpu_ctx, oracle):
+    bb = backbone.single_chain(80, 9)
+    src = bb.atom_sources.copy()
+    src[[4, 50], 3] = 0
+    src[30, 4] = 0
+    bb = backbone.Backbone(bb.coords, src)
+    cm = np.ones(80, np.float32)
+    cm[10:25] = 0.0
+    tt = (np.arange(80) * 7 % 20).astype(np.int32)
+    seeds = np.array([1, 2], dtype=np.uint64)
+    _say("design chain mask + missing atoms")
+    res = gpu_ctx.design(bb.coords, bb.atom_sources, 2, seeds, order_seeds=seeds, temperature=0.1, chain_mask=cm,
+                         true_tokens=tt)
+    check_design(oracle, bb, res, seeds, 0.1, chain_mask=cm, true_tokens=tt)
+    assert (res["tokens"][:, 10:25] == tt[10:25]).all()
+    _say("design greedy n_to_c")
+    g = gpu_ctx.design(bb.coords, bb.atom_sources, 1, seeds[:1], order_mode=_lib.ORDER_N_TO_C, temperature=0.0)
+    check_design(oracle, bb, g, seeds[:1], 0.0, greedy=True)
+
+
+@pytest.mark.parametrize("L", [1, 7, 47, 49])
+def test_design_small_lengths(gpu_ctx, oracle, L):
+    bb = backbone.single_chain(L, L)
+    seeds = np.array([5, 6], dtype=np.uint64)
+    _say(f"design L={L}")
+    res = gpu_ctx.design(bb.coords, bb.atom_sources, 2, seeds, order_seeds=seeds, temperature=0.1)
+    check_design(oracle, bb, res, seeds, 0.1)
+
+
+@pytest.mark.parametrize("case", golden_cases()[:2], ids=lambda c: c["fixture_id"])
+def test_design_golden_structures(gpu_ctx, oracle, case):
+    bb, _ = pdb.read_pdb(FIXTURES / case["pdb"])
+    seeds = np.array([case["seed"]], dtype=np.uint64)
+    _say(f"design {case['fixture_id']}")
+    res = gpu_ctx.design(bb.coords, bb.atom_sources, 1, seeds, order_mode=_lib.ORDER_N_TO_C,
+                         temperature=case["sampling_temp"])
+    check_design(oracle, bb, res, seeds, case["sampling_temp"])
+
+
+def test_design_errors(gpu_ctx):
+    bb = backbone.single_chain(20, 1)
+    seeds = np.array([1], dtype=np.uint64)
+    with pytest.raises(_lib.HkbsError) as e:
+        gpu_ctx.design(bb.coords, bb.atom_sources, 1, seeds, order_mode=_lib.ORDER_INPUT_SHARED,
+                       orders=np.zeros(20, np.int32))
+    assert e.value.code == _lib.INVALID_ARGUMENT
+    with pytest.raises(_lib.HkbsError):
+        gpu_ctx.design(bb.coords, bb.atom_sources, 0, seeds, order_seeds=seeds)
+    with pytest.raises(_lib.HkbsError):
+        gpu_ctx.design(bb.coords, bb.atom_sources, 1, seeds, order_seeds=seeds, temperature=-1.0)
+    with pytest.raises(_lib.HkbsError):
+        gpu_ctx.design(bb.coords, bb.atom_sources, 1, seeds, order_seeds=seeds, temperature=float("nan"))
+
+
+def test_design_deterministic(gpu_ctx):
+    bb = backbone.single_chain(64, 2)
+    seeds = np.array([3, 4, 5], dtype=np.uint64)
+    a = gpu_ctx.design(bb.coords, bb.atom_sources, 3, seeds, order_seeds=seeds)
+    b = gpu_ctx.design(bb.coords, bb.atom_sources, 3, seeds, order_seeds=seeds)
+    np.testing.assert_array_equal(a["tokens"], b["tokens"])
+    np.testing.assert_array_equal(a["log_probs"], b["log_probs"])
