@@ -22,7 +22,8 @@ ORDER_RANDOM, ORDER_INPUT_PER_SEQUENCE, ORDER_INPUT_SHARED, ORDER_N_TO_C = range
 EXPORTS = (
     "hkbs_last_error", "hkbs_version", "hkbs_device_count", "hkbs_pmpnn_create", "hkbs_pmpnn_destroy",
     "hkbs_pmpnn_design", "hkbs_pmpnn_design_device", "hkbs_pmpnn_score", "hkbs_pmpnn_decode_order",
-    "hkbs_pmpnn_knn", "hkbs_pmpnn_encode", "hkbs_pmpnn_edge_features",
+    "hkbs_pmpnn_knn", "hkbs_pmpnn_encode", "hkbs_pmpnn_edge_features", "hkbs_pmpnn_set_timing",
+    "hkbs_pmpnn_last_timing",
 )
 
 
@@ -68,6 +69,10 @@ def load() -> C.CDLL:
     lib.hkbs_pmpnn_encode.argtypes = [_vp, _vp, _vp, _vp, _vp, _i32, _vp, _vp, _vp, _vp]
     lib.hkbs_pmpnn_edge_features.restype = _i32
     lib.hkbs_pmpnn_edge_features.argtypes = [_vp, _vp, _vp, _vp, _vp, _i32, _vp]
+    lib.hkbs_pmpnn_set_timing.restype = _i32
+    lib.hkbs_pmpnn_set_timing.argtypes = [_vp, _i32]
+    lib.hkbs_pmpnn_last_timing.restype = _i32
+    lib.hkbs_pmpnn_last_timing.argtypes = [_vp, _vp]
     _lib = lib
     return lib
 
@@ -192,6 +197,15 @@ class Context:
             self._h, coords_ptr, atom_sources_ptr, residue_indices_ptr, chain_labels_ptr, chain_mask_ptr,
             true_tokens_ptr, int(L), int(B), orders_ptr, int(shared), seeds_ptr, C.c_float(temperature),
             int(bool(greedy)), tokens_ptr, log_probs_ptr, scores_ptr, stream_ptr))
+
+    def set_timing(self, enable: bool) -> None:
+        check(self._lib.hkbs_pmpnn_set_timing(self._h, int(bool(enable))))
+
+    def last_timing(self) -> tuple[float, float, float]:
+        """Milliseconds of (featurise + encode, decoder precompute, decode loop) of the last design call."""
+        ms = np.zeros(3, np.float32)
+        check(self._lib.hkbs_pmpnn_last_timing(self._h, ptr(ms)))
+        return float(ms[0]), float(ms[1]), float(ms[2])
 
     def score(self, coords, atom_sources, tokens, order=None, residue_indices=None, chain_labels=None,
               chain_mask=None):

@@ -357,6 +357,9 @@ struct hkbs_pmpnn {
   float* weights = nullptr;
   ModelDev model{};
   DeviceArena arena;
+  bool timing = false;
+  bool timed = false;  // events hold a recorded design call
+  hipEvent_t ev[4] = {nullptr, nullptr, nullptr, nullptr};
 };
 
 namespace {
@@ -410,17 +413,18 @@ hkbs_status build_model(hkbs_pmpnn* ctx, const float* const* t) {
     for (int i = 0; i < 6; ++i) q[16 + i] = copy_raw(ar, e[12 + i], 128);  // n1g n1b n2g n2b n3g n3b
   }
   {
-    std::vector<float> w1b(384 * 128), w1d(384 * 128);
+    std::vector<float> w1b(384 * 128), w1d(512 * 128);
     for (int l = 0; l < kLayers; ++l) {
       const float* W1 = t[74 + 14 * l];
       for (int n = 0; n < 128; ++n)
         for (int k = 0; k < 128; ++k) {
           w1b[(size_t)(l * 128 + n) * 128 + k] = W1[(size_t)n * 512 + 128 + k];
           w1d[(size_t)(l * 128 + n) * 128 + k] = W1[(size_t)n * 512 + 384 + k];
+          if (l == 0) w1d[(size_t)(384 + n) * 128 + k] = W1[(size_t)n * 512 + k];
         }
     }
     o.W1b_dec_p = pack_k16(ar, {w1b.data()}, 384, 128, 0, 128);
-    o.W1d_dec_p = pack_k16(ar, {w1d.data()}, 384, 128, 0, 128);
+    o.W1d_dec_p = pack_k16(ar, {w1d.data()}, 512, 128, 0, 128);
   }
   for (int l = 0; l < kLayers; ++l) {
     const float* const* d = t + 74 + 14 * l;
@@ -430,7 +434,16 @@ hkbs_status build_model(hkbs_pmpnn* ctx, const float* const* t) {
     q[2] = pack_t(ar, d[4], 128, 128, 0, 128, 128);    // W3_t
     q[3] = pack_t(ar, d[10], 512, 128, 0, 128, 512);   // Win_t [128][512]
     q[4] = pack_t(ar, d[12], 128, 512, 0, 512, 128);   // Wout_t [512][128]
-    q[5] = pack_t(ar, d[0], 128, 512, 384, 128, 128);  // W1d_t
+    {
+      // [128][256]: columns 0..127 = W1d (inputs 384..511), 128..255 = W1a (inputs 0..127)
+      const size_t off = ar.add(128 * 256);
+      for (int n = 0; n < 128; ++n)
+        for (int k = 0; k < 128; ++k) {
+          ar.data[off + (size_t)k * 256 + n] = d[0][(size_t)n * 512 + 384 + k];
+          ar.data[off + (size_t)k * 256 + 128 + n] = d[0][(size_t)n * 512 + k];
+        }
+      q[5] = off;
+    }
     {
       // T[v][o] = sum_p W1c[o][p] W_s[v][p], in double then rounded.
       std::vector<float> T(21 * 128);
@@ -499,7 +512,7 @@ hkbs_status build_model(hkbs_pmpnn* ctx, const float* const* t) {
     w.W3_t = B + q[2];
     w.Win_t = B + q[3];
     w.Wout_t = B + q[4];
-    w.W1d_t = B + q[5];
+    w.W1da_t = B + q[5];
     w.T = B + q[6];
     w.b1 = B + q[7];
     w.b2 = B + q[8];
@@ -598,7 +611,7 @@ hkbs_status upload_inputs(hkbs_pmpnn* ctx, DeviceArena& ar, const float* coords,
 
 size_t decode_bytes(int L, int K, int B) {
   const size_t S = (size_t)L * K;
-  return aligned_bytes<float>(kLayers * S * kH) + aligned_bytes<float>((size_t)kLayers * L * kH) +
+  return aligned_bytes<float>(kLayers * S * kH) + aligned_bytes<float>((size_t)(kLayers + 1) * L * kH) +
          2 * aligned_bytes<int32_t>((size_t)B * L) + aligned_bytes<uint64_t>(B) +
          aligned_bytes<float>((size_t)B * kLayers * L * kH) + aligned_bytes<int32_t>((size_t)B * L) +
          aligned_bytes<float>((size_t)B * L * kV) + aligned_bytes<float>((size_t)B * L) + aligned_bytes<float>(B);
@@ -625,12 +638,15 @@ hkbs_status design_on_device(hkbs_pmpnn* ctx, const float* coords, const uint8_t
   const size_t S = (size_t)L * K;
   EncodeBuffers e = take_encode(ar, L, K);
   float* E1 = ar.take<float>(kLayers * S * kH);
-  float* Q = ar.take<float>((size_t)kLayers * L * kH);
+  float* Q = ar.take<float>((size_t)(kLayers + 1) * L * kH);
   int32_t* pos = ar.take<int32_t>((size_t)B * L);
   float* R = ar.take<float>((size_t)B * kLayers * L * kH);
+  if (ctx->timing) HK_CHECK(hipEventRecord(ctx->ev[0], ctx->stream), "event record failed");
   HK_CHECK(run_encode(ctx, coords, src, resid, chain, L, K, e), "encoder launch failed");
+  if (ctx->timing) HK_CHECK(hipEventRecord(ctx->ev[1], ctx->stream), "event record failed");
   HK_CHECK(launch_decoder_precompute(ctx->model, e.h_v, e.h_e, L, K, E1, Q, ctx->stream), "decoder precompute failed");
   HK_CHECK(launch_positions(orders, L, shared ? 1 : B, shared, pos, ctx->stream), "position kernel failed");
+  if (ctx->timing) HK_CHECK(hipEventRecord(ctx->ev[2], ctx->stream), "event record failed");
   DecodeArgs a{};
   a.idx = e.idx;
   a.mask = e.mask;
@@ -654,6 +670,10 @@ hkbs_status design_on_device(hkbs_pmpnn* ctx, const float* coords, const uint8_t
   a.scores = scores;
   a.chosen_lp = chosen;
   HK_CHECK(launch_decode(ctx->model, a, ctx->stream), "decode launch failed");
+  if (ctx->timing) {
+    HK_CHECK(hipEventRecord(ctx->ev[3], ctx->stream), "event record failed");
+    ctx->timed = true;
+  }
   return HKBS_OK;
 }
 
@@ -724,6 +744,8 @@ void hkbs_pmpnn_destroy(hkbs_pmpnn* ctx) {
   if (!ctx) return;
   (void)hipSetDevice(ctx->device);
   if (ctx->stream) (void)hipStreamSynchronize(ctx->stream);
+  for (hipEvent_t& ev : ctx->ev)
+    if (ev) (void)hipEventDestroy(ev);
   if (ctx->arena.base) (void)hipFree(ctx->arena.base);
   if (ctx->weights) (void)hipFree(ctx->weights);
   if (ctx->stream) (void)hipStreamDestroy(ctx->stream);
@@ -856,6 +878,27 @@ hkbs_status hkbs_pmpnn_design_device(hkbs_pmpnn* ctx, const float* coords, const
                         shared_order != 0, sampler_seeds, temperature, greedy, tokens, log_probs, scores, ar, chosen);
   ctx->stream = saved;
   return st;
+}
+
+hkbs_status hkbs_pmpnn_set_timing(hkbs_pmpnn* ctx, int32_t enable) {
+  hkbs_status st = enter(ctx);
+  if (st != HKBS_OK) return st;
+  if (enable && !ctx->ev[0])
+    for (hipEvent_t& ev : ctx->ev)
+      if (hipEventCreate(&ev) != hipSuccess) return fail(HKBS_INTERNAL_ERROR, "HIP event creation failed");
+  ctx->timing = enable != 0;
+  ctx->timed = false;
+  return HKBS_OK;
+}
+
+hkbs_status hkbs_pmpnn_last_timing(hkbs_pmpnn* ctx, float* ms) {
+  hkbs_status st = enter(ctx);
+  if (st != HKBS_OK) return st;
+  if (!ms) return fail(HKBS_INVALID_ARGUMENT, "timing output is null");
+  if (!ctx->timed) return fail(HKBS_FAILED_PRECONDITION, "no timed design call has been recorded");
+  HK_CHECK(hipEventSynchronize(ctx->ev[3]), "event synchronisation failed");
+  for (int i = 0; i < 3; ++i) HK_CHECK(hipEventElapsedTime(&ms[i], ctx->ev[i], ctx->ev[i + 1]), "event timing failed");
+  return HKBS_OK;
 }
 
 hkbs_status hkbs_pmpnn_score(hkbs_pmpnn* ctx, const float* coords, const uint8_t* atom_sources,

@@ -11,7 +11,8 @@
 // With W1 = [W1a | W1b | W1c | W1d] over [h_t | h_E | h_S | h_V] the first
 // product splits into terms that do not depend on the step:
 //   W1 [h_t, ctx_k] + b1 = A_t + E1_tk + (bw ? R^l_j : Q^l_j)    (valid slot)
-//   A_t    = W1a h^l_t + b1                         (one GEMV per step)
+//   A_t    = W1a h^l_t + b1                         (precomputed for l = 0, one fused
+//                                                    GEMV with the next W1d for l > 0)
 //   E1_tk  = W1b h_E_tk                             (precomputed, all sequences)
 //   Q^l_j  = W1d h^0_j                              (precomputed, all sequences)
 //   R^l_j  = W1d h^l_j + W1c W_s[tok_j]             (written when j is decoded)
@@ -27,28 +28,32 @@ namespace hkbs {
 namespace {
 
 constexpr int kLd = kH + 4;  // 132
-constexpr int kThreads = 256;
+constexpr int kThreads = 512;
 
-// y[o] = sum_p x[p] Wt[p][o] (+ bias) for OUT outputs, IN inputs, using all
-// 256 threads; x and y in LDS, part is LDS scratch of >= 1024 floats.
+// y[o] = sum_p x[p] Wt[p][o] (+ bias) for OUT outputs and IN inputs on all
+// threads of the block: each thread loads its PER float4 weights up front
+// (all in flight), partial sums meet in LDS. part >= 2048 floats.
 template <int IN, int OUT>
 __device__ inline void gemv(const float* __restrict__ Wt, const float* x, const float* __restrict__ bias,
                             float* part, float* y) {
   constexpr int Q4 = OUT / 4;            // float4 columns
   constexpr int GROUPS = kThreads / Q4;  // input groups
   constexpr int PER = IN / GROUPS;       // inputs per group
+  static_assert(GROUPS * OUT <= 2048, "partial buffer");
   const int q = threadIdx.x % Q4;
   const int grp = threadIdx.x / Q4;
-  float4 acc = make_float4(0.F, 0.F, 0.F, 0.F);
   const float* w = Wt + (size_t)(grp * PER) * OUT + 4 * q;
-#pragma unroll 8
+  float4 wv[PER];
+#pragma unroll
+  for (int p = 0; p < PER; ++p) wv[p] = *reinterpret_cast<const float4*>(w + (size_t)p * OUT);
+  float4 acc = make_float4(0.F, 0.F, 0.F, 0.F);
+#pragma unroll
   for (int p = 0; p < PER; ++p) {
-    const float4 wv = *reinterpret_cast<const float4*>(w + (size_t)p * OUT);
     const float xv = x[grp * PER + p];
-    acc.x += xv * wv.x;
-    acc.y += xv * wv.y;
-    acc.z += xv * wv.z;
-    acc.w += xv * wv.w;
+    acc.x += xv * wv[p].x;
+    acc.y += xv * wv[p].y;
+    acc.z += xv * wv[p].z;
+    acc.w += xv * wv[p].w;
   }
   *reinterpret_cast<float4*>(part + grp * OUT + 4 * q) = acc;
   __syncthreads();
@@ -69,14 +74,15 @@ __device__ inline void ln_vec(const float* x, const float* g, const float* b, fl
 
 __global__ __launch_bounds__(kThreads) void decode_kernel(ModelDev m, DecodeArgs a) {
   __shared__ __attribute__((aligned(16))) float G[kKmax * kLd];
-  __shared__ __attribute__((aligned(16))) float part[1024];
+  __shared__ __attribute__((aligned(16))) float part[2048];
   __shared__ __attribute__((aligned(16))) float h[kH];
-  __shared__ __attribute__((aligned(16))) float hA[kH];
+  __shared__ __attribute__((aligned(16))) float hA[2 * kH];  // [A | scratch]
   __shared__ __attribute__((aligned(16))) float x[kH];
   __shared__ __attribute__((aligned(16))) float h1[kH];
   __shared__ __attribute__((aligned(16))) float ff[kFF];
-  __shared__ __attribute__((aligned(16))) float P[2][kH];
+  __shared__ __attribute__((aligned(16))) float P[2][2 * kH];  // [W1d h | W1a h] of layers 1, 2
   __shared__ float logits[32];
+  __shared__ float tbl[17];
   __shared__ int nbr[kKmax];
   __shared__ int bwf[kKmax];
   __shared__ int tok_s;
@@ -95,6 +101,8 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(ModelDev m, DecodeArgs
   uint64_t rng = a.seeds[b];
   const float T = (a.temperature > 0.0F && isfinite(a.temperature)) ? a.temperature : 1.0F;
   const bool greedy = a.greedy || a.temperature <= 0.0F;
+  if (threadIdx.x < 17) tbl[threadIdx.x] = kExpNegTable[threadIdx.x];
+  __syncthreads();
 
   for (int step = 0; step < L; ++step) {
     const int t = order[step];
@@ -122,12 +130,15 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(ModelDev m, DecodeArgs
       nbr[threadIdx.x] = valid ? j : -1;
       bwf[threadIdx.x] = valid && pos[j] < step;
     }
-    if (threadIdx.x < kH) h[threadIdx.x] = a.h_v[(size_t)t * kH + threadIdx.x];
+    if (threadIdx.x < kH) {
+      h[threadIdx.x] = a.h_v[(size_t)t * kH + threadIdx.x];
+      // layer-0 W1a h^0_t comes from the precompute (Q block 3)
+      hA[threadIdx.x] = a.Q[((size_t)3 * L + t) * kH + threadIdx.x] + m.dec[0].b1[threadIdx.x];
+    }
     __syncthreads();
 
     for (int l = 0; l < kLayers; ++l) {
       const DecLayerDev& w = m.dec[l];
-      gemv<kH, kH>(w.W1a_t, h, w.b1, part, hA);
       // Message rows g1_k = GELU(A + E1_tk + (bw ? R : Q)_j); rows >= K are zero.
       const float* E1 = a.E1 + ((size_t)l * S + (size_t)t * K) * kH;
       const float* Ql = a.Q + (size_t)l * L * kH;
@@ -135,62 +146,63 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(ModelDev m, DecodeArgs
       for (int task = threadIdx.x; task < kKmax * (kH / 4); task += kThreads) {
         const int k = task / (kH / 4);
         const int c = 4 * (task % (kH / 4));
-        float4 v = make_float4(0.F, 0.F, 0.F, 0.F);
-        if (k < K) {
-          float4 xv = *reinterpret_cast<const float4*>(hA + c);
-          const int j = nbr[k];
-          if (j >= 0) {
-            const float4 e = *reinterpret_cast<const float4*>(E1 + (size_t)k * kH + c);
-            const float4 z = *reinterpret_cast<const float4*>((bwf[k] ? Rl : Ql) + (size_t)j * kH + c);
-            xv.x += e.x + z.x;
-            xv.y += e.y + z.y;
-            xv.z += e.z + z.z;
-            xv.w += e.w + z.w;
-          }
-          v = make_float4(gelu(xv.x), gelu(xv.y), gelu(xv.z), gelu(xv.w));
+        float4 xv = *reinterpret_cast<const float4*>(hA + c);
+        const int j = k < K ? nbr[k] : -1;
+        if (j >= 0) {
+          const float4 e = *reinterpret_cast<const float4*>(E1 + (size_t)k * kH + c);
+          const float4 z = *reinterpret_cast<const float4*>((bwf[k] ? Rl : Ql) + (size_t)j * kH + c);
+          xv.x += e.x + z.x;
+          xv.y += e.y + z.y;
+          xv.z += e.z + z.z;
+          xv.w += e.w + z.w;
         }
+        float4 v = make_float4(gelu_fast(xv.x, tbl), gelu_fast(xv.y, tbl), gelu_fast(xv.z, tbl), gelu_fast(xv.w, tbl));
+        if (k >= K) v = make_float4(0.F, 0.F, 0.F, 0.F);
         *reinterpret_cast<float4*>(G + k * kLd + c) = v;
       }
       __syncthreads();
       {
-        floatx4 acc[3][2];
+        floatx4 acc[3][1];
         zero_acc(acc);
-        mfma_tile<3, 2>(G, kLd, w.W2_p, kH, wave * 32, kH, acc);
-        // s[col] = sum over valid rows of GELU(acc + b2)
+        mfma_tile<3, 1>(G, kLd, w.W2_p, kH, wave * 16, kH, acc);
+        // x[col] = sum over valid rows of GELU(acc + b2)
+        const int col = wave * 16 + (lane & 15);
+        const float b2 = w.b2[col];
+        float s = 0.0F;
 #pragma unroll
-        for (int nb = 0; nb < 2; ++nb) {
-          const int col = wave * 32 + nb * 16 + (lane & 15);
-          const float b2 = w.b2[col];
-          float s = 0.0F;
+        for (int mb = 0; mb < 3; ++mb)
 #pragma unroll
-          for (int mb = 0; mb < 3; ++mb)
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-              const int row = mb * 16 + 4 * (lane >> 4) + i;
-              if (row < K) s += gelu(acc[mb][nb][i] + b2);
-            }
-          s += __shfl_xor(s, 16, 64);
-          s += __shfl_xor(s, 32, 64);
-          if (lane < 16) x[col] = s;
-        }
+          for (int i = 0; i < 4; ++i) {
+            const int row = mb * 16 + 4 * (lane >> 4) + i;
+            const float g = gelu_fast(acc[mb][0][i] + b2, tbl);
+            s += row < K ? g : 0.0F;
+          }
+        s += __shfl_xor(s, 16, 64);
+        s += __shfl_xor(s, 32, 64);
+        if (lane < 16) x[col] = s;
       }
       __syncthreads();
       // upd = (W3 s + K b3) / 30 ; h1 = LN1(h + upd)
-      gemv<kH, kH>(w.W3_t, x, nullptr, part, hA);
+      gemv<kH, kH>(w.W3_t, x, nullptr, part, hA + kH);
       if (threadIdx.x < kH) {
         const int c = threadIdx.x;
-        x[c] = h[c] + (hA[c] + static_cast<float>(K) * w.b3[c]) * (1.0F / 30.0F);
+        x[c] = h[c] + (hA[kH + c] + static_cast<float>(K) * w.b3[c]) * (1.0F / 30.0F);
       }
       __syncthreads();
       ln_vec(x, w.n1g, w.n1b, h1);
       gemv<kH, kFF>(w.Win_t, h1, w.bin, part, ff);
-      for (int i = threadIdx.x; i < kFF; i += kThreads) ff[i] = gelu(ff[i]);
+      ff[threadIdx.x] = gelu_fast(ff[threadIdx.x], tbl);
       __syncthreads();
-      gemv<kFF, kH>(w.Wout_t, ff, w.bout, part, hA);
-      if (threadIdx.x < kH) x[threadIdx.x] = h1[threadIdx.x] + hA[threadIdx.x];
+      gemv<kFF, kH>(w.Wout_t, ff, w.bout, part, hA + kH);
+      if (threadIdx.x < kH) x[threadIdx.x] = h1[threadIdx.x] + hA[kH + threadIdx.x];
       __syncthreads();
       ln_vec(x, w.n2g, w.n2b, h);  // h = h^{l+1}_t (active residue: mask gate is 1)
-      if (l + 1 < kLayers) gemv<kH, kH>(m.dec[l + 1].W1d_t, h, nullptr, part, P[l]);
+      if (l + 1 < kLayers) {
+        // fused [W1d | W1a] of the next layer: P (for R) and A (next message rows)
+        gemv<kH, 2 * kH>(m.dec[l + 1].W1da_t, h, nullptr, part, P[l]);
+        if (threadIdx.x < kH) hA[threadIdx.x] = P[l][kH + threadIdx.x] + m.dec[l + 1].b1[threadIdx.x];
+        __syncthreads();
+      }
     }
     // logits = W_out h + b (padded to 32 outputs)
     gemv<kH, 32>(m.Wlog_t, h, m.blog, part, logits);
@@ -336,8 +348,8 @@ hipError_t launch_decoder_precompute(const ModelDev& m, const float* h_v, const 
   if (S == 0) return hipSuccess;
   rows_gemm_kernel<<<dim3((unsigned)((S + kGemmRows - 1) / kGemmRows), kLayers), 256, 0, stream>>>(
       h_e, S, m.W1b_dec_p, kLayers * kH, E1);
-  rows_gemm_kernel<<<dim3((unsigned)((L + kGemmRows - 1) / kGemmRows), kLayers), 256, 0, stream>>>(
-      h_v, (size_t)L, m.W1d_dec_p, kLayers * kH, Q);
+  rows_gemm_kernel<<<dim3((unsigned)((L + kGemmRows - 1) / kGemmRows), kLayers + 1), 256, 0, stream>>>(
+      h_v, (size_t)L, m.W1d_dec_p, (kLayers + 1) * kH, Q);
   return hipGetLastError();
 }
 

@@ -76,6 +76,28 @@ __device__ inline float gelu(float x) {
   return 0.5F * x * (1.0F + erfv);
 }
 
+// The same GELU formula for the decode loop, which is held to a tolerance
+// rather than to bit identity: the exp table is read from LDS (tbl = 17
+// floats, kExpNegTable), 1/(1 + p v) uses the hardware reciprocal (1 ulp),
+// and the range checks that cannot fire for |v| <= 4 are dropped.
+__device__ inline float gelu_fast(float x, const float* tbl) {
+  const float v = fabsf(x) * 0.7071067811865475F;
+  const float t = __builtin_amdgcn_rcpf(1.0F + 0.3275911F * v);
+  const float poly =
+      (((((1.061405429F * t + -1.453152027F) * t) + 1.421413741F) * t + -0.284496736F) * t + 0.254829592F) * t;
+  const float q = fminf(v * v, 16.0F);
+  const int n = static_cast<int>(q + 0.5F);
+  const float r = static_cast<float>(n) - q;
+  const float e =
+      1.0F +
+      r * (1.0F +
+           r * (0.5F +
+                r * (1.0F / 6.0F + r * (1.0F / 24.0F + r * (1.0F / 120.0F + r * (1.0F / 720.0F))))));
+  float erfv = v > 4.0F ? 1.0F : 1.0F - poly * (tbl[n] * e);
+  erfv = x < 0.0F ? -erfv : erfv;
+  return 0.5F * x * (1.0F + erfv);
+}
+
 __device__ inline floatx4 mfma16(float a, float b, floatx4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
 }

@@ -44,7 +44,7 @@ struct DecLayerDev {
   const float* W3_t;   // [128][128]
   const float* Win_t;  // [128][512]
   const float* Wout_t; // [512][128]
-  const float* W1d_t;  // [128][128]
+  const float* W1da_t; // [128][256]: columns [W1d | W1a] (layers 1, 2)
   const float* T;      // [21][128]: W1c . W_s[v]
   const float *b1, *b2, *b3, *bin, *bout;
   const float *n1g, *n1b, *n2g, *n2b;
@@ -61,7 +61,7 @@ struct ModelDev {
   EncLayerDev enc[kLayers];
   DecLayerDev dec[kLayers];
   const float* W1b_dec_p;  // kpack16 128 -> 384: rows = [W1b_0; W1b_1; W1b_2] (decoder)
-  const float* W1d_dec_p;  // kpack16 128 -> 384: rows = [W1d_0; W1d_1; W1d_2]
+  const float* W1d_dec_p;  // kpack16 128 -> 512: rows = [W1d_0; W1d_1; W1d_2; W1a_0]
   const float* Wlog_t;     // [128][21]
   const float* blog;       // [21]
 };
@@ -93,7 +93,7 @@ struct DecodeArgs {
   const float* mask;      // [L]
   const float* h_v;       // [L][128] encoder output
   const float* E1;        // [3][S][128]
-  const float* Q;         // [3][L][128]
+  const float* Q;         // [4][L][128]: W1d_l h^0 (l = 0..2), W1a_0 h^0
   const int32_t* orders;  // [B][L] or [L]
   int shared_order;
   const int32_t* pos;     // [B][L] or [L]: position of residue r in the order

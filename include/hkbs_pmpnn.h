@@ -125,6 +125,14 @@ hkbs_status hkbs_pmpnn_score(hkbs_pmpnn* ctx, const float* coords, const uint8_t
 hkbs_status hkbs_pmpnn_decode_order(const float* chain_mask, const uint8_t* atom_sources,
                                     int32_t L, uint64_t seed, int32_t* order);
 
+/* Phase timing (instrumentation; no counterpart in the reference, which has
+ * no design-path profiler). With timing enabled, each design call records
+ * HIP events on the stream its kernels run on around three phases;
+ * hkbs_pmpnn_last_timing waits for the last call and returns the elapsed
+ * milliseconds of [featurise + encode, decoder precompute, decode loop]. */
+hkbs_status hkbs_pmpnn_set_timing(hkbs_pmpnn* ctx, int32_t enable);
+hkbs_status hkbs_pmpnn_last_timing(hkbs_pmpnn* ctx, float* ms /* [3] */);
+
 /* Unit-parity entry points (host memory in/out). */
 
 /* CA kNN graph: idx [L,K] and squared distances d2 [L,K], K = min(48, L)
