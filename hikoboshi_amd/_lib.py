@@ -23,7 +23,7 @@ EXPORTS = (
     "hkbs_last_error", "hkbs_version", "hkbs_device_count", "hkbs_pmpnn_create", "hkbs_pmpnn_destroy",
     "hkbs_pmpnn_design", "hkbs_pmpnn_design_device", "hkbs_pmpnn_score", "hkbs_pmpnn_decode_order",
     "hkbs_pmpnn_knn", "hkbs_pmpnn_encode", "hkbs_pmpnn_edge_features", "hkbs_pmpnn_set_timing",
-    "hkbs_pmpnn_last_timing",
+    "hkbs_pmpnn_last_timing", "hkbs_pmpnn_score_batch",
 )
 
 
@@ -61,6 +61,8 @@ def load() -> C.CDLL:
                                              C.c_float, _i32, _vp, _vp, _vp, _vp]
     lib.hkbs_pmpnn_score.restype = _i32
     lib.hkbs_pmpnn_score.argtypes = [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i32, _vp, _vp]
+    lib.hkbs_pmpnn_score_batch.restype = _i32
+    lib.hkbs_pmpnn_score_batch.argtypes = [_vp, _i32, _vp, _vp, _vp, _vp, _vp, _vp, _vp]
     lib.hkbs_pmpnn_decode_order.restype = _i32
     lib.hkbs_pmpnn_decode_order.argtypes = [_vp, _vp, _i32, C.c_uint64, _vp]
     lib.hkbs_pmpnn_knn.restype = _i32
@@ -217,3 +219,15 @@ class Context:
         check(self._lib.hkbs_pmpnn_score(self._h, ptr(c), ptr(s), ptr(r), ptr(ch), ptr(cm), ptr(t), ptr(od), L,
                                          ptr(lp), C.cast(C.byref(sc), _vp)))
         return lp, sc.value
+
+    def score_batch(self, coords, atom_sources, tokens, offsets, orders=None):
+        """Teacher-forced log-probs [sum L, 21] and scores [n] of a ragged batch."""
+        c, s, t = f32(coords), u8(atom_sources), i32(tokens)
+        off = np.ascontiguousarray(offsets, dtype=np.int64)
+        n = off.size - 1
+        lp = np.empty((int(off[-1]), 21), np.float32)
+        sc = np.empty(n, np.float32)
+        od = i32(orders)
+        check(self._lib.hkbs_pmpnn_score_batch(self._h, n, ptr(off), ptr(c), ptr(s), ptr(t), ptr(od), ptr(lp),
+                                               ptr(sc)))
+        return lp, sc

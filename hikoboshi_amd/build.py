@@ -17,7 +17,7 @@ HERE = Path(__file__).resolve().parent
 CSRC = HERE / "csrc"
 LIB = HERE / "libhkbs_pmpnn.so"
 ARCH = os.environ.get("HKBS_OFFLOAD_ARCH", "gfx950")
-SOURCES = ["knn.hip", "features.hip", "encoder.hip", "decoder.hip", "capi.hip"]
+SOURCES = ["knn.hip", "features.hip", "encoder.hip", "decoder.hip", "decoder_tf.hip", "capi.hip"]
 
 
 def hipcc() -> str:

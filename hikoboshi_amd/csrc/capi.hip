@@ -19,12 +19,6 @@
 #include <string>
 #include <vector>
 
-namespace hkbs {
-hipError_t launch_knn(const float* coords, const uint8_t* atom_src, int L, int K, int32_t* idx, float* d2,
-                      float* mask, float4* ca_scratch, hipStream_t stream);
-hipError_t launch_positions(const int32_t* orders, int L, int B, int shared, int32_t* pos, hipStream_t stream);
-}  // namespace hkbs
-
 namespace {
 
 using namespace hkbs;
@@ -455,6 +449,21 @@ hkbs_status build_model(hkbs_pmpnn* ctx, const float* const* t) {
         }
       q[6] = copy_raw(ar, T.data(), T.size());
     }
+    q[16] = pack_k16(ar, {d[4]}, 128, 128, 0, 128);   // W3_p
+    q[17] = pack_k16(ar, {d[10]}, 512, 128, 0, 128);  // Win_p
+    q[18] = pack_k16(ar, {d[12]}, 128, 512, 0, 512);  // Wout_p
+    if (l + 1 < kLayers) {
+      const float* Wn = t[74 + 14 * (l + 1)];
+      std::vector<float> nx(256 * 128);
+      for (int n = 0; n < 128; ++n)
+        for (int k = 0; k < 128; ++k) {
+          nx[(size_t)n * 128 + k] = Wn[(size_t)n * 512 + k];                // W1a of layer l+1
+          nx[(size_t)(128 + n) * 128 + k] = Wn[(size_t)n * 512 + 384 + k];  // W1d of layer l+1
+        }
+      q[19] = pack_k16(ar, {nx.data()}, 256, 128, 0, 128);
+    } else {
+      q[19] = 0;
+    }
     q[7] = copy_raw(ar, d[1], 128);    // b1
     q[8] = copy_raw(ar, d[3], 128);    // b2
     q[9] = copy_raw(ar, d[5], 128);    // b3
@@ -523,6 +532,10 @@ hkbs_status build_model(hkbs_pmpnn* ctx, const float* const* t) {
     w.n1b = B + q[13];
     w.n2g = B + q[14];
     w.n2b = B + q[15];
+    w.W3_p = B + q[16];
+    w.Win_p = B + q[17];
+    w.Wout_p = B + q[18];
+    w.Wnext_p = (l + 1 < kLayers) ? B + q[19] : nullptr;
   }
   m.W1b_dec_p = B + o.W1b_dec_p;
   m.W1d_dec_p = B + o.W1d_dec_p;
@@ -901,12 +914,211 @@ hkbs_status hkbs_pmpnn_last_timing(hkbs_pmpnn* ctx, float* ms) {
   return HKBS_OK;
 }
 
+}  // extern "C"
+
+namespace {
+
+// One teacher-forced pass over n_res residues (one protein, or a ragged
+// chunk of proteins with the same K). All pointers are device memory except
+// where noted; seg/offsets describe the chunk for the kNN (null = one protein).
+hkbs_status teacher_forced_chunk(hkbs_pmpnn* ctx, const float* coords, const uint8_t* src, const int32_t* resid,
+                                 const int32_t* chain, const int32_t* tokens, const int32_t* pos, int L, int K,
+                                 const int32_t* seg, const int64_t* offsets, float* log_probs, DeviceArena& ar) {
+  EncodeBuffers e = take_encode(ar, L, K);
+  float* Q = ar.take<float>((size_t)(kLayers + 1) * L * kH);
+  float* NB = ar.take<float>((size_t)L * 256);
+  hipStream_t s = ctx->stream;
+  HK_CHECK(launch_knn(coords, src, L, K, e.idx, e.d2, e.mask, e.ca, s, seg, offsets), "kNN launch failed");
+  HK_CHECK(launch_edge_embed(ctx->model, coords, src, resid, chain, e.idx, L, K, e.h_e, s), "feature launch failed");
+  HK_CHECK(launch_encoder(ctx->model, e.idx, e.mask, L, K, e.h_v, e.h_e, e.scratch, s), "encoder launch failed");
+  HK_CHECK(launch_q_precompute(ctx->model, e.h_v, L, Q, s), "decoder precompute failed");
+  TfArgs a{};
+  a.idx = e.idx;
+  a.pos = pos;
+  a.mask = e.mask;
+  a.tokens = tokens;
+  a.h_e = e.h_e;
+  a.Q = Q;
+  a.h = e.h_v;
+  a.NB = NB;
+  a.msg_sum = e.scratch.msg_sum;
+  a.log_probs = log_probs;
+  a.L = L;
+  a.K = K;
+  HK_CHECK(launch_teacher_forced(ctx->model, a, s), "teacher-forced launch failed");
+  return HKBS_OK;
+}
+
+size_t tf_bytes(int L, int K) {
+  return encode_bytes(L, K) + aligned_bytes<float>((size_t)(kLayers + 1) * L * kH) + aligned_bytes<float>((size_t)L * 256);
+}
+
+// inverse_fold_scalar.cpp:471-493 (double accumulation, residue order).
+float average_nll_host(const int32_t* tokens, const float* lp, const float* chain_mask, const float* mask, int L) {
+  double loss = 0.0, msum = 0.0;
+  for (int r = 0; r < L; ++r) {
+    const float active = (chain_mask ? chain_mask[r] : 1.0F) * mask[r];
+    if (active == 0.0F) continue;
+    const int32_t t = tokens[r];
+    if (t < 0 || t >= kV) continue;
+    loss -= static_cast<double>(lp[(size_t)r * kV + t]);
+    msum += static_cast<double>(active);
+  }
+  return msum > 0.0 ? static_cast<float>(loss / msum) : 0.0F;
+}
+
+bool tokens_valid(const int32_t* tokens, size_t n) {
+  for (size_t i = 0; i < n; ++i)
+    if (tokens[i] < 0 || tokens[i] >= kV) return false;
+  return true;
+}
+
+}  // namespace
+
+extern "C" {
+
 hkbs_status hkbs_pmpnn_score(hkbs_pmpnn* ctx, const float* coords, const uint8_t* atom_sources,
                              const int32_t* residue_indices, const int32_t* chain_labels, const float* chain_mask,
                              const int32_t* tokens, const int32_t* order, int32_t L, float* log_probs, float* score) {
-  (void)ctx; (void)coords; (void)atom_sources; (void)residue_indices; (void)chain_labels; (void)chain_mask;
-  (void)tokens; (void)order; (void)L; (void)log_probs; (void)score;
-  return fail(HKBS_UNIMPLEMENTED, "teacher-forced scoring is not implemented yet");
+  hkbs_status st = enter(ctx);
+  if (st != HKBS_OK) return st;
+  if (L < 0) return fail(HKBS_INVALID_ARGUMENT, "residue count is negative");
+  if (L > 0 && (!coords || !atom_sources)) return fail(HKBS_INVALID_ARGUMENT, "ProteinMPNN inverse fold coordinates pointer is null");
+  if (!log_probs) return fail(HKBS_INVALID_ARGUMENT, "ProteinMPNN teacher-forced output shape is invalid");
+  if (L > 0 && !tokens) return fail(HKBS_INVALID_ARGUMENT, "ProteinMPNN token pointer is null");
+  if (!tokens_valid(tokens, (size_t)L)) return fail(HKBS_INVALID_ARGUMENT, "ProteinMPNN token id is outside the v48 vocabulary");
+  if (L == 0) {
+    if (score) *score = 0.0F;
+    return HKBS_OK;
+  }
+  std::vector<int32_t> pos(L);
+  if (order) {
+    if (!is_permutation(order, L)) return fail(HKBS_INVALID_ARGUMENT, "ProteinMPNN input decoding_order must be a permutation");
+    for (int p = 0; p < L; ++p) pos[order[p]] = p;
+  } else {
+    std::iota(pos.begin(), pos.end(), 0);
+  }
+  const int K = std::min(kKmax, L);
+  DeviceArena& ar = ctx->arena;
+  if (ar.reserve(input_bytes(L) + tf_bytes(L, K) + 2 * aligned_bytes<int32_t>(L) + aligned_bytes<float>((size_t)L * kV) +
+                 (64u << 10)) != hipSuccess)
+    return fail(HKBS_INTERNAL_ERROR, "device workspace allocation failed");
+  ar.reset();
+  Inputs in{};
+  if ((st = upload_inputs(ctx, ar, coords, atom_sources, residue_indices, chain_labels, nullptr, nullptr, L, in)) != HKBS_OK)
+    return st;
+  int32_t* d_tok = ar.take<int32_t>(L);
+  int32_t* d_pos = ar.take<int32_t>(L);
+  float* d_lp = ar.take<float>((size_t)L * kV);
+  hipStream_t s = ctx->stream;
+  HK_CHECK(hipMemcpyAsync(d_tok, tokens, (size_t)L * 4, hipMemcpyHostToDevice, s), "H2D failed");
+  HK_CHECK(hipMemcpyAsync(d_pos, pos.data(), (size_t)L * 4, hipMemcpyHostToDevice, s), "H2D failed");
+  if ((st = teacher_forced_chunk(ctx, in.coords, in.src, in.resid, in.chain, d_tok, d_pos, L, K, nullptr, nullptr, d_lp,
+                                 ar)) != HKBS_OK)
+    return st;
+  HK_CHECK(hipMemcpyAsync(log_probs, d_lp, (size_t)L * kV * 4, hipMemcpyDeviceToHost, s), "D2H failed");
+  HK_CHECK(hipStreamSynchronize(s), "teacher-forced kernels failed");
+  if (score) {
+    std::vector<float> mask;
+    residue_mask_host(atom_sources, L, mask);
+    *score = average_nll_host(tokens, log_probs, chain_mask, mask.data(), L);
+  }
+  return HKBS_OK;
+}
+
+hkbs_status hkbs_pmpnn_score_batch(hkbs_pmpnn* ctx, int32_t n, const int64_t* offsets, const float* coords,
+                                   const uint8_t* atom_sources, const int32_t* tokens, const int32_t* orders,
+                                   float* log_probs, float* scores) {
+  hkbs_status st = enter(ctx);
+  if (st != HKBS_OK) return st;
+  if (n < 0 || !offsets) return fail(HKBS_INVALID_ARGUMENT, "ragged batch offsets are missing");
+  if (n == 0) return HKBS_OK;
+  if (offsets[0] != 0) return fail(HKBS_INVALID_ARGUMENT, "ragged batch offsets must start at 0");
+  for (int i = 0; i < n; ++i)
+    if (offsets[i + 1] <= offsets[i]) return fail(HKBS_INVALID_ARGUMENT, "ragged batch proteins must be non-empty");
+  const int64_t total = offsets[n];
+  if (total > (int64_t)1 << 30) return fail(HKBS_INVALID_ARGUMENT, "ragged batch is too large");
+  if (!coords || !atom_sources || !tokens || !log_probs)
+    return fail(HKBS_INVALID_ARGUMENT, "ragged batch pointers must be non-null");
+  if (!tokens_valid(tokens, (size_t)total)) return fail(HKBS_INVALID_ARGUMENT, "ProteinMPNN token id is outside the v48 vocabulary");
+  std::vector<int32_t> pos((size_t)total);
+  for (int i = 0; i < n; ++i) {
+    const int64_t o = offsets[i];
+    const int L = static_cast<int>(offsets[i + 1] - o);
+    if (orders) {
+      if (!is_permutation(orders + o, L)) return fail(HKBS_INVALID_ARGUMENT, "ProteinMPNN input decoding_order must be a permutation");
+      for (int p = 0; p < L; ++p) pos[(size_t)o + orders[o + p]] = p;
+    } else {
+      for (int p = 0; p < L; ++p) pos[(size_t)o + p] = p;
+    }
+  }
+  // Chunks of consecutive proteins with the same K = min(48, L), bounded in edges.
+  const size_t kChunkEdges = (size_t)4 << 20;
+  struct Chunk { int first, last; int64_t r0, r1; int K; };
+  std::vector<Chunk> chunks;
+  for (int i = 0; i < n;) {
+    const int K = (int)std::min<int64_t>(kKmax, offsets[i + 1] - offsets[i]);
+    int j = i + 1;
+    while (j < n && std::min<int64_t>(kKmax, offsets[j + 1] - offsets[j]) == K &&
+           (size_t)(offsets[j + 1] - offsets[i]) * K <= kChunkEdges)
+      ++j;
+    chunks.push_back({i, j, offsets[i], offsets[j], K});
+    i = j;
+  }
+  size_t need = 0;
+  for (const Chunk& ch : chunks) {
+    const int L = (int)(ch.r1 - ch.r0);
+    need = std::max(need, input_bytes(L) + tf_bytes(L, ch.K) + 2 * aligned_bytes<int32_t>(L) +
+                              aligned_bytes<int32_t>(L) + aligned_bytes<int64_t>(ch.last - ch.first + 1) +
+                              aligned_bytes<float>((size_t)L * kV));
+  }
+  DeviceArena& ar = ctx->arena;
+  if (ar.reserve(need + (64u << 10)) != hipSuccess) return fail(HKBS_INTERNAL_ERROR, "device workspace allocation failed");
+  hipStream_t s = ctx->stream;
+  std::vector<int32_t> seg;
+  std::vector<int64_t> loc;
+  for (const Chunk& ch : chunks) {
+    const int L = (int)(ch.r1 - ch.r0);
+    const int np = ch.last - ch.first;
+    seg.resize(L);
+    loc.resize(np + 1);
+    for (int p = 0; p < np; ++p) {
+      loc[p] = offsets[ch.first + p] - ch.r0;
+      for (int64_t r = offsets[ch.first + p]; r < offsets[ch.first + p + 1]; ++r) seg[r - ch.r0] = p;
+    }
+    loc[np] = L;
+    // The arena is reused per chunk: finish the previous chunk's copies first.
+    HK_CHECK(hipStreamSynchronize(s), "teacher-forced kernels failed");
+    ar.reset();
+    Inputs in{};
+    if ((st = upload_inputs(ctx, ar, coords + ch.r0 * 15, atom_sources + ch.r0 * 5, nullptr, nullptr, nullptr, nullptr, L,
+                            in)) != HKBS_OK)
+      return st;
+    int32_t* d_tok = ar.take<int32_t>(L);
+    int32_t* d_pos = ar.take<int32_t>(L);
+    int32_t* d_seg = ar.take<int32_t>(L);
+    int64_t* d_off = ar.take<int64_t>(np + 1);
+    float* d_lp = ar.take<float>((size_t)L * kV);
+    HK_CHECK(hipMemcpyAsync(d_tok, tokens + ch.r0, (size_t)L * 4, hipMemcpyHostToDevice, s), "H2D failed");
+    HK_CHECK(hipMemcpyAsync(d_pos, pos.data() + ch.r0, (size_t)L * 4, hipMemcpyHostToDevice, s), "H2D failed");
+    HK_CHECK(hipMemcpyAsync(d_seg, seg.data(), (size_t)L * 4, hipMemcpyHostToDevice, s), "H2D failed");
+    HK_CHECK(hipMemcpyAsync(d_off, loc.data(), (size_t)(np + 1) * 8, hipMemcpyHostToDevice, s), "H2D failed");
+    if ((st = teacher_forced_chunk(ctx, in.coords, in.src, nullptr, nullptr, d_tok, d_pos, L, ch.K, d_seg, d_off, d_lp,
+                                   ar)) != HKBS_OK)
+      return st;
+    HK_CHECK(hipMemcpyAsync(log_probs + ch.r0 * kV, d_lp, (size_t)L * kV * 4, hipMemcpyDeviceToHost, s), "D2H failed");
+  }
+  HK_CHECK(hipStreamSynchronize(s), "teacher-forced kernels failed");
+  if (scores) {
+    std::vector<float> mask;
+    for (int i = 0; i < n; ++i) {
+      const int64_t o = offsets[i];
+      const int L = static_cast<int>(offsets[i + 1] - o);
+      residue_mask_host(atom_sources + o * 5, L, mask);
+      scores[i] = average_nll_host(tokens + o, log_probs + o * kV, nullptr, mask.data(), L);
+    }
+  }
+  return HKBS_OK;
 }
 
 hkbs_status hkbs_pmpnn_knn(hkbs_pmpnn* ctx, const float* coords, const uint8_t* atom_sources, int32_t L, int32_t* idx,

@@ -353,6 +353,13 @@ hipError_t launch_decoder_precompute(const ModelDev& m, const float* h_v, const 
   return hipGetLastError();
 }
 
+hipError_t launch_q_precompute(const ModelDev& m, const float* h_v, int L, float* Q, hipStream_t stream) {
+  if (L <= 0) return hipSuccess;
+  rows_gemm_kernel<<<dim3((unsigned)((L + kGemmRows - 1) / kGemmRows), kLayers + 1), 256, 0, stream>>>(
+      h_v, (size_t)L, m.W1d_dec_p, (kLayers + 1) * kH, Q);
+  return hipGetLastError();
+}
+
 hipError_t launch_decode(const ModelDev& m, const DecodeArgs& a, hipStream_t stream) {
   if (a.L <= 0 || a.B <= 0) return hipSuccess;
   decode_kernel<<<a.B, kThreads, 0, stream>>>(m, a);

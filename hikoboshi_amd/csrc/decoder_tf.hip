@@ -1,0 +1,246 @@
+// Teacher-forced ProteinMPNN decoder (scoring).
+//
+// Reference: run_teacher_forced_decoder (cpp/modules/mpnn/inverse_fold_scalar.cpp:575-663)
+// with proteinmpnn_decoder_layer_scalar over all L rows
+// (cpp/modules/mpnn/decoder_layer_scalar.cpp:26-151) and a plain log_softmax
+// (cpp/primitives/compute/log_softmax_scalar.cpp:8-37). With the causal masks
+// of the decoding order, row t of layer l sees for neighbour j
+//   bw (j before t): [h_E_tj, W_s[tok_j], h^l_j],  fw: [h_E_tj, 0, h^0_j],
+// both scaled by the row mask. As in the autoregressive kernel the W1 product
+// is split into A_t = W1a h^l_t + b1, E1 = W1b h_E (here computed in the edge
+// kernel on MFMA, every edge is used once per layer), R^l_j = W1d h^l_j +
+// W1c W_s[tok_j] and Q^l_j = W1d h^0_j; and sum_k (W3 g_k + b3) = W3 sum_k g_k + K b3.
+// Per layer:
+//   tf_edge_kernel  tiles of whole residues (<= 96 edge rows): W1b and W2 on
+//                   fp32 MFMA, GELU, neighbour sum (all K slots, no attention mask).
+//   tf_node_kernel  tiles of 16 residues: W3, LN1, FFN, LN2, row-mask gate,
+//                   then the next layer's [A | R] terms, or for the last layer
+//                   logits and log_softmax in the reference's order.
+// Rows may belong to different proteins of a ragged batch: every neighbour
+// index is global, so the kernels never look at protein boundaries.
+#include "device_math.hpp"
+#include "pmpnn_internal.hpp"
+
+namespace hkbs {
+namespace {
+
+constexpr int kRows = 96;
+constexpr int kLd = kH + 4;
+constexpr int kLdF = kFF + 4;
+
+// NB[r] = [A^0_r = W1a_0 h^0_r + b1_0 | R^0_r = W1d_0 h^0_r + T_0[tok_r]]
+__global__ void tf_init_kernel(ModelDev m, const float* __restrict__ Q, const int32_t* __restrict__ tokens, int L,
+                               float* __restrict__ NB) {
+  const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= (size_t)L * kH) return;
+  const size_t r = i / kH;
+  const int c = static_cast<int>(i % kH);
+  NB[r * 256 + c] = Q[((size_t)3 * L + r) * kH + c] + m.dec[0].b1[c];
+  NB[r * 256 + kH + c] = Q[r * kH + c] + m.dec[0].T[tokens[r] * kH + c];
+}
+
+__global__ __launch_bounds__(256) void tf_edge_kernel(DecLayerDev w, const float* __restrict__ W1b_p, int layer,
+                                                      const float* __restrict__ h_e, const int32_t* __restrict__ idx,
+                                                      const int32_t* __restrict__ pos, const float* __restrict__ mask,
+                                                      const float* __restrict__ NB, const float* __restrict__ Ql, int L,
+                                                      int K, float* __restrict__ msg_sum) {
+  __shared__ __attribute__((aligned(16))) float A[kRows * kLd];
+  const int nres = kRows / K;
+  const int r0 = blockIdx.x * nres;
+  const int nr = min(nres, L - r0);
+  const int n_rows = nr * K;
+  const size_t slot0 = (size_t)r0 * K;
+  const int wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63;
+
+  for (int task = threadIdx.x; task < kRows * (kH / 4); task += blockDim.x) {
+    const int row = task / (kH / 4), c4 = task % (kH / 4);
+    float4 v = make_float4(0.F, 0.F, 0.F, 0.F);
+    if (row < n_rows) v = *reinterpret_cast<const float4*>(h_e + (slot0 + row) * kH + 4 * c4);
+    *reinterpret_cast<float4*>(A + row * kLd + 4 * c4) = v;
+  }
+  __syncthreads();
+  floatx4 acc[6][2];
+  zero_acc(acc);
+  mfma_tile<6, 2>(A, kLd, W1b_p, kLayers * kH, layer * kH + wave * 32, kH, acc);
+  __syncthreads();
+#pragma unroll
+  for (int mb = 0; mb < 6; ++mb)
+#pragma unroll
+    for (int nb = 0; nb < 2; ++nb)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int row = mb * 16 + 4 * (lane >> 4) + i;
+        const int col = wave * 32 + nb * 16 + (lane & 15);
+        float v = 0.0F;
+        if (row < n_rows) {
+          const int t = r0 + row / K;
+          const int j = idx[slot0 + row];
+          float x = NB[(size_t)t * 256 + col];
+          if (j >= 0 && j < L && mask[t] != 0.0F)
+            x += acc[mb][nb][i] + (pos[j] < pos[t] ? NB[(size_t)j * 256 + kH + col] : Ql[(size_t)j * kH + col]);
+          v = gelu(x);
+        }
+        A[row * kLd + col] = v;
+      }
+  __syncthreads();
+  zero_acc(acc);
+  mfma_tile<6, 2>(A, kLd, w.W2_p, kH, wave * 32, kH, acc);
+  __syncthreads();
+#pragma unroll
+  for (int mb = 0; mb < 6; ++mb)
+#pragma unroll
+    for (int nb = 0; nb < 2; ++nb)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int row = mb * 16 + 4 * (lane >> 4) + i;
+        const int col = wave * 32 + nb * 16 + (lane & 15);
+        A[row * kLd + col] = (row < n_rows) ? gelu(acc[mb][nb][i] + w.b2[col]) : 0.0F;
+      }
+  __syncthreads();
+  for (int task = threadIdx.x; task < nr * kH; task += blockDim.x) {
+    const int lr = task / kH, c = task % kH;
+    float s = 0.0F;
+    for (int k = 0; k < K; ++k) s += A[(lr * K + k) * kLd + c];
+    msg_sum[(size_t)(r0 + lr) * kH + c] = s;
+  }
+}
+
+__global__ __launch_bounds__(256) void tf_node_kernel(ModelDev m, int layer, const float* __restrict__ msg_sum,
+                                                      const float* __restrict__ mask, const int32_t* __restrict__ tokens,
+                                                      int L, int K, float* __restrict__ h, float* __restrict__ NB,
+                                                      float* __restrict__ log_probs) {
+  __shared__ __attribute__((aligned(16))) float A[16 * kLd];
+  __shared__ __attribute__((aligned(16))) float X[16 * kLd];
+  __shared__ __attribute__((aligned(16))) float F[16 * kLdF];
+  const DecLayerDev& w = m.dec[layer];
+  const int r0 = blockIdx.x * 16;
+  const int wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63;
+
+  for (int task = threadIdx.x; task < 16 * (kH / 4); task += blockDim.x) {
+    const int row = task / (kH / 4), c4 = task % (kH / 4);
+    float4 v = make_float4(0.F, 0.F, 0.F, 0.F);
+    if (r0 + row < L) v = *reinterpret_cast<const float4*>(msg_sum + (size_t)(r0 + row) * kH + 4 * c4);
+    *reinterpret_cast<float4*>(A + row * kLd + 4 * c4) = v;
+  }
+  __syncthreads();
+  {
+    floatx4 acc[1][2];
+    zero_acc(acc);
+    mfma_tile<1, 2>(A, kLd, w.W3_p, kH, wave * 32, kH, acc);
+#pragma unroll
+    for (int nb = 0; nb < 2; ++nb)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int row = 4 * (lane >> 4) + i;
+        const int col = wave * 32 + nb * 16 + (lane & 15);
+        float v = 0.0F;
+        if (r0 + row < L)
+          v = h[(size_t)(r0 + row) * kH + col] + (acc[0][nb][i] + static_cast<float>(K) * w.b3[col]) * (1.0F / 30.0F);
+        X[row * kLd + col] = v;
+      }
+  }
+  __syncthreads();
+  for (int row = wave; row < 16; row += 4) ln_row_wave(X + row * kLd, w.n1g, w.n1b, A + row * kLd);  // h1
+  __syncthreads();
+  {
+    floatx4 acc[1][8];
+    zero_acc(acc);
+    mfma_tile<1, 8>(A, kLd, w.Win_p, kFF, wave * 128, kH, acc);
+#pragma unroll
+    for (int nb = 0; nb < 8; ++nb)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int row = 4 * (lane >> 4) + i;
+        const int col = wave * 128 + nb * 16 + (lane & 15);
+        F[row * kLdF + col] = gelu(acc[0][nb][i] + w.bin[col]);
+      }
+  }
+  __syncthreads();
+  {
+    floatx4 acc[1][2];
+    zero_acc(acc);
+    mfma_tile<1, 2>(F, kLdF, w.Wout_p, kH, wave * 32, kFF, acc);
+#pragma unroll
+    for (int nb = 0; nb < 2; ++nb)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int row = 4 * (lane >> 4) + i;
+        const int col = wave * 32 + nb * 16 + (lane & 15);
+        X[row * kLd + col] = A[row * kLd + col] + (acc[0][nb][i] + w.bout[col]);
+      }
+  }
+  __syncthreads();
+  for (int row = wave; row < 16; row += 4) {
+    float* out = A + row * kLd;
+    ln_row_wave(X + row * kLd, w.n2g, w.n2b, out);
+    const float mk = (r0 + row < L) ? mask[r0 + row] : 0.0F;
+    if (mk != 1.0F) {  // decoder_layer_scalar.cpp:123-140
+      out[lane] *= mk;
+      out[lane + 64] *= mk;
+    }
+    if (r0 + row < L) {
+      h[(size_t)(r0 + row) * kH + lane] = out[lane];
+      h[(size_t)(r0 + row) * kH + lane + 64] = out[lane + 64];
+    }
+  }
+  __syncthreads();
+  if (layer + 1 < kLayers) {
+    const DecLayerDev& wn = m.dec[layer + 1];
+    floatx4 acc[1][4];
+    zero_acc(acc);
+    mfma_tile<1, 4>(A, kLd, w.Wnext_p, 2 * kH, wave * 64, kH, acc);
+#pragma unroll
+    for (int nb = 0; nb < 4; ++nb)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int row = 4 * (lane >> 4) + i;
+        const int col = wave * 64 + nb * 16 + (lane & 15);  // [0,128): A, [128,256): R
+        if (r0 + row >= L) continue;
+        const size_t r = r0 + row;
+        NB[r * 256 + col] = col < kH ? acc[0][nb][i] + wn.b1[col]
+                                     : acc[0][nb][i] + wn.T[tokens[r] * kH + (col - kH)];
+      }
+    return;
+  }
+  // logits = W_out h + b, then log_softmax, both in the reference's order.
+  __shared__ float lg[16 * 32];
+  for (int task = threadIdx.x; task < 16 * kV; task += blockDim.x) {
+    const int row = task / kV, v = task % kV;
+    float acc = 0.0F;
+    for (int p = 0; p < kH; ++p) acc += A[row * kLd + p] * m.Wlog_t[p * 32 + v];
+    lg[row * 32 + v] = acc + m.blog[v];
+  }
+  __syncthreads();
+  if (threadIdx.x < 16 && r0 + threadIdx.x < L) {
+    const float* z = lg + threadIdx.x * 32;
+    float row_max = -__builtin_inff();
+    for (int d = 0; d < kV; ++d)
+      if (z[d] > row_max) row_max = z[d];
+    float row_sum = 0.0F;
+    for (int d = 0; d < kV; ++d) row_sum += expf(z[d] - row_max);
+    const float lrs = logf(row_sum);
+    float* out = log_probs + (size_t)(r0 + threadIdx.x) * kV;
+    for (int d = 0; d < kV; ++d) out[d] = (z[d] - row_max) - lrs;
+  }
+}
+
+}  // namespace
+
+hipError_t launch_teacher_forced(const ModelDev& m, const TfArgs& a, hipStream_t stream) {
+  const int L = a.L, K = a.K;
+  if (L <= 0) return hipSuccess;
+  tf_init_kernel<<<(unsigned)(((size_t)L * kH + 255) / 256), 256, 0, stream>>>(m, a.Q, a.tokens, L, a.NB);
+  const int nres = kRows / K;
+  const unsigned edge_tiles = (unsigned)((L + nres - 1) / nres);
+  const unsigned node_tiles = (unsigned)((L + 15) / 16);
+  for (int l = 0; l < kLayers; ++l) {
+    tf_edge_kernel<<<edge_tiles, 256, 0, stream>>>(m.dec[l], m.W1b_dec_p, l, a.h_e, a.idx, a.pos, a.mask, a.NB,
+                                                   a.Q + (size_t)l * L * kH, L, K, a.msg_sum);
+    tf_node_kernel<<<node_tiles, 256, 0, stream>>>(m, l, a.msg_sum, a.mask, a.tokens, L, K, a.h, a.NB, a.log_probs);
+  }
+  return hipGetLastError();
+}
+
+}  // namespace hkbs

@@ -82,17 +82,25 @@ __global__ void prep_ca_kernel(const float* __restrict__ coords, const uint8_t* 
   mask[r] = valid ? 1.0F : 0.0F;
 }
 
+// Rows of a ragged batch (seg != null) only see the residues of their own
+// protein, [offsets[seg[q]], offsets[seg[q] + 1]); indices stay global.
 __global__ __launch_bounds__(256) void knn_kernel(const float4* __restrict__ ca, int L, int K,
+                                                  const int32_t* __restrict__ seg, const int64_t* __restrict__ offsets,
                                                   int32_t* __restrict__ idx, float* __restrict__ d2) {
   const int lane = threadIdx.x & 63;
   const int q = blockIdx.x * 4 + (threadIdx.x >> 6);
   if (q >= L) return;  // whole wave exits together; no block barriers below
+  int lo = 0, hi = L;
+  if (seg) {
+    lo = static_cast<int>(offsets[seg[q]]);
+    hi = static_cast<int>(offsets[seg[q] + 1]);
+  }
   const float4 qc = ca[q];
   const bool qvalid = qc.w != 0.F;
 
   float row_max = 1.0e-6F;
   if (qvalid) {
-    for (int t = lane; t < L; t += 64) {
+    for (int t = lo + lane; t < hi; t += 64) {
       const float4 tc = ca[t];
       if (tc.w == 0.F) continue;
       const float c = knn_d2(qc, tc);
@@ -107,10 +115,10 @@ __global__ __launch_bounds__(256) void knn_kernel(const float4* __restrict__ ca,
 
   const uint64_t kNone = ~0ull;
   uint64_t best = kNone;  // lane i: i-th smallest key so far
-  for (int base = 0; base < L; base += 64) {
+  for (int base = lo; base < hi; base += 64) {
     const int t = base + lane;
     uint64_t key = kNone;
-    if (t < L) {
+    if (t < hi) {
       const float4 tc = ca[t];
       const float d = (qvalid && tc.w != 0.F) ? knn_d2(qc, tc) : row_max;
       if (d < __builtin_inff()) key = (static_cast<uint64_t>(__float_as_uint(d)) << 32) | static_cast<uint32_t>(t);
@@ -135,10 +143,11 @@ __global__ __launch_bounds__(256) void knn_kernel(const float4* __restrict__ ca,
 }  // namespace
 
 hipError_t launch_knn(const float* coords, const uint8_t* atom_src, int L, int K, int32_t* idx, float* d2,
-                      float* mask, float4* ca_scratch, hipStream_t stream) {
+                      float* mask, float4* ca_scratch, hipStream_t stream, const int32_t* seg,
+                      const int64_t* offsets) {
   if (L <= 0) return hipSuccess;
   prep_ca_kernel<<<(L + 255) / 256, 256, 0, stream>>>(coords, atom_src, L, ca_scratch, mask);
-  knn_kernel<<<(L + 3) / 4, 256, 0, stream>>>(ca_scratch, L, K, idx, d2);
+  knn_kernel<<<(L + 3) / 4, 256, 0, stream>>>(ca_scratch, L, K, seg, offsets, idx, d2);
   return hipGetLastError();
 }
 

@@ -45,6 +45,10 @@ struct DecLayerDev {
   const float* Win_t;  // [128][512]
   const float* Wout_t; // [512][128]
   const float* W1da_t; // [128][256]: columns [W1d | W1a] (layers 1, 2)
+  const float* W3_p;   // kpack16 128 -> 128 (teacher forcing)
+  const float* Win_p;  // kpack16 128 -> 512
+  const float* Wout_p; // kpack16 512 -> 128
+  const float* Wnext_p; // kpack16 128 -> 256: rows [W1a; W1d] of the next layer (layers 0, 1)
   const float* T;      // [21][128]: W1c . W_s[v]
   const float *b1, *b2, *b3, *bin, *bout;
   const float *n1g, *n1b, *n2g, *n2b;
@@ -67,8 +71,11 @@ struct ModelDev {
 };
 
 // Launchers (each enqueues on `stream`; shapes are validated by the caller).
+// seg/offsets (optional): ragged batch, row q belongs to protein seg[q] whose
+// residues are [offsets[seg[q]], offsets[seg[q] + 1]).
 hipError_t launch_knn(const float* coords, const uint8_t* atom_src, int L, int K, int32_t* idx,
-                      float* d2, float* mask, float4* ca_scratch, hipStream_t stream);
+                      float* d2, float* mask, float4* ca_scratch, hipStream_t stream,
+                      const int32_t* seg = nullptr, const int64_t* offsets = nullptr);
 // pos[b][orders[b][s]] = s for each of n_orders orders of length L.
 hipError_t launch_positions(const int32_t* orders, int L, int n_orders, int shared, int32_t* pos,
                             hipStream_t stream);
@@ -110,5 +117,21 @@ struct DecodeArgs {
   float* chosen_lp;       // [B][L] workspace: log-prob of the written token
 };
 hipError_t launch_decode(const ModelDev& m, const DecodeArgs& a, hipStream_t stream);
+// Q[l] = W1d_l h^0 (l < 3), Q[3] = W1a_0 h^0, without the E1 edge products.
+hipError_t launch_q_precompute(const ModelDev& m, const float* h_v, int L, float* Q, hipStream_t stream);
+struct TfArgs {
+  const int32_t* idx;     // [L][K] global neighbour indices
+  const int32_t* pos;     // [L] position of each residue in its protein's decoding order
+  const float* mask;      // [L]
+  const int32_t* tokens;  // [L]
+  const float* h_e;       // [L*K][128] encoder edge states
+  const float* Q;         // [4][L][128]
+  float* h;               // [L][128] in: encoder h_V, out: decoder state (overwritten)
+  float* NB;              // [L][256] workspace: [A | R] terms of the current layer
+  float* msg_sum;         // [L][128] workspace
+  float* log_probs;       // [L][21] output
+  int L, K;
+};
+hipError_t launch_teacher_forced(const ModelDev& m, const TfArgs& a, hipStream_t stream);
 
 }  // namespace hkbs

@@ -120,6 +120,16 @@ hkbs_status hkbs_pmpnn_score(hkbs_pmpnn* ctx, const float* coords, const uint8_t
                              const float* chain_mask, const int32_t* tokens,
                              const int32_t* order, int32_t L, float* log_probs, float* score);
 
+/* Teacher-forced scoring of a ragged batch of n single-chain proteins
+ * (configuration "4,096 backbones, L in [50, 500]"): protein i holds residues
+ * [offsets[i], offsets[i+1]) of coords [sum L,5,3], atom_sources [sum L,5] and
+ * tokens [sum L]; orders (or NULL = N-to-C) holds each protein's permutation
+ * of 0..L_i-1 at the same offsets. Outputs log_probs [sum L,21] and scores [n].
+ * Proteins are processed in chunks that share K = min(48, L). Host memory. */
+hkbs_status hkbs_pmpnn_score_batch(hkbs_pmpnn* ctx, int32_t n, const int64_t* offsets, const float* coords,
+                                   const uint8_t* atom_sources, const int32_t* tokens,
+                                   const int32_t* orders, float* log_probs, float* scores);
+
 /* Host helper: the reference's decoding order (decode_order_scalar.cpp:61-116)
  * for one sequence; chain_mask may be NULL. Bit-exact on the same libm. */
 hkbs_status hkbs_pmpnn_decode_order(const float* chain_mask, const uint8_t* atom_sources,

@@ -216,3 +216,65 @@ def test_design_deterministic(gpu_ctx):
     b = gpu_ctx.design(bb.coords, bb.atom_sources, 3, seeds, order_seeds=seeds)
     np.testing.assert_array_equal(a["tokens"], b["tokens"])
     np.testing.assert_array_equal(a["log_probs"], b["log_probs"])
+
+
+# ------------------------------------------------------- teacher forcing --
+
+@pytest.mark.parametrize("case", golden_cases(), ids=lambda c: c["fixture_id"])
+def test_teacher_forced_goldens(gpu_ctx, oracle, case):
+    # tests/parity/proteinmpnn_v48_020/recovery_parity.py:78-176: 1e-4 vs upstream PyTorch, argmax exact
+    bb, seq = pdb.read_pdb(FIXTURES / case["pdb"])
+    tok = pdb.sequence_to_tokens(seq)
+    _say(f"teacher forced {case['fixture_id']}")
+    lp, score = gpu_ctx.score(bb.coords, bb.atom_sources, tok)
+    gold = np.asarray(case["teacher_log_probs"], np.float32).reshape(case["teacher_log_probs_shape"])
+    olp, oscore = oracle.teacher_forced(bb, tok)
+    _say(f"  vs golden {np.abs(lp - gold).max():.3g}  vs oracle {np.abs(lp - olp).max():.3g}")
+    assert np.abs(lp - gold).max() <= 1e-4
+    assert np.abs(lp - olp).max() <= 1e-4
+    assert "".join(backbone.ALPHABET[i] for i in lp.argmax(1)) == case["teacher_argmax_sequence"]
+    assert score == pytest.approx(oscore, abs=1e-5)
+
+
+def test_teacher_forced_random_order_masks(gpu_ctx, oracle):
+    bb = backbone.single_chain(300, 5)
+    src = bb.atom_sources.copy()
+    src[[7, 150], 3] = 0
+    src[33, 4] = 0
+    bb = backbone.Backbone(bb.coords, src)
+    rng = np.random.default_rng(4)
+    tok = rng.integers(0, 21, 300).astype(np.int32)
+    order = rng.permutation(300).astype(np.int32)
+    cm = np.ones(300, np.float32)
+    cm[100:140] = 0
+    _say("teacher forced L=300 random order, masks")
+    lp, score = gpu_ctx.score(bb.coords, bb.atom_sources, tok, order=order, chain_mask=cm)
+    enc = oracle.encode(bb)
+    olp, oscore = oracle.teacher_forced_decode(enc, tok, order, chain_mask=cm)
+    _say(f"  max|dlogp|={np.abs(lp - olp).max():.3g}")
+    assert np.abs(lp - olp).max() <= 1e-4
+    assert score == pytest.approx(oscore, abs=1e-5)
+    with pytest.raises(_lib.HkbsError) as e:
+        gpu_ctx.score(bb.coords, bb.atom_sources, np.full(300, 21, np.int32))
+    assert e.value.code == _lib.INVALID_ARGUMENT
+
+
+def test_teacher_forced_ragged_batch(gpu_ctx, oracle):
+    # ragged batch as in the scoring configuration (lengths in [50, 500]) plus one L < 48 protein
+    coords, src, tok, off = backbone.ragged_batch(5, 11, lmin=50, lmax=260)
+    small = backbone.single_chain(30, 2)
+    coords = np.concatenate([coords, small.coords])
+    src = np.concatenate([src, small.atom_sources])
+    tok = np.concatenate([tok, np.arange(30, dtype=np.int32) % 20])
+    off = np.append(off, off[-1] + 30)
+    _say(f"teacher forced ragged batch lengths {np.diff(off).tolist()}")
+    lp, scores = gpu_ctx.score_batch(coords, src, tok, off)
+    worst = 0.0
+    for i in range(len(off) - 1):
+        sl = slice(off[i], off[i + 1])
+        bb = backbone.Backbone(coords[sl], src[sl])
+        olp, oscore = oracle.teacher_forced(bb, tok[sl])
+        worst = max(worst, float(np.abs(lp[sl] - olp).max()))
+        assert scores[i] == pytest.approx(oscore, abs=1e-5)
+    _say(f"  max|dlogp|={worst:.3g}")
+    assert worst <= 1e-4
