@@ -354,6 +354,7 @@ struct hkbs_pmpnn {
   bool timing = false;
   bool timed = false;  // events hold a recorded design call
   hipEvent_t ev[4] = {nullptr, nullptr, nullptr, nullptr};
+  uint32_t* fault = nullptr;  // device word raised by the last decode if a team barrier timed out
 };
 
 namespace {
@@ -627,7 +628,8 @@ size_t decode_bytes(int L, int K, int B) {
   return aligned_bytes<float>(kLayers * S * kH) + aligned_bytes<float>((size_t)(kLayers + 1) * L * kH) +
          2 * aligned_bytes<int32_t>((size_t)B * L) + aligned_bytes<uint64_t>(B) +
          aligned_bytes<float>((size_t)B * kLayers * L * kH) + aligned_bytes<int32_t>((size_t)B * L) +
-         aligned_bytes<float>((size_t)B * L * kV) + aligned_bytes<float>((size_t)B * L) + aligned_bytes<float>(B);
+         aligned_bytes<float>((size_t)B * L * kV) + aligned_bytes<float>((size_t)B * L) + aligned_bytes<float>(B) +
+         aligned_bytes<uint32_t>((size_t)B + 1);
 }
 
 hkbs_status enter(hkbs_pmpnn* ctx) {
@@ -654,11 +656,14 @@ hkbs_status design_on_device(hkbs_pmpnn* ctx, const float* coords, const uint8_t
   float* Q = ar.take<float>((size_t)(kLayers + 1) * L * kH);
   int32_t* pos = ar.take<int32_t>((size_t)B * L);
   float* R = ar.take<float>((size_t)B * kLayers * L * kH);
+  uint32_t* sync = ar.take<uint32_t>((size_t)B + 1);  // B team counters + fault word
+  ctx->fault = sync + B;
   if (ctx->timing) HK_CHECK(hipEventRecord(ctx->ev[0], ctx->stream), "event record failed");
   HK_CHECK(run_encode(ctx, coords, src, resid, chain, L, K, e), "encoder launch failed");
   if (ctx->timing) HK_CHECK(hipEventRecord(ctx->ev[1], ctx->stream), "event record failed");
   HK_CHECK(launch_decoder_precompute(ctx->model, e.h_v, e.h_e, L, K, E1, Q, ctx->stream), "decoder precompute failed");
   HK_CHECK(launch_positions(orders, L, shared ? 1 : B, shared, pos, ctx->stream), "position kernel failed");
+  HK_CHECK(launch_zero(reinterpret_cast<float*>(sync), (size_t)B + 1, ctx->stream), "workspace clear failed");
   if (ctx->timing) HK_CHECK(hipEventRecord(ctx->ev[2], ctx->stream), "event record failed");
   DecodeArgs a{};
   a.idx = e.idx;
@@ -682,6 +687,8 @@ hkbs_status design_on_device(hkbs_pmpnn* ctx, const float* coords, const uint8_t
   a.log_probs = log_probs;
   a.scores = scores;
   a.chosen_lp = chosen;
+  a.sync = sync;
+  a.fault = sync + B;
   HK_CHECK(launch_decode(ctx->model, a, ctx->stream), "decode launch failed");
   if (ctx->timing) {
     HK_CHECK(hipEventRecord(ctx->ev[3], ctx->stream), "event record failed");
@@ -851,7 +858,10 @@ hkbs_status hkbs_pmpnn_design(hkbs_pmpnn* ctx, const float* coords, const uint8_
   HK_CHECK(hipMemcpyAsync(tokens, d_tokens, (size_t)B * L * 4, hipMemcpyDeviceToHost, s), "D2H failed");
   if (log_probs) HK_CHECK(hipMemcpyAsync(log_probs, d_lp, (size_t)B * L * kV * 4, hipMemcpyDeviceToHost, s), "D2H failed");
   if (scores) HK_CHECK(hipMemcpyAsync(scores, d_scores, (size_t)B * 4, hipMemcpyDeviceToHost, s), "D2H failed");
+  uint32_t fault = 0;
+  HK_CHECK(hipMemcpyAsync(&fault, ctx->fault, sizeof(fault), hipMemcpyDeviceToHost, s), "D2H failed");
   HK_CHECK(hipStreamSynchronize(s), "design kernels failed");
+  if (fault) return fail(HKBS_INTERNAL_ERROR, "decode team barrier timed out");
   if (orders_out) {
     for (int b = 0; b < B; ++b)
       std::memcpy(orders_out + (size_t)b * L, host_orders.data() + (shared ? 0 : (size_t)b * L), (size_t)L * 4);

@@ -21,6 +21,10 @@
 //
 // One workgroup decodes one sequence for all L steps (persistent); the
 // sequences of a batch are independent once the encoder outputs exist.
+// Consecutive independent residues are decoded together (see decode_kernel).
+#include <algorithm>
+#include <cstdlib>
+
 #include "device_math.hpp"
 #include "pmpnn_internal.hpp"
 
@@ -30,64 +34,162 @@ namespace {
 constexpr int kLd = kH + 4;  // 132
 constexpr int kThreads = 512;
 
-// y[o] = sum_p x[p] Wt[p][o] (+ bias) for OUT outputs and IN inputs on all
-// threads of the block: each thread loads its PER float4 weights up front
-// (all in flight), partial sums meet in LDS. part >= 2048 floats.
+constexpr int kGroup = 4;  // residues decoded together when independent
+
+// Y[i][o] = sum_p X[i][p] Wt[p][o] (+ bias) for i < m rows (m <= kGroup), OUT
+// outputs and IN inputs on all threads: each thread loads its PER float4
+// weights once (all in flight) and applies them to every row; partial sums
+// meet in LDS. X rows have stride IN, Y rows stride ldy. part >= 8192 floats.
 template <int IN, int OUT>
-__device__ inline void gemv(const float* __restrict__ Wt, const float* x, const float* __restrict__ bias,
-                            float* part, float* y) {
+__device__ inline void gemv_m(const float* __restrict__ Wt, const float* X, int m, const float* __restrict__ bias,
+                              float* part, float* Y, int ldy) {
   constexpr int Q4 = OUT / 4;            // float4 columns
   constexpr int GROUPS = kThreads / Q4;  // input groups
   constexpr int PER = IN / GROUPS;       // inputs per group
-  static_assert(GROUPS * OUT <= 2048, "partial buffer");
+  static_assert(GROUPS * OUT * kGroup <= 8192, "partial buffer");
   const int q = threadIdx.x % Q4;
   const int grp = threadIdx.x / Q4;
   const float* w = Wt + (size_t)(grp * PER) * OUT + 4 * q;
   float4 wv[PER];
 #pragma unroll
   for (int p = 0; p < PER; ++p) wv[p] = *reinterpret_cast<const float4*>(w + (size_t)p * OUT);
-  float4 acc = make_float4(0.F, 0.F, 0.F, 0.F);
+  for (int i = 0; i < m; ++i) {
+    float4 acc = make_float4(0.F, 0.F, 0.F, 0.F);
+    const float* x = X + i * IN + grp * PER;
 #pragma unroll
-  for (int p = 0; p < PER; ++p) {
-    const float xv = x[grp * PER + p];
-    acc.x += xv * wv[p].x;
-    acc.y += xv * wv[p].y;
-    acc.z += xv * wv[p].z;
-    acc.w += xv * wv[p].w;
+    for (int p = 0; p < PER; ++p) {
+      const float xv = x[p];
+      acc.x += xv * wv[p].x;
+      acc.y += xv * wv[p].y;
+      acc.z += xv * wv[p].z;
+      acc.w += xv * wv[p].w;
+    }
+    *reinterpret_cast<float4*>(part + (i * GROUPS + grp) * OUT + 4 * q) = acc;
   }
-  *reinterpret_cast<float4*>(part + grp * OUT + 4 * q) = acc;
   __syncthreads();
-  for (int o = threadIdx.x; o < OUT; o += kThreads) {
+  for (int task = threadIdx.x; task < m * OUT; task += kThreads) {
+    const int i = task / OUT, o = task % OUT;
     float s = 0.0F;
 #pragma unroll
-    for (int g = 0; g < GROUPS; ++g) s += part[g * OUT + o];
-    y[o] = bias ? s + bias[o] : s;
+    for (int g = 0; g < GROUPS; ++g) s += part[(i * GROUPS + g) * OUT + o];
+    Y[i * ldy + o] = bias ? s + bias[o] : s;
   }
   __syncthreads();
 }
 
-// LayerNorm of a 128-vector in LDS by wave 0; result visible after the barrier.
-__device__ inline void ln_vec(const float* x, const float* g, const float* b, float* out) {
-  if (threadIdx.x < 64) ln_row_wave(x, g, b, out);
-  __syncthreads();
+// One sampler draw on logits z (reference order, sampler_scalar.cpp:49-92);
+// state is the splitmix64 state before this draw. Writes log-probs to lp.
+__device__ inline int sample_token(const float* logits, float T, bool greedy, uint64_t state, float* lp) {
+  float z[kV], p[kV];
+  float row_max = -__builtin_inff();
+  for (int i = 0; i < kV; ++i) {
+    z[i] = logits[i] / T;
+    row_max = (row_max < z[i]) ? z[i] : row_max;
+  }
+  float row_sum = 0.0F;
+  for (int i = 0; i < kV; ++i) {
+    const float e = expf(z[i] - row_max);
+    p[i] = e;
+    row_sum += e;
+  }
+  const float log_sum = logf(row_sum);
+  const float inv_sum = 1.0F / row_sum;
+  for (int i = 0; i < kV; ++i) lp[i] = (z[i] - row_max) - log_sum;
+  if (greedy) {
+    int best = 0;
+    float bv = z[0];
+    for (int i = 1; i < kV; ++i)
+      if (z[i] > bv) {
+        best = i;
+        bv = z[i];
+      }
+    return best;
+  }
+  uint64_t zz = state + 0x9E3779B97F4A7C15ull;
+  zz = (zz ^ (zz >> 30)) * 0xBF58476D1CE4E5B9ull;
+  zz = (zz ^ (zz >> 27)) * 0x94D049BB133111EBull;
+  zz ^= zz >> 31;
+  const double u = static_cast<double>(zz >> 11) * (1.0 / 9007199254740992.0);
+  double cum = 0.0;
+  for (int i = 0; i < kV; ++i) {
+    cum += static_cast<double>(p[i] * inv_sum);
+    if (u < cum) return i;
+  }
+  return kV - 1;
 }
 
-__global__ __launch_bounds__(kThreads) void decode_kernel(ModelDev m, DecodeArgs a) {
-  __shared__ __attribute__((aligned(16))) float G[kKmax * kLd];
-  __shared__ __attribute__((aligned(16))) float part[2048];
-  __shared__ __attribute__((aligned(16))) float h[kH];
-  __shared__ __attribute__((aligned(16))) float hA[2 * kH];  // [A | scratch]
-  __shared__ __attribute__((aligned(16))) float x[kH];
-  __shared__ __attribute__((aligned(16))) float h1[kH];
-  __shared__ __attribute__((aligned(16))) float ff[kFF];
-  __shared__ __attribute__((aligned(16))) float P[2][2 * kH];  // [W1d h | W1a h] of layers 1, 2
-  __shared__ float logits[32];
-  __shared__ float tbl[17];
-  __shared__ int nbr[kKmax];
-  __shared__ int bwf[kKmax];
-  __shared__ int tok_s;
+// Relaxed device-scope accesses: written through to the level every CU of
+// the device reads, so team members see them after a team_sync.
+__device__ inline void store_dev(float* p, float v) { __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
+__device__ inline float load_dev(const float* p) {
+  return __hip_atomic_load(const_cast<float*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
 
-  const int b = blockIdx.x;
+constexpr uint32_t kSpinLimit = 1u << 20;  // polls (~1 s) before a team gives up
+
+// Barrier over the P workgroups of a team. Every wave first waits for its own
+// stores; thread 0 then counts the workgroup in and polls until all P have
+// arrived `target / P` times. Returns false (and raises the fault word) if the
+// wait does not end; the caller then stops so that every wave exits.
+__device__ inline bool team_sync(uint32_t* counter, uint32_t target, uint32_t* fault, int* bad) {
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    uint32_t n = 0;
+    while (__hip_atomic_load(counter, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < target) {
+      __builtin_amdgcn_s_sleep(1);
+      if (++n == kSpinLimit) {
+        *bad = 1;
+        __hip_atomic_store(fault, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        break;
+      }
+    }
+  }
+  __syncthreads();
+  return *bad == 0;
+}
+
+// Decodes one sequence per team of P workgroups (P = a.team, 1..4). Steps are
+// taken in groups of up to kGroup consecutive residues of the order in which
+// no residue is a kNN neighbour of a later one: such residues do not read
+// each other's state, so they run together (bw for every member means
+// "decoded before the group"). Member i of a group runs on team rank i % P;
+// a rank with several members shares each weight load and barrier between
+// them. Tokens are drawn in order, member i using the i-th next state of the
+// sequence's counter stream, so the split does not change any draw. The
+// state a later group reads (R rows, chosen log-probs) is written with
+// device-scope stores and published by a team barrier at the end of each
+// group. With P > 1 the grid is 8 * ceil(B / 8) * P workgroups and rank r of
+// sequence b runs as workgroup 8 (P (b / 8) + r) + b % 8, so that a team
+// shares one XCD when workgroups are dealt round-robin over the 8 XCDs; the
+// launch is cooperative, so every team member is resident.
+__global__ __launch_bounds__(kThreads) void decode_kernel(ModelDev m, DecodeArgs a) {
+  __shared__ __attribute__((aligned(16))) float G[2 * kKmax * kLd];
+  __shared__ __attribute__((aligned(16))) float part[8192];
+  __shared__ __attribute__((aligned(16))) float ff[kGroup * kFF];  // also [m][256] scratch
+  __shared__ __attribute__((aligned(16))) float h[kGroup * kH];
+  __shared__ __attribute__((aligned(16))) float hA[kGroup * kH];
+  __shared__ __attribute__((aligned(16))) float x[kGroup * kH];
+  __shared__ __attribute__((aligned(16))) float h1[kGroup * kH];
+  __shared__ __attribute__((aligned(16))) float Pd[kGroup * 2 * kH];  // W1d h^l of layers 1, 2
+  __shared__ float logits[kGroup * 32];
+  __shared__ float tbl[17];
+  __shared__ int nbr[kGroup * kKmax];
+  __shared__ int bwf[kGroup * kKmax];
+  __shared__ int tres[kGroup];
+  __shared__ int tok_s[kGroup];
+  __shared__ int m_s;
+  __shared__ int bad;
+
+  const int P = a.team;
+  int b = blockIdx.x, rank = 0;
+  if (P > 1) {
+    const int xcd = blockIdx.x % 8, slot = blockIdx.x / 8;
+    rank = slot % P;
+    b = (slot / P) * 8 + xcd;
+  }
+  if (b >= a.B) return;  // padding team: all of its ranks leave together
   const int L = a.L, K = a.K;
   const size_t S = (size_t)L * K;
   const int wave = threadIdx.x >> 6;
@@ -98,184 +200,239 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(ModelDev m, DecodeArgs
   int32_t* tokens = a.tokens + (size_t)b * L;
   float* lp_out = a.log_probs ? a.log_probs + (size_t)b * L * kV : nullptr;
   float* chosen = a.chosen_lp + (size_t)b * L;
+  uint32_t* counter = a.sync + b;
+  uint32_t passes = 0;
   uint64_t rng = a.seeds[b];
   const float T = (a.temperature > 0.0F && isfinite(a.temperature)) ? a.temperature : 1.0F;
   const bool greedy = a.greedy || a.temperature <= 0.0F;
   if (threadIdx.x < 17) tbl[threadIdx.x] = kExpNegTable[threadIdx.x];
+  if (threadIdx.x == 0) bad = 0;
   __syncthreads();
 
-  for (int step = 0; step < L; ++step) {
-    const int t = order[step];
-    if (t < 0 || t >= L) continue;  // malformed device order: skip the entry
-    const bool active = a.mask[t] != 0.0F;
-    if (!active) {
+  int step = 0;
+  while (step < L) {
+    const int t0 = order[step];
+    if (t0 < 0 || t0 >= L) {  // malformed device order: skip the entry
+      ++step;
+      continue;
+    }
+    if (a.mask[t0] == 0.0F) {
       // inverse_fold_scalar.cpp:804-813: fallback token, zero log-probs, no draw.
-      const int tok = (a.true_tokens && a.true_tokens[t] >= 0 && a.true_tokens[t] < kV) ? a.true_tokens[t] : kV - 1;
-      if (threadIdx.x == 0) {
-        tokens[t] = tok;
-        chosen[t] = 0.0F;
+      if (rank == 0) {
+        const int tok =
+            (a.true_tokens && a.true_tokens[t0] >= 0 && a.true_tokens[t0] < kV) ? a.true_tokens[t0] : kV - 1;
+        if (threadIdx.x == 0) {
+          tokens[t0] = tok;
+          store_dev(chosen + t0, 0.0F);
+        }
+        if (lp_out && threadIdx.x < kV) lp_out[(size_t)t0 * kV + threadIdx.x] = 0.0F;
+        for (int i = threadIdx.x; i < kLayers * kH; i += kThreads) {
+          const int l = i / kH, c = i % kH;
+          const float base = (l == 0) ? a.Q[(size_t)t0 * kH + c] : 0.0F;
+          store_dev(R + ((size_t)l * L + t0) * kH + c, base + m.dec[l].T[tok * kH + c]);
+        }
       }
-      if (lp_out && threadIdx.x < kV) lp_out[(size_t)t * kV + threadIdx.x] = 0.0F;
-      for (int i = threadIdx.x; i < kLayers * kH; i += kThreads) {
-        const int l = i / kH, c = i % kH;
-        const float base = (l == 0) ? a.Q[(size_t)t * kH + c] : 0.0F;
-        R[((size_t)l * L + t) * kH + c] = base + m.dec[l].T[tok * kH + c];
-      }
+      ++step;
+      if (P > 1 && !team_sync(counter, ++passes * P, a.fault, &bad)) break;
       __syncthreads();
       continue;
     }
-    if (threadIdx.x < K) {
-      const int j = a.idx[(size_t)t * K + threadIdx.x];
-      const bool valid = j >= 0 && j < L;
-      nbr[threadIdx.x] = valid ? j : -1;
-      bwf[threadIdx.x] = valid && pos[j] < step;
-    }
-    if (threadIdx.x < kH) {
-      h[threadIdx.x] = a.h_v[(size_t)t * kH + threadIdx.x];
-      // layer-0 W1a h^0_t comes from the precompute (Q block 3)
-      hA[threadIdx.x] = a.Q[((size_t)3 * L + t) * kH + threadIdx.x] + m.dec[0].b1[threadIdx.x];
+    // Group: stop before the first later residue that is inactive, out of
+    // range, or has an earlier group member among its neighbours.
+    if (threadIdx.x == 0) m_s = min(kGroup, L - step);
+    __syncthreads();
+    if (threadIdx.x < (kGroup - 1) * K) {
+      const int c = 1 + threadIdx.x / K, k = threadIdx.x % K;
+      if (step + c < L) {
+        const int tc = order[step + c];
+        bool stop = tc < 0 || tc >= L;
+        if (!stop) {
+          stop = a.mask[tc] == 0.0F;
+          const int j = a.idx[(size_t)tc * K + k];
+          if (j >= 0 && j < L && pos[j] >= step && pos[j] < step + c) stop = true;
+        }
+        if (stop) atomicMin(&m_s, c);
+      }
     }
     __syncthreads();
+    const int mg = m_s;
+    const int ml = mg > rank ? (mg - rank + P - 1) / P : 0;  // members of this rank: rank + P i
+    if (ml > 0) {
+      if (threadIdx.x < ml * K) {
+        const int i = threadIdx.x / K, k = threadIdx.x % K;
+        const int t = order[step + rank + P * i];
+        const int j = a.idx[(size_t)t * K + k];
+        const bool valid = j >= 0 && j < L;
+        nbr[i * kKmax + k] = valid ? j : -1;
+        bwf[i * kKmax + k] = valid && pos[j] < step;
+        if (k == 0) tres[i] = t;
+      }
+      for (int task = threadIdx.x; task < ml * kH; task += kThreads) {
+        const int i = task / kH, c = task % kH;
+        const int t = order[step + rank + P * i];
+        h[i * kH + c] = a.h_v[(size_t)t * kH + c];
+        // layer-0 W1a h^0_t comes from the precompute (Q block 3)
+        hA[i * kH + c] = a.Q[((size_t)3 * L + t) * kH + c] + m.dec[0].b1[c];
+      }
+      __syncthreads();
 
-    for (int l = 0; l < kLayers; ++l) {
-      const DecLayerDev& w = m.dec[l];
-      // Message rows g1_k = GELU(A + E1_tk + (bw ? R : Q)_j); rows >= K are zero.
-      const float* E1 = a.E1 + ((size_t)l * S + (size_t)t * K) * kH;
-      const float* Ql = a.Q + (size_t)l * L * kH;
-      const float* Rl = R + (size_t)l * L * kH;
-      for (int task = threadIdx.x; task < kKmax * (kH / 4); task += kThreads) {
-        const int k = task / (kH / 4);
-        const int c = 4 * (task % (kH / 4));
-        float4 xv = *reinterpret_cast<const float4*>(hA + c);
-        const int j = k < K ? nbr[k] : -1;
-        if (j >= 0) {
-          const float4 e = *reinterpret_cast<const float4*>(E1 + (size_t)k * kH + c);
-          const float4 z = *reinterpret_cast<const float4*>((bwf[k] ? Rl : Ql) + (size_t)j * kH + c);
-          xv.x += e.x + z.x;
-          xv.y += e.y + z.y;
-          xv.z += e.z + z.z;
-          xv.w += e.w + z.w;
-        }
-        float4 v = make_float4(gelu_fast(xv.x, tbl), gelu_fast(xv.y, tbl), gelu_fast(xv.z, tbl), gelu_fast(xv.w, tbl));
-        if (k >= K) v = make_float4(0.F, 0.F, 0.F, 0.F);
-        *reinterpret_cast<float4*>(G + k * kLd + c) = v;
-      }
-      __syncthreads();
-      {
-        floatx4 acc[3][1];
-        zero_acc(acc);
-        mfma_tile<3, 1>(G, kLd, w.W2_p, kH, wave * 16, kH, acc);
-        // x[col] = sum over valid rows of GELU(acc + b2)
-        const int col = wave * 16 + (lane & 15);
+      for (int l = 0; l < kLayers; ++l) {
+        const DecLayerDev& w = m.dec[l];
+        const float* Ql = a.Q + (size_t)l * L * kH;
+        const float* Rl = R + (size_t)l * L * kH;
+        // W2 fragments of this wave's 16 columns stay in registers for all members.
+        const int r = lane & 15, g = lane >> 4;
+        const int col = wave * 16 + r;
+        float4 bw[kH / 16];
+#pragma unroll
+        for (int kb = 0; kb < kH / 16; ++kb)
+          bw[kb] = *reinterpret_cast<const float4*>(w.W2_p + ((size_t)kb * kH + col) * 16 + 4 * g);
         const float b2 = w.b2[col];
-        float s = 0.0F;
+        for (int i0 = 0; i0 < ml; i0 += 2) {
+          {
+            // Message rows g1 = GELU(A + E1_tk + (bw ? R : Q)_j) of members i0, i0 + 1;
+            // rows >= K are zero. Thread owns columns c..c+3 of rows r0 + 16 s
+            // (member i0 + s / 3, slot 16 (s % 3) + r0); all gathers are issued
+            // before the first use.
+            constexpr int kS = 2 * kKmax / 16;
+            static_assert(kKmax == 48 && kThreads == 512, "row mapping");
+            const int c = 4 * (threadIdx.x & 31);
+            const int r0 = threadIdx.x >> 5;
+            float4 e[kS], z[kS];
 #pragma unroll
-        for (int mb = 0; mb < 3; ++mb)
+            for (int s = 0; s < kS; ++s) {
+              const int i = i0 + s / 3, k = 16 * (s % 3) + r0;
+              e[s] = make_float4(0.F, 0.F, 0.F, 0.F);
+              z[s] = e[s];
+              if (i < ml && k < K) {
+                const int j = nbr[i * kKmax + k];
+                if (j >= 0) {
+                  e[s] = *reinterpret_cast<const float4*>(a.E1 + ((size_t)l * S + (size_t)tres[i] * K + k) * kH + c);
+                  z[s] = *reinterpret_cast<const float4*>((bwf[i * kKmax + k] ? Rl : Ql) + (size_t)j * kH + c);
+                }
+              }
+            }
 #pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            const int row = mb * 16 + 4 * (lane >> 4) + i;
-            const float g = gelu_fast(acc[mb][0][i] + b2, tbl);
-            s += row < K ? g : 0.0F;
+            for (int s = 0; s < kS; ++s) {
+              const int i = i0 + s / 3, k = 16 * (s % 3) + r0;
+              if (i < ml) {
+                float4 xv = *reinterpret_cast<const float4*>(hA + i * kH + c);
+                xv.x += e[s].x + z[s].x;
+                xv.y += e[s].y + z[s].y;
+                xv.z += e[s].z + z[s].z;
+                xv.w += e[s].w + z[s].w;
+                float4 v = make_float4(gelu_fast(xv.x, tbl), gelu_fast(xv.y, tbl), gelu_fast(xv.z, tbl),
+                                       gelu_fast(xv.w, tbl));
+                if (k >= K) v = make_float4(0.F, 0.F, 0.F, 0.F);
+                *reinterpret_cast<float4*>(G + ((s / 3) * kKmax + k) * kLd + c) = v;
+              }
+            }
           }
-        s += __shfl_xor(s, 16, 64);
-        s += __shfl_xor(s, 32, 64);
-        if (lane < 16) x[col] = s;
-      }
-      __syncthreads();
-      // upd = (W3 s + K b3) / 30 ; h1 = LN1(h + upd)
-      gemv<kH, kH>(w.W3_t, x, nullptr, part, hA + kH);
-      if (threadIdx.x < kH) {
-        const int c = threadIdx.x;
-        x[c] = h[c] + (hA[kH + c] + static_cast<float>(K) * w.b3[c]) * (1.0F / 30.0F);
-      }
-      __syncthreads();
-      ln_vec(x, w.n1g, w.n1b, h1);
-      gemv<kH, kFF>(w.Win_t, h1, w.bin, part, ff);
-      ff[threadIdx.x] = gelu_fast(ff[threadIdx.x], tbl);
-      __syncthreads();
-      gemv<kFF, kH>(w.Wout_t, ff, w.bout, part, hA + kH);
-      if (threadIdx.x < kH) x[threadIdx.x] = h1[threadIdx.x] + hA[kH + threadIdx.x];
-      __syncthreads();
-      ln_vec(x, w.n2g, w.n2b, h);  // h = h^{l+1}_t (active residue: mask gate is 1)
-      if (l + 1 < kLayers) {
-        // fused [W1d | W1a] of the next layer: P (for R) and A (next message rows)
-        gemv<kH, 2 * kH>(m.dec[l + 1].W1da_t, h, nullptr, part, P[l]);
-        if (threadIdx.x < kH) hA[threadIdx.x] = P[l][kH + threadIdx.x] + m.dec[l + 1].b1[threadIdx.x];
+          __syncthreads();
+          for (int i = i0; i < ml && i < i0 + 2; ++i) {
+            const float* Gi = G + (i - i0) * kKmax * kLd;
+            floatx4 acc[3];
+#pragma unroll
+            for (int mb = 0; mb < 3; ++mb) acc[mb] = floatx4{0.F, 0.F, 0.F, 0.F};
+#pragma unroll
+            for (int kb = 0; kb < kH / 16; ++kb) {
+#pragma unroll
+              for (int mb = 0; mb < 3; ++mb) {
+                const float4 av = *reinterpret_cast<const float4*>(Gi + (mb * 16 + r) * kLd + kb * 16 + 4 * g);
+                acc[mb] = mfma16(av.x, bw[kb].x, acc[mb]);
+                acc[mb] = mfma16(av.y, bw[kb].y, acc[mb]);
+                acc[mb] = mfma16(av.z, bw[kb].z, acc[mb]);
+                acc[mb] = mfma16(av.w, bw[kb].w, acc[mb]);
+              }
+            }
+            // x[i][col] = sum over the member's K rows of GELU(acc + b2)
+            float sum = 0.0F;
+#pragma unroll
+            for (int mb = 0; mb < 3; ++mb)
+#pragma unroll
+              for (int e = 0; e < 4; ++e) {
+                const int row = mb * 16 + 4 * g + e;
+                const float gv = gelu_fast(acc[mb][e] + b2, tbl);
+                sum += row < K ? gv : 0.0F;
+              }
+            sum += __shfl_xor(sum, 16, 64);
+            sum += __shfl_xor(sum, 32, 64);
+            if (lane < 16) x[i * kH + col] = sum;
+          }
+          __syncthreads();
+        }
+        // upd = (W3 s + K b3) / 30 ; h1 = LN1(h + upd)
+        gemv_m<kH, kH>(w.W3_t, x, ml, nullptr, part, ff, kH);
+        for (int task = threadIdx.x; task < ml * kH; task += kThreads) {
+          const int c = task % kH;
+          x[task] = h[task] + (ff[task] + static_cast<float>(K) * w.b3[c]) * (1.0F / 30.0F);
+        }
         __syncthreads();
-      }
-    }
-    // logits = W_out h + b (padded to 32 outputs)
-    gemv<kH, 32>(m.Wlog_t, h, m.blog, part, logits);
-    if (threadIdx.x == 0) {
-      // sampler_scalar.cpp:49-92 in the reference's operation order.
-      float z[kV], p[kV];
-      float row_max = -__builtin_inff();
-      for (int i = 0; i < kV; ++i) {
-        z[i] = logits[i] / T;
-        row_max = (row_max < z[i]) ? z[i] : row_max;
-      }
-      float row_sum = 0.0F;
-      for (int i = 0; i < kV; ++i) {
-        const float e = expf(z[i] - row_max);
-        p[i] = e;
-        row_sum += e;
-      }
-      const float log_sum = logf(row_sum);
-      const float inv_sum = 1.0F / row_sum;
-      int s_tok;
-      if (greedy) {
-        s_tok = 0;
-        float bv = z[0];
-        for (int i = 1; i < kV; ++i)
-          if (z[i] > bv) {
-            s_tok = i;
-            bv = z[i];
+        if (wave < ml) ln_row_wave(x + wave * kH, w.n1g, w.n1b, h1 + wave * kH);
+        __syncthreads();
+        gemv_m<kH, kFF>(w.Win_t, h1, ml, w.bin, part, ff, kFF);
+        for (int task = threadIdx.x; task < ml * kFF; task += kThreads) ff[task] = gelu_fast(ff[task], tbl);
+        __syncthreads();
+        gemv_m<kFF, kH>(w.Wout_t, ff, ml, w.bout, part, x, kH);
+        for (int task = threadIdx.x; task < ml * kH; task += kThreads) x[task] = h1[task] + x[task];
+        __syncthreads();
+        if (wave < ml) ln_row_wave(x + wave * kH, w.n2g, w.n2b, h + wave * kH);  // h^{l+1} (mask gate is 1)
+        __syncthreads();
+        if (l + 1 < kLayers) {
+          // fused [W1d | W1a] of the next layer: W1d h is kept for R (completed with
+          // T[tok] after sampling), W1a h + b1 is the next A.
+          gemv_m<kH, 2 * kH>(m.dec[l + 1].W1da_t, h, ml, nullptr, part, ff, 2 * kH);
+          for (int task = threadIdx.x; task < ml * kH; task += kThreads) {
+            const int i = task / kH, c = task % kH;
+            Pd[(i * 2 + l) * kH + c] = ff[i * 2 * kH + c];
+            hA[task] = ff[i * 2 * kH + kH + c] + m.dec[l + 1].b1[c];
           }
-      } else {
-        rng += 0x9E3779B97F4A7C15ull;
-        uint64_t zz = rng;
-        zz = (zz ^ (zz >> 30)) * 0xBF58476D1CE4E5B9ull;
-        zz = (zz ^ (zz >> 27)) * 0x94D049BB133111EBull;
-        zz ^= zz >> 31;
-        const double u = static_cast<double>(zz >> 11) * (1.0 / 9007199254740992.0);
-        double cum = 0.0;
-        s_tok = kV - 1;
-        for (int i = 0; i < kV; ++i) {
-          cum += static_cast<double>(p[i] * inv_sum);
-          if (u < cum) {
-            s_tok = i;
-            break;
-          }
+          __syncthreads();
         }
       }
-      const float design = (a.chain_mask ? a.chain_mask[t] : 1.0F) * a.mask[t];
-      int tok = s_tok;
-      if (design == 0.0F)
-        tok = (a.true_tokens && a.true_tokens[t] >= 0 && a.true_tokens[t] < kV) ? a.true_tokens[t] : kV - 1;
-      tokens[t] = tok;
-      tok_s = tok;
-      for (int i = 0; i < kV; ++i) {
-        const float lpv = (z[i] - row_max) - log_sum;
-        if (lp_out) lp_out[(size_t)t * kV + i] = lpv;
-        if (i == tok) chosen[t] = lpv;
+      // logits = W_out h + b (padded to 32 outputs), then one draw per member.
+      gemv_m<kH, 32>(m.Wlog_t, h, ml, m.blog, part, logits, 32);
+      if (threadIdx.x < ml) {
+        const int i = threadIdx.x;
+        const int t = tres[i];
+        const int gi = rank + P * i;
+        float lpv[kV];
+        const int s_tok = sample_token(logits + i * 32, T, greedy, rng + (uint64_t)gi * 0x9E3779B97F4A7C15ull, lpv);
+        const float design = (a.chain_mask ? a.chain_mask[t] : 1.0F) * a.mask[t];
+        int tok = s_tok;
+        if (design == 0.0F)
+          tok = (a.true_tokens && a.true_tokens[t] >= 0 && a.true_tokens[t] < kV) ? a.true_tokens[t] : kV - 1;
+        tokens[t] = tok;
+        tok_s[i] = tok;
+        for (int v = 0; v < kV; ++v) {
+          if (lp_out) lp_out[(size_t)t * kV + v] = lpv[v];
+          if (v == tok) store_dev(chosen + t, lpv[v]);
+        }
+      }
+      __syncthreads();
+      for (int task = threadIdx.x; task < ml * kLayers * kH; task += kThreads) {
+        const int i = task / (kLayers * kH), l = (task / kH) % kLayers, c = task % kH;
+        const int t = tres[i];
+        const float base = (l == 0) ? a.Q[(size_t)t * kH + c] : Pd[(i * 2 + l - 1) * kH + c];
+        store_dev(R + ((size_t)l * L + t) * kH + c, base + m.dec[l].T[tok_s[i] * kH + c]);
       }
     }
-    __syncthreads();
-    const int tok = tok_s;
-    for (int i = threadIdx.x; i < kLayers * kH; i += kThreads) {
-      const int l = i / kH, c = i % kH;
-      const float base = (l == 0) ? a.Q[(size_t)t * kH + c] : P[l - 1][c];
-      R[((size_t)l * L + t) * kH + c] = base + m.dec[l].T[tok * kH + c];
-    }
+    if (!greedy) rng += (uint64_t)mg * 0x9E3779B97F4A7C15ull;
+    step += mg;
+    if (P > 1 && !team_sync(counter, ++passes * P, a.fault, &bad)) break;
     __syncthreads();
   }
   // Mean NLL over designed residues in residue order (inverse_fold_scalar.cpp:471-493).
-  if (a.scores && threadIdx.x == 0) {
+  if (a.scores && rank == 0 && threadIdx.x == 0) {
+    if (bad) {
+      a.scores[b] = __builtin_nanf("");
+      return;
+    }
     double loss = 0.0, msum = 0.0;
     for (int r = 0; r < L; ++r) {
       const float act = (a.chain_mask ? a.chain_mask[r] : 1.0F) * a.mask[r];
       if (act == 0.0F) continue;
-      loss -= static_cast<double>(chosen[r]);
+      loss -= static_cast<double>(load_dev(chosen + r));
       msum += static_cast<double>(act);
     }
     a.scores[b] = msum > 0.0 ? static_cast<float>(loss / msum) : 0.0F;
@@ -360,9 +517,32 @@ hipError_t launch_q_precompute(const ModelDev& m, const float* h_v, int L, float
   return hipGetLastError();
 }
 
-hipError_t launch_decode(const ModelDev& m, const DecodeArgs& a, hipStream_t stream) {
-  if (a.L <= 0 || a.B <= 0) return hipSuccess;
-  decode_kernel<<<a.B, kThreads, 0, stream>>>(m, a);
+hipError_t launch_decode(const ModelDev& m, const DecodeArgs& args, hipStream_t stream) {
+  if (args.L <= 0 || args.B <= 0) return hipSuccess;
+  DecodeArgs a = args;
+  ModelDev mm = m;
+  int dev = 0, cus = 0, coop = 0, per_cu = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e == hipSuccess) e = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
+  if (e == hipSuccess) e = hipDeviceGetAttribute(&coop, hipDeviceAttributeCooperativeLaunch, dev);
+  if (e == hipSuccess) e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, decode_kernel, kThreads, 0);
+  if (e != hipSuccess) return e;
+  const long resident = (long)cus * per_cu;
+  const long teams_per_xcd = (a.B + 7) / 8;
+  int P = 4;
+  if (const char* env = std::getenv("HKBS_DECODE_TEAM")) P = std::max(1, std::min(4, std::atoi(env)));
+  while (P > 1 && 8 * teams_per_xcd * P > resident) --P;
+  if (!coop || !a.sync || !a.fault) P = 1;
+  if (P > 1) {
+    a.team = P;
+    void* kargs[] = {&mm, &a};
+    e = hipLaunchCooperativeKernel(reinterpret_cast<const void*>(&decode_kernel),
+                                   dim3((unsigned)(8 * teams_per_xcd * P)), dim3(kThreads), kargs, 0, stream);
+    if (e == hipSuccess) return hipSuccess;
+    (void)hipGetLastError();  // not launchable as a team here: one workgroup per sequence
+  }
+  a.team = 1;
+  decode_kernel<<<a.B, kThreads, 0, stream>>>(mm, a);
   return hipGetLastError();
 }
 

@@ -115,7 +115,12 @@ struct DecodeArgs {
   float* log_probs;       // [B][L][21] or null
   float* scores;          // [B] or null
   float* chosen_lp;       // [B][L] workspace: log-prob of the written token
+  uint32_t* sync;         // [B] team barrier counters, zero at launch
+  uint32_t* fault;        // [1] set when a team barrier times out, zero at launch
+  int team;               // workgroups per sequence (set by launch_decode)
 };
+// Decodes with up to 4 workgroups per sequence when the device keeps every
+// workgroup of the grid resident (cooperative launch), else one per sequence.
 hipError_t launch_decode(const ModelDev& m, const DecodeArgs& a, hipStream_t stream);
 // Q[l] = W1d_l h^0 (l < 3), Q[3] = W1a_0 h^0, without the E1 edge products.
 hipError_t launch_q_precompute(const ModelDev& m, const float* h_v, int L, float* Q, hipStream_t stream);

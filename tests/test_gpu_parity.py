@@ -209,6 +209,30 @@ def test_design_errors(gpu_ctx):
         gpu_ctx.design(bb.coords, bb.atom_sources, 1, seeds, order_seeds=seeds, temperature=float("nan"))
 
 
+@pytest.mark.parametrize("B", [9, 64])
+def test_design_team_split_is_exact(gpu_ctx, oracle, B, monkeypatch):
+    """Several workgroups per sequence give the same bits as one workgroup per sequence."""
+    bb = backbone.single_chain(120, 4)
+    src = bb.atom_sources.copy()
+    src[[3, 60, 61], 0] = 0  # inactive residues take the one-residue path
+    bb = backbone.Backbone(bb.coords, src)
+    cm = np.ones(120, np.float32)
+    cm[40:50] = 0.0
+    tt = (np.arange(120) * 5 % 20).astype(np.int32)
+    seeds = (np.arange(B) + 31).astype(np.uint64)
+    out = {}
+    for team in ("1", "2", "4"):
+        monkeypatch.setenv("HKBS_DECODE_TEAM", team)
+        _say(f"design team={team} B={B}")
+        out[team] = gpu_ctx.design(bb.coords, bb.atom_sources, B, seeds, order_seeds=seeds, temperature=0.1,
+                                   chain_mask=cm, true_tokens=tt)
+    for team in ("2", "4"):
+        for key in ("tokens", "log_probs", "scores"):
+            np.testing.assert_array_equal(out[team][key], out["1"][key], err_msg=f"team {team} {key}")
+    check_design(oracle, bb, {k: v[:2] for k, v in out["4"].items()}, seeds[:2], 0.1, chain_mask=cm,
+                 true_tokens=tt)
+
+
 def test_design_deterministic(gpu_ctx):
     bb = backbone.single_chain(64, 2)
     seeds = np.array([3, 4, 5], dtype=np.uint64)
