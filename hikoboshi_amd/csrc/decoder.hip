@@ -36,45 +36,71 @@ constexpr int kThreads = 512;
 
 constexpr int kGroup = 4;  // residues decoded together when independent
 
-// Y[i][o] = sum_p X[i][p] Wt[p][o] (+ bias) for i < m rows (m <= kGroup), OUT
-// outputs and IN inputs on all threads: each thread loads its PER float4
-// weights once (all in flight) and applies them to every row; partial sums
-// meet in LDS. X rows have stride IN, Y rows stride ldy. part >= 8192 floats.
-template <int IN, int OUT>
-__device__ inline void gemv_m(const float* __restrict__ Wt, const float* X, int m, const float* __restrict__ bias,
-                              float* part, float* Y, int ldy) {
-  constexpr int Q4 = OUT / 4;            // float4 columns
-  constexpr int GROUPS = kThreads / Q4;  // input groups
-  constexpr int PER = IN / GROUPS;       // inputs per group
-  static_assert(GROUPS * OUT * kGroup <= 8192, "partial buffer");
-  const int q = threadIdx.x % Q4;
-  const int grp = threadIdx.x / Q4;
-  const float* w = Wt + (size_t)(grp * PER) * OUT + 4 * q;
-  float4 wv[PER];
+// Y[i][o] = sum_p X[i][p] Wt[p][o] for i < m rows (m <= kGroup), OUT outputs
+// and IN inputs on all threads. Thread (q, grp) owns float4 column q and
+// inputs [grp PER, (grp + 1) PER), taken in NP parts of PP inputs so that a
+// part's weight loads can be issued while the previous part (or the previous
+// step's reduction) is still running. fma() accumulates one part in input
+// order, store() leaves per-group partial sums in LDS (part >= 8192 floats),
+// and after a barrier sum() adds the groups of one output in a fixed order.
+template <int IN, int OUT, int NP = 1>
+struct Gemv {
+  static constexpr int Q4 = OUT / 4;            // float4 columns
+  static constexpr int GROUPS = kThreads / Q4;  // input groups
+  static constexpr int PER = IN / GROUPS;       // inputs per group
+  static constexpr int PP = PER / NP;           // inputs per part
+  static_assert(GROUPS * OUT * kGroup <= 8192 && PP * NP == PER, "partial buffer");
+  struct Part {
+    float4 w[PP];
+  };
+
+  static __device__ inline void load(Part& P, const float* __restrict__ Wt, int k) {
+    const int q = threadIdx.x % Q4, grp = threadIdx.x / Q4;
+    const float* p = Wt + (size_t)(grp * PER + k * PP) * OUT + 4 * q;
 #pragma unroll
-  for (int p = 0; p < PER; ++p) wv[p] = *reinterpret_cast<const float4*>(w + (size_t)p * OUT);
-  for (int i = 0; i < m; ++i) {
-    float4 acc = make_float4(0.F, 0.F, 0.F, 0.F);
-    const float* x = X + i * IN + grp * PER;
-#pragma unroll
-    for (int p = 0; p < PER; ++p) {
-      const float xv = x[p];
-      acc.x += xv * wv[p].x;
-      acc.y += xv * wv[p].y;
-      acc.z += xv * wv[p].z;
-      acc.w += xv * wv[p].w;
-    }
-    *reinterpret_cast<float4*>(part + (i * GROUPS + grp) * OUT + 4 * q) = acc;
+    for (int i = 0; i < PP; ++i) P.w[i] = *reinterpret_cast<const float4*>(p + (size_t)i * OUT);
   }
-  __syncthreads();
-  for (int task = threadIdx.x; task < m * OUT; task += kThreads) {
-    const int i = task / OUT, o = task % OUT;
+  static __device__ inline void fma(const Part& P, int k, const float* X, int m, float4 (&acc)[kGroup]) {
+    const int grp = threadIdx.x / Q4;
+#pragma unroll
+    for (int i = 0; i < kGroup; ++i) {
+      if (i >= m) break;
+      const float* x = X + i * IN + grp * PER + k * PP;
+#pragma unroll
+      for (int p = 0; p < PP; ++p) {
+        const float xv = x[p];
+        acc[i].x += xv * P.w[p].x;
+        acc[i].y += xv * P.w[p].y;
+        acc[i].z += xv * P.w[p].z;
+        acc[i].w += xv * P.w[p].w;
+      }
+    }
+  }
+  static __device__ inline void store(const float4 (&acc)[kGroup], int m, float* part) {
+    const int q = threadIdx.x % Q4, grp = threadIdx.x / Q4;
+#pragma unroll
+    for (int i = 0; i < kGroup; ++i) {
+      if (i >= m) break;
+      *reinterpret_cast<float4*>(part + (i * GROUPS + grp) * OUT + 4 * q) = acc[i];
+    }
+  }
+  static __device__ inline float sum(const float* part, int i, int o) {
     float s = 0.0F;
 #pragma unroll
     for (int g = 0; g < GROUPS; ++g) s += part[(i * GROUPS + g) * OUT + o];
-    Y[i * ldy + o] = bias ? s + bias[o] : s;
+    return s;
   }
-  __syncthreads();
+};
+
+using G3 = Gemv<kH, kH>;
+using GIn = Gemv<kH, kFF, 2>;
+using GOut = Gemv<kFF, kH, 2>;
+using GDa = Gemv<kH, 2 * kH>;
+using GLog = Gemv<kH, 32>;
+
+__device__ inline void zero4(float4 (&acc)[kGroup]) {
+#pragma unroll
+  for (int i = 0; i < kGroup; ++i) acc[i] = make_float4(0.F, 0.F, 0.F, 0.F);
 }
 
 // One sampler draw on logits z (reference order, sampler_scalar.cpp:49-92);
@@ -361,37 +387,97 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(ModelDev m, DecodeArgs
           }
           __syncthreads();
         }
-        // upd = (W3 s + K b3) / 30 ; h1 = LN1(h + upd)
-        gemv_m<kH, kH>(w.W3_t, x, ml, nullptr, part, ff, kH);
-        for (int task = threadIdx.x; task < ml * kH; task += kThreads) {
-          const int c = task % kH;
-          x[task] = h[task] + (ff[task] + static_cast<float>(K) * w.b3[c]) * (1.0F / 30.0F);
+        // upd = (W3 s + K b3) / 30 ; h1 = LN1(h + upd): wave i owns member i
+        float4 acc[kGroup];
+        zero4(acc);
+        G3::Part g3;
+        G3::load(g3, w.W3_t, 0);
+        G3::fma(g3, 0, x, ml, acc);
+        G3::store(acc, ml, part);
+        GIn::Part in0;  // first half of W_in in flight during the reduction and LN1
+        GIn::load(in0, w.Win_t, 0);
+        __syncthreads();
+        if (wave < ml) {
+          float v[2];
+#pragma unroll
+          for (int hh = 0; hh < 2; ++hh) {
+            const int c = lane + 64 * hh;
+            v[hh] = h[wave * kH + c] + (G3::sum(part, wave, c) + static_cast<float>(K) * w.b3[c]) * (1.0F / 30.0F);
+          }
+          ln_regs_wave(v[0], v[1], w.n1g, w.n1b, h1 + wave * kH);
         }
         __syncthreads();
-        if (wave < ml) ln_row_wave(x + wave * kH, w.n1g, w.n1b, h1 + wave * kH);
+        // f = GELU(W_in h1 + b)
+        zero4(acc);
+        GIn::fma(in0, 0, h1, ml, acc);
+        {
+          GIn::Part in1;
+          GIn::load(in1, w.Win_t, 1);
+          GIn::fma(in1, 1, h1, ml, acc);
+        }
+        GIn::store(acc, ml, part);
+        GOut::Part out0;  // first half of W_out in flight during the reduction and GELU
+        GOut::load(out0, w.Wout_t, 0);
         __syncthreads();
-        gemv_m<kH, kFF>(w.Win_t, h1, ml, w.bin, part, ff, kFF);
-        for (int task = threadIdx.x; task < ml * kFF; task += kThreads) ff[task] = gelu_fast(ff[task], tbl);
+        for (int task = threadIdx.x; task < ml * kFF; task += kThreads) {
+          const int i = task / kFF, o = task % kFF;
+          ff[task] = gelu_fast(GIn::sum(part, i, o) + w.bin[o], tbl);
+        }
         __syncthreads();
-        gemv_m<kFF, kH>(w.Wout_t, ff, ml, w.bout, part, x, kH);
-        for (int task = threadIdx.x; task < ml * kH; task += kThreads) x[task] = h1[task] + x[task];
+        // h^{l+1} = LN2(h1 + (W_out f + b)) (the mask gate is 1 for an active residue)
+        zero4(acc);
+        GOut::fma(out0, 0, ff, ml, acc);
+        {
+          GOut::Part out1;
+          GOut::load(out1, w.Wout_t, 1);
+          GOut::fma(out1, 1, ff, ml, acc);
+        }
+        GOut::store(acc, ml, part);
+        // The next layer's fused weights load during LN2. The last layer loads its
+        // own (unused) instead: an unconditional load keeps the register budget.
+        GDa::Part da;
+        GDa::load(da, m.dec[l + 1 < kLayers ? l + 1 : l].W1da_t, 0);
         __syncthreads();
-        if (wave < ml) ln_row_wave(x + wave * kH, w.n2g, w.n2b, h + wave * kH);  // h^{l+1} (mask gate is 1)
+        if (wave < ml) {
+          float v[2];
+#pragma unroll
+          for (int hh = 0; hh < 2; ++hh) {
+            const int c = lane + 64 * hh;
+            v[hh] = h1[wave * kH + c] + (GOut::sum(part, wave, c) + w.bout[c]);
+          }
+          ln_regs_wave(v[0], v[1], w.n2g, w.n2b, h + wave * kH);
+        }
         __syncthreads();
         if (l + 1 < kLayers) {
           // fused [W1d | W1a] of the next layer: W1d h is kept for R (completed with
           // T[tok] after sampling), W1a h + b1 is the next A.
-          gemv_m<kH, 2 * kH>(m.dec[l + 1].W1da_t, h, ml, nullptr, part, ff, 2 * kH);
+          zero4(acc);
+          GDa::fma(da, 0, h, ml, acc);
+          GDa::store(acc, ml, part);
+          __syncthreads();
           for (int task = threadIdx.x; task < ml * kH; task += kThreads) {
             const int i = task / kH, c = task % kH;
-            Pd[(i * 2 + l) * kH + c] = ff[i * 2 * kH + c];
-            hA[task] = ff[i * 2 * kH + kH + c] + m.dec[l + 1].b1[c];
+            Pd[(i * 2 + l) * kH + c] = GDa::sum(part, i, c);
+            hA[task] = GDa::sum(part, i, kH + c) + m.dec[l + 1].b1[c];
           }
           __syncthreads();
         }
       }
       // logits = W_out h + b (padded to 32 outputs), then one draw per member.
-      gemv_m<kH, 32>(m.Wlog_t, h, ml, m.blog, part, logits, 32);
+      {
+        float4 acc[kGroup];
+        zero4(acc);
+        GLog::Part lg;
+        GLog::load(lg, m.Wlog_t, 0);
+        GLog::fma(lg, 0, h, ml, acc);
+        GLog::store(acc, ml, part);
+      }
+      __syncthreads();
+      for (int task = threadIdx.x; task < ml * 32; task += kThreads) {
+        const int i = task / 32, o = task % 32;
+        logits[task] = GLog::sum(part, i, o) + m.blog[o];
+      }
+      __syncthreads();
       if (threadIdx.x < ml) {
         const int i = threadIdx.x;
         const int t = tres[i];

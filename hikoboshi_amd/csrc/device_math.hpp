@@ -251,15 +251,20 @@ __device__ inline float wave_sum(float v) {
   return v;
 }
 
-__device__ inline void ln_row_wave(const float* in, const float* g, const float* b, float* out) {
+// LayerNorm of a row held in registers (lane: elements lane and lane + 64).
+__device__ inline void ln_regs_wave(float x0, float x1, const float* g, const float* b, float* out) {
   const int lane = threadIdx.x & 63;
-  const float x0 = in[lane], x1 = in[lane + 64];
   const float mean = wave_sum(x0 + x1) * (1.0F / 128.0F);
   const float d0 = x0 - mean, d1 = x1 - mean;
   const float var = wave_sum(d0 * d0 + d1 * d1) * (1.0F / 128.0F);
   const float inv = 1.0F / sqrtf(var + 1.0e-5F);
   out[lane] = d0 * inv * g[lane] + b[lane];
   out[lane + 64] = d1 * inv * g[lane + 64] + b[lane + 64];
+}
+
+__device__ inline void ln_row_wave(const float* in, const float* g, const float* b, float* out) {
+  const int lane = threadIdx.x & 63;
+  ln_regs_wave(in[lane], in[lane + 64], g, b, out);
 }
 
 }  // namespace hkbs

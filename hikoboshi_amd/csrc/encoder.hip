@@ -19,7 +19,7 @@
 // Kernels per layer:
 //   edge_msg_kernel    tile of whole residues (<= 96 edge rows): W1 (e, h_j
 //                      terms), W2, W3, then the masked neighbour sum.
-//   node_kernel        tile of 32 residues: LN1, FFN, LN2, mask, and the W11
+//   node_kernel        tile of 4 residues: LN1, FFN, LN2, mask, and the W11
 //                      and next-layer W1 prefixes.
 //   edge_update_kernel tile of whole residues: W11, W12, W13, residual, LN3.
 #include "device_math.hpp"
@@ -33,8 +33,7 @@ constexpr int kLdE = 98;     // k-major leading dimension of edge tiles
 constexpr int kEdgeRM = 6;   // rows per thread (16 row groups)
 constexpr int kEdgeCN = 8;   // cols per thread (16 col groups)
 constexpr int kKC = 32;      // weight rows staged per chunk
-constexpr int kNodeRows = 32;
-constexpr int kLdN = 36;
+constexpr int kNodeRows = 4;
 
 // Loads rows of a [*, 128] row-major matrix into a k-major LDS tile
 // A[k * lda + row] (row < n_rows, gathered through rowptr), zero elsewhere.
@@ -130,84 +129,119 @@ __global__ __launch_bounds__(256) void edge_msg_kernel(EncLayerDev w, const floa
   }
 }
 
-// Node update for 32 residues: LN1(h + upd), FFN, LN2, mask; then the W11 prefix
-// of this layer's edge update and (when Wnext_t is given) the next layer's W1 prefix.
+// acc[j][r] += A[k][row0 + r] * Wt[k][c0 + j * CS] for k = k0 .. k0 + KB - 1 in
+// order (A k-major with leading dimension lda, one rounding per product and
+// per sum); w holds the KB weight rows of the thread's columns.
+template <int KB, int CPT, int RPT>
+__device__ inline void use_rows(const float (&w)[KB][CPT], const float* A, int lda, int row0, int k0,
+                                float (&acc)[CPT][RPT]) {
+#pragma clang fp contract(off)
+#pragma unroll
+  for (int kk = 0; kk < KB; ++kk) {
+    float a[RPT];
+#pragma unroll
+    for (int r = 0; r < RPT; ++r) a[r] = A[(k0 + kk) * lda + row0 + r];
+#pragma unroll
+    for (int j = 0; j < CPT; ++j)
+#pragma unroll
+      for (int r = 0; r < RPT; ++r) acc[j][r] = acc[j][r] + a[r] * w[kk][j];
+  }
+}
+
+template <int KB, int N, int CPT, int CS>
+__device__ inline void load_rows(float (&w)[KB][CPT], const float* __restrict__ Wt, int k0, int c0) {
+#pragma unroll
+  for (int kk = 0; kk < KB; ++kk)
+#pragma unroll
+    for (int j = 0; j < CPT; ++j) w[kk][j] = Wt[(size_t)(k0 + kk) * N + c0 + j * CS];
+}
+
+// Sequential-k product of a few rows with the thread's columns c0 + j * CS of
+// Wt [K][N] (t-layout). Weights stream from global memory 16 k-rows at a time
+// with the next 16 in flight while the current ones are used.
+template <int K, int N, int CPT, int CS, int RPT>
+__device__ inline void col_gemm(const float* __restrict__ Wt, const float* A, int lda, int row0, int c0,
+                                float (&acc)[CPT][RPT]) {
+  constexpr int KB = 16;
+  static_assert(K % (2 * KB) == 0, "k chunking");
+  float wa[KB][CPT], wb[KB][CPT];
+  load_rows<KB, N, CPT, CS>(wa, Wt, 0, c0);
+  for (int k0 = 0; k0 < K; k0 += 2 * KB) {
+    load_rows<KB, N, CPT, CS>(wb, Wt, k0 + KB, c0);
+    use_rows<KB, CPT, RPT>(wa, A, lda, row0, k0, acc);
+    if (k0 + 2 * KB < K) load_rows<KB, N, CPT, CS>(wa, Wt, k0 + 2 * KB, c0);
+    use_rows<KB, CPT, RPT>(wb, A, lda, row0, k0 + KB, acc);
+  }
+}
+
+// Node update for kNodeRows residues: LN1(h + upd), FFN, LN2, mask; then the
+// W11 prefix of this layer's edge update and (when Wnext_t is given) the next
+// layer's W1 prefix. Few rows per workgroup keep the grid wide; every thread
+// owns whole output columns, so each dot product runs over k in order.
 __global__ __launch_bounds__(256) void node_kernel(EncLayerDev w, const float* __restrict__ Wnext_t,
                                                    const float* __restrict__ msg_sum, const float* __restrict__ mask,
                                                    int L, float* __restrict__ h_v, float* __restrict__ prefix) {
 #pragma clang fp contract(off)
-  __shared__ __attribute__((aligned(16))) float A[kH * kLdN];
-  __shared__ __attribute__((aligned(16))) float X[kH * kLdN];
-  __shared__ __attribute__((aligned(16))) float F[kFF * kLdN];
-  __shared__ __attribute__((aligned(16))) float Wbuf[16 * kFF];
-  const int r0 = blockIdx.x * kNodeRows;
-  const int nr = min(kNodeRows, L - r0);
-  const int rg = threadIdx.x / 32, cg = threadIdx.x % 32;
-  const int row0 = rg * 4;
+  constexpr int NR = kNodeRows;
+  __shared__ __attribute__((aligned(16))) float X[kH * NR];   // k-major [d][row]
+  __shared__ __attribute__((aligned(16))) float H1[kH * NR];
+  __shared__ __attribute__((aligned(16))) float F[kFF * NR];
+  __shared__ __attribute__((aligned(16))) float H2[kH * NR];
+  const int r0 = blockIdx.x * NR;
+  const int nr = min(NR, L - r0);
+  const int t = threadIdx.x;
+  static_assert(NR == 4, "thread mapping");
 
   // X = h + upd (axpy order: 1 * residual + input)
-  for (int i = threadIdx.x; i < kNodeRows * kH; i += blockDim.x) {
-    const int row = i % kNodeRows, d = i / kNodeRows;
+  for (int i = t; i < NR * kH; i += blockDim.x) {
+    const int row = i % NR, d = i / NR;
     float v = 0.0F;
     if (row < nr) v = h_v[(size_t)(r0 + row) * kH + d] + msg_sum[(size_t)(r0 + row) * kH + d];
-    X[d * kLdN + row] = v;
+    X[d * NR + row] = v;
   }
   __syncthreads();
-  if (threadIdx.x < kNodeRows) welford_ln_col(X + threadIdx.x, A + threadIdx.x, kLdN, w.n1g, w.n1b);  // A = h1
+  if (t < NR) welford_ln_col(X + t, H1 + t, NR, w.n1g, w.n1b);
+  __syncthreads();
   {
-    float acc[4][16];
+    // W_in: columns t and t + 256 of all rows, then GELU
+    float acc[2][NR] = {};
+    col_gemm<kH, kFF, 2, 256, NR>(w.Win_t, H1, NR, 0, t, acc);
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
+    for (int j = 0; j < 2; ++j)
 #pragma unroll
-      for (int j = 0; j < 16; ++j) acc[i][j] = 0.0F;
-    seq_gemm<4, 16, kFF, 16>(acc, A, kLdN, row0, w.Win_t, kFF, kH, Wbuf, cg * 16);
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-#pragma unroll
-      for (int j = 0; j < 16; ++j) F[(cg * 16 + j) * kLdN + row0 + i] = gelu(acc[i][j] + w.bin[cg * 16 + j]);
+      for (int r = 0; r < NR; ++r) F[(t + 256 * j) * NR + r] = gelu(acc[j][r] + w.bin[t + 256 * j]);
   }
+  __syncthreads();
   {
-    float acc[4][4];
+    // W_out: column t % 128 of rows 2 (t / 128) + {0, 1}; X = h1 + (W_out f + b)
+    const int c = t % kH, rr = 2 * (t / kH);
+    float acc[1][2] = {};
+    col_gemm<kFF, kH, 1, 0, 2>(w.Wout_t, F, NR, rr, c, acc);
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
-#pragma unroll
-      for (int j = 0; j < 4; ++j) acc[i][j] = 0.0F;
-    seq_gemm<4, 4, kH, 16>(acc, F, kLdN, row0, w.Wout_t, kH, kFF, Wbuf, cg * 4);
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const int d = cg * 4 + j;
-        X[d * kLdN + row0 + i] = A[d * kLdN + row0 + i] + (acc[i][j] + w.bout[d]);
-      }
+    for (int r = 0; r < 2; ++r) X[c * NR + rr + r] = H1[c * NR + rr + r] + (acc[0][r] + w.bout[c]);
   }
   __syncthreads();
-  if (threadIdx.x < kNodeRows) {
-    const int row = threadIdx.x;
-    welford_ln_col(X + row, A + row, kLdN, w.n2g, w.n2b);
-    const float mk = row < nr ? mask[r0 + row] : 0.0F;
-    for (int d = 0; d < kH; ++d) A[d * kLdN + row] *= mk;
+  if (t < NR) {
+    welford_ln_col(X + t, H2 + t, NR, w.n2g, w.n2b);
+    const float mk = t < nr ? mask[r0 + t] : 0.0F;
+    for (int d = 0; d < kH; ++d) H2[d * NR + t] *= mk;
   }
   __syncthreads();
-  for (int i = threadIdx.x; i < nr * kH; i += blockDim.x) {
+  for (int i = t; i < nr * kH; i += blockDim.x) {
     const int row = i / kH, d = i % kH;
-    h_v[(size_t)(r0 + row) * kH + d] = A[d * kLdN + row];
+    h_v[(size_t)(r0 + row) * kH + d] = H2[d * NR + row];
   }
-  // prefixes: [0,128) of W11 and of the next layer's W1 over h'
-  for (int part = 0; part < 2; ++part) {
+  // prefixes: [0,128) of W11 (threads 0..127) and of the next layer's W1 (128..255) over h'
+  {
+    const int part = t / kH, c = t % kH;
     const float* Wt = part == 0 ? w.W11_t : Wnext_t;
-    if (!Wt) break;
-    float acc[4][4];
+    if (Wt) {
+      float acc[1][NR] = {};
+      col_gemm<kH, kH, 1, 0, NR>(Wt, H2, NR, 0, c, acc);
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
-#pragma unroll
-      for (int j = 0; j < 4; ++j) acc[i][j] = 0.0F;
-    seq_gemm<4, 4, kH, 16>(acc, A, kLdN, row0, Wt, kH, kH, Wbuf, cg * 4);
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-      if (row0 + i < nr)
-#pragma unroll
-        for (int j = 0; j < 4; ++j) prefix[(size_t)(r0 + row0 + i) * 256 + part * 128 + cg * 4 + j] = acc[i][j];
+      for (int r = 0; r < NR; ++r)
+        if (r < nr) prefix[(size_t)(r0 + r) * 256 + part * 128 + c] = acc[0][r];
+    }
   }
 }
 
