@@ -245,6 +245,26 @@ size_t pack_k16(HostArena& ar, const std::vector<const float*>& row_blocks, int 
   return off;
 }
 
+// fp16 split of W [N][kin] (N outputs, kin inputs) for the fp16 MFMA:
+// W = hi + lo / 2048 with hi = fp16(W) and lo = fp16((W - hi) * 2048), each
+// stored as [kin / 8][N][8] halves (two per float slot). Returns the offset of
+// hi; lo follows at hi + N * kin / 2.
+size_t pack_f16_split(HostArena& ar, const float* W, int N, int kin) {
+  const size_t half_slots = (size_t)N * kin / 2;
+  const size_t off = ar.add(2 * half_slots);
+  auto* hi = reinterpret_cast<_Float16*>(ar.data.data() + off);
+  auto* lo = reinterpret_cast<_Float16*>(ar.data.data() + off + half_slots);
+  for (int n = 0; n < N; ++n)
+    for (int k = 0; k < kin; ++k) {
+      const float w = W[(size_t)n * kin + k];
+      const _Float16 h = static_cast<_Float16>(w);
+      const size_t at = ((size_t)(k / 8) * N + n) * 8 + k % 8;
+      hi[at] = h;
+      lo[at] = static_cast<_Float16>((w - static_cast<float>(h)) * 2048.0F);
+    }
+  return off;
+}
+
 // Transposed: W [N][kin] columns [c0, c0 + kd) -> [kd][ldo] (first N columns used).
 size_t pack_t(HostArena& ar, const float* W, int N, int kin, int c0, int kd, int ldo) {
   const size_t off = ar.add((size_t)kd * ldo);
@@ -376,7 +396,7 @@ hkbs_status build_model(hkbs_pmpnn* ctx, const float* const* t) {
     size_t pos_w, pos_b, edge_t, ne_g, ne_b, We_t, We_b, Ws;
     size_t W1b_dec_p, W1d_dec_p, Wlog_t, blog;
     size_t enc[kLayers][22];
-    size_t dec[kLayers][20];
+    size_t dec[kLayers][22];
   } o{};
   o.pos_w = copy_raw(ar, t[0], 16 * 66);
   o.pos_b = copy_raw(ar, t[1], 16);
@@ -450,6 +470,7 @@ hkbs_status build_model(hkbs_pmpnn* ctx, const float* const* t) {
         }
       q[6] = copy_raw(ar, T.data(), T.size());
     }
+    q[20] = pack_f16_split(ar, d[2], 128, 128);       // W2 hi, lo (fp16)
     q[16] = pack_k16(ar, {d[4]}, 128, 128, 0, 128);   // W3_p
     q[17] = pack_k16(ar, {d[10]}, 512, 128, 0, 128);  // Win_p
     q[18] = pack_k16(ar, {d[12]}, 128, 512, 0, 512);  // Wout_p
@@ -519,6 +540,8 @@ hkbs_status build_model(hkbs_pmpnn* ctx, const float* const* t) {
     DecLayerDev& w = m.dec[l];
     w.W1a_t = B + q[0];
     w.W2_p = B + q[1];
+    w.W2h = B + q[20];
+    w.W2l = B + q[20] + 128 * 128 / 2;
     w.W3_t = B + q[2];
     w.Win_t = B + q[3];
     w.Wout_t = B + q[4];

@@ -32,6 +32,9 @@ namespace hkbs {
 namespace {
 
 constexpr int kLd = kH + 4;  // 132
+constexpr int kLdH = kH + 8;  // 136 halves: 16-byte rows that step 4 banks
+typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+typedef _Float16 half4 __attribute__((ext_vector_type(4)));
 constexpr int kThreads = 512;
 
 constexpr int kGroup = 4;  // residues decoded together when independent
@@ -103,45 +106,48 @@ __device__ inline void zero4(float4 (&acc)[kGroup]) {
   for (int i = 0; i < kGroup; ++i) acc[i] = make_float4(0.F, 0.F, 0.F, 0.F);
 }
 
-// One sampler draw on logits z (reference order, sampler_scalar.cpp:49-92);
-// state is the splitmix64 state before this draw. Writes log-probs to lp.
-__device__ inline int sample_token(const float* logits, float T, bool greedy, uint64_t state, float* lp) {
-  float z[kV], p[kV];
-  float row_max = -__builtin_inff();
-  for (int i = 0; i < kV; ++i) {
-    z[i] = logits[i] / T;
-    row_max = (row_max < z[i]) ? z[i] : row_max;
+// One sampler draw on a row of logits by one wave (reference operation order,
+// sampler_scalar.cpp:49-92); state is the splitmix64 state before this draw.
+// Lane v < kV computes token v's scaled logit, exponential and log-prob
+// (returned in *lp); the sum of exponentials and the double-precision CDF
+// walk run over the tokens in order, identically in every lane. Returns the
+// drawn token, the same in every lane.
+__device__ inline int sample_wave(const float* logits, float T, bool greedy, uint64_t state, float* lp) {
+  const int lane = threadIdx.x & 63;
+  const bool tok_lane = lane < kV;
+  const float z = tok_lane ? logits[lane] / T : -__builtin_inff();
+  float row_max = z;
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) {
+    const float o = __shfl_xor(row_max, off, 64);
+    row_max = (row_max < o) ? o : row_max;
   }
+  const float e = tok_lane ? expf(z - row_max) : 0.0F;
   float row_sum = 0.0F;
-  for (int i = 0; i < kV; ++i) {
-    const float e = expf(z[i] - row_max);
-    p[i] = e;
-    row_sum += e;
-  }
+#pragma unroll
+  for (int v = 0; v < kV; ++v) row_sum += __shfl(e, v, 64);
   const float log_sum = logf(row_sum);
   const float inv_sum = 1.0F / row_sum;
-  for (int i = 0; i < kV; ++i) lp[i] = (z[i] - row_max) - log_sum;
+  *lp = (z - row_max) - log_sum;
   if (greedy) {
-    int best = 0;
-    float bv = z[0];
-    for (int i = 1; i < kV; ++i)
-      if (z[i] > bv) {
-        best = i;
-        bv = z[i];
-      }
-    return best;
+    // first token holding the maximum (strict > scan)
+    const unsigned long long hits = __ballot(tok_lane && z == row_max);
+    return __ffsll(static_cast<long long>(hits)) - 1;
   }
   uint64_t zz = state + 0x9E3779B97F4A7C15ull;
   zz = (zz ^ (zz >> 30)) * 0xBF58476D1CE4E5B9ull;
   zz = (zz ^ (zz >> 27)) * 0x94D049BB133111EBull;
   zz ^= zz >> 31;
   const double u = static_cast<double>(zz >> 11) * (1.0 / 9007199254740992.0);
+  const float p = e * inv_sum;
   double cum = 0.0;
-  for (int i = 0; i < kV; ++i) {
-    cum += static_cast<double>(p[i] * inv_sum);
-    if (u < cum) return i;
+  int tok = kV - 1;
+#pragma unroll
+  for (int v = 0; v < kV; ++v) {
+    cum += static_cast<double>(__shfl(p, v, 64));
+    if (u < cum && tok == kV - 1 && v < kV - 1) tok = v;
   }
-  return kV - 1;
+  return tok;
 }
 
 // Relaxed device-scope accesses: written through to the level every CU of
@@ -191,7 +197,8 @@ __device__ inline bool team_sync(uint32_t* counter, uint32_t target, uint32_t* f
 // shares one XCD when workgroups are dealt round-robin over the 8 XCDs; the
 // launch is cooperative, so every team member is resident.
 __global__ __launch_bounds__(kThreads) void decode_kernel(ModelDev m, DecodeArgs a) {
-  __shared__ __attribute__((aligned(16))) float G[2 * kKmax * kLd];
+  // message rows of two members as fp16 pairs: [member][hi, lo][row][kLdH]
+  __shared__ __attribute__((aligned(16))) _Float16 G16[2 * 2 * kKmax * kLdH];
   __shared__ __attribute__((aligned(16))) float part[8192];
   __shared__ __attribute__((aligned(16))) float ff[kGroup * kFF];  // also [m][256] scratch
   __shared__ __attribute__((aligned(16))) float h[kGroup * kH];
@@ -309,10 +316,14 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(ModelDev m, DecodeArgs
         // W2 fragments of this wave's 16 columns stay in registers for all members.
         const int r = lane & 15, g = lane >> 4;
         const int col = wave * 16 + r;
-        float4 bw[kH / 16];
+        // B fragments of the 16x16x32 fp16 MFMA: column col, k = 32 kb + 8 g + 0..7
+        half8 bh[kH / 32], bl[kH / 32];
 #pragma unroll
-        for (int kb = 0; kb < kH / 16; ++kb)
-          bw[kb] = *reinterpret_cast<const float4*>(w.W2_p + ((size_t)kb * kH + col) * 16 + 4 * g);
+        for (int kb = 0; kb < kH / 32; ++kb) {
+          const size_t at = ((size_t)(4 * kb + g) * kH + col) * 4;  // float slots of 8 halves
+          bh[kb] = __builtin_bit_cast(half8, *reinterpret_cast<const float4*>(w.W2h + at));
+          bl[kb] = __builtin_bit_cast(half8, *reinterpret_cast<const float4*>(w.W2l + at));
+        }
         const float b2 = w.b2[col];
         for (int i0 = 0; i0 < ml; i0 += 2) {
           {
@@ -350,27 +361,49 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(ModelDev m, DecodeArgs
                 float4 v = make_float4(gelu_fast(xv.x, tbl), gelu_fast(xv.y, tbl), gelu_fast(xv.z, tbl),
                                        gelu_fast(xv.w, tbl));
                 if (k >= K) v = make_float4(0.F, 0.F, 0.F, 0.F);
-                *reinterpret_cast<float4*>(G + ((s / 3) * kKmax + k) * kLd + c) = v;
+                // split for the fp16 MFMA: v = hi + lo / 2048 to about 2^-22 relative
+                _Float16* gh = G16 + (((s / 3) * 2) * kKmax + k) * kLdH + c;
+                _Float16* gl = gh + kKmax * kLdH;
+                const float vv[4] = {v.x, v.y, v.z, v.w};
+                half4 hv, lv;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                  const float cl = __builtin_amdgcn_fmed3f(vv[e], -65504.0F, 65504.0F);
+                  hv[e] = static_cast<_Float16>(cl);
+                  lv[e] = static_cast<_Float16>((vv[e] - static_cast<float>(hv[e])) * 2048.0F);
+                }
+                *reinterpret_cast<half4*>(gh) = hv;
+                *reinterpret_cast<half4*>(gl) = lv;
               }
             }
           }
           __syncthreads();
           for (int i = i0; i < ml && i < i0 + 2; ++i) {
-            const float* Gi = G + (i - i0) * kKmax * kLd;
-            floatx4 acc[3];
+            const _Float16* Gh = G16 + (i - i0) * 2 * kKmax * kLdH;
+            const _Float16* Gl = Gh + kKmax * kLdH;
+            // W2 product as hi.hi + (hi.lo + lo.hi) / 2048 on the fp16 MFMA
+            floatx4 acc[3], cor[3];
 #pragma unroll
-            for (int mb = 0; mb < 3; ++mb) acc[mb] = floatx4{0.F, 0.F, 0.F, 0.F};
+            for (int mb = 0; mb < 3; ++mb) {
+              acc[mb] = floatx4{0.F, 0.F, 0.F, 0.F};
+              cor[mb] = acc[mb];
+            }
 #pragma unroll
-            for (int kb = 0; kb < kH / 16; ++kb) {
+            for (int kb = 0; kb < kH / 32; ++kb) {
 #pragma unroll
               for (int mb = 0; mb < 3; ++mb) {
-                const float4 av = *reinterpret_cast<const float4*>(Gi + (mb * 16 + r) * kLd + kb * 16 + 4 * g);
-                acc[mb] = mfma16(av.x, bw[kb].x, acc[mb]);
-                acc[mb] = mfma16(av.y, bw[kb].y, acc[mb]);
-                acc[mb] = mfma16(av.z, bw[kb].z, acc[mb]);
-                acc[mb] = mfma16(av.w, bw[kb].w, acc[mb]);
+                const int at = (mb * 16 + r) * kLdH + 32 * kb + 8 * g;
+                const half8 ah = *reinterpret_cast<const half8*>(Gh + at);
+                const half8 al = *reinterpret_cast<const half8*>(Gl + at);
+                acc[mb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, bh[kb], acc[mb], 0, 0, 0);
+                cor[mb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, bl[kb], cor[mb], 0, 0, 0);
+                cor[mb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al, bh[kb], cor[mb], 0, 0, 0);
               }
             }
+#pragma unroll
+            for (int mb = 0; mb < 3; ++mb)
+#pragma unroll
+              for (int e = 0; e < 4; ++e) acc[mb][e] += cor[mb][e] * (1.0F / 2048.0F);
             // x[i][col] = sum over the member's K rows of GELU(acc + b2)
             float sum = 0.0F;
 #pragma unroll
@@ -478,21 +511,21 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(ModelDev m, DecodeArgs
         logits[task] = GLog::sum(part, i, o) + m.blog[o];
       }
       __syncthreads();
-      if (threadIdx.x < ml) {
-        const int i = threadIdx.x;
+      if (wave < ml) {  // wave i draws member i
+        const int i = wave;
         const int t = tres[i];
         const int gi = rank + P * i;
-        float lpv[kV];
-        const int s_tok = sample_token(logits + i * 32, T, greedy, rng + (uint64_t)gi * 0x9E3779B97F4A7C15ull, lpv);
+        float lpv;
+        const int s_tok = sample_wave(logits + i * 32, T, greedy, rng + (uint64_t)gi * 0x9E3779B97F4A7C15ull, &lpv);
         const float design = (a.chain_mask ? a.chain_mask[t] : 1.0F) * a.mask[t];
         int tok = s_tok;
         if (design == 0.0F)
           tok = (a.true_tokens && a.true_tokens[t] >= 0 && a.true_tokens[t] < kV) ? a.true_tokens[t] : kV - 1;
-        tokens[t] = tok;
-        tok_s[i] = tok;
-        for (int v = 0; v < kV; ++v) {
-          if (lp_out) lp_out[(size_t)t * kV + v] = lpv[v];
-          if (v == tok) store_dev(chosen + t, lpv[v]);
+        if (lp_out && lane < kV) lp_out[(size_t)t * kV + lane] = lpv;
+        if (lane == tok) store_dev(chosen + t, lpv);
+        if (lane == 0) {
+          tokens[t] = tok;
+          tok_s[i] = tok;
         }
       }
       __syncthreads();

@@ -41,6 +41,8 @@ struct EncLayerDev {
 struct DecLayerDev {
   const float* W1a_t;  // [128][128]
   const float* W2_p;   // kpack16 128 -> 128
+  const float* W2h;    // [16][128][8] fp16: W2 = W2h + W2l / 2048 (decode loop)
+  const float* W2l;
   const float* W3_t;   // [128][128]
   const float* Win_t;  // [128][512]
   const float* Wout_t; // [512][128]
