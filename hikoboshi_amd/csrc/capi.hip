@@ -375,6 +375,7 @@ struct hkbs_pmpnn {
   bool timed = false;  // events hold a recorded design call
   hipEvent_t ev[4] = {nullptr, nullptr, nullptr, nullptr};
   uint32_t* fault = nullptr;  // device word raised by the last decode if a team barrier timed out
+  DecodeArgs last_decode{};   // arguments of the last decode launch (for a one-workgroup rerun)
 };
 
 namespace {
@@ -577,13 +578,14 @@ struct EncodeBuffers {
   float* h_v;
   float* h_e;
   EncoderScratch scratch;
+  float* msg_sum;  // [L][128] teacher-forced message sums
 };
 
 size_t encode_bytes(int L, int K) {
   const size_t S = (size_t)L * K;
   return aligned_bytes<float>(L) + aligned_bytes<float4>(L) + aligned_bytes<int32_t>(S) + aligned_bytes<float>(S) +
          aligned_bytes<float>((size_t)L * kH) + aligned_bytes<float>(S * kH) + aligned_bytes<float>((size_t)L * 256) +
-         aligned_bytes<float>((size_t)L * kH);
+         aligned_bytes<float>(S * kH) + aligned_bytes<float>((size_t)L * kH);
 }
 
 EncodeBuffers take_encode(DeviceArena& ar, int L, int K) {
@@ -596,7 +598,8 @@ EncodeBuffers take_encode(DeviceArena& ar, int L, int K) {
   e.h_v = ar.take<float>((size_t)L * kH);
   e.h_e = ar.take<float>(S * kH);
   e.scratch.prefix = ar.take<float>((size_t)L * 256);
-  e.scratch.msg_sum = ar.take<float>((size_t)L * kH);
+  e.scratch.msg = ar.take<float>(S * kH);
+  e.msg_sum = ar.take<float>((size_t)L * kH);
   return e;
 }
 
@@ -712,6 +715,7 @@ hkbs_status design_on_device(hkbs_pmpnn* ctx, const float* coords, const uint8_t
   a.chosen_lp = chosen;
   a.sync = sync;
   a.fault = sync + B;
+  ctx->last_decode = a;
   HK_CHECK(launch_decode(ctx->model, a, ctx->stream), "decode launch failed");
   if (ctx->timing) {
     HK_CHECK(hipEventRecord(ctx->ev[3], ctx->stream), "event record failed");
@@ -884,7 +888,15 @@ hkbs_status hkbs_pmpnn_design(hkbs_pmpnn* ctx, const float* coords, const uint8_
   uint32_t fault = 0;
   HK_CHECK(hipMemcpyAsync(&fault, ctx->fault, sizeof(fault), hipMemcpyDeviceToHost, s), "D2H failed");
   HK_CHECK(hipStreamSynchronize(s), "design kernels failed");
-  if (fault) return fail(HKBS_INTERNAL_ERROR, "decode team barrier timed out");
+  if (fault) {
+    // A team of workgroups could not run together (the device was busy with
+    // other work): decode again with one workgroup per sequence.
+    HK_CHECK(launch_decode(ctx->model, ctx->last_decode, s, 1), "decode launch failed");
+    HK_CHECK(hipMemcpyAsync(tokens, d_tokens, (size_t)B * L * 4, hipMemcpyDeviceToHost, s), "D2H failed");
+    if (log_probs) HK_CHECK(hipMemcpyAsync(log_probs, d_lp, (size_t)B * L * kV * 4, hipMemcpyDeviceToHost, s), "D2H failed");
+    if (scores) HK_CHECK(hipMemcpyAsync(scores, d_scores, (size_t)B * 4, hipMemcpyDeviceToHost, s), "D2H failed");
+    HK_CHECK(hipStreamSynchronize(s), "design kernels failed");
+  }
   if (orders_out) {
     for (int b = 0; b < B; ++b)
       std::memcpy(orders_out + (size_t)b * L, host_orders.data() + (shared ? 0 : (size_t)b * L), (size_t)L * 4);
@@ -974,7 +986,7 @@ hkbs_status teacher_forced_chunk(hkbs_pmpnn* ctx, const float* coords, const uin
   a.Q = Q;
   a.h = e.h_v;
   a.NB = NB;
-  a.msg_sum = e.scratch.msg_sum;
+  a.msg_sum = e.msg_sum;
   a.log_probs = log_probs;
   a.L = L;
   a.K = K;

@@ -24,6 +24,7 @@
 // Consecutive independent residues are decoded together (see decode_kernel).
 #include <algorithm>
 #include <cstdlib>
+#include <cstring>
 
 #include "device_math.hpp"
 #include "pmpnn_internal.hpp"
@@ -34,6 +35,11 @@ namespace {
 constexpr int kLd = kH + 4;  // 132
 constexpr int kLdH = kH + 8;  // 136 halves: 16-byte rows that step 4 banks
 typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+// Per-layer vectors kept in LDS for the whole kernel: [b1 b2 b3 bin bout n1g n1b n2g n2b]
+constexpr int kPrmB1 = 0, kPrmB2 = 128, kPrmB3 = 256, kPrmBin = 384, kPrmBout = 896, kPrmN1g = 1024,
+              kPrmN1b = 1152, kPrmN2g = 1280, kPrmN2b = 1408, kPrmLayer = 1536;
+constexpr int kPrmLog = kLayers * kPrmLayer;  // logits bias (32)
+constexpr int kPrmSize = kPrmLog + 32;
 typedef _Float16 half4 __attribute__((ext_vector_type(4)));
 constexpr int kThreads = 512;
 
@@ -116,16 +122,11 @@ __device__ inline int sample_wave(const float* logits, float T, bool greedy, uin
   const int lane = threadIdx.x & 63;
   const bool tok_lane = lane < kV;
   const float z = tok_lane ? logits[lane] / T : -__builtin_inff();
-  float row_max = z;
-#pragma unroll
-  for (int off = 32; off > 0; off >>= 1) {
-    const float o = __shfl_xor(row_max, off, 64);
-    row_max = (row_max < o) ? o : row_max;
-  }
+  const float row_max = wave_max(z);
   const float e = tok_lane ? expf(z - row_max) : 0.0F;
   float row_sum = 0.0F;
 #pragma unroll
-  for (int v = 0; v < kV; ++v) row_sum += __shfl(e, v, 64);
+  for (int v = 0; v < kV; ++v) row_sum += lane_f32(e, v);
   const float log_sum = logf(row_sum);
   const float inv_sum = 1.0F / row_sum;
   *lp = (z - row_max) - log_sum;
@@ -144,7 +145,7 @@ __device__ inline int sample_wave(const float* logits, float T, bool greedy, uin
   int tok = kV - 1;
 #pragma unroll
   for (int v = 0; v < kV; ++v) {
-    cum += static_cast<double>(__shfl(p, v, 64));
+    cum += static_cast<double>(lane_f32(p, v));
     if (u < cum && tok == kV - 1 && v < kV - 1) tok = v;
   }
   return tok;
@@ -157,13 +158,13 @@ __device__ inline float load_dev(const float* p) {
   return __hip_atomic_load(const_cast<float*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-constexpr uint32_t kSpinLimit = 1u << 20;  // polls (~1 s) before a team gives up
+constexpr uint32_t kSpinLimit = 1u << 20;  // default polls (~1 s) before a team gives up
 
 // Barrier over the P workgroups of a team. Every wave first waits for its own
 // stores; thread 0 then counts the workgroup in and polls until all P have
 // arrived `target / P` times. Returns false (and raises the fault word) if the
 // wait does not end; the caller then stops so that every wave exits.
-__device__ inline bool team_sync(uint32_t* counter, uint32_t target, uint32_t* fault, int* bad) {
+__device__ inline bool team_sync(uint32_t* counter, uint32_t target, uint32_t spin_limit, uint32_t* fault, int* bad) {
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
   if (threadIdx.x == 0) {
@@ -171,7 +172,7 @@ __device__ inline bool team_sync(uint32_t* counter, uint32_t target, uint32_t* f
     uint32_t n = 0;
     while (__hip_atomic_load(counter, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < target) {
       __builtin_amdgcn_s_sleep(1);
-      if (++n == kSpinLimit) {
+      if (++n >= spin_limit) {
         *bad = 1;
         __hip_atomic_store(fault, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         break;
@@ -207,6 +208,7 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(ModelDev m, DecodeArgs
   __shared__ __attribute__((aligned(16))) float h1[kGroup * kH];
   __shared__ __attribute__((aligned(16))) float Pd[kGroup * 2 * kH];  // W1d h^l of layers 1, 2
   __shared__ float logits[kGroup * 32];
+  __shared__ __attribute__((aligned(16))) float prm[kPrmSize];
   __shared__ float tbl[17];
   __shared__ int nbr[kGroup * kKmax];
   __shared__ int bwf[kGroup * kKmax];
@@ -240,6 +242,22 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(ModelDev m, DecodeArgs
   const bool greedy = a.greedy || a.temperature <= 0.0F;
   if (threadIdx.x < 17) tbl[threadIdx.x] = kExpNegTable[threadIdx.x];
   if (threadIdx.x == 0) bad = 0;
+  for (int l = 0; l < kLayers; ++l) {
+    const DecLayerDev& w = m.dec[l];
+    float* p = prm + l * kPrmLayer;
+    for (int i = threadIdx.x; i < kH; i += kThreads) {
+      p[kPrmB1 + i] = w.b1[i];
+      p[kPrmB2 + i] = w.b2[i];
+      p[kPrmB3 + i] = w.b3[i];
+      p[kPrmBout + i] = w.bout[i];
+      p[kPrmN1g + i] = w.n1g[i];
+      p[kPrmN1b + i] = w.n1b[i];
+      p[kPrmN2g + i] = w.n2g[i];
+      p[kPrmN2b + i] = w.n2b[i];
+    }
+    for (int i = threadIdx.x; i < kFF; i += kThreads) p[kPrmBin + i] = w.bin[i];
+  }
+  if (threadIdx.x < 32) prm[kPrmLog + threadIdx.x] = m.blog[threadIdx.x];
   __syncthreads();
 
   int step = 0;
@@ -266,7 +284,7 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(ModelDev m, DecodeArgs
         }
       }
       ++step;
-      if (P > 1 && !team_sync(counter, ++passes * P, a.fault, &bad)) break;
+      if (P > 1 && !team_sync(counter, ++passes * P, a.spin_limit, a.fault, &bad)) break;
       __syncthreads();
       continue;
     }
@@ -305,7 +323,7 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(ModelDev m, DecodeArgs
         const int t = order[step + rank + P * i];
         h[i * kH + c] = a.h_v[(size_t)t * kH + c];
         // layer-0 W1a h^0_t comes from the precompute (Q block 3)
-        hA[i * kH + c] = a.Q[((size_t)3 * L + t) * kH + c] + m.dec[0].b1[c];
+        hA[i * kH + c] = a.Q[((size_t)3 * L + t) * kH + c] + prm[kPrmB1 + c];
       }
       __syncthreads();
 
@@ -324,7 +342,8 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(ModelDev m, DecodeArgs
           bh[kb] = __builtin_bit_cast(half8, *reinterpret_cast<const float4*>(w.W2h + at));
           bl[kb] = __builtin_bit_cast(half8, *reinterpret_cast<const float4*>(w.W2l + at));
         }
-        const float b2 = w.b2[col];
+        const float* pl = prm + l * kPrmLayer;
+        const float b2 = pl[kPrmB2 + col];
         for (int i0 = 0; i0 < ml; i0 += 2) {
           {
             // Message rows g1 = GELU(A + E1_tk + (bw ? R : Q)_j) of members i0, i0 + 1;
@@ -435,9 +454,9 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(ModelDev m, DecodeArgs
 #pragma unroll
           for (int hh = 0; hh < 2; ++hh) {
             const int c = lane + 64 * hh;
-            v[hh] = h[wave * kH + c] + (G3::sum(part, wave, c) + static_cast<float>(K) * w.b3[c]) * (1.0F / 30.0F);
+            v[hh] = h[wave * kH + c] + (G3::sum(part, wave, c) + static_cast<float>(K) * pl[kPrmB3 + c]) * (1.0F / 30.0F);
           }
-          ln_regs_wave(v[0], v[1], w.n1g, w.n1b, h1 + wave * kH);
+          ln_regs_wave(v[0], v[1], pl + kPrmN1g, pl + kPrmN1b, h1 + wave * kH);
         }
         __syncthreads();
         // f = GELU(W_in h1 + b)
@@ -454,7 +473,7 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(ModelDev m, DecodeArgs
         __syncthreads();
         for (int task = threadIdx.x; task < ml * kFF; task += kThreads) {
           const int i = task / kFF, o = task % kFF;
-          ff[task] = gelu_fast(GIn::sum(part, i, o) + w.bin[o], tbl);
+          ff[task] = gelu_fast(GIn::sum(part, i, o) + pl[kPrmBin + o], tbl);
         }
         __syncthreads();
         // h^{l+1} = LN2(h1 + (W_out f + b)) (the mask gate is 1 for an active residue)
@@ -476,9 +495,9 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(ModelDev m, DecodeArgs
 #pragma unroll
           for (int hh = 0; hh < 2; ++hh) {
             const int c = lane + 64 * hh;
-            v[hh] = h1[wave * kH + c] + (GOut::sum(part, wave, c) + w.bout[c]);
+            v[hh] = h1[wave * kH + c] + (GOut::sum(part, wave, c) + pl[kPrmBout + c]);
           }
-          ln_regs_wave(v[0], v[1], w.n2g, w.n2b, h + wave * kH);
+          ln_regs_wave(v[0], v[1], pl + kPrmN2g, pl + kPrmN2b, h + wave * kH);
         }
         __syncthreads();
         if (l + 1 < kLayers) {
@@ -491,7 +510,7 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(ModelDev m, DecodeArgs
           for (int task = threadIdx.x; task < ml * kH; task += kThreads) {
             const int i = task / kH, c = task % kH;
             Pd[(i * 2 + l) * kH + c] = GDa::sum(part, i, c);
-            hA[task] = GDa::sum(part, i, kH + c) + m.dec[l + 1].b1[c];
+            hA[task] = GDa::sum(part, i, kH + c) + pl[kPrmLayer + kPrmB1 + c];
           }
           __syncthreads();
         }
@@ -508,7 +527,7 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(ModelDev m, DecodeArgs
       __syncthreads();
       for (int task = threadIdx.x; task < ml * 32; task += kThreads) {
         const int i = task / 32, o = task % 32;
-        logits[task] = GLog::sum(part, i, o) + m.blog[o];
+        logits[task] = GLog::sum(part, i, o) + prm[kPrmLog + o];
       }
       __syncthreads();
       if (wave < ml) {  // wave i draws member i
@@ -538,7 +557,7 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(ModelDev m, DecodeArgs
     }
     if (!greedy) rng += (uint64_t)mg * 0x9E3779B97F4A7C15ull;
     step += mg;
-    if (P > 1 && !team_sync(counter, ++passes * P, a.fault, &bad)) break;
+    if (P > 1 && !team_sync(counter, ++passes * P, a.spin_limit, a.fault, &bad)) break;
     __syncthreads();
   }
   // Mean NLL over designed residues in residue order (inverse_fold_scalar.cpp:471-493).
@@ -636,29 +655,41 @@ hipError_t launch_q_precompute(const ModelDev& m, const float* h_v, int L, float
   return hipGetLastError();
 }
 
-hipError_t launch_decode(const ModelDev& m, const DecodeArgs& args, hipStream_t stream) {
+hipError_t launch_decode(const ModelDev& m, const DecodeArgs& args, hipStream_t stream, int max_team) {
   if (args.L <= 0 || args.B <= 0) return hipSuccess;
   DecodeArgs a = args;
   ModelDev mm = m;
-  int dev = 0, cus = 0, coop = 0, per_cu = 0;
+  int dev = 0, cus = 0, per_cu = 0;
   hipError_t e = hipGetDevice(&dev);
   if (e == hipSuccess) e = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
-  if (e == hipSuccess) e = hipDeviceGetAttribute(&coop, hipDeviceAttributeCooperativeLaunch, dev);
   if (e == hipSuccess) e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, decode_kernel, kThreads, 0);
   if (e != hipSuccess) return e;
   const long resident = (long)cus * per_cu;
   const long teams_per_xcd = (a.B + 7) / 8;
-  int P = 4;
-  if (const char* env = std::getenv("HKBS_DECODE_TEAM")) P = std::max(1, std::min(4, std::atoi(env)));
+  int P = std::max(1, std::min(4, max_team));
+  if (const char* env = std::getenv("HKBS_DECODE_TEAM")) P = std::max(1, std::min(P, std::atoi(env)));
   while (P > 1 && 8 * teams_per_xcd * P > resident) --P;
-  if (!coop || !a.sync || !a.fault) P = 1;
+  if (!a.sync || !a.fault) P = 1;
+  a.spin_limit = kSpinLimit;
+  if (const char* env = std::getenv("HKBS_DECODE_SPIN_LIMIT")) a.spin_limit = (uint32_t)std::max(1, std::atoi(env));
   if (P > 1) {
     a.team = P;
-    void* kargs[] = {&mm, &a};
-    e = hipLaunchCooperativeKernel(reinterpret_cast<const void*>(&decode_kernel),
-                                   dim3((unsigned)(8 * teams_per_xcd * P)), dim3(kThreads), kargs, 0, stream);
-    if (e == hipSuccess) return hipSuccess;
-    (void)hipGetLastError();  // not launchable as a team here: one workgroup per sequence
+    const dim3 grid((unsigned)(8 * teams_per_xcd * P));
+    const char* mode = std::getenv("HKBS_DECODE_LAUNCH");
+    if (mode && std::strcmp(mode, "cooperative") == 0) {
+      void* kargs[] = {&mm, &a};
+      e = hipLaunchCooperativeKernel(reinterpret_cast<const void*>(&decode_kernel), grid, dim3(kThreads), kargs, 0,
+                                     stream);
+      if (e == hipSuccess) return hipSuccess;
+      (void)hipGetLastError();  // not launchable as a team here: one workgroup per sequence
+    } else {
+      // The whole grid fits the device at once (one workgroup per CU at most),
+      // so on a device running nothing else every team is resident. Every
+      // team barrier wait is bounded: a member that is not resident ends the
+      // wait with the fault word raised instead of hanging.
+      decode_kernel<<<grid, kThreads, 0, stream>>>(mm, a);
+      return hipGetLastError();
+    }
   }
   a.team = 1;
   decode_kernel<<<a.B, kThreads, 0, stream>>>(mm, a);

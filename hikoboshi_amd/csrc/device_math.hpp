@@ -169,24 +169,50 @@ __device__ inline void store_acc(const floatx4 (&acc)[MB][NB], float* C, int ldc
 // block of outputs and walks k in order; parallelism comes from the outputs.
 //   A   : LDS, k-major: A[k * lda + row].
 //   W   : global, transposed weights W[k * ldw + col] (col < NC).
-//   Wbuf: LDS staging for KC x NC floats.
+//   Wbuf: LDS staging, 2 x KC x NC floats: chunk c + 1 of the weights is
+//         loaded into registers while chunk c is used, then stored to the
+//         other half.
 // The thread's block is rows [r0, r0 + RM), cols [c0, c0 + CN). Every thread
-// of the block must call it (it contains barriers); it starts with a barrier,
-// so LDS writes made before the call are visible.
+// of the 256-thread block must call it (it contains barriers); it starts and
+// ends with a barrier, so LDS writes made before the call are visible and A
+// may be overwritten after it.
 template <int RM, int CN, int NC, int KC>
 __device__ inline void seq_gemm(float (&acc)[RM][CN], const float* A, int lda, int r0,
                                 const float* __restrict__ W, int ldw, int kd, float* Wbuf, int c0) {
 #pragma clang fp contract(off)
-  for (int k0 = 0; k0 < kd; k0 += KC) {
-    __syncthreads();
-    for (int i = threadIdx.x; i < KC * (NC / 4); i += blockDim.x) {
-      const int kk = i / (NC / 4);
-      const int c4 = i % (NC / 4);
-      float4 v = make_float4(0.F, 0.F, 0.F, 0.F);
-      if (k0 + kk < kd) v = *reinterpret_cast<const float4*>(W + (size_t)(k0 + kk) * ldw + 4 * c4);
-      *reinterpret_cast<float4*>(Wbuf + kk * NC + 4 * c4) = v;
+  constexpr int kBlock = 256;
+  constexpr int V = KC * (NC / 4);  // float4 per chunk
+  constexpr int PT = (V + kBlock - 1) / kBlock;
+  float4 stage[PT];
+  const int nchunks = (kd + KC - 1) / KC;
+#pragma unroll
+  for (int p = 0; p < PT; ++p) {
+    const int i = threadIdx.x + p * kBlock;
+    const int kk = i / (NC / 4), c4 = i % (NC / 4);
+    stage[p] = make_float4(0.F, 0.F, 0.F, 0.F);
+    if (i < V && kk < kd) stage[p] = *reinterpret_cast<const float4*>(W + (size_t)kk * ldw + 4 * c4);
+  }
+  __syncthreads();
+#pragma unroll
+  for (int p = 0; p < PT; ++p) {
+    const int i = threadIdx.x + p * kBlock;
+    if (i < V) *reinterpret_cast<float4*>(Wbuf + i * 4) = stage[p];
+  }
+  __syncthreads();
+  for (int c = 0; c < nchunks; ++c) {
+    const int k0 = c * KC;
+    const bool more = c + 1 < nchunks;
+    if (more) {
+#pragma unroll
+      for (int p = 0; p < PT; ++p) {
+        const int i = threadIdx.x + p * kBlock;
+        const int kk = i / (NC / 4), c4 = i % (NC / 4);
+        stage[p] = make_float4(0.F, 0.F, 0.F, 0.F);
+        if (i < V && k0 + KC + kk < kd)
+          stage[p] = *reinterpret_cast<const float4*>(W + (size_t)(k0 + KC + kk) * ldw + 4 * c4);
+      }
     }
-    __syncthreads();
+    const float* Wc = Wbuf + (c & 1) * (KC * NC);
     const int kn = (kd - k0) < KC ? (kd - k0) : KC;
     for (int kk = 0; kk < kn; ++kk) {
       float a[RM];
@@ -205,7 +231,7 @@ __device__ inline void seq_gemm(float (&acc)[RM][CN], const float* A, int lda, i
           a[i] = v.x; a[i + 1] = v.y;
         }
       }
-      const float* wp = Wbuf + kk * NC + c0;
+      const float* wp = Wc + kk * NC + c0;
 #pragma unroll
       for (int j = 0; j < CN; j += 4) {
         const float4 v = *reinterpret_cast<const float4*>(wp + j);
@@ -216,6 +242,15 @@ __device__ inline void seq_gemm(float (&acc)[RM][CN], const float* A, int lda, i
 #pragma unroll
         for (int j = 0; j < CN; ++j) acc[i][j] = acc[i][j] + a[i] * w[j];
     }
+    if (more) {
+      float* Wn = Wbuf + ((c + 1) & 1) * (KC * NC);
+#pragma unroll
+      for (int p = 0; p < PT; ++p) {
+        const int i = threadIdx.x + p * kBlock;
+        if (i < V) *reinterpret_cast<float4*>(Wn + i * 4) = stage[p];
+      }
+    }
+    __syncthreads();
   }
 }
 
@@ -245,10 +280,36 @@ __device__ inline void welford_ln_col(const float* x, float* out, int ld, const 
 // Two-pass LayerNorm statistics of a 128-float row held as 2 floats per lane
 // of one wave (lane holds elements lane and lane + 64). eps = 1e-5
 // (cpp/include/hikoboshi/universal/detail/mpnn_d64_weights.hpp:27).
+// Lane permutations within a row of 16 lanes on the DPP path (no LDS trip):
+// 0xB1 = quad_perm [1,0,3,2], 0x4E = quad_perm [2,3,0,1], 0x141 =
+// row_half_mirror, 0x140 = row_mirror.
+template <int CTRL>
+__device__ inline float dpp_f32(float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
+}
+
+__device__ inline float lane_f32(float v, int lane) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), lane));
+}
+
+// Sum over the 64 lanes of a wave as a pairwise tree (lanes 2i and 2i + 1,
+// then quads, 8s, rows of 16, then the four row sums as (r0 + r1) + (r2 +
+// r3)); every lane gets the same bits.
 __device__ inline float wave_sum(float v) {
-#pragma unroll
-  for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
-  return v;
+  v += dpp_f32<0xB1>(v);
+  v += dpp_f32<0x4E>(v);
+  v += dpp_f32<0x141>(v);  // after the quads, mirroring within 8 lanes pairs quad 0 with quad 1
+  v += dpp_f32<0x140>(v);  // and mirroring within 16 lanes pairs the two halves
+  return (lane_f32(v, 0) + lane_f32(v, 16)) + (lane_f32(v, 32) + lane_f32(v, 48));
+}
+
+// Maximum over the 64 lanes of a wave (order does not matter for max).
+__device__ inline float wave_max(float v) {
+  v = fmaxf(v, dpp_f32<0xB1>(v));
+  v = fmaxf(v, dpp_f32<0x4E>(v));
+  v = fmaxf(v, dpp_f32<0x141>(v));
+  v = fmaxf(v, dpp_f32<0x140>(v));
+  return fmaxf(fmaxf(lane_f32(v, 0), lane_f32(v, 16)), fmaxf(lane_f32(v, 32), lane_f32(v, 48)));
 }
 
 // LayerNorm of a row held in registers (lane: elements lane and lane + 64).

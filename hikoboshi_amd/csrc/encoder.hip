@@ -17,20 +17,22 @@
 // kernels continue the sum with the e_ij and h_j terms.
 //
 // Kernels per layer:
-//   edge_msg_kernel    tile of whole residues (<= 96 edge rows): W1 (e, h_j
-//                      terms), W2, W3, then the masked neighbour sum.
-//   node_kernel        tile of 4 residues: LN1, FFN, LN2, mask, and the W11
-//                      and next-layer W1 prefixes.
-//   edge_update_kernel tile of whole residues: W11, W12, W13, residual, LN3.
+//   edge_msg_kernel    tile of 32 edge rows: W1 (e, h_j terms), W2, W3 -> m_ij.
+//   node_kernel        tile of 4 residues: the masked neighbour sum of m_ij in
+//                      slot order, LN1, FFN, LN2, mask, and the W11 and
+//                      next-layer W1 prefixes.
+//   edge_update_kernel tile of 32 edge rows: W11, W12, W13, residual, LN3.
+// Small tiles keep several workgroups on every CU; the weights stream through
+// LDS in double-buffered chunks.
 #include "device_math.hpp"
 #include "pmpnn_internal.hpp"
 
 namespace hkbs {
 namespace {
 
-constexpr int kRows = 96;    // edge rows per tile
-constexpr int kLdE = 98;     // k-major leading dimension of edge tiles
-constexpr int kEdgeRM = 6;   // rows per thread (16 row groups)
+constexpr int kRows = 32;    // edge rows per tile (any rows of the [L * K] edge list)
+constexpr int kLdE = 36;     // k-major leading dimension of edge tiles
+constexpr int kEdgeRM = 2;   // rows per thread (16 row groups)
 constexpr int kEdgeCN = 8;   // cols per thread (16 col groups)
 constexpr int kKC = 32;      // weight rows staged per chunk
 constexpr int kNodeRows = 4;
@@ -52,20 +54,19 @@ __device__ inline void load_kmajor(float* A, int lda, int n_tile_rows, RowFn row
   }
 }
 
-// Message pass: msg_sum[i] = sum over valid slots (in order) of (1/30) mask_attend m_ij.
+// Edge messages m_ij = W3 GELU(W2 GELU(W1 [h_i, e_ij, h_j] + b1) + b2) + b3 for
+// a tile of kRows consecutive edge rows; the neighbour sum is taken in order
+// by node_kernel.
 __global__ __launch_bounds__(256) void edge_msg_kernel(EncLayerDev w, const float* __restrict__ h_e,
                                                        const float* __restrict__ h_v, const int32_t* __restrict__ idx,
-                                                       const float* __restrict__ mask,
                                                        const float* __restrict__ prefix, int L, int K,
-                                                       float* __restrict__ msg_sum) {
+                                                       float* __restrict__ msg) {
 #pragma clang fp contract(off)
   __shared__ __attribute__((aligned(16))) float A[kH * kLdE];
-  __shared__ __attribute__((aligned(16))) float Wbuf[kKC * kH];
-  const int nres = kRows / K;
-  const int r0 = blockIdx.x * nres;
-  const int nr = min(nres, L - r0);
-  const int n_rows = nr * K;
-  const size_t slot0 = (size_t)r0 * K;
+  __shared__ __attribute__((aligned(16))) float Wbuf[2 * kKC * kH];
+  const size_t S = (size_t)L * K;
+  const size_t slot0 = (size_t)blockIdx.x * kRows;
+  const int n_rows = (int)min((size_t)kRows, S - slot0);
   const int rg = threadIdx.x / 16, cg = threadIdx.x % 16;
   const int row0 = rg * kEdgeRM, col0 = cg * kEdgeCN;
 
@@ -73,7 +74,7 @@ __global__ __launch_bounds__(256) void edge_msg_kernel(EncLayerDev w, const floa
 #pragma unroll
   for (int i = 0; i < kEdgeRM; ++i) {
     const int row = row0 + i;
-    const float* pre = row < n_rows ? prefix + (size_t)(r0 + row / K) * 256 + 128 : nullptr;
+    const float* pre = row < n_rows ? prefix + ((slot0 + row) / K) * 256 + 128 : nullptr;
 #pragma unroll
     for (int j = 0; j < kEdgeCN; ++j) acc[i][j] = pre ? pre[col0 + j] : 0.0F;
   }
@@ -81,14 +82,12 @@ __global__ __launch_bounds__(256) void edge_msg_kernel(EncLayerDev w, const floa
     return row < n_rows ? h_e + (slot0 + row) * kH : nullptr;
   });
   seq_gemm<kEdgeRM, kEdgeCN, kH, kKC>(acc, A, kLdE, row0, w.W1_t + 128 * kH, kH, kH, Wbuf, col0);
-  __syncthreads();
   load_kmajor(A, kLdE, kRows, [&](int row) -> const float* {
     if (row >= n_rows) return nullptr;
     const int j = idx[slot0 + row];
     return (j >= 0 && j < L) ? h_v + (size_t)j * kH : nullptr;
   });
   seq_gemm<kEdgeRM, kEdgeCN, kH, kKC>(acc, A, kLdE, row0, w.W1_t + 256 * kH, kH, kH, Wbuf, col0);
-  __syncthreads();
 #pragma unroll
   for (int i = 0; i < kEdgeRM; ++i)
 #pragma unroll
@@ -97,7 +96,6 @@ __global__ __launch_bounds__(256) void edge_msg_kernel(EncLayerDev w, const floa
       acc[i][j] = 0.0F;
     }
   seq_gemm<kEdgeRM, kEdgeCN, kH, kKC>(acc, A, kLdE, row0, w.W2_t, kH, kH, Wbuf, col0);
-  __syncthreads();
 #pragma unroll
   for (int i = 0; i < kEdgeRM; ++i)
 #pragma unroll
@@ -106,27 +104,11 @@ __global__ __launch_bounds__(256) void edge_msg_kernel(EncLayerDev w, const floa
       acc[i][j] = 0.0F;
     }
   seq_gemm<kEdgeRM, kEdgeCN, kH, kKC>(acc, A, kLdE, row0, w.W3_t, kH, kH, Wbuf, col0);
-  __syncthreads();
 #pragma unroll
   for (int i = 0; i < kEdgeRM; ++i)
+    if (row0 + i < n_rows)
 #pragma unroll
-    for (int j = 0; j < kEdgeCN; ++j) A[(col0 + j) * kLdE + row0 + i] = acc[i][j] + w.b3[col0 + j];
-  __syncthreads();
-  const float scale = 1.0F / 30.0F;
-  for (int task = threadIdx.x; task < nr * kH; task += blockDim.x) {
-    const int lr = task / kH, c = task % kH;
-    const int r = r0 + lr;
-    float upd = 0.0F;
-    for (int k = 0; k < K; ++k) {
-      const int j = idx[slot0 + lr * K + k];
-      if (!(j >= 0 && j < L)) continue;
-      float alpha = scale;
-      alpha *= mask[r] * mask[j];
-      if (alpha == 0.0F) continue;
-      upd = alpha * A[c * kLdE + lr * K + k] + upd;
-    }
-    msg_sum[(size_t)r * kH + c] = upd;
-  }
+      for (int j = 0; j < kEdgeCN; ++j) msg[(slot0 + row0 + i) * kH + col0 + j] = acc[i][j] + w.b3[col0 + j];
 }
 
 // acc[j][r] += A[k][row0 + r] * Wt[k][c0 + j * CS] for k = k0 .. k0 + KB - 1 in
@@ -157,12 +139,11 @@ __device__ inline void load_rows(float (&w)[KB][CPT], const float* __restrict__ 
 }
 
 // Sequential-k product of a few rows with the thread's columns c0 + j * CS of
-// Wt [K][N] (t-layout). Weights stream from global memory 16 k-rows at a time
-// with the next 16 in flight while the current ones are used.
-template <int K, int N, int CPT, int CS, int RPT>
+// Wt [K][N] (t-layout). Weights stream from global memory KB k-rows at a time
+// with the next KB in flight while the current ones are used.
+template <int K, int N, int CPT, int CS, int RPT, int KB>
 __device__ inline void col_gemm(const float* __restrict__ Wt, const float* A, int lda, int row0, int c0,
                                 float (&acc)[CPT][RPT]) {
-  constexpr int KB = 16;
   static_assert(K % (2 * KB) == 0, "k chunking");
   float wa[KB][CPT], wb[KB][CPT];
   load_rows<KB, N, CPT, CS>(wa, Wt, 0, c0);
@@ -179,8 +160,9 @@ __device__ inline void col_gemm(const float* __restrict__ Wt, const float* A, in
 // layer's W1 prefix. Few rows per workgroup keep the grid wide; every thread
 // owns whole output columns, so each dot product runs over k in order.
 __global__ __launch_bounds__(256) void node_kernel(EncLayerDev w, const float* __restrict__ Wnext_t,
-                                                   const float* __restrict__ msg_sum, const float* __restrict__ mask,
-                                                   int L, float* __restrict__ h_v, float* __restrict__ prefix) {
+                                                   const float* __restrict__ msg, const int32_t* __restrict__ idx,
+                                                   const float* __restrict__ mask, int L, int K,
+                                                   float* __restrict__ h_v, float* __restrict__ prefix) {
 #pragma clang fp contract(off)
   constexpr int NR = kNodeRows;
   __shared__ __attribute__((aligned(16))) float X[kH * NR];   // k-major [d][row]
@@ -192,12 +174,38 @@ __global__ __launch_bounds__(256) void node_kernel(EncLayerDev w, const float* _
   const int t = threadIdx.x;
   static_assert(NR == 4, "thread mapping");
 
-  // X = h + upd (axpy order: 1 * residual + input)
-  for (int i = t; i < NR * kH; i += blockDim.x) {
-    const int row = i % NR, d = i / NR;
-    float v = 0.0F;
-    if (row < nr) v = h_v[(size_t)(r0 + row) * kH + d] + msg_sum[(size_t)(r0 + row) * kH + d];
-    X[d * NR + row] = v;
+  // upd = sum over valid slots, in order, of (1/30) mask_i mask_j m_ij; then
+  // X = h + upd (axpy order: 1 * residual + input). Thread t owns column
+  // t % 128 of rows 2 (t / 128) + {0, 1}; a row's K messages, neighbour
+  // indices and masks are all loaded before the sum starts.
+  {
+    const int d = t % kH, rb = 2 * (t / kH);
+    for (int q = 0; q < 2; ++q) {
+      const int row = rb + q;
+      float v = 0.0F;
+      if (row < nr) {
+        const int r = r0 + row;
+        float mv[kKmax], mj[kKmax];
+#pragma unroll
+        for (int k = 0; k < kKmax; ++k) {
+          const int j = k < K ? idx[(size_t)r * K + k] : -1;
+          const bool valid = j >= 0 && j < L;
+          mv[k] = valid ? msg[((size_t)r * K + k) * kH + d] : 0.0F;
+          mj[k] = valid ? mask[j] : 0.0F;
+        }
+        const float mr = mask[r];
+        float upd = 0.0F;
+#pragma unroll
+        for (int k = 0; k < kKmax; ++k) {
+          float alpha = 1.0F / 30.0F;
+          alpha *= mr * mj[k];
+          if (alpha == 0.0F) continue;  // also every invalid slot (mj = 0)
+          upd = alpha * mv[k] + upd;
+        }
+        v = h_v[(size_t)r * kH + d] + upd;
+      }
+      X[d * NR + row] = v;
+    }
   }
   __syncthreads();
   if (t < NR) welford_ln_col(X + t, H1 + t, NR, w.n1g, w.n1b);
@@ -205,7 +213,7 @@ __global__ __launch_bounds__(256) void node_kernel(EncLayerDev w, const float* _
   {
     // W_in: columns t and t + 256 of all rows, then GELU
     float acc[2][NR] = {};
-    col_gemm<kH, kFF, 2, 256, NR>(w.Win_t, H1, NR, 0, t, acc);
+    col_gemm<kH, kFF, 2, 256, NR, 32>(w.Win_t, H1, NR, 0, t, acc);
 #pragma unroll
     for (int j = 0; j < 2; ++j)
 #pragma unroll
@@ -216,7 +224,7 @@ __global__ __launch_bounds__(256) void node_kernel(EncLayerDev w, const float* _
     // W_out: column t % 128 of rows 2 (t / 128) + {0, 1}; X = h1 + (W_out f + b)
     const int c = t % kH, rr = 2 * (t / kH);
     float acc[1][2] = {};
-    col_gemm<kFF, kH, 1, 0, 2>(w.Wout_t, F, NR, rr, c, acc);
+    col_gemm<kFF, kH, 1, 0, 2, 32>(w.Wout_t, F, NR, rr, c, acc);
 #pragma unroll
     for (int r = 0; r < 2; ++r) X[c * NR + rr + r] = H1[c * NR + rr + r] + (acc[0][r] + w.bout[c]);
   }
@@ -237,7 +245,7 @@ __global__ __launch_bounds__(256) void node_kernel(EncLayerDev w, const float* _
     const float* Wt = part == 0 ? w.W11_t : Wnext_t;
     if (Wt) {
       float acc[1][NR] = {};
-      col_gemm<kH, kH, 1, 0, NR>(Wt, H2, NR, 0, c, acc);
+      col_gemm<kH, kH, 1, 0, NR, 32>(Wt, H2, NR, 0, c, acc);
 #pragma unroll
       for (int r = 0; r < NR; ++r)
         if (r < nr) prefix[(size_t)(r0 + r) * 256 + part * 128 + c] = acc[0][r];
@@ -251,12 +259,10 @@ __global__ __launch_bounds__(256) void edge_update_kernel(EncLayerDev w, float* 
                                                           const float* __restrict__ prefix, int L, int K) {
 #pragma clang fp contract(off)
   __shared__ __attribute__((aligned(16))) float A[kH * kLdE];
-  __shared__ __attribute__((aligned(16))) float Wbuf[kKC * kH];
-  const int nres = kRows / K;
-  const int r0 = blockIdx.x * nres;
-  const int nr = min(nres, L - r0);
-  const int n_rows = nr * K;
-  const size_t slot0 = (size_t)r0 * K;
+  __shared__ __attribute__((aligned(16))) float Wbuf[2 * kKC * kH];
+  const size_t S = (size_t)L * K;
+  const size_t slot0 = (size_t)blockIdx.x * kRows;
+  const int n_rows = (int)min((size_t)kRows, S - slot0);
   const int rg = threadIdx.x / 16, cg = threadIdx.x % 16;
   const int row0 = rg * kEdgeRM, col0 = cg * kEdgeCN;
 
@@ -264,7 +270,7 @@ __global__ __launch_bounds__(256) void edge_update_kernel(EncLayerDev w, float* 
 #pragma unroll
   for (int i = 0; i < kEdgeRM; ++i) {
     const int row = row0 + i;
-    const float* pre = row < n_rows ? prefix + (size_t)(r0 + row / K) * 256 : nullptr;
+    const float* pre = row < n_rows ? prefix + ((slot0 + row) / K) * 256 : nullptr;
 #pragma unroll
     for (int j = 0; j < kEdgeCN; ++j) acc[i][j] = pre ? pre[col0 + j] : 0.0F;
   }
@@ -272,14 +278,12 @@ __global__ __launch_bounds__(256) void edge_update_kernel(EncLayerDev w, float* 
     return row < n_rows ? h_e + (slot0 + row) * kH : nullptr;
   });
   seq_gemm<kEdgeRM, kEdgeCN, kH, kKC>(acc, A, kLdE, row0, w.W11_t + 128 * kH, kH, kH, Wbuf, col0);
-  __syncthreads();
   load_kmajor(A, kLdE, kRows, [&](int row) -> const float* {
     if (row >= n_rows) return nullptr;
     const int j = idx[slot0 + row];
     return (j >= 0 && j < L) ? h_v + (size_t)j * kH : nullptr;
   });
   seq_gemm<kEdgeRM, kEdgeCN, kH, kKC>(acc, A, kLdE, row0, w.W11_t + 256 * kH, kH, kH, Wbuf, col0);
-  __syncthreads();
 #pragma unroll
   for (int i = 0; i < kEdgeRM; ++i)
 #pragma unroll
@@ -288,7 +292,6 @@ __global__ __launch_bounds__(256) void edge_update_kernel(EncLayerDev w, float* 
       acc[i][j] = 0.0F;
     }
   seq_gemm<kEdgeRM, kEdgeCN, kH, kKC>(acc, A, kLdE, row0, w.W12_t, kH, kH, Wbuf, col0);
-  __syncthreads();
 #pragma unroll
   for (int i = 0; i < kEdgeRM; ++i)
 #pragma unroll
@@ -297,7 +300,6 @@ __global__ __launch_bounds__(256) void edge_update_kernel(EncLayerDev w, float* 
       acc[i][j] = 0.0F;
     }
   seq_gemm<kEdgeRM, kEdgeCN, kH, kKC>(acc, A, kLdE, row0, w.W13_t, kH, kH, Wbuf, col0);
-  __syncthreads();
   // x = 1 * e + m  (axpy order), then LN3 per valid row
 #pragma unroll
   for (int i = 0; i < kEdgeRM; ++i)
@@ -339,13 +341,12 @@ hipError_t launch_encoder(const ModelDev& m, const int32_t* idx, const float* ma
   if (e != hipSuccess) return e;
   e = launch_zero(ws.prefix, (size_t)L * 256, stream);
   if (e != hipSuccess) return e;
-  const int nres = kRows / K;
-  const unsigned edge_tiles = (unsigned)((L + nres - 1) / nres);
+  const unsigned edge_tiles = (unsigned)(((size_t)L * K + kRows - 1) / kRows);
   const unsigned node_tiles = (unsigned)((L + kNodeRows - 1) / kNodeRows);
   for (int l = 0; l < kLayers; ++l) {
-    edge_msg_kernel<<<edge_tiles, 256, 0, stream>>>(m.enc[l], h_e, h_v, idx, mask, ws.prefix, L, K, ws.msg_sum);
-    node_kernel<<<node_tiles, 256, 0, stream>>>(m.enc[l], l + 1 < kLayers ? m.enc[l + 1].W1_t : nullptr, ws.msg_sum,
-                                                mask, L, h_v, ws.prefix);
+    edge_msg_kernel<<<edge_tiles, 256, 0, stream>>>(m.enc[l], h_e, h_v, idx, ws.prefix, L, K, ws.msg);
+    node_kernel<<<node_tiles, 256, 0, stream>>>(m.enc[l], l + 1 < kLayers ? m.enc[l + 1].W1_t : nullptr, ws.msg,
+                                                idx, mask, L, K, h_v, ws.prefix);
     edge_update_kernel<<<edge_tiles, 256, 0, stream>>>(m.enc[l], h_e, h_v, idx, ws.prefix, L, K);
   }
   return hipGetLastError();

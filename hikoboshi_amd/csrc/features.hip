@@ -117,7 +117,7 @@ __global__ __launch_bounds__(256) void edge_embed_kernel(ModelDev m, const float
 #pragma clang fp contract(off)
   __shared__ __attribute__((aligned(16))) float A[kEdgeIn * kLdT];
   __shared__ __attribute__((aligned(16))) float X[kH * kLdT];
-  __shared__ __attribute__((aligned(16))) float Wbuf[32 * kH];
+  __shared__ __attribute__((aligned(16))) float Wbuf[2 * 32 * kH];
   const size_t S = (size_t)L * K;
   const size_t slot0 = (size_t)blockIdx.x * kTile;
   const int rg = threadIdx.x / 32, cg = threadIdx.x % 32;

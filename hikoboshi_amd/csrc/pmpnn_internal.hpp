@@ -89,7 +89,7 @@ hipError_t launch_edge_embed(const ModelDev& m, const float* coords, const uint8
                              int K, float* h_e, hipStream_t stream);
 struct EncoderScratch {
   float* prefix;   // [L][256]: sequential partial sums over the h_i inputs of [W11 | next W1]
-  float* msg_sum;  // [L][128]
+  float* msg;      // [L * K][128] edge messages of the current layer
 };
 // Fills n floats with zero (a kernel, so it can sit inside a captured graph).
 hipError_t launch_zero(float* p, size_t n, hipStream_t stream);
@@ -120,10 +120,13 @@ struct DecodeArgs {
   uint32_t* sync;         // [B] team barrier counters, zero at launch
   uint32_t* fault;        // [1] set when a team barrier times out, zero at launch
   int team;               // workgroups per sequence (set by launch_decode)
+  uint32_t spin_limit;    // polls before a team barrier gives up (set by launch_decode)
 };
-// Decodes with up to 4 workgroups per sequence when the device keeps every
-// workgroup of the grid resident (cooperative launch), else one per sequence.
-hipError_t launch_decode(const ModelDev& m, const DecodeArgs& a, hipStream_t stream);
+// Decodes with up to min(4, max_team) workgroups per sequence when the whole
+// grid fits the device at once, else one per sequence. A team launch that
+// could not run its members together raises *a.fault (and leaves NaN scores);
+// run it again with max_team = 1.
+hipError_t launch_decode(const ModelDev& m, const DecodeArgs& a, hipStream_t stream, int max_team = 4);
 // Q[l] = W1d_l h^0 (l < 3), Q[3] = W1a_0 h^0, without the E1 edge products.
 hipError_t launch_q_precompute(const ModelDev& m, const float* h_v, int L, float* Q, hipStream_t stream);
 struct TfArgs {

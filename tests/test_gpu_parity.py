@@ -233,6 +233,22 @@ def test_design_team_split_is_exact(gpu_ctx, oracle, B, monkeypatch):
                  true_tokens=tt)
 
 
+def test_design_team_barrier_timeout_reruns(gpu_ctx, monkeypatch):
+    """A team barrier that gives up (forced here by a one-poll wait limit) leaves
+    the kernel early with the fault word raised; the design call then decodes
+    again with one workgroup per sequence and returns the same bits."""
+    bb = backbone.single_chain(90, 6)
+    seeds = (np.arange(5) + 3).astype(np.uint64)
+    monkeypatch.setenv("HKBS_DECODE_TEAM", "1")
+    ref = gpu_ctx.design(bb.coords, bb.atom_sources, 5, seeds, order_seeds=seeds, temperature=0.1)
+    monkeypatch.setenv("HKBS_DECODE_TEAM", "4")
+    monkeypatch.setenv("HKBS_DECODE_SPIN_LIMIT", "1")
+    _say("design with a one-poll team barrier")
+    out = gpu_ctx.design(bb.coords, bb.atom_sources, 5, seeds, order_seeds=seeds, temperature=0.1)
+    for key in ("tokens", "log_probs", "scores"):
+        np.testing.assert_array_equal(out[key], ref[key], err_msg=key)
+
+
 def test_design_deterministic(gpu_ctx):
     bb = backbone.single_chain(64, 2)
     seeds = np.array([3, 4, 5], dtype=np.uint64)
