@@ -655,7 +655,8 @@ size_t decode_bytes(int L, int K, int B) {
          2 * aligned_bytes<int32_t>((size_t)B * L) + aligned_bytes<uint64_t>(B) +
          aligned_bytes<float>((size_t)B * kLayers * L * kH) + aligned_bytes<int32_t>((size_t)B * L) +
          aligned_bytes<float>((size_t)B * L * kV) + aligned_bytes<float>((size_t)B * L) + aligned_bytes<float>(B) +
-         aligned_bytes<uint32_t>((size_t)B + 1);
+         aligned_bytes<uint32_t>((size_t)B + 1) + aligned_bytes<int32_t>((size_t)B * L) +
+         2 * aligned_bytes<int32_t>((size_t)B * L * K);
 }
 
 hkbs_status enter(hkbs_pmpnn* ctx) {
@@ -683,6 +684,10 @@ hkbs_status design_on_device(hkbs_pmpnn* ctx, const float* coords, const uint8_t
   int32_t* pos = ar.take<int32_t>((size_t)B * L);
   float* R = ar.take<float>((size_t)B * kLayers * L * kH);
   uint32_t* sync = ar.take<uint32_t>((size_t)B + 1);  // B team counters + fault word
+  const size_t nq = shared ? 1 : (size_t)B;
+  int32_t* gsize = ar.take<int32_t>(nq * L);
+  int32_t* nbj = ar.take<int32_t>(nq * L * K);
+  int32_t* nbp = ar.take<int32_t>(nq * L * K);
   ctx->fault = sync + B;
   if (ctx->timing) HK_CHECK(hipEventRecord(ctx->ev[0], ctx->stream), "event record failed");
   HK_CHECK(run_encode(ctx, coords, src, resid, chain, L, K, e), "encoder launch failed");
@@ -715,6 +720,9 @@ hkbs_status design_on_device(hkbs_pmpnn* ctx, const float* coords, const uint8_t
   a.chosen_lp = chosen;
   a.sync = sync;
   a.fault = sync + B;
+  a.gsize = gsize;
+  a.nbj = nbj;
+  a.nbp = nbp;
   ctx->last_decode = a;
   HK_CHECK(launch_decode(ctx->model, a, ctx->stream), "decode launch failed");
   if (ctx->timing) {

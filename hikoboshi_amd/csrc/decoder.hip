@@ -214,7 +214,6 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(ModelDev m, DecodeArgs
   __shared__ int bwf[kGroup * kKmax];
   __shared__ int tres[kGroup];
   __shared__ int tok_s[kGroup];
-  __shared__ int m_s;
   __shared__ int bad;
 
   const int P = a.team;
@@ -230,7 +229,9 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(ModelDev m, DecodeArgs
   const int wave = threadIdx.x >> 6;
   const int lane = threadIdx.x & 63;
   const int32_t* order = a.shared_order ? a.orders : a.orders + (size_t)b * L;
-  const int32_t* pos = a.shared_order ? a.pos : a.pos + (size_t)b * L;
+  const int32_t* gsize = a.shared_order ? a.gsize : a.gsize + (size_t)b * L;
+  const int32_t* nbj = a.shared_order ? a.nbj : a.nbj + (size_t)b * L * K;
+  const int32_t* nbp = a.shared_order ? a.nbp : a.nbp + (size_t)b * L * K;
   float* R = a.R + (size_t)b * kLayers * L * kH;
   int32_t* tokens = a.tokens + (size_t)b * L;
   float* lp_out = a.log_probs ? a.log_probs + (size_t)b * L * kV : nullptr;
@@ -288,35 +289,17 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(ModelDev m, DecodeArgs
       __syncthreads();
       continue;
     }
-    // Group: stop before the first later residue that is inactive, out of
-    // range, or has an earlier group member among its neighbours.
-    if (threadIdx.x == 0) m_s = min(kGroup, L - step);
-    __syncthreads();
-    if (threadIdx.x < (kGroup - 1) * K) {
-      const int c = 1 + threadIdx.x / K, k = threadIdx.x % K;
-      if (step + c < L) {
-        const int tc = order[step + c];
-        bool stop = tc < 0 || tc >= L;
-        if (!stop) {
-          stop = a.mask[tc] == 0.0F;
-          const int j = a.idx[(size_t)tc * K + k];
-          if (j >= 0 && j < L && pos[j] >= step && pos[j] < step + c) stop = true;
-        }
-        if (stop) atomicMin(&m_s, c);
-      }
-    }
-    __syncthreads();
-    const int mg = m_s;
+    // Group of consecutive independent steps (sizes precomputed per step).
+    const int mg = gsize[step];
     const int ml = mg > rank ? (mg - rank + P - 1) / P : 0;  // members of this rank: rank + P i
     if (ml > 0) {
       if (threadIdx.x < ml * K) {
         const int i = threadIdx.x / K, k = threadIdx.x % K;
-        const int t = order[step + rank + P * i];
-        const int j = a.idx[(size_t)t * K + k];
-        const bool valid = j >= 0 && j < L;
-        nbr[i * kKmax + k] = valid ? j : -1;
-        bwf[i * kKmax + k] = valid && pos[j] < step;
-        if (k == 0) tres[i] = t;
+        const size_t at = (size_t)(step + rank + P * i) * K + k;
+        const int j = nbj[at];
+        nbr[i * kKmax + k] = j;
+        bwf[i * kKmax + k] = nbp[at] < step;  // empty slots hold position L
+        if (k == 0) tres[i] = order[step + rank + P * i];
       }
       for (int task = threadIdx.x; task < ml * kH; task += kThreads) {
         const int i = task / kH, c = task % kH;
@@ -327,6 +310,8 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(ModelDev m, DecodeArgs
       }
       __syncthreads();
 
+      GLog::Part lg;  // logits weights in flight for the whole pass
+      GLog::load(lg, m.Wlog_t, 0);
       for (int l = 0; l < kLayers; ++l) {
         const DecLayerDev& w = m.dec[l];
         const float* Ql = a.Q + (size_t)l * L * kH;
@@ -344,6 +329,8 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(ModelDev m, DecodeArgs
         }
         const float* pl = prm + l * kPrmLayer;
         const float b2 = pl[kPrmB2 + col];
+        G3::Part g3;  // W3 in flight during the message rows and their product
+        G3::load(g3, w.W3_t, 0);
         for (int i0 = 0; i0 < ml; i0 += 2) {
           {
             // Message rows g1 = GELU(A + E1_tk + (bw ? R : Q)_j) of members i0, i0 + 1;
@@ -442,8 +429,6 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(ModelDev m, DecodeArgs
         // upd = (W3 s + K b3) / 30 ; h1 = LN1(h + upd): wave i owns member i
         float4 acc[kGroup];
         zero4(acc);
-        G3::Part g3;
-        G3::load(g3, w.W3_t, 0);
         G3::fma(g3, 0, x, ml, acc);
         G3::store(acc, ml, part);
         GIn::Part in0;  // first half of W_in in flight during the reduction and LN1
@@ -519,8 +504,6 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(ModelDev m, DecodeArgs
       {
         float4 acc[kGroup];
         zero4(acc);
-        GLog::Part lg;
-        GLog::load(lg, m.Wlog_t, 0);
         GLog::fma(lg, 0, h, ml, acc);
         GLog::store(acc, ml, part);
       }
@@ -626,6 +609,56 @@ __global__ void scatter_positions_kernel(const int32_t* __restrict__ orders, int
   if (r >= 0 && r < L) pos[(size_t)b * L + r] = s;
 }
 
+// Neighbour lists in decoding order: for step s of order q, slot k holds
+// j = idx[order[s], k] and its position pos[j] (-1 and L for an empty slot).
+__global__ void neighbour_schedule_kernel(const int32_t* __restrict__ orders, const int32_t* __restrict__ pos,
+                                          const int32_t* __restrict__ idx, int L, int K, int32_t* __restrict__ nbj,
+                                          int32_t* __restrict__ nbp) {
+  const int q = blockIdx.y;
+  const size_t n = (size_t)L * K;
+  for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x) {
+    const int s = (int)(i / K), k = (int)(i % K);
+    const int t = orders[(size_t)q * L + s];
+    int j = -1, p = L;
+    if (t >= 0 && t < L) {
+      const int jj = idx[(size_t)t * K + k];
+      if (jj >= 0 && jj < L) {
+        j = jj;
+        p = pos[(size_t)q * L + jj];
+      }
+    }
+    nbj[(size_t)q * n + i] = j;
+    nbp[(size_t)q * n + i] = p;
+  }
+}
+
+// Size of the group that starts at step s: it stops before the first later
+// step whose residue is inactive or out of range, or has a neighbour decoded
+// at a step in [s, that step) (decode_kernel decodes a group's members
+// together, so none may read another's state).
+__global__ void group_schedule_kernel(const int32_t* __restrict__ orders, const float* __restrict__ mask,
+                                      const int32_t* __restrict__ nbp, int L, int K, int32_t* __restrict__ gsize) {
+  const int q = blockIdx.y;
+  const int s = blockIdx.x * blockDim.x + threadIdx.x;
+  if (s >= L) return;
+  const int32_t* order = orders + (size_t)q * L;
+  const int32_t* np = nbp + (size_t)q * L * K;
+  int m = min(kGroup, L - s);
+  for (int c = 1; c < m; ++c) {
+    const int tc = order[s + c];
+    bool stop = tc < 0 || tc >= L || mask[tc] == 0.0F;
+    for (int k = 0; k < K && !stop; ++k) {
+      const int p = np[(size_t)(s + c) * K + k];
+      stop = p >= s && p < s + c;
+    }
+    if (stop) {
+      m = c;
+      break;
+    }
+  }
+  gsize[(size_t)q * L + s] = m;
+}
+
 }  // namespace
 
 hipError_t launch_positions(const int32_t* orders, int L, int n_orders, int shared, int32_t* pos, hipStream_t stream) {
@@ -670,6 +703,16 @@ hipError_t launch_decode(const ModelDev& m, const DecodeArgs& args, hipStream_t 
   if (const char* env = std::getenv("HKBS_DECODE_TEAM")) P = std::max(1, std::min(P, std::atoi(env)));
   while (P > 1 && 8 * teams_per_xcd * P > resident) --P;
   if (!a.sync || !a.fault) P = 1;
+  {
+    const int nq = a.shared_order ? 1 : a.B;
+    const size_t n = (size_t)a.L * a.K;
+    neighbour_schedule_kernel<<<dim3((unsigned)std::min<size_t>((n + 255) / 256, 4096), nq), 256, 0, stream>>>(
+        a.orders, a.pos, a.idx, a.L, a.K, a.nbj, a.nbp);
+    group_schedule_kernel<<<dim3((unsigned)((a.L + 255) / 256), nq), 256, 0, stream>>>(a.orders, a.mask, a.nbp, a.L,
+                                                                                         a.K, a.gsize);
+    e = hipGetLastError();
+    if (e != hipSuccess) return e;
+  }
   a.spin_limit = kSpinLimit;
   if (const char* env = std::getenv("HKBS_DECODE_SPIN_LIMIT")) a.spin_limit = (uint32_t)std::max(1, std::atoi(env));
   if (P > 1) {

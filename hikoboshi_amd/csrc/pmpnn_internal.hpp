@@ -106,6 +106,9 @@ struct DecodeArgs {
   const int32_t* orders;  // [B][L] or [L]
   int shared_order;
   const int32_t* pos;     // [B][L] or [L]: position of residue r in the order
+  int32_t* gsize;         // [B][L] or [L] workspace: group size starting at each step
+  int32_t* nbj;           // [B][L][K] or [L][K] workspace: neighbours of the residue at each step
+  int32_t* nbp;           // same shape: their positions in the order (L for an empty slot)
   const float* chain_mask;   // [L] or null
   const int32_t* true_tokens; // [L] or null
   const uint64_t* seeds;  // [B]
