@@ -13,7 +13,9 @@ Printed JSON also carries
                       FLOP per sampled residue (reference arithmetic),
   decode_hbm          the same kernel against HBM bandwidth (compulsory bytes),
   cpu_baseline        the reference's own scalar path (oracle/_ref) on a bounded
-                      sample of the same workload, timed on this host.
+                      sample of the same workload (one sequence per host core, up to
+                      16 forked worker processes), timed on this host before the GPU
+                      is touched.
 """
 from __future__ import annotations
 
@@ -45,7 +47,8 @@ def parse_args():
     p.add_argument("--num-seqs", type=int, default=64)
     p.add_argument("--temperature", type=float, default=0.1)
     p.add_argument("--seed", type=int, default=7)
-    p.add_argument("--cpu-sample", type=int, default=2, help="sequences timed on the CPU baseline")
+    p.add_argument("--cpu-sample", type=int, default=0,
+                   help="sequences timed on the CPU baseline (default: one per worker process)")
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     p.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
                    help="only run a device-to-device copy of MIB MiB (HBM-counter calibration) and exit")
@@ -79,9 +82,10 @@ def measured_traffic(workload: str):
     return None, None
 
 
-def cpu_baseline(bb, order, seeds, temperature, n, gpu_tokens, gpu_lp):
-    """Reference scalar path, one module call per sequence (it re-encodes each time)."""
-    from hikoboshi_amd import weights
+def _cpu_design(job):
+    """One CPU worker: the reference's scalar module call for each sequence index in the job."""
+    idxs, L, seed, temperature, order = job
+    from hikoboshi_amd import backbone, weights
     import oracle
 
     tensors = weights.load_tensors()
@@ -89,23 +93,51 @@ def cpu_baseline(bb, order, seeds, temperature, n, gpu_tokens, gpu_lp):
         impl, kind = oracle.Reference(tensors), "reference"
     else:
         impl, kind = oracle.Oracle(tensors), "port"
+    bb = backbone.single_chain(L, seed)
+    out = []
+    for b in idxs:
+        t0 = time.perf_counter()
+        o = impl.inverse_fold(bb, seed=seed + b, order_seed=seed + b, temperature=temperature, input_order=order,
+                              use_input_order=True)
+        out.append((b, o["tokens"], o["log_probs"], time.perf_counter() - t0))
+    return kind, out
+
+
+def cpu_baseline(L, seed, temperature, order, n, workers):
+    """Reference scalar path on `n` of the sequences, one single-threaded module call per
+    sequence (it re-encodes each time, as the reference's per-sample loop does), spread over
+    `workers` forked processes. Runs before this process touches the GPU."""
+    import multiprocessing as mp
+
+    jobs = [(list(range(w, n, workers)), L, seed, temperature, order) for w in range(workers)]
+    jobs = [j for j in jobs if j[0]]
     t0 = time.perf_counter()
-    outs = [impl.inverse_fold(bb, seed=int(seeds[b]), order_seed=int(seeds[b]), temperature=temperature,
-                              input_order=order, use_input_order=True) for b in range(n)]
-    dt = time.perf_counter() - t0
-    same = [bool((o["tokens"] == gpu_tokens[b]).all()) for b, o in enumerate(outs)]
-    dlp = [float(np.abs(o["log_probs"] - gpu_lp[b]).max()) for b, o in enumerate(outs) if same[b]]
+    with mp.get_context("fork").Pool(len(jobs)) as pool:
+        res = pool.map(_cpu_design, jobs)
+    wall = time.perf_counter() - t0
+    kind = res[0][0]
+    seqs = sorted((r for _, rs in res for r in rs), key=lambda r: r[0])
+    per_seq = float(np.mean([r[3] for r in seqs]))
     return {
-        "value": n * bb.L / dt,
+        "value": n * L / wall,
         "unit": "residues/s",
-        "cores": 1,
+        "cores": len(jobs),
         "kind": kind,
-        "sample": f"{n} of the {len(seeds)} sequences (L={bb.L}, shared order, sampler seeds "
-                  f"{int(seeds[0])}..{int(seeds[n - 1])}), one single-threaded module call each "
+        "sample": f"{n} of the sequences (L={L}, shared order, sampler seeds {seed}..{seed + n - 1}) on "
+                  f"{len(jobs)} forked worker processes, one single-threaded module call per sequence "
                   f"(featurise + encode + decode, re-encoding per sequence as the reference does); "
-                  f"{dt:.1f} s",
-        "parity_spot_check": {"tokens_identical": same, "max_abs_dlogp": max(dlp) if dlp else None},
+                  f"{wall:.1f} s wall including worker start-up",
+        "single_core_value": L / per_seq,
+        "_outputs": {r[0]: (r[1], r[2]) for r in seqs},
     }
+
+
+def spot_check(cpu, gpu_tokens, gpu_lp):
+    out = cpu.pop("_outputs")
+    same = {b: bool((t == gpu_tokens[b]).all()) for b, (t, _) in out.items()}
+    dlp = [float(np.abs(lp - gpu_lp[b]).max()) for b, (_, lp) in out.items() if same[b]]
+    cpu["parity_spot_check"] = {"tokens_identical": int(sum(same.values())), "of": len(same),
+                                "max_abs_dlogp": max(dlp) if dlp else None}
 
 
 def main() -> int:
@@ -116,13 +148,27 @@ def main() -> int:
         print(json.dumps({"error": "this build runs on one GPU; --gpus must be 1 (the path shards by "
                                    "sequences across GPUs, which this benchmark does not launch)"}))
         return 2
-    from hikoboshi_amd import _lib, backbone, hip, weights
+    from hikoboshi_amd import backbone, weights
 
     L, B, T = args.L, args.num_seqs, args.temperature
     K = min(48, L)
     bb = backbone.single_chain(L, args.seed)
-    order = _lib.decode_order(bb.atom_sources, args.seed)
     seeds = (args.seed + np.arange(B)).astype(np.uint64)
+    cpu = None
+    if not args.no_cpu:
+        # The CPU leg runs first, in forked workers, while this process has not touched the GPU.
+        import oracle
+
+        valid = (bb.atom_sources[:, :4] != 0).all(1).astype(np.float32)
+        host_order = oracle.Oracle(weights.load_tensors()).decode_order(L, args.seed, residue_mask=valid)
+        workers = max(1, min(16, os.cpu_count() or 1))
+        cpu = cpu_baseline(L, args.seed, T, host_order, max(1, min(args.cpu_sample or workers, B)), workers)
+
+    from hikoboshi_amd import _lib, hip
+
+    order = _lib.decode_order(bb.atom_sources, args.seed)
+    if cpu is not None and not np.array_equal(order, host_order):
+        raise RuntimeError("decode order differs between the library and the oracle")
     ctx = _lib.Context(weights.read_package_bytes(), device=0)
 
     d_coords = hip.DeviceBuffer.from_array(bb.coords)
@@ -215,9 +261,9 @@ def main() -> int:
             "backward_edges": e_bw,
         },
     }
-    if not args.no_cpu:
-        n = max(1, min(args.cpu_sample, B))
-        result["cpu_baseline"] = cpu_baseline(bb, order, seeds, T, n, h_tokens.array, h_lp.array)
+    if cpu is not None:
+        spot_check(cpu, h_tokens.array, h_lp.array)
+        result["cpu_baseline"] = cpu
     ctx.close()
     print(json.dumps(result), flush=True)
     return 0

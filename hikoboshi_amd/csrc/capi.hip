@@ -695,7 +695,6 @@ hkbs_status design_on_device(hkbs_pmpnn* ctx, const float* coords, const uint8_t
   HK_CHECK(launch_decoder_precompute(ctx->model, e.h_v, e.h_e, L, K, E1, Q, ctx->stream), "decoder precompute failed");
   HK_CHECK(launch_positions(orders, L, shared ? 1 : B, shared, pos, ctx->stream), "position kernel failed");
   HK_CHECK(launch_zero(reinterpret_cast<float*>(sync), (size_t)B + 1, ctx->stream), "workspace clear failed");
-  if (ctx->timing) HK_CHECK(hipEventRecord(ctx->ev[2], ctx->stream), "event record failed");
   DecodeArgs a{};
   a.idx = e.idx;
   a.mask = e.mask;
@@ -724,6 +723,8 @@ hkbs_status design_on_device(hkbs_pmpnn* ctx, const float* coords, const uint8_t
   a.nbj = nbj;
   a.nbp = nbp;
   ctx->last_decode = a;
+  HK_CHECK(launch_decode_schedule(a, ctx->stream), "decode schedule launch failed");
+  if (ctx->timing) HK_CHECK(hipEventRecord(ctx->ev[2], ctx->stream), "event record failed");
   HK_CHECK(launch_decode(ctx->model, a, ctx->stream), "decode launch failed");
   if (ctx->timing) {
     HK_CHECK(hipEventRecord(ctx->ev[3], ctx->stream), "event record failed");

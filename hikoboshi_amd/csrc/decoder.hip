@@ -688,6 +688,17 @@ hipError_t launch_q_precompute(const ModelDev& m, const float* h_v, int L, float
   return hipGetLastError();
 }
 
+hipError_t launch_decode_schedule(const DecodeArgs& a, hipStream_t stream) {
+  if (a.L <= 0 || a.B <= 0) return hipSuccess;
+  const int nq = a.shared_order ? 1 : a.B;
+  const size_t n = (size_t)a.L * a.K;
+  neighbour_schedule_kernel<<<dim3((unsigned)std::min<size_t>((n + 255) / 256, 4096), nq), 256, 0, stream>>>(
+      a.orders, a.pos, a.idx, a.L, a.K, a.nbj, a.nbp);
+  group_schedule_kernel<<<dim3((unsigned)((a.L + 255) / 256), nq), 256, 0, stream>>>(a.orders, a.mask, a.nbp, a.L, a.K,
+                                                                                       a.gsize);
+  return hipGetLastError();
+}
+
 hipError_t launch_decode(const ModelDev& m, const DecodeArgs& args, hipStream_t stream, int max_team) {
   if (args.L <= 0 || args.B <= 0) return hipSuccess;
   DecodeArgs a = args;
@@ -703,16 +714,6 @@ hipError_t launch_decode(const ModelDev& m, const DecodeArgs& args, hipStream_t 
   if (const char* env = std::getenv("HKBS_DECODE_TEAM")) P = std::max(1, std::min(P, std::atoi(env)));
   while (P > 1 && 8 * teams_per_xcd * P > resident) --P;
   if (!a.sync || !a.fault) P = 1;
-  {
-    const int nq = a.shared_order ? 1 : a.B;
-    const size_t n = (size_t)a.L * a.K;
-    neighbour_schedule_kernel<<<dim3((unsigned)std::min<size_t>((n + 255) / 256, 4096), nq), 256, 0, stream>>>(
-        a.orders, a.pos, a.idx, a.L, a.K, a.nbj, a.nbp);
-    group_schedule_kernel<<<dim3((unsigned)((a.L + 255) / 256), nq), 256, 0, stream>>>(a.orders, a.mask, a.nbp, a.L,
-                                                                                         a.K, a.gsize);
-    e = hipGetLastError();
-    if (e != hipSuccess) return e;
-  }
   a.spin_limit = kSpinLimit;
   if (const char* env = std::getenv("HKBS_DECODE_SPIN_LIMIT")) a.spin_limit = (uint32_t)std::max(1, std::atoi(env));
   if (P > 1) {

@@ -125,6 +125,9 @@ struct DecodeArgs {
   int team;               // workgroups per sequence (set by launch_decode)
   uint32_t spin_limit;    // polls before a team barrier gives up (set by launch_decode)
 };
+// Group sizes and per-step neighbour lists (a.gsize, a.nbj, a.nbp) from the
+// orders, positions and kNN graph; launch_decode reads them.
+hipError_t launch_decode_schedule(const DecodeArgs& a, hipStream_t stream);
 // Decodes with up to min(4, max_team) workgroups per sequence when the whole
 // grid fits the device at once, else one per sequence. A team launch that
 // could not run its members together raises *a.fault (and leaves NaN scores);

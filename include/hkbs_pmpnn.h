@@ -102,7 +102,13 @@ hkbs_status hkbs_pmpnn_design(hkbs_pmpnn* ctx, const float* coords, const uint8_
 /* Device-resident variant: every pointer argument is device memory, orders
  * is [B,L] or [L] (shared != 0), and the call is enqueued on `stream`
  * (a hipStream_t; NULL = the context's stream) without synchronising.
- * residue_indices / chain_labels / chain_mask / true_tokens may be NULL. */
+ * residue_indices / chain_labels / chain_mask / true_tokens may be NULL.
+ * When B leaves CUs free, each sequence is decoded by a team of up to four
+ * workgroups that must run at the same time; on a device busy with other
+ * work a team can fail to assemble, and then that sequence's score is NaN
+ * (the synchronous hkbs_pmpnn_design detects this and decodes again with one
+ * workgroup per sequence). HKBS_DECODE_TEAM=1 in the environment disables
+ * teams. */
 hkbs_status hkbs_pmpnn_design_device(hkbs_pmpnn* ctx, const float* coords,
                                      const uint8_t* atom_sources, const int32_t* residue_indices,
                                      const int32_t* chain_labels, const float* chain_mask,
@@ -139,7 +145,8 @@ hkbs_status hkbs_pmpnn_decode_order(const float* chain_mask, const uint8_t* atom
  * no design-path profiler). With timing enabled, each design call records
  * HIP events on the stream its kernels run on around three phases;
  * hkbs_pmpnn_last_timing waits for the last call and returns the elapsed
- * milliseconds of [featurise + encode, decoder precompute, decode loop]. */
+ * milliseconds of [featurise + encode, decoder precompute and decode
+ * schedule, decode loop (the decode kernel alone)]. */
 hkbs_status hkbs_pmpnn_set_timing(hkbs_pmpnn* ctx, int32_t enable);
 hkbs_status hkbs_pmpnn_last_timing(hkbs_pmpnn* ctx, float* ms /* [3] */);
 
