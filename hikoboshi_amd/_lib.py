@@ -23,7 +23,7 @@ EXPORTS = (
     "hkbs_last_error", "hkbs_version", "hkbs_device_count", "hkbs_pmpnn_create", "hkbs_pmpnn_destroy",
     "hkbs_pmpnn_design", "hkbs_pmpnn_design_device", "hkbs_pmpnn_score", "hkbs_pmpnn_decode_order",
     "hkbs_pmpnn_knn", "hkbs_pmpnn_encode", "hkbs_pmpnn_edge_features", "hkbs_pmpnn_set_timing",
-    "hkbs_pmpnn_last_timing", "hkbs_pmpnn_score_batch",
+    "hkbs_pmpnn_last_timing", "hkbs_pmpnn_score_batch", "hkbs_pmpnn_backbone_noise",
 )
 
 
@@ -63,6 +63,8 @@ def load() -> C.CDLL:
     lib.hkbs_pmpnn_score.argtypes = [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i32, _vp, _vp]
     lib.hkbs_pmpnn_score_batch.restype = _i32
     lib.hkbs_pmpnn_score_batch.argtypes = [_vp, _i32, _vp, _vp, _vp, _vp, _vp, _vp, _vp]
+    lib.hkbs_pmpnn_backbone_noise.restype = _i32
+    lib.hkbs_pmpnn_backbone_noise.argtypes = [_vp, _vp, _i32, C.c_float, C.c_uint64, _vp]
     lib.hkbs_pmpnn_decode_order.restype = _i32
     lib.hkbs_pmpnn_decode_order.argtypes = [_vp, _vp, _i32, C.c_uint64, _vp]
     lib.hkbs_pmpnn_knn.restype = _i32
@@ -111,6 +113,16 @@ def version() -> str:
 
 def device_count() -> int:
     return int(load().hkbs_device_count())
+
+
+def backbone_noise(coords, atom_sources, sigma: float, seed: int) -> np.ndarray:
+    """Coordinates plus the reference's per-sample Gaussian backbone noise (host)."""
+    c = f32(coords)
+    src = u8(atom_sources)
+    out = np.empty_like(c)
+    check(load().hkbs_pmpnn_backbone_noise(ptr(c), ptr(src), int(c.shape[0]), C.c_float(sigma), C.c_uint64(seed),
+                                           ptr(out)))
+    return out
 
 
 def decode_order(atom_sources: np.ndarray, seed: int, chain_mask: np.ndarray | None = None) -> np.ndarray:

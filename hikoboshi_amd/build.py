@@ -17,7 +17,9 @@ HERE = Path(__file__).resolve().parent
 CSRC = HERE / "csrc"
 LIB = HERE / "libhkbs_pmpnn.so"
 ARCH = os.environ.get("HKBS_OFFLOAD_ARCH", "gfx950")
-SOURCES = ["knn.hip", "features.hip", "encoder.hip", "decoder.hip", "decoder_tf.hip", "capi.hip"]
+SOURCES = ["knn.hip", "features.hip", "encoder.hip", "decoder.hip", "decoder_tf.hip", "capi.hip", "host_noise.cpp"]
+# Host-only C++ (no device code), without floating-point contraction.
+HOST_FLAGS = ["-ffp-contract=off"]
 
 
 def hipcc() -> str:
@@ -38,7 +40,8 @@ def build(verbose: bool = False) -> Path:
     ]
     for src in SOURCES:
         obj = obj_dir / (Path(src).stem + ".o")
-        cmd = common + ["-c", str(CSRC / src), "-o", str(obj)]
+        extra = HOST_FLAGS if src.endswith(".cpp") else []
+        cmd = common + extra + ["-c", str(CSRC / src), "-o", str(obj)]
         if verbose:
             print(" ".join(cmd), flush=True)
         subprocess.run(cmd, check=True)

@@ -818,6 +818,15 @@ hkbs_status hkbs_pmpnn_decode_order(const float* chain_mask, const uint8_t* atom
   return HKBS_OK;
 }
 
+hkbs_status hkbs_pmpnn_backbone_noise(const float* coords, const uint8_t* atom_sources, int32_t L, float sigma,
+                                      uint64_t seed, float* out) {
+  if (L < 0) return fail(HKBS_INVALID_ARGUMENT, "residue count is negative");
+  if (!std::isfinite(sigma) || sigma < 0.0F) return fail(HKBS_INVALID_ARGUMENT, "inverse-fold backbone_noise must be finite and >= 0");
+  if (L > 0 && (!coords || !atom_sources || !out)) return fail(HKBS_INVALID_ARGUMENT, "backbone noise pointers must be non-null");
+  if (L > 0) backbone_noise_host(coords, atom_sources, L, sigma, seed, out);
+  return HKBS_OK;
+}
+
 hkbs_status hkbs_pmpnn_design(hkbs_pmpnn* ctx, const float* coords, const uint8_t* atom_sources,
                               const int32_t* residue_indices, const int32_t* chain_labels, const float* chain_mask,
                               const int32_t* true_tokens, int32_t L, int32_t B, int32_t order_mode,

@@ -93,6 +93,9 @@ struct EncoderScratch {
 };
 // Fills n floats with zero (a kernel, so it can sit inside a captured graph).
 hipError_t launch_zero(float* p, size_t n, hipStream_t stream);
+// Host: out = coords + the reference's Gaussian backbone noise (host_noise.cpp).
+void backbone_noise_host(const float* coords, const uint8_t* atom_sources, int32_t L, float sigma, uint64_t seed,
+                         float* out);
 hipError_t launch_encoder(const ModelDev& m, const int32_t* idx, const float* mask, int L, int K,
                           float* h_v, float* h_e, const EncoderScratch& ws, hipStream_t stream);
 hipError_t launch_decoder_precompute(const ModelDev& m, const float* h_v, const float* h_e, int L,

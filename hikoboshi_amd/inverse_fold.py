@@ -1,0 +1,198 @@
+"""Python mirror of the reference's ``hikoboshi.inverse_fold`` (python/hikoboshi/inverse_fold.py)
+on the MI355X design path.
+
+Semantics follow the reference's algorithm layer (cpp/algorithms/inverse_fold.cpp:221-356):
+sample i uses seed + i for both its random decoding order and its sampler
+stream, ``sampling_temp <= 0`` means greedy, ``decode_order="n_to_c"`` uses the
+identity order for every sample, backbone noise (if > 0) perturbs the
+coordinates of each sample with that sample's seed before it is encoded, and
+``recovery_vs_native`` is the fraction of standard native residues the design
+reproduces. Without noise the backbone is encoded once and all samples are
+decoded in one batched call (value-identical to the per-sample loop).
+"""
+from __future__ import annotations
+
+from dataclasses import dataclass, field
+from pathlib import Path
+from typing import Any
+
+import numpy as np
+
+from . import _lib, design_io, pdb, weights
+from .backbone import ALPHABET, Backbone
+from .exceptions import FailedPreconditionError, HikoboshiError, InvalidArgumentError, from_status
+
+#: package id and aliases accepted for design (cpp/weights/provider.cpp:36-41), case-insensitive
+PACKAGE_ID = "proteinmpnn-v48-eps020"
+PACKAGE_ALIASES = (PACKAGE_ID, "v_48_020", "Hikoboshi-ProteinMPNN-v48-020", "proteinmpnn-v48-020", "proteinmpnn")
+#: the reference's other compiled packages, which resolve but are not design models
+OTHER_PACKAGES = ("hikoboshi-mpnn-d64", "mpnn64", "mpnn-64", "Hikoboshi-MPNN-64", "hikoboshi-esm2-8m", "esm2-8m",
+                  "esm2_8m", "Hikoboshi-ESM2-8M")
+UNKNOWN_PACKAGE = ("unknown Hikoboshi package id; available compiled package IDs/aliases: "
+                   "hikoboshi-mpnn-d64, mpnn64, mpnn-64, Hikoboshi-MPNN-64, hikoboshi-esm2-8m, esm2-8m, esm2_8m, "
+                   "Hikoboshi-ESM2-8M, proteinmpnn-v48-eps020, v_48_020, Hikoboshi-ProteinMPNN-v48-020, "
+                   "proteinmpnn-v48-020, proteinmpnn")
+STANDARD_AA = set("ACDEFGHIKLMNPQRSTVWY")
+
+
+@dataclass(frozen=True)
+class InverseFoldSequenceResult:
+    sequence: str
+    score: float
+    recovery_vs_native: float | None
+    seed: int
+    decode_order: str
+
+
+@dataclass(frozen=True)
+class InverseFoldLogProbsArtifact:
+    path: str
+    shape: tuple[int, int, int]
+    written: bool
+
+
+@dataclass(frozen=True)
+class InverseFoldResult:
+    sequences: tuple[InverseFoldSequenceResult, ...]
+    logprobs: InverseFoldLogProbsArtifact
+    #: [num_seqs, L, 21] temperature-scaled log-probs (not part of the reference's Python result)
+    log_prob_values: np.ndarray | None = field(default=None, compare=False, repr=False)
+
+
+def resolve_package(package: str | None) -> str:
+    """Package alias resolution and the design-model check (cpp/api/inverse_fold.cpp:95-128)."""
+    if package is None or package == "":
+        return PACKAGE_ID
+    low = str(package).lower()
+    if any(low == a.lower() for a in PACKAGE_ALIASES):
+        return PACKAGE_ID
+    if any(low == a.lower() for a in OTHER_PACKAGES):
+        raise InvalidArgumentError("inverse_fold requires proteinmpnn-v48-eps020; it does not use the aligner "
+                                   "hikoboshi-mpnn-d64 package")
+    raise InvalidArgumentError(UNKNOWN_PACKAGE)
+
+
+def parse_decode_order(text: str | None) -> str:
+    if text is None or text == "" or text == "random":
+        return "random"
+    if text in ("n_to_c", "n-to-c"):
+        return "n_to_c"
+    raise InvalidArgumentError("inverse_fold decode_order must be 'random' or 'n_to_c'")
+
+
+def recovery_vs_native(sequence: str, native: str | None) -> float | None:
+    """cpp/algorithms/inverse_fold.cpp:160-184 (None when no standard native residue is known)."""
+    if not native or len(native) < len(sequence):
+        return None
+    compared = matches = 0
+    for designed, nat in zip(sequence, native):
+        nat = nat.upper()
+        if nat not in STANDARD_AA:
+            continue
+        compared += 1
+        matches += designed.upper() == nat
+    return matches / compared if compared else None
+
+
+_CONTEXT: _lib.Context | None = None
+
+
+def _context() -> _lib.Context:
+    global _CONTEXT
+    if _CONTEXT is None:
+        _CONTEXT = _lib.Context(weights.read_package_bytes(), device=0)
+    return _CONTEXT
+
+
+def load_structure(structure: Any, chain_id: str | None = None) -> tuple[Backbone, str | None]:
+    """A PDB path, a Backbone, or a mapping with coords [L,5,3], atom_sources [L,5] and optional residue_codes."""
+    if isinstance(structure, Backbone):
+        return structure, structure.meta.get("residue_codes")
+    if isinstance(structure, dict):
+        bb = Backbone(np.asarray(structure["coords"], np.float32), np.asarray(structure["atom_sources"], np.uint8))
+        return bb, structure.get("residue_codes")
+    if isinstance(structure, (str, Path)):
+        path = Path(structure)
+        if not path.exists():
+            from .exceptions import UnavailableError
+            raise UnavailableError("structure file not readable")
+        return pdb.read_pdb(path, chain=chain_id)
+    raise InvalidArgumentError("structure must be a path, a Backbone or a coordinate mapping")
+
+
+def design(bb: Backbone, native: str | None, *, num_seqs: int = 1, sampling_temp: float = 0.1, seed: int = 0,
+           decode_order: str = "random", backbone_noise: float = 0.0, keep_log_probs: bool = True) -> InverseFoldResult:
+    """The algorithm-level design loop on a loaded backbone (validation order of inverse_fold.cpp:232-261)."""
+    L = bb.L
+    T = float(np.float32(sampling_temp))
+    noise = float(np.float32(backbone_noise))
+    if L == 0:
+        raise InvalidArgumentError("inverse-fold structure must contain at least one residue")
+    if num_seqs <= 0:
+        raise InvalidArgumentError("inverse-fold num_seqs must be greater than zero")
+    if not np.isfinite(T) or T < 0.0:
+        raise InvalidArgumentError("inverse-fold sampling_temp must be finite and >= 0")
+    if not np.isfinite(noise) or noise < 0.0:
+        raise InvalidArgumentError("inverse-fold backbone_noise must be finite and >= 0")
+    order = parse_decode_order(decode_order)
+    seeds = (np.uint64(seed) + np.arange(num_seqs, dtype=np.uint64)).astype(np.uint64)
+    mode = _lib.ORDER_N_TO_C if order == "n_to_c" else _lib.ORDER_RANDOM
+    ctx = _context()
+    try:
+        if noise > 0.0:
+            outs = []
+            for s in seeds:
+                coords = _lib.backbone_noise(bb.coords, bb.atom_sources, noise, int(s))
+                outs.append(ctx.design(coords, bb.atom_sources, 1, np.array([s], np.uint64), order_mode=mode,
+                                       order_seeds=np.array([s], np.uint64), temperature=T, greedy=T <= 0.0))
+            res = {k: np.concatenate([o[k] for o in outs]) for k in ("tokens", "log_probs", "scores")}
+        else:
+            res = ctx.design(bb.coords, bb.atom_sources, int(num_seqs), seeds, order_mode=mode, order_seeds=seeds,
+                             temperature=T, greedy=T <= 0.0)
+    except _lib.HkbsError as exc:
+        raise from_status(exc.code, exc.detail) from exc
+    seqs = []
+    for i in range(num_seqs):
+        s = "".join(ALPHABET[t] if 0 <= t < 21 else "X" for t in res["tokens"][i])
+        seqs.append(InverseFoldSequenceResult(sequence=s, score=float(np.float32(res["scores"][i])),
+                                              recovery_vs_native=recovery_vs_native(s, native), seed=int(seeds[i]),
+                                              decode_order=order))
+    values = res["log_probs"] if keep_log_probs else None
+    return InverseFoldResult(tuple(seqs), InverseFoldLogProbsArtifact("", (0, 0, 0), False), values)
+
+
+class InverseFoldNamespace:
+    def __call__(self, structure: Any, **kwargs: Any) -> InverseFoldResult:
+        return self.from_structure(structure, **kwargs)
+
+    def from_structure(self, structure: Any, *, num_seqs: int = 1, sampling_temp: float = 0.1, seed: int = 0,
+                       decode_order: str = "random", package: str | None = None, backbone_noise: float = 0.0,
+                       out_logprobs: str | None = None, chain_id: str | None = None, chain_index: int | None = None,
+                       pdb_model_id: str | None = None, pdb_model_index: int | None = None,
+                       **kwargs: Any) -> InverseFoldResult:
+        if kwargs:
+            raise InvalidArgumentError(f"inverse_fold.from_structure got unexpected keyword arguments: "
+                                       f"{', '.join(sorted(kwargs))}")
+        order = parse_decode_order(decode_order)
+        resolve_package(package)
+        bb, native = load_structure(structure, chain_id=chain_id)
+        result = design(bb, native, num_seqs=int(num_seqs), sampling_temp=float(sampling_temp), seed=int(seed),
+                        decode_order=order, backbone_noise=float(backbone_noise))
+        artifact = InverseFoldLogProbsArtifact("", (0, 0, 0), False)
+        if out_logprobs:
+            design_io.write_inverse_fold_logprobs_npz(out_logprobs, result.log_prob_values)
+            artifact = InverseFoldLogProbsArtifact(str(out_logprobs), tuple(result.log_prob_values.shape), True)
+        return InverseFoldResult(result.sequences, artifact, result.log_prob_values)
+
+    def from_pdb(self, structure: Any, **kwargs: Any) -> InverseFoldResult:
+        return self.from_structure(structure, **kwargs)
+
+    def from_cif(self, structure: Any, **kwargs: Any) -> InverseFoldResult:
+        return self.from_structure(structure, **kwargs)
+
+
+inverse_fold = InverseFoldNamespace()
+
+__all__ = ["InverseFoldNamespace", "inverse_fold", "InverseFoldResult", "InverseFoldSequenceResult",
+           "InverseFoldLogProbsArtifact", "design", "resolve_package", "parse_decode_order", "recovery_vs_native",
+           "HikoboshiError", "FailedPreconditionError"]

@@ -141,6 +141,14 @@ hkbs_status hkbs_pmpnn_score_batch(hkbs_pmpnn* ctx, int32_t n, const int64_t* of
 hkbs_status hkbs_pmpnn_decode_order(const float* chain_mask, const uint8_t* atom_sources,
                                     int32_t L, uint64_t seed, int32_t* order);
 
+/* Host helper: out[L,5,3] = coords + the reference's backbone noise for one
+ * sample (cpp/algorithms/inverse_fold.cpp:191-207, applied per sample with
+ * that sample's seed by the per-sample loop at :292-310): mt19937_64 seeded
+ * with seed ^ 0x4D504E4E76343875, std::normal_distribution<float>(0, sigma),
+ * x/y/z of every present atom in order. out may equal coords. */
+hkbs_status hkbs_pmpnn_backbone_noise(const float* coords, const uint8_t* atom_sources, int32_t L,
+                                      float sigma, uint64_t seed, float* out);
+
 /* Phase timing (instrumentation; no counterpart in the reference, which has
  * no design-path profiler). With timing enabled, each design call records
  * HIP events on the stream its kernels run on around three phases;

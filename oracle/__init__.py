@@ -212,7 +212,8 @@ class Reference:
             raise FileNotFoundError(f"{path} not built")
         lib = C.CDLL(str(path))
         lib.ref_set_weights.argtypes = [C.c_void_p]
-        for name in ("ref_inverse_fold", "ref_teacher_forced", "ref_algorithm_inverse_fold"):
+        for name in ("ref_inverse_fold", "ref_teacher_forced", "ref_algorithm_inverse_fold",
+                     "ref_algorithm_inverse_fold_ex", "ref_write_design_outputs"):
             getattr(lib, name).restype = C.c_int
         self.lib = lib
         self._t = _TensorTable(tensors)
@@ -271,3 +272,39 @@ class Reference:
                                                  _p(tokens, _i32p), _p(lp, _f32p), _p(scores, _f32p))
         assert st == 0, st
         return dict(tokens=tokens, log_probs=lp, scores=scores)
+
+    def algorithm_inverse_fold_ex(self, bb, num_seqs, seed, temperature, n_to_c=False, backbone_noise=0.0,
+                                  residue_codes=None):
+        """The reference's per-sample loop with backbone noise and native residue codes."""
+        L = bb.L
+        tokens = np.empty((num_seqs, L), np.int32)
+        lp = np.empty((num_seqs, L, V), np.float32)
+        scores = np.empty(num_seqs, np.float64)
+        rec = np.empty(num_seqs, np.float64)
+        rec_ok = np.empty(num_seqs, np.int32)
+        c, s = _f32(bb.coords), _u8(bb.atom_sources)
+        codes = None if residue_codes is None else C.create_string_buffer(residue_codes.encode(), L)
+        st = self.lib.ref_algorithm_inverse_fold_ex(
+            _p(c, _f32p), _p(s, _u8p), codes, C.c_int32(L), C.c_int32(num_seqs), C.c_uint64(seed),
+            C.c_float(temperature), C.c_int(int(n_to_c)), C.c_float(backbone_noise), _p(tokens, _i32p),
+            _p(lp, _f32p), scores.ctypes.data_as(C.c_void_p), rec.ctypes.data_as(C.c_void_p), _p(rec_ok, _i32p))
+        if st != 0:
+            raise ValueError(f"reference status {st}")
+        return dict(tokens=tokens, log_probs=lp, scores=scores,
+                    recovery=[float(r) if ok else None for r, ok in zip(rec, rec_ok)])
+
+    def write_design_outputs(self, fasta_path, npz_path, sequences, scores, seeds, n_to_c, temperature,
+                             log_probs=None):
+        """The reference's FASTA / NPZ writers (cpp/io/design_fasta_writer.cpp) on plain arrays."""
+        n = len(sequences)
+        L = len(sequences[0]) if n else 0
+        seq = C.create_string_buffer("".join(sequences).encode(), max(1, n * L))
+        sc = np.ascontiguousarray(scores, np.float64)
+        sd = np.ascontiguousarray(seeds, np.uint64)
+        lp = None if log_probs is None else np.ascontiguousarray(log_probs, np.float32)
+        st = self.lib.ref_write_design_outputs(
+            (fasta_path or "").encode(), (npz_path or "").encode(), C.c_int32(n), C.c_int32(L), seq,
+            sc.ctypes.data_as(C.c_void_p), sd.ctypes.data_as(C.c_void_p), C.c_int(int(n_to_c)),
+            C.c_float(temperature), None if lp is None else _p(lp, _f32p))
+        if st != 0:
+            raise ValueError(f"reference status {st}")

@@ -40,7 +40,8 @@ SRCS := \
   $(REF)/cpp/modules/mpnn/decode_order_scalar.cpp \
   $(REF)/cpp/modules/mpnn/sampler_scalar.cpp \
   $(REF)/cpp/modules/mpnn/inverse_fold_scalar.cpp \
-  $(REF)/cpp/algorithms/inverse_fold.cpp
+  $(REF)/cpp/algorithms/inverse_fold.cpp \
+  $(REF)/cpp/io/design_fasta_writer.cpp
 
 OBJS := $(patsubst $(REF)/cpp/%.cpp,$(OUT)/obj/%.o,$(SRCS)) $(OUT)/obj/ref_driver.o
 

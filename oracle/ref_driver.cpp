@@ -12,6 +12,8 @@
 // 136-286) without needing the generated blob translation unit.
 
 #include <hikoboshi/algorithms/inverse_fold.hpp>
+#include <hikoboshi/api/results.hpp>
+#include <hikoboshi/io/design_fasta_writer.hpp>
 #include <hikoboshi/modules/detail/mpnn_workspace.hpp>
 #include <hikoboshi/modules/mpnn/inverse_fold.hpp>
 #include <hikoboshi/modules/mpnn/proteinmpnn_decoder.hpp>
@@ -21,6 +23,7 @@
 #include <algorithm>
 #include <cstdint>
 #include <cstring>
+#include <string>
 #include <vector>
 
 namespace {
@@ -268,6 +271,77 @@ int ref_algorithm_inverse_fold(const float* coords, const std::uint8_t* atom_src
   }
   std::memcpy(log_probs, result.value.logprobs.values.data(),
               result.value.logprobs.values.size() * sizeof(float));
+  return 0;
+}
+
+// The algorithm-level loop with backbone noise and native residue codes (for
+// recovery_vs_native): recovery[i] = value, recovery_valid[i] = 0/1.
+int ref_algorithm_inverse_fold_ex(const float* coords, const std::uint8_t* atom_src, const char* residue_codes,
+                                  std::int32_t L, std::int32_t num_seqs, std::uint64_t seed, float temperature,
+                                  int n_to_c, float backbone_noise, std::int32_t* tokens, float* log_probs,
+                                  double* scores, double* recovery, std::int32_t* recovery_valid) {
+  const std::size_t n = static_cast<std::size_t>(L);
+  hikoboshi::algorithms::InverseFoldRequest req{};
+  req.structure.residue_count = n;
+  req.structure.coordinates = sp(coords, n * 15U);
+  req.structure.atom_sources = {reinterpret_cast<const hu::AtomSource*>(atom_src), n * 5U};
+  req.structure.residue_codes = {residue_codes, residue_codes ? n : 0};
+  req.structure.residues = {nullptr, 0};
+  req.weights = &g_weights;
+  req.options.sampling_temp = temperature;
+  req.options.num_seqs = static_cast<std::size_t>(num_seqs);
+  req.options.seed = seed;
+  req.options.decode_order = n_to_c ? hikoboshi::algorithms::InverseFoldDecodeOrder::NToC
+                                    : hikoboshi::algorithms::InverseFoldDecodeOrder::Random;
+  req.options.backbone_noise = backbone_noise;
+  req.options.keep_log_probs = true;
+  const auto result = hikoboshi::algorithms::inverse_fold_proteinmpnn_v48_020(req);
+  if (!result.status.ok()) return code(result.status);
+  static const char kAlphabet[] = "ACDEFGHIKLMNPQRSTVWYX";
+  for (std::size_t i = 0; i < result.value.sequences.size(); ++i) {
+    const auto& s = result.value.sequences[i];
+    scores[i] = s.score;
+    recovery[i] = s.recovery_vs_native.value;
+    recovery_valid[i] = s.recovery_vs_native.valid ? 1 : 0;
+    for (std::size_t r = 0; r < n; ++r) {
+      const char* hit = std::strchr(kAlphabet, s.sequence[r]);
+      tokens[i * n + r] = hit ? static_cast<std::int32_t>(hit - kAlphabet) : 20;
+    }
+  }
+  std::memcpy(log_probs, result.value.logprobs.values.data(),
+              result.value.logprobs.values.size() * sizeof(float));
+  return 0;
+}
+
+// The reference's FASTA and NPZ writers on a result assembled from plain
+// arrays: sequences [n][L] letters, scores [n], seeds [n]. An empty path
+// skips that writer.
+int ref_write_design_outputs(const char* fasta_path, const char* npz_path, std::int32_t num_seqs, std::int32_t L,
+                             const char* sequences, const double* scores, const std::uint64_t* seeds, int n_to_c,
+                             float temperature, const float* log_probs) {
+  hikoboshi::api::InverseFoldResult res{};
+  for (std::int32_t i = 0; i < num_seqs; ++i) {
+    hikoboshi::api::InverseFoldSequenceResult s{};
+    s.sequence.assign(sequences + static_cast<std::size_t>(i) * L, static_cast<std::size_t>(L));
+    s.score = scores[i];
+    s.seed = seeds[i];
+    s.decode_order = n_to_c ? hikoboshi::api::InverseFoldDecodeOrder::NToC : hikoboshi::api::InverseFoldDecodeOrder::Random;
+    res.sequences.push_back(std::move(s));
+  }
+  res.logprobs.num_seqs = static_cast<std::size_t>(num_seqs);
+  res.logprobs.residue_count = static_cast<std::size_t>(L);
+  res.logprobs.vocab_size = 21;
+  if (log_probs) res.logprobs.values.assign(log_probs, log_probs + static_cast<std::size_t>(num_seqs) * L * 21);
+  if (fasta_path && fasta_path[0]) {
+    hikoboshi::io::DesignFastaWriterOptions opt{};
+    opt.sampling_temp = temperature;
+    const hu::Status st = hikoboshi::io::write_design_fasta(fasta_path, res, opt);
+    if (!st.ok()) return code(st);
+  }
+  if (npz_path && npz_path[0]) {
+    const hu::Status st = hikoboshi::io::write_inverse_fold_logprobs_npz(npz_path, res);
+    if (!st.ok()) return code(st);
+  }
   return 0;
 }
 

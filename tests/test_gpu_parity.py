@@ -318,3 +318,54 @@ def test_teacher_forced_ragged_batch(gpu_ctx, oracle):
         assert scores[i] == pytest.approx(oscore, abs=1e-5)
     _say(f"  max|dlogp|={worst:.3g}")
     assert worst <= 1e-4
+
+
+# ------------------------------------------------------ entry-point glue --
+
+def test_inverse_fold_api_matches_algorithm_layer(oracle, tmp_path):
+    """hikoboshi_amd.inverse_fold: seed + i per sample for order and sampler, FASTA/NPZ artifacts."""
+    from hikoboshi_amd import design_io
+    from hikoboshi_amd import inverse_fold as ifold
+
+    case = golden_cases()[0]
+    path = FIXTURES / case["pdb"]
+    bb, native = pdb.read_pdb(path)
+    npz = tmp_path / "lp.npz"
+    _say(f"inverse_fold api {case['fixture_id']}")
+    res = ifold.inverse_fold(str(path), num_seqs=3, sampling_temp=0.1, seed=5, out_logprobs=str(npz))
+    assert [s.seed for s in res.sequences] == [5, 6, 7]
+    assert res.logprobs.written and res.logprobs.shape == (3, bb.L, 21)
+    with np.load(npz) as z:
+        np.testing.assert_array_equal(z["log_probs"], res.log_prob_values)
+    tokens = np.array([[backbone.ALPHABET.index(c) for c in s.sequence] for s in res.sequences], np.int32)
+    orders = np.stack([_lib.decode_order(bb.atom_sources, 5 + i) for i in range(3)])
+    check_design(oracle, bb, dict(tokens=tokens, log_probs=res.log_prob_values, orders=orders),
+                 np.arange(5, 8, dtype=np.uint64), 0.1)
+    for s in res.sequences:
+        assert s.recovery_vs_native == ifold.recovery_vs_native(s.sequence, native)
+    ref = oracle.algorithm_inverse_fold(bb, 3, 5, 0.1)
+    np.testing.assert_allclose([s.score for s in res.sequences], ref["scores"], atol=5e-5)
+    # the CLI, in process, writes the same designs
+    fa = tmp_path / "out.fasta"
+    from hikoboshi_amd.__main__ import main
+    assert main(["design", "--pdb", str(path), "--out", str(fa), "--num-seqs=3", "--seed", "5"]) == 0
+    assert fa.read_text() == design_io.design_fasta_text(res.sequences, 0.1)
+
+
+def test_inverse_fold_noise_and_n_to_c(oracle):
+    """Backbone noise: each sample is encoded from its own noised coordinates."""
+    from hikoboshi_amd import inverse_fold as ifold
+
+    bb = backbone.single_chain(70, 12)
+    _say("inverse_fold noise n_to_c")
+    res = ifold.design(bb, None, num_seqs=2, sampling_temp=0.2, seed=9, decode_order="n_to_c", backbone_noise=0.3)
+    for i, s in enumerate(res.sequences):
+        noisy = backbone.Backbone(_lib.backbone_noise(bb.coords, bb.atom_sources, 0.3, 9 + i), bb.atom_sources)
+        tokens = np.array([[backbone.ALPHABET.index(c) for c in s.sequence]], np.int32)
+        check_design(oracle, noisy, dict(tokens=tokens, log_probs=res.log_prob_values[i:i + 1],
+                                         orders=np.arange(70, dtype=np.int32)[None]),
+                     np.array([9 + i], np.uint64), 0.2)
+        assert s.decode_order == "n_to_c" and s.recovery_vs_native is None
+    g = ifold.design(bb, None, num_seqs=1, sampling_temp=0.0, seed=1)
+    ref = oracle.algorithm_inverse_fold(bb, 1, 1, 0.0)
+    assert g.sequences[0].sequence == "".join(backbone.ALPHABET[t] for t in ref["tokens"][0])
