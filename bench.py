@@ -47,6 +47,8 @@ def parse_args():
     p.add_argument("--num-seqs", type=int, default=64)
     p.add_argument("--temperature", type=float, default=0.1)
     p.add_argument("--seed", type=int, default=7)
+    p.add_argument("--precision", choices=("fp32", "bf16"), default="fp32",
+                   help="design arithmetic (bf16: bf16 weights and activations into the products)")
     p.add_argument("--cpu-sample", type=int, default=0,
                    help="sequences timed on the CPU baseline (default: one per worker process)")
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
@@ -170,6 +172,8 @@ def main() -> int:
     if cpu is not None and not np.array_equal(order, host_order):
         raise RuntimeError("decode order differs between the library and the oracle")
     ctx = _lib.Context(weights.read_package_bytes(), device=0)
+    if args.precision == "bf16":
+        ctx.set_precision(_lib.PRECISION_BF16)
 
     d_coords = hip.DeviceBuffer.from_array(bb.coords)
     d_src = hip.DeviceBuffer.from_array(bb.atom_sources)
@@ -215,7 +219,7 @@ def main() -> int:
     e_bw = int((pos[idx] < pos[:, None]).sum())
     bytes_step = 4.0 * (B * (3 * H * e_bw + L * (2 * H + V + 1)) + L * (2 * K + 1) * H + W_DEC) / L
     achieved = B * L * F_RES / (decode_ms * 1e-3) / 1e12
-    traffic, traffic_src = measured_traffic(f"design_L{L}_B{B}")
+    traffic, traffic_src = measured_traffic(f"design_L{L}_B{B}" + ("" if args.precision == "fp32" else "_bf16"))
     result = {
         "metric": METRIC,
         "value": round(B * L / (ms_per_step * 1e-3), 1),
@@ -227,10 +231,10 @@ def main() -> int:
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "f32",
+        "dtype": "f32" if args.precision == "fp32" else "bf16",
         "data": "synthetic",
         "config": {
-            "workload": f"design_L{L}_B{B}",
+            "workload": f"design_L{L}_B{B}" + ("" if args.precision == "fp32" else "_bf16"),
             "L": L, "num_seqs": B, "k_neighbors": K, "temperature": T,
             "backbone": f"NeRF ideal-geometry single chain, helix/strand segments, seed {args.seed}",
             "decode_order": f"shared random permutation (reference routine, seed {args.seed})",

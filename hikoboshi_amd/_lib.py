@@ -17,13 +17,14 @@ STATUS_NAMES = {
     0: "Ok", 1: "InvalidArgument", 2: "FailedPrecondition", 3: "Unavailable", 4: "Unimplemented", 5: "InternalError",
 }
 ORDER_RANDOM, ORDER_INPUT_PER_SEQUENCE, ORDER_INPUT_SHARED, ORDER_N_TO_C = range(4)
+PRECISION_FP32, PRECISION_BF16, PRECISION_FP16 = range(3)
 
 #: Symbols declared in include/hkbs_pmpnn.h.
 EXPORTS = (
     "hkbs_last_error", "hkbs_version", "hkbs_device_count", "hkbs_pmpnn_create", "hkbs_pmpnn_destroy",
     "hkbs_pmpnn_design", "hkbs_pmpnn_design_device", "hkbs_pmpnn_score", "hkbs_pmpnn_decode_order",
     "hkbs_pmpnn_knn", "hkbs_pmpnn_encode", "hkbs_pmpnn_edge_features", "hkbs_pmpnn_set_timing",
-    "hkbs_pmpnn_last_timing", "hkbs_pmpnn_score_batch", "hkbs_pmpnn_backbone_noise",
+    "hkbs_pmpnn_last_timing", "hkbs_pmpnn_score_batch", "hkbs_pmpnn_backbone_noise", "hkbs_pmpnn_set_precision",
 )
 
 
@@ -73,6 +74,8 @@ def load() -> C.CDLL:
     lib.hkbs_pmpnn_encode.argtypes = [_vp, _vp, _vp, _vp, _vp, _i32, _vp, _vp, _vp, _vp]
     lib.hkbs_pmpnn_edge_features.restype = _i32
     lib.hkbs_pmpnn_edge_features.argtypes = [_vp, _vp, _vp, _vp, _vp, _i32, _vp]
+    lib.hkbs_pmpnn_set_precision.restype = _i32
+    lib.hkbs_pmpnn_set_precision.argtypes = [_vp, _i32]
     lib.hkbs_pmpnn_set_timing.restype = _i32
     lib.hkbs_pmpnn_set_timing.argtypes = [_vp, _i32]
     lib.hkbs_pmpnn_last_timing.restype = _i32
@@ -211,6 +214,10 @@ class Context:
             self._h, coords_ptr, atom_sources_ptr, residue_indices_ptr, chain_labels_ptr, chain_mask_ptr,
             true_tokens_ptr, int(L), int(B), orders_ptr, int(shared), seeds_ptr, C.c_float(temperature),
             int(bool(greedy)), tokens_ptr, log_probs_ptr, scores_ptr, stream_ptr))
+
+    def set_precision(self, precision: int) -> None:
+        """PRECISION_FP32 (default), PRECISION_BF16 or PRECISION_FP16 for later design calls."""
+        check(self._lib.hkbs_pmpnn_set_precision(self._h, int(precision)))
 
     def set_timing(self, enable: bool) -> None:
         check(self._lib.hkbs_pmpnn_set_timing(self._h, int(bool(enable))))

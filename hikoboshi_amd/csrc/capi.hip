@@ -265,6 +265,42 @@ size_t pack_f16_split(HostArena& ar, const float* W, int N, int kin) {
   return off;
 }
 
+// fp32 -> bf16, round to nearest even (NaN stays NaN).
+uint16_t to_bf16(float f) {
+  uint32_t u = 0;
+  std::memcpy(&u, &f, 4);
+  if ((u & 0x7F800000u) == 0x7F800000u && (u & 0x7FFFFFu)) return static_cast<uint16_t>((u >> 16) | 0x40);
+  u += 0x7FFFu + ((u >> 16) & 1u);
+  return static_cast<uint16_t>(u >> 16);
+}
+
+// bf16 copy of n floats already packed at float offset src (same layout).
+size_t copy_bf16(HostArena& ar, size_t src, size_t n) {
+  const size_t off = ar.add((n + 1) / 2);
+  auto* dst = reinterpret_cast<uint16_t*>(ar.data.data() + off);
+  const float* s = ar.data.data() + src;
+  for (size_t i = 0; i < n; ++i) dst[i] = to_bf16(s[i]);
+  return off;
+}
+
+// fp16 copy of n floats already packed at float offset src (same layout).
+size_t copy_f16(HostArena& ar, size_t src, size_t n) {
+  const size_t off = ar.add((n + 1) / 2);
+  auto* dst = reinterpret_cast<_Float16*>(ar.data.data() + off);
+  const float* s = ar.data.data() + src;
+  for (size_t i = 0; i < n; ++i) dst[i] = static_cast<_Float16>(s[i]);
+  return off;
+}
+
+// bf16 of W [N][kin] as [kin / 8][N][8] (the B fragments of the 16x16x32 MFMA).
+size_t pack_bf16_k8(HostArena& ar, const float* W, int N, int kin) {
+  const size_t off = ar.add((size_t)N * kin / 2);
+  auto* dst = reinterpret_cast<uint16_t*>(ar.data.data() + off);
+  for (int n = 0; n < N; ++n)
+    for (int k = 0; k < kin; ++k) dst[((size_t)(k / 8) * N + n) * 8 + k % 8] = to_bf16(W[(size_t)n * kin + k]);
+  return off;
+}
+
 // Transposed: W [N][kin] columns [c0, c0 + kd) -> [kd][ldo] (first N columns used).
 size_t pack_t(HostArena& ar, const float* W, int N, int kin, int c0, int kd, int ldo) {
   const size_t off = ar.add((size_t)kd * ldo);
@@ -376,6 +412,7 @@ struct hkbs_pmpnn {
   hipEvent_t ev[4] = {nullptr, nullptr, nullptr, nullptr};
   uint32_t* fault = nullptr;  // device word raised by the last decode if a team barrier timed out
   DecodeArgs last_decode{};   // arguments of the last decode launch (for a one-workgroup rerun)
+  int precision = HKBS_PRECISION_FP32;
 };
 
 namespace {
@@ -395,9 +432,11 @@ hkbs_status build_model(hkbs_pmpnn* ctx, const float* const* t) {
   HostArena ar;
   struct Off {
     size_t pos_w, pos_b, edge_t, ne_g, ne_b, We_t, We_b, Ws;
-    size_t W1b_dec_p, W1d_dec_p, Wlog_t, blog;
+    size_t W1b_dec_p, W1d_dec_p, Wlog_t, blog, Wlog_h, Wlog_f;
     size_t enc[kLayers][22];
     size_t dec[kLayers][22];
+    size_t dec_h[kLayers][4];  // bf16 copies of W3_t, Win_t, Wout_t, W1da_t
+    size_t dec_f[kLayers][4];  // fp16 copies of the same
   } o{};
   o.pos_w = copy_raw(ar, t[0], 16 * 66);
   o.pos_b = copy_raw(ar, t[1], 16);
@@ -472,6 +511,7 @@ hkbs_status build_model(hkbs_pmpnn* ctx, const float* const* t) {
       q[6] = copy_raw(ar, T.data(), T.size());
     }
     q[20] = pack_f16_split(ar, d[2], 128, 128);       // W2 hi, lo (fp16)
+    q[21] = pack_bf16_k8(ar, d[2], 128, 128);         // W2 (bf16)
     q[16] = pack_k16(ar, {d[4]}, 128, 128, 0, 128);   // W3_p
     q[17] = pack_k16(ar, {d[10]}, 512, 128, 0, 128);  // Win_p
     q[18] = pack_k16(ar, {d[12]}, 128, 512, 0, 512);  // Wout_p
@@ -487,6 +527,14 @@ hkbs_status build_model(hkbs_pmpnn* ctx, const float* const* t) {
     } else {
       q[19] = 0;
     }
+    o.dec_h[l][0] = copy_bf16(ar, q[2], 128 * 128);  // W3_t
+    o.dec_h[l][1] = copy_bf16(ar, q[3], 128 * 512);  // Win_t
+    o.dec_h[l][2] = copy_bf16(ar, q[4], 512 * 128);  // Wout_t
+    o.dec_h[l][3] = copy_bf16(ar, q[5], 128 * 256);  // W1da_t
+    o.dec_f[l][0] = copy_f16(ar, q[2], 128 * 128);
+    o.dec_f[l][1] = copy_f16(ar, q[3], 128 * 512);
+    o.dec_f[l][2] = copy_f16(ar, q[4], 512 * 128);
+    o.dec_f[l][3] = copy_f16(ar, q[5], 128 * 256);
     q[7] = copy_raw(ar, d[1], 128);    // b1
     q[8] = copy_raw(ar, d[3], 128);    // b2
     q[9] = copy_raw(ar, d[5], 128);    // b3
@@ -496,6 +544,8 @@ hkbs_status build_model(hkbs_pmpnn* ctx, const float* const* t) {
   }
   o.Wlog_t = pack_t(ar, t[116], 21, 128, 0, 128, 32);
   o.blog = copy_raw(ar, t[117], 21, 32);
+  o.Wlog_h = copy_bf16(ar, o.Wlog_t, 128 * 32);
+  o.Wlog_f = copy_f16(ar, o.Wlog_t, 128 * 32);
 
   HK_CHECK(hipMalloc(&ctx->weights, ar.data.size() * sizeof(float)), "device allocation of weights failed");
   HK_CHECK(hipMemcpy(ctx->weights, ar.data.data(), ar.data.size() * sizeof(float), hipMemcpyHostToDevice),
@@ -543,6 +593,15 @@ hkbs_status build_model(hkbs_pmpnn* ctx, const float* const* t) {
     w.W2_p = B + q[1];
     w.W2h = B + q[20];
     w.W2l = B + q[20] + 128 * 128 / 2;
+    w.W2_b = reinterpret_cast<const uint16_t*>(B + q[21]);
+    w.W3_h = reinterpret_cast<const uint16_t*>(B + o.dec_h[l][0]);
+    w.Win_h = reinterpret_cast<const uint16_t*>(B + o.dec_h[l][1]);
+    w.Wout_h = reinterpret_cast<const uint16_t*>(B + o.dec_h[l][2]);
+    w.W1da_h = reinterpret_cast<const uint16_t*>(B + o.dec_h[l][3]);
+    w.W3_f = reinterpret_cast<const uint16_t*>(B + o.dec_f[l][0]);
+    w.Win_f = reinterpret_cast<const uint16_t*>(B + o.dec_f[l][1]);
+    w.Wout_f = reinterpret_cast<const uint16_t*>(B + o.dec_f[l][2]);
+    w.W1da_f = reinterpret_cast<const uint16_t*>(B + o.dec_f[l][3]);
     w.W3_t = B + q[2];
     w.Win_t = B + q[3];
     w.Wout_t = B + q[4];
@@ -566,6 +625,8 @@ hkbs_status build_model(hkbs_pmpnn* ctx, const float* const* t) {
   m.W1d_dec_p = B + o.W1d_dec_p;
   m.Wlog_t = B + o.Wlog_t;
   m.blog = B + o.blog;
+  m.Wlog_h = reinterpret_cast<const uint16_t*>(B + o.Wlog_h);
+  m.Wlog_f = reinterpret_cast<const uint16_t*>(B + o.Wlog_f);
   return HKBS_OK;
 }
 
@@ -722,6 +783,7 @@ hkbs_status design_on_device(hkbs_pmpnn* ctx, const float* coords, const uint8_t
   a.gsize = gsize;
   a.nbj = nbj;
   a.nbp = nbp;
+  a.precision = ctx->precision;
   ctx->last_decode = a;
   HK_CHECK(launch_decode_schedule(a, ctx->stream), "decode schedule launch failed");
   if (ctx->timing) HK_CHECK(hipEventRecord(ctx->ev[2], ctx->stream), "event record failed");
@@ -954,6 +1016,15 @@ hkbs_status hkbs_pmpnn_design_device(hkbs_pmpnn* ctx, const float* coords, const
                         shared_order != 0, sampler_seeds, temperature, greedy, tokens, log_probs, scores, ar, chosen);
   ctx->stream = saved;
   return st;
+}
+
+hkbs_status hkbs_pmpnn_set_precision(hkbs_pmpnn* ctx, int32_t precision) {
+  hkbs_status st = enter(ctx);
+  if (st != HKBS_OK) return st;
+  if (precision != HKBS_PRECISION_FP32 && precision != HKBS_PRECISION_BF16 && precision != HKBS_PRECISION_FP16)
+    return fail(HKBS_INVALID_ARGUMENT, "unknown precision");
+  ctx->precision = precision;
+  return HKBS_OK;
 }
 
 hkbs_status hkbs_pmpnn_set_timing(hkbs_pmpnn* ctx, int32_t enable) {

@@ -25,6 +25,7 @@
 #include <algorithm>
 #include <cstdlib>
 #include <cstring>
+#include <type_traits>
 
 #include "device_math.hpp"
 #include "pmpnn_internal.hpp"
@@ -41,6 +42,8 @@ constexpr int kPrmB1 = 0, kPrmB2 = 128, kPrmB3 = 256, kPrmBin = 384, kPrmBout = 
 constexpr int kPrmLog = kLayers * kPrmLayer;  // logits bias (32)
 constexpr int kPrmSize = kPrmLog + 32;
 typedef _Float16 half4 __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
 constexpr int kThreads = 512;
 
 constexpr int kGroup = 4;  // residues decoded together when independent
@@ -52,22 +55,46 @@ constexpr int kGroup = 4;  // residues decoded together when independent
 // step's reduction) is still running. fma() accumulates one part in input
 // order, store() leaves per-group partial sums in LDS (part >= 8192 floats),
 // and after a barrier sum() adds the groups of one output in a fixed order.
-template <int IN, int OUT, int NP = 1>
+constexpr int kPrecFp32 = 0, kPrecBf16 = 1, kPrecFp16 = 2;  // decode arithmetic (DecodeArgs.precision)
+
+template <int IN, int OUT, int NP = 1, int WT = kPrecFp32>
 struct Gemv {
   static constexpr int Q4 = OUT / 4;            // float4 columns
   static constexpr int GROUPS = kThreads / Q4;  // input groups
   static constexpr int PER = IN / GROUPS;       // inputs per group
   static constexpr int PP = PER / NP;           // inputs per part
   static_assert(GROUPS * OUT * kGroup <= 8192 && PP * NP == PER, "partial buffer");
+  // fp32 weights: one float4 per input; bf16 / fp16 weights: four 16-bit values (8 bytes) per input
+  using W4 = typename std::conditional<WT == kPrecFp32, float4, uint2>::type;
   struct Part {
-    float4 w[PP];
+    W4 w[PP];
   };
 
-  static __device__ inline void load(Part& P, const float* __restrict__ Wt, int k) {
+  static __device__ inline void load(Part& P, const void* __restrict__ Wt, int k) {
     const int q = threadIdx.x % Q4, grp = threadIdx.x / Q4;
-    const float* p = Wt + (size_t)(grp * PER + k * PP) * OUT + 4 * q;
+    const size_t at = (size_t)(grp * PER + k * PP) * OUT + 4 * q;
+    if constexpr (WT != kPrecFp32) {
+      const uint16_t* p = static_cast<const uint16_t*>(Wt) + at;
 #pragma unroll
-    for (int i = 0; i < PP; ++i) P.w[i] = *reinterpret_cast<const float4*>(p + (size_t)i * OUT);
+      for (int i = 0; i < PP; ++i) P.w[i] = *reinterpret_cast<const uint2*>(p + (size_t)i * OUT);
+    } else {
+      const float* p = static_cast<const float*>(Wt) + at;
+#pragma unroll
+      for (int i = 0; i < PP; ++i) P.w[i] = *reinterpret_cast<const float4*>(p + (size_t)i * OUT);
+    }
+  }
+  static __device__ inline float half_lo(uint32_t v) {
+    return static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(v & 0xFFFFu)));
+  }
+  static __device__ inline float4 widen(const W4& w) {
+    if constexpr (WT == kPrecBf16) {
+      return make_float4(__uint_as_float(w.x << 16), __uint_as_float(w.x & 0xFFFF0000u), __uint_as_float(w.y << 16),
+                         __uint_as_float(w.y & 0xFFFF0000u));
+    } else if constexpr (WT == kPrecFp16) {
+      return make_float4(half_lo(w.x), half_lo(w.x >> 16), half_lo(w.y), half_lo(w.y >> 16));
+    } else {
+      return w;
+    }
   }
   static __device__ inline void fma(const Part& P, int k, const float* X, int m, float4 (&acc)[kGroup]) {
     const int grp = threadIdx.x / Q4;
@@ -78,10 +105,11 @@ struct Gemv {
 #pragma unroll
       for (int p = 0; p < PP; ++p) {
         const float xv = x[p];
-        acc[i].x += xv * P.w[p].x;
-        acc[i].y += xv * P.w[p].y;
-        acc[i].z += xv * P.w[p].z;
-        acc[i].w += xv * P.w[p].w;
+        const float4 wv = widen(P.w[p]);
+        acc[i].x += xv * wv.x;
+        acc[i].y += xv * wv.y;
+        acc[i].z += xv * wv.z;
+        acc[i].w += xv * wv.w;
       }
     }
   }
@@ -100,12 +128,6 @@ struct Gemv {
     return s;
   }
 };
-
-using G3 = Gemv<kH, kH>;
-using GIn = Gemv<kH, kFF, 2>;
-using GOut = Gemv<kFF, kH, 2>;
-using GDa = Gemv<kH, 2 * kH>;
-using GLog = Gemv<kH, 32>;
 
 __device__ inline void zero4(float4 (&acc)[kGroup]) {
 #pragma unroll
@@ -196,8 +218,20 @@ __device__ inline bool team_sync(uint32_t* counter, uint32_t target, uint32_t sp
 // group. With P > 1 the grid is 8 * ceil(B / 8) * P workgroups and rank r of
 // sequence b runs as workgroup 8 (P (b / 8) + r) + b % 8, so that a team
 // shares one XCD when workgroups are dealt round-robin over the 8 XCDs; the
-// launch is cooperative, so every team member is resident.
+// whole grid fits the device at once.
+// PREC = kPrecFp32: fp32 weights, W2 product on the fp16 MFMA with hi/lo
+// operands (fp32-level accuracy). kPrecBf16 / kPrecFp16: 16-bit weights for
+// every product (GEMVs widen them to fp32 and accumulate in fp32), message rows
+// rounded to 16 bits for one 16x16x32 MFMA per k-block; activations,
+// LayerNorm and the sampler stay fp32.
+template <int PREC>
 __global__ __launch_bounds__(kThreads) void decode_kernel(ModelDev m, DecodeArgs a) {
+  constexpr bool BF = PREC == kPrecBf16, HF = PREC == kPrecFp16;
+  using G3 = Gemv<kH, kH, 1, PREC>;
+  using GIn = Gemv<kH, kFF, 2, PREC>;
+  using GOut = Gemv<kFF, kH, 2, PREC>;
+  using GDa = Gemv<kH, 2 * kH, 1, PREC>;
+  using GLog = Gemv<kH, 32, 1, PREC>;
   // message rows of two members as fp16 pairs: [member][hi, lo][row][kLdH]
   __shared__ __attribute__((aligned(16))) _Float16 G16[2 * 2 * kKmax * kLdH];
   __shared__ __attribute__((aligned(16))) float part[8192];
@@ -310,8 +344,8 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(ModelDev m, DecodeArgs
       }
       __syncthreads();
 
-      GLog::Part lg;  // logits weights in flight for the whole pass
-      GLog::load(lg, m.Wlog_t, 0);
+      typename GLog::Part lg;  // logits weights in flight for the whole pass
+      GLog::load(lg, (BF ? static_cast<const void*>(m.Wlog_h) : HF ? static_cast<const void*>(m.Wlog_f) : m.Wlog_t), 0);
       for (int l = 0; l < kLayers; ++l) {
         const DecLayerDev& w = m.dec[l];
         const float* Ql = a.Q + (size_t)l * L * kH;
@@ -319,18 +353,23 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(ModelDev m, DecodeArgs
         // W2 fragments of this wave's 16 columns stay in registers for all members.
         const int r = lane & 15, g = lane >> 4;
         const int col = wave * 16 + r;
-        // B fragments of the 16x16x32 fp16 MFMA: column col, k = 32 kb + 8 g + 0..7
+        // B fragments of the 16x16x32 MFMA: column col, k = 32 kb + 8 g + 0..7
         half8 bh[kH / 32], bl[kH / 32];
+        bf16x8 bb[kH / 32];
 #pragma unroll
         for (int kb = 0; kb < kH / 32; ++kb) {
           const size_t at = ((size_t)(4 * kb + g) * kH + col) * 4;  // float slots of 8 halves
-          bh[kb] = __builtin_bit_cast(half8, *reinterpret_cast<const float4*>(w.W2h + at));
-          bl[kb] = __builtin_bit_cast(half8, *reinterpret_cast<const float4*>(w.W2l + at));
+          if constexpr (BF) {
+            bb[kb] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const float4*>(w.W2_b + 2 * at));
+          } else {
+            bh[kb] = __builtin_bit_cast(half8, *reinterpret_cast<const float4*>(w.W2h + at));
+            if constexpr (!HF) bl[kb] = __builtin_bit_cast(half8, *reinterpret_cast<const float4*>(w.W2l + at));
+          }
         }
         const float* pl = prm + l * kPrmLayer;
         const float b2 = pl[kPrmB2 + col];
-        G3::Part g3;  // W3 in flight during the message rows and their product
-        G3::load(g3, w.W3_t, 0);
+        typename G3::Part g3;  // W3 in flight during the message rows and their product
+        G3::load(g3, (BF ? static_cast<const void*>(w.W3_h) : HF ? static_cast<const void*>(w.W3_f) : w.W3_t), 0);
         for (int i0 = 0; i0 < ml; i0 += 2) {
           {
             // Message rows g1 = GELU(A + E1_tk + (bw ? R : Q)_j) of members i0, i0 + 1;
@@ -367,19 +406,31 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(ModelDev m, DecodeArgs
                 float4 v = make_float4(gelu_fast(xv.x, tbl), gelu_fast(xv.y, tbl), gelu_fast(xv.z, tbl),
                                        gelu_fast(xv.w, tbl));
                 if (k >= K) v = make_float4(0.F, 0.F, 0.F, 0.F);
-                // split for the fp16 MFMA: v = hi + lo / 2048 to about 2^-22 relative
                 _Float16* gh = G16 + (((s / 3) * 2) * kKmax + k) * kLdH + c;
-                _Float16* gl = gh + kKmax * kLdH;
                 const float vv[4] = {v.x, v.y, v.z, v.w};
-                half4 hv, lv;
+                if constexpr (BF) {
+                  bf16x4 bv;
 #pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                  const float cl = __builtin_amdgcn_fmed3f(vv[e], -65504.0F, 65504.0F);
-                  hv[e] = static_cast<_Float16>(cl);
-                  lv[e] = static_cast<_Float16>((vv[e] - static_cast<float>(hv[e])) * 2048.0F);
+                  for (int e = 0; e < 4; ++e) bv[e] = static_cast<__bf16>(vv[e]);
+                  *reinterpret_cast<bf16x4*>(gh) = bv;
+                } else if constexpr (HF) {
+                  half4 hv;
+#pragma unroll
+                  for (int e = 0; e < 4; ++e) hv[e] = static_cast<_Float16>(__builtin_amdgcn_fmed3f(vv[e], -65504.0F, 65504.0F));
+                  *reinterpret_cast<half4*>(gh) = hv;
+                } else {
+                  // split for the fp16 MFMA: v = hi + lo / 2048 to about 2^-22 relative
+                  _Float16* gl = gh + kKmax * kLdH;
+                  half4 hv, lv;
+#pragma unroll
+                  for (int e = 0; e < 4; ++e) {
+                    const float cl = __builtin_amdgcn_fmed3f(vv[e], -65504.0F, 65504.0F);
+                    hv[e] = static_cast<_Float16>(cl);
+                    lv[e] = static_cast<_Float16>((vv[e] - static_cast<float>(hv[e])) * 2048.0F);
+                  }
+                  *reinterpret_cast<half4*>(gh) = hv;
+                  *reinterpret_cast<half4*>(gl) = lv;
                 }
-                *reinterpret_cast<half4*>(gh) = hv;
-                *reinterpret_cast<half4*>(gl) = lv;
               }
             }
           }
@@ -387,7 +438,7 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(ModelDev m, DecodeArgs
           for (int i = i0; i < ml && i < i0 + 2; ++i) {
             const _Float16* Gh = G16 + (i - i0) * 2 * kKmax * kLdH;
             const _Float16* Gl = Gh + kKmax * kLdH;
-            // W2 product as hi.hi + (hi.lo + lo.hi) / 2048 on the fp16 MFMA
+            // W2 product: hi.hi + (hi.lo + lo.hi) / 2048 on the fp16 MFMA, or bf16 x bf16
             floatx4 acc[3], cor[3];
 #pragma unroll
             for (int mb = 0; mb < 3; ++mb) {
@@ -399,17 +450,27 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(ModelDev m, DecodeArgs
 #pragma unroll
               for (int mb = 0; mb < 3; ++mb) {
                 const int at = (mb * 16 + r) * kLdH + 32 * kb + 8 * g;
-                const half8 ah = *reinterpret_cast<const half8*>(Gh + at);
-                const half8 al = *reinterpret_cast<const half8*>(Gl + at);
-                acc[mb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, bh[kb], acc[mb], 0, 0, 0);
-                cor[mb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, bl[kb], cor[mb], 0, 0, 0);
-                cor[mb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al, bh[kb], cor[mb], 0, 0, 0);
+                if constexpr (BF) {
+                  const bf16x8 ab = *reinterpret_cast<const bf16x8*>(Gh + at);
+                  acc[mb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ab, bb[kb], acc[mb], 0, 0, 0);
+                } else if constexpr (HF) {
+                  const half8 ah = *reinterpret_cast<const half8*>(Gh + at);
+                  acc[mb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, bh[kb], acc[mb], 0, 0, 0);
+                } else {
+                  const half8 ah = *reinterpret_cast<const half8*>(Gh + at);
+                  const half8 al = *reinterpret_cast<const half8*>(Gl + at);
+                  acc[mb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, bh[kb], acc[mb], 0, 0, 0);
+                  cor[mb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, bl[kb], cor[mb], 0, 0, 0);
+                  cor[mb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al, bh[kb], cor[mb], 0, 0, 0);
+                }
               }
             }
+            if constexpr (PREC == kPrecFp32) {
 #pragma unroll
-            for (int mb = 0; mb < 3; ++mb)
+              for (int mb = 0; mb < 3; ++mb)
 #pragma unroll
-              for (int e = 0; e < 4; ++e) acc[mb][e] += cor[mb][e] * (1.0F / 2048.0F);
+                for (int e = 0; e < 4; ++e) acc[mb][e] += cor[mb][e] * (1.0F / 2048.0F);
+            }
             // x[i][col] = sum over the member's K rows of GELU(acc + b2)
             float sum = 0.0F;
 #pragma unroll
@@ -431,8 +492,8 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(ModelDev m, DecodeArgs
         zero4(acc);
         G3::fma(g3, 0, x, ml, acc);
         G3::store(acc, ml, part);
-        GIn::Part in0;  // first half of W_in in flight during the reduction and LN1
-        GIn::load(in0, w.Win_t, 0);
+        typename GIn::Part in0;  // first half of W_in in flight during the reduction and LN1
+        GIn::load(in0, (BF ? static_cast<const void*>(w.Win_h) : HF ? static_cast<const void*>(w.Win_f) : w.Win_t), 0);
         __syncthreads();
         if (wave < ml) {
           float v[2];
@@ -448,13 +509,13 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(ModelDev m, DecodeArgs
         zero4(acc);
         GIn::fma(in0, 0, h1, ml, acc);
         {
-          GIn::Part in1;
-          GIn::load(in1, w.Win_t, 1);
+          typename GIn::Part in1;
+          GIn::load(in1, (BF ? static_cast<const void*>(w.Win_h) : HF ? static_cast<const void*>(w.Win_f) : w.Win_t), 1);
           GIn::fma(in1, 1, h1, ml, acc);
         }
         GIn::store(acc, ml, part);
-        GOut::Part out0;  // first half of W_out in flight during the reduction and GELU
-        GOut::load(out0, w.Wout_t, 0);
+        typename GOut::Part out0;  // first half of W_out in flight during the reduction and GELU
+        GOut::load(out0, (BF ? static_cast<const void*>(w.Wout_h) : HF ? static_cast<const void*>(w.Wout_f) : w.Wout_t), 0);
         __syncthreads();
         for (int task = threadIdx.x; task < ml * kFF; task += kThreads) {
           const int i = task / kFF, o = task % kFF;
@@ -465,15 +526,18 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(ModelDev m, DecodeArgs
         zero4(acc);
         GOut::fma(out0, 0, ff, ml, acc);
         {
-          GOut::Part out1;
-          GOut::load(out1, w.Wout_t, 1);
+          typename GOut::Part out1;
+          GOut::load(out1, (BF ? static_cast<const void*>(w.Wout_h) : HF ? static_cast<const void*>(w.Wout_f) : w.Wout_t), 1);
           GOut::fma(out1, 1, ff, ml, acc);
         }
         GOut::store(acc, ml, part);
         // The next layer's fused weights load during LN2. The last layer loads its
         // own (unused) instead: an unconditional load keeps the register budget.
-        GDa::Part da;
-        GDa::load(da, m.dec[l + 1 < kLayers ? l + 1 : l].W1da_t, 0);
+        typename GDa::Part da;
+        {
+          const DecLayerDev& nx = m.dec[l + 1 < kLayers ? l + 1 : l];
+          GDa::load(da, (BF ? static_cast<const void*>(nx.W1da_h) : HF ? static_cast<const void*>(nx.W1da_f) : nx.W1da_t), 0);
+        }
         __syncthreads();
         if (wave < ml) {
           float v[2];
@@ -699,14 +763,17 @@ hipError_t launch_decode_schedule(const DecodeArgs& a, hipStream_t stream) {
   return hipGetLastError();
 }
 
-hipError_t launch_decode(const ModelDev& m, const DecodeArgs& args, hipStream_t stream, int max_team) {
+namespace {
+
+template <int PREC>
+hipError_t launch_decode_as(const ModelDev& m, const DecodeArgs& args, hipStream_t stream, int max_team) {
   if (args.L <= 0 || args.B <= 0) return hipSuccess;
   DecodeArgs a = args;
   ModelDev mm = m;
   int dev = 0, cus = 0, per_cu = 0;
   hipError_t e = hipGetDevice(&dev);
   if (e == hipSuccess) e = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
-  if (e == hipSuccess) e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, decode_kernel, kThreads, 0);
+  if (e == hipSuccess) e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, decode_kernel<PREC>, kThreads, 0);
   if (e != hipSuccess) return e;
   const long resident = (long)cus * per_cu;
   const long teams_per_xcd = (a.B + 7) / 8;
@@ -722,7 +789,7 @@ hipError_t launch_decode(const ModelDev& m, const DecodeArgs& args, hipStream_t 
     const char* mode = std::getenv("HKBS_DECODE_LAUNCH");
     if (mode && std::strcmp(mode, "cooperative") == 0) {
       void* kargs[] = {&mm, &a};
-      e = hipLaunchCooperativeKernel(reinterpret_cast<const void*>(&decode_kernel), grid, dim3(kThreads), kargs, 0,
+      e = hipLaunchCooperativeKernel(reinterpret_cast<const void*>(&decode_kernel<PREC>), grid, dim3(kThreads), kargs, 0,
                                      stream);
       if (e == hipSuccess) return hipSuccess;
       (void)hipGetLastError();  // not launchable as a team here: one workgroup per sequence
@@ -731,13 +798,26 @@ hipError_t launch_decode(const ModelDev& m, const DecodeArgs& args, hipStream_t 
       // so on a device running nothing else every team is resident. Every
       // team barrier wait is bounded: a member that is not resident ends the
       // wait with the fault word raised instead of hanging.
-      decode_kernel<<<grid, kThreads, 0, stream>>>(mm, a);
+      decode_kernel<PREC><<<grid, kThreads, 0, stream>>>(mm, a);
       return hipGetLastError();
     }
   }
   a.team = 1;
-  decode_kernel<<<a.B, kThreads, 0, stream>>>(mm, a);
+  decode_kernel<PREC><<<a.B, kThreads, 0, stream>>>(mm, a);
   return hipGetLastError();
+}
+
+}  // namespace
+
+hipError_t launch_decode(const ModelDev& m, const DecodeArgs& args, hipStream_t stream, int max_team) {
+  switch (args.precision) {
+    case kPrecBf16:
+      return launch_decode_as<kPrecBf16>(m, args, stream, max_team);
+    case kPrecFp16:
+      return launch_decode_as<kPrecFp16>(m, args, stream, max_team);
+    default:
+      return launch_decode_as<kPrecFp32>(m, args, stream, max_team);
+  }
 }
 
 }  // namespace hkbs

@@ -43,6 +43,10 @@ struct DecLayerDev {
   const float* W2_p;   // kpack16 128 -> 128
   const float* W2h;    // [16][128][8] fp16: W2 = W2h + W2l / 2048 (decode loop)
   const float* W2l;
+  // bf16 copies for the bf16 decode (round to nearest even; same layouts as
+  // the fp32 t-layouts, W2 as [16][128][8] like W2h)
+  const uint16_t *W2_b, *W3_h, *Win_h, *Wout_h, *W1da_h;
+  const uint16_t *W3_f, *Win_f, *Wout_f, *W1da_f;  // fp16 copies (W2 in fp16 is W2h)
   const float* W3_t;   // [128][128]
   const float* Win_t;  // [128][512]
   const float* Wout_t; // [512][128]
@@ -68,8 +72,10 @@ struct ModelDev {
   DecLayerDev dec[kLayers];
   const float* W1b_dec_p;  // kpack16 128 -> 384: rows = [W1b_0; W1b_1; W1b_2] (decoder)
   const float* W1d_dec_p;  // kpack16 128 -> 512: rows = [W1d_0; W1d_1; W1d_2; W1a_0]
-  const float* Wlog_t;     // [128][21]
-  const float* blog;       // [21]
+  const float* Wlog_t;     // [128][32] (21 used)
+  const float* blog;       // [32] (21 used)
+  const uint16_t* Wlog_h;  // bf16 copy of Wlog_t
+  const uint16_t* Wlog_f;  // fp16 copy of Wlog_t
 };
 
 // Launchers (each enqueues on `stream`; shapes are validated by the caller).
@@ -127,6 +133,7 @@ struct DecodeArgs {
   uint32_t* fault;        // [1] set when a team barrier times out, zero at launch
   int team;               // workgroups per sequence (set by launch_decode)
   uint32_t spin_limit;    // polls before a team barrier gives up (set by launch_decode)
+  int precision;          // 0 fp32, 1 bf16, 2 fp16 weights and message rows (see decode_kernel)
 };
 // Group sizes and per-step neighbour lists (a.gsize, a.nbj, a.nbp) from the
 // orders, positions and kNN graph; launch_decode reads them.

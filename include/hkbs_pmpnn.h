@@ -62,6 +62,15 @@ enum {
   HKBS_ORDER_N_TO_C = 3
 };
 
+/* Arithmetic of the design path (hkbs_pmpnn_set_precision); the featurisation and
+ * encoder stay in the reference's fp32 rounding in every mode. */
+enum {
+  HKBS_PRECISION_FP32 = 0, /* default: log-probs within 1e-4 of the reference */
+  HKBS_PRECISION_BF16 = 1, /* bf16 weights and activations into the decoder's products, fp32
+                              accumulation, LayerNorm and softmax */
+  HKBS_PRECISION_FP16 = 2  /* the same with fp16 (three more significant bits than bf16) */
+};
+
 typedef struct hkbs_pmpnn hkbs_pmpnn;
 
 /* Static detail text of the calling thread's last non-OK status. */
@@ -148,6 +157,10 @@ hkbs_status hkbs_pmpnn_decode_order(const float* chain_mask, const uint8_t* atom
  * x/y/z of every present atom in order. out may equal coords. */
 hkbs_status hkbs_pmpnn_backbone_noise(const float* coords, const uint8_t* atom_sources, int32_t L,
                                       float sigma, uint64_t seed, float* out);
+
+/* Selects the arithmetic of later design and score calls on this context
+ * (no counterpart in the reference, which has only its fp32 scalar path). */
+hkbs_status hkbs_pmpnn_set_precision(hkbs_pmpnn* ctx, int32_t precision);
 
 /* Phase timing (instrumentation; no counterpart in the reference, which has
  * no design-path profiler). With timing enabled, each design call records
