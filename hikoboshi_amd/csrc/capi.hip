@@ -784,10 +784,12 @@ hkbs_status design_on_device(hkbs_pmpnn* ctx, const float* coords, const uint8_t
   a.nbj = nbj;
   a.nbp = nbp;
   a.precision = ctx->precision;
+  const int team = decode_team_size(a.precision, B, 8);
+  a.max_run = std::min(8, 4 * team);
   ctx->last_decode = a;
   HK_CHECK(launch_decode_schedule(a, ctx->stream), "decode schedule launch failed");
   if (ctx->timing) HK_CHECK(hipEventRecord(ctx->ev[2], ctx->stream), "event record failed");
-  HK_CHECK(launch_decode(ctx->model, a, ctx->stream), "decode launch failed");
+  HK_CHECK(launch_decode(ctx->model, a, ctx->stream, team), "decode launch failed");
   if (ctx->timing) {
     HK_CHECK(hipEventRecord(ctx->ev[3], ctx->stream), "event record failed");
     ctx->timed = true;
@@ -971,7 +973,10 @@ hkbs_status hkbs_pmpnn_design(hkbs_pmpnn* ctx, const float* coords, const uint8_
   if (fault) {
     // A team of workgroups could not run together (the device was busy with
     // other work): decode again with one workgroup per sequence.
-    HK_CHECK(launch_decode(ctx->model, ctx->last_decode, s, 1), "decode launch failed");
+    DecodeArgs one = ctx->last_decode;
+    one.max_run = 4;  // runs one workgroup can hold
+    HK_CHECK(launch_decode_schedule(one, s), "decode schedule launch failed");
+    HK_CHECK(launch_decode(ctx->model, one, s, 1), "decode launch failed");
     HK_CHECK(hipMemcpyAsync(tokens, d_tokens, (size_t)B * L * 4, hipMemcpyDeviceToHost, s), "D2H failed");
     if (log_probs) HK_CHECK(hipMemcpyAsync(log_probs, d_lp, (size_t)B * L * kV * 4, hipMemcpyDeviceToHost, s), "D2H failed");
     if (scores) HK_CHECK(hipMemcpyAsync(scores, d_scores, (size_t)B * 4, hipMemcpyDeviceToHost, s), "D2H failed");

@@ -46,7 +46,8 @@ typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
 constexpr int kThreads = 512;
 
-constexpr int kGroup = 4;  // residues decoded together when independent
+constexpr int kGroup = 4;   // residues one workgroup decodes together (sizes its LDS)
+constexpr int kMaxRun = 8;  // residues a team decodes together (at most kGroup per rank)
 
 // Y[i][o] = sum_p X[i][p] Wt[p][o] for i < m rows (m <= kGroup), OUT outputs
 // and IN inputs on all threads. Thread (q, grp) owns float4 column q and
@@ -206,7 +207,7 @@ __device__ inline bool team_sync(uint32_t* counter, uint32_t target, uint32_t sp
 }
 
 // Decodes one sequence per team of P workgroups (P = a.team, 1..4). Steps are
-// taken in groups of up to kGroup consecutive residues of the order in which
+// taken in groups of up to a.max_run (<= kGroup * P) consecutive residues of the order in which
 // no residue is a kNN neighbour of a later one: such residues do not read
 // each other's state, so they run together (bw for every member means
 // "decoded before the group"). Member i of a group runs on team rank i % P;
@@ -326,6 +327,11 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(ModelDev m, DecodeArgs
     // Group of consecutive independent steps (sizes precomputed per step).
     const int mg = gsize[step];
     const int ml = mg > rank ? (mg - rank + P - 1) / P : 0;  // members of this rank: rank + P i
+    if (ml > kGroup) {  // a schedule built for a larger team: refuse rather than overrun LDS
+      if (threadIdx.x == 0) __hip_atomic_store(a.fault, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      bad = 1;
+      break;
+    }
     if (ml > 0) {
       if (threadIdx.x < ml * K) {
         const int i = threadIdx.x / K, k = threadIdx.x % K;
@@ -701,13 +707,14 @@ __global__ void neighbour_schedule_kernel(const int32_t* __restrict__ orders, co
 // at a step in [s, that step) (decode_kernel decodes a group's members
 // together, so none may read another's state).
 __global__ void group_schedule_kernel(const int32_t* __restrict__ orders, const float* __restrict__ mask,
-                                      const int32_t* __restrict__ nbp, int L, int K, int32_t* __restrict__ gsize) {
+                                      const int32_t* __restrict__ nbp, int L, int K, int max_run,
+                                      int32_t* __restrict__ gsize) {
   const int q = blockIdx.y;
   const int s = blockIdx.x * blockDim.x + threadIdx.x;
   if (s >= L) return;
   const int32_t* order = orders + (size_t)q * L;
   const int32_t* np = nbp + (size_t)q * L * K;
-  int m = min(kGroup, L - s);
+  int m = min(max_run, L - s);
   for (int c = 1; c < m; ++c) {
     const int tc = order[s + c];
     bool stop = tc < 0 || tc >= L || mask[tc] == 0.0F;
@@ -759,28 +766,38 @@ hipError_t launch_decode_schedule(const DecodeArgs& a, hipStream_t stream) {
   neighbour_schedule_kernel<<<dim3((unsigned)std::min<size_t>((n + 255) / 256, 4096), nq), 256, 0, stream>>>(
       a.orders, a.pos, a.idx, a.L, a.K, a.nbj, a.nbp);
   group_schedule_kernel<<<dim3((unsigned)((a.L + 255) / 256), nq), 256, 0, stream>>>(a.orders, a.mask, a.nbp, a.L, a.K,
-                                                                                       a.gsize);
+                                                                                       a.max_run, a.gsize);
   return hipGetLastError();
 }
 
 namespace {
+
+// Workgroups per sequence: up to min(8, max_team, HKBS_DECODE_TEAM) while the
+// grid (8 * ceil(B / 8) * P workgroups, one per CU) fits the device at once.
+template <int PREC>
+int team_size_as(int B, int max_team) {
+  int dev = 0, cus = 0, per_cu = 0;
+  if (hipGetDevice(&dev) != hipSuccess ||
+      hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+      hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, decode_kernel<PREC>, kThreads, 0) != hipSuccess)
+    return 1;
+  const long resident = (long)cus * per_cu;
+  const long teams_per_xcd = (B + 7) / 8;
+  int P = std::max(1, std::min(8, max_team));
+  if (const char* env = std::getenv("HKBS_DECODE_TEAM")) P = std::max(1, std::min(P, std::atoi(env)));
+  while (P > 1 && 8 * teams_per_xcd * P > resident) --P;
+  return P;
+}
 
 template <int PREC>
 hipError_t launch_decode_as(const ModelDev& m, const DecodeArgs& args, hipStream_t stream, int max_team) {
   if (args.L <= 0 || args.B <= 0) return hipSuccess;
   DecodeArgs a = args;
   ModelDev mm = m;
-  int dev = 0, cus = 0, per_cu = 0;
-  hipError_t e = hipGetDevice(&dev);
-  if (e == hipSuccess) e = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
-  if (e == hipSuccess) e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, decode_kernel<PREC>, kThreads, 0);
-  if (e != hipSuccess) return e;
-  const long resident = (long)cus * per_cu;
   const long teams_per_xcd = (a.B + 7) / 8;
-  int P = std::max(1, std::min(4, max_team));
-  if (const char* env = std::getenv("HKBS_DECODE_TEAM")) P = std::max(1, std::min(P, std::atoi(env)));
-  while (P > 1 && 8 * teams_per_xcd * P > resident) --P;
+  int P = team_size_as<PREC>(a.B, max_team);
   if (!a.sync || !a.fault) P = 1;
+  if (a.max_run > kGroup * P) return hipErrorInvalidValue;  // the schedule assumed a larger team
   a.spin_limit = kSpinLimit;
   if (const char* env = std::getenv("HKBS_DECODE_SPIN_LIMIT")) a.spin_limit = (uint32_t)std::max(1, std::atoi(env));
   if (P > 1) {
@@ -789,10 +806,8 @@ hipError_t launch_decode_as(const ModelDev& m, const DecodeArgs& args, hipStream
     const char* mode = std::getenv("HKBS_DECODE_LAUNCH");
     if (mode && std::strcmp(mode, "cooperative") == 0) {
       void* kargs[] = {&mm, &a};
-      e = hipLaunchCooperativeKernel(reinterpret_cast<const void*>(&decode_kernel<PREC>), grid, dim3(kThreads), kargs, 0,
-                                     stream);
-      if (e == hipSuccess) return hipSuccess;
-      (void)hipGetLastError();  // not launchable as a team here: one workgroup per sequence
+      return hipLaunchCooperativeKernel(reinterpret_cast<const void*>(&decode_kernel<PREC>), grid, dim3(kThreads),
+                                        kargs, 0, stream);
     } else {
       // The whole grid fits the device at once (one workgroup per CU at most),
       // so on a device running nothing else every team is resident. Every
@@ -808,6 +823,17 @@ hipError_t launch_decode_as(const ModelDev& m, const DecodeArgs& args, hipStream
 }
 
 }  // namespace
+
+int decode_team_size(int precision, int B, int max_team) {
+  switch (precision) {
+    case kPrecBf16:
+      return team_size_as<kPrecBf16>(B, max_team);
+    case kPrecFp16:
+      return team_size_as<kPrecFp16>(B, max_team);
+    default:
+      return team_size_as<kPrecFp32>(B, max_team);
+  }
+}
 
 hipError_t launch_decode(const ModelDev& m, const DecodeArgs& args, hipStream_t stream, int max_team) {
   switch (args.precision) {

@@ -134,15 +134,20 @@ struct DecodeArgs {
   int team;               // workgroups per sequence (set by launch_decode)
   uint32_t spin_limit;    // polls before a team barrier gives up (set by launch_decode)
   int precision;          // 0 fp32, 1 bf16, 2 fp16 weights and message rows (see decode_kernel)
+  int max_run;            // longest run of independent steps decoded together (<= 4 * team size)
 };
 // Group sizes and per-step neighbour lists (a.gsize, a.nbj, a.nbp) from the
 // orders, positions and kNN graph; launch_decode reads them.
 hipError_t launch_decode_schedule(const DecodeArgs& a, hipStream_t stream);
-// Decodes with up to min(4, max_team) workgroups per sequence when the whole
-// grid fits the device at once, else one per sequence. A team launch that
-// could not run its members together raises *a.fault (and leaves NaN scores);
-// run it again with max_team = 1.
-hipError_t launch_decode(const ModelDev& m, const DecodeArgs& a, hipStream_t stream, int max_team = 4);
+// Workgroups per sequence the decode will use for B sequences (1..min(8, max_team)).
+int decode_team_size(int precision, int B, int max_team);
+// Decodes with up to min(8, max_team) workgroups per sequence when the whole
+// grid fits the device at once, else one per sequence; a.max_run must not
+// exceed 4 x that team size (the schedule has to be built for it). A team
+// launch that could not run its members together raises *a.fault (and leaves
+// NaN scores); rebuild the schedule with max_run = 4 and run it again with
+// max_team = 1.
+hipError_t launch_decode(const ModelDev& m, const DecodeArgs& a, hipStream_t stream, int max_team = 8);
 // Q[l] = W1d_l h^0 (l < 3), Q[3] = W1a_0 h^0, without the E1 edge products.
 hipError_t launch_q_precompute(const ModelDev& m, const float* h_v, int L, float* Q, hipStream_t stream);
 struct TfArgs {
