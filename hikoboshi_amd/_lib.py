@@ -1,4 +1,5 @@
-"""ctypes binding of the C ABI in include/hkbs_pmpnn.h (libhkbs_pmpnn.so).
+"""ctypes binding of the C ABI in include/hkbs_pmpnn.h and include/hkbs_structure.h
+(libhkbs_pmpnn.so).
 
 The product path has no fallback: if the HIP library is missing or no GPU is
 visible, calls raise HkbsError.
@@ -19,13 +20,28 @@ STATUS_NAMES = {
 ORDER_RANDOM, ORDER_INPUT_PER_SEQUENCE, ORDER_INPUT_SHARED, ORDER_N_TO_C = range(4)
 PRECISION_FP32, PRECISION_BF16, PRECISION_FP16 = range(3)
 
-#: Symbols declared in include/hkbs_pmpnn.h.
+#: Symbols declared in include/*.h.
 EXPORTS = (
     "hkbs_last_error", "hkbs_version", "hkbs_device_count", "hkbs_pmpnn_create", "hkbs_pmpnn_destroy",
     "hkbs_pmpnn_design", "hkbs_pmpnn_design_device", "hkbs_pmpnn_score", "hkbs_pmpnn_decode_order",
     "hkbs_pmpnn_knn", "hkbs_pmpnn_encode", "hkbs_pmpnn_edge_features", "hkbs_pmpnn_set_timing",
     "hkbs_pmpnn_last_timing", "hkbs_pmpnn_score_batch", "hkbs_pmpnn_backbone_noise", "hkbs_pmpnn_set_precision",
+    "hkbs_structure_default_options", "hkbs_structure_detect_format", "hkbs_structure_load_file",
+    "hkbs_structure_load_buffer", "hkbs_structure_free", "hkbs_structure_residue_count", "hkbs_structure_coords",
+    "hkbs_structure_atom_sources", "hkbs_structure_residue_codes", "hkbs_structure_model_index",
+    "hkbs_structure_text", "hkbs_structure_residue_name", "hkbs_structure_residue_numbering",
+    "hkbs_structure_chain_break_count", "hkbs_structure_chain_breaks",
 )
+FORMAT_UNKNOWN, FORMAT_PDB, FORMAT_MMCIF = range(3)
+TEXT_INPUT_ID, TEXT_SOURCE_FILENAME, TEXT_MODEL_ID, TEXT_CHAIN_ID, TEXT_ALTLOC_NOTE = range(5)
+
+
+class StructureOptions(C.Structure):
+    """hkbs_structure_options (include/hkbs_structure.h)."""
+
+    _fields_ = [("has_model_index", C.c_int32), ("model_index", C.c_int32), ("model_id", C.c_char_p),
+                ("chain_id", C.c_char_p), ("has_chain_index", C.c_int32), ("chain_index", C.c_uint64),
+                ("infer_missing_atoms", C.c_int32), ("include_modified_residues", C.c_int32)]
 
 
 class HkbsError(RuntimeError):
@@ -80,6 +96,35 @@ def load() -> C.CDLL:
     lib.hkbs_pmpnn_set_timing.argtypes = [_vp, _i32]
     lib.hkbs_pmpnn_last_timing.restype = _i32
     lib.hkbs_pmpnn_last_timing.argtypes = [_vp, _vp]
+    opts = C.POINTER(StructureOptions)
+    lib.hkbs_structure_default_options.argtypes = [opts]
+    lib.hkbs_structure_detect_format.restype = _i32
+    lib.hkbs_structure_detect_format.argtypes = [C.c_char_p, C.c_char_p, _sz]
+    lib.hkbs_structure_load_file.restype = _i32
+    lib.hkbs_structure_load_file.argtypes = [C.c_char_p, opts, C.POINTER(_vp)]
+    lib.hkbs_structure_load_buffer.restype = _i32
+    lib.hkbs_structure_load_buffer.argtypes = [C.c_char_p, _sz, _i32, C.c_char_p, opts, C.POINTER(_vp)]
+    lib.hkbs_structure_free.argtypes = [_vp]
+    lib.hkbs_structure_residue_count.restype = _sz
+    lib.hkbs_structure_residue_count.argtypes = [_vp]
+    lib.hkbs_structure_coords.restype = C.POINTER(C.c_float)
+    lib.hkbs_structure_coords.argtypes = [_vp]
+    lib.hkbs_structure_atom_sources.restype = C.POINTER(C.c_uint8)
+    lib.hkbs_structure_atom_sources.argtypes = [_vp]
+    lib.hkbs_structure_residue_codes.restype = C.c_char_p
+    lib.hkbs_structure_residue_codes.argtypes = [_vp]
+    lib.hkbs_structure_model_index.restype = _i32
+    lib.hkbs_structure_model_index.argtypes = [_vp]
+    lib.hkbs_structure_text.restype = C.c_char_p
+    lib.hkbs_structure_text.argtypes = [_vp, _i32]
+    lib.hkbs_structure_residue_name.restype = C.c_char_p
+    lib.hkbs_structure_residue_name.argtypes = [_vp, _sz]
+    lib.hkbs_structure_residue_numbering.restype = _i32
+    lib.hkbs_structure_residue_numbering.argtypes = [_vp, _vp, _vp, _vp]
+    lib.hkbs_structure_chain_break_count.restype = _sz
+    lib.hkbs_structure_chain_break_count.argtypes = [_vp]
+    lib.hkbs_structure_chain_breaks.restype = C.POINTER(C.c_uint64)
+    lib.hkbs_structure_chain_breaks.argtypes = [_vp]
     _lib = lib
     return lib
 

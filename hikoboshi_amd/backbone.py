@@ -190,3 +190,8 @@ WORKLOADS = {
     "complex_4x256_B256": dict(L=1024, B=256, temperature=0.2, seed=7, order="shared_random"),
     "long_L4000_B32": dict(L=4000, B=32, temperature=0.1, seed=7, order="shared_random"),
 }
+
+
+def sequence_to_tokens(seq: str) -> np.ndarray:
+    """One-letter codes -> ProteinMPNN token ids (anything outside the 20 standard letters -> 20, X)."""
+    return np.array([ALPHABET.index(c) if c in ALPHABET[:20] else 20 for c in seq], dtype=np.int32)

@@ -17,7 +17,8 @@ HERE = Path(__file__).resolve().parent
 CSRC = HERE / "csrc"
 LIB = HERE / "libhkbs_pmpnn.so"
 ARCH = os.environ.get("HKBS_OFFLOAD_ARCH", "gfx950")
-SOURCES = ["knn.hip", "features.hip", "encoder.hip", "decoder.hip", "decoder_tf.hip", "capi.hip", "host_noise.cpp"]
+SOURCES = ["knn.hip", "features.hip", "encoder.hip", "decoder.hip", "decoder_tf.hip", "capi.hip", "host_noise.cpp",
+           "structure_io.cpp"]
 # Host-only C++ (no device code), without floating-point contraction.
 HOST_FLAGS = ["-ffp-contract=off"]
 

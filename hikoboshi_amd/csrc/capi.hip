@@ -6,6 +6,7 @@
 // the host (bit-exact with the reference's libm-based routine), manage a
 // grow-only device workspace and enqueue the kernels on the context stream.
 #include "../../include/hkbs_pmpnn.h"
+#include "host_status.hpp"
 #include "pmpnn_internal.hpp"
 
 #include <hip/hip_runtime.h>
@@ -798,6 +799,8 @@ hkbs_status design_on_device(hkbs_pmpnn* ctx, const float* coords, const uint8_t
 }
 
 }  // namespace
+
+hkbs_status hkbs::report_error(hkbs_status code, const char* detail) { return fail(code, detail); }
 
 extern "C" {
 

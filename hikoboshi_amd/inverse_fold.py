@@ -12,15 +12,16 @@ decoded in one batched call (value-identical to the per-sample loop).
 """
 from __future__ import annotations
 
+import os
+import warnings
 from dataclasses import dataclass, field
-from pathlib import Path
 from typing import Any
 
 import numpy as np
 
-from . import _lib, design_io, pdb, weights
+from . import _lib, design_io, structure, weights
 from .backbone import ALPHABET, Backbone
-from .exceptions import FailedPreconditionError, HikoboshiError, InvalidArgumentError, from_status
+from .exceptions import FailedPreconditionError, HikoboshiError, InternalError, InvalidArgumentError, from_status
 
 #: package id and aliases accepted for design (cpp/weights/provider.cpp:36-41), case-insensitive
 PACKAGE_ID = "proteinmpnn-v48-eps020"
@@ -104,19 +105,49 @@ def _context() -> _lib.Context:
     return _CONTEXT
 
 
-def load_structure(structure: Any, chain_id: str | None = None) -> tuple[Backbone, str | None]:
-    """A PDB path, a Backbone, or a mapping with coords [L,5,3], atom_sources [L,5] and optional residue_codes."""
-    if isinstance(structure, Backbone):
-        return structure, structure.meta.get("residue_codes")
-    if isinstance(structure, dict):
-        bb = Backbone(np.asarray(structure["coords"], np.float32), np.asarray(structure["atom_sources"], np.uint8))
-        return bb, structure.get("residue_codes")
-    if isinstance(structure, (str, Path)):
-        path = Path(structure)
-        if not path.exists():
-            from .exceptions import UnavailableError
-            raise UnavailableError("structure file not readable")
-        return pdb.read_pdb(path, chain=chain_id)
+def _check_selection(chain_id, chain_index, pdb_model_id, pdb_model_index) -> None:
+    if chain_id is not None and chain_index is not None:
+        raise InvalidArgumentError("choose either chain_id or chain_index, not both")
+    if pdb_model_id is not None and pdb_model_index is not None:
+        raise InvalidArgumentError("choose either pdb_model_id or pdb_model_index, not both")
+    for name, value in (("chain_id", chain_id), ("pdb_model_id", pdb_model_id)):
+        if value is not None and not isinstance(value, str):
+            raise TypeError(f"{name} must be a string or None")
+
+
+def structure_options(chain_id: str | None = None, chain_index: int | None = None, pdb_model_id: str | None = None,
+                      pdb_model_index: int | None = None) -> structure.StructureLoadOptions:
+    """Selection keywords -> loader options, with the checks of python/hikoboshi/_chain_resolve.py:79-100 and
+    cpp/include/hikoboshi/bindings/engine_helpers.hpp:302-332 (empty strings leave a selection unset)."""
+    _check_selection(chain_id, chain_index, pdb_model_id, pdb_model_index)
+    for name, value in (("chain_index", chain_index), ("pdb_model_index", pdb_model_index)):
+        if value is not None and not isinstance(value, int):
+            raise InvalidArgumentError(f"{name} must be an int")
+    if chain_index is not None and chain_index < 0:
+        raise InternalError("can't convert negative int to unsigned")
+    if pdb_model_index is not None and not -2**63 <= pdb_model_index < 2**63:
+        raise InternalError("Python int too large to convert to C long")
+    model_index = None
+    if pdb_model_index is not None:  # narrowed to a C int like the reference binding
+        model_index = (int(pdb_model_index) + 2**31) % 2**32 - 2**31
+    return structure.StructureLoadOptions(model_index=model_index, model_id=pdb_model_id or "",
+                                          chain_id=chain_id or "",
+                                          chain_index=None if chain_index is None else int(chain_index) % 2**64)
+
+
+def load_structure(structure_arg: Any, options: structure.StructureLoadOptions | None = None,
+                   **selection: Any) -> tuple[Backbone, str | None]:
+    """A PDB / mmCIF path (loaded by the library's structure loader with the given selection), a Backbone,
+    or a mapping with coords [L,5,3], atom_sources [L,5] and optional residue_codes."""
+    if isinstance(structure_arg, Backbone):
+        return structure_arg, structure_arg.meta.get("residue_codes")
+    if isinstance(structure_arg, dict):
+        bb = Backbone(np.asarray(structure_arg["coords"], np.float32),
+                      np.asarray(structure_arg["atom_sources"], np.uint8))
+        return bb, structure_arg.get("residue_codes")
+    if isinstance(structure_arg, (str, os.PathLike)):
+        loaded = structure.load_structure_from_file(structure_arg, options or structure_options(**selection))
+        return loaded.backbone(), loaded.residue_codes
     raise InvalidArgumentError("structure must be a path, a Backbone or a coordinate mapping")
 
 
@@ -161,6 +192,24 @@ def design(bb: Backbone, native: str | None, *, num_seqs: int = 1, sampling_temp
     return InverseFoldResult(tuple(seqs), InverseFoldLogProbsArtifact("", (0, 0, 0), False), values)
 
 
+def _deprecated_model_kwargs(kwargs: dict, pdb_model_id: str | None,
+                             pdb_model_index: int | None) -> tuple[str | None, int | None]:
+    """model_id / model_index spellings (python/hikoboshi/_chain_resolve.py:30-61)."""
+    context = "inverse_fold.from_structure"
+    if "model_id" in kwargs:
+        if pdb_model_id is not None:
+            raise InvalidArgumentError(f"choose either pdb_model_id or deprecated model_id for {context}, not both")
+        pdb_model_id = kwargs.pop("model_id")
+        warnings.warn("model_id is deprecated; use pdb_model_id", DeprecationWarning, stacklevel=3)
+    if "model_index" in kwargs:
+        if pdb_model_index is not None:
+            raise InvalidArgumentError(f"choose either pdb_model_index or deprecated model_index for {context}, "
+                                       "not both")
+        pdb_model_index = kwargs.pop("model_index")
+        warnings.warn("model_index is deprecated; use pdb_model_index", DeprecationWarning, stacklevel=3)
+    return pdb_model_id, pdb_model_index
+
+
 class InverseFoldNamespace:
     def __call__(self, structure: Any, **kwargs: Any) -> InverseFoldResult:
         return self.from_structure(structure, **kwargs)
@@ -170,12 +219,17 @@ class InverseFoldNamespace:
                        out_logprobs: str | None = None, chain_id: str | None = None, chain_index: int | None = None,
                        pdb_model_id: str | None = None, pdb_model_index: int | None = None,
                        **kwargs: Any) -> InverseFoldResult:
+        """python/hikoboshi/inverse_fold.py:20-65 and the argument order of
+        cpp/bindings/inverse_fold_bindings.cpp:182-274 (decode order, structure selection and loading, then
+        the package)."""
+        pdb_model_id, pdb_model_index = _deprecated_model_kwargs(kwargs, pdb_model_id, pdb_model_index)
         if kwargs:
-            raise InvalidArgumentError(f"inverse_fold.from_structure got unexpected keyword arguments: "
-                                       f"{', '.join(sorted(kwargs))}")
+            raise InvalidArgumentError(f"unknown inverse_fold.from_structure keyword(s): {', '.join(sorted(kwargs))}")
+        _check_selection(chain_id, chain_index, pdb_model_id, pdb_model_index)
         order = parse_decode_order(decode_order)
+        bb, native = load_structure(structure, structure_options(chain_id, chain_index, pdb_model_id,
+                                                                 pdb_model_index))
         resolve_package(package)
-        bb, native = load_structure(structure, chain_id=chain_id)
         result = design(bb, native, num_seqs=int(num_seqs), sampling_temp=float(sampling_temp), seed=int(seed),
                         decode_order=order, backbone_noise=float(backbone_noise))
         artifact = InverseFoldLogProbsArtifact("", (0, 0, 0), False)
@@ -194,5 +248,6 @@ class InverseFoldNamespace:
 inverse_fold = InverseFoldNamespace()
 
 __all__ = ["InverseFoldNamespace", "inverse_fold", "InverseFoldResult", "InverseFoldSequenceResult",
-           "InverseFoldLogProbsArtifact", "design", "resolve_package", "parse_decode_order", "recovery_vs_native",
+           "InverseFoldLogProbsArtifact", "design", "resolve_package", "parse_decode_order", "recovery_vs_native", "load_structure",
+           "structure_options",
            "HikoboshiError", "FailedPreconditionError"]

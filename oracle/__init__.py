@@ -308,3 +308,72 @@ class Reference:
             C.c_float(temperature), None if lp is None else _p(lp, _f32p))
         if st != 0:
             raise ValueError(f"reference status {st}")
+
+    def load_structure(self, *, path=None, content=None, fmt="pdb", label="", model_index=None, model_id="",
+                       chain_id="", chain_index=None, infer=True, include_modified=True):
+        """The reference's structure loader (cpp/io/structure_loader.cpp:167-276): a file when ``path`` is
+        given, else ``content`` parsed as ``fmt`` ("pdb" / "mmcif"). Returns (status, detail, result dict or
+        None)."""
+        lib = self.lib
+        lib.ref_structure_load.restype = C.c_int
+        lib.ref_structure_load.argtypes = [C.c_int, C.c_char_p, C.c_char_p, C.c_size_t, C.c_char_p, C.c_int, C.c_int,
+                                           C.c_char_p, C.c_char_p, C.c_int, C.c_uint64, C.c_int, C.c_int,
+                                           C.POINTER(C.c_void_p), C.POINTER(C.c_char_p)]
+        lib.ref_structure_count.restype = C.c_size_t
+        lib.ref_structure_count.argtypes = [C.c_void_p]
+        lib.ref_structure_arrays.restype = C.c_size_t
+        lib.ref_structure_arrays.argtypes = [C.c_void_p] + [C.c_void_p] * 7
+        lib.ref_structure_text.restype = C.c_char_p
+        lib.ref_structure_text.argtypes = [C.c_void_p, C.c_size_t]
+        lib.ref_structure_model_index.argtypes = [C.c_void_p]
+        lib.ref_structure_free.argtypes = [C.c_void_p]
+        data = None if content is None else (content.encode() if isinstance(content, str) else bytes(content))
+        source = 0 if path is not None else (1 if fmt == "pdb" else 2)
+        h, detail = C.c_void_p(), C.c_char_p()
+        st = lib.ref_structure_load(source, None if path is None else str(path).encode(), data,
+                                    0 if data is None else len(data), label.encode(), int(model_index is not None),
+                                    int(model_index or 0), model_id.encode(), chain_id.encode(),
+                                    int(chain_index is not None), int(chain_index or 0), int(infer),
+                                    int(include_modified), C.byref(h), C.byref(detail))
+        msg = (detail.value or b"").decode()
+        if st != 0:
+            return st, msg, None
+        try:
+            L = int(lib.ref_structure_count(h))
+            coords = np.zeros((L, 5, 3), np.float32)
+            src = np.zeros((L, 5), np.uint8)
+            codes = C.create_string_buffer(max(L, 1))
+            numbers = np.zeros(L, np.int32)
+            icodes = np.zeros(L, np.uint8)
+            records = np.zeros(L, np.int64)
+            breaks = np.zeros(max(L, 1), np.uint64)
+            vp = lambda a: a.ctypes.data_as(C.c_void_p)  # noqa: E731
+            nb = lib.ref_structure_arrays(h, vp(coords), vp(src), C.cast(codes, C.c_void_p), vp(numbers), vp(icodes),
+                                          vp(records), vp(breaks))
+            text = [lib.ref_structure_text(h, f).decode("utf-8", "replace") for f in range(5)]
+            names = [lib.ref_structure_text(h, 5 + i).decode("utf-8", "replace") for i in range(L)]
+            out = dict(coords=coords, atom_sources=src, residue_codes=codes.raw[:L].decode(), residue_numbers=numbers,
+                       insertion_codes=icodes, source_record_indices=records,
+                       chain_breaks=tuple(int(b) for b in breaks[:nb]), input_id=text[0], source_filename=text[1],
+                       model_id=text[2], chain_id=text[3], altloc_note=text[4], residue_names=names,
+                       model_index=int(lib.ref_structure_model_index(h)))
+        finally:
+            lib.ref_structure_free(h)
+        return 0, msg, out
+
+    def detect_structure_format(self, path, content):
+        data = content.encode() if isinstance(content, str) else bytes(content)
+        self.lib.ref_detect_structure_format.argtypes = [C.c_char_p, C.c_char_p, C.c_size_t]
+        return {0: "unknown", 1: "pdb", 2: "mmcif"}[self.lib.ref_detect_structure_format(str(path).encode(), data,
+                                                                                           len(data))]
+
+    def residue_template(self):
+        out = np.zeros((5, 3), np.float32)
+        self.lib.ref_residue_template(out.ctypes.data_as(C.c_void_p))
+        return out
+
+    def virtual_cb(self, n, ca, c):
+        a = [np.ascontiguousarray(v, np.float32) for v in (n, ca, c)]
+        out = np.zeros(3, np.float32)
+        self.lib.ref_virtual_cb(*[v.ctypes.data_as(C.c_void_p) for v in a], out.ctypes.data_as(C.c_void_p))
+        return out

@@ -41,7 +41,16 @@ SRCS := \
   $(REF)/cpp/modules/mpnn/sampler_scalar.cpp \
   $(REF)/cpp/modules/mpnn/inverse_fold_scalar.cpp \
   $(REF)/cpp/algorithms/inverse_fold.cpp \
-  $(REF)/cpp/io/design_fasta_writer.cpp
+  $(REF)/cpp/io/design_fasta_writer.cpp \
+  $(REF)/cpp/io/pdb_parser.cpp \
+  $(REF)/cpp/io/mmcif_parser.cpp \
+  $(REF)/cpp/io/structure_normalize.cpp \
+  $(REF)/cpp/io/structure_atoms.cpp \
+  $(REF)/cpp/io/atom_inference.cpp \
+  $(REF)/cpp/io/atom_inference_kabsch.cpp \
+  $(REF)/cpp/io/virtual_cb.cpp \
+  $(REF)/cpp/io/residue_table.cpp \
+  $(REF)/cpp/io/structure_loader.cpp
 
 OBJS := $(patsubst $(REF)/cpp/%.cpp,$(OUT)/obj/%.o,$(SRCS)) $(OUT)/obj/ref_driver.o
 

@@ -13,7 +13,10 @@
 
 #include <hikoboshi/algorithms/inverse_fold.hpp>
 #include <hikoboshi/api/results.hpp>
+#include <hikoboshi/io/atom_inference.hpp>
 #include <hikoboshi/io/design_fasta_writer.hpp>
+#include <hikoboshi/io/residue_table.hpp>
+#include <hikoboshi/io/structure_loader.hpp>
 #include <hikoboshi/modules/detail/mpnn_workspace.hpp>
 #include <hikoboshi/modules/mpnn/inverse_fold.hpp>
 #include <hikoboshi/modules/mpnn/proteinmpnn_decoder.hpp>
@@ -343,6 +346,88 @@ int ref_write_design_outputs(const char* fasta_path, const char* npz_path, std::
     if (!st.ok()) return code(st);
   }
   return 0;
+}
+
+// ------------------------------------------------------------------------
+// The reference's structure loader (cpp/io/structure_loader.cpp) behind an
+// opaque handle. source: 0 = file at path, 1 = PDB text, 2 = mmCIF text.
+// Options follow StructureLoadOptions; returns the StatusCode value and sets
+// *detail to the status detail.
+int ref_structure_load(int source, const char* path, const char* content, std::size_t nbytes, const char* label,
+                       int has_model_index, int model_index, const char* model_id, const char* chain_id,
+                       int has_chain_index, std::uint64_t chain_index, int infer, int include_modified,
+                       void** out, const char** detail) {
+  namespace io = hikoboshi::io;
+  io::StructureLoadOptions opt{};
+  if (has_model_index) opt.model_index = model_index;
+  if (model_id) opt.model_id = model_id;
+  if (chain_id) opt.chain_id = chain_id;
+  if (has_chain_index) opt.chain_index = static_cast<std::size_t>(chain_index);
+  opt.infer_missing_atoms = infer != 0;
+  opt.include_modified_residues = include_modified != 0;
+  const std::string_view text(content ? content : "", content ? nbytes : 0);
+  const std::string_view origin(label ? label : "");
+  hu::Result<io::LoadedStructure> r = source == 0   ? io::load_structure_from_file(path, opt)
+                                      : source == 1 ? io::load_pdb_from_string(text, origin, opt)
+                                                    : io::load_mmcif_from_string(text, origin, opt);
+  *detail = r.status.detail ? r.status.detail : "";
+  *out = nullptr;
+  if (!r.status.ok()) return code(r.status);
+  *out = new io::LoadedStructure(std::move(r.value));
+  return 0;
+}
+
+void ref_structure_free(void* h) { delete static_cast<hikoboshi::io::LoadedStructure*>(h); }
+
+std::size_t ref_structure_count(void* h) { return static_cast<hikoboshi::io::LoadedStructure*>(h)->residue_count(); }
+
+// coords [L,5,3], sources [L,5], codes [L], numbers [L], icodes [L],
+// records [L] (source_record_index), breaks [n_breaks] (returns n_breaks).
+std::size_t ref_structure_arrays(void* h, float* coords, std::uint8_t* sources, char* codes, std::int32_t* numbers,
+                                 char* icodes, std::int64_t* records, std::uint64_t* breaks) {
+  const hu::StructureView v = static_cast<hikoboshi::io::LoadedStructure*>(h)->view();
+  std::memcpy(coords, v.coordinates.data, v.coordinates.size * sizeof(float));
+  for (std::size_t i = 0; i < v.atom_sources.size; ++i) sources[i] = static_cast<std::uint8_t>(v.atom_sources.data[i]);
+  for (std::size_t i = 0; i < v.residue_count; ++i) {
+    codes[i] = v.residue_codes.data[i];
+    numbers[i] = v.residues.data[i].residue_number;
+    icodes[i] = v.residues.data[i].insertion_code;
+    records[i] = v.residues.data[i].source_record_index;
+  }
+  if (breaks)
+    for (std::size_t i = 0; i < v.chain_breaks.size; ++i) breaks[i] = v.chain_breaks.data[i].after_residue_index;
+  return v.chain_breaks.size;
+}
+
+// 0 input id, 1 source filename, 2 selected model id, 3 selected chain id,
+// 4 altloc note, 5 + i: original residue name of residue i.
+const char* ref_structure_text(void* h, std::size_t field) {
+  static thread_local std::string buf;
+  const auto* s = static_cast<hikoboshi::io::LoadedStructure*>(h);
+  switch (field) {
+    case 0: buf = std::string(s->input_id()); break;
+    case 1: buf = std::string(s->source_filename()); break;
+    case 2: buf = std::string(s->selected_model_id()); break;
+    case 3: buf = std::string(s->selected_chain_id()); break;
+    case 4: buf = std::string(s->altloc_note()); break;
+    default: buf = std::string(s->view().residues.data[field - 5].original_residue_name);
+  }
+  return buf.c_str();
+}
+
+int ref_structure_model_index(void* h) { return static_cast<hikoboshi::io::LoadedStructure*>(h)->selected_model_index(); }
+
+int ref_detect_structure_format(const char* path, const char* content, std::size_t nbytes) {
+  return static_cast<int>(hikoboshi::io::detect_structure_format(path ? path : "", std::string_view(content ? content : "", content ? nbytes : 0)));
+}
+
+void ref_residue_template(float* out) {
+  const auto& t = hikoboshi::io::canonical_residue_template();
+  std::memcpy(out, t.coords.data(), t.coords.size() * sizeof(float));
+}
+
+void ref_virtual_cb(const float* n, const float* ca, const float* c, float* out) {
+  hikoboshi::io::glycine_virtual_cb(n, ca, c, out);
 }
 
 }  // extern "C"

@@ -9,7 +9,7 @@ the reference arithmetic and reports its own draw at every position).
 import numpy as np
 import pytest
 
-from hikoboshi_amd import _lib, backbone, pdb
+from hikoboshi_amd import _lib, backbone, structure
 
 from .conftest import FIXTURES, golden_cases
 
@@ -186,7 +186,7 @@ def test_design_small_lengths(gpu_ctx, oracle, L):
 
 @pytest.mark.parametrize("case", golden_cases()[:2], ids=lambda c: c["fixture_id"])
 def test_design_golden_structures(gpu_ctx, oracle, case):
-    bb, _ = pdb.read_pdb(FIXTURES / case["pdb"])
+    bb, _ = structure.read_backbone(FIXTURES / case["pdb"])
     seeds = np.array([case["seed"]], dtype=np.uint64)
     _say(f"design {case['fixture_id']}")
     res = gpu_ctx.design(bb.coords, bb.atom_sources, 1, seeds, order_mode=_lib.ORDER_N_TO_C,
@@ -263,8 +263,8 @@ def test_design_deterministic(gpu_ctx):
 @pytest.mark.parametrize("case", golden_cases(), ids=lambda c: c["fixture_id"])
 def test_teacher_forced_goldens(gpu_ctx, oracle, case):
     # tests/parity/proteinmpnn_v48_020/recovery_parity.py:78-176: 1e-4 vs upstream PyTorch, argmax exact
-    bb, seq = pdb.read_pdb(FIXTURES / case["pdb"])
-    tok = pdb.sequence_to_tokens(seq)
+    bb, seq = structure.read_backbone(FIXTURES / case["pdb"])
+    tok = backbone.sequence_to_tokens(seq)
     _say(f"teacher forced {case['fixture_id']}")
     lp, score = gpu_ctx.score(bb.coords, bb.atom_sources, tok)
     gold = np.asarray(case["teacher_log_probs"], np.float32).reshape(case["teacher_log_probs_shape"])
@@ -329,7 +329,7 @@ def test_inverse_fold_api_matches_algorithm_layer(oracle, tmp_path):
 
     case = golden_cases()[0]
     path = FIXTURES / case["pdb"]
-    bb, native = pdb.read_pdb(path)
+    bb, native = structure.read_backbone(path)
     npz = tmp_path / "lp.npz"
     _say(f"inverse_fold api {case['fixture_id']}")
     res = ifold.inverse_fold(str(path), num_seqs=3, sampling_temp=0.1, seed=5, out_logprobs=str(npz))
@@ -350,6 +350,30 @@ def test_inverse_fold_api_matches_algorithm_layer(oracle, tmp_path):
     from hikoboshi_amd.__main__ import main
     assert main(["design", "--pdb", str(path), "--out", str(fa), "--num-seqs=3", "--seed", "5"]) == 0
     assert fa.read_text() == design_io.design_fasta_text(res.sequences, 0.1)
+
+
+def test_inverse_fold_from_cif_selected_chain(oracle, tmp_path):
+    """An mmCIF file with two chains, atoms missing from the selected one: the loader's chain selection and
+    inference feed the design path, which matches the oracle on the loaded backbone."""
+    from hikoboshi_amd import inverse_fold as ifold
+
+    from .test_structure import records_from_pdb, to_mmcif
+
+    fix = sorted(FIXTURES.glob("*.pdb"))
+    recs = records_from_pdb(fix[2].read_text(), "A") + records_from_pdb(fix[3].read_text(), "B", drop_every=5)
+    path = tmp_path / "pair.cif"
+    path.write_text(to_mmcif([(1, recs)], np.random.default_rng(4)))
+    loaded = structure.load_structure_from_file(path, structure.StructureLoadOptions(chain_id="B"))
+    bb = loaded.backbone()
+    assert (bb.atom_sources == 2).any()
+    _say(f"inverse_fold from_cif chain B L={bb.L}")
+    res = ifold.inverse_fold.from_cif(str(path), chain_id="B", num_seqs=2, sampling_temp=0.1, seed=3)
+    tokens = np.array([[backbone.ALPHABET.index(c) for c in s.sequence] for s in res.sequences], np.int32)
+    orders = np.stack([_lib.decode_order(bb.atom_sources, 3 + i) for i in range(2)])
+    check_design(oracle, bb, dict(tokens=tokens, log_probs=res.log_prob_values, orders=orders),
+                 np.arange(3, 5, dtype=np.uint64), 0.1)
+    for s in res.sequences:
+        assert s.recovery_vs_native == ifold.recovery_vs_native(s.sequence, loaded.residue_codes)
 
 
 def test_inverse_fold_noise_and_n_to_c(oracle):

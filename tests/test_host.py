@@ -5,7 +5,7 @@ import re
 import numpy as np
 import pytest
 
-from hikoboshi_amd import _lib, backbone, pdb, weights
+from hikoboshi_amd import _lib, backbone, structure, weights
 
 from .conftest import FIXTURES, ROOT, golden_cases
 
@@ -74,13 +74,13 @@ def test_ragged_batch():
 
 @pytest.mark.parametrize("case", golden_cases(), ids=lambda c: c["fixture_id"])
 def test_pdb_reader(case):
-    bb, seq = pdb.read_pdb(FIXTURES / case["pdb"])
+    bb, seq = structure.read_backbone(FIXTURES / case["pdb"])
     assert seq == case["native_sequence"] and bb.L == case["residue_count"]
     assert (bb.atom_sources != 0).all()
 
 
 def _declared_functions():
-    text = (ROOT / "include" / "hkbs_pmpnn.h").read_text()
+    text = "".join(h.read_text() for h in sorted((ROOT / "include").glob("*.h")))
     return sorted(set(re.findall(r"\b(hkbs_\w+)\s*\(", text)))
 
 

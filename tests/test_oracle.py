@@ -10,7 +10,7 @@ import math
 import numpy as np
 import pytest
 
-from hikoboshi_amd import backbone, pdb
+from hikoboshi_amd import backbone, structure
 from hikoboshi_amd.backbone import ALPHABET
 
 from .conftest import FIXTURES, golden_cases
@@ -112,9 +112,9 @@ def test_knn_bit_exact_vs_reference(oracle, reference):
 def test_teacher_forced_matches_pytorch_goldens(oracle, case):
     # tests/parity/proteinmpnn_v48_020/recovery_parity.py:78-176: log-probs within 1e-4,
     # teacher argmax sequence exact.
-    bb, seq = pdb.read_pdb(FIXTURES / case["pdb"])
+    bb, seq = structure.read_backbone(FIXTURES / case["pdb"])
     assert seq == case["native_sequence"]
-    lp, score = oracle.teacher_forced(bb, pdb.sequence_to_tokens(seq))
+    lp, score = oracle.teacher_forced(bb, backbone.sequence_to_tokens(seq))
     gold = np.asarray(case["teacher_log_probs"], np.float32).reshape(case["teacher_log_probs_shape"])
     assert np.abs(lp - gold).max() <= 1e-4
     argmax = "".join(ALPHABET[i] for i in lp.argmax(1))
@@ -124,8 +124,8 @@ def test_teacher_forced_matches_pytorch_goldens(oracle, case):
 
 @pytest.mark.parametrize("case", golden_cases(), ids=lambda c: c["fixture_id"])
 def test_teacher_forced_bit_exact_vs_reference(oracle, reference, case):
-    bb, seq = pdb.read_pdb(FIXTURES / case["pdb"])
-    tok = pdb.sequence_to_tokens(seq)
+    bb, seq = structure.read_backbone(FIXTURES / case["pdb"])
+    tok = backbone.sequence_to_tokens(seq)
     a = oracle.teacher_forced(bb, tok)
     b = reference.teacher_forced(bb, tok)
     np.testing.assert_array_equal(a[0], b[0])
