@@ -30,7 +30,8 @@ EXPORTS = (
     "hkbs_structure_load_buffer", "hkbs_structure_free", "hkbs_structure_residue_count", "hkbs_structure_coords",
     "hkbs_structure_atom_sources", "hkbs_structure_residue_codes", "hkbs_structure_model_index",
     "hkbs_structure_text", "hkbs_structure_residue_name", "hkbs_structure_residue_numbering",
-    "hkbs_structure_chain_break_count", "hkbs_structure_chain_breaks",
+    "hkbs_structure_chain_break_count", "hkbs_structure_chain_breaks", "hkbs_structure_chain_count",
+    "hkbs_structure_chain_name", "hkbs_structure_chain_labels",
 )
 FORMAT_UNKNOWN, FORMAT_PDB, FORMAT_MMCIF = range(3)
 TEXT_INPUT_ID, TEXT_SOURCE_FILENAME, TEXT_MODEL_ID, TEXT_CHAIN_ID, TEXT_ALTLOC_NOTE = range(5)
@@ -41,7 +42,8 @@ class StructureOptions(C.Structure):
 
     _fields_ = [("has_model_index", C.c_int32), ("model_index", C.c_int32), ("model_id", C.c_char_p),
                 ("chain_id", C.c_char_p), ("has_chain_index", C.c_int32), ("chain_index", C.c_uint64),
-                ("infer_missing_atoms", C.c_int32), ("include_modified_residues", C.c_int32)]
+                ("infer_missing_atoms", C.c_int32), ("include_modified_residues", C.c_int32),
+                ("chain_ids", C.POINTER(C.c_char_p)), ("n_chain_ids", C.c_size_t), ("all_chains", C.c_int32)]
 
 
 class HkbsError(RuntimeError):
@@ -125,6 +127,12 @@ def load() -> C.CDLL:
     lib.hkbs_structure_chain_break_count.argtypes = [_vp]
     lib.hkbs_structure_chain_breaks.restype = C.POINTER(C.c_uint64)
     lib.hkbs_structure_chain_breaks.argtypes = [_vp]
+    lib.hkbs_structure_chain_count.restype = _sz
+    lib.hkbs_structure_chain_count.argtypes = [_vp]
+    lib.hkbs_structure_chain_name.restype = C.c_char_p
+    lib.hkbs_structure_chain_name.argtypes = [_vp, _sz]
+    lib.hkbs_structure_chain_labels.restype = _i32
+    lib.hkbs_structure_chain_labels.argtypes = [_vp, _vp]
     _lib = lib
     return lib
 

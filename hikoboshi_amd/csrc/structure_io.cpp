@@ -32,6 +32,7 @@
 #include <sstream>
 #include <string>
 #include <string_view>
+#include <tuple>
 #include <utility>
 #include <vector>
 
@@ -44,6 +45,8 @@ struct hkbs_structure {
   std::vector<char> icodes;
   std::vector<int64_t> first_records;
   std::vector<uint64_t> breaks;
+  std::vector<int32_t> labels;      // chain of each residue (index into chains)
+  std::vector<std::string> chains;  // selected chains in output order
   std::string input_id, model_id, chain_id, altloc_note;
   int32_t model_index = 0;
 };
@@ -387,19 +390,36 @@ struct Options {
   std::optional<int32_t> model_index;
   std::string model_id, chain_id;
   std::optional<uint64_t> chain_index;
+  std::optional<std::vector<std::string>> chain_list;  // several chains, in this order
+  bool all_chains = false;
   bool infer = true, include_modified = true;
 };
 
-Options read_options(const hkbs_structure_options* o) {
-  Options r;
-  if (o == nullptr) return r;
+Status read_options(const hkbs_structure_options* o, Options& r) {
+  if (o == nullptr) return {};
   if (o->has_model_index) r.model_index = o->model_index;
   if (o->model_id) r.model_id = o->model_id;
   if (o->chain_id) r.chain_id = o->chain_id;
   if (o->has_chain_index) r.chain_index = o->chain_index;
   r.infer = o->infer_missing_atoms != 0;
   r.include_modified = o->include_modified_residues != 0;
-  return r;
+  r.all_chains = o->all_chains != 0;
+  if (o->n_chain_ids > 0) {
+    if (o->chain_ids == nullptr) return invalid("chain_ids must be non-null when n_chain_ids > 0");
+    std::vector<std::string> ids;
+    for (size_t i = 0; i < o->n_chain_ids; ++i) {
+      if (o->chain_ids[i] == nullptr) return invalid("chain_ids entries must be non-null");
+      if (std::find(ids.begin(), ids.end(), o->chain_ids[i]) != ids.end()) return invalid("chain ids must be distinct");
+      ids.emplace_back(o->chain_ids[i]);
+    }
+    r.chain_list = std::move(ids);
+  }
+  // chain_id over chain_index is the reference's own precedence; the chain
+  // lists exclude both.
+  const int selections =
+      (!r.chain_id.empty() || r.chain_index.has_value()) + r.chain_list.has_value() + r.all_chains;
+  if (selections > 1) return invalid("choose one chain selection: chain_id, chain_index, chain_ids or all_chains");
+  return {};
 }
 
 struct Residue {
@@ -447,30 +467,44 @@ Status normalize(const std::vector<AtomRecord>& recs, const Options& opt, hkbs_s
     if (r.model == model && polymer_atom(r, opt.include_modified) &&
         std::find(chains.begin(), chains.end(), r.chain) == chains.end())
       chains.push_back(r.chain);
-  if (!opt.chain_id.empty()) {
-    if (std::find(chains.begin(), chains.end(), opt.chain_id) == chains.end())
-      return invalid("requested chain id not present in selected model");
-    s.chain_id = opt.chain_id;
+  const auto present = [&](const std::string& c) { return std::find(chains.begin(), chains.end(), c) != chains.end(); };
+  if (opt.chain_list) {
+    for (const std::string& c : *opt.chain_list)
+      if (!present(c)) return invalid("requested chain id not present in selected model");
+    s.chains = *opt.chain_list;
+  } else if (opt.all_chains) {
+    if (chains.empty()) return invalid("selected model has no polymer chains");
+    s.chains = chains;
+  } else if (!opt.chain_id.empty()) {
+    if (!present(opt.chain_id)) return invalid("requested chain id not present in selected model");
+    s.chains = {opt.chain_id};
   } else if (opt.chain_index) {
     if (*opt.chain_index >= chains.size()) return invalid("requested chain index out of range");
-    s.chain_id = chains[*opt.chain_index];
-  } else if (std::find(chains.begin(), chains.end(), "A") != chains.end()) {
-    s.chain_id = "A";
+    s.chains = {chains[*opt.chain_index]};
+  } else if (present("A")) {
+    s.chains = {"A"};
   } else if (!chains.empty()) {
-    s.chain_id = chains.front();
+    s.chains = {chains.front()};
   } else {
     return invalid("selected model has no polymer chains");
   }
+  // The chain text field: the chain id, or the selected ids joined by commas.
+  for (size_t c = 0; c < s.chains.size(); ++c) s.chain_id += (c ? "," : "") + s.chains[c];
 
-  // Residues keyed by (number, insertion code) in order of first appearance;
-  // records arrive in file order, so creation order is file order.
-  std::map<std::pair<int32_t, char>, size_t> slot_of;
+  // Residues keyed by (chain, number, insertion code) in order of first
+  // appearance; records arrive in file order, so creation order is file
+  // order. Several chains are then grouped in the selected chain order.
+  std::map<std::tuple<size_t, int32_t, char>, size_t> slot_of;
+  std::vector<size_t> chain_of;
   bool altloc_used = false;
   for (const AtomRecord& r : recs) {
-    if (r.model != model || r.chain != s.chain_id || !polymer_atom(r, opt.include_modified)) continue;
-    const auto key = std::make_pair(r.residue_number, r.icode);
+    if (r.model != model || !polymer_atom(r, opt.include_modified)) continue;
+    const auto ch = std::find(s.chains.begin(), s.chains.end(), r.chain);
+    if (ch == s.chains.end()) continue;
+    const auto key = std::make_tuple(static_cast<size_t>(ch - s.chains.begin()), r.residue_number, r.icode);
     auto it = slot_of.find(key);
     if (it == slot_of.end()) {
+      chain_of.push_back(std::get<0>(key));
       Residue res;
       res.code = residue_code(r.residue);
       res.name = r.residue;
@@ -492,10 +526,26 @@ Status normalize(const std::vector<AtomRecord>& recs, const Options& opt, hkbs_s
     res.chosen[a] = r.altloc;
   }
   if (residues.empty()) return invalid("selected chain has no accepted amino-acid residues");
+  if (s.chains.size() > 1) {
+    std::vector<size_t> perm(residues.size());
+    for (size_t i = 0; i < perm.size(); ++i) perm[i] = i;
+    std::stable_sort(perm.begin(), perm.end(), [&](size_t a, size_t b) { return chain_of[a] < chain_of[b]; });
+    std::vector<Residue> grouped;
+    std::vector<size_t> grouped_chain;
+    for (size_t i : perm) {
+      grouped.push_back(std::move(residues[i]));
+      grouped_chain.push_back(chain_of[i]);
+    }
+    residues.swap(grouped);
+    chain_of.swap(grouped_chain);
+  }
+  for (size_t c : chain_of) s.labels.push_back(static_cast<int32_t>(c));
 
   // A chain break follows residue i-1 when the numbering skips ahead, or when
-  // an inserted residue (non-blank code) is followed by the plain number.
+  // an inserted residue (non-blank code) is followed by the plain number;
+  // residues of different chains are never compared.
   for (size_t i = 1; i < residues.size(); ++i) {
+    if (chain_of[i] != chain_of[i - 1]) continue;
     const Residue& p = residues[i - 1];
     const Residue& c = residues[i];
     const bool skip = static_cast<int64_t>(c.number) > static_cast<int64_t>(p.number) + 1;
@@ -778,7 +828,9 @@ hkbs_status load(string_view text, int32_t format, string_view label, const hkbs
                                                                          : "no _atom_site rows present in mmCIF input");
   auto s = std::make_unique<hkbs_structure>();
   s->input_id = std::string(label);
-  const Options opt = read_options(options);
+  Options opt;
+  const Status read = read_options(options, opt);
+  if (!read.ok()) return report_error(read.code, read.detail);
   std::vector<Residue> residues;
   const Status st = normalize(recs, opt, *s, residues);
   if (!st.ok()) return report_error(st.code, st.detail);
@@ -865,6 +917,18 @@ hkbs_status hkbs_structure_residue_numbering(const hkbs_structure* s, int32_t* n
   if (numbers) std::copy(s->numbers.begin(), s->numbers.end(), numbers);
   if (icodes) std::copy(s->icodes.begin(), s->icodes.end(), icodes);
   if (records) std::copy(s->first_records.begin(), s->first_records.begin() + L, records);
+  return HKBS_OK;
+}
+
+size_t hkbs_structure_chain_count(const hkbs_structure* s) { return s ? s->chains.size() : 0; }
+
+const char* hkbs_structure_chain_name(const hkbs_structure* s, size_t chain) {
+  return (s && chain < s->chains.size()) ? s->chains[chain].c_str() : kEmpty;
+}
+
+hkbs_status hkbs_structure_chain_labels(const hkbs_structure* s, int32_t* labels) {
+  if (s == nullptr || labels == nullptr) return report_error(HKBS_INVALID_ARGUMENT, "structure handle and labels must be non-null");
+  std::copy(s->labels.begin(), s->labels.end(), labels);
   return HKBS_OK;
 }
 

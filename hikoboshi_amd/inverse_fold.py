@@ -116,7 +116,8 @@ def _check_selection(chain_id, chain_index, pdb_model_id, pdb_model_index) -> No
 
 
 def structure_options(chain_id: str | None = None, chain_index: int | None = None, pdb_model_id: str | None = None,
-                      pdb_model_index: int | None = None) -> structure.StructureLoadOptions:
+                      pdb_model_index: int | None = None, chain_ids: Any = None,
+                      all_chains: bool = False) -> structure.StructureLoadOptions:
     """Selection keywords -> loader options, with the checks of python/hikoboshi/_chain_resolve.py:79-100 and
     cpp/include/hikoboshi/bindings/engine_helpers.hpp:302-332 (empty strings leave a selection unset)."""
     _check_selection(chain_id, chain_index, pdb_model_id, pdb_model_index)
@@ -130,9 +131,17 @@ def structure_options(chain_id: str | None = None, chain_index: int | None = Non
     model_index = None
     if pdb_model_index is not None:  # narrowed to a C int like the reference binding
         model_index = (int(pdb_model_index) + 2**31) % 2**32 - 2**31
+    if chain_ids is not None or all_chains:
+        if chain_id is not None or chain_index is not None or (chain_ids is not None and all_chains):
+            raise InvalidArgumentError("choose one chain selection: chain_id, chain_index, chain_ids or all_chains")
+        if chain_ids is not None:
+            if isinstance(chain_ids, str) or not all(isinstance(c, str) for c in chain_ids):
+                raise InvalidArgumentError("chain_ids must be a sequence of chain id strings")
+            chain_ids = tuple(chain_ids)
     return structure.StructureLoadOptions(model_index=model_index, model_id=pdb_model_id or "",
                                           chain_id=chain_id or "",
-                                          chain_index=None if chain_index is None else int(chain_index) % 2**64)
+                                          chain_index=None if chain_index is None else int(chain_index) % 2**64,
+                                          chain_ids=chain_ids, all_chains=bool(all_chains))
 
 
 def load_structure(structure_arg: Any, options: structure.StructureLoadOptions | None = None,
@@ -175,11 +184,13 @@ def design(bb: Backbone, native: str | None, *, num_seqs: int = 1, sampling_temp
             for s in seeds:
                 coords = _lib.backbone_noise(bb.coords, bb.atom_sources, noise, int(s))
                 outs.append(ctx.design(coords, bb.atom_sources, 1, np.array([s], np.uint64), order_mode=mode,
-                                       order_seeds=np.array([s], np.uint64), temperature=T, greedy=T <= 0.0))
+                                       order_seeds=np.array([s], np.uint64), temperature=T, greedy=T <= 0.0,
+                                       residue_indices=bb.residue_indices, chain_labels=bb.chain_labels))
             res = {k: np.concatenate([o[k] for o in outs]) for k in ("tokens", "log_probs", "scores")}
         else:
             res = ctx.design(bb.coords, bb.atom_sources, int(num_seqs), seeds, order_mode=mode, order_seeds=seeds,
-                             temperature=T, greedy=T <= 0.0)
+                             temperature=T, greedy=T <= 0.0, residue_indices=bb.residue_indices,
+                             chain_labels=bb.chain_labels)
     except _lib.HkbsError as exc:
         raise from_status(exc.code, exc.detail) from exc
     seqs = []
@@ -218,17 +229,18 @@ class InverseFoldNamespace:
                        decode_order: str = "random", package: str | None = None, backbone_noise: float = 0.0,
                        out_logprobs: str | None = None, chain_id: str | None = None, chain_index: int | None = None,
                        pdb_model_id: str | None = None, pdb_model_index: int | None = None,
-                       **kwargs: Any) -> InverseFoldResult:
+                       chain_ids: Any = None, all_chains: bool = False, **kwargs: Any) -> InverseFoldResult:
         """python/hikoboshi/inverse_fold.py:20-65 and the argument order of
         cpp/bindings/inverse_fold_bindings.cpp:182-274 (decode order, structure selection and loading, then
-        the package)."""
+        the package). ``chain_ids`` (a sequence) or ``all_chains=True`` extend the reference's one-chain
+        selection: the chains are designed together, with ProteinMPNN's chain labels and residue offsets."""
         pdb_model_id, pdb_model_index = _deprecated_model_kwargs(kwargs, pdb_model_id, pdb_model_index)
         if kwargs:
             raise InvalidArgumentError(f"unknown inverse_fold.from_structure keyword(s): {', '.join(sorted(kwargs))}")
         _check_selection(chain_id, chain_index, pdb_model_id, pdb_model_index)
         order = parse_decode_order(decode_order)
         bb, native = load_structure(structure, structure_options(chain_id, chain_index, pdb_model_id,
-                                                                 pdb_model_index))
+                                                                 pdb_model_index, chain_ids, all_chains))
         resolve_package(package)
         result = design(bb, native, num_seqs=int(num_seqs), sampling_temp=float(sampling_temp), seed=int(seed),
                         decode_order=order, backbone_noise=float(backbone_noise))

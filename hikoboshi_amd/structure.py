@@ -19,7 +19,7 @@ import numpy as np
 
 from . import _lib
 from .backbone import Backbone
-from .exceptions import from_status
+from .exceptions import InvalidArgumentError, from_status
 
 FORMATS = {_lib.FORMAT_UNKNOWN: "unknown", _lib.FORMAT_PDB: "pdb", _lib.FORMAT_MMCIF: "mmcif"}
 
@@ -34,8 +34,13 @@ class StructureLoadOptions:
     chain_index: int | None = None
     infer_missing_atoms: bool = True
     include_modified_residues: bool = True
+    #: several chains, designed together in this order (an extension of the reference's options)
+    chain_ids: tuple[str, ...] | None = None
+    #: every polymer chain of the model in order of first appearance (extension)
+    all_chains: bool = False
 
-    def _c(self) -> _lib.StructureOptions:
+    def _c(self) -> tuple[_lib.StructureOptions, object]:
+        """The C struct, and the buffer its chain_ids point into (keep it alive for the call)."""
         o = _lib.StructureOptions()
         _lib.load().hkbs_structure_default_options(C.byref(o))
         if self.model_index is not None:
@@ -46,7 +51,16 @@ class StructureLoadOptions:
             o.has_chain_index, o.chain_index = 1, int(self.chain_index)
         o.infer_missing_atoms = int(bool(self.infer_missing_atoms))
         o.include_modified_residues = int(bool(self.include_modified_residues))
-        return o
+        keep = None
+        if self.chain_ids is not None:
+            ids = [str(c).encode() for c in self.chain_ids]
+            if not ids:
+                raise InvalidArgumentError("chain_ids must name at least one chain")
+            keep = (C.c_char_p * len(ids))(*ids)
+            o.chain_ids = C.cast(keep, C.POINTER(C.c_char_p))
+            o.n_chain_ids = len(ids)
+        o.all_chains = int(bool(self.all_chains))
+        return o, keep
 
 
 @dataclass(frozen=True)
@@ -77,16 +91,27 @@ class LoadedStructure:
     source_filename: str
     selected_model_id: str
     selected_model_index: int
-    selected_chain_id: str
+    selected_chain_id: str  # several selected chains: their ids joined by commas
     altloc_note: str
     numbering: dict = field(repr=False, compare=False, default_factory=dict)
+    #: selected chains in output order, and each residue's index into them
+    chain_ids: tuple[str, ...] = ()
+    chain_labels: np.ndarray | None = field(default=None, repr=False, compare=False)
 
     @property
     def residue_count(self) -> int:
         return len(self.residue_codes)
 
     def backbone(self) -> Backbone:
-        return Backbone(self.coords, self.atom_sources, name=Path(self.input_id).stem or "structure",
+        """The design input. Several chains carry ProteinMPNN's multichain encoding: chain labels, and residue
+        indices that count positions with a jump of 100 between chains (only same-chain offsets enter the
+        positional features)."""
+        labels = resid = None
+        if len(self.chain_ids) > 1:
+            labels = np.ascontiguousarray(self.chain_labels, np.int32)
+            resid = (np.arange(self.residue_count, dtype=np.int32) + 100 * labels).astype(np.int32)
+        return Backbone(self.coords, self.atom_sources, residue_indices=resid, chain_labels=labels,
+                        name=Path(self.input_id).stem or "structure",
                         meta={"residue_codes": self.residue_codes, "chain_id": self.selected_chain_id,
                               "model_id": self.selected_model_id})
 
@@ -116,16 +141,22 @@ def _take(handle: C.c_void_p) -> LoadedStructure:
         text = {f: lib.hkbs_structure_text(handle, f).decode("utf-8", "replace") for f in range(5)}
         model_index = int(lib.hkbs_structure_model_index(handle))
         names = [lib.hkbs_structure_residue_name(handle, i).decode("utf-8", "replace") for i in range(L)]
+        chains = tuple(lib.hkbs_structure_chain_name(handle, c).decode("utf-8", "replace")
+                       for c in range(int(lib.hkbs_structure_chain_count(handle))))
+        labels = np.zeros(L, np.int32)
+        if L:
+            _status(lib.hkbs_structure_chain_labels(handle, _lib.ptr(labels)))
     finally:
         lib.hkbs_structure_free(handle)
     chain, model_id, fname = text[_lib.TEXT_CHAIN_ID], text[_lib.TEXT_MODEL_ID], text[_lib.TEXT_SOURCE_FILENAME]
     residues = tuple(
-        ResidueMetadata(codes[i], names[i], chain, model_id, model_index, int(numbers[i]), chr(icodes[i]),
-                        f"{chain}_{int(numbers[i])}", i, fname, int(records[i]))
+        ResidueMetadata(codes[i], names[i], chains[labels[i]], model_id, model_index, int(numbers[i]), chr(icodes[i]),
+                        f"{chains[labels[i]]}_{int(numbers[i])}", i, fname, int(records[i]))
         for i in range(L))
     return LoadedStructure(coords.reshape(L, 5, 3), src.reshape(L, 5), codes, residues, breaks,
                            text[_lib.TEXT_INPUT_ID], fname, model_id, model_index, chain, text[_lib.TEXT_ALTLOC_NOTE],
-                           {"residue_numbers": numbers, "insertion_codes": icodes, "source_record_indices": records})
+                           {"residue_numbers": numbers, "insertion_codes": icodes, "source_record_indices": records},
+                           chains, labels)
 
 
 def detect_structure_format(path: str | os.PathLike = "", content: str | bytes = b"") -> str:
@@ -138,8 +169,9 @@ def load_structure_from_file(path: str | os.PathLike,
                              options: StructureLoadOptions | None = None) -> LoadedStructure:
     """cpp/io/structure_loader.cpp:167-194: read, detect format, parse, select, infer."""
     h = C.c_void_p()
-    _status(_lib.load().hkbs_structure_load_file(os.fsencode(path), C.byref((options or StructureLoadOptions())._c()),
-                                                 C.byref(h)))
+    opts, keep = (options or StructureLoadOptions())._c()
+    _status(_lib.load().hkbs_structure_load_file(os.fsencode(path), C.byref(opts), C.byref(h)))
+    del keep
     return _take(h)
 
 
@@ -147,8 +179,10 @@ def _load_text(content: str | bytes, fmt: int, origin_label: str,
                options: StructureLoadOptions | None) -> LoadedStructure:
     data = content.encode() if isinstance(content, str) else bytes(content)
     h = C.c_void_p()
-    _status(_lib.load().hkbs_structure_load_buffer(data, len(data), fmt, origin_label.encode(),
-                                                   C.byref((options or StructureLoadOptions())._c()), C.byref(h)))
+    opts, keep = (options or StructureLoadOptions())._c()
+    _status(_lib.load().hkbs_structure_load_buffer(data, len(data), fmt, origin_label.encode(), C.byref(opts),
+                                                   C.byref(h)))
+    del keep
     return _take(h)
 
 

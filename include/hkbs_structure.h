@@ -38,13 +38,21 @@ enum {
   HKBS_TEXT_INPUT_ID = 0,        /* file name without directories */
   HKBS_TEXT_SOURCE_FILENAME = 1, /* same as the input id for file loads */
   HKBS_TEXT_MODEL_ID = 2,        /* id string of the selected model */
-  HKBS_TEXT_CHAIN_ID = 3,        /* selected chain ("" for a blank chain column) */
+  HKBS_TEXT_CHAIN_ID = 3,        /* selected chain ("" for a blank chain column); several
+                                    selected chains are joined by commas */
   HKBS_TEXT_ALTLOC_NOTE = 4      /* "altloc selection applied" or "" */
 };
 
 /* StructureLoadOptions. Unset selections fall back to model 1 and chain "A"
- * (else the first polymer chain of the model). chain_id wins over
- * chain_index; model_index wins over model_id. */
+ * (else the first polymer chain of the model); model_index wins over
+ * model_id and chain_id over chain_index. chain_ids and all_chains exclude
+ * every other chain selection.
+ *
+ * chain_ids / all_chains extend the reference's options (which select one
+ * chain) so that a multichain design reaches hkbs_pmpnn_design: residues are
+ * grouped by chain in the requested order (all_chains: order of first
+ * appearance in the model) and hkbs_structure_chain_labels gives each
+ * residue's chain. */
 typedef struct hkbs_structure_options {
   int32_t has_model_index;
   int32_t model_index;
@@ -54,6 +62,9 @@ typedef struct hkbs_structure_options {
   uint64_t chain_index;
   int32_t infer_missing_atoms;       /* default 1 */
   int32_t include_modified_residues; /* default 1 */
+  const char* const* chain_ids;      /* n_chain_ids distinct chain ids ("" = blank chain) */
+  size_t n_chain_ids;
+  int32_t all_chains;                /* every polymer chain of the selected model */
 } hkbs_structure_options;
 
 typedef struct hkbs_structure hkbs_structure;
@@ -93,7 +104,12 @@ const char* hkbs_structure_residue_name(const hkbs_structure* structure, size_t 
 /* Per-residue numbering; each output (length L) may be NULL. */
 hkbs_status hkbs_structure_residue_numbering(const hkbs_structure* structure, int32_t* residue_numbers,
                                              char* insertion_codes, int64_t* source_record_indices);
-/* Chain breaks: indices of the residues after which the numbering jumps. */
+/* Selected chains in output order, and each residue's index into them (L values). */
+size_t hkbs_structure_chain_count(const hkbs_structure* structure);
+const char* hkbs_structure_chain_name(const hkbs_structure* structure, size_t chain);
+hkbs_status hkbs_structure_chain_labels(const hkbs_structure* structure, int32_t* labels);
+/* Chain breaks: indices of the residues after which the numbering jumps
+ * within a chain. */
 size_t hkbs_structure_chain_break_count(const hkbs_structure* structure);
 const uint64_t* hkbs_structure_chain_breaks(const hkbs_structure* structure);
 

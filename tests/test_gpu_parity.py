@@ -376,6 +376,35 @@ def test_inverse_fold_from_cif_selected_chain(oracle, tmp_path):
         assert s.recovery_vs_native == ifold.recovery_vs_native(s.sequence, loaded.residue_codes)
 
 
+def test_inverse_fold_several_chains(oracle, tmp_path):
+    """all_chains: two chains designed together with chain labels and per-chain residue offsets, against the
+    oracle on the same multichain backbone (cross-chain edges use the chain-break positional class)."""
+    from hikoboshi_amd import inverse_fold as ifold
+
+    from .test_structure import records_from_pdb, to_mmcif
+
+    fix = sorted(FIXTURES.glob("*.pdb"))
+    recs = records_from_pdb(fix[0].read_text(), "H") + records_from_pdb(fix[4].read_text(), "L", drop_every=3)
+    # the second chain is moved next to the first so that cross-chain kNN edges exist
+    recs = [dict(r, xyz=np.asarray(r["xyz"]) + (6.0, 0.0, 0.0)) if r["chain"] == "L" else r for r in recs]
+    path = tmp_path / "hl.cif"
+    path.write_text(to_mmcif([(1, recs)], np.random.default_rng(9)))
+    loaded = structure.load_structure_from_file(path, structure.StructureLoadOptions(all_chains=True))
+    bb = loaded.backbone()
+    assert loaded.chain_ids == ("H", "L") and bb.chain_labels is not None
+    enc_idx = oracle.encode(bb)[1]
+    assert (bb.chain_labels[enc_idx] != bb.chain_labels[:, None]).any(), "no cross-chain neighbours"
+    _say(f"inverse_fold two chains L={bb.L}")
+    res = ifold.inverse_fold(str(path), all_chains=True, num_seqs=2, sampling_temp=0.2, seed=11)
+    tokens = np.array([[backbone.ALPHABET.index(c) for c in s.sequence] for s in res.sequences], np.int32)
+    orders = np.stack([_lib.decode_order(bb.atom_sources, 11 + i) for i in range(2)])
+    check_design(oracle, bb, dict(tokens=tokens, log_probs=res.log_prob_values, orders=orders),
+                 np.arange(11, 13, dtype=np.uint64), 0.2)
+    # a single-chain design of the same file differs (other chain absent from the graph)
+    one = ifold.inverse_fold(str(path), chain_id="H", num_seqs=1, sampling_temp=0.2, seed=11)
+    assert len(one.sequences[0].sequence) == int((bb.chain_labels == 0).sum())
+
+
 def test_inverse_fold_noise_and_n_to_c(oracle):
     """Backbone noise: each sample is encoded from its own noised coordinates."""
     from hikoboshi_amd import inverse_fold as ifold

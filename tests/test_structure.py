@@ -548,3 +548,75 @@ def test_inverse_fold_selection_keywords(tmp_path):
         f(str(tmp_path / "missing.pdb"), package="nope")
     opts = ifold.structure_options(pdb_model_index=2**32 + 2, chain_index=3)
     assert opts.model_index == 2 and opts.chain_index == 3
+    # several chains (extension): labels and offsets reach the backbone
+    bb2, native2 = ifold.load_structure(str(path), all_chains=True)
+    assert native2 == native + native_b and bb2.L == bb.L + bb_b.L
+    np.testing.assert_array_equal(bb2.chain_labels, np.repeat([0, 1], [bb.L, bb_b.L]))
+    assert ifold.load_structure(str(path), chain_ids=["B", "A"])[1] == native_b + native
+    with pytest.raises(InvalidArgumentError, match="choose one chain selection"):
+        f(str(path), chain_ids=["A"], chain_id="A")
+    with pytest.raises(InvalidArgumentError, match="chain_ids must be a sequence of chain id strings"):
+        f(str(path), chain_ids="AB")
+
+
+# ---------------------------------------------------- several chains ----
+def _block_equals_single_chain(multi, single, rows):
+    assert multi.coords[rows].view(np.uint32).tobytes() == single.coords.view(np.uint32).tobytes()
+    np.testing.assert_array_equal(multi.atom_sources[rows], single.atom_sources)
+    assert "".join(multi.residue_codes[i] for i in rows) == single.residue_codes
+    for key in ("residue_numbers", "insertion_codes", "source_record_indices"):
+        np.testing.assert_array_equal(multi.numbering[key][rows], single.numbering[key])
+    assert [multi.residues[i].original_residue_name for i in rows] == [m.original_residue_name for m in single.residues]
+
+
+@pytest.mark.parametrize("seed", range(12))
+@pytest.mark.parametrize("fmt", ["pdb", "mmcif"])
+def test_several_chains_are_single_chain_loads_side_by_side(seed, fmt):
+    """all_chains / chain_ids (an extension of the reference's one-chain selection): each chain's block is
+    exactly that chain's own load; chain breaks are the per-chain breaks shifted to the block; labels index
+    the selected chains."""
+    models = scene(seed, n_models=1 + seed % 2)
+    text = to_pdb(models) if fmt == "pdb" else to_mmcif(models, np.random.default_rng(seed))
+    load = S.load_pdb_from_string if fmt == "pdb" else S.load_mmcif_from_string
+    for opts in (S.StructureLoadOptions(all_chains=True), S.StructureLoadOptions(chain_ids=("A", "B")),
+                 S.StructureLoadOptions(chain_ids=("B", "A"), model_index=1 + seed % 2, infer_missing_atoms=seed % 3 > 0)):
+        multi = load(text, "m", opts)
+        expect = ("B", "A") if opts.all_chains else opts.chain_ids
+        assert multi.chain_ids == expect and multi.selected_chain_id == ",".join(expect)
+        labels = multi.chain_labels
+        assert (np.diff(labels) >= 0).all() and set(labels) == set(range(len(expect)))
+        breaks = []
+        for c, cid in enumerate(expect):
+            single = load(text, "m", S.StructureLoadOptions(chain_id=cid, model_index=opts.model_index,
+                                                           infer_missing_atoms=opts.infer_missing_atoms))
+            rows = np.flatnonzero(labels == c)
+            assert rows.size == single.residue_count
+            _block_equals_single_chain(multi, single, rows)
+            assert all(multi.residues[i].chain_id == cid for i in rows)
+            breaks += [int(rows[0]) + b for b in single.chain_breaks]
+        assert multi.chain_breaks == tuple(breaks)
+        bb = multi.backbone()
+        np.testing.assert_array_equal(bb.chain_labels, labels)
+        np.testing.assert_array_equal(bb.residue_indices, np.arange(multi.residue_count) + 100 * labels)
+    one = load(text, "m")
+    assert one.chain_ids == ("A",) and not one.chain_labels.any() and one.backbone().residue_indices is None
+
+
+def test_several_chains_errors():
+    text = to_pdb(scene(2))
+    cases = [(dict(chain_ids=("A", "Q")), "requested chain id not present in selected model"),
+             (dict(chain_ids=("A", "A")), "chain ids must be distinct"),
+             (dict(chain_ids=("A",), chain_id="B"), "choose one chain selection"),
+             (dict(all_chains=True, chain_index=0), "choose one chain selection"),
+             (dict(all_chains=True, chain_ids=("A",)), "choose one chain selection"),
+             (dict(chain_ids=()), "chain_ids must name at least one chain")]
+    for kw, msg in cases:
+        with pytest.raises(InvalidArgumentError, match=msg):
+            S.load_pdb_from_string(text, "e", S.StructureLoadOptions(**kw))
+    # the reference's own precedence stays: chain_id over chain_index
+    assert S.load_pdb_from_string(text, "e", S.StructureLoadOptions(chain_id="B", chain_index=0)).chain_ids == ("B",)
+    water = pdb_atom(1, "O", "HOH", "W", 1, (0, 0, 0), het=True) + "\n" + "\n".join(_residue("B", 1, "VAL"))
+    assert S.load_pdb_from_string(water, "w", S.StructureLoadOptions(all_chains=True)).chain_ids == ("B",)
+    with pytest.raises(InvalidArgumentError, match="selected model has no polymer chains"):
+        S.load_pdb_from_string(pdb_atom(1, "O", "HOH", "W", 1, (0, 0, 0), het=True), "w",
+                               S.StructureLoadOptions(all_chains=True))
