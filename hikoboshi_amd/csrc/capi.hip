@@ -711,14 +711,21 @@ hkbs_status upload_inputs(hkbs_pmpnn* ctx, DeviceArena& ar, const float* coords,
   return HKBS_OK;
 }
 
+// Pass schedule of up to B orders: sched, pstart, npass, draw and scratch.
+size_t schedule_bytes(int L, int B) {
+  const size_t nq = (size_t)B;
+  return 2 * aligned_bytes<int32_t>(nq * L) + aligned_bytes<int32_t>(nq * (L + 2)) + aligned_bytes<int32_t>(nq) +
+         aligned_bytes<int32_t>(nq * (3 * (size_t)L + 2));
+}
+
 size_t decode_bytes(int L, int K, int B) {
   const size_t S = (size_t)L * K;
   return aligned_bytes<float>(kLayers * S * kH) + aligned_bytes<float>((size_t)(kLayers + 1) * L * kH) +
          2 * aligned_bytes<int32_t>((size_t)B * L) + aligned_bytes<uint64_t>(B) +
          aligned_bytes<float>((size_t)B * kLayers * L * kH) + aligned_bytes<int32_t>((size_t)B * L) +
          aligned_bytes<float>((size_t)B * L * kV) + aligned_bytes<float>((size_t)B * L) + aligned_bytes<float>(B) +
-         aligned_bytes<uint32_t>((size_t)B + 1) + aligned_bytes<int32_t>((size_t)B * L) +
-         2 * aligned_bytes<int32_t>((size_t)B * L * K);
+         aligned_bytes<uint32_t>((size_t)B + 1) + 2 * aligned_bytes<int32_t>((size_t)B * L * K) +
+         schedule_bytes(L, B);
 }
 
 hkbs_status enter(hkbs_pmpnn* ctx) {
@@ -747,9 +754,13 @@ hkbs_status design_on_device(hkbs_pmpnn* ctx, const float* coords, const uint8_t
   float* R = ar.take<float>((size_t)B * kLayers * L * kH);
   uint32_t* sync = ar.take<uint32_t>((size_t)B + 1);  // B team counters + fault word
   const size_t nq = shared ? 1 : (size_t)B;
-  int32_t* gsize = ar.take<int32_t>(nq * L);
   int32_t* nbj = ar.take<int32_t>(nq * L * K);
   int32_t* nbp = ar.take<int32_t>(nq * L * K);
+  int32_t* sched = ar.take<int32_t>(nq * L);
+  int32_t* pstart = ar.take<int32_t>(nq * (L + 2));
+  int32_t* npass = ar.take<int32_t>(nq);
+  int32_t* draw = ar.take<int32_t>(nq * L);
+  int32_t* sched_tmp = ar.take<int32_t>(nq * (3 * (size_t)L + 2));
   ctx->fault = sync + B;
   if (ctx->timing) HK_CHECK(hipEventRecord(ctx->ev[0], ctx->stream), "event record failed");
   HK_CHECK(run_encode(ctx, coords, src, resid, chain, L, K, e), "encoder launch failed");
@@ -781,12 +792,16 @@ hkbs_status design_on_device(hkbs_pmpnn* ctx, const float* coords, const uint8_t
   a.chosen_lp = chosen;
   a.sync = sync;
   a.fault = sync + B;
-  a.gsize = gsize;
   a.nbj = nbj;
   a.nbp = nbp;
+  a.sched = sched;
+  a.pstart = pstart;
+  a.npass = npass;
+  a.draw = draw;
+  a.sched_tmp = sched_tmp;
   a.precision = ctx->precision;
   const int team = decode_team_size(a.precision, B, 8);
-  a.max_run = std::min(8, 4 * team);
+  a.max_members = kDecodeGroup * team;
   ctx->last_decode = a;
   HK_CHECK(launch_decode_schedule(a, ctx->stream), "decode schedule launch failed");
   if (ctx->timing) HK_CHECK(hipEventRecord(ctx->ev[2], ctx->stream), "event record failed");
@@ -977,7 +992,7 @@ hkbs_status hkbs_pmpnn_design(hkbs_pmpnn* ctx, const float* coords, const uint8_
     // A team of workgroups could not run together (the device was busy with
     // other work): decode again with one workgroup per sequence.
     DecodeArgs one = ctx->last_decode;
-    one.max_run = 4;  // runs one workgroup can hold
+    one.max_members = kDecodeGroup;  // steps one workgroup can hold
     HK_CHECK(launch_decode_schedule(one, s), "decode schedule launch failed");
     HK_CHECK(launch_decode(ctx->model, one, s, 1), "decode launch failed");
     HK_CHECK(hipMemcpyAsync(tokens, d_tokens, (size_t)B * L * 4, hipMemcpyDeviceToHost, s), "D2H failed");

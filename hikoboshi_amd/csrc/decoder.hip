@@ -46,8 +46,7 @@ typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
 constexpr int kThreads = 512;
 
-constexpr int kGroup = 4;   // residues one workgroup decodes together (sizes its LDS)
-constexpr int kMaxRun = 8;  // residues a team decodes together (at most kGroup per rank)
+constexpr int kGroup = kDecodeGroup;  // steps one workgroup decodes in a pass (sizes its LDS)
 
 // Y[i][o] = sum_p X[i][p] Wt[p][o] for i < m rows (m <= kGroup), OUT outputs
 // and IN inputs on all threads. Thread (q, grp) owns float4 column q and
@@ -206,17 +205,19 @@ __device__ inline bool team_sync(uint32_t* counter, uint32_t target, uint32_t sp
   return *bad == 0;
 }
 
-// Decodes one sequence per team of P workgroups (P = a.team, 1..4). Steps are
-// taken in groups of up to a.max_run (<= kGroup * P) consecutive residues of the order in which
-// no residue is a kNN neighbour of a later one: such residues do not read
-// each other's state, so they run together (bw for every member means
-// "decoded before the group"). Member i of a group runs on team rank i % P;
-// a rank with several members shares each weight load and barrier between
-// them. Tokens are drawn in order, member i using the i-th next state of the
-// sequence's counter stream, so the split does not change any draw. The
-// state a later group reads (R rows, chosen log-probs) is written with
-// device-scope stores and published by a team barrier at the end of each
-// group. With P > 1 the grid is 8 * ceil(B / 8) * P workgroups and rank r of
+// Decodes one sequence per team of P workgroups (P = a.team, 1..8) in the
+// passes of the dependency schedule (dag_schedule_kernel): a pass holds up to
+// a.max_members (<= kGroup * P) steps whose earlier kNN neighbours were all
+// decoded in earlier passes, so each step sees the inputs of sequential
+// decoding (bw = the neighbour's position is before the step's own). Member i
+// of a pass runs on team rank i % P; a rank with several members shares each
+// weight load and barrier between them. A step's token comes from draw
+// a.draw[u] of the sequence's counter stream, i.e. draws are consumed in order
+// of u whatever pass decodes the step. The state a later pass reads (R rows,
+// chosen log-probs) is written with device-scope stores and published by a
+// team barrier at the end of each pass. Pass 0 (inactive residues: fallback
+// token, zero log-probs, no draw) runs first, on rank 0.
+// With P > 1 the grid is 8 * ceil(B / 8) * P workgroups and rank r of
 // sequence b runs as workgroup 8 (P (b / 8) + r) + b % 8, so that a team
 // shares one XCD when workgroups are dealt round-robin over the 8 XCDs; the
 // whole grid fits the device at once.
@@ -248,6 +249,7 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(ModelDev m, DecodeArgs
   __shared__ int nbr[kGroup * kKmax];
   __shared__ int bwf[kGroup * kKmax];
   __shared__ int tres[kGroup];
+  __shared__ int ures[kGroup];
   __shared__ int tok_s[kGroup];
   __shared__ int bad;
 
@@ -264,16 +266,20 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(ModelDev m, DecodeArgs
   const int wave = threadIdx.x >> 6;
   const int lane = threadIdx.x & 63;
   const int32_t* order = a.shared_order ? a.orders : a.orders + (size_t)b * L;
-  const int32_t* gsize = a.shared_order ? a.gsize : a.gsize + (size_t)b * L;
-  const int32_t* nbj = a.shared_order ? a.nbj : a.nbj + (size_t)b * L * K;
-  const int32_t* nbp = a.shared_order ? a.nbp : a.nbp + (size_t)b * L * K;
+  const size_t qo = a.shared_order ? 0 : (size_t)b;
+  const int32_t* nbj = a.nbj + qo * L * K;
+  const int32_t* nbp = a.nbp + qo * L * K;
+  const int32_t* sched = a.sched + qo * L;
+  const int32_t* pstart = a.pstart + qo * (L + 2);
+  const int32_t* draw = a.draw + qo * L;
+  const int npass = a.npass[qo];
   float* R = a.R + (size_t)b * kLayers * L * kH;
   int32_t* tokens = a.tokens + (size_t)b * L;
   float* lp_out = a.log_probs ? a.log_probs + (size_t)b * L * kV : nullptr;
   float* chosen = a.chosen_lp + (size_t)b * L;
   uint32_t* counter = a.sync + b;
   uint32_t passes = 0;
-  uint64_t rng = a.seeds[b];
+  const uint64_t seed = a.seeds[b];
   const float T = (a.temperature > 0.0F && isfinite(a.temperature)) ? a.temperature : 1.0F;
   const bool greedy = a.greedy || a.temperature <= 0.0F;
   if (threadIdx.x < 17) tbl[threadIdx.x] = kExpNegTable[threadIdx.x];
@@ -296,36 +302,36 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(ModelDev m, DecodeArgs
   if (threadIdx.x < 32) prm[kPrmLog + threadIdx.x] = m.blog[threadIdx.x];
   __syncthreads();
 
-  int step = 0;
-  while (step < L) {
-    const int t0 = order[step];
-    if (t0 < 0 || t0 >= L) {  // malformed device order: skip the entry
-      ++step;
-      continue;
-    }
-    if (a.mask[t0] == 0.0F) {
-      // inverse_fold_scalar.cpp:804-813: fallback token, zero log-probs, no draw.
+  // Pass 0: inactive residues (inverse_fold_scalar.cpp:804-813): fallback
+  // token, zero log-probs, no draw; R rows Q + T[tok] (layer 0) and T[tok].
+  {
+    const int s0 = pstart[0], n0 = pstart[1] - pstart[0];
+    if (n0 > 0) {
       if (rank == 0) {
-        const int tok =
-            (a.true_tokens && a.true_tokens[t0] >= 0 && a.true_tokens[t0] < kV) ? a.true_tokens[t0] : kV - 1;
-        if (threadIdx.x == 0) {
-          tokens[t0] = tok;
-          store_dev(chosen + t0, 0.0F);
+        for (int i = threadIdx.x; i < n0; i += kThreads) {
+          const int t = order[sched[s0 + i]];
+          const int tok = (a.true_tokens && a.true_tokens[t] >= 0 && a.true_tokens[t] < kV) ? a.true_tokens[t] : kV - 1;
+          tokens[t] = tok;
+          store_dev(chosen + t, 0.0F);
         }
-        if (lp_out && threadIdx.x < kV) lp_out[(size_t)t0 * kV + threadIdx.x] = 0.0F;
-        for (int i = threadIdx.x; i < kLayers * kH; i += kThreads) {
-          const int l = i / kH, c = i % kH;
-          const float base = (l == 0) ? a.Q[(size_t)t0 * kH + c] : 0.0F;
-          store_dev(R + ((size_t)l * L + t0) * kH + c, base + m.dec[l].T[tok * kH + c]);
+        if (lp_out)
+          for (int task = threadIdx.x; task < n0 * kV; task += kThreads)
+            lp_out[(size_t)order[sched[s0 + task / kV]] * kV + task % kV] = 0.0F;
+        for (int task = threadIdx.x; task < n0 * kLayers * kH; task += kThreads) {
+          const int i = task / (kLayers * kH), l = (task / kH) % kLayers, c = task % kH;
+          const int t = order[sched[s0 + i]];
+          const int tok = (a.true_tokens && a.true_tokens[t] >= 0 && a.true_tokens[t] < kV) ? a.true_tokens[t] : kV - 1;
+          const float base = (l == 0) ? a.Q[(size_t)t * kH + c] : 0.0F;
+          store_dev(R + ((size_t)l * L + t) * kH + c, base + m.dec[l].T[tok * kH + c]);
         }
       }
-      ++step;
-      if (P > 1 && !team_sync(counter, ++passes * P, a.spin_limit, a.fault, &bad)) break;
+      if (P > 1 && !team_sync(counter, ++passes * P, a.spin_limit, a.fault, &bad)) goto finish;
       __syncthreads();
-      continue;
     }
-    // Group of consecutive independent steps (sizes precomputed per step).
-    const int mg = gsize[step];
+  }
+  for (int pass = 1; pass <= npass; ++pass) {
+    const int s0 = pstart[pass];
+    const int mg = pstart[pass + 1] - s0;
     const int ml = mg > rank ? (mg - rank + P - 1) / P : 0;  // members of this rank: rank + P i
     if (ml > kGroup) {  // a schedule built for a larger team: refuse rather than overrun LDS
       if (threadIdx.x == 0) __hip_atomic_store(a.fault, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -335,15 +341,18 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(ModelDev m, DecodeArgs
     if (ml > 0) {
       if (threadIdx.x < ml * K) {
         const int i = threadIdx.x / K, k = threadIdx.x % K;
-        const size_t at = (size_t)(step + rank + P * i) * K + k;
-        const int j = nbj[at];
-        nbr[i * kKmax + k] = j;
-        bwf[i * kKmax + k] = nbp[at] < step;  // empty slots hold position L
-        if (k == 0) tres[i] = order[step + rank + P * i];
+        const int u = sched[s0 + rank + P * i];
+        const size_t at = (size_t)u * K + k;
+        nbr[i * kKmax + k] = nbj[at];
+        bwf[i * kKmax + k] = nbp[at] < u;  // empty slots hold position L
+        if (k == 0) {
+          tres[i] = order[u];
+          ures[i] = u;
+        }
       }
       for (int task = threadIdx.x; task < ml * kH; task += kThreads) {
         const int i = task / kH, c = task % kH;
-        const int t = order[step + rank + P * i];
+        const int t = order[sched[s0 + rank + P * i]];
         h[i * kH + c] = a.h_v[(size_t)t * kH + c];
         // layer-0 W1a h^0_t comes from the precompute (Q block 3)
         hA[i * kH + c] = a.Q[((size_t)3 * L + t) * kH + c] + prm[kPrmB1 + c];
@@ -586,9 +595,9 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(ModelDev m, DecodeArgs
       if (wave < ml) {  // wave i draws member i
         const int i = wave;
         const int t = tres[i];
-        const int gi = rank + P * i;
         float lpv;
-        const int s_tok = sample_wave(logits + i * 32, T, greedy, rng + (uint64_t)gi * 0x9E3779B97F4A7C15ull, &lpv);
+        const uint64_t state = seed + (uint64_t)draw[ures[i]] * 0x9E3779B97F4A7C15ull;
+        const int s_tok = sample_wave(logits + i * 32, T, greedy, state, &lpv);
         const float design = (a.chain_mask ? a.chain_mask[t] : 1.0F) * a.mask[t];
         int tok = s_tok;
         if (design == 0.0F)
@@ -608,11 +617,10 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(ModelDev m, DecodeArgs
         store_dev(R + ((size_t)l * L + t) * kH + c, base + m.dec[l].T[tok_s[i] * kH + c]);
       }
     }
-    if (!greedy) rng += (uint64_t)mg * 0x9E3779B97F4A7C15ull;
-    step += mg;
     if (P > 1 && !team_sync(counter, ++passes * P, a.spin_limit, a.fault, &bad)) break;
     __syncthreads();
   }
+finish:
   // Mean NLL over designed residues in residue order (inverse_fold_scalar.cpp:471-493).
   if (a.scores && rank == 0 && threadIdx.x == 0) {
     if (bad) {
@@ -702,32 +710,134 @@ __global__ void neighbour_schedule_kernel(const int32_t* __restrict__ orders, co
   }
 }
 
-// Size of the group that starts at step s: it stops before the first later
-// step whose residue is inactive or out of range, or has a neighbour decoded
-// at a step in [s, that step) (decode_kernel decodes a group's members
-// together, so none may read another's state).
-__global__ void group_schedule_kernel(const int32_t* __restrict__ orders, const float* __restrict__ mask,
-                                      const int32_t* __restrict__ nbp, int L, int K, int max_run,
-                                      int32_t* __restrict__ gsize) {
-  const int q = blockIdx.y;
-  const int s = blockIdx.x * blockDim.x + threadIdx.x;
-  if (s >= L) return;
+// Dependency schedule of one decoding order (one wave per order q). Step u
+// (residue order[u]) reads the state of every kNN neighbour decoded before it,
+// so it may run in the first pass after all of those steps' passes. Steps are
+// placed in order of u into the earliest such pass that holds fewer than
+// max_members steps (first fit). Every step then sees exactly the inputs of
+// sequential decoding, whatever pass it runs in. Inactive residues (mask 0)
+// read nothing and form pass 0, which runs before all others; entries outside
+// 0..L-1 are dropped. If the order is not a permutation (a residue repeated),
+// every active step gets a pass of its own, in order: sequential decoding
+// (also selected by sequential != 0; HKBS_DECODE_SCHEDULE=sequential).
+// Outputs per order: sched [L] (steps grouped by pass, increasing u within a
+// pass), pstart [L + 2] (pass p holds sched[pstart[p] .. pstart[p + 1])),
+// npass (passes after pass 0) and draw [L] (index of the step's sampler draw
+// among the active steps: the sampler stream is consumed in order of u).
+// pass_of / fill live in LDS (kLds) or in the global scratch gpass / gfill.
+constexpr int kSchedLdsMaxL = 8000;  // pass_of [L] and fill [L + 2] in at most 64 KiB of dynamic LDS
+
+template <bool kLds>
+__global__ __launch_bounds__(64) void dag_schedule_kernel(const int32_t* __restrict__ orders,
+                                                          const int32_t* __restrict__ pos,
+                                                          const float* __restrict__ mask,
+                                                          const int32_t* __restrict__ nbp, int L, int K,
+                                                          int max_members, int sequential,
+                                                          int32_t* __restrict__ sched,
+                                                          int32_t* __restrict__ pstart, int32_t* __restrict__ npass,
+                                                          int32_t* __restrict__ draw, int32_t* __restrict__ gpass,
+                                                          int32_t* __restrict__ gfill, int32_t* __restrict__ gslot) {
+  extern __shared__ int32_t sched_lds[];
+  const int q = blockIdx.x;
+  const int lane = threadIdx.x;
   const int32_t* order = orders + (size_t)q * L;
+  const int32_t* pq = pos + (size_t)q * L;
   const int32_t* np = nbp + (size_t)q * L * K;
-  int m = min(max_run, L - s);
-  for (int c = 1; c < m; ++c) {
-    const int tc = order[s + c];
-    bool stop = tc < 0 || tc >= L || mask[tc] == 0.0F;
-    for (int k = 0; k < K && !stop; ++k) {
-      const int p = np[(size_t)(s + c) * K + k];
-      stop = p >= s && p < s + c;
+  int32_t* pass_of = kLds ? sched_lds : gpass + (size_t)q * L;
+  int32_t* fill = kLds ? sched_lds + L : gfill + (size_t)q * (L + 2);
+  int32_t* slot = gslot + (size_t)q * L;
+  int32_t* sq = sched + (size_t)q * L;
+  int32_t* ps = pstart + (size_t)q * (L + 2);
+  int32_t* dq = draw + (size_t)q * L;
+  for (int i = lane; i < L + 2; i += 64) fill[i] = 0;
+  bool perm = true;
+  for (int u = lane; u < L; u += 64) {
+    const int t = order[u];
+    perm = perm && t >= 0 && t < L && pq[t] == u;
+  }
+  perm = __all(perm) && !sequential;
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  // Steps are read 16 at a time (all loads of a chunk in flight together);
+  // the placement itself is sequential in u.
+  constexpr int kChunk = 16;
+  int last = 0, ndraw = 0;
+  for (int u0 = 0; u0 < L; u0 += kChunk) {
+    int tt[kChunk], pp[kChunk];
+    float mm[kChunk];
+#pragma unroll
+    for (int c = 0; c < kChunk; ++c) {
+      const int u = u0 + c;
+      tt[c] = u < L ? order[u] : -1;
+      pp[c] = (u < L && lane < K) ? np[(size_t)u * K + lane] : L;
     }
-    if (stop) {
-      m = c;
-      break;
+#pragma unroll
+    for (int c = 0; c < kChunk; ++c) mm[c] = (tt[c] >= 0 && tt[c] < L) ? mask[tt[c]] : 0.0F;
+#pragma unroll
+    for (int c = 0; c < kChunk; ++c) {
+      const int u = u0 + c;
+      int r;
+      if (u >= L) {
+        continue;
+      } else if (tt[c] < 0 || tt[c] >= L) {
+        r = -1;
+      } else if (mm[c] == 0.0F) {
+        r = 0;
+      } else if (perm) {
+        int need = 1;
+        if (pp[c] < u) {
+          const int p = pp[c];
+          const int before =
+              kLds ? pass_of[p] : __hip_atomic_load(pass_of + p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+          need = before + 1;
+        }
+        r = static_cast<int>(wave_max(static_cast<float>(need)));
+        while ((kLds ? fill[r] : __hip_atomic_load(fill + r, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP)) >=
+               max_members)
+          ++r;
+      } else {
+        r = last + 1;
+      }
+      if (lane == 0) {
+        dq[u] = r > 0 ? ndraw : -1;
+        if (r >= 0) {
+          const int f = kLds ? fill[r] : __hip_atomic_load(fill + r, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+          slot[u] = f;
+          if (kLds) {
+            pass_of[u] = r;
+            fill[r] = f + 1;
+          } else {
+            __hip_atomic_store(pass_of + u, r, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+            __hip_atomic_store(fill + r, f + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+          }
+        } else if (kLds) {
+          pass_of[u] = -1;
+        } else {
+          __hip_atomic_store(pass_of + u, -1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+        }
+      }
+      if (!kLds) __builtin_amdgcn_s_waitcnt(0);
+      if (r > 0) ++ndraw;
+      last = r > last ? r : last;
     }
   }
-  gsize[(size_t)q * L + s] = m;
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  if (lane == 0) {
+    int at = 0;
+    for (int p = 0; p <= last; ++p) {
+      ps[p] = at;
+      at += fill[p];
+    }
+    ps[last + 1] = at;
+    npass[q] = last;
+  }
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  for (int u = lane; u < L; u += 64) {
+    const int r = pass_of[u];
+    if (r >= 0) sq[ps[r] + slot[u]] = u;
+  }
 }
 
 }  // namespace
@@ -765,8 +875,20 @@ hipError_t launch_decode_schedule(const DecodeArgs& a, hipStream_t stream) {
   const size_t n = (size_t)a.L * a.K;
   neighbour_schedule_kernel<<<dim3((unsigned)std::min<size_t>((n + 255) / 256, 4096), nq), 256, 0, stream>>>(
       a.orders, a.pos, a.idx, a.L, a.K, a.nbj, a.nbp);
-  group_schedule_kernel<<<dim3((unsigned)((a.L + 255) / 256), nq), 256, 0, stream>>>(a.orders, a.mask, a.nbp, a.L, a.K,
-                                                                                       a.max_run, a.gsize);
+  const char* mode = std::getenv("HKBS_DECODE_SCHEDULE");
+  const int sequential = mode && std::strcmp(mode, "sequential") == 0;
+  if (a.max_members < 1) return hipErrorInvalidValue;
+  if (a.L <= kSchedLdsMaxL) {
+    dag_schedule_kernel<true><<<nq, 64, sizeof(int32_t) * (2 * (size_t)a.L + 2), stream>>>(
+        a.orders, a.pos, a.mask, a.nbp, a.L, a.K, a.max_members, sequential, a.sched, a.pstart, a.npass, a.draw,
+        nullptr, nullptr, a.sched_tmp);
+  } else {
+    int32_t* gpass = a.sched_tmp + (size_t)nq * a.L;
+    int32_t* gfill = gpass + (size_t)nq * a.L;
+    dag_schedule_kernel<false><<<nq, 64, 0, stream>>>(a.orders, a.pos, a.mask, a.nbp, a.L, a.K, a.max_members,
+                                                      sequential, a.sched, a.pstart, a.npass, a.draw, gpass, gfill,
+                                                      a.sched_tmp);
+  }
   return hipGetLastError();
 }
 
@@ -797,7 +919,7 @@ hipError_t launch_decode_as(const ModelDev& m, const DecodeArgs& args, hipStream
   const long teams_per_xcd = (a.B + 7) / 8;
   int P = team_size_as<PREC>(a.B, max_team);
   if (!a.sync || !a.fault) P = 1;
-  if (a.max_run > kGroup * P) return hipErrorInvalidValue;  // the schedule assumed a larger team
+  if (a.max_members < 1 || a.max_members > kGroup * P) return hipErrorInvalidValue;  // the schedule assumed a larger team
   a.spin_limit = kSpinLimit;
   if (const char* env = std::getenv("HKBS_DECODE_SPIN_LIMIT")) a.spin_limit = (uint32_t)std::max(1, std::atoi(env));
   if (P > 1) {

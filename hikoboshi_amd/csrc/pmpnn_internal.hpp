@@ -115,9 +115,16 @@ struct DecodeArgs {
   const int32_t* orders;  // [B][L] or [L]
   int shared_order;
   const int32_t* pos;     // [B][L] or [L]: position of residue r in the order
-  int32_t* gsize;         // [B][L] or [L] workspace: group size starting at each step
   int32_t* nbj;           // [B][L][K] or [L][K] workspace: neighbours of the residue at each step
   int32_t* nbp;           // same shape: their positions in the order (L for an empty slot)
+  // Pass schedule per order (nq = 1 for a shared order, else B), built by
+  // launch_decode_schedule: pass p decodes the steps sched[pstart[p] ..
+  // pstart[p + 1]); pass 0 holds the inactive steps; passes 1..npass follow.
+  int32_t* sched;         // [nq][L]
+  int32_t* pstart;        // [nq][L + 2]
+  int32_t* npass;         // [nq]
+  int32_t* draw;          // [nq][L]: sampler draw index of each active step, -1 otherwise
+  int32_t* sched_tmp;     // [nq][3 L + 2] scratch of the schedule kernel
   const float* chain_mask;   // [L] or null
   const int32_t* true_tokens; // [L] or null
   const uint64_t* seeds;  // [B]
@@ -134,19 +141,21 @@ struct DecodeArgs {
   int team;               // workgroups per sequence (set by launch_decode)
   uint32_t spin_limit;    // polls before a team barrier gives up (set by launch_decode)
   int precision;          // 0 fp32, 1 bf16, 2 fp16 weights and message rows (see decode_kernel)
-  int max_run;            // longest run of independent steps decoded together (<= 4 * team size)
+  int max_members;        // most steps one pass decodes (<= kDecodeGroup * team size)
 };
-// Group sizes and per-step neighbour lists (a.gsize, a.nbj, a.nbp) from the
-// orders, positions and kNN graph; launch_decode reads them.
+constexpr int kDecodeGroup = 4;  // steps one workgroup decodes in a pass
+// Per-step neighbour lists (a.nbj, a.nbp) and the pass schedule (a.sched,
+// a.pstart, a.npass, a.draw) from the orders, positions, mask and kNN graph;
+// launch_decode reads them.
 hipError_t launch_decode_schedule(const DecodeArgs& a, hipStream_t stream);
 // Workgroups per sequence the decode will use for B sequences (1..min(8, max_team)).
 int decode_team_size(int precision, int B, int max_team);
 // Decodes with up to min(8, max_team) workgroups per sequence when the whole
-// grid fits the device at once, else one per sequence; a.max_run must not
-// exceed 4 x that team size (the schedule has to be built for it). A team
-// launch that could not run its members together raises *a.fault (and leaves
-// NaN scores); rebuild the schedule with max_run = 4 and run it again with
-// max_team = 1.
+// grid fits the device at once, else one per sequence; a.max_members must not
+// exceed kDecodeGroup x that team size (the schedule has to be built for it).
+// A team launch that could not run its members together raises *a.fault (and
+// leaves NaN scores); rebuild the schedule with max_members = kDecodeGroup and
+// run it again with max_team = 1.
 hipError_t launch_decode(const ModelDev& m, const DecodeArgs& a, hipStream_t stream, int max_team = 8);
 // Q[l] = W1d_l h^0 (l < 3), Q[3] = W1a_0 h^0, without the E1 edge products.
 hipError_t launch_q_precompute(const ModelDev& m, const float* h_v, int L, float* Q, hipStream_t stream);

@@ -233,6 +233,49 @@ def test_design_team_split_is_exact(gpu_ctx, oracle, B, monkeypatch):
                  true_tokens=tt)
 
 
+@pytest.mark.parametrize("L,B,shared", [(120, 5, False), (300, 64, True)])
+def test_design_dependency_schedule_is_exact(gpu_ctx, oracle, L, B, shared, monkeypatch):
+    """Passes of steps whose earlier neighbours are done give the bits of one step per pass in order
+    (HKBS_DECODE_SCHEDULE=sequential), with inactive residues and a chain mask in the order."""
+    bb = backbone.single_chain(L, 8)
+    src = bb.atom_sources.copy()
+    src[[2, L // 2, L // 2 + 1, L - 1], 1] = 0
+    bb = backbone.Backbone(bb.coords, src)
+    cm = np.ones(L, np.float32)
+    cm[L // 4:L // 4 + 9] = 0.0
+    tt = (np.arange(L) * 3 % 20).astype(np.int32)
+    seeds = (np.arange(B) + 17).astype(np.uint64)
+    kw = dict(order_mode=_lib.ORDER_INPUT_SHARED, orders=_lib.decode_order(bb.atom_sources, 17)) if shared else \
+        dict(order_seeds=seeds)
+    out = {}
+    for mode in ("sequential", "dependency"):
+        monkeypatch.setenv("HKBS_DECODE_SCHEDULE", mode)
+        _say(f"design schedule={mode} L={L} B={B}")
+        out[mode] = gpu_ctx.design(bb.coords, bb.atom_sources, B, seeds, temperature=0.1, chain_mask=cm,
+                                   true_tokens=tt, **kw)
+    for key in ("tokens", "log_probs", "scores", "orders"):
+        np.testing.assert_array_equal(out["dependency"][key], out["sequential"][key], err_msg=key)
+    check_design(oracle, bb, {k: v[:2] for k, v in out["dependency"].items()}, seeds[:2], 0.1, chain_mask=cm,
+                 true_tokens=tt)
+
+
+def test_design_dependency_schedule_long_chain(gpu_ctx, monkeypatch):
+    """Above 8000 residues the schedule keeps its per-step tables in global memory: same bits as the
+    sequential schedule."""
+    L = 8100
+    bb = backbone.single_chain(L, 3)
+    seeds = np.array([9], dtype=np.uint64)
+    order = _lib.decode_order(bb.atom_sources, 9)
+    out = {}
+    for mode in ("sequential", "dependency"):
+        monkeypatch.setenv("HKBS_DECODE_SCHEDULE", mode)
+        _say(f"design schedule={mode} L={L}")
+        out[mode] = gpu_ctx.design(bb.coords, bb.atom_sources, 1, seeds, order_mode=_lib.ORDER_INPUT_SHARED,
+                                   orders=order, temperature=0.1)
+    for key in ("tokens", "log_probs", "scores"):
+        np.testing.assert_array_equal(out["dependency"][key], out["sequential"][key], err_msg=key)
+
+
 def test_design_team_barrier_timeout_reruns(gpu_ctx, monkeypatch):
     """A team barrier that gives up (forced here by a one-poll wait limit) leaves
     the kernel early with the fault word raised; the design call then decodes
