@@ -14,6 +14,7 @@
 #include <algorithm>
 #include <cmath>
 #include <cstdio>
+#include <cstdlib>
 #include <cstring>
 #include <map>
 #include <numeric>
@@ -712,10 +713,10 @@ hkbs_status upload_inputs(hkbs_pmpnn* ctx, DeviceArena& ar, const float* coords,
 }
 
 // Pass schedule of up to B orders: sched, pstart, npass, draw and scratch.
-size_t schedule_bytes(int L, int B) {
+size_t schedule_bytes(int L, int K, int B) {
   const size_t nq = (size_t)B;
   return 2 * aligned_bytes<int32_t>(nq * L) + aligned_bytes<int32_t>(nq * (L + 2)) + aligned_bytes<int32_t>(nq) +
-         aligned_bytes<int32_t>(nq * (3 * (size_t)L + 2));
+         aligned_bytes<int32_t>(sched_scratch_words(L, K, nq));
 }
 
 size_t decode_bytes(int L, int K, int B) {
@@ -725,7 +726,7 @@ size_t decode_bytes(int L, int K, int B) {
          aligned_bytes<float>((size_t)B * kLayers * L * kH) + aligned_bytes<int32_t>((size_t)B * L) +
          aligned_bytes<float>((size_t)B * L * kV) + aligned_bytes<float>((size_t)B * L) + aligned_bytes<float>(B) +
          aligned_bytes<uint32_t>((size_t)B + 1) + 2 * aligned_bytes<int32_t>((size_t)B * L * K) +
-         schedule_bytes(L, B);
+         schedule_bytes(L, K, B);
 }
 
 hkbs_status enter(hkbs_pmpnn* ctx) {
@@ -760,7 +761,7 @@ hkbs_status design_on_device(hkbs_pmpnn* ctx, const float* coords, const uint8_t
   int32_t* pstart = ar.take<int32_t>(nq * (L + 2));
   int32_t* npass = ar.take<int32_t>(nq);
   int32_t* draw = ar.take<int32_t>(nq * L);
-  int32_t* sched_tmp = ar.take<int32_t>(nq * (3 * (size_t)L + 2));
+  int32_t* sched_tmp = ar.take<int32_t>(sched_scratch_words(L, K, nq));
   ctx->fault = sync + B;
   if (ctx->timing) HK_CHECK(hipEventRecord(ctx->ev[0], ctx->stream), "event record failed");
   HK_CHECK(run_encode(ctx, coords, src, resid, chain, L, K, e), "encoder launch failed");
@@ -802,6 +803,8 @@ hkbs_status design_on_device(hkbs_pmpnn* ctx, const float* coords, const uint8_t
   a.precision = ctx->precision;
   const int team = decode_team_size(a.precision, B, 8);
   a.max_members = kDecodeGroup * team;
+  if (const char* env = std::getenv("HKBS_DECODE_MAX_MEMBERS"))
+    a.max_members = std::max(1, std::min(a.max_members, std::atoi(env)));
   ctx->last_decode = a;
   HK_CHECK(launch_decode_schedule(a, ctx->stream), "decode schedule launch failed");
   if (ctx->timing) HK_CHECK(hipEventRecord(ctx->ev[2], ctx->stream), "event record failed");

@@ -710,133 +710,251 @@ __global__ void neighbour_schedule_kernel(const int32_t* __restrict__ orders, co
   }
 }
 
-// Dependency schedule of one decoding order (one wave per order q). Step u
-// (residue order[u]) reads the state of every kNN neighbour decoded before it,
-// so it may run in the first pass after all of those steps' passes. Steps are
-// placed in order of u into the earliest such pass that holds fewer than
-// max_members steps (first fit). Every step then sees exactly the inputs of
-// sequential decoding, whatever pass it runs in. Inactive residues (mask 0)
-// read nothing and form pass 0, which runs before all others; entries outside
-// 0..L-1 are dropped. If the order is not a permutation (a residue repeated),
-// every active step gets a pass of its own, in order: sequential decoding
-// (also selected by sequential != 0; HKBS_DECODE_SCHEDULE=sequential).
+// Dependency schedule of each decoding order q. Step u (residue order[u])
+// reads the state of every kNN neighbour decoded before it, so it may run in
+// any pass after those steps' passes; each step then sees exactly the inputs
+// of sequential decoding, whatever pass it runs in. Pass p takes the
+// max_members smallest u among the steps whose earlier active neighbours are
+// all placed in passes < p (a ready list ordered by u). Inactive residues
+// (mask 0) read nothing and form pass 0, which runs before all others; entries
+// outside 0..L-1 are dropped. If the order is not a permutation (a residue
+// repeated), every active step gets a pass of its own, in order: sequential
+// decoding (also selected by HKBS_DECODE_SCHEDULE=sequential).
 // Outputs per order: sched [L] (steps grouped by pass, increasing u within a
 // pass), pstart [L + 2] (pass p holds sched[pstart[p] .. pstart[p + 1])),
 // npass (passes after pass 0) and draw [L] (index of the step's sampler draw
 // among the active steps: the sampler stream is consumed in order of u).
-// pass_of / fill live in LDS (kLds) or in the global scratch gpass / gfill.
-constexpr int kSchedLdsMaxL = 8000;  // pass_of [L] and fill [L + 2] in at most 64 KiB of dynamic LDS
+// Four kernels: pending-dependency and dependent counts over all (step, slot)
+// pairs; per order the permutation check, draw indices, pass 0 and the
+// dependents' offsets; the dependents lists; per order the pass loop, with
+// the pending counts as bytes in LDS.
+constexpr int kSchedThreads = 512;
+constexpr int kSchedMaxL = 60000;  // pending counts as L bytes of LDS
 
-template <bool kLds>
-__global__ __launch_bounds__(64) void dag_schedule_kernel(const int32_t* __restrict__ orders,
-                                                          const int32_t* __restrict__ pos,
-                                                          const float* __restrict__ mask,
-                                                          const int32_t* __restrict__ nbp, int L, int K,
-                                                          int max_members, int sequential,
-                                                          int32_t* __restrict__ sched,
-                                                          int32_t* __restrict__ pstart, int32_t* __restrict__ npass,
-                                                          int32_t* __restrict__ draw, int32_t* __restrict__ gpass,
-                                                          int32_t* __restrict__ gfill, int32_t* __restrict__ gslot) {
-  extern __shared__ int32_t sched_lds[];
+// Active step u of order q: valid residue with mask != 0.
+__device__ inline bool sched_active(const int32_t* order, const float* mask, int L, int u) {
+  const int t = order[u];
+  return t >= 0 && t < L && mask[t] != 0.0F;
+}
+
+// indeg[q][u]: earlier active neighbours of active step u; dcnt[q][p]: later
+// active steps that have step p as an earlier neighbour. Both zero on entry.
+__global__ void dep_count_kernel(const int32_t* __restrict__ orders, const float* __restrict__ mask,
+                                 const int32_t* __restrict__ nbp, int L, int K, int32_t* __restrict__ indeg,
+                                 int32_t* __restrict__ dcnt) {
+  const int q = blockIdx.y;
+  const int32_t* order = orders + (size_t)q * L;
+  const int32_t* np = nbp + (size_t)q * L * K;
+  const size_t n = (size_t)L * K;
+  for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x) {
+    const int u = (int)(i / K);
+    const int p = np[i];
+    if (p >= u || p < 0 || !sched_active(order, mask, L, u) || !sched_active(order, mask, L, p)) continue;
+    atomicAdd(indeg + (size_t)q * L + u, 1);
+    atomicAdd(dcnt + (size_t)q * (L + 1) + p, 1);
+  }
+}
+
+// Block-wide exclusive prefix sum of v over kSchedThreads threads; *total
+// receives the sum. Uses 8 words of LDS at tmp; ends with a barrier.
+__device__ inline int block_scan(int v, int* tmp, int* total) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  int inc = v;
+#pragma unroll
+  for (int d = 1; d < 64; d <<= 1) {
+    const int o = __shfl_up(inc, d, 64);
+    if (lane >= d) inc += o;
+  }
+  if (lane == 63) tmp[wave] = inc;
+  __syncthreads();
+  int before = 0, all = 0;
+#pragma unroll
+  for (int w = 0; w < kSchedThreads / 64; ++w) {
+    const int x = tmp[w];
+    before += w < wave ? x : 0;
+    all += x;
+  }
+  *total = all;
+  __syncthreads();
+  return before + inc - v;
+}
+
+// Per order (one block): permutation flag, draw indices, pass 0 (inactive
+// steps in order), exclusive offsets of the dependents lists (dcnt -> off, in
+// place, off[L] = total) and meta = {permutation, active steps, inactive steps}.
+__global__ __launch_bounds__(kSchedThreads) void sched_prep_kernel(const int32_t* __restrict__ orders,
+                                                                   const int32_t* __restrict__ pos,
+                                                                   const float* __restrict__ mask, int L,
+                                                                   int sequential, int32_t* __restrict__ off,
+                                                                   int32_t* __restrict__ draw,
+                                                                   int32_t* __restrict__ sched,
+                                                                   int32_t* __restrict__ pstart,
+                                                                   int32_t* __restrict__ meta) {
+  __shared__ int tmp[kSchedThreads / 64];
+  __shared__ int bad;
   const int q = blockIdx.x;
-  const int lane = threadIdx.x;
   const int32_t* order = orders + (size_t)q * L;
   const int32_t* pq = pos + (size_t)q * L;
+  int32_t* oq = off + (size_t)q * (L + 1);
+  int32_t* dq = draw + (size_t)q * L;
+  int32_t* sq = sched + (size_t)q * L;
+  if (threadIdx.x == 0) bad = sequential;
+  __syncthreads();
+  for (int u = threadIdx.x; u < L; u += kSchedThreads) {
+    const int t = order[u];
+    if (t < 0 || t >= L || pq[t] != u) bad = 1;
+  }
+  int act = 0, inact = 0, deps = 0;
+  for (int u0 = 0; u0 < L; u0 += kSchedThreads) {
+    const int u = u0 + threadIdx.x;
+    const bool valid = u < L && order[u] >= 0 && order[u] < L;
+    const bool a = valid && mask[order[u]] != 0.0F;
+    const bool z = valid && !a;
+    int tot;
+    const int ra = block_scan(a ? 1 : 0, tmp, &tot);
+    if (u < L) dq[u] = a ? act + ra : -1;
+    act += tot;
+    const int rz = block_scan(z ? 1 : 0, tmp, &tot);
+    if (z) sq[inact + rz] = u;
+    inact += tot;
+    const int c = u < L ? oq[u] : 0;
+    const int rc = block_scan(c, tmp, &tot);
+    if (u < L) oq[u] = deps + rc;
+    deps += tot;
+  }
+  if (threadIdx.x == 0) {
+    oq[L] = deps;
+    int32_t* ps = pstart + (size_t)q * (L + 2);
+    ps[0] = 0;
+    ps[1] = inact;
+    meta[(size_t)q * 4 + 0] = !bad;
+    meta[(size_t)q * 4 + 1] = act;
+    meta[(size_t)q * 4 + 2] = inact;
+  }
+}
+
+// dlist[q][off[p] ..]: the later active steps that wait for step p (any order
+// inside a list). cur is zero on entry.
+__global__ void dep_fill_kernel(const int32_t* __restrict__ orders, const float* __restrict__ mask,
+                                const int32_t* __restrict__ nbp, int L, int K, const int32_t* __restrict__ off,
+                                int32_t* __restrict__ cur, int32_t* __restrict__ dlist) {
+  const int q = blockIdx.y;
+  const int32_t* order = orders + (size_t)q * L;
   const int32_t* np = nbp + (size_t)q * L * K;
-  int32_t* pass_of = kLds ? sched_lds : gpass + (size_t)q * L;
-  int32_t* fill = kLds ? sched_lds + L : gfill + (size_t)q * (L + 2);
-  int32_t* slot = gslot + (size_t)q * L;
+  const size_t n = (size_t)L * K;
+  for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x) {
+    const int u = (int)(i / K);
+    const int p = np[i];
+    if (p >= u || p < 0 || !sched_active(order, mask, L, u) || !sched_active(order, mask, L, p)) continue;
+    const int slot = atomicAdd(cur + (size_t)q * L + p, 1);
+    dlist[(size_t)q * L * K + off[(size_t)q * (L + 1) + p] + slot] = u;
+  }
+}
+
+// Pending count of step u: byte u of the packed LDS words; 0xFF = placed,
+// inactive or dropped.
+__device__ inline int sched_pending(const uint32_t* w, int u) { return (w[u >> 2] >> (8 * (u & 3))) & 0xFF; }
+
+// Per order (one block): the pass loop. Pass p scans the steps from the first
+// unplaced one, in blocks of kSchedThreads, for ready ones (pending count 0)
+// until it holds max_members, then clears their dependents' counts.
+__global__ __launch_bounds__(kSchedThreads) void ready_schedule_kernel(
+    const int32_t* __restrict__ orders, const float* __restrict__ mask, int L, int K, int max_members,
+    const int32_t* __restrict__ indeg, const int32_t* __restrict__ off, const int32_t* __restrict__ dlist,
+    const int32_t* __restrict__ draw, const int32_t* __restrict__ meta, int32_t* __restrict__ sched,
+    int32_t* __restrict__ pstart, int32_t* __restrict__ npass) {
+  extern __shared__ __attribute__((aligned(16))) uint32_t pend[];  // ceil(L / 4) words
+  __shared__ int tmp[kSchedThreads / 64];
+  __shared__ int chosen[256];
+  __shared__ int low_s, found_s;
+  const int q = blockIdx.x;
+  const int32_t* order = orders + (size_t)q * L;
+  const int32_t* ig = indeg + (size_t)q * L;
+  const int32_t* oq = off + (size_t)q * (L + 1);
+  const int32_t* dl = dlist + (size_t)q * L * K;
   int32_t* sq = sched + (size_t)q * L;
   int32_t* ps = pstart + (size_t)q * (L + 2);
-  int32_t* dq = draw + (size_t)q * L;
-  for (int i = lane; i < L + 2; i += 64) fill[i] = 0;
-  bool perm = true;
-  for (int u = lane; u < L; u += 64) {
-    const int t = order[u];
-    perm = perm && t >= 0 && t < L && pq[t] == u;
-  }
-  perm = __all(perm) && !sequential;
-  __builtin_amdgcn_s_waitcnt(0);
-  __syncthreads();
-  // Steps are read 16 at a time (all loads of a chunk in flight together);
-  // the placement itself is sequential in u.
-  constexpr int kChunk = 16;
-  int last = 0, ndraw = 0;
-  for (int u0 = 0; u0 < L; u0 += kChunk) {
-    int tt[kChunk], pp[kChunk];
-    float mm[kChunk];
-#pragma unroll
-    for (int c = 0; c < kChunk; ++c) {
-      const int u = u0 + c;
-      tt[c] = u < L ? order[u] : -1;
-      pp[c] = (u < L && lane < K) ? np[(size_t)u * K + lane] : L;
-    }
-#pragma unroll
-    for (int c = 0; c < kChunk; ++c) mm[c] = (tt[c] >= 0 && tt[c] < L) ? mask[tt[c]] : 0.0F;
-#pragma unroll
-    for (int c = 0; c < kChunk; ++c) {
-      const int u = u0 + c;
-      int r;
-      if (u >= L) {
-        continue;
-      } else if (tt[c] < 0 || tt[c] >= L) {
-        r = -1;
-      } else if (mm[c] == 0.0F) {
-        r = 0;
-      } else if (perm) {
-        int need = 1;
-        if (pp[c] < u) {
-          const int p = pp[c];
-          const int before =
-              kLds ? pass_of[p] : __hip_atomic_load(pass_of + p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-          need = before + 1;
-        }
-        r = static_cast<int>(wave_max(static_cast<float>(need)));
-        while ((kLds ? fill[r] : __hip_atomic_load(fill + r, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP)) >=
-               max_members)
-          ++r;
-      } else {
-        r = last + 1;
+  const int perm = meta[(size_t)q * 4 + 0], nact = meta[(size_t)q * 4 + 1], n0 = meta[(size_t)q * 4 + 2];
+  const int32_t* dq = draw + (size_t)q * L;
+  if (!perm) {
+    // One pass per active step, in order of u.
+    for (int u = threadIdx.x; u < L; u += kSchedThreads) {
+      const int d = dq[u];
+      if (d >= 0) {
+        sq[n0 + d] = u;
+        ps[1 + d + 1] = n0 + d + 1;
       }
-      if (lane == 0) {
-        dq[u] = r > 0 ? ndraw : -1;
-        if (r >= 0) {
-          const int f = kLds ? fill[r] : __hip_atomic_load(fill + r, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-          slot[u] = f;
-          if (kLds) {
-            pass_of[u] = r;
-            fill[r] = f + 1;
-          } else {
-            __hip_atomic_store(pass_of + u, r, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-            __hip_atomic_store(fill + r, f + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-          }
-        } else if (kLds) {
-          pass_of[u] = -1;
-        } else {
-          __hip_atomic_store(pass_of + u, -1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    }
+    if (threadIdx.x == 0) {
+      ps[1] = n0;
+      npass[q] = nact;
+    }
+    return;
+  }
+  const int words = (L + 3) / 4;
+  for (int w = threadIdx.x; w < words; w += kSchedThreads) {
+    uint32_t v = 0;
+    for (int b = 0; b < 4; ++b) {
+      const int u = 4 * w + b;
+      const uint32_t c = (u < L && sched_active(order, mask, L, u)) ? (uint32_t)min(ig[u], 254) : 0xFFu;
+      v |= c << (8 * b);
+    }
+    pend[w] = v;
+  }
+  if (threadIdx.x == 0) low_s = 0;
+  __syncthreads();
+  int placed = 0, pass = 0, out = n0;
+  const int cap = min(max_members, 256);
+  while (placed < nact) {
+    ++pass;
+    int found = 0;
+    for (int cursor = low_s; found < cap && cursor < L; cursor += kSchedThreads) {
+      const int u = cursor + threadIdx.x;
+      const bool rdy = u < L && sched_pending(pend, u) == 0;
+      int tot;
+      const int rank = block_scan(rdy ? 1 : 0, tmp, &tot);
+      if (rdy && found + rank < cap) chosen[found + rank] = u;
+      found = min(cap, found + tot);
+    }
+    // The first unplaced step is always ready (its earlier neighbours are all
+    // placed); taking it when nothing was found guarantees progress.
+    if (found == 0) {
+      if (threadIdx.x == 0) chosen[0] = low_s;
+      found = 1;
+    }
+    __syncthreads();
+    // chosen[0 .. found) is increasing in u: the pass's members in order.
+    for (int i = threadIdx.x; i < found; i += kSchedThreads) {
+      const int u = chosen[i];
+      sq[out + i] = u;
+      atomicOr(pend + (u >> 2), 0xFFu << (8 * (u & 3)));
+    }
+    if (threadIdx.x == 0) ps[pass] = out;
+    // Dependents: wave w takes members w, w + 8, ...; lane j their j-th dependent.
+    {
+      const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+      for (int i = wave; i < found; i += kSchedThreads / 64) {
+        const int u = chosen[i];
+        const int b = oq[u], e = oq[u + 1];
+        for (int j = b + lane; j < e; j += 64) {
+          const int v = dl[j];
+          atomicSub(pend + (v >> 2), 1u << (8 * (v & 3)));
         }
       }
-      if (!kLds) __builtin_amdgcn_s_waitcnt(0);
-      if (r > 0) ++ndraw;
-      last = r > last ? r : last;
     }
-  }
-  __builtin_amdgcn_s_waitcnt(0);
-  __syncthreads();
-  if (lane == 0) {
-    int at = 0;
-    for (int p = 0; p <= last; ++p) {
-      ps[p] = at;
-      at += fill[p];
+    __syncthreads();
+    if (threadIdx.x == 0) {
+      int lo = low_s;
+      while (lo < L && sched_pending(pend, lo) == 0xFF) ++lo;
+      low_s = lo;
     }
-    ps[last + 1] = at;
-    npass[q] = last;
+    out += found;
+    placed += found;
+    __syncthreads();
   }
-  __builtin_amdgcn_s_waitcnt(0);
-  __syncthreads();
-  for (int u = lane; u < L; u += 64) {
-    const int r = pass_of[u];
-    if (r >= 0) sq[ps[r] + slot[u]] = u;
+  if (threadIdx.x == 0) {
+    ps[pass + 1] = out;
+    npass[q] = pass;
   }
 }
 
@@ -876,19 +994,23 @@ hipError_t launch_decode_schedule(const DecodeArgs& a, hipStream_t stream) {
   neighbour_schedule_kernel<<<dim3((unsigned)std::min<size_t>((n + 255) / 256, 4096), nq), 256, 0, stream>>>(
       a.orders, a.pos, a.idx, a.L, a.K, a.nbj, a.nbp);
   const char* mode = std::getenv("HKBS_DECODE_SCHEDULE");
-  const int sequential = mode && std::strcmp(mode, "sequential") == 0;
+  const int sequential = (mode && std::strcmp(mode, "sequential") == 0) || a.L > kSchedMaxL;
   if (a.max_members < 1) return hipErrorInvalidValue;
-  if (a.L <= kSchedLdsMaxL) {
-    dag_schedule_kernel<true><<<nq, 64, sizeof(int32_t) * (2 * (size_t)a.L + 2), stream>>>(
-        a.orders, a.pos, a.mask, a.nbp, a.L, a.K, a.max_members, sequential, a.sched, a.pstart, a.npass, a.draw,
-        nullptr, nullptr, a.sched_tmp);
-  } else {
-    int32_t* gpass = a.sched_tmp + (size_t)nq * a.L;
-    int32_t* gfill = gpass + (size_t)nq * a.L;
-    dag_schedule_kernel<false><<<nq, 64, 0, stream>>>(a.orders, a.pos, a.mask, a.nbp, a.L, a.K, a.max_members,
-                                                      sequential, a.sched, a.pstart, a.npass, a.draw, gpass, gfill,
-                                                      a.sched_tmp);
-  }
+  const size_t L = (size_t)a.L;
+  int32_t* indeg = a.sched_tmp;            // [nq][L]
+  int32_t* off = indeg + nq * L;           // [nq][L + 1]: counts, then offsets
+  int32_t* cur = off + nq * (L + 1);       // [nq][L]
+  int32_t* meta = cur + nq * L;            // [nq][4]
+  int32_t* dlist = meta + nq * 4;          // [nq][L K]
+  hipError_t err = launch_zero(reinterpret_cast<float*>(indeg), nq * (3 * L + 1), stream);
+  if (err != hipSuccess) return err;
+  const unsigned blocks = (unsigned)std::min<size_t>((n + 255) / 256, 2048);
+  dep_count_kernel<<<dim3(blocks, nq), 256, 0, stream>>>(a.orders, a.mask, a.nbp, a.L, a.K, indeg, off);
+  sched_prep_kernel<<<nq, kSchedThreads, 0, stream>>>(a.orders, a.pos, a.mask, a.L, sequential, off, a.draw, a.sched,
+                                                     a.pstart, meta);
+  dep_fill_kernel<<<dim3(blocks, nq), 256, 0, stream>>>(a.orders, a.mask, a.nbp, a.L, a.K, off, cur, dlist);
+  ready_schedule_kernel<<<nq, kSchedThreads, sizeof(uint32_t) * ((L + 3) / 4), stream>>>(
+      a.orders, a.mask, a.L, a.K, a.max_members, indeg, off, dlist, a.draw, meta, a.sched, a.pstart, a.npass);
   return hipGetLastError();
 }
 

@@ -124,7 +124,7 @@ struct DecodeArgs {
   int32_t* pstart;        // [nq][L + 2]
   int32_t* npass;         // [nq]
   int32_t* draw;          // [nq][L]: sampler draw index of each active step, -1 otherwise
-  int32_t* sched_tmp;     // [nq][3 L + 2] scratch of the schedule kernel
+  int32_t* sched_tmp;     // scratch of the schedule kernels: sched_scratch_words(L, K, nq) words
   const float* chain_mask;   // [L] or null
   const int32_t* true_tokens; // [L] or null
   const uint64_t* seeds;  // [B]
@@ -144,6 +144,8 @@ struct DecodeArgs {
   int max_members;        // most steps one pass decodes (<= kDecodeGroup * team size)
 };
 constexpr int kDecodeGroup = 4;  // steps one workgroup decodes in a pass
+// int32 words of DecodeArgs.sched_tmp for nq orders of length L with K neighbours.
+inline size_t sched_scratch_words(size_t L, size_t K, size_t nq) { return nq * (3 * L + 1 + 4 + L * K); }
 // Per-step neighbour lists (a.nbj, a.nbp) and the pass schedule (a.sched,
 // a.pstart, a.npass, a.draw) from the orders, positions, mask and kNN graph;
 // launch_decode reads them.

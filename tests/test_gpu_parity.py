@@ -260,8 +260,7 @@ def test_design_dependency_schedule_is_exact(gpu_ctx, oracle, L, B, shared, monk
 
 
 def test_design_dependency_schedule_long_chain(gpu_ctx, monkeypatch):
-    """Above 8000 residues the schedule keeps its per-step tables in global memory: same bits as the
-    sequential schedule."""
+    """A long chain (8,100 residues, 260 passes of up to 32 steps): same bits as the sequential schedule."""
     L = 8100
     bb = backbone.single_chain(L, 3)
     seeds = np.array([9], dtype=np.uint64)
