@@ -79,7 +79,8 @@ __device__ inline float gelu(float x) {
 // The same GELU formula for the decode loop, which is held to a tolerance
 // rather than to bit identity: the exp table is read from LDS (tbl = 17
 // floats, kExpNegTable), 1/(1 + p v) uses the hardware reciprocal (1 ulp),
-// and the range checks that cannot fire for |v| <= 4 are dropped.
+// and the whole formula is evaluated for every lane with the v > 4 and sign
+// cases as selects (no branch around the table load).
 __device__ inline float gelu_fast(float x, const float* tbl) {
   const float v = fabsf(x) * 0.7071067811865475F;
   const float t = __builtin_amdgcn_rcpf(1.0F + 0.3275911F * v);
@@ -93,7 +94,9 @@ __device__ inline float gelu_fast(float x, const float* tbl) {
       r * (1.0F +
            r * (0.5F +
                 r * (1.0F / 6.0F + r * (1.0F / 24.0F + r * (1.0F / 120.0F + r * (1.0F / 720.0F))))));
-  float erfv = v > 4.0F ? 1.0F : 1.0F - poly * (tbl[n] * e);
+  const float ex = tbl[n];
+  const float mag = 1.0F - poly * (ex * e);
+  float erfv = v > 4.0F ? 1.0F : mag;
   erfv = x < 0.0F ? -erfv : erfv;
   return 0.5F * x * (1.0F + erfv);
 }
