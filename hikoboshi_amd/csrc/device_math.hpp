@@ -260,6 +260,45 @@ __device__ inline void seq_gemm(float (&acc)[RM][CN], const float* A, int lda, i
 // Welford LayerNorm of one 128-wide row read from a k-major LDS column
 // (x[d * ld]), written to out[d * ld] (may alias). Reference order of
 // cpp/primitives/compute/layer_norm_scalar.cpp:8-40, eps 1e-5.
+// Welford mean and 1 / sqrt(var + eps) of 128 values x[d * ld] in the
+// reference's order (the statistics half of welford_ln_col).
+__device__ inline void welford_stats_col(const float* x, int ld, float* mean_out, float* inv_out) {
+#pragma clang fp contract(off)
+  float mean = 0.0F, m2 = 0.0F;
+  for (int d = 0; d < 128; ++d) {
+    const float v = x[d * ld];
+    const float count = static_cast<float>(d + 1);
+    const float delta = v - mean;
+    mean += delta / count;
+    const float delta2 = v - mean;
+    m2 += delta * delta2;
+  }
+  const float var = m2 / 128.0F;
+  *mean_out = mean;
+  *inv_out = 1.0F / sqrtf(var + 1.0e-5F);
+}
+
+// LayerNorm of the rows r < rows of a column-major LDS tile (x[d * ld + r],
+// d < 128) into out (may alias x), for rows with valid(r): thread r computes
+// row r's Welford statistics (the reference's recurrence) into stat [2 *
+// rows], then the whole block normalises the elements in parallel with the
+// reference's per-element expression. Starts and ends with a barrier.
+template <typename Valid>
+__device__ inline void ln_cols_block(const float* x, float* out, int ld, int rows, const float* __restrict__ g,
+                                     const float* __restrict__ b, float* stat, Valid valid) {
+#pragma clang fp contract(off)
+  __syncthreads();
+  if ((int)threadIdx.x < rows && valid((int)threadIdx.x))
+    welford_stats_col(x + threadIdx.x, ld, stat + threadIdx.x, stat + rows + threadIdx.x);
+  __syncthreads();
+  for (int i = threadIdx.x; i < rows * 128; i += blockDim.x) {
+    const int r = i % rows, d = i / rows;
+    if (!valid(r)) continue;
+    out[d * ld + r] = (x[d * ld + r] - stat[r]) * stat[rows + r] * g[d] + b[d];
+  }
+  __syncthreads();
+}
+
 __device__ inline void welford_ln_col(const float* x, float* out, int ld, const float* __restrict__ g,
                                       const float* __restrict__ b) {
 #pragma clang fp contract(off)

@@ -175,9 +175,25 @@ __global__ __launch_bounds__(256) void node_kernel(EncLayerDev w, const float* _
   static_assert(NR == 4, "thread mapping");
 
   // upd = sum over valid slots, in order, of (1/30) mask_i mask_j m_ij; then
-  // X = h + upd (axpy order: 1 * residual + input). Thread t owns column
-  // t % 128 of rows 2 (t / 128) + {0, 1}; a row's K messages, neighbour
-  // indices and masks are all loaded before the sum starts.
+  // X = h + upd (axpy order: 1 * residual + input). The weight of each
+  // (row, slot) is computed once into LDS (0 for an invalid slot); thread t
+  // owns column t % 128 of rows 2 (t / 128) + {0, 1}, issues all of its
+  // message loads at once and sums them in slot order.
+  __shared__ float alpha_s[NR * kKmax];
+  if (t < NR * kKmax) {
+    const int row = t / kKmax, k = t % kKmax;
+    float alpha = 0.0F;
+    if (row < nr && k < K) {
+      const int r = r0 + row;
+      const int j = idx[(size_t)r * K + k];
+      if (j >= 0 && j < L) {
+        alpha = 1.0F / 30.0F;
+        alpha *= mask[r] * mask[j];
+      }
+    }
+    alpha_s[t] = alpha;
+  }
+  __syncthreads();
   {
     const int d = t % kH, rb = 2 * (t / kH);
     for (int q = 0; q < 2; ++q) {
@@ -185,21 +201,14 @@ __global__ __launch_bounds__(256) void node_kernel(EncLayerDev w, const float* _
       float v = 0.0F;
       if (row < nr) {
         const int r = r0 + row;
-        float mv[kKmax], mj[kKmax];
+        float mv[kKmax];
 #pragma unroll
-        for (int k = 0; k < kKmax; ++k) {
-          const int j = k < K ? idx[(size_t)r * K + k] : -1;
-          const bool valid = j >= 0 && j < L;
-          mv[k] = valid ? msg[((size_t)r * K + k) * kH + d] : 0.0F;
-          mj[k] = valid ? mask[j] : 0.0F;
-        }
-        const float mr = mask[r];
+        for (int k = 0; k < kKmax; ++k) mv[k] = k < K ? msg[((size_t)r * K + k) * kH + d] : 0.0F;
         float upd = 0.0F;
 #pragma unroll
         for (int k = 0; k < kKmax; ++k) {
-          float alpha = 1.0F / 30.0F;
-          alpha *= mr * mj[k];
-          if (alpha == 0.0F) continue;  // also every invalid slot (mj = 0)
+          const float alpha = alpha_s[row * kKmax + k];
+          if (alpha == 0.0F) continue;  // also every invalid slot
           upd = alpha * mv[k] + upd;
         }
         v = h_v[(size_t)r * kH + d] + upd;
@@ -208,7 +217,15 @@ __global__ __launch_bounds__(256) void node_kernel(EncLayerDev w, const float* _
     }
   }
   __syncthreads();
-  if (t < NR) welford_ln_col(X + t, H1 + t, NR, w.n1g, w.n1b);
+  // LayerNorms: Welford statistics of each row by one thread (the reference's
+  // sequential recurrence), then every element normalised in parallel.
+  __shared__ float ln_mean[NR], ln_inv[NR];
+  if (t < NR) welford_stats_col(X + t, NR, ln_mean + t, ln_inv + t);
+  __syncthreads();
+  for (int i = t; i < NR * kH; i += blockDim.x) {
+    const int row = i % NR, d = i / NR;
+    H1[i] = (X[i] - ln_mean[row]) * ln_inv[row] * w.n1g[d] + w.n1b[d];
+  }
   __syncthreads();
   {
     // W_in: columns t and t + 256 of all rows, then GELU
@@ -229,10 +246,13 @@ __global__ __launch_bounds__(256) void node_kernel(EncLayerDev w, const float* _
     for (int r = 0; r < 2; ++r) X[c * NR + rr + r] = H1[c * NR + rr + r] + (acc[0][r] + w.bout[c]);
   }
   __syncthreads();
-  if (t < NR) {
-    welford_ln_col(X + t, H2 + t, NR, w.n2g, w.n2b);
-    const float mk = t < nr ? mask[r0 + t] : 0.0F;
-    for (int d = 0; d < kH; ++d) H2[d * NR + t] *= mk;
+  if (t < NR) welford_stats_col(X + t, NR, ln_mean + t, ln_inv + t);
+  __syncthreads();
+  for (int i = t; i < NR * kH; i += blockDim.x) {
+    const int row = i % NR, d = i / NR;
+    float v = (X[i] - ln_mean[row]) * ln_inv[row] * w.n2g[d] + w.n2b[d];
+    v *= row < nr ? mask[r0 + row] : 0.0F;
+    H2[i] = v;
   }
   __syncthreads();
   for (int i = t; i < nr * kH; i += blockDim.x) {
@@ -308,12 +328,13 @@ __global__ __launch_bounds__(256) void edge_update_kernel(EncLayerDev w, float* 
       const int row = row0 + i, c = col0 + j;
       A[c * kLdE + row] = (row < n_rows) ? h_e[(slot0 + row) * kH + c] + (acc[i][j] + w.b13[c]) : 0.0F;
     }
-  __syncthreads();
-  if (threadIdx.x < n_rows) {
-    const int j = idx[slot0 + threadIdx.x];
-    if (j >= 0 && j < L) welford_ln_col(A + threadIdx.x, A + threadIdx.x, kLdE, w.n3g, w.n3b);
+  __shared__ float ln_stat[2 * kRows];
+  __shared__ int row_ok[kRows];
+  if (threadIdx.x < kRows) {
+    const int j = (int)threadIdx.x < n_rows ? idx[slot0 + threadIdx.x] : -1;
+    row_ok[threadIdx.x] = j >= 0 && j < L;
   }
-  __syncthreads();
+  ln_cols_block(A, A, kLdE, n_rows, w.n3g, w.n3b, ln_stat, [&](int r) { return row_ok[r] != 0; });
   for (int i = threadIdx.x; i < n_rows * kH; i += blockDim.x) {
     const int row = i / kH, c = i % kH;
     const int j = idx[slot0 + row];

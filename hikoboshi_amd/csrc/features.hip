@@ -148,8 +148,8 @@ __global__ __launch_bounds__(256) void edge_embed_kernel(ModelDev m, const float
   for (int i = 0; i < 4; ++i)
 #pragma unroll
     for (int j = 0; j < 4; ++j) X[(col0 + j) * kLdT + row0 + i] = acc[i][j];
-  __syncthreads();
-  if (threadIdx.x < kTile) welford_ln_col(X + threadIdx.x, A + threadIdx.x, kLdT, m.ne_g, m.ne_b);
+  __shared__ float ln_stat[2 * kTile];
+  ln_cols_block(X, A, kLdT, kTile, m.ne_g, m.ne_b, ln_stat, [](int) { return true; });
 #pragma unroll
   for (int i = 0; i < 4; ++i)
 #pragma unroll
