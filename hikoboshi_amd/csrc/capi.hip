@@ -406,6 +406,9 @@ void residue_mask_host(const uint8_t* src, int L, std::vector<float>& mask) {
 struct hkbs_pmpnn {
   int device = 0;
   hipStream_t stream = nullptr;
+  hipStream_t side = nullptr;   // builds the decode schedule while the encoder runs
+  hipEvent_t fork = nullptr;    // kNN graph ready (recorded on stream)
+  hipEvent_t join = nullptr;    // schedule ready (recorded on side)
   float* weights = nullptr;
   ModelDev model{};
   DeviceArena arena;
@@ -763,12 +766,6 @@ hkbs_status design_on_device(hkbs_pmpnn* ctx, const float* coords, const uint8_t
   int32_t* draw = ar.take<int32_t>(nq * L);
   int32_t* sched_tmp = ar.take<int32_t>(sched_scratch_words(L, K, nq));
   ctx->fault = sync + B;
-  if (ctx->timing) HK_CHECK(hipEventRecord(ctx->ev[0], ctx->stream), "event record failed");
-  HK_CHECK(run_encode(ctx, coords, src, resid, chain, L, K, e), "encoder launch failed");
-  if (ctx->timing) HK_CHECK(hipEventRecord(ctx->ev[1], ctx->stream), "event record failed");
-  HK_CHECK(launch_decoder_precompute(ctx->model, e.h_v, e.h_e, L, K, E1, Q, ctx->stream), "decoder precompute failed");
-  HK_CHECK(launch_positions(orders, L, shared ? 1 : B, shared, pos, ctx->stream), "position kernel failed");
-  HK_CHECK(launch_zero(reinterpret_cast<float*>(sync), (size_t)B + 1, ctx->stream), "workspace clear failed");
   DecodeArgs a{};
   a.idx = e.idx;
   a.mask = e.mask;
@@ -806,7 +803,23 @@ hkbs_status design_on_device(hkbs_pmpnn* ctx, const float* coords, const uint8_t
   if (const char* env = std::getenv("HKBS_DECODE_MAX_MEMBERS"))
     a.max_members = std::max(1, std::min(a.max_members, std::atoi(env)));
   ctx->last_decode = a;
-  HK_CHECK(launch_decode_schedule(a, ctx->stream), "decode schedule launch failed");
+  // The decode schedule needs only the kNN graph and the orders: it is built
+  // on the side stream while the encoder runs, and the decode waits for it.
+  if (ctx->timing) HK_CHECK(hipEventRecord(ctx->ev[0], ctx->stream), "event record failed");
+  HK_CHECK(launch_knn(coords, src, L, K, e.idx, e.d2, e.mask, e.ca, ctx->stream), "kNN launch failed");
+  HK_CHECK(hipEventRecord(ctx->fork, ctx->stream), "event record failed");
+  HK_CHECK(hipStreamWaitEvent(ctx->side, ctx->fork, 0), "stream wait failed");
+  HK_CHECK(launch_positions(orders, L, shared ? 1 : B, shared, pos, ctx->side), "position kernel failed");
+  HK_CHECK(launch_decode_schedule(a, ctx->side), "decode schedule launch failed");
+  HK_CHECK(hipEventRecord(ctx->join, ctx->side), "event record failed");
+  HK_CHECK(launch_edge_embed(ctx->model, coords, src, resid, chain, e.idx, L, K, e.h_e, ctx->stream),
+           "encoder launch failed");
+  HK_CHECK(launch_encoder(ctx->model, e.idx, e.mask, L, K, e.h_v, e.h_e, e.scratch, ctx->stream),
+           "encoder launch failed");
+  if (ctx->timing) HK_CHECK(hipEventRecord(ctx->ev[1], ctx->stream), "event record failed");
+  HK_CHECK(launch_decoder_precompute(ctx->model, e.h_v, e.h_e, L, K, E1, Q, ctx->stream), "decoder precompute failed");
+  HK_CHECK(launch_zero(reinterpret_cast<float*>(sync), (size_t)B + 1, ctx->stream), "workspace clear failed");
+  HK_CHECK(hipStreamWaitEvent(ctx->stream, ctx->join, 0), "stream wait failed");
   if (ctx->timing) HK_CHECK(hipEventRecord(ctx->ev[2], ctx->stream), "event record failed");
   HK_CHECK(launch_decode(ctx->model, a, ctx->stream, team), "decode launch failed");
   if (ctx->timing) {
@@ -868,8 +881,11 @@ hkbs_status hkbs_pmpnn_create(const uint8_t* data, size_t nbytes, int32_t device
   if (hipSetDevice(device) != hipSuccess) return fail(HKBS_UNAVAILABLE, "HIP device is not available");
   hkbs_pmpnn* ctx = new hkbs_pmpnn();
   ctx->device = device;
-  if (hipStreamCreateWithFlags(&ctx->stream, hipStreamNonBlocking) != hipSuccess) {
-    delete ctx;
+  if (hipStreamCreateWithFlags(&ctx->stream, hipStreamNonBlocking) != hipSuccess ||
+      hipStreamCreateWithFlags(&ctx->side, hipStreamNonBlocking) != hipSuccess ||
+      hipEventCreateWithFlags(&ctx->fork, hipEventDisableTiming) != hipSuccess ||
+      hipEventCreateWithFlags(&ctx->join, hipEventDisableTiming) != hipSuccess) {
+    hkbs_pmpnn_destroy(ctx);
     return fail(HKBS_UNAVAILABLE, "HIP stream creation failed");
   }
   const hkbs_status st = build_model(ctx, ptrs.data());
@@ -885,8 +901,12 @@ void hkbs_pmpnn_destroy(hkbs_pmpnn* ctx) {
   if (!ctx) return;
   (void)hipSetDevice(ctx->device);
   if (ctx->stream) (void)hipStreamSynchronize(ctx->stream);
+  if (ctx->side) (void)hipStreamSynchronize(ctx->side);
   for (hipEvent_t& ev : ctx->ev)
     if (ev) (void)hipEventDestroy(ev);
+  if (ctx->fork) (void)hipEventDestroy(ctx->fork);
+  if (ctx->join) (void)hipEventDestroy(ctx->join);
+  if (ctx->side) (void)hipStreamDestroy(ctx->side);
   if (ctx->arena.base) (void)hipFree(ctx->arena.base);
   if (ctx->weights) (void)hipFree(ctx->weights);
   if (ctx->stream) (void)hipStreamDestroy(ctx->stream);
