@@ -24,6 +24,8 @@
 //   edge_update_kernel tile of 32 edge rows: W11, W12, W13, residual, LN3.
 // Small tiles keep several workgroups on every CU; the weights stream through
 // LDS in double-buffered chunks.
+#include <cstdlib>
+
 #include "device_math.hpp"
 #include "pmpnn_internal.hpp"
 
@@ -35,7 +37,6 @@ constexpr int kLdE = 36;     // k-major leading dimension of edge tiles
 constexpr int kEdgeRM = 2;   // rows per thread (16 row groups)
 constexpr int kEdgeCN = 8;   // cols per thread (16 col groups)
 constexpr int kKC = 32;      // weight rows staged per chunk
-constexpr int kNodeRows = 4;
 
 // Loads rows of a [*, 128] row-major matrix into a k-major LDS tile
 // A[k * lda + row] (row < n_rows, gathered through rowptr), zero elsewhere.
@@ -155,16 +156,21 @@ __device__ inline void col_gemm(const float* __restrict__ Wt, const float* A, in
   }
 }
 
-// Node update for kNodeRows residues: LN1(h + upd), FFN, LN2, mask; then the
-// W11 prefix of this layer's edge update and (when Wnext_t is given) the next
-// layer's W1 prefix. Few rows per workgroup keep the grid wide; every thread
-// owns whole output columns, so each dot product runs over k in order.
+// Node update for NR residues: LN1(h + upd), FFN, LN2, mask; then the W11
+// prefix of this layer's edge update and (when Wnext_t is given) the next
+// layer's W1 prefix. Every thread owns whole output columns, so each dot
+// product runs over k in order. Each weight element read from L2 serves NR
+// rows: few rows keep the grid wide when L is small, more rows cut the weight
+// traffic when L is large.
+template <int NR>
 __global__ __launch_bounds__(256) void node_kernel(EncLayerDev w, const float* __restrict__ Wnext_t,
                                                    const float* __restrict__ msg, const int32_t* __restrict__ idx,
                                                    const float* __restrict__ mask, int L, int K,
                                                    float* __restrict__ h_v, float* __restrict__ prefix) {
 #pragma clang fp contract(off)
-  constexpr int NR = kNodeRows;
+  static_assert(NR % 2 == 0 && NR <= 16, "thread mapping");
+  constexpr int NH = NR / 2;  // rows per thread in the column-per-thread phases
+  constexpr int KB = NR <= 4 ? 32 : 64 / NR;  // weight rows in flight per half-step
   __shared__ __attribute__((aligned(16))) float X[kH * NR];   // k-major [d][row]
   __shared__ __attribute__((aligned(16))) float H1[kH * NR];
   __shared__ __attribute__((aligned(16))) float F[kFF * NR];
@@ -172,16 +178,15 @@ __global__ __launch_bounds__(256) void node_kernel(EncLayerDev w, const float* _
   const int r0 = blockIdx.x * NR;
   const int nr = min(NR, L - r0);
   const int t = threadIdx.x;
-  static_assert(NR == 4, "thread mapping");
 
   // upd = sum over valid slots, in order, of (1/30) mask_i mask_j m_ij; then
   // X = h + upd (axpy order: 1 * residual + input). The weight of each
   // (row, slot) is computed once into LDS (0 for an invalid slot); thread t
-  // owns column t % 128 of rows 2 (t / 128) + {0, 1}, issues all of its
-  // message loads at once and sums them in slot order.
+  // owns column t % 128 of rows NH (t / 128) + q, q < NH, issues all of a
+  // row's message loads at once and sums them in slot order.
   __shared__ float alpha_s[NR * kKmax];
-  if (t < NR * kKmax) {
-    const int row = t / kKmax, k = t % kKmax;
+  for (int i = t; i < NR * kKmax; i += blockDim.x) {
+    const int row = i / kKmax, k = i % kKmax;
     float alpha = 0.0F;
     if (row < nr && k < K) {
       const int r = r0 + row;
@@ -191,12 +196,12 @@ __global__ __launch_bounds__(256) void node_kernel(EncLayerDev w, const float* _
         alpha *= mask[r] * mask[j];
       }
     }
-    alpha_s[t] = alpha;
+    alpha_s[i] = alpha;
   }
   __syncthreads();
   {
-    const int d = t % kH, rb = 2 * (t / kH);
-    for (int q = 0; q < 2; ++q) {
+    const int d = t % kH, rb = NH * (t / kH);
+    for (int q = 0; q < NH; ++q) {
       const int row = rb + q;
       float v = 0.0F;
       if (row < nr) {
@@ -230,7 +235,7 @@ __global__ __launch_bounds__(256) void node_kernel(EncLayerDev w, const float* _
   {
     // W_in: columns t and t + 256 of all rows, then GELU
     float acc[2][NR] = {};
-    col_gemm<kH, kFF, 2, 256, NR, 32>(w.Win_t, H1, NR, 0, t, acc);
+    col_gemm<kH, kFF, 2, 256, NR, KB>(w.Win_t, H1, NR, 0, t, acc);
 #pragma unroll
     for (int j = 0; j < 2; ++j)
 #pragma unroll
@@ -238,12 +243,12 @@ __global__ __launch_bounds__(256) void node_kernel(EncLayerDev w, const float* _
   }
   __syncthreads();
   {
-    // W_out: column t % 128 of rows 2 (t / 128) + {0, 1}; X = h1 + (W_out f + b)
-    const int c = t % kH, rr = 2 * (t / kH);
-    float acc[1][2] = {};
-    col_gemm<kFF, kH, 1, 0, 2, 32>(w.Wout_t, F, NR, rr, c, acc);
+    // W_out: column t % 128 of rows NH (t / 128) + r, r < NH; X = h1 + (W_out f + b)
+    const int c = t % kH, rr = NH * (t / kH);
+    float acc[1][NH] = {};
+    col_gemm<kFF, kH, 1, 0, NH, KB>(w.Wout_t, F, NR, rr, c, acc);
 #pragma unroll
-    for (int r = 0; r < 2; ++r) X[c * NR + rr + r] = H1[c * NR + rr + r] + (acc[0][r] + w.bout[c]);
+    for (int r = 0; r < NH; ++r) X[c * NR + rr + r] = H1[c * NR + rr + r] + (acc[0][r] + w.bout[c]);
   }
   __syncthreads();
   if (t < NR) welford_stats_col(X + t, NR, ln_mean + t, ln_inv + t);
@@ -265,7 +270,7 @@ __global__ __launch_bounds__(256) void node_kernel(EncLayerDev w, const float* _
     const float* Wt = part == 0 ? w.W11_t : Wnext_t;
     if (Wt) {
       float acc[1][NR] = {};
-      col_gemm<kH, kH, 1, 0, NR, 32>(Wt, H2, NR, 0, c, acc);
+      col_gemm<kH, kH, 1, 0, NR, KB>(Wt, H2, NR, 0, c, acc);
 #pragma unroll
       for (int r = 0; r < NR; ++r)
         if (r < nr) prefix[(size_t)(r0 + r) * 256 + part * 128 + c] = acc[0][r];
@@ -348,6 +353,17 @@ __global__ void zero_kernel(float* __restrict__ p, size_t n) {
 
 }  // namespace
 
+// Residues per node_kernel workgroup for a chain of L residues (2, 4, 8 or
+// 16; HKBS_ENCODER_NODE_ROWS overrides). The arithmetic of every row is the
+// same for all four, so the choice changes only the speed.
+static int encoder_node_rows(int L) {
+  if (const char* env = std::getenv("HKBS_ENCODER_NODE_ROWS")) {
+    const int n = std::atoi(env);
+    if (n == 2 || n == 4 || n == 8 || n == 16) return n;
+  }
+  return L >= 1500 ? 8 : 4;  // measured: 4 is fastest up to L = 1000, 8 from L = 2000
+}
+
 hipError_t launch_zero(float* p, size_t n, hipStream_t stream) {
   if (n == 0) return hipSuccess;
   const size_t blocks = (n + 255) / 256;
@@ -363,11 +379,19 @@ hipError_t launch_encoder(const ModelDev& m, const int32_t* idx, const float* ma
   e = launch_zero(ws.prefix, (size_t)L * 256, stream);
   if (e != hipSuccess) return e;
   const unsigned edge_tiles = (unsigned)(((size_t)L * K + kRows - 1) / kRows);
-  const unsigned node_tiles = (unsigned)((L + kNodeRows - 1) / kNodeRows);
+  const int node_rows = encoder_node_rows(L);
+  const unsigned node_tiles = (unsigned)((L + node_rows - 1) / node_rows);
   for (int l = 0; l < kLayers; ++l) {
     edge_msg_kernel<<<edge_tiles, 256, 0, stream>>>(m.enc[l], h_e, h_v, idx, ws.prefix, L, K, ws.msg);
-    node_kernel<<<node_tiles, 256, 0, stream>>>(m.enc[l], l + 1 < kLayers ? m.enc[l + 1].W1_t : nullptr, ws.msg,
-                                                idx, mask, L, K, h_v, ws.prefix);
+    const float* Wnext = l + 1 < kLayers ? m.enc[l + 1].W1_t : nullptr;
+    if (node_rows == 16)
+      node_kernel<16><<<node_tiles, 256, 0, stream>>>(m.enc[l], Wnext, ws.msg, idx, mask, L, K, h_v, ws.prefix);
+    else if (node_rows == 8)
+      node_kernel<8><<<node_tiles, 256, 0, stream>>>(m.enc[l], Wnext, ws.msg, idx, mask, L, K, h_v, ws.prefix);
+    else if (node_rows == 4)
+      node_kernel<4><<<node_tiles, 256, 0, stream>>>(m.enc[l], Wnext, ws.msg, idx, mask, L, K, h_v, ws.prefix);
+    else
+      node_kernel<2><<<node_tiles, 256, 0, stream>>>(m.enc[l], Wnext, ws.msg, idx, mask, L, K, h_v, ws.prefix);
     edge_update_kernel<<<edge_tiles, 256, 0, stream>>>(m.enc[l], h_e, h_v, idx, ws.prefix, L, K);
   }
   return hipGetLastError();

@@ -90,6 +90,26 @@ def test_encoder(gpu_ctx, oracle, L):
     np.testing.assert_array_equal(he, ohe)
 
 
+@pytest.mark.parametrize("L", [30, 301])
+def test_encoder_node_rows_same_bits(gpu_ctx, oracle, L, monkeypatch):
+    """Residues per node_kernel workgroup (2, 4, 8, 16; 8 is the choice for long chains) change
+    only the grid: the encoder output is bit-identical to the oracle for every setting, including a
+    ragged last tile (L = 301) and masked residues."""
+    bb = backbone.single_chain(L, 9)
+    src = bb.atom_sources.copy()
+    src[[2, 17], 3] = 0
+    src[9, 4] = 0
+    bb = backbone.Backbone(bb.coords, src)
+    omask, oidx, ohv, ohe = oracle.encode(bb)
+    for rows in ("2", "4", "8", "16"):
+        monkeypatch.setenv("HKBS_ENCODER_NODE_ROWS", rows)
+        _say(f"encode L={L} node rows={rows}")
+        mask, idx, hv, he = gpu_ctx.encode(bb.coords, bb.atom_sources)
+        np.testing.assert_array_equal(idx, oidx)
+        np.testing.assert_array_equal(hv, ohv, err_msg=f"rows={rows}")
+        np.testing.assert_array_equal(he, ohe, err_msg=f"rows={rows}")
+
+
 # ---------------------------------------------------------------- design --
 
 def replay(oracle, enc, order, seed, temperature, tokens, log_probs, greedy=False, chain_mask=None,
