@@ -107,7 +107,12 @@ constexpr int kTile = 32;  // edge slots per workgroup
 constexpr int kLdT = 36;   // k-major leading dimension
 
 // h_E = W_e . LN(W_edge . f) + b_e in the reference's rounding order
-// (sequential sums without FMA, Welford LayerNorm).
+// (sequential sums without FMA, Welford LayerNorm). The 416 features of the
+// tile are built in groups of kGroupChunks 16-feature chunks (one chunk of one
+// slot per thread) and each group is consumed by the next k-range of the
+// W_edge product, so one 128-row LDS tile serves features, the W_edge output
+// and the LayerNorm output, and three workgroups fit on a CU.
+constexpr int kGroupChunks = 8;
 __global__ __launch_bounds__(256) void edge_embed_kernel(ModelDev m, const float* __restrict__ coords,
                                                          const uint8_t* __restrict__ src,
                                                          const int32_t* __restrict__ resid,
@@ -115,35 +120,35 @@ __global__ __launch_bounds__(256) void edge_embed_kernel(ModelDev m, const float
                                                          const int32_t* __restrict__ idx, int L, int K,
                                                          float* __restrict__ h_e) {
 #pragma clang fp contract(off)
-  __shared__ __attribute__((aligned(16))) float A[kEdgeIn * kLdT];
-  __shared__ __attribute__((aligned(16))) float X[kH * kLdT];
+  static_assert(kGroupChunks * 16 <= kH && kGroupChunks * kTile == 256, "tile sizes");
+  __shared__ __attribute__((aligned(16))) float A[kH * kLdT];
   __shared__ __attribute__((aligned(16))) float Wbuf[2 * 32 * kH];
   const size_t S = (size_t)L * K;
   const size_t slot0 = (size_t)blockIdx.x * kTile;
   const int rg = threadIdx.x / 32, cg = threadIdx.x % 32;
   const int row0 = rg * 4, col0 = cg * 4;
+  const int frow = threadIdx.x % kTile, fchunk = threadIdx.x / kTile;
+  const size_t fslot = slot0 + frow;
+  const int fr = fslot < S ? static_cast<int>(fslot / K) : 0;
+  const int fj = fslot < S ? idx[fslot] : -1;
 
-  for (int task = threadIdx.x; task < kTile * 26; task += 256) {
-    const int row = task % kTile;
-    const int c = task / kTile;
-    const size_t slot = slot0 + row;
-    float out[16];
-    if (slot < S) {
-      const int r = static_cast<int>(slot / K);
-      edge_chunk(m, coords, src, resid, chain, L, r, idx[slot], c, out);
-    } else {
-#pragma unroll
-      for (int f = 0; f < 16; ++f) out[f] = 0.0F;
-    }
-#pragma unroll
-    for (int f = 0; f < 16; ++f) A[(c * 16 + f) * kLdT + row] = out[f];
-  }
   float acc[4][4];
 #pragma unroll
   for (int i = 0; i < 4; ++i)
 #pragma unroll
     for (int j = 0; j < 4; ++j) acc[i][j] = 0.0F;
-  seq_gemm<4, 4, kH, 32>(acc, A, kLdT, row0, m.edge_t, kH, kEdgeIn, Wbuf, col0);
+  for (int c0 = 0; c0 < 26; c0 += kGroupChunks) {
+    const int nc = min(kGroupChunks, 26 - c0);
+    // A is free here: seq_gemm ends with a barrier
+    if (fchunk < nc) {
+      float out[16];
+      edge_chunk(m, coords, src, resid, chain, L, fr, fj, c0 + fchunk, out);  // zeros when fj is not a residue
+#pragma unroll
+      for (int f = 0; f < 16; ++f) A[(fchunk * 16 + f) * kLdT + frow] = out[f];
+    }
+    seq_gemm<4, 4, kH, 32>(acc, A, kLdT, row0, m.edge_t + (size_t)c0 * 16 * kH, kH, nc * 16, Wbuf, col0);
+  }
+  float* X = A;
 #pragma unroll
   for (int i = 0; i < 4; ++i)
 #pragma unroll
