@@ -3,7 +3,9 @@
     python -m hikoboshi_amd.build
 
 hipcc compiles the kernels and the C-ABI layer in one shared object. Packed
-FP32 instruction selection is disabled on the device side.
+FP32 instruction selection is disabled on the device side. build_device_check()
+builds the test-only library tests/libdevice_math_check.so (an exhaustive GPU
+check of the device GELUs) with the same device flags.
 """
 from __future__ import annotations
 
@@ -16,6 +18,8 @@ from pathlib import Path
 HERE = Path(__file__).resolve().parent
 CSRC = HERE / "csrc"
 LIB = HERE / "libhkbs_pmpnn.so"
+CHECK_SRC = HERE.parent / "tests" / "csrc" / "device_math_check.hip"
+CHECK_LIB = HERE.parent / "tests" / "libdevice_math_check.so"
 ARCH = os.environ.get("HKBS_OFFLOAD_ARCH", "gfx950")
 SOURCES = ["knn.hip", "features.hip", "encoder.hip", "decoder.hip", "decoder_tf.hip", "capi.hip", "host_noise.cpp",
            "structure_io.cpp"]
@@ -30,15 +34,19 @@ def hipcc() -> str:
     raise RuntimeError("hipcc not found")
 
 
-def build(verbose: bool = False) -> Path:
-    objs = []
-    obj_dir = HERE / "_build"
-    obj_dir.mkdir(exist_ok=True)
-    common = [
+def _common() -> list:
+    return [
         hipcc(), "-std=c++17", "-O3", "-fPIC", f"--offload-arch={ARCH}",
         "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
         "-Wno-unused-command-line-argument", "-I", str(HERE.parent / "include"),
     ]
+
+
+def build(verbose: bool = False) -> Path:
+    objs = []
+    obj_dir = HERE / "_build"
+    obj_dir.mkdir(exist_ok=True)
+    common = _common()
     for src in SOURCES:
         obj = obj_dir / (Path(src).stem + ".o")
         extra = HOST_FLAGS if src.endswith(".cpp") else []
@@ -56,6 +64,17 @@ def build(verbose: bool = False) -> Path:
     return LIB
 
 
+def build_device_check(verbose: bool = False) -> Path:
+    tmp = CHECK_LIB.with_suffix(".so.tmp")
+    cmd = _common() + ["-shared", str(CHECK_SRC), "-o", str(tmp)]
+    if verbose:
+        print(" ".join(cmd), flush=True)
+    subprocess.run(cmd, check=True)
+    tmp.replace(CHECK_LIB)
+    return CHECK_LIB
+
+
 if __name__ == "__main__":
     build(verbose="-v" in sys.argv)
+    build_device_check(verbose="-v" in sys.argv)
     print(LIB)

@@ -53,34 +53,47 @@ __device__ inline float fast_exp_neg(float x) {
   return kExpNegTable[n] * e;
 }
 
-// GELU with the Abramowitz-Stegun 7.1.26 erf used by the reference.
+// 1 / y for y in [1, 2.32] (the range of 1 + p v below), correctly rounded:
+// the hardware reciprocal is within an ulp and one FMA Newton step rounds it
+// to 1 / y (equal to IEEE division at every float of the range).
+__device__ inline float recip_unit_range(float y) {
+  const float r0 = __builtin_amdgcn_rcpf(y);
+  const float e = __builtin_fmaf(-y, r0, 1.0F);
+  return __builtin_fmaf(e, r0, r0);
+}
+
+// GELU with the Abramowitz-Stegun 7.1.26 erf used by the reference
+// (gelu.hpp:22-51, fast_exp_neg.hpp:12-55): sign and magnitude of
+// v = x / sqrt(2), erf = 1 - poly(t) exp(-v^2) with t = 1 / (1 + p v), exp by
+// table and degree-6 Taylor, erf = sign for v > 4, GELU = 0.5 x (1 + erf),
+// every operation rounded as in the reference. Evaluated without branches:
+// for v <= 4 the exp argument v^2 lies in [0, 16], where fast_exp_neg's range
+// checks do nothing; for v > 4 the value is selected away. The result equals
+// the reference expression bit for bit for every float x (a GPU test compares
+// all 2^32 inputs with the branching form).
 __device__ inline float gelu(float x) {
 #pragma clang fp contract(off)
-  float v = x * 0.7071067811865475F;
-  float sign = 1.0F;
-  if (v < 0.0F) {
-    sign = -1.0F;
-    v = -v;
-  }
-  float erfv;
-  if (v > 4.0F) {
-    erfv = sign;
-  } else {
-    const float t = 1.0F / (1.0F + 0.3275911F * v);
-    const float poly =
-        (((((1.061405429F * t + -1.453152027F) * t) + 1.421413741F) * t + -0.284496736F) * t +
-         0.254829592F) *
-        t;
-    erfv = sign * (1.0F - poly * fast_exp_neg(-(v * v)));
-  }
+  const float vs = x * 0.7071067811865475F;
+  const float v = fabsf(vs);
+  const float t = recip_unit_range(1.0F + 0.3275911F * v);
+  const float poly =
+      (((((1.061405429F * t + -1.453152027F) * t) + 1.421413741F) * t + -0.284496736F) * t + 0.254829592F) * t;
+  const float q = fminf(v * v, 16.0F);
+  const int n = static_cast<int>(q + 0.5F);
+  const float r = -(q - static_cast<float>(n));
+  const float e =
+      1.0F + r * (1.0F + r * (0.5F + r * (1.0F / 6.0F + r * (1.0F / 24.0F + r * (1.0F / 120.0F + r * (1.0F / 720.0F))))));
+  const float mag = 1.0F - poly * (kExpNegTable[n] * e);
+  const float erfv = __builtin_copysignf(v > 4.0F ? 1.0F : mag, vs);
   return 0.5F * x * (1.0F + erfv);
 }
 
 // The same GELU formula for the decode loop, which is held to a tolerance
 // rather than to bit identity: the exp table is read from LDS (tbl = 17
-// floats, kExpNegTable), 1/(1 + p v) uses the hardware reciprocal (1 ulp),
-// and the whole formula is evaluated for every lane with the v > 4 and sign
-// cases as selects (no branch around the table load).
+// floats, kExpNegTable), 1/(1 + p v) is the hardware reciprocal (1 ulp) and
+// contraction is allowed. No v > 4 case is needed: there q is clamped to 16
+// and poly(t) exp(-16) < 2^-25, so mag rounds to exactly 1. The sign is copied
+// from x (for x = -0 the result is -0 either way).
 __device__ inline float gelu_fast(float x, const float* tbl) {
   const float v = fabsf(x) * 0.7071067811865475F;
   const float t = __builtin_amdgcn_rcpf(1.0F + 0.3275911F * v);
@@ -96,9 +109,7 @@ __device__ inline float gelu_fast(float x, const float* tbl) {
                 r * (1.0F / 6.0F + r * (1.0F / 24.0F + r * (1.0F / 120.0F + r * (1.0F / 720.0F))))));
   const float ex = tbl[n];
   const float mag = 1.0F - poly * (ex * e);
-  float erfv = v > 4.0F ? 1.0F : mag;
-  erfv = x < 0.0F ? -erfv : erfv;
-  return 0.5F * x * (1.0F + erfv);
+  return 0.5F * x * (1.0F + __builtin_copysignf(mag, x));
 }
 
 __device__ inline floatx4 mfma16(float a, float b, floatx4 c) {

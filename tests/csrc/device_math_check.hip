@@ -1,0 +1,123 @@
+// Exhaustive GPU check of the device GELUs in hikoboshi_amd/csrc/device_math.hpp
+// against their straightforward forms, over all 2^32 float bit patterns.
+//
+//   gelu      (encoder, bit-exact path) vs gelu_branching: the reference's
+//             expression as written in cpp/include/hikoboshi/primitives/compute/gelu.hpp:22-51
+//             with fast_exp_neg (cpp/include/hikoboshi/primitives/detail/fast_exp_neg.hpp:12-55),
+//             IEEE division and every range check taken as a branch;
+//   gelu_fast (decode loop) vs gelu_fast_select: the same formula with the
+//             hardware reciprocal, the v > 4 case as a select and the sign by
+//             comparison (the form gelu_fast replaced).
+// Results must agree bit for bit (any NaN equals any NaN). Test infrastructure
+// only: built into tests/libdevice_math_check.so and called by
+// tests/test_gpu_device_math.py.
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+#include "../../hikoboshi_amd/csrc/device_math.hpp"
+
+namespace {
+
+using hkbs::kExpNegTable;
+
+__device__ float fast_exp_neg_branching(float x) {
+#pragma clang fp contract(off)
+  if (x != x) return x;
+  float neg_x = -x;
+  if (neg_x > 16.0F) return 0.0F;
+  if (neg_x < 0.0F) neg_x = 0.0F;
+  int n = static_cast<int>(neg_x + 0.5F);
+  if (n > 16) n = 16;
+  const float r = -(neg_x - static_cast<float>(n));
+  const float e =
+      1.0F + r * (1.0F + r * (0.5F + r * (1.0F / 6.0F + r * (1.0F / 24.0F + r * (1.0F / 120.0F + r * (1.0F / 720.0F))))));
+  return kExpNegTable[n] * e;
+}
+
+__device__ float gelu_branching(float x) {
+#pragma clang fp contract(off)
+  float v = x * 0.7071067811865475F;
+  float sign = 1.0F;
+  if (v < 0.0F) {
+    sign = -1.0F;
+    v = -v;
+  }
+  float erfv;
+  if (v > 4.0F) {
+    erfv = sign;
+  } else {
+    const float t = 1.0F / (1.0F + 0.3275911F * v);
+    const float poly =
+        (((((1.061405429F * t + -1.453152027F) * t) + 1.421413741F) * t + -0.284496736F) * t + 0.254829592F) * t;
+    erfv = sign * (1.0F - poly * fast_exp_neg_branching(-(v * v)));
+  }
+  return 0.5F * x * (1.0F + erfv);
+}
+
+__device__ float gelu_fast_select(float x, const float* tbl) {
+  const float v = fabsf(x) * 0.7071067811865475F;
+  const float t = __builtin_amdgcn_rcpf(1.0F + 0.3275911F * v);
+  const float poly =
+      (((((1.061405429F * t + -1.453152027F) * t) + 1.421413741F) * t + -0.284496736F) * t + 0.254829592F) * t;
+  const float q = fminf(v * v, 16.0F);
+  const int n = static_cast<int>(q + 0.5F);
+  const float r = static_cast<float>(n) - q;
+  const float e =
+      1.0F +
+      r * (1.0F +
+           r * (0.5F +
+                r * (1.0F / 6.0F + r * (1.0F / 24.0F + r * (1.0F / 120.0F + r * (1.0F / 720.0F))))));
+  const float ex = tbl[n];
+  const float mag = 1.0F - poly * (ex * e);
+  float erfv = v > 4.0F ? 1.0F : mag;
+  erfv = x < 0.0F ? -erfv : erfv;
+  return 0.5F * x * (1.0F + erfv);
+}
+
+__device__ inline bool same_bits(float a, float b) {
+  return (a != a && b != b) || __float_as_uint(a) == __float_as_uint(b);
+}
+
+// counts[0], first[0]: gelu; counts[1], first[1]: gelu_fast (first = smallest
+// mismatching bit pattern, 0xFFFFFFFF if none).
+__global__ void check_kernel(unsigned long long* counts, unsigned int* first) {
+  __shared__ float tbl[17];
+  if (threadIdx.x < 17) tbl[threadIdx.x] = kExpNegTable[threadIdx.x];
+  __syncthreads();
+  const uint64_t stride = (uint64_t)gridDim.x * blockDim.x;
+  for (uint64_t bits = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; bits < (1ull << 32); bits += stride) {
+    const float x = __uint_as_float(static_cast<unsigned int>(bits));
+    if (!same_bits(hkbs::gelu(x), gelu_branching(x))) {
+      atomicAdd(&counts[0], 1ull);
+      atomicMin(&first[0], static_cast<unsigned int>(bits));
+    }
+    if (!same_bits(hkbs::gelu_fast(x, tbl), gelu_fast_select(x, tbl))) {
+      atomicAdd(&counts[1], 1ull);
+      atomicMin(&first[1], static_cast<unsigned int>(bits));
+    }
+  }
+}
+
+}  // namespace
+
+// Runs the check on the current device; writes 2 counts and 2 first
+// mismatches. Returns the HIP status of the run.
+extern "C" int hkbs_check_device_gelu(unsigned long long* counts_out, unsigned int* first_out) {
+  unsigned long long* counts = nullptr;
+  unsigned int* first = nullptr;
+  hipError_t e = hipMalloc(&counts, 2 * sizeof(unsigned long long));
+  if (e == hipSuccess) e = hipMalloc(&first, 2 * sizeof(unsigned int));
+  if (e == hipSuccess) e = hipMemset(counts, 0, 2 * sizeof(unsigned long long));
+  if (e == hipSuccess) e = hipMemset(first, 0xFF, 2 * sizeof(unsigned int));
+  if (e == hipSuccess) {
+    check_kernel<<<8192, 256>>>(counts, first);
+    e = hipGetLastError();
+  }
+  if (e == hipSuccess) e = hipDeviceSynchronize();
+  if (e == hipSuccess) e = hipMemcpy(counts_out, counts, 2 * sizeof(unsigned long long), hipMemcpyDeviceToHost);
+  if (e == hipSuccess) e = hipMemcpy(first_out, first, 2 * sizeof(unsigned int), hipMemcpyDeviceToHost);
+  if (counts) (void)hipFree(counts);
+  if (first) (void)hipFree(first);
+  return static_cast<int>(e);
+}
