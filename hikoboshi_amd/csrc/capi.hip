@@ -805,17 +805,19 @@ hkbs_status design_on_device(hkbs_pmpnn* ctx, const float* coords, const uint8_t
   ctx->last_decode = a;
   // The decode schedule needs only the kNN graph and the orders: it is built
   // on the side stream while the encoder runs, and the decode waits for it.
+  // The encoder is enqueued first so that its launches do not queue behind
+  // the schedule's on the host.
   if (ctx->timing) HK_CHECK(hipEventRecord(ctx->ev[0], ctx->stream), "event record failed");
   HK_CHECK(launch_knn(coords, src, L, K, e.idx, e.d2, e.mask, e.ca, ctx->stream), "kNN launch failed");
   HK_CHECK(hipEventRecord(ctx->fork, ctx->stream), "event record failed");
-  HK_CHECK(hipStreamWaitEvent(ctx->side, ctx->fork, 0), "stream wait failed");
-  HK_CHECK(launch_positions(orders, L, shared ? 1 : B, shared, pos, ctx->side), "position kernel failed");
-  HK_CHECK(launch_decode_schedule(a, ctx->side), "decode schedule launch failed");
-  HK_CHECK(hipEventRecord(ctx->join, ctx->side), "event record failed");
   HK_CHECK(launch_edge_embed(ctx->model, coords, src, resid, chain, e.idx, L, K, e.h_e, ctx->stream),
            "encoder launch failed");
   HK_CHECK(launch_encoder(ctx->model, e.idx, e.mask, L, K, e.h_v, e.h_e, e.scratch, ctx->stream),
            "encoder launch failed");
+  HK_CHECK(hipStreamWaitEvent(ctx->side, ctx->fork, 0), "stream wait failed");
+  HK_CHECK(launch_positions(orders, L, shared ? 1 : B, shared, pos, ctx->side), "position kernel failed");
+  HK_CHECK(launch_decode_schedule(a, ctx->side), "decode schedule launch failed");
+  HK_CHECK(hipEventRecord(ctx->join, ctx->side), "event record failed");
   if (ctx->timing) HK_CHECK(hipEventRecord(ctx->ev[1], ctx->stream), "event record failed");
   HK_CHECK(launch_decoder_precompute(ctx->model, e.h_v, e.h_e, L, K, E1, Q, ctx->stream), "decoder precompute failed");
   HK_CHECK(launch_zero(reinterpret_cast<float*>(sync), (size_t)B + 1, ctx->stream), "workspace clear failed");
