@@ -21,7 +21,7 @@ LIB = HERE / "libhkbs_pmpnn.so"
 CHECK_SRC = HERE.parent / "tests" / "csrc" / "device_math_check.hip"
 CHECK_LIB = HERE.parent / "tests" / "libdevice_math_check.so"
 ARCH = os.environ.get("HKBS_OFFLOAD_ARCH", "gfx950")
-SOURCES = ["knn.hip", "features.hip", "encoder.hip", "decoder.hip", "decoder_tf.hip", "capi.hip", "host_noise.cpp",
+SOURCES = ["knn.hip", "features.hip", "encoder.hip", "encoder16.hip", "decoder.hip", "decoder_tf.hip", "capi.hip", "host_noise.cpp",
            "structure_io.cpp"]
 # Host-only C++ (no device code), without floating-point contraction.
 HOST_FLAGS = ["-ffp-contract=off"]

@@ -442,6 +442,8 @@ hkbs_status build_model(hkbs_pmpnn* ctx, const float* const* t) {
     size_t dec[kLayers][22];
     size_t dec_h[kLayers][4];  // bf16 copies of W3_t, Win_t, Wout_t, W1da_t
     size_t dec_f[kLayers][4];  // fp16 copies of the same
+    size_t enc16[2 + 8 * kLayers];  // split-fp16 encoder weights: W_edge, W_e, then per layer
+                                    // W1 W2 W3 W11 W12 W13 W_in W_out
   } o{};
   o.pos_w = copy_raw(ar, t[0], 16 * 66);
   o.pos_b = copy_raw(ar, t[1], 16);
@@ -471,6 +473,24 @@ hkbs_status build_model(hkbs_pmpnn* ctx, const float* const* t) {
     q[14] = copy_raw(ar, e[19], 512);                 // bin
     q[15] = copy_raw(ar, e[21], 128);                 // bout
     for (int i = 0; i < 6; ++i) q[16 + i] = copy_raw(ar, e[12 + i], 128);  // n1g n1b n2g n2b n3g n3b
+  }
+  {
+    auto pk = [&](const float* W, int N, int kin) { return pack_f16_split(ar, W, N, kin); };
+    size_t* q = o.enc16;
+    q[0] = pk(t[2], 128, 416);  // W_edge
+    q[1] = pk(t[5], 128, 128);  // W_e
+    for (int l = 0; l < kLayers; ++l) {
+      const float* const* e = t + 8 + 22 * l;
+      size_t* ql = q + 2 + 8 * l;
+      ql[0] = pk(e[0], 128, 384);   // W1
+      ql[1] = pk(e[2], 128, 128);   // W2
+      ql[2] = pk(e[4], 128, 128);   // W3
+      ql[3] = pk(e[6], 128, 384);   // W11
+      ql[4] = pk(e[8], 128, 128);   // W12
+      ql[5] = pk(e[10], 128, 128);  // W13
+      ql[6] = pk(e[18], 512, 128);  // W_in
+      ql[7] = pk(e[20], 128, 512);  // W_out
+    }
   }
   {
     std::vector<float> w1b(384 * 128), w1d(512 * 128);
@@ -632,6 +652,24 @@ hkbs_status build_model(hkbs_pmpnn* ctx, const float* const* t) {
   m.blog = B + o.blog;
   m.Wlog_h = reinterpret_cast<const uint16_t*>(B + o.Wlog_h);
   m.Wlog_f = reinterpret_cast<const uint16_t*>(B + o.Wlog_f);
+  {
+    auto u16 = [&](size_t off) { return reinterpret_cast<const uint16_t*>(B + off); };
+    const size_t* q = o.enc16;
+    m.enc16.Wedge = u16(q[0]);
+    m.enc16.We = u16(q[1]);
+    for (int l = 0; l < kLayers; ++l) {
+      const size_t* ql = q + 2 + 8 * l;
+      Enc16LayerDev& w = m.enc16.layer[l];
+      w.W1 = u16(ql[0]);
+      w.W2 = u16(ql[1]);
+      w.W3 = u16(ql[2]);
+      w.W11 = u16(ql[3]);
+      w.W12 = u16(ql[4]);
+      w.W13 = u16(ql[5]);
+      w.Win = u16(ql[6]);
+      w.Wout = u16(ql[7]);
+    }
+  }
   return HKBS_OK;
 }
 
@@ -669,13 +707,23 @@ EncodeBuffers take_encode(DeviceArena& ar, int L, int K) {
   return e;
 }
 
+// Featurisation and encoder: the reference's fp32 rounding sequence, or in the
+// 16-bit modes the split-operand fp16 MFMA (fp32-level accuracy).
+hipError_t launch_featurise_encode(hkbs_pmpnn* ctx, const float* coords, const uint8_t* src, const int32_t* resid,
+                                   const int32_t* chain, int L, int K, const EncodeBuffers& e) {
+  if (ctx->precision != HKBS_PRECISION_FP32)
+    return launch_encoder16(ctx->model, coords, src, resid, chain, e.idx, e.mask, L, K, e.h_v, e.h_e, e.scratch,
+                            ctx->stream);
+  hipError_t err = launch_edge_embed(ctx->model, coords, src, resid, chain, e.idx, L, K, e.h_e, ctx->stream);
+  if (err != hipSuccess) return err;
+  return launch_encoder(ctx->model, e.idx, e.mask, L, K, e.h_v, e.h_e, e.scratch, ctx->stream);
+}
+
 hipError_t run_encode(hkbs_pmpnn* ctx, const float* coords, const uint8_t* src, const int32_t* resid,
                       const int32_t* chain, int L, int K, const EncodeBuffers& e) {
   hipError_t err = launch_knn(coords, src, L, K, e.idx, e.d2, e.mask, e.ca, ctx->stream);
   if (err != hipSuccess) return err;
-  err = launch_edge_embed(ctx->model, coords, src, resid, chain, e.idx, L, K, e.h_e, ctx->stream);
-  if (err != hipSuccess) return err;
-  return launch_encoder(ctx->model, e.idx, e.mask, L, K, e.h_v, e.h_e, e.scratch, ctx->stream);
+  return launch_featurise_encode(ctx, coords, src, resid, chain, L, K, e);
 }
 
 struct Inputs {
@@ -810,10 +858,7 @@ hkbs_status design_on_device(hkbs_pmpnn* ctx, const float* coords, const uint8_t
   if (ctx->timing) HK_CHECK(hipEventRecord(ctx->ev[0], ctx->stream), "event record failed");
   HK_CHECK(launch_knn(coords, src, L, K, e.idx, e.d2, e.mask, e.ca, ctx->stream), "kNN launch failed");
   HK_CHECK(hipEventRecord(ctx->fork, ctx->stream), "event record failed");
-  HK_CHECK(launch_edge_embed(ctx->model, coords, src, resid, chain, e.idx, L, K, e.h_e, ctx->stream),
-           "encoder launch failed");
-  HK_CHECK(launch_encoder(ctx->model, e.idx, e.mask, L, K, e.h_v, e.h_e, e.scratch, ctx->stream),
-           "encoder launch failed");
+  HK_CHECK(launch_featurise_encode(ctx, coords, src, resid, chain, L, K, e), "encoder launch failed");
   HK_CHECK(hipStreamWaitEvent(ctx->side, ctx->fork, 0), "stream wait failed");
   HK_CHECK(launch_positions(orders, L, shared ? 1 : B, shared, pos, ctx->side), "position kernel failed");
   HK_CHECK(launch_decode_schedule(a, ctx->side), "decode schedule launch failed");

@@ -19,70 +19,11 @@
 // multiplied by W_edge, normalised and multiplied by W_e without leaving the
 // CU, all in the reference's rounding order (h_E is bit-identical).
 #include "device_math.hpp"
+#include "edge_chunk.hpp"
 #include "pmpnn_internal.hpp"
 
 namespace hkbs {
 namespace {
-
-__device__ __constant__ static const int8_t kPairQ[25] = {1, 0, 2, 3, 4, 1, 1, 1, 1, 0, 0, 0, 4,
-                                                          4, 3, 0, 2, 3, 4, 2, 3, 4, 2, 3, 2};
-__device__ __constant__ static const int8_t kPairN[25] = {1, 0, 2, 3, 4, 0, 2, 3, 4, 2, 3, 4, 2,
-                                                          3, 2, 1, 1, 1, 1, 0, 0, 0, 4, 4, 3};
-
-// Writes the 16 features of chunk c (0 = positional, 1..25 = atom pair c-1)
-// of edge slot (r, j) to out[0..16).
-__device__ inline void edge_chunk(const ModelDev& m, const float* __restrict__ coords,
-                                  const uint8_t* __restrict__ src, const int32_t* __restrict__ resid,
-                                  const int32_t* __restrict__ chain, int L, int r, int j, int c,
-                                  float* out) {
-#pragma clang fp contract(off)
-  if (j < 0 || j >= L) {
-#pragma unroll
-    for (int f = 0; f < 16; ++f) out[f] = 0.0F;
-    return;
-  }
-  if (c == 0) {
-    int cls;
-    const int ci = chain ? chain[r] : 0;
-    const int cj = chain ? chain[j] : 0;
-    if (ci != cj) {
-      cls = kPosClasses - 1;
-    } else {
-      int off = (resid ? resid[r] : r) - (resid ? resid[j] : j);
-      off = off < -32 ? -32 : (off > 32 ? 32 : off);
-      cls = off + 32;
-    }
-#pragma unroll
-    for (int d = 0; d < 16; ++d) out[d] = m.pos_w[d * kPosClasses + cls] + m.pos_b[d];
-    return;
-  }
-  const int p = c - 1;
-  const int qa = kPairQ[p], na = kPairN[p];
-  if (src[(size_t)r * 5 + qa] == 0 || src[(size_t)j * 5 + na] == 0) {
-#pragma unroll
-    for (int f = 0; f < 16; ++f) out[f] = 0.0F;
-    return;
-  }
-  const float* qx = coords + ((size_t)r * 5 + qa) * 3;
-  const float* nx = coords + ((size_t)j * 5 + na) * 3;
-  float sq = 0.0F;
-#pragma unroll
-  for (int ax = 0; ax < 3; ++ax) {
-    const float delta = nx[ax] - qx[ax];
-    sq += delta * delta;
-  }
-  sq = sq + 1.0e-6F;
-  const float dist = sqrtf(sq);
-  const float center_step = (22.0F - 2.0F) / static_cast<float>(kRbf - 1);
-  const float sigma = (22.0F - 2.0F) / (static_cast<float>(kRbf) / 0.7071067811865475F);
-  const float two_sigma_sq = 2.0F * sigma * sigma;
-#pragma unroll
-  for (int f = 0; f < 16; ++f) {
-    const float center = 2.0F + static_cast<float>(f) * center_step;
-    const float delta = dist - center;
-    out[f] = fast_exp_neg(-(delta * delta) / two_sigma_sq);
-  }
-}
 
 __global__ __launch_bounds__(256) void edge_features_kernel(ModelDev m, const float* __restrict__ coords,
                                                             const uint8_t* __restrict__ src,

@@ -38,6 +38,21 @@ struct EncLayerDev {
   const float *n1g, *n1b, *n2g, *n2b, *n3g, *n3b;
 };
 
+// Encoder weights for the fp16 MFMA with split operands: W [N][K] (out x in)
+// as hi = fp16(W) and lo = fp16((W - hi) * 2048), each stored as [K / 8][N][8]
+// halves (lo follows hi, K * N halves later), so lane (r, g) of a wave reads
+// the 8 consecutive k of column n = n0 + r with one 16-byte load.
+struct Enc16LayerDev {
+  const uint16_t *W1, *W2, *W3;     // K = 384 ([h_i | e_ij | h_j]), 128, 128; N = 128
+  const uint16_t *W11, *W12, *W13;  // the same for the edge update
+  const uint16_t *Win, *Wout;       // 128 -> 512, 512 -> 128
+};
+struct Enc16Dev {
+  const uint16_t* Wedge;  // 416 -> 128
+  const uint16_t* We;     // 128 -> 128
+  Enc16LayerDev layer[kLayers];
+};
+
 struct DecLayerDev {
   const float* W1a_t;  // [128][128]
   const float* W2_p;   // kpack16 128 -> 128
@@ -76,6 +91,7 @@ struct ModelDev {
   const float* blog;       // [32] (21 used)
   const uint16_t* Wlog_h;  // bf16 copy of Wlog_t
   const uint16_t* Wlog_f;  // fp16 copy of Wlog_t
+  Enc16Dev enc16;          // split-fp16 encoder weights (16-bit design modes)
 };
 
 // Launchers (each enqueues on `stream`; shapes are validated by the caller).
@@ -104,6 +120,12 @@ void backbone_noise_host(const float* coords, const uint8_t* atom_sources, int32
                          float* out);
 hipError_t launch_encoder(const ModelDev& m, const int32_t* idx, const float* mask, int L, int K,
                           float* h_v, float* h_e, const EncoderScratch& ws, hipStream_t stream);
+// Featurisation and encoder on the fp16 MFMA with split operands (fp32-level
+// accuracy; the 16-bit design modes); kNN (idx, mask) comes from launch_knn.
+// ws.prefix holds the neighbour sums ([L][128]).
+hipError_t launch_encoder16(const ModelDev& m, const float* coords, const uint8_t* atom_src,
+                            const int32_t* resid, const int32_t* chain, const int32_t* idx, const float* mask,
+                            int L, int K, float* h_v, float* h_e, const EncoderScratch& ws, hipStream_t stream);
 hipError_t launch_decoder_precompute(const ModelDev& m, const float* h_v, const float* h_e, int L,
                                      int K, float* E1, float* Q, hipStream_t stream);
 struct DecodeArgs {

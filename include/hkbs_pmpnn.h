@@ -62,12 +62,14 @@ enum {
   HKBS_ORDER_N_TO_C = 3
 };
 
-/* Arithmetic of the design path (hkbs_pmpnn_set_precision); the featurisation and
- * encoder stay in the reference's fp32 rounding in every mode. */
+/* Arithmetic of the design path (hkbs_pmpnn_set_precision). The kNN graph and
+ * the decoding order are exact in every mode. */
 enum {
-  HKBS_PRECISION_FP32 = 0, /* default: log-probs within 1e-4 of the reference */
-  HKBS_PRECISION_BF16 = 1, /* bf16 weights and activations into the decoder's products, fp32
-                              accumulation, LayerNorm and softmax */
+  HKBS_PRECISION_FP32 = 0, /* default: featurisation and encoder in the reference's fp32 rounding,
+                              log-probs within 1e-4 of the reference */
+  HKBS_PRECISION_BF16 = 1, /* bf16 weights and activations into every product of the edge
+                              embedding, encoder and decoder (MFMA), fp32 accumulation,
+                              GELU, LayerNorm and softmax */
   HKBS_PRECISION_FP16 = 2  /* the same with fp16 (three more significant bits than bf16) */
 };
 
@@ -158,8 +160,9 @@ hkbs_status hkbs_pmpnn_decode_order(const float* chain_mask, const uint8_t* atom
 hkbs_status hkbs_pmpnn_backbone_noise(const float* coords, const uint8_t* atom_sources, int32_t L,
                                       float sigma, uint64_t seed, float* out);
 
-/* Selects the arithmetic of later design and score calls on this context
- * (no counterpart in the reference, which has only its fp32 scalar path). */
+/* Selects the arithmetic of later design and encode calls on this context
+ * (teacher-forced scoring stays fp32; no counterpart in the reference, which
+ * has only its fp32 scalar path). */
 hkbs_status hkbs_pmpnn_set_precision(hkbs_pmpnn* ctx, int32_t precision);
 
 /* Phase timing (instrumentation; no counterpart in the reference, which has
@@ -179,8 +182,8 @@ hkbs_status hkbs_pmpnn_knn(hkbs_pmpnn* ctx, const float* coords, const uint8_t* 
                            int32_t L, int32_t* idx, float* d2);
 
 /* Featurise + encode (inverse_fold_scalar.cpp:300-352): residue mask [L],
- * neighbour idx [L,K], node states h_V [L,128], edge states h_E [L,K,128].
- * Any output may be NULL. */
+ * neighbour idx [L,K], node states h_V [L,128], edge states h_E [L,K,128], in
+ * the context's precision (the design path's encoder). Any output may be NULL. */
 hkbs_status hkbs_pmpnn_encode(hkbs_pmpnn* ctx, const float* coords, const uint8_t* atom_sources,
                               const int32_t* residue_indices, const int32_t* chain_labels,
                               int32_t L, float* mask, int32_t* idx, float* h_v, float* h_e);
