@@ -23,7 +23,7 @@
 //                  [h_i | e_ij | h_j] -> W1, GELU, W2, GELU, W3 -> the masked
 //                  sum over the residue's slots / 30 -> upd[i].
 //   node16         16 residues per workgroup (1 wave): LN1(h + upd), the FFN
-//                  on the MFMA, LN2, mask.
+//                  on the MFMA, LN2, mask, all 16 rows at once.
 //   edge_update16  32 edge slots per workgroup (2 waves): [h_i | e_ij | h_j]
 //                  -> W11, GELU, W12, GELU, W13, residual, LN3 -> h_E (valid
 //                  slots).
@@ -50,7 +50,8 @@ __device__ inline floatx4 mfma_f16(f16x8 a, f16x8 b, floatx4 c) {
 // acc[nt] = A[16 rows][K] . W[K][n0 + 16 nt + (0..15)] for nt < NT. A is the
 // wave's fp32 slab (lda floats per row); Wp the split weights, hi as
 // [K / 8][N][8] halves and lo at Wp + K * N. With lane = 16 g + r, acc[nt][i]
-// is row 4 g + i, column n0 + 16 nt + r.
+// is row 4 g + i, column n0 + 16 nt + r. The next k-step's weight fragments
+// load while the current ones are used.
 template <int NT>
 __device__ inline void wave_gemm(const float* A, int lda, const uint16_t* __restrict__ Wp, int N, int n0, int K,
                                  floatx4 (&acc)[NT]) {
@@ -64,7 +65,21 @@ __device__ inline void wave_gemm(const float* A, int lda, const uint16_t* __rest
     acc[nt] = floatx4{0.F, 0.F, 0.F, 0.F};
     cor[nt] = acc[nt];
   }
-  for (int kb = 0; kb < K / 32; ++kb) {
+  const int nkb = K / 32;
+  f16x8 bh[NT], bl[NT];
+#pragma unroll
+  for (int nt = 0; nt < NT; ++nt) {
+    bh[nt] = *reinterpret_cast<const f16x8*>(wh + (size_t)nt * 16 * 8);
+    bl[nt] = *reinterpret_cast<const f16x8*>(wl + (size_t)nt * 16 * 8);
+  }
+  for (int kb = 0; kb < nkb; ++kb) {
+    const int kn = kb + 1 < nkb ? kb + 1 : kb;
+    f16x8 nh[NT], nl[NT];
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) {
+      nh[nt] = *reinterpret_cast<const f16x8*>(wh + (size_t)kn * kstep + (size_t)nt * 16 * 8);
+      nl[nt] = *reinterpret_cast<const f16x8*>(wl + (size_t)kn * kstep + (size_t)nt * 16 * 8);
+    }
     const float4* ap = reinterpret_cast<const float4*>(A + r * lda + 32 * kb + 8 * g);
     const float4 a0 = ap[0], a1 = ap[1];
     const float av[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
@@ -77,11 +92,14 @@ __device__ inline void wave_gemm(const float* A, int lda, const uint16_t* __rest
     }
 #pragma unroll
     for (int nt = 0; nt < NT; ++nt) {
-      const f16x8 bh = *reinterpret_cast<const f16x8*>(wh + (size_t)kb * kstep + (size_t)nt * 16 * 8);
-      const f16x8 bl = *reinterpret_cast<const f16x8*>(wl + (size_t)kb * kstep + (size_t)nt * 16 * 8);
-      acc[nt] = mfma_f16(ah, bh, acc[nt]);
-      cor[nt] = mfma_f16(ah, bl, cor[nt]);
-      cor[nt] = mfma_f16(al, bh, cor[nt]);
+      acc[nt] = mfma_f16(ah, bh[nt], acc[nt]);
+      cor[nt] = mfma_f16(ah, bl[nt], cor[nt]);
+      cor[nt] = mfma_f16(al, bh[nt], cor[nt]);
+    }
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) {
+      bh[nt] = nh[nt];
+      bl[nt] = nl[nt];
     }
   }
 #pragma unroll
@@ -262,52 +280,54 @@ __global__ __launch_bounds__(192) void edge_msg16_kernel(EncLayerDev w, Enc16Lay
     upd[(size_t)res * kH + threadIdx.x] = (part[0][threadIdx.x] + part[1][threadIdx.x]) + part[2][threadIdx.x];
 }
 
-// 16 residues per workgroup of one wave.
+// 16 residues per workgroup of one wave; lane (r, g) holds rows 4 g + i,
+// columns 16 nt + r of every 128-wide activation (the MFMA output layout), so
+// both LayerNorms run on all 16 rows at once.
 __global__ __launch_bounds__(64) void node16_kernel(EncLayerDev w, Enc16LayerDev w16, const float* __restrict__ upd,
                                                     const float* __restrict__ mask, int L, float* __restrict__ h_v) {
-  __shared__ __attribute__((aligned(16))) float X[16][kH];
   __shared__ __attribute__((aligned(16))) float A[16 * kLdH];
   __shared__ __attribute__((aligned(16))) float F[16 * kLdF];
   __shared__ float tbl[17];
   const int lane = threadIdx.x & 63, r = lane & 15, g = lane >> 4;
   const int r0 = blockIdx.x * 16;
   if (lane < 17) tbl[lane] = kExpNegTable[lane];
-  for (int i = 0; i < 16; ++i) {
-    const int res = r0 + i;
-    if (res < L) {  // the same for every lane
-      const float x0 = h_v[(size_t)res * kH + lane] + upd[(size_t)res * kH + lane];
-      const float x1 = h_v[(size_t)res * kH + lane + 64] + upd[(size_t)res * kH + lane + 64];
-      ln_regs_wave(x0, x1, w.n1g, w.n1b, X[i]);
-    } else {
-      X[i][lane] = 0.0F;
-      X[i][lane + 64] = 0.0F;
+  floatx4 x[8];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int res = r0 + 4 * g + i;
+#pragma unroll
+    for (int nt = 0; nt < 8; ++nt) {
+      const size_t at = (size_t)res * kH + 16 * nt + r;
+      x[nt][i] = res < L ? h_v[at] + upd[at] : 0.0F;
     }
   }
+  ln_acc(x, w.n1g, w.n1b);
+#pragma unroll
+  for (int nt = 0; nt < 8; ++nt)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) A[(4 * g + i) * kLdH + 16 * nt + r] = x[nt][i];
   __syncthreads();
-  for (int t = lane; t < 16 * kH; t += 64) A[(t / kH) * kLdH + t % kH] = X[t / kH][t % kH];
-  __syncthreads();
+  floatx4 acc[8];
   for (int c = 0; c < kFF / kH; ++c) {
-    floatx4 acc[8];
     wave_gemm<8>(A, kLdH, w16.Win, kFF, kH * c, kH, acc);
     store_gelu<8>(acc, w.bin, kH * c, F, kLdF, tbl);
   }
   __syncthreads();
-  floatx4 acc[8];
   wave_gemm<8>(F, kLdF, w16.Wout, kH, 0, kFF, acc);
 #pragma unroll
   for (int nt = 0; nt < 8; ++nt) {
-    const int col = 16 * nt + r;
+    const float bv = w.bout[16 * nt + r];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) X[4 * g + i][col] = X[4 * g + i][col] + (acc[nt][i] + w.bout[col]);
+    for (int i = 0; i < 4; ++i) x[nt][i] = x[nt][i] + (acc[nt][i] + bv);
   }
-  __syncthreads();
-  for (int i = 0; i < 16; ++i) {
-    const int res = r0 + i;
-    if (res >= L) break;  // the same for every lane
-    ln_regs_wave(X[i][lane], X[i][lane + 64], w.n2g, w.n2b, X[i]);
+  ln_acc(x, w.n2g, w.n2b);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int res = r0 + 4 * g + i;
+    if (res >= L) continue;
     const float mk = mask[res];
-    h_v[(size_t)res * kH + lane] = X[i][lane] * mk;
-    h_v[(size_t)res * kH + lane + 64] = X[i][lane + 64] * mk;
+#pragma unroll
+    for (int nt = 0; nt < 8; ++nt) h_v[(size_t)res * kH + 16 * nt + r] = x[nt][i] * mk;
   }
 }
 
