@@ -232,6 +232,7 @@ def main() -> int:
     e_bw = int((pos[idx] < pos[:, None]).sum())
     bytes_step = 4.0 * (B * (3 * H * e_bw + L * (2 * H + V + 1)) + L * (2 * K + 1) * H + W_DEC) / L
     achieved = B * L * F_RES / (decode_ms * 1e-3) / 1e12
+    f_enc = L * K * 128 * 8768 + 786432 * L  # featurise + encode FLOP per backbone
     traffic, traffic_src = measured_traffic(f"design_L{L}_B{B}" + ("" if args.precision == "fp32" else "_bf16"))
     result = {
         "metric": METRIC,
@@ -284,6 +285,17 @@ def main() -> int:
             "unit": "GB/s",
             "frac": round(bytes_step / (us_step * 1e-6) / 1e9 / PEAK_HBM_GBPS, 5),
             "backward_edges": e_bw,
+        },
+        "encoder": {
+            "flop": f_enc,
+            "ms": round(float(ph[0]), 4),
+            "achieved": round(f_enc / (float(ph[0]) * 1e-3) / 1e12, 3),
+            "peak": PEAK_FP32_TFLOPS,
+            "unit": "TFLOP/s",
+            "frac": round(f_enc / (float(ph[0]) * 1e-3) / 1e12 / PEAK_FP32_TFLOPS, 4),
+            "note": ("featurise + encode, F_enc = S*128*8768 + 786432*L FLOP per backbone; in fp32 the "
+                     "encoder keeps the reference's rounding sequence (separate multiply and add on the "
+                     "VALU, ceiling peak/4) and in the 16-bit modes runs on the fp16 MFMA"),
         },
     }
     if cpu is not None:
