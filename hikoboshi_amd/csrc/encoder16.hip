@@ -22,8 +22,8 @@
 //   edge_msg16     one residue per workgroup (3 waves = 48 slots):
 //                  [h_i | e_ij | h_j] -> W1, GELU, W2, GELU, W3 -> the masked
 //                  sum over the residue's slots / 30 -> upd[i].
-//   node16         16 residues per workgroup (1 wave): LN1(h + upd), the FFN
-//                  on the MFMA, LN2, mask, all 16 rows at once.
+//   node16         16 residues per workgroup (4 waves, a quarter of the FFN
+//                  each): LN1(h + upd), the FFN on the MFMA, LN2, mask.
 //   edge_update16  32 edge slots per workgroup (2 waves): [h_i | e_ij | h_j]
 //                  -> W11, GELU, W12, GELU, W13, residual, LN3 -> h_E (valid
 //                  slots).
@@ -49,15 +49,16 @@ __device__ inline floatx4 mfma_f16(f16x8 a, f16x8 b, floatx4 c) {
 
 // acc[nt] = A[16 rows][K] . W[K][n0 + 16 nt + (0..15)] for nt < NT. A is the
 // wave's fp32 slab (lda floats per row); Wp the split weights, hi as
-// [K / 8][N][8] halves and lo at Wp + K * N. With lane = 16 g + r, acc[nt][i]
+// [K / 8][N][8] halves and lo at Wp + K * N (or Wp + lo_off when Wp starts
+// inside a larger matrix). With lane = 16 g + r, acc[nt][i]
 // is row 4 g + i, column n0 + 16 nt + r. The next k-step's weight fragments
 // load while the current ones are used.
 template <int NT>
 __device__ inline void wave_gemm(const float* A, int lda, const uint16_t* __restrict__ Wp, int N, int n0, int K,
-                                 floatx4 (&acc)[NT]) {
+                                 floatx4 (&acc)[NT], size_t lo_off = 0) {
   const int lane = threadIdx.x & 63, r = lane & 15, g = lane >> 4;
   const uint16_t* wh = Wp + ((size_t)g * N + n0 + r) * 8;
-  const uint16_t* wl = wh + (size_t)K * N;
+  const uint16_t* wl = wh + (lo_off ? lo_off : (size_t)K * N);
   const size_t kstep = (size_t)4 * N * 8;  // halves per 32 inputs
   floatx4 cor[NT];
 #pragma unroll
@@ -280,45 +281,60 @@ __global__ __launch_bounds__(192) void edge_msg16_kernel(EncLayerDev w, Enc16Lay
     upd[(size_t)res * kH + threadIdx.x] = (part[0][threadIdx.x] + part[1][threadIdx.x]) + part[2][threadIdx.x];
 }
 
-// 16 residues per workgroup of one wave; lane (r, g) holds rows 4 g + i,
-// columns 16 nt + r of every 128-wide activation (the MFMA output layout), so
-// both LayerNorms run on all 16 rows at once.
-__global__ __launch_bounds__(64) void node16_kernel(EncLayerDev w, Enc16LayerDev w16, const float* __restrict__ upd,
-                                                    const float* __restrict__ mask, int L, float* __restrict__ h_v) {
+// 16 residues per workgroup of four waves; lane (r, g) of a wave holds rows
+// 4 g + i, columns 16 nt + r of a 128-wide block (the MFMA output layout).
+// Wave 0 forms h1 = LN1(h + upd) for all 16 rows; wave w computes the FFN
+// hidden columns [128 w, 128 w + 128) and the W_out partial sum over those
+// inputs; wave 0 adds the four partials in order, the residual, LN2 and the
+// mask.
+__global__ __launch_bounds__(256) void node16_kernel(EncLayerDev w, Enc16LayerDev w16, const float* __restrict__ upd,
+                                                     const float* __restrict__ mask, int L, float* __restrict__ h_v) {
   __shared__ __attribute__((aligned(16))) float A[16 * kLdH];
   __shared__ __attribute__((aligned(16))) float F[16 * kLdF];
+  __shared__ __attribute__((aligned(16))) float Pt[4][16 * kLdH];
   __shared__ float tbl[17];
-  const int lane = threadIdx.x & 63, r = lane & 15, g = lane >> 4;
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, r = lane & 15, g = lane >> 4;
   const int r0 = blockIdx.x * 16;
-  if (lane < 17) tbl[lane] = kExpNegTable[lane];
+  if (threadIdx.x < 17) tbl[threadIdx.x] = kExpNegTable[threadIdx.x];
   floatx4 x[8];
+  if (wave == 0) {
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int res = r0 + 4 * g + i;
+    for (int i = 0; i < 4; ++i) {
+      const int res = r0 + 4 * g + i;
 #pragma unroll
-    for (int nt = 0; nt < 8; ++nt) {
-      const size_t at = (size_t)res * kH + 16 * nt + r;
-      x[nt][i] = res < L ? h_v[at] + upd[at] : 0.0F;
+      for (int nt = 0; nt < 8; ++nt) {
+        const size_t at = (size_t)res * kH + 16 * nt + r;
+        x[nt][i] = res < L ? h_v[at] + upd[at] : 0.0F;
+      }
     }
+    ln_acc(x, w.n1g, w.n1b);
+#pragma unroll
+    for (int nt = 0; nt < 8; ++nt)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) A[(4 * g + i) * kLdH + 16 * nt + r] = x[nt][i];
   }
-  ln_acc(x, w.n1g, w.n1b);
+  __syncthreads();
+  floatx4 acc[8];
+  wave_gemm<8>(A, kLdH, w16.Win, kFF, kH * wave, kH, acc);
+  store_gelu<8>(acc, w.bin, kH * wave, F, kLdF, tbl);
+  __syncthreads();
+  // inputs [128 w, 128 w + 128) of W_out: its packed rows 16 w .. 16 w + 15
+  wave_gemm<8>(F + kH * wave, kLdF, w16.Wout + (size_t)wave * 16 * kH * 8, kH, 0, kH, acc, (size_t)kFF * kH);
 #pragma unroll
   for (int nt = 0; nt < 8; ++nt)
 #pragma unroll
-    for (int i = 0; i < 4; ++i) A[(4 * g + i) * kLdH + 16 * nt + r] = x[nt][i];
+    for (int i = 0; i < 4; ++i) Pt[wave][(4 * g + i) * kLdH + 16 * nt + r] = acc[nt][i];
   __syncthreads();
-  floatx4 acc[8];
-  for (int c = 0; c < kFF / kH; ++c) {
-    wave_gemm<8>(A, kLdH, w16.Win, kFF, kH * c, kH, acc);
-    store_gelu<8>(acc, w.bin, kH * c, F, kLdF, tbl);
-  }
-  __syncthreads();
-  wave_gemm<8>(F, kLdF, w16.Wout, kH, 0, kFF, acc);
+  if (wave != 0) return;
 #pragma unroll
   for (int nt = 0; nt < 8; ++nt) {
-    const float bv = w.bout[16 * nt + r];
+    const int col = 16 * nt + r;
+    const float bv = w.bout[col];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) x[nt][i] = x[nt][i] + (acc[nt][i] + bv);
+    for (int i = 0; i < 4; ++i) {
+      const int at = (4 * g + i) * kLdH + col;
+      x[nt][i] = x[nt][i] + ((((Pt[0][at] + Pt[1][at]) + Pt[2][at]) + Pt[3][at]) + bv);
+    }
   }
   ln_acc(x, w.n2g, w.n2b);
 #pragma unroll
@@ -392,7 +408,7 @@ hipError_t launch_encoder16(const ModelDev& m, const float* coords, const uint8_
   for (int l = 0; l < kLayers; ++l) {
     const Enc16LayerDev& w16 = m.enc16.layer[l];
     edge_msg16_kernel<<<(unsigned)L, 192, 0, stream>>>(m.enc[l], w16, h_e, h_v, idx, mask, L, K, upd);
-    node16_kernel<<<(unsigned)((L + 15) / 16), 64, 0, stream>>>(m.enc[l], w16, upd, mask, L, h_v);
+    node16_kernel<<<(unsigned)((L + 15) / 16), 256, 0, stream>>>(m.enc[l], w16, upd, mask, L, h_v);
     edge_update16_kernel<<<tiles, 128, 0, stream>>>(m.enc[l], w16, h_e, h_v, idx, L, K);
   }
   return hipGetLastError();
