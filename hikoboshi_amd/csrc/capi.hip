@@ -1156,8 +1156,10 @@ hkbs_status teacher_forced_chunk(hkbs_pmpnn* ctx, const float* coords, const uin
   float* NB = ar.take<float>((size_t)L * 256);
   hipStream_t s = ctx->stream;
   HK_CHECK(launch_knn(coords, src, L, K, e.idx, e.d2, e.mask, e.ca, s, seg, offsets), "kNN launch failed");
-  HK_CHECK(launch_edge_embed(ctx->model, coords, src, resid, chain, e.idx, L, K, e.h_e, s), "feature launch failed");
-  HK_CHECK(launch_encoder(ctx->model, e.idx, e.mask, L, K, e.h_v, e.h_e, e.scratch, s), "encoder launch failed");
+  // Teacher-forced log-probs are not temperature-scaled, so the 1e-4 bar leaves room for the fp32-accurate
+  // split-operand MFMA encoder (about 2x the throughput of the reference-order encoder).
+  HK_CHECK(launch_encoder16(ctx->model, coords, src, resid, chain, e.idx, e.mask, L, K, e.h_v, e.h_e, e.scratch, s),
+           "encoder launch failed");
   HK_CHECK(launch_q_precompute(ctx->model, e.h_v, L, Q, s), "decoder precompute failed");
   TfArgs a{};
   a.idx = e.idx;

@@ -131,7 +131,10 @@ hkbs_status hkbs_pmpnn_design_device(hkbs_pmpnn* ctx, const float* coords,
 
 /* Teacher-forced scoring of one protein (proteinmpnn_teacher_forced_forward_scalar,
  * cpp/modules/mpnn/inverse_fold_scalar.cpp:905-952): plain log_softmax
- * log-probs [L,21] and mean NLL. order may be NULL (N-to-C). Host memory. */
+ * log-probs [L,21] and mean NLL. order may be NULL (N-to-C). Host memory.
+ * Scoring runs in fp32 accuracy in every precision mode; its encoder is the
+ * split-operand MFMA one (fp32-accurate, not the reference's rounding
+ * sequence), since untempered log-probs leave room within 1e-4. */
 hkbs_status hkbs_pmpnn_score(hkbs_pmpnn* ctx, const float* coords, const uint8_t* atom_sources,
                              const int32_t* residue_indices, const int32_t* chain_labels,
                              const float* chain_mask, const int32_t* tokens,
@@ -161,8 +164,8 @@ hkbs_status hkbs_pmpnn_backbone_noise(const float* coords, const uint8_t* atom_s
                                       float sigma, uint64_t seed, float* out);
 
 /* Selects the arithmetic of later design and encode calls on this context
- * (teacher-forced scoring stays fp32; no counterpart in the reference, which
- * has only its fp32 scalar path). */
+ * (teacher-forced scoring is the same in every mode; no counterpart in the
+ * reference, which has only its fp32 scalar path). */
 hkbs_status hkbs_pmpnn_set_precision(hkbs_pmpnn* ctx, int32_t precision);
 
 /* Phase timing (instrumentation; no counterpart in the reference, which has
