@@ -848,6 +848,7 @@ hkbs_status design_on_device(hkbs_pmpnn* ctx, const float* coords, const uint8_t
   a.precision = ctx->precision;
   const int team = decode_team_size(a.precision, B, 8);
   a.max_members = kDecodeGroup * team;
+  a.pass_granule = team;
   if (const char* env = std::getenv("HKBS_DECODE_MAX_MEMBERS"))
     a.max_members = std::max(1, std::min(a.max_members, std::atoi(env)));
   ctx->last_decode = a;
@@ -1063,6 +1064,7 @@ hkbs_status hkbs_pmpnn_design(hkbs_pmpnn* ctx, const float* coords, const uint8_
     // other work): decode again with one workgroup per sequence.
     DecodeArgs one = ctx->last_decode;
     one.max_members = kDecodeGroup;  // steps one workgroup can hold
+    one.pass_granule = 1;
     HK_CHECK(launch_decode_schedule(one, s), "decode schedule launch failed");
     HK_CHECK(launch_decode(ctx->model, one, s, 1), "decode launch failed");
     HK_CHECK(hipMemcpyAsync(tokens, d_tokens, (size_t)B * L * 4, hipMemcpyDeviceToHost, s), "D2H failed");

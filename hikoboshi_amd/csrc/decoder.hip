@@ -730,6 +730,8 @@ __global__ void neighbour_schedule_kernel(const int32_t* __restrict__ orders, co
 // the pending counts as bytes in LDS.
 constexpr int kSchedThreads = 512;
 constexpr int kSchedMaxL = 60000;  // pending counts as L bytes of LDS
+constexpr int kSchedPrioMaxL = 8192;  // balanced passes up to this length (heights as 2 L bytes of LDS)
+constexpr int kSchedCand = 1024;      // ready steps a balanced pass chooses from
 
 // Active step u of order q: valid residue with mask != 0.
 __device__ inline bool sched_active(const int32_t* order, const float* mask, int L, int u) {
@@ -855,17 +857,80 @@ __global__ void dep_fill_kernel(const int32_t* __restrict__ orders, const float*
 // inactive or dropped.
 __device__ inline int sched_pending(const uint32_t* w, int u) { return (w[u >> 2] >> (8 * (u & 3))) & 0xFF; }
 
-// Per order (one block): the pass loop. Pass p scans the steps from the first
-// unplaced one, in blocks of kSchedThreads, for ready ones (pending count 0)
-// until it holds max_members, then clears their dependents' counts.
+// Height of every active step of one order: 1 + the largest height among the
+// later steps that wait for it, 1 when none does (the longest chain of
+// dependent steps it starts). Computed in rounds: round r gives height r to
+// the steps whose dependents all have heights, then takes them off their own
+// earlier neighbours' counts of dependents still without one. ht[u] = 0xFFFF
+// for an inactive step; outw holds those counts as 16-bit halves. Returns the
+// number of rounds, the longest chain. Every round places at least one step
+// (dependencies run from smaller to larger u), so the loop ends.
+__device__ int sched_heights(const int32_t* order, const float* mask, const int32_t* np, const int32_t* oq,
+                             int L, int K, int nact, uint16_t* ht, uint32_t* outw, int* list, int* tmp) {
+  uint16_t* outc = reinterpret_cast<uint16_t*>(outw);
+  for (int u = threadIdx.x; u < L; u += kSchedThreads) {
+    const bool a = sched_active(order, mask, L, u);
+    ht[u] = a ? 0 : 0xFFFF;
+    outc[u] = (uint16_t)(a ? oq[u + 1] - oq[u] : 0);  // < L <= kSchedPrioMaxL
+  }
+  __syncthreads();
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  int rounds = 0, left = nact;
+  while (left > 0) {
+    ++rounds;
+    int got = 0;
+    // Blocks of kSchedThreads steps in increasing u. A step placed here only
+    // lowers the counts of smaller steps, whose blocks this round has already
+    // examined, so no step gets the height of a dependent placed this round.
+    for (int c0 = 0; c0 < L; c0 += kSchedThreads) {
+      const int u = c0 + threadIdx.x;
+      const bool now = u < L && ht[u] == 0 && outc[u] == 0;
+      int tot;
+      const int r = block_scan(now ? 1 : 0, tmp, &tot);
+      if (now) {
+        ht[u] = (uint16_t)rounds;
+        list[r] = u;
+      }
+      __syncthreads();
+      // wave w takes the placed steps w, w + 8, ...; lane k their slot k (K <= 64)
+      for (int i = wave; i < tot; i += kSchedThreads / 64) {
+        const int v = list[i];
+        if (lane < K) {
+          const int p = np[(size_t)v * K + lane];
+          if (p >= 0 && p < v && ht[p] != 0xFFFF) atomicSub(outw + (p >> 1), 1u << (16 * (p & 1)));
+        }
+      }
+      __syncthreads();
+      got += tot;
+    }
+    left -= got;
+    if (got == 0) break;
+  }
+  return rounds;
+}
+
+// Per order (one block): the pass loop. Pass p takes ready steps (pending
+// count 0), at most max_members, then clears their dependents' counts.
+//   - granule <= 1 (or L > kSchedPrioMaxL): the first ready steps in order of
+//     u, scanning from the first unplaced one.
+//   - granule G > 1 (a team of G workgroups shares each pass, so a pass costs
+//     about as much as its share for the busiest workgroup, ceil(m / G)): a
+//     step is forced when its height reaches the passes left in the longest
+//     chain (deferring it would lengthen the schedule). The pass takes
+//     k = max(G floor(n / G), G ceil(f / G), min(n, G)) of its n ready steps
+//     (f forced; at most max_members): the k highest, ties to smaller u. It
+//     never defers a forced step unless max_members does.
 __global__ __launch_bounds__(kSchedThreads) void ready_schedule_kernel(
-    const int32_t* __restrict__ orders, const float* __restrict__ mask, int L, int K, int max_members,
-    const int32_t* __restrict__ indeg, const int32_t* __restrict__ off, const int32_t* __restrict__ dlist,
-    const int32_t* __restrict__ draw, const int32_t* __restrict__ meta, int32_t* __restrict__ sched,
-    int32_t* __restrict__ pstart, int32_t* __restrict__ npass) {
-  extern __shared__ __attribute__((aligned(16))) uint32_t pend[];  // ceil(L / 4) words
+    const int32_t* __restrict__ orders, const float* __restrict__ mask, const int32_t* __restrict__ nbp, int L,
+    int K, int max_members, int granule, const int32_t* __restrict__ indeg, const int32_t* __restrict__ off,
+    const int32_t* __restrict__ dlist, const int32_t* __restrict__ draw, const int32_t* __restrict__ meta,
+    int32_t* __restrict__ sched, int32_t* __restrict__ pstart, int32_t* __restrict__ npass) {
+  // ceil(L / 4) words of pending counts, then (balanced passes) 16-bit heights
+  // and dependents' counts, ceil(L / 2) words each
+  extern __shared__ __attribute__((aligned(16))) uint32_t pend[];
   __shared__ int tmp[kSchedThreads / 64];
   __shared__ int chosen[256];
+  __shared__ int cand[kSchedCand];
   __shared__ int low_s, found_s;
   const int q = blockIdx.x;
   const int32_t* order = orders + (size_t)q * L;
@@ -892,6 +957,12 @@ __global__ __launch_bounds__(kSchedThreads) void ready_schedule_kernel(
     return;
   }
   const int words = (L + 3) / 4;
+  const bool balance = granule > 1 && L <= kSchedPrioMaxL;
+  uint16_t* ht = reinterpret_cast<uint16_t*>(pend + words);
+  int height = 0;
+  if (balance)
+    height = sched_heights(order, mask, nbp + (size_t)q * L * K, oq, L, K, nact, ht, pend + words + (L + 1) / 2,
+                           cand, tmp);
   for (int w = threadIdx.x; w < words; w += kSchedThreads) {
     uint32_t v = 0;
     for (int b = 0; b < 4; ++b) {
@@ -908,13 +979,92 @@ __global__ __launch_bounds__(kSchedThreads) void ready_schedule_kernel(
   while (placed < nact) {
     ++pass;
     int found = 0;
-    for (int cursor = low_s; found < cap && cursor < L; cursor += kSchedThreads) {
-      const int u = cursor + threadIdx.x;
-      const bool rdy = u < L && sched_pending(pend, u) == 0;
-      int tot;
-      const int rank = block_scan(rdy ? 1 : 0, tmp, &tot);
-      if (rdy && found + rank < cap) chosen[found + rank] = u;
-      found = min(cap, found + tot);
+    if (!balance) {
+      for (int cursor = low_s; found < cap && cursor < L; cursor += kSchedThreads) {
+        const int u = cursor + threadIdx.x;
+        const bool rdy = u < L && sched_pending(pend, u) == 0;
+        int tot;
+        const int rank = block_scan(rdy ? 1 : 0, tmp, &tot);
+        if (rdy && found + rank < cap) chosen[found + rank] = u;
+        found = min(cap, found + tot);
+      }
+    } else {
+      // candidates: the first kSchedCand ready steps, in order of u
+      const int remaining = height - pass + 1;
+      int n = 0, myf = 0, tot;
+      for (int cursor = low_s; n < kSchedCand && cursor < L; cursor += kSchedThreads) {
+        const int u = cursor + threadIdx.x;
+        const bool rdy = u < L && sched_pending(pend, u) == 0;
+        const int rank = block_scan(rdy ? 1 : 0, tmp, &tot);
+        if (rdy && n + rank < kSchedCand) {
+          cand[n + rank] = u;
+          myf += (int)ht[u] >= remaining;
+        }
+        n = min(kSchedCand, n + tot);
+      }
+      const int G = granule;
+      __syncthreads();  // cand complete
+      if (n <= 64) {
+        // one wave: lane i holds candidate i; its rank orders by height, then u
+        if (threadIdx.x < 64) {
+          const int lane = threadIdx.x;
+          const bool in = lane < n;
+          const int u = in ? cand[lane] : 0;
+          const int h = in ? (int)ht[u] : -1;
+          const int f = __popcll(__ballot(in && h >= remaining));
+          const int k = min(max(max(G * (n / G), G * ((f + G - 1) / G)), min(n, G)), min(n, cap));
+          bool sel = in;
+          if (k < n) {
+            int rank = 0;
+            for (int j = 0; j < n; ++j) {
+              const int hj = __shfl(h, j, 64);
+              rank += (hj > h) || (hj == h && j < lane);
+            }
+            sel = in && rank < k;
+          }
+          const unsigned long long m = __ballot(sel);
+          if (sel) chosen[__popcll(m & ((1ULL << lane) - 1))] = u;
+          if (lane == 0) found_s = __popcll(m);
+        }
+        __syncthreads();
+        found = found_s;
+      } else {
+        block_scan(myf, tmp, &tot);
+        const int f = tot;
+        int k = max(max(G * (n / G), G * ((f + G - 1) / G)), min(n, G));
+        k = min(k, min(n, cap));
+        if (k < n) {
+          // threshold height thr: the largest with at least k candidates at or above it
+          int lo = 1, hi = height;
+          while (lo < hi) {
+            const int mid = (lo + hi + 1) >> 1;
+            int c = 0;
+            for (int i = threadIdx.x; i < n; i += kSchedThreads) c += (int)ht[cand[i]] >= mid;
+            block_scan(c, tmp, &tot);
+            if (tot >= k) lo = mid;
+            else hi = mid - 1;
+          }
+          const int thr = lo;
+          int c = 0;
+          for (int i = threadIdx.x; i < n; i += kSchedThreads) c += (int)ht[cand[i]] > thr;
+          block_scan(c, tmp, &tot);
+          const int need = k - tot;  // candidates at height thr to take, the smallest u first
+          int eq = 0;
+          for (int c0 = 0; c0 < n; c0 += kSchedThreads) {
+            const int i = c0 + threadIdx.x;
+            const int h = i < n ? (int)ht[cand[i]] : 0;
+            const int er = block_scan(i < n && h == thr ? 1 : 0, tmp, &tot);
+            const bool sel = i < n && (h > thr || (h == thr && eq + er < need));
+            eq += tot;
+            const int r = block_scan(sel ? 1 : 0, tmp, &tot);
+            if (sel) chosen[found + r] = cand[i];
+            found += tot;
+          }
+        } else {
+          for (int i = threadIdx.x; i < k; i += kSchedThreads) chosen[i] = cand[i];
+          found = k;
+        }
+      }
     }
     // The first unplaced step is always ready (its earlier neighbours are all
     // placed); taking it when nothing was found guarantees progress.
@@ -1009,8 +1159,11 @@ hipError_t launch_decode_schedule(const DecodeArgs& a, hipStream_t stream) {
   sched_prep_kernel<<<nq, kSchedThreads, 0, stream>>>(a.orders, a.pos, a.mask, a.L, sequential, off, a.draw, a.sched,
                                                      a.pstart, meta);
   dep_fill_kernel<<<dim3(blocks, nq), 256, 0, stream>>>(a.orders, a.mask, a.nbp, a.L, a.K, off, cur, dlist);
-  ready_schedule_kernel<<<nq, kSchedThreads, sizeof(uint32_t) * ((L + 3) / 4), stream>>>(
-      a.orders, a.mask, a.L, a.K, a.max_members, indeg, off, dlist, a.draw, meta, a.sched, a.pstart, a.npass);
+  const bool balance = a.pass_granule > 1 && a.L <= kSchedPrioMaxL;
+  const size_t lds_words = (L + 3) / 4 + (balance ? 2 * ((L + 1) / 2) : 0);
+  ready_schedule_kernel<<<nq, kSchedThreads, sizeof(uint32_t) * lds_words, stream>>>(
+      a.orders, a.mask, a.nbp, a.L, a.K, a.max_members, a.pass_granule, indeg, off, dlist, a.draw, meta, a.sched,
+      a.pstart, a.npass);
   return hipGetLastError();
 }
 

@@ -164,6 +164,7 @@ struct DecodeArgs {
   uint32_t spin_limit;    // polls before a team barrier gives up (set by launch_decode)
   int precision;          // 0 fp32, 1 bf16, 2 fp16 weights and message rows (see decode_kernel)
   int max_members;        // most steps one pass decodes (<= kDecodeGroup * team size)
+  int pass_granule;       // team size the schedule balances passes for (<= 1: none)
 };
 constexpr int kDecodeGroup = 4;  // steps one workgroup decodes in a pass
 // int32 words of DecodeArgs.sched_tmp for nq orders of length L with K neighbours.
