@@ -34,8 +34,8 @@ namespace {
 
 constexpr int kRows = 32;    // edge rows per tile (any rows of the [L * K] edge list)
 constexpr int kLdE = 36;     // k-major leading dimension of edge tiles
-constexpr int kEdgeRM = 2;   // rows per thread (16 row groups)
-constexpr int kEdgeCN = 8;   // cols per thread (16 col groups)
+constexpr int kEdgeRM = 4;   // rows per thread (8 row groups)
+constexpr int kEdgeCN = 4;   // cols per thread (32 col groups)
 constexpr int kKC = 32;      // weight rows staged per chunk
 
 // Loads rows of a [*, 128] row-major matrix into a k-major LDS tile
@@ -68,7 +68,7 @@ __global__ __launch_bounds__(256) void edge_msg_kernel(EncLayerDev w, const floa
   const size_t S = (size_t)L * K;
   const size_t slot0 = (size_t)blockIdx.x * kRows;
   const int n_rows = (int)min((size_t)kRows, S - slot0);
-  const int rg = threadIdx.x / 16, cg = threadIdx.x % 16;
+  const int rg = threadIdx.x / 32, cg = threadIdx.x % 32;
   const int row0 = rg * kEdgeRM, col0 = cg * kEdgeCN;
 
   float acc[kEdgeRM][kEdgeCN];
@@ -288,7 +288,7 @@ __global__ __launch_bounds__(256) void edge_update_kernel(EncLayerDev w, float* 
   const size_t S = (size_t)L * K;
   const size_t slot0 = (size_t)blockIdx.x * kRows;
   const int n_rows = (int)min((size_t)kRows, S - slot0);
-  const int rg = threadIdx.x / 16, cg = threadIdx.x % 16;
+  const int rg = threadIdx.x / 32, cg = threadIdx.x % 32;
   const int row0 = rg * kEdgeRM, col0 = cg * kEdgeCN;
 
   float acc[kEdgeRM][kEdgeCN];
