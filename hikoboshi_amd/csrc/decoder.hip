@@ -245,7 +245,7 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(ModelDev m, DecodeArgs
   __shared__ __attribute__((aligned(16))) float Pd[kGroup * 2 * kH];  // W1d h^l of layers 1, 2
   __shared__ float logits[kGroup * 32];
   __shared__ __attribute__((aligned(16))) float prm[kPrmSize];
-  __shared__ float tbl[17];
+  __shared__ __attribute__((aligned(16))) float gtab[kGeluPolyRows * 8];  // GELU polynomials
   __shared__ int nbr[kGroup * kKmax];
   __shared__ int bwf[kGroup * kKmax];
   __shared__ int tres[kGroup];
@@ -282,7 +282,7 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(ModelDev m, DecodeArgs
   const uint64_t seed = a.seeds[b];
   const float T = (a.temperature > 0.0F && isfinite(a.temperature)) ? a.temperature : 1.0F;
   const bool greedy = a.greedy || a.temperature <= 0.0F;
-  if (threadIdx.x < 17) tbl[threadIdx.x] = kExpNegTable[threadIdx.x];
+  for (int i = threadIdx.x; i < kGeluPolyRows * 8; i += kThreads) gtab[i] = kGeluPoly[i];
   if (threadIdx.x == 0) bad = 0;
   for (int l = 0; l < kLayers; ++l) {
     const DecLayerDev& w = m.dec[l];
@@ -418,8 +418,8 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(ModelDev m, DecodeArgs
                 xv.y += e[s].y + z[s].y;
                 xv.z += e[s].z + z[s].z;
                 xv.w += e[s].w + z[s].w;
-                float4 v = make_float4(gelu_fast(xv.x, tbl), gelu_fast(xv.y, tbl), gelu_fast(xv.z, tbl),
-                                       gelu_fast(xv.w, tbl));
+                float4 v = make_float4(gelu_poly(xv.x, gtab), gelu_poly(xv.y, gtab), gelu_poly(xv.z, gtab),
+                                       gelu_poly(xv.w, gtab));
                 if (k >= K) v = make_float4(0.F, 0.F, 0.F, 0.F);
                 _Float16* gh = G16 + (((s / 3) * 2) * kKmax + k) * kLdH + c;
                 const float vv[4] = {v.x, v.y, v.z, v.w};
@@ -493,7 +493,7 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(ModelDev m, DecodeArgs
 #pragma unroll
               for (int e = 0; e < 4; ++e) {
                 const int row = mb * 16 + 4 * g + e;
-                const float gv = gelu_fast(acc[mb][e] + b2, tbl);
+                const float gv = gelu_poly(acc[mb][e] + b2, gtab);
                 sum += row < K ? gv : 0.0F;
               }
             sum += __shfl_xor(sum, 16, 64);
@@ -534,7 +534,7 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(ModelDev m, DecodeArgs
         __syncthreads();
         for (int task = threadIdx.x; task < ml * kFF; task += kThreads) {
           const int i = task / kFF, o = task % kFF;
-          ff[task] = gelu_fast(GIn::sum(part, i, o) + pl[kPrmBin + o], tbl);
+          ff[task] = gelu_poly(GIn::sum(part, i, o) + pl[kPrmBin + o], gtab);
         }
         __syncthreads();
         // h^{l+1} = LN2(h1 + (W_out f + b)) (the mask gate is 1 for an active residue)

@@ -10,6 +10,8 @@
 
 #include <cstdint>
 
+#include "gelu_poly_table.hpp"
+
 namespace hkbs {
 
 typedef float floatx4 __attribute__((ext_vector_type(4)));
@@ -109,6 +111,36 @@ __device__ inline float gelu_fast(float x, const float* tbl) {
                 r * (1.0F / 6.0F + r * (1.0F / 24.0F + r * (1.0F / 120.0F + r * (1.0F / 720.0F))))));
   const float ex = tbl[n];
   const float mag = 1.0F - poly * (ex * e);
+  return 0.5F * x * (1.0F + __builtin_copysignf(mag, x));
+}
+
+// The decode loop's GELU with the A&S term P(v) (erf = 1 - P) taken from a
+// per-segment polynomial instead of the reciprocal, the Horner in t and the
+// exp Taylor polynomial (gelu_poly_gen.py fits the table to the reference
+// expression, within 7.4e-8 absolute; the segments keep the reference's exp
+// table breakpoints, and row 17, v >= sqrt(15.5), is zero since the
+// reference's 1 - P rounds to 1 there). tab = the kGeluPolyRows x 8 table in
+// LDS (16-byte aligned). The tail keeps the reference's rounding of
+// mag = 1 - P and 0.5 x (1 + copysign(mag, x)). About 20 VALU slots against
+// the 31 of gelu_fast. Over all 2^32 inputs it is closer to the reference
+// expression than gelu_fast (5.1 against 7.5 units of ulp(result) + |x| 2^-25)
+// and equal to it on infinities and NaN.
+__device__ inline float gelu_poly(float x, const float* tab) {
+  // v > 4 takes row 17 (zero) as the reference's v > 4 case does; clamping v
+  // rather than q keeps u finite for x = +-inf and NaN
+  const float v = fminf(fabsf(x) * 0.7071067811865475F, 4.0F);
+  const float q = v * v;
+  const int row = static_cast<int>(q + 0.5F) + (v >= kGeluPolySplit ? 1 : 0);
+  const float4 c0 = *reinterpret_cast<const float4*>(tab + 8 * row);
+  const float4 c1 = *reinterpret_cast<const float4*>(tab + 8 * row + 4);
+  const float u = v - c0.x;
+  float p = c1.w * u + c1.z;
+  p = p * u + c1.y;
+  p = p * u + c1.x;
+  p = p * u + c0.w;
+  p = p * u + c0.z;
+  p = p * u + c0.y;
+  const float mag = 1.0F - p;
   return 0.5F * x * (1.0F + __builtin_copysignf(mag, x));
 }
 

@@ -5,11 +5,18 @@
 //             expression as written in cpp/include/hikoboshi/primitives/compute/gelu.hpp:22-51
 //             with fast_exp_neg (cpp/include/hikoboshi/primitives/detail/fast_exp_neg.hpp:12-55),
 //             IEEE division and every range check taken as a branch;
-//   gelu_fast (decode loop) vs gelu_fast_select: the same formula with the
-//             hardware reciprocal, the v > 4 case as a select and the sign by
-//             comparison (the form gelu_fast replaced).
-// Results must agree bit for bit (any NaN equals any NaN). Test infrastructure
-// only: built into tests/libdevice_math_check.so and called by
+//   gelu_fast (earlier decode loop) vs gelu_fast_select: the same formula with
+//             the hardware reciprocal, the v > 4 case as a select and the sign
+//             by comparison (the form gelu_fast replaced).
+// Those results must agree bit for bit (any NaN equals any NaN). The decode
+// loop's gelu_poly (the A&S term from per-segment polynomials) is measured
+// against gelu: on non-finite inputs it must agree bit for bit; on finite
+// inputs the largest |gelu_poly - gelu| in units of
+//   ulp(gelu(x)) + |x| 2^-25  (one ulp of the result plus half an x-scaled step
+//                              of the float grid under 1 that mag = 1 - P is
+//                              rounded to)
+// is reported, with the same figure for gelu_fast for comparison. Test
+// infrastructure only: built into tests/libdevice_math_check.so and called by
 // tests/test_gpu_device_math.py.
 #include <hip/hip_runtime.h>
 
@@ -79,12 +86,27 @@ __device__ inline bool same_bits(float a, float b) {
   return (a != a && b != b) || __float_as_uint(a) == __float_as_uint(b);
 }
 
-// counts[0], first[0]: gelu; counts[1], first[1]: gelu_fast (first = smallest
-// mismatching bit pattern, 0xFFFFFFFF if none).
-__global__ void check_kernel(unsigned long long* counts, unsigned int* first) {
+// |a - b| in units of ulp(b) + |x| 2^-25 (b finite).
+__device__ inline float dev_units(float a, float b, float x) {
+  const float ab = fabsf(b);
+  const float ulp = __uint_as_float(__float_as_uint(ab) + 1u) - ab;
+  const float unit = fmaxf(ulp, 1.4e-45F) + fabsf(x) * 2.98023224e-08F;
+  return fabsf(a - b) / unit;
+}
+
+// counts[0], first[0]: gelu; counts[1], first[1]: gelu_fast; counts[2],
+// first[2]: gelu_poly on non-finite inputs (first = smallest mismatching bit
+// pattern, 0xFFFFFFFF if none). worst[0], worst[1]: largest deviation units
+// (float bits) of gelu_poly and gelu_fast against gelu on finite inputs;
+// worst[2]: the input of worst[0].
+__global__ void check_kernel(unsigned long long* counts, unsigned int* first, unsigned int* worst) {
   __shared__ float tbl[17];
+  __shared__ __attribute__((aligned(16))) float gtab[hkbs::kGeluPolyRows * 8];
   if (threadIdx.x < 17) tbl[threadIdx.x] = kExpNegTable[threadIdx.x];
+  for (int i = threadIdx.x; i < hkbs::kGeluPolyRows * 8; i += blockDim.x) gtab[i] = hkbs::kGeluPoly[i];
   __syncthreads();
+  float w_poly = 0.0F, w_fast = 0.0F;
+  unsigned int w_at = 0xFFFFFFFFu;
   const uint64_t stride = (uint64_t)gridDim.x * blockDim.x;
   for (uint64_t bits = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; bits < (1ull << 32); bits += stride) {
     const float x = __uint_as_float(static_cast<unsigned int>(bits));
@@ -92,32 +114,58 @@ __global__ void check_kernel(unsigned long long* counts, unsigned int* first) {
       atomicAdd(&counts[0], 1ull);
       atomicMin(&first[0], static_cast<unsigned int>(bits));
     }
-    if (!same_bits(hkbs::gelu_fast(x, tbl), gelu_fast_select(x, tbl))) {
+    const float fast = hkbs::gelu_fast(x, tbl);
+    if (!same_bits(fast, gelu_fast_select(x, tbl))) {
       atomicAdd(&counts[1], 1ull);
       atomicMin(&first[1], static_cast<unsigned int>(bits));
     }
+    const float ref = hkbs::gelu(x);
+    const float poly = hkbs::gelu_poly(x, gtab);
+    if (!isfinite(x)) {
+      if (!same_bits(poly, ref)) {
+        atomicAdd(&counts[2], 1ull);
+        atomicMin(&first[2], static_cast<unsigned int>(bits));
+      }
+    } else if (isfinite(ref)) {
+      const float d = dev_units(poly, ref, x);
+      if (!(d <= w_poly)) {  // also catches a NaN result
+        w_poly = d != d ? 3.0e38F : d;
+        w_at = static_cast<unsigned int>(bits);
+      }
+      const float df = dev_units(fast, ref, x);
+      w_fast = fmaxf(w_fast, df != df ? 3.0e38F : df);
+    }
   }
+  const unsigned int prev = atomicMax(&worst[0], __float_as_uint(w_poly));
+  if (__float_as_uint(w_poly) > prev) atomicExch(&worst[2], w_at);
+  atomicMax(&worst[1], __float_as_uint(w_fast));
 }
 
 }  // namespace
 
-// Runs the check on the current device; writes 2 counts and 2 first
-// mismatches. Returns the HIP status of the run.
-extern "C" int hkbs_check_device_gelu(unsigned long long* counts_out, unsigned int* first_out) {
+// Runs the check on the current device; writes 3 counts, 3 first mismatches
+// and worst[3] (see check_kernel). Returns the HIP status of the run.
+extern "C" int hkbs_check_device_gelu(unsigned long long* counts_out, unsigned int* first_out,
+                                      unsigned int* worst_out) {
   unsigned long long* counts = nullptr;
   unsigned int* first = nullptr;
-  hipError_t e = hipMalloc(&counts, 2 * sizeof(unsigned long long));
-  if (e == hipSuccess) e = hipMalloc(&first, 2 * sizeof(unsigned int));
-  if (e == hipSuccess) e = hipMemset(counts, 0, 2 * sizeof(unsigned long long));
-  if (e == hipSuccess) e = hipMemset(first, 0xFF, 2 * sizeof(unsigned int));
+  unsigned int* worst = nullptr;
+  hipError_t e = hipMalloc(&counts, 3 * sizeof(unsigned long long));
+  if (e == hipSuccess) e = hipMalloc(&first, 3 * sizeof(unsigned int));
+  if (e == hipSuccess) e = hipMalloc(&worst, 3 * sizeof(unsigned int));
+  if (e == hipSuccess) e = hipMemset(counts, 0, 3 * sizeof(unsigned long long));
+  if (e == hipSuccess) e = hipMemset(first, 0xFF, 3 * sizeof(unsigned int));
+  if (e == hipSuccess) e = hipMemset(worst, 0, 3 * sizeof(unsigned int));
   if (e == hipSuccess) {
-    check_kernel<<<8192, 256>>>(counts, first);
+    check_kernel<<<8192, 256>>>(counts, first, worst);
     e = hipGetLastError();
   }
   if (e == hipSuccess) e = hipDeviceSynchronize();
-  if (e == hipSuccess) e = hipMemcpy(counts_out, counts, 2 * sizeof(unsigned long long), hipMemcpyDeviceToHost);
-  if (e == hipSuccess) e = hipMemcpy(first_out, first, 2 * sizeof(unsigned int), hipMemcpyDeviceToHost);
+  if (e == hipSuccess) e = hipMemcpy(counts_out, counts, 3 * sizeof(unsigned long long), hipMemcpyDeviceToHost);
+  if (e == hipSuccess) e = hipMemcpy(first_out, first, 3 * sizeof(unsigned int), hipMemcpyDeviceToHost);
+  if (e == hipSuccess) e = hipMemcpy(worst_out, worst, 3 * sizeof(unsigned int), hipMemcpyDeviceToHost);
   if (counts) (void)hipFree(counts);
   if (first) (void)hipFree(first);
+  if (worst) (void)hipFree(worst);
   return static_cast<int>(e);
 }

@@ -1,14 +1,18 @@
 """Exhaustive GPU check of the device GELUs (tests/csrc/device_math_check.hip).
 
 The encoder's gelu is evaluated without branches and with a reciprocal plus
-one Newton step in place of IEEE division; the decode loop's gelu_fast drops
-the v > 4 select and copies the sign. Both must equal their straightforward
-forms (the reference expression of cpp/include/hikoboshi/primitives/compute/gelu.hpp:22-51
+one Newton step in place of IEEE division; gelu_fast drops the v > 4 select
+and copies the sign. Both must equal their straightforward forms (the
+reference expression of cpp/include/hikoboshi/primitives/compute/gelu.hpp:22-51
 with fast_exp_neg.hpp:12-55, and the select form) bit for bit for every one of
 the 2^32 float inputs; the encoder tests then pin the straightforward form
-against the oracle.
+against the oracle. The decode loop's gelu_poly takes the A&S term from
+per-segment polynomials: on every finite input it must stay within
+POLY_UNITS units of ulp(gelu(x)) + |x| 2^-25 of gelu (the bit-exact reference
+form), and agree bit for bit on infinities and NaNs.
 """
 import ctypes as C
+import struct
 from pathlib import Path
 
 import pytest
@@ -16,6 +20,7 @@ import pytest
 pytestmark = pytest.mark.gpu
 
 LIB = Path(__file__).resolve().parent / "libdevice_math_check.so"
+POLY_UNITS = 6.0  # measured 5.08 (gelu_fast, the form it replaced: 7.55)
 
 
 def test_device_gelu_all_inputs():
@@ -23,9 +28,16 @@ def test_device_gelu_all_inputs():
         pytest.fail(f"{LIB} is not built (run __graft_entry__.build())")
     lib = C.CDLL(str(LIB))
     lib.hkbs_check_device_gelu.restype = C.c_int
-    counts = (C.c_ulonglong * 2)()
-    first = (C.c_uint * 2)()
+    counts = (C.c_ulonglong * 3)()
+    first = (C.c_uint * 3)()
+    worst = (C.c_uint * 3)()
     print("device gelu: 2^32 inputs", flush=True)
-    assert lib.hkbs_check_device_gelu(counts, first) == 0
+    assert lib.hkbs_check_device_gelu(counts, first, worst) == 0
+    as_float = lambda u: struct.unpack("<f", struct.pack("<I", u))[0]
+    w_poly, w_fast, at = as_float(worst[0]), as_float(worst[1]), as_float(worst[2])
+    print(f"gelu_poly: largest deviation {w_poly:.3f} units (near x = {at!r}); gelu_fast: {w_fast:.3f} units",
+          flush=True)
     assert counts[0] == 0, f"gelu differs from the reference form on {counts[0]} inputs (first {first[0]:#010x})"
     assert counts[1] == 0, f"gelu_fast differs from the select form on {counts[1]} inputs (first {first[1]:#010x})"
+    assert counts[2] == 0, f"gelu_poly differs on {counts[2]} non-finite inputs (first {first[2]:#010x})"
+    assert w_poly <= POLY_UNITS, f"gelu_poly deviates by {w_poly} units at x = {at!r}"
