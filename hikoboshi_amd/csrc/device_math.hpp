@@ -90,8 +90,8 @@ __device__ inline float gelu(float x) {
   return 0.5F * x * (1.0F + erfv);
 }
 
-// The same GELU formula for the decode loop, which is held to a tolerance
-// rather than to bit identity: the exp table is read from LDS (tbl = 17
+// The same GELU formula for code held to a tolerance rather than to bit
+// identity (the 16-bit encoder; the decode loop uses gelu_poly below): the exp table is read from LDS (tbl = 17
 // floats, kExpNegTable), 1/(1 + p v) is the hardware reciprocal (1 ulp) and
 // contraction is allowed. No v > 4 case is needed: there q is clamped to 16
 // and poly(t) exp(-16) < 2^-25, so mag rounds to exactly 1. The sign is copied
