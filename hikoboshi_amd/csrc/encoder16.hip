@@ -15,18 +15,25 @@
 // of LDS, split into hi / lo fragments as it is read, and it produces all 128
 // output columns as 8 MFMA tiles while the split weights stream from L2.
 //
+// The h_i block of W1 [h_i | e_ij | h_j] (and of W11) is the same for all K
+// slots of residue i, so node16 computes it once per residue into a prefix
+// buffer [L][256] (W11 part for this layer's edge update, W1 part for the
+// next layer's messages; zero for layer 0, where h = 0) and the edge kernels
+// run K = 256 over [e_ij | h_j], starting from the prefix.
+//
 // Kernels:
 //   edge_embed16   32 edge slots per workgroup (2 waves): 416 features ->
 //                  W_edge -> LN -> W_e -> h_E.
 //   per layer:
 //   edge_msg16     one residue per workgroup (3 waves = 48 slots):
-//                  [h_i | e_ij | h_j] -> W1, GELU, W2, GELU, W3 -> the masked
+//                  prefix + W1 [e_ij | h_j], GELU, W2, GELU, W3 -> the masked
 //                  sum over the residue's slots / 30 -> upd[i].
 //   node16         16 residues per workgroup (4 waves, a quarter of the FFN
-//                  each): LN1(h + upd), the FFN on the MFMA, LN2, mask.
-//   edge_update16  32 edge slots per workgroup (2 waves): [h_i | e_ij | h_j]
-//                  -> W11, GELU, W12, GELU, W13, residual, LN3 -> h_E (valid
-//                  slots).
+//                  each): LN1(h + upd), the FFN on the MFMA, LN2, mask; then
+//                  the W11 and next-layer W1 prefixes of the new h.
+//   edge_update16  32 edge slots per workgroup (2 waves): prefix + W11
+//                  [e_ij | h_j], GELU, W12, GELU, W13, residual, LN3 -> h_E
+//                  (valid slots).
 #include "device_math.hpp"
 #include "edge_chunk.hpp"
 #include "pmpnn_internal.hpp"
@@ -36,7 +43,7 @@ namespace {
 
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 
-constexpr int kLdA = 3 * kH + 4;   // floats per slab row of [h_i | e_ij | h_j] (16-byte pad)
+constexpr int kLdA = 2 * kH + 4;   // floats per slab row of [e_ij | h_j] (16-byte pad)
 constexpr int kLdX = kEdgeIn + 4;  // floats per slab row of edge features
 constexpr int kLdF = kFF + 4;      // floats per row of the FFN hidden layer
 constexpr int kLdH = kH + 4;       // floats per row of a 128-wide activation
@@ -157,21 +164,19 @@ __device__ inline void ln_acc(floatx4 (&acc)[8], const float* __restrict__ gam, 
   }
 }
 
-// The wave's 16 slab rows [h_v[res] | h_e[slot] | h_v[j]] with slot =
-// slot_of(row) (negative: a zero row), res = slot / K and j = idx[slot]
-// (outside [0, L): a zero h_j block).
+// The wave's 16 slab rows [h_e[slot] | h_v[j]] with slot = slot_of(row)
+// (negative: a zero row) and j = idx[slot] (outside [0, L): a zero h_j
+// block).
 template <typename SlotOf>
 __device__ inline void build_rows(float* A, const float* __restrict__ h_v, const float* __restrict__ h_e,
                                   const int32_t* __restrict__ idx, int L, int K, SlotOf slot_of) {
   const int lane = threadIdx.x & 63;
-  for (int t = lane; t < 16 * 96; t += 64) {
-    const int row = t / 96, c4 = t % 96, part = c4 / 32, col = 4 * (c4 % 32);
+  for (int t = lane; t < 16 * 64; t += 64) {
+    const int row = t / 64, c4 = t % 64, part = c4 / 32, col = 4 * (c4 % 32);
     const long long slot = slot_of(row);
     float4 v = make_float4(0.F, 0.F, 0.F, 0.F);
     if (slot >= 0) {
       if (part == 0) {
-        v = *reinterpret_cast<const float4*>(h_v + (size_t)(slot / K) * kH + col);
-      } else if (part == 1) {
         v = *reinterpret_cast<const float4*>(h_e + (size_t)slot * kH + col);
       } else {
         const int j = idx[slot];
@@ -230,7 +235,8 @@ __global__ __launch_bounds__(128) void edge_embed16_kernel(ModelDev m, const flo
 __global__ __launch_bounds__(192) void edge_msg16_kernel(EncLayerDev w, Enc16LayerDev w16,
                                                          const float* __restrict__ h_e, const float* __restrict__ h_v,
                                                          const int32_t* __restrict__ idx,
-                                                         const float* __restrict__ mask, int L, int K,
+                                                         const float* __restrict__ mask,
+                                                         const float* __restrict__ prefix, int L, int K,
                                                          float* __restrict__ upd) {
   __shared__ __attribute__((aligned(16))) float slab[3][16 * kLdA];
   __shared__ float tbl[17];
@@ -245,7 +251,14 @@ __global__ __launch_bounds__(192) void edge_msg16_kernel(EncLayerDev w, Enc16Lay
   });
   __syncthreads();
   floatx4 acc[8];
-  wave_gemm<8>(A, kLdA, w16.W1, kH, 0, 3 * kH, acc);
+  // rows 128 .. 383 of W1 (packed k-blocks 16 ..) over [e_ij | h_j], plus the h_i prefix
+  wave_gemm<8>(A, kLdA, w16.W1 + (size_t)16 * kH * 8, kH, 0, 2 * kH, acc, (size_t)3 * kH * kH);
+#pragma unroll
+  for (int nt = 0; nt < 8; ++nt) {
+    const float pv = prefix[(size_t)res * 256 + kH + 16 * nt + r];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) acc[nt][i] += pv;
+  }
   __syncthreads();
   store_gelu<8>(acc, w.b1, 0, A, kLdH, tbl);
   __syncthreads();
@@ -288,7 +301,8 @@ __global__ __launch_bounds__(192) void edge_msg16_kernel(EncLayerDev w, Enc16Lay
 // inputs; wave 0 adds the four partials in order, the residual, LN2 and the
 // mask.
 __global__ __launch_bounds__(256) void node16_kernel(EncLayerDev w, Enc16LayerDev w16, const float* __restrict__ upd,
-                                                     const float* __restrict__ mask, int L, float* __restrict__ h_v) {
+                                                     const float* __restrict__ mask, int L, float* __restrict__ h_v,
+                                                     const uint16_t* __restrict__ W1_next, float* __restrict__ prefix) {
   __shared__ __attribute__((aligned(16))) float A[16 * kLdH];
   __shared__ __attribute__((aligned(16))) float F[16 * kLdF];
   __shared__ __attribute__((aligned(16))) float Pt[4][16 * kLdH];
@@ -325,7 +339,7 @@ __global__ __launch_bounds__(256) void node16_kernel(EncLayerDev w, Enc16LayerDe
 #pragma unroll
     for (int i = 0; i < 4; ++i) Pt[wave][(4 * g + i) * kLdH + 16 * nt + r] = acc[nt][i];
   __syncthreads();
-  if (wave != 0) return;
+  if (wave == 0) {
 #pragma unroll
   for (int nt = 0; nt < 8; ++nt) {
     const int col = 16 * nt + r;
@@ -340,16 +354,35 @@ __global__ __launch_bounds__(256) void node16_kernel(EncLayerDev w, Enc16LayerDe
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const int res = r0 + 4 * g + i;
-    if (res >= L) continue;
-    const float mk = mask[res];
+    const float mk = res < L ? mask[res] : 0.0F;
 #pragma unroll
-    for (int nt = 0; nt < 8; ++nt) h_v[(size_t)res * kH + 16 * nt + r] = x[nt][i] * mk;
+    for (int nt = 0; nt < 8; ++nt) {
+      const float hv = x[nt][i] * mk;
+      A[(4 * g + i) * kLdH + 16 * nt + r] = hv;
+      if (res < L) h_v[(size_t)res * kH + 16 * nt + r] = hv;
+    }
+  }
+  }
+  __syncthreads();
+  // prefixes of the new h: wave 0 the h_i rows of this layer's W11, wave 1
+  // those of the next layer's W1 (packed k-blocks 0 .. 15 of the K = 384
+  // matrices; lo 384 x 128 halves after hi)
+  if (wave >= 2 || (wave == 1 && !W1_next)) return;
+  floatx4 pacc[8];
+  wave_gemm<8>(A, kLdH, wave == 0 ? w16.W11 : W1_next, kH, 0, kH, pacc, (size_t)3 * kH * kH);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int res = r0 + 4 * g + i;
+    if (res >= L) continue;
+#pragma unroll
+    for (int nt = 0; nt < 8; ++nt) prefix[(size_t)res * 256 + kH * wave + 16 * nt + r] = pacc[nt][i];
   }
 }
 
 __global__ __launch_bounds__(128) void edge_update16_kernel(EncLayerDev w, Enc16LayerDev w16, float* __restrict__ h_e,
                                                             const float* __restrict__ h_v,
-                                                            const int32_t* __restrict__ idx, int L, int K) {
+                                                            const int32_t* __restrict__ idx,
+                                                            const float* __restrict__ prefix, int L, int K) {
   __shared__ __attribute__((aligned(16))) float slab[2][16 * kLdA];
   __shared__ float tbl[17];
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, r = lane & 15, g = lane >> 4;
@@ -360,7 +393,14 @@ __global__ __launch_bounds__(128) void edge_update16_kernel(EncLayerDev w, Enc16
   build_rows(A, h_v, h_e, idx, L, K, [&](int row) -> long long { return base + row < S ? base + row : -1; });
   __syncthreads();
   floatx4 acc[8];
-  wave_gemm<8>(A, kLdA, w16.W11, kH, 0, 3 * kH, acc);
+  wave_gemm<8>(A, kLdA, w16.W11 + (size_t)16 * kH * 8, kH, 0, 2 * kH, acc, (size_t)3 * kH * kH);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const long long slot = base + 4 * g + i;
+    const size_t res = slot < S ? (size_t)(slot / K) : 0;
+#pragma unroll
+    for (int nt = 0; nt < 8; ++nt) acc[nt][i] += prefix[res * 256 + 16 * nt + r];
+  }
   __syncthreads();
   store_gelu<8>(acc, w.b11, 0, A, kLdH, tbl);
   __syncthreads();
@@ -404,12 +444,16 @@ hipError_t launch_encoder16(const ModelDev& m, const float* coords, const uint8_
   hipError_t e = launch_zero(h_v, (size_t)L * kH, stream);
   if (e != hipSuccess) return e;
   edge_embed16_kernel<<<tiles, 128, 0, stream>>>(m, coords, atom_src, resid, chain, idx, L, K, h_e);
-  float* upd = ws.prefix;  // [L][128] of the [L][256] prefix buffer
+  e = launch_zero(ws.prefix, (size_t)L * 256, stream);  // layer 0: h = 0, so its W1 prefix is 0
+  if (e != hipSuccess) return e;
+  float* upd = ws.msg;  // [L][128] neighbour sums (the [S][128] message buffer is otherwise unused here)
   for (int l = 0; l < kLayers; ++l) {
     const Enc16LayerDev& w16 = m.enc16.layer[l];
-    edge_msg16_kernel<<<(unsigned)L, 192, 0, stream>>>(m.enc[l], w16, h_e, h_v, idx, mask, L, K, upd);
-    node16_kernel<<<(unsigned)((L + 15) / 16), 256, 0, stream>>>(m.enc[l], w16, upd, mask, L, h_v);
-    edge_update16_kernel<<<tiles, 128, 0, stream>>>(m.enc[l], w16, h_e, h_v, idx, L, K);
+    const uint16_t* W1_next = l + 1 < kLayers ? m.enc16.layer[l + 1].W1 : nullptr;
+    edge_msg16_kernel<<<(unsigned)L, 192, 0, stream>>>(m.enc[l], w16, h_e, h_v, idx, mask, ws.prefix, L, K, upd);
+    node16_kernel<<<(unsigned)((L + 15) / 16), 256, 0, stream>>>(m.enc[l], w16, upd, mask, L, h_v, W1_next,
+                                                                ws.prefix);
+    edge_update16_kernel<<<tiles, 128, 0, stream>>>(m.enc[l], w16, h_e, h_v, idx, ws.prefix, L, K);
   }
   return hipGetLastError();
 }

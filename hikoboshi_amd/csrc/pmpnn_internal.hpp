@@ -122,7 +122,8 @@ hipError_t launch_encoder(const ModelDev& m, const int32_t* idx, const float* ma
                           float* h_v, float* h_e, const EncoderScratch& ws, hipStream_t stream);
 // Featurisation and encoder on the fp16 MFMA with split operands (fp32-level
 // accuracy; the 16-bit design modes); kNN (idx, mask) comes from launch_knn.
-// ws.prefix holds the neighbour sums ([L][128]).
+// ws.prefix receives the per-residue h_i products ([L][256]) and ws.msg the
+// neighbour sums ([L][128]).
 hipError_t launch_encoder16(const ModelDev& m, const float* coords, const uint8_t* atom_src,
                             const int32_t* resid, const int32_t* chain, const int32_t* idx, const float* mask,
                             int L, int K, float* h_v, float* h_e, const EncoderScratch& ws, hipStream_t stream);
