@@ -45,6 +45,9 @@ __global__ __launch_bounds__(256) void tf_edge_kernel(DecLayerDev w, const float
                                                       const float* __restrict__ NB, const float* __restrict__ Ql, int L,
                                                       int K, float* __restrict__ msg_sum) {
   __shared__ __attribute__((aligned(16))) float A[kRows * kLd];
+  // per edge row, formed once: its residue t, and its neighbour j with the
+  // backward flag (pos[j] < pos[t]) in bit 31, or -1 when the slot adds nothing
+  __shared__ int row_t[kRows], row_j[kRows];
   const int nres = kRows / K;
   const int r0 = blockIdx.x * nres;
   const int nr = min(nres, L - r0);
@@ -52,6 +55,13 @@ __global__ __launch_bounds__(256) void tf_edge_kernel(DecLayerDev w, const float
   const size_t slot0 = (size_t)r0 * K;
   const int wave = threadIdx.x >> 6;
   const int lane = threadIdx.x & 63;
+  if (threadIdx.x < n_rows) {
+    const int row = threadIdx.x;
+    const int t = r0 + row / K;
+    const int j = idx[slot0 + row];
+    row_t[row] = t;
+    row_j[row] = (j >= 0 && j < L && mask[t] != 0.0F) ? (j | (pos[j] < pos[t] ? (int)0x80000000u : 0)) : -1;
+  }
 
   for (int task = threadIdx.x; task < kRows * (kH / 4); task += blockDim.x) {
     const int row = task / (kH / 4), c4 = task % (kH / 4);
@@ -74,11 +84,13 @@ __global__ __launch_bounds__(256) void tf_edge_kernel(DecLayerDev w, const float
         const int col = wave * 32 + nb * 16 + (lane & 15);
         float v = 0.0F;
         if (row < n_rows) {
-          const int t = r0 + row / K;
-          const int j = idx[slot0 + row];
+          const int t = row_t[row];
+          const int jb = row_j[row];
           float x = NB[(size_t)t * 256 + col];
-          if (j >= 0 && j < L && mask[t] != 0.0F)
-            x += acc[mb][nb][i] + (pos[j] < pos[t] ? NB[(size_t)j * 256 + kH + col] : Ql[(size_t)j * kH + col]);
+          if (jb != -1) {
+            const int j = jb & 0x7FFFFFFF;
+            x += acc[mb][nb][i] + (jb < 0 ? NB[(size_t)j * 256 + kH + col] : Ql[(size_t)j * kH + col]);
+          }
           v = gelu(x);
         }
         A[row * kLd + col] = v;
