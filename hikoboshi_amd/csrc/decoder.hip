@@ -713,9 +713,11 @@ __global__ void neighbour_schedule_kernel(const int32_t* __restrict__ orders, co
 // Dependency schedule of each decoding order q. Step u (residue order[u])
 // reads the state of every kNN neighbour decoded before it, so it may run in
 // any pass after those steps' passes; each step then sees exactly the inputs
-// of sequential decoding, whatever pass it runs in. Pass p takes the
-// max_members smallest u among the steps whose earlier active neighbours are
-// all placed in passes < p (a ready list ordered by u). Inactive residues
+// of sequential decoding, whatever pass it runs in. Pass p takes up to
+// max_members of the steps whose earlier active neighbours are all placed in
+// passes < p: the smallest u, or, for a team of workgroups, a count balanced
+// for the team and the steps on the longest chains first (see
+// ready_schedule_kernel). Inactive residues
 // (mask 0) read nothing and form pass 0, which runs before all others; entries
 // outside 0..L-1 are dropped. If the order is not a permutation (a residue
 // repeated), every active step gets a pass of its own, in order: sequential
@@ -726,8 +728,8 @@ __global__ void neighbour_schedule_kernel(const int32_t* __restrict__ orders, co
 // among the active steps: the sampler stream is consumed in order of u).
 // Four kernels: pending-dependency and dependent counts over all (step, slot)
 // pairs; per order the permutation check, draw indices, pass 0 and the
-// dependents' offsets; the dependents lists; per order the pass loop, with
-// the pending counts as bytes in LDS.
+// dependents' offsets; the dependents lists; per order the step heights (for
+// balanced passes) and the pass loop, with the pending counts as bytes in LDS.
 constexpr int kSchedThreads = 512;
 constexpr int kSchedMaxL = 60000;  // pending counts as L bytes of LDS
 constexpr int kSchedPrioMaxL = 8192;  // balanced passes up to this length (heights as 2 L bytes of LDS)
