@@ -60,7 +60,33 @@ def parse_args():
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     p.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
                    help="only run a device-to-device copy of MIB MiB (HBM-counter calibration) and exit")
+    p.add_argument("--score-batch", type=int, default=0, metavar="N",
+                   help="instead of the design benchmark, time teacher-forced scoring of a ragged batch of N "
+                        "synthetic proteins (L ~ U[50, 500], native tokens) from host buffers")
     return p.parse_args()
+
+
+def score_batch_bench(args) -> int:
+    """Teacher-forced log-probs of a ragged batch (hkbs_pmpnn_score_batch): one step = one call on the
+    whole batch, from host buffers to host buffers (the call is synchronous, PCIe included)."""
+    from hikoboshi_amd import _lib, backbone, weights
+
+    coords, src, tokens, offsets = backbone.ragged_batch(args.score_batch, args.seed)
+    ctx = _lib.Context(weights.read_package_bytes())
+    for _ in range(args.warmup):
+        ctx.score_batch(coords, src, tokens, offsets)
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        ctx.score_batch(coords, src, tokens, offsets)
+    dt = (time.perf_counter() - t0) / args.steps
+    n_res = int(offsets[-1])
+    print(json.dumps({
+        "metric": "teacher-forced residues/sec, ragged batch", "value": round(n_res / dt, 1), "unit": "residues/s",
+        "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(dt * 1e3, 3),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "f32", "data": "synthetic",
+        "config": {"workload": f"score_ragged{args.score_batch}", "proteins": args.score_batch, "residues": n_res,
+                   "L_range": [50, 500], "seed": args.seed, "inputs": "host buffers (PCIe included)"}}), flush=True)
+    return 0
 
 
 def calibrate_copy(mib: int) -> int:
@@ -156,6 +182,8 @@ def main() -> int:
         print(json.dumps({"error": "this build runs on one GPU; --gpus must be 1 (the path shards by "
                                    "sequences across GPUs, which this benchmark does not launch)"}))
         return 2
+    if args.score_batch:
+        return score_batch_bench(args)
     from hikoboshi_amd import backbone, weights
 
     L, B, T = args.L, args.num_seqs, args.temperature
