@@ -1,22 +1,28 @@
 #!/usr/bin/env python3
 """Batched ProteinMPNN v_48_020 design on one MI355X.
 
-One step = one design of B=64 sequences on one synthetic L=300 backbone
-(featurise + encode + 300 autoregressive decode steps + device-to-host copy
-of tokens, log-probs and scores), inputs resident in HBM before the timed
-region. value = sampled residues/s = B * L / step time.
+Headline: one step = one design of B = 64 sequences on one synthetic L = 300
+backbone with the inputs resident in HBM: featurise + encode + 300
+autoregressive decode steps + the copy of tokens, log-probs and scores into
+pinned host memory. value = B * L / step time (sampled residues/s). Every
+timed step checks that all scores are finite: a decode team that failed to
+assemble leaves a NaN score, so a failed design is never counted.
 
-Printed JSON also carries
-  us_per_decode_step  decode-loop kernel time / L (HIP events on the kernels' stream),
-  roofline            dominant kernel (decode loop) against the fp32 peak, with
-                      achieved = B * L * F_res / decode time, F_res = 29,103,360
-                      FLOP per sampled residue (reference arithmetic); the loop
-                      performs F_exec = 5,795,072 of them (executed_frac),
-  decode_hbm          the same kernel against HBM bandwidth (compulsory bytes),
-  cpu_baseline        the reference's own scalar path (oracle/_ref) on a bounded
-                      sample of the same workload (one sequence per host core, up to
-                      16 forked worker processes), timed on this host before the GPU
-                      is touched.
+The JSON line also carries
+  us_per_decode_step  decode-kernel time / L (HIP events on the stream the kernels run on);
+  roofline            the decode kernel (the dominant kernel) against HBM bandwidth:
+                      achieved = algorithmic bytes per launch / kernel time, the compulsory
+                      bytes of one decode being 4 [B (3 H E_bw + L (2H + V + 1)) + L (2K + 1) H
+                      + W_dec] (E_bw = kNN edges to earlier positions); traffic = HBM bytes per
+                      launch from the committed rocprofv3 counters; and the FLOP the launch
+                      executes against the VALU fp32 and MFMA fp16 peaks;
+  encoder             featurise + encode against the fp32 peak;
+  cpu_baseline        the reference's own scalar code (oracle/_ref) on a bounded sample of the
+                      same workload, timed on this host's cores before the GPU is touched;
+  configs             the other workloads: L = 120 x 8 with per-sequence random orders, the
+                      4 x 256 complex x 256 sequences, the 4,096-protein teacher-forced ragged
+                      batch and L = 4,000 x 32 in bf16, each with its time, throughput, a spot
+                      check against the CPU reference and a CPU baseline of its own.
 """
 from __future__ import annotations
 
@@ -31,17 +37,23 @@ import numpy as np
 ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
+from hikoboshi_amd import backbone  # noqa: E402  (numpy only; no GPU)
+
 METRIC = "sampled residues/sec at L=300×64 seqs; µs per decode step"
 F_RES = 29_103_360        # FLOP per sampled residue, reference arithmetic at K=48
-# FLOP per sampled residue the restructured decode loop performs (fp32-equivalent products):
-# per layer W2 over the 48 message rows, the row sums A + E1 + R|Q and the column sums, W3 on
-# the summed rows, W_in and W_out; the fused next-layer [W1d | W1a] of layers 0 and 1; logits.
-F_EXEC = 3 * (2 * 48 * 128 * 128 + 2 * 48 * 128 + 48 * 128 + 2 * 128 * 128 + 2 * 2 * 128 * 512) \
-    + 2 * (2 * 128 * 256) + 2 * 128 * 21
+# FLOP per sampled residue the restructured decode loop executes, split by unit: per layer the
+# W2 product over the 48 message rows (on the fp16 MFMA as three products of split operands,
+# hi.hi + hi.lo + lo.hi), and on the VALU the row sums A + E1 + R|Q and column sums, W3 on the
+# summed rows, W_in and W_out, plus the fused next-layer [W1d | W1a] of layers 0 and 1 and logits.
+F_W2 = 3 * (2 * 48 * 128 * 128)
+F_VALU = 3 * (2 * 48 * 128 + 48 * 128 + 2 * 128 * 128 + 2 * 2 * 128 * 512) + 2 * (2 * 128 * 256) + 2 * 128 * 21
+F_EXEC = F_W2 + F_VALU
 W_DEC = 698_133           # decoder + W_out + W_s floats
-PEAK_FP32_TFLOPS = 157.3  # MI355X dense fp32
+PEAK_FP32_TFLOPS = 157.3  # MI355X dense fp32 (vector and matrix)
+PEAK_FP16_TFLOPS = 2500.0 # MI355X dense fp16 MFMA
 PEAK_HBM_GBPS = 8000.0    # MI355X HBM3E
 H, V = 128, 21
+C4_CPU_PROTEINS = 32      # proteins of the ragged batch the CPU baseline scores
 
 
 def parse_args():
@@ -54,22 +66,289 @@ def parse_args():
     p.add_argument("--temperature", type=float, default=0.1)
     p.add_argument("--seed", type=int, default=7)
     p.add_argument("--precision", choices=("fp32", "bf16"), default="fp32",
-                   help="design arithmetic (bf16: bf16 weights and activations into the products)")
-    p.add_argument("--cpu-sample", type=int, default=0,
-                   help="sequences timed on the CPU baseline (default: one per worker process)")
-    p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+                   help="design arithmetic of the headline workload (bf16: bf16 decoder)")
+    p.add_argument("--workers", type=int, default=0, help="CPU worker processes (default: min(16, host CPUs))")
+    p.add_argument("--no-cpu", action="store_true", help="skip the CPU baselines")
+    p.add_argument("--no-configs", action="store_true", help="headline workload only")
     p.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
                    help="only run a device-to-device copy of MIB MiB (HBM-counter calibration) and exit")
     p.add_argument("--score-batch", type=int, default=0, metavar="N",
-                   help="instead of the design benchmark, time teacher-forced scoring of a ragged batch of N "
-                        "synthetic proteins (L ~ U[50, 500], native tokens) from host buffers")
+                   help="only time teacher-forced scoring of a ragged batch of N synthetic proteins "
+                        "(L ~ U[50, 500], native tokens) from host buffers")
     return p.parse_args()
+
+
+# ------------------------------------------------------------------ inputs --
+
+def workloads(args):
+    """Synthetic inputs of every workload, built on the host before the CPU workers fork."""
+    import oracle
+    from hikoboshi_amd import weights
+
+    seed = args.seed
+    orc = oracle.Oracle(weights.load_tensors())
+
+    def shared_order(bb):
+        valid = (bb.atom_sources[:, :4] != 0).all(1).astype(np.float32)
+        return orc.decode_order(bb.L, seed, residue_mask=valid)
+
+    L, B = args.L, args.num_seqs
+    bb = backbone.single_chain(L, seed)
+    suffix = "" if args.precision == "fp32" else "_bf16"
+    W = {"C2": dict(name=f"design_L{L}_B{B}{suffix}", bb=bb, B=B, T=args.temperature, order=shared_order(bb),
+                    seeds=(seed + np.arange(B)).astype(np.uint64), precision=args.precision,
+                    cpu_seqs=list(range(min(B, 16))))}
+    if not args.no_configs:
+        c1 = backbone.single_chain(120, seed)
+        W["C1"] = dict(name="design_L120_B8", bb=c1, B=8, T=0.1, order=None,
+                       seeds=(seed + np.arange(8)).astype(np.uint64), precision="fp32", cpu_seqs=list(range(8)))
+        cx = backbone.tetrahedral_complex(256, seed)
+        W["C3"] = dict(name="complex_4x256_B256", bb=cx, B=256, T=0.2, order=shared_order(cx),
+                       seeds=(seed + np.arange(256)).astype(np.uint64), precision="fp32",
+                       cpu_seqs=[int(b) for b in np.linspace(0, 255, 16).round()])
+        c5 = backbone.single_chain(4000, seed)
+        W["C5"] = dict(name="long_L4000_B32_bf16", bb=c5, B=32, T=0.1, order=shared_order(c5),
+                       seeds=(seed + np.arange(32)).astype(np.uint64), precision="bf16", cpu_seqs=[0])
+        coords, src, tok, off = backbone.ragged_batch(4096, seed)
+        pick = np.sort(np.random.default_rng(seed).choice(4096, C4_CPU_PROTEINS, replace=False))
+        W["C4"] = dict(name="score_ragged4096", batch=(coords, src, tok, off), cpu_proteins=[int(i) for i in pick])
+    return W
+
+
+# --------------------------------------------------------------- CPU leg --
+
+_W = {}      # workloads, inherited by the forked workers
+_IMPL = None  # per worker: the reference build (or the C restatement when it is absent)
+
+
+def _init_worker():
+    global _IMPL
+    import oracle
+    from hikoboshi_amd import weights
+
+    tensors = weights.load_tensors()
+    _IMPL = (oracle.Reference(tensors), "reference") if oracle.Reference.available() else \
+        (oracle.Oracle(tensors), "port")
+
+
+def _cpu_task(task):
+    """One single-threaded reference call: a design module call for one sequence (it featurises and
+    encodes the backbone again, as the reference's per-sample loop does) or the teacher-forced
+    forward of one protein. Returns the outputs and the call's own seconds."""
+    cfg, i = task
+    impl, kind = _IMPL
+    w = _W[cfg]
+    if cfg == "C4":
+        coords, src, tok, off = w["batch"]
+        sl = slice(int(off[i]), int(off[i + 1]))
+        t0 = time.perf_counter()
+        lp, _ = impl.teacher_forced(backbone.Backbone(coords[sl], src[sl]), tok[sl])
+        return cfg, i, None, lp, time.perf_counter() - t0, kind
+    seed = int(w["seeds"][i])
+    t0 = time.perf_counter()
+    o = impl.inverse_fold(w["bb"], seed=seed, order_seed=seed, temperature=w["T"], input_order=w["order"],
+                          use_input_order=w["order"] is not None)
+    return cfg, i, o["tokens"], o["log_probs"], time.perf_counter() - t0, kind
+
+
+def _task_cost(task):
+    cfg, i = task
+    if cfg == "C4":
+        off = _W["C4"]["batch"][3]
+        return int(off[i + 1] - off[i])
+    return _W[cfg]["bb"].L
+
+
+def host_cpu():
+    model = ""
+    try:
+        with open("/proc/cpuinfo", encoding="utf-8") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    try:
+        usable = len(os.sched_getaffinity(0))
+    except AttributeError:
+        usable = os.cpu_count() or 1
+    return model, os.cpu_count() or 1, usable
+
+
+def cpu_leg(workers):
+    """Every CPU task of every workload in one pool of forked single-threaded workers, longest first.
+    Each task times its own reference call, so worker start-up and weight loading are excluded."""
+    import multiprocessing as mp
+
+    tasks = []
+    for cfg, w in _W.items():
+        ids = w["cpu_proteins"] if cfg == "C4" else w["cpu_seqs"]
+        tasks += [(cfg, i) for i in ids]
+    tasks.sort(key=_task_cost, reverse=True)
+    t0 = time.perf_counter()
+    with mp.get_context("fork").Pool(workers, initializer=_init_worker) as pool:
+        res = list(pool.imap_unordered(_cpu_task, tasks, chunksize=1))
+    wall = time.perf_counter() - t0
+    out = {}
+    for cfg, i, tok, lp, dt, kind in res:
+        out.setdefault(cfg, {"kind": kind, "outputs": {}, "seconds": 0.0})
+        out[cfg]["outputs"][i] = (tok, lp)
+        out[cfg]["seconds"] += dt
+    return out, wall
+
+
+def cpu_summary(cfg, got, workers, model, wall):
+    """Residues per second of the reference on `workers` cores: each task's own time under the
+    all-core load of the pool, cores x residues / (sum of task seconds)."""
+    w = _W[cfg]
+    if cfg == "C4":
+        off = w["batch"][3]
+        residues = int(sum(off[i + 1] - off[i] for i in got["outputs"]))
+        what = (f"teacher-forced forward of {len(got['outputs'])} randomly chosen proteins of the batch "
+                f"({residues} residues), one call per protein")
+    else:
+        residues = w["bb"].L * len(got["outputs"])
+        ids = sorted(got["outputs"])
+        what = (f"{len(ids)} of the {w['B']} sequences (indices {ids[0]}..{ids[-1]}), one design module call "
+                f"per sequence (featurise + encode + decode, re-encoding per sequence as the reference's "
+                f"per-sample loop does)")
+    single = residues / got["seconds"]
+    return {
+        "value": round(single * workers, 2), "unit": "residues/s", "cores": workers, "kind": got["kind"],
+        "sample": f"{what}, spread over {workers} forked single-threaded worker processes; value = cores x "
+                  f"residues / sum of per-call seconds (start-up and weight loading excluded); the pool ran "
+                  f"{wall:.1f} s for all workloads",
+        "single_core_value": round(single, 3), "cpu_model": model, "seconds": round(got["seconds"], 2),
+    }
+
+
+def spot_check(got, tokens, log_probs):
+    """Reference outputs against the GPU's for the sequences the CPU leg ran."""
+    same, worst = 0, 0.0
+    for b, (tok, lp) in got["outputs"].items():
+        if np.array_equal(tok, tokens[b]):
+            same += 1
+            worst = max(worst, float(np.abs(lp - log_probs[b]).max()))
+    return {"tokens_identical": same, "of": len(got["outputs"]), "max_abs_dlogp": worst if same else None}
+
+
+# --------------------------------------------------------------- GPU leg --
+
+class DeviceDesign:
+    """One workload's device-resident inputs and outputs; step() = one design call on device
+    buffers, the copy of its outputs to pinned host memory, a wait for the stream and a check
+    that every score is finite."""
+
+    def __init__(self, ctx, w, order):
+        from hikoboshi_amd import hip
+
+        bb, B, L = w["bb"], w["B"], w["bb"].L
+        self.ctx, self.L, self.B, self.T, self.hip = ctx, L, B, w["T"], hip
+        self.d = {k: hip.DeviceBuffer.from_array(v) for k, v in
+                  (("coords", bb.coords), ("src", bb.atom_sources), ("order", order), ("seeds", w["seeds"]))}
+        for k, v in (("resid", bb.residue_indices), ("chain", bb.chain_labels)):
+            self.d[k] = hip.DeviceBuffer.from_array(v) if v is not None else None
+        self.d["tokens"] = hip.DeviceBuffer(B * L * 4)
+        self.d["lp"] = hip.DeviceBuffer(B * L * V * 4)
+        self.d["scores"] = hip.DeviceBuffer(B * 4)
+        self.h_tokens = hip.PinnedBuffer((B, L), np.int32)
+        self.h_lp = hip.PinnedBuffer((B, L, V), np.float32)
+        self.h_scores = hip.PinnedBuffer((B,), np.float32)
+        self.stream = hip.Stream()
+
+    def step(self):
+        d, hip = self.d, self.hip
+        self.ctx.design_device(d["coords"].addr, d["src"].addr, self.L, self.B, d["order"].addr, 1,
+                               d["seeds"].addr, self.T, d["tokens"].addr, d["lp"].addr, d["scores"].addr,
+                               stream_ptr=self.stream.h.value,
+                               residue_indices_ptr=d["resid"].addr if d["resid"] else None,
+                               chain_labels_ptr=d["chain"].addr if d["chain"] else None)
+        hip.memcpy_d2h_async(self.h_tokens, d["tokens"], self.B * self.L * 4, self.stream)
+        hip.memcpy_d2h_async(self.h_lp, d["lp"], self.B * self.L * V * 4, self.stream)
+        hip.memcpy_d2h_async(self.h_scores, d["scores"], self.B * 4, self.stream)
+        self.stream.sync()
+        if not np.isfinite(self.h_scores.array).all():
+            raise RuntimeError("a design returned a non-finite score (a decode team failed to assemble)")
+
+    def run(self, steps, warmup):
+        """ms per step over `steps` timed steps and the mean phase times (featurise + encode,
+        decoder precompute, decode kernel) of those steps."""
+        self.ctx.set_timing(True)
+        for _ in range(warmup):
+            self.step()
+        self.hip.device_synchronize()
+        phases = []
+        t0 = time.perf_counter()
+        for _ in range(steps):
+            self.step()
+            phases.append(self.ctx.last_timing())
+        self.hip.device_synchronize()
+        ms = (time.perf_counter() - t0) * 1e3 / steps
+        self.ctx.set_timing(False)
+        return ms, np.mean(np.array(phases), axis=0)
+
+
+def measured_traffic(workload: str):
+    """HBM bytes per decode_kernel launch from the committed rocprofv3 summary, if it covers this workload."""
+    path = os.path.join(ROOT, "profiles", f"decode_kernel_{workload}.md")
+    key = f"decode_kernel HBM bytes per launch ({workload}):"
+    try:
+        with open(path, encoding="utf-8") as f:
+            for line in f:
+                if line.startswith(key):
+                    return int(line.split(":")[1].strip()), os.path.relpath(path, ROOT)
+    except OSError:
+        pass
+    return None, None
+
+
+def decode_roofline(ctx, w, order, decode_ms):
+    """The decode kernel against HBM bandwidth (algorithmic bytes) and its executed FLOP against the
+    VALU fp32 and MFMA fp16 peaks."""
+    bb, B, L = w["bb"], w["B"], w["bb"].L
+    K = min(48, L)
+    idx, _ = ctx.knn(bb.coords, bb.atom_sources)
+    pos = np.empty(L, np.int64)
+    pos[order] = np.arange(L)
+    e_bw = int((pos[idx] < pos[:, None]).sum())
+    launch_bytes = 4.0 * (B * (3 * H * e_bw + L * (2 * H + V + 1)) + L * (2 * K + 1) * H + W_DEC)
+    t = decode_ms * 1e-3
+    achieved = launch_bytes / t / 1e9
+    traffic, traffic_src = measured_traffic(w["name"])
+    valu = B * L * F_VALU / t / 1e12
+    mfma = B * L * 3 * F_W2 / t / 1e12
+    return {
+        "kernel": "decode_kernel",
+        "bound": "hbm",
+        "achieved": round(achieved, 2),
+        "peak": PEAK_HBM_GBPS,
+        "unit": "GB/s",
+        "frac": round(achieved / PEAK_HBM_GBPS, 5),
+        "traffic": traffic,
+        "kernel_ms": round(decode_ms, 4),
+        "algorithmic_bytes": int(launch_bytes),
+        "algorithmic_units": (f"4 [B (3 H E_bw + L (2H + V + 1)) + L (2K + 1) H + W_dec] bytes per launch, "
+                              f"B={B} L={L} K={K} E_bw={e_bw} W_dec={W_DEC}"),
+        "traffic_source": (f"{traffic_src}: rocprofv3 FETCH_SIZE x2.0 + WRITE_SIZE x1.0 (copy-kernel "
+                           "calibrated), bytes per launch") if traffic else None,
+        "executed": {
+            "valu_fp32": {"flop_per_residue": F_VALU, "achieved_tflops": round(valu, 3), "peak": PEAK_FP32_TFLOPS,
+                          "frac": round(valu / PEAK_FP32_TFLOPS, 4)},
+            "mfma_fp16": {"flop_per_residue": 3 * F_W2, "achieved_tflops": round(mfma, 3), "peak": PEAK_FP16_TFLOPS,
+                          "frac": round(mfma / PEAK_FP16_TFLOPS, 4),
+                          "note": "W2 as three fp16 products of split operands (hi.hi + hi.lo + lo.hi)"},
+            "reference_flop_per_residue": F_RES,
+        },
+        "limiter": ("latency: neither HBM nor the arithmetic units are near their peaks; the SQ counters in "
+                    "profiles/ show waves waiting most of their cycles on L2 weight streaming and barriers"),
+    }
 
 
 def score_batch_bench(args) -> int:
     """Teacher-forced log-probs of a ragged batch (hkbs_pmpnn_score_batch): one step = one call on the
     whole batch, from host buffers to host buffers (the call is synchronous, PCIe included)."""
-    from hikoboshi_amd import _lib, backbone, weights
+    from hikoboshi_amd import _lib, weights
 
     coords, src, tokens, offsets = backbone.ragged_batch(args.score_batch, args.seed)
     ctx = _lib.Context(weights.read_package_bytes())
@@ -77,8 +356,10 @@ def score_batch_bench(args) -> int:
         ctx.score_batch(coords, src, tokens, offsets)
     t0 = time.perf_counter()
     for _ in range(args.steps):
-        ctx.score_batch(coords, src, tokens, offsets)
+        _, sc = ctx.score_batch(coords, src, tokens, offsets)
     dt = (time.perf_counter() - t0) / args.steps
+    if not np.isfinite(sc).all():
+        raise RuntimeError("non-finite teacher-forced score")
     n_res = int(offsets[-1])
     print(json.dumps({
         "metric": "teacher-forced residues/sec, ragged batch", "value": round(n_res / dt, 1), "unit": "residues/s",
@@ -102,76 +383,105 @@ def calibrate_copy(mib: int) -> int:
     return 0
 
 
-def measured_traffic(workload: str):
-    """HBM bytes per decode_kernel launch from the committed rocprofv3 summary, if it covers this workload."""
-    path = os.path.join(ROOT, "profiles", f"decode_kernel_{workload}.md")
-    key = f"decode_kernel HBM bytes per launch ({workload}):"
-    try:
-        with open(path, encoding="utf-8") as f:
-            for line in f:
-                if line.startswith(key):
-                    return int(line.split(":")[1].strip()), os.path.relpath(path, ROOT)
-    except OSError:
-        pass
-    return None, None
+def run_configs(ctx, cpu, workers, model, wall, steps, warmup):
+    """C1, C3, C4 and C5 on the GPU, each with its CPU baseline and spot check."""
+    from hikoboshi_amd import _lib
 
+    out = {}
+    # C1: host buffers through hkbs_pmpnn_design, a random order per sequence (seed 7 + i for order and
+    # sampler, the reference's per-sample loop), host order generation and PCIe included.
+    w = _W["C1"]
+    bb = w["bb"]
 
-def _cpu_design(job):
-    """One CPU worker: the reference's scalar module call for each sequence index in the job."""
-    idxs, L, seed, temperature, order = job
-    from hikoboshi_amd import backbone, weights
-    import oracle
+    def c1():
+        r = ctx.design(bb.coords, bb.atom_sources, w["B"], w["seeds"], order_seeds=w["seeds"], temperature=w["T"])
+        if not np.isfinite(r["scores"]).all():
+            raise RuntimeError("non-finite score")
+        return r
 
-    tensors = weights.load_tensors()
-    if oracle.Reference.available():
-        impl, kind = oracle.Reference(tensors), "reference"
-    else:
-        impl, kind = oracle.Oracle(tensors), "port"
-    bb = backbone.single_chain(L, seed)
-    out = []
-    for b in idxs:
-        t0 = time.perf_counter()
-        o = impl.inverse_fold(bb, seed=seed + b, order_seed=seed + b, temperature=temperature, input_order=order,
-                              use_input_order=True)
-        out.append((b, o["tokens"], o["log_probs"], time.perf_counter() - t0))
-    return kind, out
-
-
-def cpu_baseline(L, seed, temperature, order, n, workers):
-    """Reference scalar path on `n` of the sequences, one single-threaded module call per
-    sequence (it re-encodes each time, as the reference's per-sample loop does), spread over
-    `workers` forked processes. Runs before this process touches the GPU."""
-    import multiprocessing as mp
-
-    jobs = [(list(range(w, n, workers)), L, seed, temperature, order) for w in range(workers)]
-    jobs = [j for j in jobs if j[0]]
+    for _ in range(warmup):
+        c1()
     t0 = time.perf_counter()
-    with mp.get_context("fork").Pool(len(jobs)) as pool:
-        res = pool.map(_cpu_design, jobs)
-    wall = time.perf_counter() - t0
-    kind = res[0][0]
-    seqs = sorted((r for _, rs in res for r in rs), key=lambda r: r[0])
-    per_seq = float(np.mean([r[3] for r in seqs]))
-    return {
-        "value": n * L / wall,
-        "unit": "residues/s",
-        "cores": len(jobs),
-        "kind": kind,
-        "sample": f"{n} of the sequences (L={L}, shared order, sampler seeds {seed}..{seed + n - 1}) on "
-                  f"{len(jobs)} forked worker processes, one single-threaded module call per sequence "
-                  f"(featurise + encode + decode, re-encoding per sequence as the reference does); "
-                  f"{wall:.1f} s wall including worker start-up",
-        "single_core_value": L / per_seq,
-        "_outputs": {r[0]: (r[1], r[2]) for r in seqs},
-    }
+    for _ in range(steps):
+        r = c1()
+    ms = (time.perf_counter() - t0) * 1e3 / steps
+    out["C1"] = {"workload": w["name"], "L": bb.L, "num_seqs": w["B"], "temperature": w["T"],
+                 "decode_order": "random per sequence (seed 7+i, order and sampler)",
+                 "inputs": "host buffers (hkbs_pmpnn_design; host order generation and PCIe included)",
+                 "ms": round(ms, 4), "value": round(w["B"] * bb.L / (ms * 1e-3), 1), "unit": "residues/s"}
+    if "C1" in cpu:
+        out["C1"]["parity_spot_check"] = spot_check(cpu["C1"], r["tokens"], r["log_probs"])
+        out["C1"]["cpu_baseline"] = cpu_summary("C1", cpu["C1"], workers, model, wall)
 
+    # C3 and C5: device-resident inputs, outputs copied to pinned host memory (as the headline).
+    for cfg in ("C3", "C5"):
+        w = _W[cfg]
+        order = _lib.decode_order(w["bb"].atom_sources, int(w["seeds"][0]))
+        if not np.array_equal(order, w["order"]):
+            raise RuntimeError(f"{cfg}: decode order differs between the library and the oracle")
+        run = DeviceDesign(ctx, w, order)
+        res = {"workload": w["name"], "L": w["bb"].L, "num_seqs": w["B"], "temperature": w["T"],
+               "decode_order": "shared random permutation (reference routine, seed 7)",
+               "inputs": "device buffers, outputs copied to pinned host memory"}
+        if cfg == "C5":
+            ms32, ph32 = run.run(steps, warmup)
+            fp32_tokens, fp32_lp = run.h_tokens.array.copy(), run.h_lp.array.copy()
+            res["fp32"] = {"ms": round(ms32, 4), "value": round(w["B"] * w["bb"].L / (ms32 * 1e-3), 1),
+                           "decode_ms": round(float(ph32[2]), 4)}
+            ctx.set_precision(_lib.PRECISION_BF16)
+        try:
+            ms, ph = run.run(steps, warmup)
+        finally:
+            ctx.set_precision(_lib.PRECISION_FP32)
+        res.update({"dtype": "bf16" if cfg == "C5" else "f32", "ms": round(ms, 4),
+                    "value": round(w["B"] * w["bb"].L / (ms * 1e-3), 1), "unit": "residues/s",
+                    "phase_ms": {"featurise_encode": round(float(ph[0]), 4),
+                                 "decoder_precompute": round(float(ph[1]), 4), "decode_loop": round(float(ph[2]), 4)},
+                    "us_per_decode_step": round(float(ph[2]) * 1e3 / w["bb"].L, 3)})
+        if cfg == "C5":
+            # bf16 against the fp32 path on the bf16 run's own trajectory at the config's T (contract 2e-2)
+            worst = 0.0
+            bb = w["bb"]
+            for b in range(2):
+                tok = run.h_tokens.array[b].copy()
+                lp1, _ = ctx.score(bb.coords, bb.atom_sources, tok, order=order)
+                z = lp1.astype(np.float64) / w["T"]
+                z -= z.max(1, keepdims=True)
+                ref = z - np.log(np.exp(z).sum(1, keepdims=True))
+                worst = max(worst, float(np.abs(run.h_lp.array[b] - ref).max()))
+            res["bf16_vs_fp32"] = {"max_abs_dlogp": round(worst, 5), "sequences": 2, "contract": 2e-2,
+                                   "note": "fp32 teacher-forced log-probs of the bf16 run's tokens and order, at T"}
+            tokens, lps = fp32_tokens, fp32_lp
+        else:
+            tokens, lps = run.h_tokens.array, run.h_lp.array
+        if cfg in cpu:
+            res["parity_spot_check"] = spot_check(cpu[cfg], tokens, lps)
+            if cfg == "C5":
+                res["parity_spot_check"]["against"] = "the fp32 run"
+            res["cpu_baseline"] = cpu_summary(cfg, cpu[cfg], workers, model, wall)
+        out[cfg] = res
 
-def spot_check(cpu, gpu_tokens, gpu_lp):
-    out = cpu.pop("_outputs")
-    same = {b: bool((t == gpu_tokens[b]).all()) for b, (t, _) in out.items()}
-    dlp = [float(np.abs(lp - gpu_lp[b]).max()) for b, (_, lp) in out.items() if same[b]]
-    cpu["parity_spot_check"] = {"tokens_identical": int(sum(same.values())), "of": len(same),
-                                "max_abs_dlogp": max(dlp) if dlp else None}
+    # C4: teacher-forced scoring of the ragged batch from host buffers (synchronous, PCIe included).
+    w = _W["C4"]
+    coords, src, tok, off = w["batch"]
+    for _ in range(max(1, warmup // 2)):
+        ctx.score_batch(coords, src, tok, off)
+    n4 = max(1, min(3, steps))
+    t0 = time.perf_counter()
+    for _ in range(n4):
+        lp, sc = ctx.score_batch(coords, src, tok, off)
+    ms = (time.perf_counter() - t0) * 1e3 / n4
+    if not np.isfinite(sc).all():
+        raise RuntimeError("non-finite teacher-forced score")
+    res = {"workload": w["name"], "proteins": 4096, "residues": int(off[-1]), "L_range": [50, 500],
+           "decode_order": "n_to_c", "inputs": "host buffers (hkbs_pmpnn_score_batch; PCIe included)",
+           "ms": round(ms, 3), "value": round(int(off[-1]) / (ms * 1e-3), 1), "unit": "residues/s"}
+    if "C4" in cpu:
+        worst = max(float(np.abs(lp[off[i]:off[i + 1]] - olp).max()) for i, (_, olp) in cpu["C4"]["outputs"].items())
+        res["parity_spot_check"] = {"proteins": len(cpu["C4"]["outputs"]), "max_abs_dlogp": worst}
+        res["cpu_baseline"] = cpu_summary("C4", cpu["C4"], workers, model, wall)
+    out["C4"] = res
+    return out
 
 
 def main() -> int:
@@ -184,84 +494,30 @@ def main() -> int:
         return 2
     if args.score_batch:
         return score_batch_bench(args)
-    from hikoboshi_amd import backbone, weights
 
-    L, B, T = args.L, args.num_seqs, args.temperature
-    K = min(48, L)
-    bb = backbone.single_chain(L, args.seed)
-    seeds = (args.seed + np.arange(B)).astype(np.uint64)
-    cpu = None
+    _W.update(workloads(args))
+    model, ncpu, usable = host_cpu()
+    workers = args.workers or max(1, min(16, usable))
+    cpu, wall = {}, 0.0
     if not args.no_cpu:
         # The CPU leg runs first, in forked workers, while this process has not touched the GPU.
-        import oracle
+        cpu, wall = cpu_leg(workers)
 
-        valid = (bb.atom_sources[:, :4] != 0).all(1).astype(np.float32)
-        host_order = oracle.Oracle(weights.load_tensors()).decode_order(L, args.seed, residue_mask=valid)
-        workers = max(1, min(16, os.cpu_count() or 1))
-        cpu = cpu_baseline(L, args.seed, T, host_order, max(1, min(args.cpu_sample or workers, B)), workers)
+    from hikoboshi_amd import _lib, weights
 
-    from hikoboshi_amd import _lib, hip
-
+    w = _W["C2"]
+    bb, L, B, T = w["bb"], w["bb"].L, w["B"], w["T"]
+    K = min(48, L)
     order = _lib.decode_order(bb.atom_sources, args.seed)
-    if cpu is not None and not np.array_equal(order, host_order):
+    if not np.array_equal(order, w["order"]):
         raise RuntimeError("decode order differs between the library and the oracle")
     ctx = _lib.Context(weights.read_package_bytes(), device=0)
     if args.precision == "bf16":
         ctx.set_precision(_lib.PRECISION_BF16)
-
-    d_coords = hip.DeviceBuffer.from_array(bb.coords)
-    d_src = hip.DeviceBuffer.from_array(bb.atom_sources)
-    d_order = hip.DeviceBuffer.from_array(order)
-    d_seeds = hip.DeviceBuffer.from_array(seeds)
-    d_tokens = hip.DeviceBuffer(B * L * 4)
-    d_lp = hip.DeviceBuffer(B * L * V * 4)
-    d_scores = hip.DeviceBuffer(B * 4)
-    h_tokens = hip.PinnedBuffer((B, L), np.int32)
-    h_lp = hip.PinnedBuffer((B, L, V), np.float32)
-    h_scores = hip.PinnedBuffer((B,), np.float32)
-    stream = hip.Stream()
-
-    def step(to_host: bool):
-        # One design of B sequences with inputs resident in HBM; the designs (tokens, log-probs,
-        # scores) are complete in HBM when the stream drains. to_host adds their copy to pinned
-        # host memory (the PCIe-inclusive rate, reported beside the value).
-        ctx.design_device(d_coords.addr, d_src.addr, L, B, d_order.addr, 1, d_seeds.addr, T, d_tokens.addr,
-                          d_lp.addr, d_scores.addr, stream_ptr=stream.h.value)
-        if to_host:
-            hip.memcpy_d2h_async(h_tokens, d_tokens, B * L * 4, stream)
-            hip.memcpy_d2h_async(h_lp, d_lp, B * L * V * 4, stream)
-            hip.memcpy_d2h_async(h_scores, d_scores, B * 4, stream)
-        stream.sync()
-
-    def timed(n: int, to_host: bool):
-        hip.device_synchronize()
-        t0 = time.perf_counter()
-        for _ in range(n):
-            step(to_host)
-            phases.append(ctx.last_timing())
-        hip.device_synchronize()
-        return (time.perf_counter() - t0) * 1e3 / n
-
-    ctx.set_timing(True)
-    for _ in range(args.warmup):
-        step(True)
-    phases = []
-    ms_per_step = timed(args.steps, False)
-    ms_with_d2h = timed(min(args.steps, 5), True)  # also leaves this design's outputs on the host
-    ph = np.mean(np.array(phases), axis=0)
+    run = DeviceDesign(ctx, w, order)
+    ms_per_step, ph = run.run(args.steps, args.warmup)
     decode_ms = float(ph[2])
-    us_step = decode_ms * 1e3 / L
-
-    # compulsory decode-step bytes (fp32): per sequence 3 H per backward edge, per-step writes,
-    # shared h_E rows + encoder h_V of neighbours + self, decoder weights once.
-    idx, _ = ctx.knn(bb.coords, bb.atom_sources)
-    pos = np.empty(L, np.int64)
-    pos[order] = np.arange(L)
-    e_bw = int((pos[idx] < pos[:, None]).sum())
-    bytes_step = 4.0 * (B * (3 * H * e_bw + L * (2 * H + V + 1)) + L * (2 * K + 1) * H + W_DEC) / L
-    achieved = B * L * F_RES / (decode_ms * 1e-3) / 1e12
     f_enc = L * K * 128 * 8768 + 786432 * L  # featurise + encode FLOP per backbone
-    traffic, traffic_src = measured_traffic(f"design_L{L}_B{B}" + ("" if args.precision == "fp32" else "_bf16"))
     result = {
         "metric": METRIC,
         "value": round(B * L / (ms_per_step * 1e-3), 1),
@@ -276,44 +532,18 @@ def main() -> int:
         "dtype": "f32" if args.precision == "fp32" else "bf16",
         "data": "synthetic",
         "config": {
-            "workload": f"design_L{L}_B{B}" + ("" if args.precision == "fp32" else "_bf16"),
+            "workload": w["name"],
             "L": L, "num_seqs": B, "k_neighbors": K, "temperature": T,
             "backbone": f"NeRF ideal-geometry single chain, helix/strand segments, seed {args.seed}",
             "decode_order": f"shared random permutation (reference routine, seed {args.seed})",
             "sampler_seeds": f"{args.seed}+b (splitmix64 counter streams)",
             "weights": "ProteinMPNN v_48_020 (bundled package)",
+            "step": "device-resident inputs -> designs copied to pinned host memory (D2H included)",
         },
-        "pcie_inclusive": {"ms_per_step": round(ms_with_d2h, 4),
-                           "value": round(B * L / (ms_with_d2h * 1e-3), 1),
-                           "note": "same step plus the copy of tokens, log-probs and scores to pinned host memory"},
-        "us_per_decode_step": round(us_step, 3),
+        "us_per_decode_step": round(decode_ms * 1e3 / L, 3),
         "phase_ms": {"featurise_encode": round(float(ph[0]), 4), "decoder_precompute": round(float(ph[1]), 4),
                      "decode_loop": round(decode_ms, 4)},
-        "roofline": {
-            "kernel": "decode_kernel",
-            "bound": "mfma",
-            "achieved": round(achieved, 3),
-            "peak": PEAK_FP32_TFLOPS,
-            "unit": "TFLOP/s",
-            "frac": round(achieved / PEAK_FP32_TFLOPS, 4),
-            "traffic": traffic,
-            "traffic_source": (f"{traffic_src}: rocprofv3 FETCH_SIZE x2.0 + WRITE_SIZE x1.0 (copy-kernel "
-                               "calibrated), bytes per launch") if traffic else None,
-            "algorithmic_units": f"B*L*F_res = {B}*{L}*{F_RES} FLOP per launch",
-            "executed_flop_per_residue": F_EXEC,
-            "executed_frac": round(B * L * F_EXEC / (decode_ms * 1e-3) / 1e12 / PEAK_FP32_TFLOPS, 4),
-            "note": ("frac counts the reference's arithmetic; the restructured loop performs "
-                     f"{F_RES / F_EXEC:.2f}x fewer FLOP (edge products precomputed once per design, W3 applied "
-                     "to the neighbour sum), so frac can exceed 1; executed_frac is the hardware fraction"),
-        },
-        "decode_hbm": {
-            "bytes_per_step": round(bytes_step, 1),
-            "achieved": round(bytes_step / (us_step * 1e-6) / 1e9, 2),
-            "peak": PEAK_HBM_GBPS,
-            "unit": "GB/s",
-            "frac": round(bytes_step / (us_step * 1e-6) / 1e9 / PEAK_HBM_GBPS, 5),
-            "backward_edges": e_bw,
-        },
+        "roofline": decode_roofline(ctx, w, order, decode_ms),
         "encoder": {
             "flop": f_enc,
             "ms": round(float(ph[0]), 4),
@@ -326,9 +556,13 @@ def main() -> int:
                      "VALU, ceiling peak/4) and in the 16-bit modes runs on the fp16 MFMA"),
         },
     }
-    if cpu is not None:
-        spot_check(cpu, h_tokens.array, h_lp.array)
-        result["cpu_baseline"] = cpu
+    if "C2" in cpu:
+        cb = cpu_summary("C2", cpu["C2"], workers, model, wall)
+        cb["host_cpus"] = {"nproc": ncpu, "usable": usable}
+        cb["parity_spot_check"] = spot_check(cpu["C2"], run.h_tokens.array, run.h_lp.array)
+        result["cpu_baseline"] = cb
+    if not args.no_configs:
+        result["configs"] = run_configs(ctx, cpu, workers, model, wall, min(args.steps, 5), min(args.warmup, 2))
     ctx.close()
     print(json.dumps(result), flush=True)
     return 0

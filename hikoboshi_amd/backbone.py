@@ -51,17 +51,33 @@ class Backbone:
         return int(self.coords.shape[0])
 
 
+def _norm3(v):
+    """Euclidean norm over the last axis of [..., 3], summed x, y, z in order."""
+    return np.sqrt((v[..., 0] * v[..., 0] + v[..., 1] * v[..., 1]) + v[..., 2] * v[..., 2])
+
+
+def _cross3(a, b):
+    return np.stack([a[..., 1] * b[..., 2] - a[..., 2] * b[..., 1],
+                     a[..., 2] * b[..., 0] - a[..., 0] * b[..., 2],
+                     a[..., 0] * b[..., 1] - a[..., 1] * b[..., 0]], axis=-1)
+
+
 def _place(a, b, c, length, angle_deg, torsion_deg):
-    """NeRF: position D with |CD| = length, angle BCD, torsion ABCD."""
+    """NeRF: position D with |CD| = length, angle BCD, torsion ABCD, for [n, 3] batches of points
+    (torsion_deg a scalar or [n])."""
     ang = np.deg2rad(angle_deg)
     tor = np.deg2rad(torsion_deg)
     bc = c - b
-    bc /= np.linalg.norm(bc)
-    n = np.cross(b - a, bc)
-    n /= np.linalg.norm(n)
-    m = np.stack([bc, np.cross(n, bc), n], axis=1)
-    d2 = np.array([-length * np.cos(ang), length * np.sin(ang) * np.cos(tor), length * np.sin(ang) * np.sin(tor)])
-    return c + m @ d2
+    bc = bc / _norm3(bc)[:, None]
+    n = _cross3(b - a, bc)
+    n = n / _norm3(n)[:, None]
+    m = _cross3(n, bc)
+    d0 = -length * np.cos(ang)
+    d1 = length * np.sin(ang) * np.cos(tor)
+    d2 = length * np.sin(ang) * np.sin(tor)
+    d1 = np.broadcast_to(d1, (a.shape[0],))[:, None]
+    d2 = np.broadcast_to(d2, (a.shape[0],))[:, None]
+    return c + ((bc * d0 + m * d1) + n * d2)
 
 
 def virtual_cb(n: np.ndarray, ca: np.ndarray, c: np.ndarray) -> np.ndarray:
@@ -80,6 +96,7 @@ def virtual_cb(n: np.ndarray, ca: np.ndarray, c: np.ndarray) -> np.ndarray:
 
 
 def _phi_psi(L: int, rng: np.random.Generator) -> tuple[np.ndarray, np.ndarray]:
+    """Per segment: its length, then (phi, psi) jitter pairs residue by residue."""
     phi = np.empty(L)
     psi = np.empty(L)
     pos, helix = 0, True
@@ -87,31 +104,37 @@ def _phi_psi(L: int, rng: np.random.Generator) -> tuple[np.ndarray, np.ndarray]:
         seg = int(rng.integers(8, 16))
         base = HELIX if helix else STRAND
         end = min(L, pos + seg)
-        for i in range(pos, end):
-            phi[i] = base[0] + rng.normal(0.0, 10.0)
-            psi[i] = base[1] + rng.normal(0.0, 10.0)
+        z = rng.normal(0.0, 10.0, size=2 * (end - pos)).reshape(-1, 2)
+        phi[pos:end] = base[0] + z[:, 0]
+        psi[pos:end] = base[1] + z[:, 1]
         pos, helix = end, not helix
     return phi, psi
+
+
+def _nerf(phi: np.ndarray, psi: np.ndarray) -> np.ndarray:
+    """float64 [n, Lmax, 4, 3] N, CA, C, O of n chains built together residue by residue from
+    [n, Lmax] torsions (a shorter chain ignores what lies beyond its own length)."""
+    n, L = phi.shape
+    xyz = np.zeros((n, L, 4, 3))
+    t = np.deg2rad(180.0 - ANG_N_CA_C)
+    xyz[:, 0, 1] = (N_CA, 0.0, 0.0)
+    xyz[:, 0, 2] = xyz[:, 0, 1] + CA_C * np.array([np.cos(t), np.sin(t), 0.0])
+    for i in range(L):
+        N, CA, C = xyz[:, i, 0], xyz[:, i, 1], xyz[:, i, 2]
+        n_next = _place(N, CA, C, C_N, ANG_CA_C_N, psi[:, i])
+        xyz[:, i, 3] = _place(n_next, CA, C, C_O, ANG_CA_C_O, 180.0)
+        if i + 1 < L:
+            ca_next = _place(CA, C, n_next, N_CA, ANG_C_N_CA, 180.0)
+            xyz[:, i + 1, 0] = n_next
+            xyz[:, i + 1, 1] = ca_next
+            xyz[:, i + 1, 2] = _place(C, n_next, ca_next, CA_C, ANG_N_CA_C, phi[:, i + 1])
+    return xyz
 
 
 def _chain_backbone(L: int, rng: np.random.Generator) -> np.ndarray:
     """float64 [L, 4, 3] N, CA, C, O."""
     phi, psi = _phi_psi(L, rng)
-    xyz = np.zeros((L, 4, 3))
-    N = np.zeros(3)
-    CA = np.array([N_CA, 0.0, 0.0])
-    t = np.deg2rad(180.0 - ANG_N_CA_C)
-    C = CA + CA_C * np.array([np.cos(t), np.sin(t), 0.0])
-    xyz[0, :3] = N, CA, C
-    for i in range(L):
-        N, CA, C = xyz[i, 0], xyz[i, 1], xyz[i, 2]
-        n_next = _place(N, CA, C, C_N, ANG_CA_C_N, psi[i])
-        xyz[i, 3] = _place(n_next, CA, C, C_O, ANG_CA_C_O, 180.0)
-        if i + 1 < L:
-            ca_next = _place(CA, C, n_next, N_CA, ANG_C_N_CA, 180.0)
-            c_next = _place(C, n_next, ca_next, CA_C, ANG_N_CA_C, phi[i + 1])
-            xyz[i + 1, :3] = n_next, ca_next, c_next
-    return xyz
+    return _nerf(phi[None], psi[None])[0]
 
 
 def _assemble(bb4: np.ndarray) -> tuple[np.ndarray, np.ndarray]:
@@ -165,21 +188,29 @@ def ragged_batch(n: int, seed: int, lmin: int = 50, lmax: int = 500):
     """n backbones with L ~ U[lmin, lmax] and i.i.d. native tokens, packed ragged.
 
     Returns (coords [sum L,5,3], atom_sources [sum L,5], tokens [sum L], offsets int64 [n+1]).
+    The random draws run protein by protein (lengths first, then per protein its torsions and
+    tokens); the geometry of all proteins is built together.
     """
     rng = np.random.default_rng(seed)
     lens = rng.integers(lmin, lmax + 1, size=n)
     offsets = np.zeros(n + 1, dtype=np.int64)
     offsets[1:] = np.cumsum(lens)
-    coords = np.empty((offsets[-1], 5, 3), dtype=np.float32)
-    src = np.empty((offsets[-1], 5), dtype=np.uint8)
+    Lmax = int(lens.max()) if n else 0
+    phi = np.zeros((n, Lmax))
+    psi = np.zeros((n, Lmax))
     tokens = np.empty(offsets[-1], dtype=np.int32)
     for i, L in enumerate(lens):
-        bb = _chain_backbone(int(L), rng)
-        bb -= bb[:, 1].mean(axis=0)
-        c, s = _assemble(bb)
-        sl = slice(offsets[i], offsets[i + 1])
-        coords[sl], src[sl] = c, s
-        tokens[sl] = native_tokens(int(L), rng)
+        phi[i, :L], psi[i, :L] = _phi_psi(int(L), rng)
+        tokens[offsets[i]:offsets[i + 1]] = native_tokens(int(L), rng)
+    coords = np.empty((offsets[-1], 5, 3), dtype=np.float32)
+    src = np.empty((offsets[-1], 5), dtype=np.uint8)
+    for b0 in range(0, n, 1024):  # bounded memory: [1024, Lmax, 4, 3] float64 per block
+        xyz = _nerf(phi[b0:b0 + 1024], psi[b0:b0 + 1024])
+        for i in range(b0, min(n, b0 + 1024)):
+            bb = xyz[i - b0, :lens[i]].copy()
+            bb -= bb[:, 1].mean(axis=0)
+            sl = slice(offsets[i], offsets[i + 1])
+            coords[sl], src[sl] = _assemble(bb)
     return coords, src, tokens, offsets
 
 

@@ -797,6 +797,10 @@ hkbs_status design_on_device(hkbs_pmpnn* ctx, const float* coords, const uint8_t
                              const int32_t* chain, const float* chain_mask, const int32_t* true_tokens, int L, int B,
                              const int32_t* orders, int shared, const uint64_t* seeds, float temperature, int greedy,
                              int32_t* tokens, float* log_probs, float* scores, DeviceArena& ar, float* chosen) {
+  // The decode runs as an ordinary launch whose grid is resident at once, with
+  // bounded team barriers; a cooperative launch is not offered.
+  if (const char* mode = std::getenv("HKBS_DECODE_LAUNCH"); mode && std::strcmp(mode, "cooperative") == 0)
+    return fail(HKBS_UNIMPLEMENTED, "cooperative decode launch is not supported");
   const int K = std::min(kKmax, L);
   const size_t S = (size_t)L * K;
   EncodeBuffers e = take_encode(ar, L, K);
@@ -1283,8 +1287,11 @@ hkbs_status hkbs_pmpnn_score_batch(hkbs_pmpnn* ctx, int32_t n, const int64_t* of
       for (int p = 0; p < L; ++p) pos[(size_t)o + p] = p;
     }
   }
-  // Chunks of consecutive proteins with the same K = min(48, L), bounded in edges.
-  const size_t kChunkEdges = (size_t)4 << 20;
+  // Chunks of consecutive proteins with the same K = min(48, L), bounded in edges
+  // (HKBS_SCORE_CHUNK_EDGES lowers the bound, so that tests can reach several chunks).
+  size_t kChunkEdges = (size_t)4 << 20;
+  if (const char* env = std::getenv("HKBS_SCORE_CHUNK_EDGES"))
+    kChunkEdges = std::max<size_t>(1, std::min<size_t>(kChunkEdges, std::strtoull(env, nullptr, 10)));
   struct Chunk { int first, last; int64_t r0, r1; int K; };
   std::vector<Chunk> chunks;
   for (int i = 0; i < n;) {
@@ -1311,6 +1318,9 @@ hkbs_status hkbs_pmpnn_score_batch(hkbs_pmpnn* ctx, int32_t n, const int64_t* of
   for (const Chunk& ch : chunks) {
     const int L = (int)(ch.r1 - ch.r0);
     const int np = ch.last - ch.first;
+    // The arena and the host staging vectors are reused per chunk: finish the
+    // previous chunk's kernels and copies (which read seg and loc) first.
+    HK_CHECK(hipStreamSynchronize(s), "teacher-forced kernels failed");
     seg.resize(L);
     loc.resize(np + 1);
     for (int p = 0; p < np; ++p) {
@@ -1318,8 +1328,6 @@ hkbs_status hkbs_pmpnn_score_batch(hkbs_pmpnn* ctx, int32_t n, const int64_t* of
       for (int64_t r = offsets[ch.first + p]; r < offsets[ch.first + p + 1]; ++r) seg[r - ch.r0] = p;
     }
     loc[np] = L;
-    // The arena is reused per chunk: finish the previous chunk's copies first.
-    HK_CHECK(hipStreamSynchronize(s), "teacher-forced kernels failed");
     ar.reset();
     Inputs in{};
     if ((st = upload_inputs(ctx, ar, coords + ch.r0 * 15, atom_sources + ch.r0 * 5, nullptr, nullptr, nullptr, nullptr, L,

@@ -173,19 +173,35 @@ __device__ inline int sample_wave(const float* logits, float T, bool greedy, uin
   return tok;
 }
 
-// Relaxed device-scope accesses: written through to the level every CU of
-// the device reads, so team members see them after a team_sync.
+// Device-scope accesses of the state team members exchange (R rows, chosen
+// log-probs): the stores write through to the device coherence point and the
+// loads are served from it, never from a CU's L1 or an XCD's L2 copy that
+// could predate another workgroup's store. Relaxed atomics at agent scope.
 __device__ inline void store_dev(float* p, float v) { __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
 __device__ inline float load_dev(const float* p) {
   return __hip_atomic_load(const_cast<float*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+// Four consecutive floats (16-byte aligned) as two 8-byte device-scope loads.
+__device__ inline float4 load4_dev(const float* p) {
+  uint64_t* q = reinterpret_cast<uint64_t*>(const_cast<float*>(p));
+  const uint64_t a = __hip_atomic_load(q, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  const uint64_t b = __hip_atomic_load(q + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  return make_float4(__uint_as_float((uint32_t)a), __uint_as_float((uint32_t)(a >> 32)), __uint_as_float((uint32_t)b),
+                     __uint_as_float((uint32_t)(b >> 32)));
 }
 
 constexpr uint32_t kSpinLimit = 1u << 20;  // default polls (~1 s) before a team gives up
 
 // Barrier over the P workgroups of a team. Every wave first waits for its own
-// stores; thread 0 then counts the workgroup in and polls until all P have
-// arrived `target / P` times. Returns false (and raises the fault word) if the
-// wait does not end; the caller then stops so that every wave exits.
+// memory operations (so its device-scope stores of exchanged state have
+// completed at the device coherence point) and the workgroup meets at a
+// barrier; thread 0 then counts the workgroup in with a device-scope atomic
+// and polls the count with device-scope loads until all P have arrived
+// `target / P` times, and the workgroup meets again. Exchanged state is read
+// only after that, and only with device-scope loads (load_dev, load4_dev), so
+// a member sees every store the others made before they arrived, wherever
+// the members run on the device. Returns false (and raises the fault word) if
+// the wait does not end; the caller then stops so that every wave exits.
 __device__ inline bool team_sync(uint32_t* counter, uint32_t target, uint32_t spin_limit, uint32_t* fault, int* bad) {
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
@@ -405,7 +421,8 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(ModelDev m, DecodeArgs
                 const int j = nbr[i * kKmax + k];
                 if (j >= 0) {
                   e[s] = *reinterpret_cast<const float4*>(a.E1 + ((size_t)l * S + (size_t)tres[i] * K + k) * kH + c);
-                  z[s] = *reinterpret_cast<const float4*>((bwf[i * kKmax + k] ? Rl : Ql) + (size_t)j * kH + c);
+                  z[s] = bwf[i * kKmax + k] ? load4_dev(Rl + (size_t)j * kH + c)  // R: written by the team
+                                                : *reinterpret_cast<const float4*>(Ql + (size_t)j * kH + c);
                 }
               }
             }
@@ -1202,19 +1219,13 @@ hipError_t launch_decode_as(const ModelDev& m, const DecodeArgs& args, hipStream
   if (P > 1) {
     a.team = P;
     const dim3 grid((unsigned)(8 * teams_per_xcd * P));
-    const char* mode = std::getenv("HKBS_DECODE_LAUNCH");
-    if (mode && std::strcmp(mode, "cooperative") == 0) {
-      void* kargs[] = {&mm, &a};
-      return hipLaunchCooperativeKernel(reinterpret_cast<const void*>(&decode_kernel<PREC>), grid, dim3(kThreads),
-                                        kargs, 0, stream);
-    } else {
-      // The whole grid fits the device at once (one workgroup per CU at most),
-      // so on a device running nothing else every team is resident. Every
-      // team barrier wait is bounded: a member that is not resident ends the
-      // wait with the fault word raised instead of hanging.
-      decode_kernel<PREC><<<grid, kThreads, 0, stream>>>(mm, a);
-      return hipGetLastError();
-    }
+    // team_size_as sized the grid so that all of it is resident at once
+    // (at most the occupancy limit per CU over all CUs), so on a device
+    // running nothing else every team is resident. Every team barrier wait is
+    // bounded: a member that is not resident ends the wait with the fault
+    // word raised instead of hanging.
+    decode_kernel<PREC><<<grid, kThreads, 0, stream>>>(mm, a);
+    return hipGetLastError();
   }
   a.team = 1;
   decode_kernel<PREC><<<a.B, kThreads, 0, stream>>>(mm, a);

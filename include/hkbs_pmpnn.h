@@ -67,10 +67,13 @@ enum {
 enum {
   HKBS_PRECISION_FP32 = 0, /* default: featurisation and encoder in the reference's fp32 rounding,
                               log-probs within 1e-4 of the reference */
-  HKBS_PRECISION_BF16 = 1, /* bf16 weights and activations into every product of the edge
-                              embedding, encoder and decoder (MFMA), fp32 accumulation,
-                              GELU, LayerNorm and softmax */
-  HKBS_PRECISION_FP16 = 2  /* the same with fp16 (three more significant bits than bf16) */
+  HKBS_PRECISION_BF16 = 1, /* decoder in bf16: bf16 weights of every decoder product and bf16
+                              message rows into the W2 MFMA, fp32 accumulation, GELU, LayerNorm
+                              and softmax. Featurisation and encoder run on the fp16 MFMA with
+                              each operand split into two fp16 halves (fp32-level accuracy,
+                              not the reference's rounding sequence) */
+  HKBS_PRECISION_FP16 = 2  /* the same with an fp16 decoder (three more significant bits than
+                              bf16) */
 };
 
 typedef struct hkbs_pmpnn hkbs_pmpnn;
@@ -114,7 +117,7 @@ hkbs_status hkbs_pmpnn_design(hkbs_pmpnn* ctx, const float* coords, const uint8_
  * is [B,L] or [L] (shared != 0), and the call is enqueued on `stream`
  * (a hipStream_t; NULL = the context's stream) without synchronising.
  * residue_indices / chain_labels / chain_mask / true_tokens may be NULL.
- * When B leaves CUs free, each sequence is decoded by a team of up to four
+ * When B leaves CUs free, each sequence is decoded by a team of up to eight
  * workgroups that must run at the same time; on a device busy with other
  * work a team can fail to assemble, and then that sequence's score is NaN
  * (the synchronous hkbs_pmpnn_design detects this and decodes again with one

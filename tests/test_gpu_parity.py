@@ -311,6 +311,17 @@ def test_design_team_barrier_timeout_reruns(gpu_ctx, monkeypatch):
         np.testing.assert_array_equal(out[key], ref[key], err_msg=key)
 
 
+def test_design_cooperative_launch_unimplemented(gpu_ctx, monkeypatch):
+    """The decode is an ordinary launch with bounded team barriers; asking for a cooperative launch is
+    refused before anything is enqueued."""
+    bb = backbone.single_chain(20, 1)
+    seeds = np.array([1], dtype=np.uint64)
+    monkeypatch.setenv("HKBS_DECODE_LAUNCH", "cooperative")
+    with pytest.raises(_lib.HkbsError) as e:
+        gpu_ctx.design(bb.coords, bb.atom_sources, 1, seeds, order_seeds=seeds)
+    assert e.value.code == _lib.UNIMPLEMENTED
+
+
 def test_design_deterministic(gpu_ctx):
     bb = backbone.single_chain(64, 2)
     seeds = np.array([3, 4, 5], dtype=np.uint64)

@@ -163,6 +163,47 @@ def test_design_bit_exact_vs_reference(oracle, reference, name, bb, kw, mode):
     assert a["score"] == b["score"]
 
 
+def _k_below_l_cases():
+    """Backbones longer than 48 residues, where K = 48 < L (cpp/modules/mpnn/inverse_fold_scalar.cpp:892-896):
+    every kNN row is a strict subset of the chain, so a K/L mix-up changes the graph."""
+    bb = backbone.single_chain(300, 6)
+    src = bb.atom_sources.copy()
+    src[[11, 150], 3] = 0  # inactive residues
+    src[70, 4] = 0  # missing CB
+    return [("L120", backbone.single_chain(120, 4)), ("L300_masked", backbone.Backbone(bb.coords, src)),
+            ("complex4x64", backbone.tetrahedral_complex(64, 2))]
+
+
+@pytest.mark.parametrize("name,bb", _k_below_l_cases(), ids=lambda v: v if isinstance(v, str) else "")
+@pytest.mark.parametrize("mode", ["random", "n_to_c"])
+def test_design_bit_exact_vs_reference_k_below_l(oracle, reference, name, bb, mode):
+    kw = dict(seed=41, order_seed=41, temperature=0.1, use_input_order=mode == "n_to_c")
+    if name == "L300_masked":
+        cm = np.ones(bb.L, np.float32)
+        cm[200:230] = 0
+        kw.update(chain_mask=cm, true_tokens=(np.arange(bb.L) * 7 % 20).astype(np.int32))
+    a = oracle.inverse_fold(bb, **kw)
+    b = reference.inverse_fold(bb, **kw)
+    assert oracle.encode(bb)[1].shape == (bb.L, 48) and bb.L > 48
+    for k in ("tokens", "log_probs", "order"):
+        np.testing.assert_array_equal(a[k], b[k], err_msg=k)
+    assert a["score"] == b["score"]
+
+
+@pytest.mark.parametrize("name,bb", _k_below_l_cases(), ids=lambda v: v if isinstance(v, str) else "")
+def test_teacher_forced_bit_exact_vs_reference_k_below_l(oracle, reference, name, bb):
+    """Teacher forcing with a random input order and a chain mask, K = 48 < L."""
+    rng = np.random.default_rng(5)
+    tok = rng.integers(0, 21, bb.L).astype(np.int32)
+    order = rng.permutation(bb.L).astype(np.int32)
+    cm = np.ones(bb.L, np.float32)
+    cm[bb.L // 3:bb.L // 2] = 0
+    a = oracle.teacher_forced(bb, tok, input_order=order, chain_mask=cm)
+    b = reference.teacher_forced(bb, tok, input_order=order, chain_mask=cm)
+    np.testing.assert_array_equal(a[0], b[0])
+    assert a[1] == b[1]
+
+
 def test_algorithm_loop_bit_exact_vs_reference(oracle, reference):
     bb = backbone.single_chain(30, 7)
     a = oracle.algorithm_inverse_fold(bb, 3, 7, 0.1)
