@@ -23,7 +23,8 @@ PRECISION_FP32, PRECISION_BF16, PRECISION_FP16 = range(3)
 #: Symbols declared in include/*.h.
 EXPORTS = (
     "hkbs_last_error", "hkbs_version", "hkbs_device_count", "hkbs_pmpnn_create", "hkbs_pmpnn_destroy",
-    "hkbs_pmpnn_design", "hkbs_pmpnn_design_device", "hkbs_pmpnn_score", "hkbs_pmpnn_decode_order",
+    "hkbs_pmpnn_design", "hkbs_pmpnn_design_device", "hkbs_pmpnn_design_device_noalloc", "hkbs_pmpnn_score",
+    "hkbs_pmpnn_decode_order",
     "hkbs_pmpnn_knn", "hkbs_pmpnn_encode", "hkbs_pmpnn_edge_features", "hkbs_pmpnn_set_timing",
     "hkbs_pmpnn_last_timing", "hkbs_pmpnn_score_batch", "hkbs_pmpnn_backbone_noise", "hkbs_pmpnn_set_precision",
     "hkbs_structure_default_options", "hkbs_structure_detect_format", "hkbs_structure_load_file",
@@ -78,6 +79,8 @@ def load() -> C.CDLL:
     lib.hkbs_pmpnn_design_device.restype = _i32
     lib.hkbs_pmpnn_design_device.argtypes = [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _i32, _i32, _vp, _i32, _vp,
                                              C.c_float, _i32, _vp, _vp, _vp, _vp]
+    lib.hkbs_pmpnn_design_device_noalloc.restype = _i32
+    lib.hkbs_pmpnn_design_device_noalloc.argtypes = lib.hkbs_pmpnn_design_device.argtypes
     lib.hkbs_pmpnn_score.restype = _i32
     lib.hkbs_pmpnn_score.argtypes = [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i32, _vp, _vp]
     lib.hkbs_pmpnn_score_batch.restype = _i32

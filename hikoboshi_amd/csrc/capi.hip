@@ -403,8 +403,16 @@ void residue_mask_host(const uint8_t* src, int L, std::vector<float>& mask) {
 
 }  // namespace
 
+// Scratch of hkbs_pmpnn_design_device_noalloc: one static array per GPU that
+// the library runs on (held until the process ends). Host code never uses the
+// array's name as an address: hkbs_pmpnn_create looks up this device's
+// address with hipGetSymbolAddress and keeps it in the context.
+constexpr size_t kNoAllocScratchBytes = (size_t)128 << 20;
+static __device__ __align__(256) unsigned char scratch[kNoAllocScratchBytes];
+
 struct hkbs_pmpnn {
   int device = 0;
+  char* scratch = nullptr;      // this device's address of `scratch`
   hipStream_t stream = nullptr;
   hipStream_t side = nullptr;   // builds the decode schedule while the encoder runs
   hipEvent_t fork = nullptr;    // kNN graph ready (recorded on stream)
@@ -792,6 +800,18 @@ hkbs_status check_temperature(float temperature) {
   return HKBS_OK;
 }
 
+// Bytes a device design takes from its arena: the chosen-log-prob buffer of
+// the device entry points, then design_on_device's buffers in its order.
+size_t design_scratch_bytes(int L, int B, bool shared) {
+  const int K = std::min(kKmax, L);
+  const size_t S = (size_t)L * K, nq = shared ? 1 : (size_t)B;
+  return aligned_bytes<float>((size_t)B * L) + encode_bytes(L, K) + aligned_bytes<float>(kLayers * S * kH) +
+         aligned_bytes<float>((size_t)(kLayers + 1) * L * kH) + aligned_bytes<int32_t>((size_t)B * L) +
+         aligned_bytes<float>((size_t)B * kLayers * L * kH) + aligned_bytes<uint32_t>((size_t)B + 1) +
+         2 * aligned_bytes<int32_t>(nq * L * K) + aligned_bytes<int32_t>(nq * L) + aligned_bytes<int32_t>(nq * (L + 2)) +
+         aligned_bytes<int32_t>(nq) + aligned_bytes<int32_t>(nq * L) + aligned_bytes<int32_t>(sched_scratch_words(L, K, nq));
+}
+
 // Shared implementation of the device design path. All pointers device.
 hkbs_status design_on_device(hkbs_pmpnn* ctx, const float* coords, const uint8_t* src, const int32_t* resid,
                              const int32_t* chain, const float* chain_mask, const int32_t* true_tokens, int L, int B,
@@ -817,6 +837,7 @@ hkbs_status design_on_device(hkbs_pmpnn* ctx, const float* coords, const uint8_t
   int32_t* npass = ar.take<int32_t>(nq);
   int32_t* draw = ar.take<int32_t>(nq * L);
   int32_t* sched_tmp = ar.take<int32_t>(sched_scratch_words(L, K, nq));
+  if (ar.used > ar.cap) return fail(HKBS_INTERNAL_ERROR, "design workspace exceeds its reservation");
   ctx->fault = sync + B;
   DecodeArgs a{};
   a.idx = e.idx;
@@ -940,6 +961,12 @@ hkbs_status hkbs_pmpnn_create(const uint8_t* data, size_t nbytes, int32_t device
     hkbs_pmpnn_destroy(ctx);
     return fail(HKBS_UNAVAILABLE, "HIP stream creation failed");
   }
+  void* sp = nullptr;
+  if (hipGetSymbolAddress(&sp, HIP_SYMBOL(scratch)) != hipSuccess || !sp) {
+    hkbs_pmpnn_destroy(ctx);
+    return fail(HKBS_UNAVAILABLE, "device scratch of the allocation-free design is not available");
+  }
+  ctx->scratch = static_cast<char*>(sp);
   const hkbs_status st = build_model(ctx, ptrs.data());
   if (st != HKBS_OK) {
     hkbs_pmpnn_destroy(ctx);
@@ -1110,6 +1137,38 @@ hkbs_status hkbs_pmpnn_design_device(hkbs_pmpnn* ctx, const float* coords, const
     return fail(HKBS_INTERNAL_ERROR, "device workspace allocation failed");
   }
   ar.reset();
+  float* chosen = ar.take<float>((size_t)B * L);
+  st = design_on_device(ctx, coords, atom_sources, residue_indices, chain_labels, chain_mask, true_tokens, L, B, orders,
+                        shared_order != 0, sampler_seeds, temperature, greedy, tokens, log_probs, scores, ar, chosen);
+  ctx->stream = saved;
+  return st;
+}
+
+hkbs_status hkbs_pmpnn_design_device_noalloc(hkbs_pmpnn* ctx, const float* coords, const uint8_t* atom_sources,
+                                             const int32_t* residue_indices, const int32_t* chain_labels,
+                                             const float* chain_mask, const int32_t* true_tokens, int32_t L, int32_t B,
+                                             const int32_t* orders, int32_t shared_order,
+                                             const uint64_t* sampler_seeds, float temperature, int32_t greedy,
+                                             int32_t* tokens, float* log_probs, float* scores, void* stream) {
+  hkbs_status st = enter(ctx);
+  if (st != HKBS_OK) return st;
+  if (L < 0) return fail(HKBS_INVALID_ARGUMENT, "residue count is negative");
+  if (B <= 0) return fail(HKBS_INVALID_ARGUMENT, "inverse-fold num_seqs must be greater than zero");
+  if ((st = check_temperature(temperature)) != HKBS_OK) return st;
+  if (L == 0) return HKBS_OK;
+  if (!coords || !atom_sources || !orders || !sampler_seeds || !tokens)
+    return fail(HKBS_INVALID_ARGUMENT, "device design pointers must be non-null");
+  if (design_scratch_bytes(L, B, shared_order != 0) > kNoAllocScratchBytes)
+    return fail(HKBS_INVALID_ARGUMENT,
+                "request needs more device scratch than the allocation-free design holds (128 MiB)");
+  DeviceArena ar;  // borrows this device's static scratch; never freed
+  ar.base = ctx->scratch;
+  ar.cap = kNoAllocScratchBytes;
+  hipStream_t saved = ctx->stream;
+  if (stream) {
+    HK_CHECK(hipStreamSynchronize(saved), "context stream failed");
+    ctx->stream = static_cast<hipStream_t>(stream);
+  }
   float* chosen = ar.take<float>((size_t)B * L);
   st = design_on_device(ctx, coords, atom_sources, residue_indices, chain_labels, chain_mask, true_tokens, L, B, orders,
                         shared_order != 0, sampler_seeds, temperature, greedy, tokens, log_probs, scores, ar, chosen);

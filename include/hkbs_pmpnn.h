@@ -132,6 +132,30 @@ hkbs_status hkbs_pmpnn_design_device(hkbs_pmpnn* ctx, const float* coords,
                                      int32_t greedy, int32_t* tokens, float* log_probs,
                                      float* scores, void* stream);
 
+/* Allocation-free variant of hkbs_pmpnn_design_device, with the same arguments,
+ * outputs and bits. No counterpart in the reference (its scalar path allocates
+ * std::vector workspaces per call); it is for callers that cannot allocate
+ * device memory: code under HIP graph capture, tight serving loops, harnesses
+ * that forbid hipMalloc. Its scratch (encoder states, decoder precompute,
+ * per-sequence decoder state, decode schedule, team barrier counters) lives in
+ * one static device array of 128 MiB per GPU, which each GPU the library runs
+ * on holds until the process ends; the call makes no hipMalloc or hipFree.
+ * A request whose scratch exceeds 128 MiB returns HKBS_INVALID_ARGUMENT (at
+ * L = 300: up to 206 sequences with a shared order, 149 with one order per
+ * sequence; L = 4,000 does not fit). Every call on one
+ * GPU shares that GPU's array and leaves its contents behind (what must start
+ * at zero is cleared by a kernel in the call): calls that overlap on one GPU,
+ * from any context or stream, race and must be serialised by the caller. */
+hkbs_status hkbs_pmpnn_design_device_noalloc(hkbs_pmpnn* ctx, const float* coords,
+                                             const uint8_t* atom_sources,
+                                             const int32_t* residue_indices,
+                                             const int32_t* chain_labels, const float* chain_mask,
+                                             const int32_t* true_tokens, int32_t L, int32_t B,
+                                             const int32_t* orders, int32_t shared_order,
+                                             const uint64_t* sampler_seeds, float temperature,
+                                             int32_t greedy, int32_t* tokens, float* log_probs,
+                                             float* scores, void* stream);
+
 /* Teacher-forced scoring of one protein (proteinmpnn_teacher_forced_forward_scalar,
  * cpp/modules/mpnn/inverse_fold_scalar.cpp:905-952): plain log_softmax
  * log-probs [L,21] and mean NLL. order may be NULL (N-to-C). Host memory.
