@@ -39,12 +39,44 @@ __global__ void tf_init_kernel(ModelDev m, const float* __restrict__ Q, const in
   NB[r * 256 + kH + c] = Q[r * kH + c] + m.dec[0].T[tokens[r] * kH + c];
 }
 
-__global__ __launch_bounds__(256) void tf_edge_kernel(DecLayerDev w, const float* __restrict__ W1b_p, int layer,
+// acc[mb][nb][i] = sum_k A[16 mb + r][k] W[n0 + 16 nb + 4 g + i][k] on the fp32
+// MFMA: mfma_tile with the operands exchanged (weights as the MFMA's A
+// operand), so that lane (r, g) holds row 16 mb + r and four consecutive
+// output columns.
+template <int MB, int NB>
+__device__ inline void mfma_tile_rows(const float* __restrict__ A, int lda, const float* __restrict__ Wp, int N,
+                                      int n0, int kdim, floatx4 (&acc)[MB][NB]) {
+  const int lane = threadIdx.x & 63;
+  const int r = lane & 15;
+  const int g = lane >> 4;
+  for (int kb = 0; kb < kdim / 16; ++kb) {
+    float4 a[MB];
+    float4 b[NB];
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb)
+      b[nb] = *reinterpret_cast<const float4*>(Wp + ((size_t)kb * N + n0 + nb * 16 + r) * 16 + 4 * g);
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb)
+      a[mb] = *reinterpret_cast<const float4*>(A + (mb * 16 + r) * lda + kb * 16 + 4 * g);
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+      for (int nb = 0; nb < NB; ++nb) {
+        acc[mb][nb] = mfma16(b[nb].x, a[mb].x, acc[mb][nb]);
+        acc[mb][nb] = mfma16(b[nb].y, a[mb].y, acc[mb][nb]);
+        acc[mb][nb] = mfma16(b[nb].z, a[mb].z, acc[mb][nb]);
+        acc[mb][nb] = mfma16(b[nb].w, a[mb].w, acc[mb][nb]);
+      }
+  }
+}
+
+__global__ __launch_bounds__(256, 2) void tf_edge_kernel(DecLayerDev w, const float* __restrict__ W1b_p, int layer,
                                                       const float* __restrict__ h_e, const int32_t* __restrict__ idx,
                                                       const int32_t* __restrict__ pos, const float* __restrict__ mask,
                                                       const float* __restrict__ NB, const float* __restrict__ Ql, int L,
                                                       int K, float* __restrict__ msg_sum) {
   __shared__ __attribute__((aligned(16))) float A[kRows * kLd];
+  __shared__ __attribute__((aligned(16))) float gtab[kGeluPolyRows * 8];
   // per edge row, formed once: its residue t, and its neighbour j with the
   // backward flag (pos[j] < pos[t]) in bit 31, or -1 when the slot adds nothing
   __shared__ int row_t[kRows], row_j[kRows];
@@ -54,7 +86,8 @@ __global__ __launch_bounds__(256) void tf_edge_kernel(DecLayerDev w, const float
   const int n_rows = nr * K;
   const size_t slot0 = (size_t)r0 * K;
   const int wave = threadIdx.x >> 6;
-  const int lane = threadIdx.x & 63;
+  const int lane = threadIdx.x & 63, r = lane & 15, g = lane >> 4;
+  for (int i = threadIdx.x; i < kGeluPolyRows * 8; i += blockDim.x) gtab[i] = kGeluPoly[i];
   if (threadIdx.x < n_rows) {
     const int row = threadIdx.x;
     const int t = r0 + row / K;
@@ -62,53 +95,82 @@ __global__ __launch_bounds__(256) void tf_edge_kernel(DecLayerDev w, const float
     row_t[row] = t;
     row_j[row] = (j >= 0 && j < L && mask[t] != 0.0F) ? (j | (pos[j] < pos[t] ? (int)0x80000000u : 0)) : -1;
   }
-
-  for (int task = threadIdx.x; task < kRows * (kH / 4); task += blockDim.x) {
-    const int row = task / (kH / 4), c4 = task % (kH / 4);
-    float4 v = make_float4(0.F, 0.F, 0.F, 0.F);
-    if (row < n_rows) v = *reinterpret_cast<const float4*>(h_e + (slot0 + row) * kH + 4 * c4);
-    *reinterpret_cast<float4*>(A + row * kLd + 4 * c4) = v;
+  {
+    // the tile's h_E rows: thread (wave w, lane c) loads float4 column c % 32 of rows 2 w + c / 32 + 8 i,
+    // all loads issued before the first store
+    constexpr int N = kRows * (kH / 4) / 256;
+    float4 v[N];
+#pragma unroll
+    for (int i = 0; i < N; ++i) {
+      const int row = 2 * wave + (lane >> 5) + 8 * i;
+      v[i] = row < n_rows ? *reinterpret_cast<const float4*>(h_e + (slot0 + row) * kH + 4 * (lane & 31))
+                          : make_float4(0.F, 0.F, 0.F, 0.F);
+    }
+#pragma unroll
+    for (int i = 0; i < N; ++i)
+      *reinterpret_cast<float4*>(A + (2 * wave + (lane >> 5) + 8 * i) * kLd + 4 * (lane & 31)) = v[i];
   }
   __syncthreads();
+  // x = A_t + (E1 + (bw ? R_j : Q_j)) for a slot that adds something, else A_t; its GELU into A.
+  // The A and R|Q rows load before the E1 product.
+  float4 base[6][2], nbr[6][2];
+#pragma unroll
+  for (int mb = 0; mb < 6; ++mb) {
+    const int row = mb * 16 + r;
+    const int t = row < n_rows ? row_t[row] : 0;
+    const int jb = row < n_rows ? row_j[row] : -1;
+    const int j = jb & 0x7FFFFFFF;
+#pragma unroll
+    for (int nb = 0; nb < 2; ++nb) {
+      const int c0 = wave * 32 + nb * 16 + 4 * g;
+      base[mb][nb] = row < n_rows ? *reinterpret_cast<const float4*>(NB + (size_t)t * 256 + c0)
+                                  : make_float4(0.F, 0.F, 0.F, 0.F);
+      nbr[mb][nb] = jb == -1 ? make_float4(0.F, 0.F, 0.F, 0.F)
+                             : *reinterpret_cast<const float4*>(jb < 0 ? NB + (size_t)j * 256 + kH + c0
+                                                                       : Ql + (size_t)j * kH + c0);
+    }
+  }
   floatx4 acc[6][2];
   zero_acc(acc);
-  mfma_tile<6, 2>(A, kLd, W1b_p, kLayers * kH, layer * kH + wave * 32, kH, acc);
+  mfma_tile_rows<6, 2>(A, kLd, W1b_p, kLayers * kH, layer * kH + wave * 32, kH, acc);
   __syncthreads();
 #pragma unroll
-  for (int mb = 0; mb < 6; ++mb)
+  for (int mb = 0; mb < 6; ++mb) {
+    const int row = mb * 16 + r;
+    const bool adds = row < n_rows && row_j[row] != -1;
 #pragma unroll
-    for (int nb = 0; nb < 2; ++nb)
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int row = mb * 16 + 4 * (lane >> 4) + i;
-        const int col = wave * 32 + nb * 16 + (lane & 15);
-        float v = 0.0F;
-        if (row < n_rows) {
-          const int t = row_t[row];
-          const int jb = row_j[row];
-          float x = NB[(size_t)t * 256 + col];
-          if (jb != -1) {
-            const int j = jb & 0x7FFFFFFF;
-            x += acc[mb][nb][i] + (jb < 0 ? NB[(size_t)j * 256 + kH + col] : Ql[(size_t)j * kH + col]);
-          }
-          v = gelu(x);
-        }
-        A[row * kLd + col] = v;
+    for (int nb = 0; nb < 2; ++nb) {
+      const int c0 = wave * 32 + nb * 16 + 4 * g;
+      float4 o = make_float4(0.F, 0.F, 0.F, 0.F);
+      if (row < n_rows) {
+        const float4 x = base[mb][nb], e = nbr[mb][nb];
+        const floatx4 y = acc[mb][nb];
+        o = adds ? make_float4(gelu_poly(x.x + (y[0] + e.x), gtab), gelu_poly(x.y + (y[1] + e.y), gtab),
+                               gelu_poly(x.z + (y[2] + e.z), gtab), gelu_poly(x.w + (y[3] + e.w), gtab))
+                 : make_float4(gelu_poly(x.x, gtab), gelu_poly(x.y, gtab), gelu_poly(x.z, gtab),
+                               gelu_poly(x.w, gtab));
       }
+      *reinterpret_cast<float4*>(A + row * kLd + c0) = o;
+    }
+  }
   __syncthreads();
   zero_acc(acc);
-  mfma_tile<6, 2>(A, kLd, w.W2_p, kH, wave * 32, kH, acc);
+  mfma_tile_rows<6, 2>(A, kLd, w.W2_p, kH, wave * 32, kH, acc);
   __syncthreads();
 #pragma unroll
-  for (int mb = 0; mb < 6; ++mb)
+  for (int nb = 0; nb < 2; ++nb) {
+    const int c0 = wave * 32 + nb * 16 + 4 * g;
+    const float4 bv = *reinterpret_cast<const float4*>(w.b2 + c0);
 #pragma unroll
-    for (int nb = 0; nb < 2; ++nb)
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int row = mb * 16 + 4 * (lane >> 4) + i;
-        const int col = wave * 32 + nb * 16 + (lane & 15);
-        A[row * kLd + col] = (row < n_rows) ? gelu(acc[mb][nb][i] + w.b2[col]) : 0.0F;
-      }
+    for (int mb = 0; mb < 6; ++mb) {
+      const int row = mb * 16 + r;
+      const floatx4 y = acc[mb][nb];
+      *reinterpret_cast<float4*>(A + row * kLd + c0) =
+          row < n_rows ? make_float4(gelu_poly(y[0] + bv.x, gtab), gelu_poly(y[1] + bv.y, gtab),
+                                     gelu_poly(y[2] + bv.z, gtab), gelu_poly(y[3] + bv.w, gtab))
+                       : make_float4(0.F, 0.F, 0.F, 0.F);
+    }
+  }
   __syncthreads();
   for (int task = threadIdx.x; task < nr * kH; task += blockDim.x) {
     const int lr = task / kH, c = task % kH;

@@ -11,9 +11,12 @@
 // sum are fp32, and h_V, h_E are stored in fp32. The kNN graph comes from the
 // exact fp32 kernel.
 //
-// A wave owns 16 rows of every product: its A operand is a 16-row fp32 slab
-// of LDS, split into hi / lo fragments as it is read, and it produces all 128
-// output columns as 8 MFMA tiles while the split weights stream from L2.
+// Edge products (the bulk of the work) run as workgroup tiles of 48 or 64 edge
+// rows and four waves: the tile's operand sits in LDS already split into fp16
+// hi / lo halves, every wave reads all of its rows and produces 32 of the 128
+// output columns, so each weight fragment streamed from L2 feeds 3 or 4 row
+// blocks. The edge embedding and the node kernel keep 16 rows per wave with
+// the fp32 operand split as it is read (wave_gemm).
 //
 // The h_i block of W1 [h_i | e_ij | h_j] (and of W11) is the same for all K
 // slots of residue i, so node16 computes it once per residue into a prefix
@@ -25,13 +28,13 @@
 //   edge_embed16   32 edge slots per workgroup (2 waves): 416 features ->
 //                  W_edge -> LN -> W_e -> h_E.
 //   per layer:
-//   edge_msg16     one residue per workgroup (3 waves = 48 slots):
+//   edge_msg16     one residue per workgroup (48 slots, 4 waves):
 //                  prefix + W1 [e_ij | h_j], GELU, W2, GELU, W3 -> the masked
 //                  sum over the residue's slots / 30 -> upd[i].
 //   node16         16 residues per workgroup (4 waves, a quarter of the FFN
 //                  each): LN1(h + upd), the FFN on the MFMA, LN2, mask; then
 //                  the W11 and next-layer W1 prefixes of the new h.
-//   edge_update16  32 edge slots per workgroup (2 waves): prefix + W11
+//   edge_update16  64 edge slots per workgroup (4 waves): prefix + W11
 //                  [e_ij | h_j], GELU, W12, GELU, W13, residual, LN3 -> h_E
 //                  (valid slots).
 #include "device_math.hpp"
@@ -43,8 +46,6 @@ namespace {
 
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 
-constexpr int kLdA = 2 * kH + 4;   // floats per slab row of [e_ij | h_j] (16-byte pad)
-constexpr int kLdX = kEdgeIn + 4;  // floats per slab row of edge features
 constexpr int kLdF = kFF + 4;      // floats per row of the FFN hidden layer
 constexpr int kLdH = kH + 4;       // floats per row of a 128-wide activation
 static_assert(kKmax == 48, "edge_msg16 covers a residue's slots with 3 waves of 16 rows");
@@ -139,6 +140,193 @@ __device__ inline float sum16(float v) {
   return v;
 }
 
+// ------------------------------------------------------------ edge tiles ----
+// A tile holds 16 RB edge rows. Its operands live in LDS split into fp16
+// halves, hi [rows][ld] then lo [rows][ld] (v = hi + lo / 2048); a row stride
+// of K + 8 halves steps 4 banks per row, so the 16-byte fragment reads of 8
+// consecutive rows cover all banks once. Wave w produces output columns
+// [32 w, 32 w + 32) as two 16-column MFMA tiles per row block, computed
+// transposed (weights as the MFMA's A operand, rows as its B operand): lane
+// (r, g) then holds row 16 rb + r, columns 32 w + 16 nt + 4 g + (0..3).
+constexpr int kTileThreads = 256;
+constexpr int kLdS2 = 2 * kH + 8;  // halves per row of a K = 256 operand ([e_ij | h_j])
+constexpr int kLdS1 = kH + 8;      // halves per row of a K = 128 operand
+typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
+
+// Four consecutive floats into the split slab at (row, col).
+__device__ inline void put_split4(_Float16* S, int rows, int ld, int row, int col, float4 v) {
+  const float f[4] = {v.x, v.y, v.z, v.w};
+  f16x4 h, l;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const _Float16 hi = static_cast<_Float16>(__builtin_amdgcn_fmed3f(f[e], -65504.0F, 65504.0F));
+    h[e] = hi;
+    l[e] = static_cast<_Float16>((f[e] - static_cast<float>(hi)) * 2048.0F);
+  }
+  *reinterpret_cast<f16x4*>(S + row * ld + col) = h;
+  *reinterpret_cast<f16x4*>(S + (rows + row) * ld + col) = l;
+}
+
+// acc[rb][nt][i] = sum_k A[16 rb + r][k] W[n0 + 16 nt + 4 g + i][k] over K
+// inputs (added to acc when accumulate), A the split slab (rows = 16 RB,
+// stride ld), W (128 outputs) split as hi [K / 8][128][8] halves with lo at
+// Wp + lo_off. Weight fragments stream through a ring of PF k-steps, so each
+// load is issued PF - 1 k-steps before its use.
+template <int RB, int K, int PF = 4>
+__device__ inline void tile_gemm(const _Float16* S, int ld, const uint16_t* __restrict__ Wp, int n0, size_t lo_off,
+                                 floatx4 (&acc)[RB][2], bool accumulate = false) {
+  constexpr int NKB = K / 32;
+  constexpr size_t kstep = (size_t)4 * kH * 8;  // halves per 32 inputs
+  static_assert(K % 32 == 0 && PF >= 2, "k-steps");
+  const int lane = threadIdx.x & 63, r = lane & 15, g = lane >> 4;
+  const _Float16* Sh = S + r * ld + 8 * g;
+  const _Float16* Sl = Sh + 16 * RB * ld;
+  const uint16_t* wh = Wp + ((size_t)g * kH + n0 + r) * 8;
+  const uint16_t* wl = wh + lo_off;
+  floatx4 cor[RB][2];
+#pragma unroll
+  for (int rb = 0; rb < RB; ++rb)
+#pragma unroll
+    for (int nt = 0; nt < 2; ++nt) {
+      cor[rb][nt] = floatx4{0.F, 0.F, 0.F, 0.F};
+      if (!accumulate) acc[rb][nt] = cor[rb][nt];
+    }
+  f16x8 bh[PF][2], bl[PF][2];
+#pragma unroll
+  for (int kb = 0; kb < PF - 1 && kb < NKB; ++kb)
+#pragma unroll
+    for (int nt = 0; nt < 2; ++nt) {
+      bh[kb][nt] = *reinterpret_cast<const f16x8*>(wh + kb * kstep + (size_t)nt * 16 * 8);
+      bl[kb][nt] = *reinterpret_cast<const f16x8*>(wl + kb * kstep + (size_t)nt * 16 * 8);
+    }
+#pragma unroll
+  for (int kb = 0; kb < NKB; ++kb) {
+    const int kn = kb + PF - 1;
+    if (kn < NKB) {
+#pragma unroll
+      for (int nt = 0; nt < 2; ++nt) {
+        bh[kn % PF][nt] = *reinterpret_cast<const f16x8*>(wh + kn * kstep + (size_t)nt * 16 * 8);
+        bl[kn % PF][nt] = *reinterpret_cast<const f16x8*>(wl + kn * kstep + (size_t)nt * 16 * 8);
+      }
+    }
+#pragma unroll
+    for (int rb = 0; rb < RB; ++rb) {
+      const f16x8 ah = *reinterpret_cast<const f16x8*>(Sh + 16 * rb * ld + 32 * kb);
+      const f16x8 al = *reinterpret_cast<const f16x8*>(Sl + 16 * rb * ld + 32 * kb);
+#pragma unroll
+      for (int nt = 0; nt < 2; ++nt) {
+        acc[rb][nt] = mfma_f16(bh[kb % PF][nt], ah, acc[rb][nt]);
+        cor[rb][nt] = mfma_f16(bh[kb % PF][nt], al, cor[rb][nt]);
+        cor[rb][nt] = mfma_f16(bl[kb % PF][nt], ah, cor[rb][nt]);
+      }
+    }
+  }
+#pragma unroll
+  for (int rb = 0; rb < RB; ++rb)
+#pragma unroll
+    for (int nt = 0; nt < 2; ++nt)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) acc[rb][nt][i] += cor[rb][nt][i] * (1.0F / 2048.0F);
+}
+
+// The tile's rows [e_ij | h_j] (slot = slot_of(row); negative: a zero row;
+// j = idx[slot] outside [0, L): a zero h_j block) into the split slab. Thread
+// (wave w, lane c) fills float4 column c of rows w, w + 4, ...; all of its
+// index loads, then all of its row loads, are issued before the first use.
+template <int RB, typename SlotOf>
+__device__ inline void tile_rows(_Float16* S, const float* __restrict__ h_v, const float* __restrict__ h_e,
+                                 const int32_t* __restrict__ idx, int L, SlotOf slot_of) {
+  constexpr int R = 16 * RB, N = R * 64 / kTileThreads;
+  const int c4 = threadIdx.x & 63, part = c4 >> 5, col = 4 * (c4 & 31), row0 = threadIdx.x >> 6;
+  long long src[N];
+#pragma unroll
+  for (int i = 0; i < N; ++i) src[i] = slot_of(row0 + 4 * i);
+  if (part) {
+#pragma unroll
+    for (int i = 0; i < N; ++i) {
+      const int j = src[i] >= 0 ? idx[src[i]] : -1;
+      src[i] = (j >= 0 && j < L) ? j : -1;
+    }
+  }
+  const float* base = part ? h_v : h_e;
+  float4 v[N];
+#pragma unroll
+  for (int i = 0; i < N; ++i)
+    v[i] = src[i] >= 0 ? *reinterpret_cast<const float4*>(base + (size_t)src[i] * kH + col)
+                       : make_float4(0.F, 0.F, 0.F, 0.F);
+#pragma unroll
+  for (int i = 0; i < N; ++i) put_split4(S, R, kLdS2, row0 + 4 * i, part * kH + col, v[i]);
+}
+
+// GELU(acc + add + bias) of the wave's columns into the split slab (K = 128
+// operand of the next product); add[rb] is a per-row base (the h_i prefix).
+template <int RB>
+__device__ inline void tile_store_gelu(const floatx4 (&acc)[RB][2], const float* __restrict__ bias,
+                                       const float4 (&add)[RB][2], _Float16* S, const float* gtab) {
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, r = lane & 15, g = lane >> 4;
+#pragma unroll
+  for (int nt = 0; nt < 2; ++nt) {
+    const int c0 = 32 * wave + 16 * nt + 4 * g;
+    const float4 bv = *reinterpret_cast<const float4*>(bias + c0);
+#pragma unroll
+    for (int rb = 0; rb < RB; ++rb) {
+      const float4 a = add[rb][nt];
+      const float4 v = make_float4(gelu_poly(acc[rb][nt][0] + a.x + bv.x, gtab), gelu_poly(acc[rb][nt][1] + a.y + bv.y, gtab),
+                                   gelu_poly(acc[rb][nt][2] + a.z + bv.z, gtab), gelu_poly(acc[rb][nt][3] + a.w + bv.w, gtab));
+      put_split4(S, 16 * RB, kLdS1, 16 * rb + r, c0, v);
+    }
+  }
+}
+
+// Two-pass LayerNorm (fp32, eps 1e-5) of each tile row, in place: a row's 128
+// columns are spread over the four waves, which exchange per-row partial
+// sums through stat[4][16 RB]. Ends with a barrier.
+template <int RB>
+__device__ inline void tile_layer_norm(floatx4 (&acc)[RB][2], const float* __restrict__ gam,
+                                       const float* __restrict__ bet, float (*stat)[16 * RB]) {
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, r = lane & 15, g = lane >> 4;
+  float mean[RB], inv[RB];
+#pragma unroll
+  for (int pass = 0; pass < 2; ++pass) {
+#pragma unroll
+    for (int rb = 0; rb < RB; ++rb) {
+      float v = 0.0F;
+#pragma unroll
+      for (int nt = 0; nt < 2; ++nt)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const float d = pass == 0 ? acc[rb][nt][i] : acc[rb][nt][i] - mean[rb];
+          v += pass == 0 ? d : d * d;
+        }
+      v += __shfl_xor(v, 16, 64);
+      v += __shfl_xor(v, 32, 64);
+      if (g == 0) stat[wave][16 * rb + r] = v;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int rb = 0; rb < RB; ++rb) {
+      const int row = 16 * rb + r;
+      const float t = ((stat[0][row] + stat[1][row]) + stat[2][row]) + stat[3][row];
+      if (pass == 0) mean[rb] = t * (1.0F / 128.0F);
+      else inv[rb] = 1.0F / sqrtf(t * (1.0F / 128.0F) + 1.0e-5F);
+    }
+    __syncthreads();
+  }
+#pragma unroll
+  for (int nt = 0; nt < 2; ++nt) {
+    const int c0 = 32 * wave + 16 * nt + 4 * g;
+    const float4 gm = *reinterpret_cast<const float4*>(gam + c0);
+    const float4 bt = *reinterpret_cast<const float4*>(bet + c0);
+#pragma unroll
+    for (int rb = 0; rb < RB; ++rb) {
+      acc[rb][nt][0] = (acc[rb][nt][0] - mean[rb]) * inv[rb] * gm.x + bt.x;
+      acc[rb][nt][1] = (acc[rb][nt][1] - mean[rb]) * inv[rb] * gm.y + bt.y;
+      acc[rb][nt][2] = (acc[rb][nt][2] - mean[rb]) * inv[rb] * gm.z + bt.z;
+      acc[rb][nt][3] = (acc[rb][nt][3] - mean[rb]) * inv[rb] * gm.w + bt.w;
+    }
+  }
+}
+
 // Two-pass LayerNorm (fp32, eps 1e-5) of the 4 rows a lane holds in acc[8]
 // (all 128 columns of the row live in the 16 lanes of its group).
 __device__ inline void ln_acc(floatx4 (&acc)[8], const float* __restrict__ gam, const float* __restrict__ bet) {
@@ -164,134 +352,135 @@ __device__ inline void ln_acc(floatx4 (&acc)[8], const float* __restrict__ gam, 
   }
 }
 
-// The wave's 16 slab rows [h_e[slot] | h_v[j]] with slot = slot_of(row)
-// (negative: a zero row) and j = idx[slot] (outside [0, L): a zero h_j
-// block).
-template <typename SlotOf>
-__device__ inline void build_rows(float* A, const float* __restrict__ h_v, const float* __restrict__ h_e,
-                                  const int32_t* __restrict__ idx, int L, int K, SlotOf slot_of) {
-  const int lane = threadIdx.x & 63;
-  for (int t = lane; t < 16 * 64; t += 64) {
-    const int row = t / 64, c4 = t % 64, part = c4 / 32, col = 4 * (c4 % 32);
-    const long long slot = slot_of(row);
-    float4 v = make_float4(0.F, 0.F, 0.F, 0.F);
-    if (slot >= 0) {
-      if (part == 0) {
-        v = *reinterpret_cast<const float4*>(h_e + (size_t)slot * kH + col);
-      } else {
-        const int j = idx[slot];
-        if (j >= 0 && j < L) v = *reinterpret_cast<const float4*>(h_v + (size_t)j * kH + col);
-      }
-    }
-    *reinterpret_cast<float4*>(A + row * kLdA + part * kH + col) = v;
-  }
-}
-
-__global__ __launch_bounds__(128) void edge_embed16_kernel(ModelDev m, const float* __restrict__ coords,
-                                                           const uint8_t* __restrict__ src,
-                                                           const int32_t* __restrict__ resid,
-                                                           const int32_t* __restrict__ chain,
-                                                           const int32_t* __restrict__ idx, int L, int K,
-                                                           float* __restrict__ h_e) {
-  __shared__ __attribute__((aligned(16))) float slab[2][16 * kLdX];
+// 64 consecutive edge slots per workgroup: one tile of 4 row blocks. The 416
+// features are built in two parts (feature chunks 0 .. 13, then 14 .. 25, 16
+// features each) so that the split slab holds 224 inputs at a time.
+constexpr int kEmbedChunks0 = 14;
+constexpr int kLdE = 16 * kEmbedChunks0 + 8;  // halves per slab row of the first part
+__global__ __launch_bounds__(kTileThreads, 2) void edge_embed16_kernel(ModelDev m, const float* __restrict__ coords,
+                                                                       const uint8_t* __restrict__ src,
+                                                                       const int32_t* __restrict__ resid,
+                                                                       const int32_t* __restrict__ chain,
+                                                                       const int32_t* __restrict__ idx, int L, int K,
+                                                                       float* __restrict__ h_e) {
+  constexpr int RB = 4, R = 16 * RB;
+  static_assert(kEdgeIn == 26 * 16 && kLdE >= kLdS1, "feature chunks");
+  __shared__ __attribute__((aligned(16))) _Float16 S[2 * R * kLdE];
+  __shared__ float stat[4][R];
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, r = lane & 15, g = lane >> 4;
-  const size_t S = (size_t)L * K;
-  const size_t base = (size_t)blockIdx.x * 32 + 16 * wave;
-  float* A = slab[wave];
-  for (int t = lane; t < 16 * 26; t += 64) {
-    const int row = t & 15, c = t >> 4;
-    const size_t slot = base + row;
-    const int j = slot < S ? idx[slot] : -1;
-    const int res = slot < S ? static_cast<int>(slot / K) : 0;
-    float out[16];
-    edge_chunk(m, coords, src, resid, chain, L, res, j, c, out);  // zeros when j is not a residue
+  const int n0 = 32 * wave;
+  const long long S_ = (long long)L * K;
+  const long long base = (long long)blockIdx.x * R;
+  floatx4 acc[RB][2];
+  // features of chunks [c0, c0 + nc) of the tile's rows into the split slab
+  auto build = [&](int c0, int nc) {
+    for (int t = threadIdx.x; t < R * nc; t += kTileThreads) {
+      const int row = t % R, c = c0 + t / R;
+      const long long slot = base + row;
+      const int j = slot < S_ ? idx[slot] : -1;
+      const int res = slot < S_ ? static_cast<int>(slot / K) : 0;
+      float out[16];
+      edge_chunk(m, coords, src, resid, chain, L, res, j, c, out);  // zeros when j is not a residue
 #pragma unroll
-    for (int f = 0; f < 16; ++f) A[row * kLdX + 16 * c + f] = out[f];
-  }
+      for (int q = 0; q < 4; ++q)
+        put_split4(S, R, kLdE, row, 16 * (c - c0) + 4 * q,
+                   make_float4(out[4 * q], out[4 * q + 1], out[4 * q + 2], out[4 * q + 3]));
+    }
+    __syncthreads();
+  };
+  constexpr int kC1 = 26 - kEmbedChunks0;
+  build(0, kEmbedChunks0);
+  tile_gemm<RB, 16 * kEmbedChunks0>(S, kLdE, m.enc16.Wedge, n0, (size_t)kEdgeIn * kH, acc);
+  __syncthreads();  // every wave is done with the first part
+  build(kEmbedChunks0, kC1);
+  tile_gemm<RB, 16 * kC1>(S, kLdE, m.enc16.Wedge + (size_t)(2 * kEmbedChunks0) * kH * 8, n0, (size_t)kEdgeIn * kH,
+                          acc, true);
+  tile_layer_norm<RB>(acc, m.ne_g, m.ne_b, stat);
+#pragma unroll
+  for (int nt = 0; nt < 2; ++nt)
+#pragma unroll
+    for (int rb = 0; rb < RB; ++rb)
+      put_split4(S, R, kLdS1, 16 * rb + r, n0 + 16 * nt + 4 * g,
+                 make_float4(acc[rb][nt][0], acc[rb][nt][1], acc[rb][nt][2], acc[rb][nt][3]));
   __syncthreads();
-  floatx4 acc[8];
-  wave_gemm<8>(A, kLdX, m.enc16.Wedge, kH, 0, kEdgeIn, acc);
-  ln_acc(acc, m.ne_g, m.ne_b);
-  __syncthreads();
+  tile_gemm<RB, kH>(S, kLdS1, m.enc16.We, n0, (size_t)kH * kH, acc);
 #pragma unroll
-  for (int nt = 0; nt < 8; ++nt)
+  for (int rb = 0; rb < RB; ++rb) {
+    const long long slot = base + 16 * rb + r;
+    if (slot >= S_) continue;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) A[(4 * g + i) * kLdH + 16 * nt + r] = acc[nt][i];
-  __syncthreads();
-  wave_gemm<8>(A, kLdH, m.enc16.We, kH, 0, kH, acc);
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const size_t slot = base + 4 * g + i;
-    if (slot >= S) continue;
-#pragma unroll
-    for (int nt = 0; nt < 8; ++nt) {
-      const int col = 16 * nt + r;
-      h_e[slot * kH + col] = acc[nt][i] + m.We_b[col];
+    for (int nt = 0; nt < 2; ++nt) {
+      const int c0 = n0 + 16 * nt + 4 * g;
+      const float4 bv = *reinterpret_cast<const float4*>(m.We_b + c0);
+      *reinterpret_cast<float4*>(h_e + (size_t)slot * kH + c0) =
+          make_float4(acc[rb][nt][0] + bv.x, acc[rb][nt][1] + bv.y, acc[rb][nt][2] + bv.z, acc[rb][nt][3] + bv.w);
     }
   }
 }
 
-// One residue per workgroup: wave w holds its slots 16 w .. 16 w + 15.
-__global__ __launch_bounds__(192) void edge_msg16_kernel(EncLayerDev w, Enc16LayerDev w16,
-                                                         const float* __restrict__ h_e, const float* __restrict__ h_v,
-                                                         const int32_t* __restrict__ idx,
-                                                         const float* __restrict__ mask,
-                                                         const float* __restrict__ prefix, int L, int K,
-                                                         float* __restrict__ upd) {
-  __shared__ __attribute__((aligned(16))) float slab[3][16 * kLdA];
-  __shared__ float tbl[17];
-  __shared__ float part[3][kH];
+// One residue per workgroup: its 48 slots as one tile of 3 row blocks.
+__global__ __launch_bounds__(kTileThreads, 3) void edge_msg16_kernel(EncLayerDev w, Enc16LayerDev w16,
+                                                                  const float* __restrict__ h_e,
+                                                                  const float* __restrict__ h_v,
+                                                                  const int32_t* __restrict__ idx,
+                                                                  const float* __restrict__ mask,
+                                                                  const float* __restrict__ prefix, int L, int K,
+                                                                  float* __restrict__ upd) {
+  constexpr int RB = 3;
+  __shared__ __attribute__((aligned(16))) _Float16 S[2 * 16 * RB * kLdS2];
+  __shared__ __attribute__((aligned(16))) float gtab[kGeluPolyRows * 8];
   const int res = blockIdx.x;
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, r = lane & 15, g = lane >> 4;
-  if (threadIdx.x < 17) tbl[threadIdx.x] = kExpNegTable[threadIdx.x];
-  float* A = slab[wave];
-  build_rows(A, h_v, h_e, idx, L, K, [&](int row) -> long long {
-    const int k = 16 * wave + row;
-    return k < K ? (long long)res * K + k : -1;
-  });
+  const int n0 = 32 * wave;
+  for (int i = threadIdx.x; i < kGeluPolyRows * 8; i += kTileThreads) gtab[i] = kGeluPoly[i];
+  tile_rows<RB>(S, h_v, h_e, idx, L, [&](int row) -> long long { return row < K ? (long long)res * K + row : -1; });
+  // weight of slot 16 rb + r in the neighbour sum: mask_i mask_j / 30 for a valid slot
+  float alpha[RB];
+#pragma unroll
+  for (int rb = 0; rb < RB; ++rb) {
+    const int k = 16 * rb + r;
+    const int j = k < K ? idx[(size_t)res * K + k] : -1;
+    alpha[rb] = (j >= 0 && j < L) ? mask[res] * mask[j] * (1.0F / 30.0F) : 0.0F;
+  }
+  float4 add[RB][2];
+#pragma unroll
+  for (int nt = 0; nt < 2; ++nt) {
+    const float4 pv = *reinterpret_cast<const float4*>(prefix + (size_t)res * 256 + kH + n0 + 16 * nt + 4 * g);
+#pragma unroll
+    for (int rb = 0; rb < RB; ++rb) add[rb][nt] = pv;
+  }
   __syncthreads();
-  floatx4 acc[8];
+  floatx4 acc[RB][2];
   // rows 128 .. 383 of W1 (packed k-blocks 16 ..) over [e_ij | h_j], plus the h_i prefix
-  wave_gemm<8>(A, kLdA, w16.W1 + (size_t)16 * kH * 8, kH, 0, 2 * kH, acc, (size_t)3 * kH * kH);
+  tile_gemm<RB, 2 * kH>(S, kLdS2, w16.W1 + (size_t)16 * kH * 8, n0, (size_t)3 * kH * kH, acc);
+  __syncthreads();  // every wave is done with [e_ij | h_j]
+  tile_store_gelu<RB>(acc, w.b1, add, S, gtab);
+  __syncthreads();
+  tile_gemm<RB, kH>(S, kLdS1, w16.W2, n0, (size_t)kH * kH, acc);
 #pragma unroll
-  for (int nt = 0; nt < 8; ++nt) {
-    const float pv = prefix[(size_t)res * 256 + kH + 16 * nt + r];
+  for (int nt = 0; nt < 2; ++nt)
 #pragma unroll
-    for (int i = 0; i < 4; ++i) acc[nt][i] += pv;
-  }
+    for (int rb = 0; rb < RB; ++rb) add[rb][nt] = make_float4(0.F, 0.F, 0.F, 0.F);
   __syncthreads();
-  store_gelu<8>(acc, w.b1, 0, A, kLdH, tbl);
+  tile_store_gelu<RB>(acc, w.b2, add, S, gtab);
   __syncthreads();
-  wave_gemm<8>(A, kLdH, w16.W2, kH, 0, kH, acc);
-  __syncthreads();
-  store_gelu<8>(acc, w.b2, 0, A, kLdH, tbl);
-  __syncthreads();
-  wave_gemm<8>(A, kLdH, w16.W3, kH, 0, kH, acc);
-  // upd = sum over valid slots of (mask_i mask_j / 30) (W3 g + b3)
-  float alpha[4];
+  tile_gemm<RB, kH>(S, kLdS1, w16.W3, n0, (size_t)kH * kH, acc);
+  // upd[col] = sum over the residue's valid slots of (mask_i mask_j / 30) (W3 g + b3)
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int k = 16 * wave + 4 * g + i;
-    alpha[i] = 0.0F;
-    if (k < K) {
-      const int j = idx[(size_t)res * K + k];
-      if (j >= 0 && j < L) alpha[i] = mask[res] * mask[j] * (1.0F / 30.0F);
+  for (int nt = 0; nt < 2; ++nt) {
+    const int c0 = n0 + 16 * nt + 4 * g;
+    const float4 bv = *reinterpret_cast<const float4*>(w.b3 + c0);
+    float sv[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const float b = i == 0 ? bv.x : i == 1 ? bv.y : i == 2 ? bv.z : bv.w;
+      float v = 0.0F;
+#pragma unroll
+      for (int rb = 0; rb < RB; ++rb) v += alpha[rb] * (acc[rb][nt][i] + b);
+      sv[i] = sum16(v);
     }
+    if (r == 0) *reinterpret_cast<float4*>(upd + (size_t)res * kH + c0) = make_float4(sv[0], sv[1], sv[2], sv[3]);
   }
-#pragma unroll
-  for (int nt = 0; nt < 8; ++nt) {
-    const int col = 16 * nt + r;
-    const float bv = w.b3[col];
-    float s = 0.0F;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) s += alpha[i] * (acc[nt][i] + bv);
-    s += __shfl_xor(s, 16, 64);
-    s += __shfl_xor(s, 32, 64);
-    if (g == 0) part[wave][col] = s;
-  }
-  __syncthreads();
-  if (threadIdx.x < kH)
-    upd[(size_t)res * kH + threadIdx.x] = (part[0][threadIdx.x] + part[1][threadIdx.x]) + part[2][threadIdx.x];
 }
 
 // 16 residues per workgroup of four waves; lane (r, g) of a wave holds rows
@@ -379,56 +568,79 @@ __global__ __launch_bounds__(256) void node16_kernel(EncLayerDev w, Enc16LayerDe
   }
 }
 
-__global__ __launch_bounds__(128) void edge_update16_kernel(EncLayerDev w, Enc16LayerDev w16, float* __restrict__ h_e,
-                                                            const float* __restrict__ h_v,
-                                                            const int32_t* __restrict__ idx,
-                                                            const float* __restrict__ prefix, int L, int K) {
-  __shared__ __attribute__((aligned(16))) float slab[2][16 * kLdA];
-  __shared__ float tbl[17];
+// 64 consecutive edge slots per workgroup: one tile of 4 row blocks.
+__global__ __launch_bounds__(kTileThreads, 2) void edge_update16_kernel(EncLayerDev w, Enc16LayerDev w16,
+                                                                     float* __restrict__ h_e,
+                                                                     const float* __restrict__ h_v,
+                                                                     const int32_t* __restrict__ idx,
+                                                                     const float* __restrict__ prefix, int L, int K) {
+  constexpr int RB = 4;
+  __shared__ __attribute__((aligned(16))) _Float16 S[2 * 16 * RB * kLdS2];
+  __shared__ float stat[4][16 * RB];
+  __shared__ __attribute__((aligned(16))) float gtab[kGeluPolyRows * 8];
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, r = lane & 15, g = lane >> 4;
-  if (threadIdx.x < 17) tbl[threadIdx.x] = kExpNegTable[threadIdx.x];
-  const long long S = (long long)L * K;
-  const long long base = (long long)blockIdx.x * 32 + 16 * wave;
-  float* A = slab[wave];
-  build_rows(A, h_v, h_e, idx, L, K, [&](int row) -> long long { return base + row < S ? base + row : -1; });
-  __syncthreads();
-  floatx4 acc[8];
-  wave_gemm<8>(A, kLdA, w16.W11 + (size_t)16 * kH * 8, kH, 0, 2 * kH, acc, (size_t)3 * kH * kH);
+  const int n0 = 32 * wave;
+  for (int i = threadIdx.x; i < kGeluPolyRows * 8; i += kTileThreads) gtab[i] = kGeluPoly[i];
+  const long long S_ = (long long)L * K;
+  const long long base = (long long)blockIdx.x * 16 * RB;
+  tile_rows<RB>(S, h_v, h_e, idx, L, [&](int row) -> long long { return base + row < S_ ? base + row : -1; });
+  float4 add[RB][2];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const long long slot = base + 4 * g + i;
-    const size_t res = slot < S ? (size_t)(slot / K) : 0;
+  for (int rb = 0; rb < RB; ++rb) {
+    const long long slot = base + 16 * rb + r;
+    const size_t res = slot < S_ ? (size_t)(slot / K) : 0;
 #pragma unroll
-    for (int nt = 0; nt < 8; ++nt) acc[nt][i] += prefix[res * 256 + 16 * nt + r];
+    for (int nt = 0; nt < 2; ++nt)
+      add[rb][nt] = *reinterpret_cast<const float4*>(prefix + res * 256 + n0 + 16 * nt + 4 * g);
   }
   __syncthreads();
-  store_gelu<8>(acc, w.b11, 0, A, kLdH, tbl);
+  floatx4 acc[RB][2];
+  tile_gemm<RB, 2 * kH>(S, kLdS2, w16.W11 + (size_t)16 * kH * 8, n0, (size_t)3 * kH * kH, acc);
   __syncthreads();
-  wave_gemm<8>(A, kLdH, w16.W12, kH, 0, kH, acc);
+  tile_store_gelu<RB>(acc, w.b11, add, S, gtab);
   __syncthreads();
-  store_gelu<8>(acc, w.b12, 0, A, kLdH, tbl);
-  __syncthreads();
-  wave_gemm<8>(A, kLdH, w16.W13, kH, 0, kH, acc);
-  // x = e + (W13 g + b13), LN3, written for slots with a valid neighbour
+  tile_gemm<RB, kH>(S, kLdS1, w16.W12, n0, (size_t)kH * kH, acc);
+  // the residual e rows load during the last two products
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const long long slot = base + 4 * g + i;
+  for (int rb = 0; rb < RB; ++rb) {
+    const long long slot = base + 16 * rb + r;
 #pragma unroll
-    for (int nt = 0; nt < 8; ++nt) {
-      const int col = 16 * nt + r;
-      const float e = slot < S ? h_e[(size_t)slot * kH + col] : 0.0F;
-      acc[nt][i] = e + (acc[nt][i] + w.b13[col]);
+    for (int nt = 0; nt < 2; ++nt)
+      add[rb][nt] = slot < S_ ? *reinterpret_cast<const float4*>(h_e + (size_t)slot * kH + n0 + 16 * nt + 4 * g)
+                              : make_float4(0.F, 0.F, 0.F, 0.F);
+  }
+  const float4 zero[RB][2] = {};
+  __syncthreads();
+  tile_store_gelu<RB>(acc, w.b12, zero, S, gtab);
+  __syncthreads();
+  tile_gemm<RB, kH>(S, kLdS1, w16.W13, n0, (size_t)kH * kH, acc);
+  // x = e + (W13 g + b13), then LN3 over each row's 128 columns (four waves)
+#pragma unroll
+  for (int nt = 0; nt < 2; ++nt) {
+    const int c0 = n0 + 16 * nt + 4 * g;
+    const float4 bv = *reinterpret_cast<const float4*>(w.b13 + c0);
+#pragma unroll
+    for (int rb = 0; rb < RB; ++rb) {
+      const float4 e = add[rb][nt];
+      acc[rb][nt][0] = e.x + (acc[rb][nt][0] + bv.x);
+      acc[rb][nt][1] = e.y + (acc[rb][nt][1] + bv.y);
+      acc[rb][nt][2] = e.z + (acc[rb][nt][2] + bv.z);
+      acc[rb][nt][3] = e.w + (acc[rb][nt][3] + bv.w);
     }
   }
-  ln_acc(acc, w.n3g, w.n3b);
+  tile_layer_norm<RB>(acc, w.n3g, w.n3b, stat);
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const long long slot = base + 4 * g + i;
-    if (slot >= S) continue;
+  for (int rb = 0; rb < RB; ++rb) {
+    const long long slot = base + 16 * rb + r;
+    if (slot >= S_) continue;
     const int j = idx[slot];
     if (j < 0 || j >= L) continue;
 #pragma unroll
-    for (int nt = 0; nt < 8; ++nt) h_e[(size_t)slot * kH + 16 * nt + r] = acc[nt][i];
+    for (int nt = 0; nt < 2; ++nt) {
+      const int c0 = n0 + 16 * nt + 4 * g;
+      *reinterpret_cast<float4*>(h_e + (size_t)slot * kH + c0) =
+          make_float4(acc[rb][nt][0], acc[rb][nt][1], acc[rb][nt][2], acc[rb][nt][3]);
+    }
   }
 }
 
@@ -440,20 +652,21 @@ hipError_t launch_encoder16(const ModelDev& m, const float* coords, const uint8_
   if (L <= 0) return hipSuccess;
   if (K < 1 || K > kKmax) return hipErrorInvalidValue;
   const size_t S = (size_t)L * K;
-  const unsigned tiles = (unsigned)((S + 31) / 32);
+  const unsigned tiles64 = (unsigned)((S + 63) / 64);
   hipError_t e = launch_zero(h_v, (size_t)L * kH, stream);
   if (e != hipSuccess) return e;
-  edge_embed16_kernel<<<tiles, 128, 0, stream>>>(m, coords, atom_src, resid, chain, idx, L, K, h_e);
+  edge_embed16_kernel<<<tiles64, kTileThreads, 0, stream>>>(m, coords, atom_src, resid, chain, idx, L, K, h_e);
   e = launch_zero(ws.prefix, (size_t)L * 256, stream);  // layer 0: h = 0, so its W1 prefix is 0
   if (e != hipSuccess) return e;
   float* upd = ws.msg;  // [L][128] neighbour sums (the [S][128] message buffer is otherwise unused here)
   for (int l = 0; l < kLayers; ++l) {
     const Enc16LayerDev& w16 = m.enc16.layer[l];
     const uint16_t* W1_next = l + 1 < kLayers ? m.enc16.layer[l + 1].W1 : nullptr;
-    edge_msg16_kernel<<<(unsigned)L, 192, 0, stream>>>(m.enc[l], w16, h_e, h_v, idx, mask, ws.prefix, L, K, upd);
+    edge_msg16_kernel<<<(unsigned)L, kTileThreads, 0, stream>>>(m.enc[l], w16, h_e, h_v, idx, mask, ws.prefix, L, K,
+                                                                 upd);
     node16_kernel<<<(unsigned)((L + 15) / 16), 256, 0, stream>>>(m.enc[l], w16, upd, mask, L, h_v, W1_next,
                                                                 ws.prefix);
-    edge_update16_kernel<<<tiles, 128, 0, stream>>>(m.enc[l], w16, h_e, h_v, idx, ws.prefix, L, K);
+    edge_update16_kernel<<<tiles64, kTileThreads, 0, stream>>>(m.enc[l], w16, h_e, h_v, idx, ws.prefix, L, K);
   }
   return hipGetLastError();
 }
