@@ -187,6 +187,8 @@ __global__ __launch_bounds__(256) void tf_node_kernel(ModelDev m, int layer, con
   __shared__ __attribute__((aligned(16))) float A[16 * kLd];
   __shared__ __attribute__((aligned(16))) float X[16 * kLd];
   __shared__ __attribute__((aligned(16))) float F[16 * kLdF];
+  __shared__ float tbl[17];
+  if (threadIdx.x < 17) tbl[threadIdx.x] = kExpNegTable[threadIdx.x];
   const DecLayerDev& w = m.dec[layer];
   const int r0 = blockIdx.x * 16;
   const int wave = threadIdx.x >> 6;
@@ -228,7 +230,7 @@ __global__ __launch_bounds__(256) void tf_node_kernel(ModelDev m, int layer, con
       for (int i = 0; i < 4; ++i) {
         const int row = 4 * (lane >> 4) + i;
         const int col = wave * 128 + nb * 16 + (lane & 15);
-        F[row * kLdF + col] = gelu(acc[0][nb][i] + w.bin[col]);
+        F[row * kLdF + col] = gelu(acc[0][nb][i] + w.bin[col], tbl);
       }
   }
   __syncthreads();

@@ -36,8 +36,10 @@ __device__ __constant__ static const float kExpNegTable[17] = {
     0.00000011253517471F,
 };
 
-// Table + degree-6 Taylor approximation of exp(x) on [-16, 0].
-__device__ inline float fast_exp_neg(float x) {
+// Table + degree-6 Taylor approximation of exp(x) on [-16, 0]; tbl holds the
+// 17 values of kExpNegTable (an LDS copy in kernels that call it often: a
+// per-lane index into __constant__ memory becomes a vector memory gather).
+__device__ inline float fast_exp_neg(float x, const float* tbl = kExpNegTable) {
 #pragma clang fp contract(off)
   if (x != x) return x;
   float neg_x = -x;
@@ -52,7 +54,7 @@ __device__ inline float fast_exp_neg(float x) {
            r * (0.5F +
                 r * (1.0F / 6.0F +
                      r * (1.0F / 24.0F + r * (1.0F / 120.0F + r * (1.0F / 720.0F))))));
-  return kExpNegTable[n] * e;
+  return tbl[n] * e;
 }
 
 // 1 / y for y in [1, 2.32] (the range of 1 + p v below), correctly rounded:
@@ -73,7 +75,7 @@ __device__ inline float recip_unit_range(float y) {
 // checks do nothing; for v > 4 the value is selected away. The result equals
 // the reference expression bit for bit for every float x (a GPU test compares
 // all 2^32 inputs with the branching form).
-__device__ inline float gelu(float x) {
+__device__ inline float gelu(float x, const float* tbl = kExpNegTable) {  // tbl: as for fast_exp_neg
 #pragma clang fp contract(off)
   const float vs = x * 0.7071067811865475F;
   const float v = fabsf(vs);
@@ -85,7 +87,7 @@ __device__ inline float gelu(float x) {
   const float r = -(q - static_cast<float>(n));
   const float e =
       1.0F + r * (1.0F + r * (0.5F + r * (1.0F / 6.0F + r * (1.0F / 24.0F + r * (1.0F / 120.0F + r * (1.0F / 720.0F))))));
-  const float mag = 1.0F - poly * (kExpNegTable[n] * e);
+  const float mag = 1.0F - poly * (tbl[n] * e);
   const float erfv = __builtin_copysignf(v > 4.0F ? 1.0F : mag, vs);
   return 0.5F * x * (1.0F + erfv);
 }

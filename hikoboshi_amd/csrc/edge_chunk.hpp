@@ -13,42 +13,30 @@ __device__ __constant__ static const int8_t kPairQ[25] = {1, 0, 2, 3, 4, 1, 1, 1
 __device__ __constant__ static const int8_t kPairN[25] = {1, 0, 2, 3, 4, 0, 2, 3, 4, 2, 3, 4, 2,
                                                           3, 2, 1, 1, 1, 1, 0, 0, 0, 4, 4, 3};
 
-// Writes the 16 features of chunk c (0 = positional, 1..25 = atom pair c-1)
-// of edge slot (r, j) to out[0..16).
-__device__ inline void edge_chunk(const ModelDev& m, const float* __restrict__ coords,
-                                  const uint8_t* __restrict__ src, const int32_t* __restrict__ resid,
-                                  const int32_t* __restrict__ chain, int L, int r, int j, int c,
-                                  float* out) {
+// The 16 positional features of class cls (chain break: kPosClasses - 1).
+__device__ inline void positional_chunk(const ModelDev& m, int cls, float* out) {
 #pragma clang fp contract(off)
-  if (j < 0 || j >= L) {
 #pragma unroll
-    for (int f = 0; f < 16; ++f) out[f] = 0.0F;
-    return;
-  }
-  if (c == 0) {
-    int cls;
-    const int ci = chain ? chain[r] : 0;
-    const int cj = chain ? chain[j] : 0;
-    if (ci != cj) {
-      cls = kPosClasses - 1;
-    } else {
-      int off = (resid ? resid[r] : r) - (resid ? resid[j] : j);
-      off = off < -32 ? -32 : (off > 32 ? 32 : off);
-      cls = off + 32;
-    }
-#pragma unroll
-    for (int d = 0; d < 16; ++d) out[d] = m.pos_w[d * kPosClasses + cls] + m.pos_b[d];
-    return;
-  }
-  const int p = c - 1;
-  const int qa = kPairQ[p], na = kPairN[p];
-  if (src[(size_t)r * 5 + qa] == 0 || src[(size_t)j * 5 + na] == 0) {
-#pragma unroll
-    for (int f = 0; f < 16; ++f) out[f] = 0.0F;
-    return;
-  }
-  const float* qx = coords + ((size_t)r * 5 + qa) * 3;
-  const float* nx = coords + ((size_t)j * 5 + na) * 3;
+  for (int d = 0; d < 16; ++d) out[d] = m.pos_w[d * kPosClasses + cls] + m.pos_b[d];
+}
+
+// Positional class of edge (r, j): kPosClasses - 1 across chains, else the
+// residue-index offset clamped to [-32, 32], shifted by 32.
+__device__ inline int positional_class(const int32_t* __restrict__ resid, const int32_t* __restrict__ chain, int r,
+                                       int j) {
+  const int ci = chain ? chain[r] : 0;
+  const int cj = chain ? chain[j] : 0;
+  if (ci != cj) return kPosClasses - 1;
+  int off = (resid ? resid[r] : r) - (resid ? resid[j] : j);
+  off = off < -32 ? -32 : (off > 32 ? 32 : off);
+  return off + 32;
+}
+
+// The 16 RBF features of the distance between atoms at qx and nx (3 floats
+// each), in the reference's operation order; tbl is the exp table
+// (kExpNegTable or a copy of it in LDS).
+__device__ inline void rbf_chunk(const float* qx, const float* nx, float* out, const float* tbl) {
+#pragma clang fp contract(off)
   float sq = 0.0F;
 #pragma unroll
   for (int ax = 0; ax < 3; ++ax) {
@@ -64,8 +52,33 @@ __device__ inline void edge_chunk(const ModelDev& m, const float* __restrict__ c
   for (int f = 0; f < 16; ++f) {
     const float center = 2.0F + static_cast<float>(f) * center_step;
     const float delta = dist - center;
-    out[f] = fast_exp_neg(-(delta * delta) / two_sigma_sq);
+    out[f] = fast_exp_neg(-(delta * delta) / two_sigma_sq, tbl);
   }
+}
+
+// Writes the 16 features of chunk c (0 = positional, 1..25 = atom pair c-1)
+// of edge slot (r, j) to out[0..16); tbl as for rbf_chunk.
+__device__ inline void edge_chunk(const ModelDev& m, const float* __restrict__ coords,
+                                  const uint8_t* __restrict__ src, const int32_t* __restrict__ resid,
+                                  const int32_t* __restrict__ chain, int L, int r, int j, int c,
+                                  float* out, const float* tbl = kExpNegTable) {
+  if (j < 0 || j >= L) {
+#pragma unroll
+    for (int f = 0; f < 16; ++f) out[f] = 0.0F;
+    return;
+  }
+  if (c == 0) {
+    positional_chunk(m, positional_class(resid, chain, r, j), out);
+    return;
+  }
+  const int p = c - 1;
+  const int qa = kPairQ[p], na = kPairN[p];
+  if (src[(size_t)r * 5 + qa] == 0 || src[(size_t)j * 5 + na] == 0) {
+#pragma unroll
+    for (int f = 0; f < 16; ++f) out[f] = 0.0F;
+    return;
+  }
+  rbf_chunk(coords + ((size_t)r * 5 + qa) * 3, coords + ((size_t)j * 5 + na) * 3, out, tbl);
 }
 
 }  // namespace hkbs

@@ -65,6 +65,8 @@ __global__ __launch_bounds__(256) void edge_msg_kernel(EncLayerDev w, const floa
 #pragma clang fp contract(off)
   __shared__ __attribute__((aligned(16))) float A[kH * kLdE];
   __shared__ __attribute__((aligned(16))) float Wbuf[2 * kKC * kH];
+  __shared__ float tbl[17];
+  if (threadIdx.x < 17) tbl[threadIdx.x] = kExpNegTable[threadIdx.x];
   const size_t S = (size_t)L * K;
   const size_t slot0 = (size_t)blockIdx.x * kRows;
   const int n_rows = (int)min((size_t)kRows, S - slot0);
@@ -93,7 +95,7 @@ __global__ __launch_bounds__(256) void edge_msg_kernel(EncLayerDev w, const floa
   for (int i = 0; i < kEdgeRM; ++i)
 #pragma unroll
     for (int j = 0; j < kEdgeCN; ++j) {
-      A[(col0 + j) * kLdE + row0 + i] = (row0 + i < n_rows) ? gelu(acc[i][j] + w.b1[col0 + j]) : 0.0F;
+      A[(col0 + j) * kLdE + row0 + i] = (row0 + i < n_rows) ? gelu(acc[i][j] + w.b1[col0 + j], tbl) : 0.0F;
       acc[i][j] = 0.0F;
     }
   seq_gemm<kEdgeRM, kEdgeCN, kH, kKC>(acc, A, kLdE, row0, w.W2_t, kH, kH, Wbuf, col0);
@@ -101,7 +103,7 @@ __global__ __launch_bounds__(256) void edge_msg_kernel(EncLayerDev w, const floa
   for (int i = 0; i < kEdgeRM; ++i)
 #pragma unroll
     for (int j = 0; j < kEdgeCN; ++j) {
-      A[(col0 + j) * kLdE + row0 + i] = (row0 + i < n_rows) ? gelu(acc[i][j] + w.b2[col0 + j]) : 0.0F;
+      A[(col0 + j) * kLdE + row0 + i] = (row0 + i < n_rows) ? gelu(acc[i][j] + w.b2[col0 + j], tbl) : 0.0F;
       acc[i][j] = 0.0F;
     }
   seq_gemm<kEdgeRM, kEdgeCN, kH, kKC>(acc, A, kLdE, row0, w.W3_t, kH, kH, Wbuf, col0);
@@ -175,6 +177,8 @@ __global__ __launch_bounds__(256) void node_kernel(EncLayerDev w, const float* _
   __shared__ __attribute__((aligned(16))) float H1[kH * NR];
   __shared__ __attribute__((aligned(16))) float F[kFF * NR];
   __shared__ __attribute__((aligned(16))) float H2[kH * NR];
+  __shared__ float tbl[17];
+  if (threadIdx.x < 17) tbl[threadIdx.x] = kExpNegTable[threadIdx.x];
   const int r0 = blockIdx.x * NR;
   const int nr = min(NR, L - r0);
   const int t = threadIdx.x;
@@ -239,7 +243,7 @@ __global__ __launch_bounds__(256) void node_kernel(EncLayerDev w, const float* _
 #pragma unroll
     for (int j = 0; j < 2; ++j)
 #pragma unroll
-      for (int r = 0; r < NR; ++r) F[(t + 256 * j) * NR + r] = gelu(acc[j][r] + w.bin[t + 256 * j]);
+      for (int r = 0; r < NR; ++r) F[(t + 256 * j) * NR + r] = gelu(acc[j][r] + w.bin[t + 256 * j], tbl);
   }
   __syncthreads();
   {
@@ -285,6 +289,8 @@ __global__ __launch_bounds__(256) void edge_update_kernel(EncLayerDev w, float* 
 #pragma clang fp contract(off)
   __shared__ __attribute__((aligned(16))) float A[kH * kLdE];
   __shared__ __attribute__((aligned(16))) float Wbuf[2 * kKC * kH];
+  __shared__ float tbl[17];
+  if (threadIdx.x < 17) tbl[threadIdx.x] = kExpNegTable[threadIdx.x];
   const size_t S = (size_t)L * K;
   const size_t slot0 = (size_t)blockIdx.x * kRows;
   const int n_rows = (int)min((size_t)kRows, S - slot0);
@@ -313,7 +319,7 @@ __global__ __launch_bounds__(256) void edge_update_kernel(EncLayerDev w, float* 
   for (int i = 0; i < kEdgeRM; ++i)
 #pragma unroll
     for (int j = 0; j < kEdgeCN; ++j) {
-      A[(col0 + j) * kLdE + row0 + i] = (row0 + i < n_rows) ? gelu(acc[i][j] + w.b11[col0 + j]) : 0.0F;
+      A[(col0 + j) * kLdE + row0 + i] = (row0 + i < n_rows) ? gelu(acc[i][j] + w.b11[col0 + j], tbl) : 0.0F;
       acc[i][j] = 0.0F;
     }
   seq_gemm<kEdgeRM, kEdgeCN, kH, kKC>(acc, A, kLdE, row0, w.W12_t, kH, kH, Wbuf, col0);
@@ -321,7 +327,7 @@ __global__ __launch_bounds__(256) void edge_update_kernel(EncLayerDev w, float* 
   for (int i = 0; i < kEdgeRM; ++i)
 #pragma unroll
     for (int j = 0; j < kEdgeCN; ++j) {
-      A[(col0 + j) * kLdE + row0 + i] = (row0 + i < n_rows) ? gelu(acc[i][j] + w.b12[col0 + j]) : 0.0F;
+      A[(col0 + j) * kLdE + row0 + i] = (row0 + i < n_rows) ? gelu(acc[i][j] + w.b12[col0 + j], tbl) : 0.0F;
       acc[i][j] = 0.0F;
     }
   seq_gemm<kEdgeRM, kEdgeCN, kH, kKC>(acc, A, kLdE, row0, w.W13_t, kH, kH, Wbuf, col0);

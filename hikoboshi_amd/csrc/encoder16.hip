@@ -371,16 +371,61 @@ __global__ __launch_bounds__(kTileThreads, 2) void edge_embed16_kernel(ModelDev 
   const int n0 = 32 * wave;
   const long long S_ = (long long)L * K;
   const long long base = (long long)blockIdx.x * R;
+  // Per tile row, staged once: the atoms of residue res (q) and of its
+  // neighbour j (n), their presence bits (q: bits 0-4, n: bits 8-12; bit 16:
+  // j is a residue) and the positional class. Waves 0, 1 and 2 load the three
+  // parts for the row of their lane.
+  __shared__ float xq[R][16], xn[R][16];
+  __shared__ int info[R][2];
+  __shared__ float tbl[17];
+  if (threadIdx.x < 17) tbl[threadIdx.x] = kExpNegTable[threadIdx.x];
+  {
+    const int row = lane;
+    const long long slot = base + row;
+    const bool in = slot < S_;
+    const int j = in ? idx[slot] : -1;
+    const int res = in ? static_cast<int>(slot / K) : 0;
+    const bool nb = j >= 0 && j < L;
+    if (wave == 0) {
+#pragma unroll
+      for (int e = 0; e < 15; ++e) xq[row][e] = coords[(size_t)res * 15 + e];
+    } else if (wave == 1) {
+#pragma unroll
+      for (int e = 0; e < 15; ++e) xn[row][e] = nb ? coords[(size_t)j * 15 + e] : 0.0F;
+    } else if (wave == 2) {
+      int bits = nb ? 1 << 16 : 0;
+#pragma unroll
+      for (int a = 0; a < 5; ++a) {
+        bits |= (src[(size_t)res * 5 + a] != 0) << a;
+        if (nb) bits |= (src[(size_t)j * 5 + a] != 0) << (8 + a);
+      }
+      info[row][0] = bits;
+      info[row][1] = nb ? positional_class(resid, chain, res, j) : 0;
+    }
+  }
+  __syncthreads();
   floatx4 acc[RB][2];
-  // features of chunks [c0, c0 + nc) of the tile's rows into the split slab
+  // features of chunks [c0, c0 + nc) of the tile's rows into the split slab: wave w takes chunks c0 + w,
+  // c0 + w + 4, ... (wave-uniform), its lanes the 64 rows
   auto build = [&](int c0, int nc) {
-    for (int t = threadIdx.x; t < R * nc; t += kTileThreads) {
-      const int row = t % R, c = c0 + t / R;
-      const long long slot = base + row;
-      const int j = slot < S_ ? idx[slot] : -1;
-      const int res = slot < S_ ? static_cast<int>(slot / K) : 0;
+    const int row = lane;
+    const int bits = info[row][0];
+    for (int c = c0 + wave; c < c0 + nc; c += 4) {
       float out[16];
-      edge_chunk(m, coords, src, resid, chain, L, res, j, c, out);  // zeros when j is not a residue
+      if (!(bits >> 16)) {
+#pragma unroll
+        for (int f = 0; f < 16; ++f) out[f] = 0.0F;
+      } else if (c == 0) {
+        positional_chunk(m, info[row][1], out);
+      } else {
+        const int qa = kPairQ[c - 1], na = kPairN[c - 1];
+        if (((bits >> qa) & (bits >> (8 + na)) & 1) == 0) {
+#pragma unroll
+          for (int f = 0; f < 16; ++f) out[f] = 0.0F;
+        } else {
+          rbf_chunk(&xq[row][3 * qa], &xn[row][3 * na], out, tbl);
+        }
+      }
 #pragma unroll
       for (int q = 0; q < 4; ++q)
         put_split4(S, R, kLdE, row, 16 * (c - c0) + 4 * q,

@@ -64,6 +64,9 @@ __global__ __launch_bounds__(256) void edge_embed_kernel(ModelDev m, const float
   static_assert(kGroupChunks * 16 <= kH && kGroupChunks * kTile == 256, "tile sizes");
   __shared__ __attribute__((aligned(16))) float A[kH * kLdT];
   __shared__ __attribute__((aligned(16))) float Wbuf[2 * 32 * kH];
+  __shared__ float tbl[17];
+  if (threadIdx.x < 17) tbl[threadIdx.x] = kExpNegTable[threadIdx.x];
+  __syncthreads();
   const size_t S = (size_t)L * K;
   const size_t slot0 = (size_t)blockIdx.x * kTile;
   const int rg = threadIdx.x / 32, cg = threadIdx.x % 32;
@@ -83,7 +86,7 @@ __global__ __launch_bounds__(256) void edge_embed_kernel(ModelDev m, const float
     // A is free here: seq_gemm ends with a barrier
     if (fchunk < nc) {
       float out[16];
-      edge_chunk(m, coords, src, resid, chain, L, fr, fj, c0 + fchunk, out);  // zeros when fj is not a residue
+      edge_chunk(m, coords, src, resid, chain, L, fr, fj, c0 + fchunk, out, tbl);  // zeros when fj is not a residue
 #pragma unroll
       for (int f = 0; f < 16; ++f) A[(fchunk * 16 + f) * kLdT + frow] = out[f];
     }
