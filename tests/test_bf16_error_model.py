@@ -1,0 +1,36 @@
+"""The bf16 error attribution model (tests/bf16_error_model.py) and its conclusion.
+
+The float64 model is first pinned to the oracle (teacher-forced log-probs at
+T = 1 within 1e-4 on the same backbone, order and tokens). Then, on an oracle
+design trajectory at T = 0.1: rounding any single group of decoder operands to
+bf16 (the weights or the inputs of one product) moves the log-probs by more
+than the 2e-2 that the long-chain bf16 configuration asks for, while weights
+carried as two bf16 terms (about 16 significant bits) stay far inside it.
+"""
+import numpy as np
+
+from hikoboshi_amd import backbone
+
+from . import bf16_error_model as bm
+
+
+def test_model_matches_oracle(oracle):
+    bb = backbone.single_chain(64, 21)
+    idx, feats = oracle.edge_features(bb)
+    mask = np.ones(bb.L)
+    model = bm.Model()
+    he, hv = model.encode(feats, idx, mask)
+    rng = np.random.default_rng(3)
+    tokens = rng.integers(0, 20, bb.L).astype(np.int32)
+    order = rng.permutation(bb.L).astype(np.int32)
+    lp = bm.log_softmax(model.decode(he, hv, idx, mask, tokens, order), 1.0)
+    olp, _ = oracle.teacher_forced_decode(oracle.encode(bb), tokens, order)
+    assert np.abs(lp - olp).max() <= 1e-4
+
+
+def test_bf16_rounding_of_any_product_exceeds_the_bound():
+    dev = bm.deviations(64, seeds=(5,))
+    single = {k: v for k, v in dev.items() if k.startswith("bf16 ") and "_" in k.split()[1]}
+    assert len(single) == 2 * len(bm.PRODUCTS)
+    assert min(single.values()) > 2e-2, single
+    assert dev["bf16 pairs (hi + lo) for every weight, exact activations"] < 2e-3
