@@ -778,14 +778,25 @@ size_t schedule_bytes(int L, int K, int B) {
          aligned_bytes<int32_t>(sched_scratch_words(L, K, nq));
 }
 
-size_t decode_bytes(int L, int K, int B) {
+// The fp32 decode reads its layer-0 message rows from a table
+// (launch_layer0_table) unless HKBS_DECODE_L0TABLE=off or the table would
+// exceed kL0TableMaxBytes; the results are the same either way.
+constexpr size_t kL0TableMaxBytes = (size_t)4 << 30;
+bool l0_table_wanted(int precision, int L) {
+  if (precision != HKBS_PRECISION_FP32) return false;
+  if (const char* env = std::getenv("HKBS_DECODE_L0TABLE"); env && std::strcmp(env, "off") == 0) return false;
+  const int K = std::min(kKmax, L);
+  return l0_table_floats((size_t)L, (size_t)K) * sizeof(float) <= kL0TableMaxBytes;
+}
+
+size_t decode_bytes(int L, int K, int B, bool l0table) {
   const size_t S = (size_t)L * K;
   return aligned_bytes<float>(kLayers * S * kH) + aligned_bytes<float>((size_t)(kLayers + 1) * L * kH) +
          2 * aligned_bytes<int32_t>((size_t)B * L) + aligned_bytes<uint64_t>(B) +
          aligned_bytes<float>((size_t)B * kLayers * L * kH) + aligned_bytes<int32_t>((size_t)B * L) +
          aligned_bytes<float>((size_t)B * L * kV) + aligned_bytes<float>((size_t)B * L) + aligned_bytes<float>(B) +
          aligned_bytes<uint32_t>((size_t)B + 1) + 2 * aligned_bytes<int32_t>((size_t)B * L * K) +
-         schedule_bytes(L, K, B);
+         schedule_bytes(L, K, B) + (l0table ? aligned_bytes<float>(l0_table_floats(L, K)) : 0);
 }
 
 hkbs_status enter(hkbs_pmpnn* ctx) {
@@ -802,21 +813,23 @@ hkbs_status check_temperature(float temperature) {
 
 // Bytes a device design takes from its arena: the chosen-log-prob buffer of
 // the device entry points, then design_on_device's buffers in its order.
-size_t design_scratch_bytes(int L, int B, bool shared) {
+size_t design_scratch_bytes(int L, int B, bool shared, bool l0table) {
   const int K = std::min(kKmax, L);
   const size_t S = (size_t)L * K, nq = shared ? 1 : (size_t)B;
   return aligned_bytes<float>((size_t)B * L) + encode_bytes(L, K) + aligned_bytes<float>(kLayers * S * kH) +
          aligned_bytes<float>((size_t)(kLayers + 1) * L * kH) + aligned_bytes<int32_t>((size_t)B * L) +
          aligned_bytes<float>((size_t)B * kLayers * L * kH) + aligned_bytes<uint32_t>((size_t)B + 1) +
          2 * aligned_bytes<int32_t>(nq * L * K) + aligned_bytes<int32_t>(nq * L) + aligned_bytes<int32_t>(nq * (L + 2)) +
-         aligned_bytes<int32_t>(nq) + aligned_bytes<int32_t>(nq * L) + aligned_bytes<int32_t>(sched_scratch_words(L, K, nq));
+         aligned_bytes<int32_t>(nq) + aligned_bytes<int32_t>(nq * L) + aligned_bytes<int32_t>(sched_scratch_words(L, K, nq)) +
+         (l0table ? aligned_bytes<float>(l0_table_floats(L, K)) : 0);
 }
 
 // Shared implementation of the device design path. All pointers device.
 hkbs_status design_on_device(hkbs_pmpnn* ctx, const float* coords, const uint8_t* src, const int32_t* resid,
                              const int32_t* chain, const float* chain_mask, const int32_t* true_tokens, int L, int B,
                              const int32_t* orders, int shared, const uint64_t* seeds, float temperature, int greedy,
-                             int32_t* tokens, float* log_probs, float* scores, DeviceArena& ar, float* chosen) {
+                             int32_t* tokens, float* log_probs, float* scores, DeviceArena& ar, float* chosen,
+                             bool l0table) {
   // The decode runs as an ordinary launch whose grid is resident at once, with
   // bounded team barriers; a cooperative launch is not offered.
   if (const char* mode = std::getenv("HKBS_DECODE_LAUNCH"); mode && std::strcmp(mode, "cooperative") == 0)
@@ -837,6 +850,7 @@ hkbs_status design_on_device(hkbs_pmpnn* ctx, const float* coords, const uint8_t
   int32_t* npass = ar.take<int32_t>(nq);
   int32_t* draw = ar.take<int32_t>(nq * L);
   int32_t* sched_tmp = ar.take<int32_t>(sched_scratch_words(L, K, nq));
+  float* l0tab = l0table ? ar.take<float>(l0_table_floats(L, K)) : nullptr;
   if (ar.used > ar.cap) return fail(HKBS_INTERNAL_ERROR, "design workspace exceeds its reservation");
   ctx->fault = sync + B;
   DecodeArgs a{};
@@ -871,6 +885,7 @@ hkbs_status design_on_device(hkbs_pmpnn* ctx, const float* coords, const uint8_t
   a.draw = draw;
   a.sched_tmp = sched_tmp;
   a.precision = ctx->precision;
+  a.l0tab = l0tab;
   const int team = decode_team_size(a.precision, B, 8);
   a.max_members = kDecodeGroup * team;
   a.pass_granule = team;
@@ -891,6 +906,7 @@ hkbs_status design_on_device(hkbs_pmpnn* ctx, const float* coords, const uint8_t
   HK_CHECK(hipEventRecord(ctx->join, ctx->side), "event record failed");
   if (ctx->timing) HK_CHECK(hipEventRecord(ctx->ev[1], ctx->stream), "event record failed");
   HK_CHECK(launch_decoder_precompute(ctx->model, e.h_v, e.h_e, L, K, E1, Q, ctx->stream), "decoder precompute failed");
+  if (l0tab) HK_CHECK(launch_layer0_table(ctx->model, E1, Q, e.idx, L, K, l0tab, ctx->stream), "layer-0 table failed");
   HK_CHECK(launch_zero(reinterpret_cast<float*>(sync), (size_t)B + 1, ctx->stream), "workspace clear failed");
   HK_CHECK(hipStreamWaitEvent(ctx->stream, ctx->join, 0), "stream wait failed");
   if (ctx->timing) HK_CHECK(hipEventRecord(ctx->ev[2], ctx->stream), "event record failed");
@@ -1061,7 +1077,8 @@ hkbs_status hkbs_pmpnn_design(hkbs_pmpnn* ctx, const float* coords, const uint8_
 
   const int K = std::min(kKmax, L);
   const size_t norders = shared ? (size_t)L : (size_t)B * L;
-  const size_t need = input_bytes(L) + encode_bytes(L, K) + decode_bytes(L, K, B) + aligned_bytes<int32_t>(norders) +
+  const bool l0table = l0_table_wanted(ctx->precision, L);
+  const size_t need = input_bytes(L) + encode_bytes(L, K) + decode_bytes(L, K, B, l0table) + aligned_bytes<int32_t>(norders) +
                       aligned_bytes<uint64_t>(B) + aligned_bytes<int32_t>((size_t)B * L) +
                       aligned_bytes<float>((size_t)B * L * kV) + aligned_bytes<float>(B) + aligned_bytes<float>((size_t)B * L) +
                       (64u << 10);
@@ -1082,7 +1099,7 @@ hkbs_status hkbs_pmpnn_design(hkbs_pmpnn* ctx, const float* coords, const uint8_
   HK_CHECK(hipMemcpyAsync(d_seeds, sampler_seeds, (size_t)B * 8, hipMemcpyHostToDevice, s), "H2D failed");
   if ((st = design_on_device(ctx, in.coords, in.src, in.resid, in.chain, in.chain_mask, in.true_tokens, L, B, d_orders,
                              shared, d_seeds, temperature, greedy, d_tokens, log_probs ? d_lp : nullptr,
-                             d_scores, ar, d_chosen)) != HKBS_OK)
+                             d_scores, ar, d_chosen, l0table)) != HKBS_OK)
     return st;
   HK_CHECK(hipMemcpyAsync(tokens, d_tokens, (size_t)B * L * 4, hipMemcpyDeviceToHost, s), "D2H failed");
   if (log_probs) HK_CHECK(hipMemcpyAsync(log_probs, d_lp, (size_t)B * L * kV * 4, hipMemcpyDeviceToHost, s), "D2H failed");
@@ -1124,7 +1141,8 @@ hkbs_status hkbs_pmpnn_design_device(hkbs_pmpnn* ctx, const float* coords, const
   if (!coords || !atom_sources || !orders || !sampler_seeds || !tokens)
     return fail(HKBS_INVALID_ARGUMENT, "device design pointers must be non-null");
   const int K = std::min(kKmax, L);
-  const size_t need = encode_bytes(L, K) + decode_bytes(L, K, B) + aligned_bytes<float>((size_t)B * L) + (64u << 10);
+  const bool l0table = l0_table_wanted(ctx->precision, L);
+  const size_t need = encode_bytes(L, K) + decode_bytes(L, K, B, l0table) + aligned_bytes<float>((size_t)B * L) + (64u << 10);
   DeviceArena& ar = ctx->arena;
   hipStream_t saved = ctx->stream;
   if (stream) {
@@ -1139,7 +1157,8 @@ hkbs_status hkbs_pmpnn_design_device(hkbs_pmpnn* ctx, const float* coords, const
   ar.reset();
   float* chosen = ar.take<float>((size_t)B * L);
   st = design_on_device(ctx, coords, atom_sources, residue_indices, chain_labels, chain_mask, true_tokens, L, B, orders,
-                        shared_order != 0, sampler_seeds, temperature, greedy, tokens, log_probs, scores, ar, chosen);
+                        shared_order != 0, sampler_seeds, temperature, greedy, tokens, log_probs, scores, ar, chosen,
+                        l0table);
   ctx->stream = saved;
   return st;
 }
@@ -1158,7 +1177,10 @@ hkbs_status hkbs_pmpnn_design_device_noalloc(hkbs_pmpnn* ctx, const float* coord
   if (L == 0) return HKBS_OK;
   if (!coords || !atom_sources || !orders || !sampler_seeds || !tokens)
     return fail(HKBS_INVALID_ARGUMENT, "device design pointers must be non-null");
-  if (design_scratch_bytes(L, B, shared_order != 0) > kNoAllocScratchBytes)
+  // The layer-0 table is used when it fits beside the rest (same results without it).
+  bool l0table = l0_table_wanted(ctx->precision, L);
+  if (l0table && design_scratch_bytes(L, B, shared_order != 0, true) > kNoAllocScratchBytes) l0table = false;
+  if (design_scratch_bytes(L, B, shared_order != 0, l0table) > kNoAllocScratchBytes)
     return fail(HKBS_INVALID_ARGUMENT,
                 "request needs more device scratch than the allocation-free design holds (128 MiB)");
   DeviceArena ar;  // borrows this device's static scratch; never freed
@@ -1171,7 +1193,8 @@ hkbs_status hkbs_pmpnn_design_device_noalloc(hkbs_pmpnn* ctx, const float* coord
   }
   float* chosen = ar.take<float>((size_t)B * L);
   st = design_on_device(ctx, coords, atom_sources, residue_indices, chain_labels, chain_mask, true_tokens, L, B, orders,
-                        shared_order != 0, sampler_seeds, temperature, greedy, tokens, log_probs, scores, ar, chosen);
+                        shared_order != 0, sampler_seeds, temperature, greedy, tokens, log_probs, scores, ar, chosen,
+                        l0table);
   ctx->stream = saved;
   return st;
 }

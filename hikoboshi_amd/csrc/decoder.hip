@@ -181,6 +181,12 @@ __device__ inline void store_dev(float* p, float v) { __hip_atomic_store(p, v, _
 __device__ inline float load_dev(const float* p) {
   return __hip_atomic_load(const_cast<float*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
+__device__ inline void store_dev(int32_t* p, int32_t v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ inline int32_t load_dev(const int32_t* p) {
+  return __hip_atomic_load(const_cast<int32_t*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
 // Four consecutive floats (16-byte aligned) as two 8-byte device-scope loads.
 __device__ inline float4 load4_dev(const float* p) {
   uint64_t* q = reinterpret_cast<uint64_t*>(const_cast<float*>(p));
@@ -264,6 +270,7 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(ModelDev m, DecodeArgs
   __shared__ __attribute__((aligned(16))) float gtab[kGeluPolyRows * 8];  // GELU polynomials
   __shared__ int nbr[kGroup * kKmax];
   __shared__ int bwf[kGroup * kKmax];
+  __shared__ int cls[kGroup * kKmax];  // layer-0 table class of each slot (with a.l0tab)
   __shared__ int tres[kGroup];
   __shared__ int ures[kGroup];
   __shared__ int tok_s[kGroup];
@@ -327,7 +334,7 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(ModelDev m, DecodeArgs
         for (int i = threadIdx.x; i < n0; i += kThreads) {
           const int t = order[sched[s0 + i]];
           const int tok = (a.true_tokens && a.true_tokens[t] >= 0 && a.true_tokens[t] < kV) ? a.true_tokens[t] : kV - 1;
-          tokens[t] = tok;
+          store_dev(tokens + t, tok);
           store_dev(chosen + t, 0.0F);
         }
         if (lp_out)
@@ -359,8 +366,11 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(ModelDev m, DecodeArgs
         const int i = threadIdx.x / K, k = threadIdx.x % K;
         const int u = sched[s0 + rank + P * i];
         const size_t at = (size_t)u * K + k;
-        nbr[i * kKmax + k] = nbj[at];
-        bwf[i * kKmax + k] = nbp[at] < u;  // empty slots hold position L
+        const int j = nbj[at];
+        const bool bw = nbp[at] < u;  // empty slots hold position L
+        nbr[i * kKmax + k] = j;
+        bwf[i * kKmax + k] = bw;
+        if (PREC == kPrecFp32 && a.l0tab) cls[i * kKmax + k] = (j >= 0 && bw) ? load_dev(tokens + j) : kV;
         if (k == 0) {
           tres[i] = order[u];
           ures[i] = u;
@@ -374,6 +384,39 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(ModelDev m, DecodeArgs
         hA[i * kH + c] = a.Q[((size_t)3 * L + t) * kH + c] + prm[kPrmB1 + c];
       }
       __syncthreads();
+      if (PREC == kPrecFp32 && a.l0tab) {
+        // x[i] = sum over slots of table rows, in the order of the MFMA path
+        // below: lane group g (rows 16 mb + 4 g + e, mb outer) sums its rows,
+        // then the four groups add as (g0 + g1) + (g2 + g3).
+        const int i = threadIdx.x >> 7, gq = (threadIdx.x >> 5) & 3, q = threadIdx.x & 31;
+        static_assert(kThreads == 128 * kGroup, "table sum mapping");
+        if (i < ml) {
+          const float* tb = a.l0tab + (size_t)tres[i] * K * kL0Classes * kH + 4 * q;
+          float4 v[12];
+#pragma unroll
+          for (int n = 0; n < 12; ++n) {
+            const int row = (n / 4) * 16 + 4 * gq + (n % 4);
+            v[n] = row < K ? *reinterpret_cast<const float4*>(tb + ((size_t)row * kL0Classes + cls[i * kKmax + row]) * kH)
+                           : make_float4(0.F, 0.F, 0.F, 0.F);
+          }
+          float4 sum = make_float4(0.F, 0.F, 0.F, 0.F);
+#pragma unroll
+          for (int n = 0; n < 12; ++n) {
+            sum.x += v[n].x;
+            sum.y += v[n].y;
+            sum.z += v[n].z;
+            sum.w += v[n].w;
+          }
+          *reinterpret_cast<float4*>(ff + (i * 4 + gq) * kH + 4 * q) = sum;
+        }
+        __syncthreads();
+        for (int task = threadIdx.x; task < ml * kH; task += kThreads) {
+          const int im = task / kH, c = task % kH;
+          const float* f = ff + im * 4 * kH + c;
+          x[task] = (f[0] + f[kH]) + (f[2 * kH] + f[3 * kH]);
+        }
+        __syncthreads();
+      }
 
       typename GLog::Part lg;  // logits weights in flight for the whole pass
       GLog::load(lg, (BF ? static_cast<const void*>(m.Wlog_h) : HF ? static_cast<const void*>(m.Wlog_f) : m.Wlog_t), 0);
@@ -381,143 +424,147 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(ModelDev m, DecodeArgs
         const DecLayerDev& w = m.dec[l];
         const float* Ql = a.Q + (size_t)l * L * kH;
         const float* Rl = R + (size_t)l * L * kH;
-        // W2 fragments of this wave's 16 columns stay in registers for all members.
-        const int r = lane & 15, g = lane >> 4;
-        const int col = wave * 16 + r;
-        // B fragments of the 16x16x32 MFMA: column col, k = 32 kb + 8 g + 0..7
-        half8 bh[kH / 32], bl[kH / 32];
-        bf16x8 bb[kH / 32];
-#pragma unroll
-        for (int kb = 0; kb < kH / 32; ++kb) {
-          const size_t at = ((size_t)(4 * kb + g) * kH + col) * 4;  // float slots of 8 halves
-          if constexpr (BF) {
-            bb[kb] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const float4*>(w.W2_b + 2 * at));
-          } else {
-            bh[kb] = __builtin_bit_cast(half8, *reinterpret_cast<const float4*>(w.W2h + at));
-            if constexpr (!HF) bl[kb] = __builtin_bit_cast(half8, *reinterpret_cast<const float4*>(w.W2l + at));
-          }
-        }
+        // Layer 0 of the fp32 decode reads its message rows from the table.
+        const bool from_tab = PREC == kPrecFp32 && l == 0 && a.l0tab != nullptr;
         const float* pl = prm + l * kPrmLayer;
-        const float b2 = pl[kPrmB2 + col];
         typename G3::Part g3;  // W3 in flight during the message rows and their product
         G3::load(g3, (BF ? static_cast<const void*>(w.W3_h) : HF ? static_cast<const void*>(w.W3_f) : w.W3_t), 0);
-        for (int i0 = 0; i0 < ml; i0 += 2) {
-          {
-            // Message rows g1 = GELU(A + E1_tk + (bw ? R : Q)_j) of members i0, i0 + 1;
-            // rows >= K are zero. Thread owns columns c..c+3 of rows r0 + 16 s
-            // (member i0 + s / 3, slot 16 (s % 3) + r0); all gathers are issued
-            // before the first use.
-            constexpr int kS = 2 * kKmax / 16;
-            static_assert(kKmax == 48 && kThreads == 512, "row mapping");
-            const int c = 4 * (threadIdx.x & 31);
-            const int r0 = threadIdx.x >> 5;
-            float4 e[kS], z[kS];
+        if (!from_tab) {  // else x holds the layer-0 message sums (table, above)
+          // W2 fragments of this wave's 16 columns stay in registers for all members.
+          const int r = lane & 15, g = lane >> 4;
+          const int col = wave * 16 + r;
+          // B fragments of the 16x16x32 MFMA: column col, k = 32 kb + 8 g + 0..7
+          half8 bh[kH / 32], bl[kH / 32];
+          bf16x8 bb[kH / 32];
 #pragma unroll
-            for (int s = 0; s < kS; ++s) {
-              const int i = i0 + s / 3, k = 16 * (s % 3) + r0;
-              e[s] = make_float4(0.F, 0.F, 0.F, 0.F);
-              z[s] = e[s];
-              if (i < ml && k < K) {
-                const int j = nbr[i * kKmax + k];
-                if (j >= 0) {
-                  e[s] = *reinterpret_cast<const float4*>(a.E1 + ((size_t)l * S + (size_t)tres[i] * K + k) * kH + c);
-                  z[s] = bwf[i * kKmax + k] ? load4_dev(Rl + (size_t)j * kH + c)  // R: written by the team
-                                                : *reinterpret_cast<const float4*>(Ql + (size_t)j * kH + c);
-                }
-              }
-            }
-#pragma unroll
-            for (int s = 0; s < kS; ++s) {
-              const int i = i0 + s / 3, k = 16 * (s % 3) + r0;
-              if (i < ml) {
-                float4 xv = *reinterpret_cast<const float4*>(hA + i * kH + c);
-                xv.x += e[s].x + z[s].x;
-                xv.y += e[s].y + z[s].y;
-                xv.z += e[s].z + z[s].z;
-                xv.w += e[s].w + z[s].w;
-                float4 v = make_float4(gelu_poly(xv.x, gtab), gelu_poly(xv.y, gtab), gelu_poly(xv.z, gtab),
-                                       gelu_poly(xv.w, gtab));
-                if (k >= K) v = make_float4(0.F, 0.F, 0.F, 0.F);
-                _Float16* gh = G16 + (((s / 3) * 2) * kKmax + k) * kLdH + c;
-                const float vv[4] = {v.x, v.y, v.z, v.w};
-                if constexpr (BF) {
-                  bf16x4 bv;
-#pragma unroll
-                  for (int e = 0; e < 4; ++e) bv[e] = static_cast<__bf16>(vv[e]);
-                  *reinterpret_cast<bf16x4*>(gh) = bv;
-                } else if constexpr (HF) {
-                  half4 hv;
-#pragma unroll
-                  for (int e = 0; e < 4; ++e) hv[e] = static_cast<_Float16>(__builtin_amdgcn_fmed3f(vv[e], -65504.0F, 65504.0F));
-                  *reinterpret_cast<half4*>(gh) = hv;
-                } else {
-                  // split for the fp16 MFMA: v = hi + lo / 2048 to about 2^-22 relative
-                  _Float16* gl = gh + kKmax * kLdH;
-                  half4 hv, lv;
-#pragma unroll
-                  for (int e = 0; e < 4; ++e) {
-                    const float cl = __builtin_amdgcn_fmed3f(vv[e], -65504.0F, 65504.0F);
-                    hv[e] = static_cast<_Float16>(cl);
-                    lv[e] = static_cast<_Float16>((vv[e] - static_cast<float>(hv[e])) * 2048.0F);
-                  }
-                  *reinterpret_cast<half4*>(gh) = hv;
-                  *reinterpret_cast<half4*>(gl) = lv;
-                }
-              }
+          for (int kb = 0; kb < kH / 32; ++kb) {
+            const size_t at = ((size_t)(4 * kb + g) * kH + col) * 4;  // float slots of 8 halves
+            if constexpr (BF) {
+              bb[kb] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const float4*>(w.W2_b + 2 * at));
+            } else {
+              bh[kb] = __builtin_bit_cast(half8, *reinterpret_cast<const float4*>(w.W2h + at));
+              if constexpr (!HF) bl[kb] = __builtin_bit_cast(half8, *reinterpret_cast<const float4*>(w.W2l + at));
             }
           }
-          __syncthreads();
-          for (int i = i0; i < ml && i < i0 + 2; ++i) {
-            const _Float16* Gh = G16 + (i - i0) * 2 * kKmax * kLdH;
-            const _Float16* Gl = Gh + kKmax * kLdH;
-            // W2 product: hi.hi + (hi.lo + lo.hi) / 2048 on the fp16 MFMA, or bf16 x bf16
-            floatx4 acc[3], cor[3];
+          const float b2 = pl[kPrmB2 + col];
+          for (int i0 = 0; i0 < ml; i0 += 2) {
+            {
+              // Message rows g1 = GELU(A + E1_tk + (bw ? R : Q)_j) of members i0, i0 + 1;
+              // rows >= K are zero. Thread owns columns c..c+3 of rows r0 + 16 s
+              // (member i0 + s / 3, slot 16 (s % 3) + r0); all gathers are issued
+              // before the first use.
+              constexpr int kS = 2 * kKmax / 16;
+              static_assert(kKmax == 48 && kThreads == 512, "row mapping");
+              const int c = 4 * (threadIdx.x & 31);
+              const int r0 = threadIdx.x >> 5;
+              float4 e[kS], z[kS];
 #pragma unroll
-            for (int mb = 0; mb < 3; ++mb) {
-              acc[mb] = floatx4{0.F, 0.F, 0.F, 0.F};
-              cor[mb] = acc[mb];
-            }
+              for (int s = 0; s < kS; ++s) {
+                const int i = i0 + s / 3, k = 16 * (s % 3) + r0;
+                e[s] = make_float4(0.F, 0.F, 0.F, 0.F);
+                z[s] = e[s];
+                if (i < ml && k < K) {
+                  const int j = nbr[i * kKmax + k];
+                  if (j >= 0) {
+                    e[s] = *reinterpret_cast<const float4*>(a.E1 + ((size_t)l * S + (size_t)tres[i] * K + k) * kH + c);
+                    z[s] = bwf[i * kKmax + k] ? load4_dev(Rl + (size_t)j * kH + c)  // R: written by the team
+                                                  : *reinterpret_cast<const float4*>(Ql + (size_t)j * kH + c);
+                  }
+                }
+              }
 #pragma unroll
-            for (int kb = 0; kb < kH / 32; ++kb) {
+              for (int s = 0; s < kS; ++s) {
+                const int i = i0 + s / 3, k = 16 * (s % 3) + r0;
+                if (i < ml) {
+                  float4 xv = *reinterpret_cast<const float4*>(hA + i * kH + c);
+                  xv.x += e[s].x + z[s].x;
+                  xv.y += e[s].y + z[s].y;
+                  xv.z += e[s].z + z[s].z;
+                  xv.w += e[s].w + z[s].w;
+                  float4 v = make_float4(gelu_poly(xv.x, gtab), gelu_poly(xv.y, gtab), gelu_poly(xv.z, gtab),
+                                         gelu_poly(xv.w, gtab));
+                  if (k >= K) v = make_float4(0.F, 0.F, 0.F, 0.F);
+                  _Float16* gh = G16 + (((s / 3) * 2) * kKmax + k) * kLdH + c;
+                  const float vv[4] = {v.x, v.y, v.z, v.w};
+                  if constexpr (BF) {
+                    bf16x4 bv;
 #pragma unroll
-              for (int mb = 0; mb < 3; ++mb) {
-                const int at = (mb * 16 + r) * kLdH + 32 * kb + 8 * g;
-                if constexpr (BF) {
-                  const bf16x8 ab = *reinterpret_cast<const bf16x8*>(Gh + at);
-                  acc[mb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ab, bb[kb], acc[mb], 0, 0, 0);
-                } else if constexpr (HF) {
-                  const half8 ah = *reinterpret_cast<const half8*>(Gh + at);
-                  acc[mb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, bh[kb], acc[mb], 0, 0, 0);
-                } else {
-                  const half8 ah = *reinterpret_cast<const half8*>(Gh + at);
-                  const half8 al = *reinterpret_cast<const half8*>(Gl + at);
-                  acc[mb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, bh[kb], acc[mb], 0, 0, 0);
-                  cor[mb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, bl[kb], cor[mb], 0, 0, 0);
-                  cor[mb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al, bh[kb], cor[mb], 0, 0, 0);
+                    for (int e = 0; e < 4; ++e) bv[e] = static_cast<__bf16>(vv[e]);
+                    *reinterpret_cast<bf16x4*>(gh) = bv;
+                  } else if constexpr (HF) {
+                    half4 hv;
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) hv[e] = static_cast<_Float16>(__builtin_amdgcn_fmed3f(vv[e], -65504.0F, 65504.0F));
+                    *reinterpret_cast<half4*>(gh) = hv;
+                  } else {
+                    // split for the fp16 MFMA: v = hi + lo / 2048 to about 2^-22 relative
+                    _Float16* gl = gh + kKmax * kLdH;
+                    half4 hv, lv;
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                      const float cl = __builtin_amdgcn_fmed3f(vv[e], -65504.0F, 65504.0F);
+                      hv[e] = static_cast<_Float16>(cl);
+                      lv[e] = static_cast<_Float16>((vv[e] - static_cast<float>(hv[e])) * 2048.0F);
+                    }
+                    *reinterpret_cast<half4*>(gh) = hv;
+                    *reinterpret_cast<half4*>(gl) = lv;
+                  }
                 }
               }
             }
-            if constexpr (PREC == kPrecFp32) {
+            __syncthreads();
+            for (int i = i0; i < ml && i < i0 + 2; ++i) {
+              const _Float16* Gh = G16 + (i - i0) * 2 * kKmax * kLdH;
+              const _Float16* Gl = Gh + kKmax * kLdH;
+              // W2 product: hi.hi + (hi.lo + lo.hi) / 2048 on the fp16 MFMA, or bf16 x bf16
+              floatx4 acc[3], cor[3];
+#pragma unroll
+              for (int mb = 0; mb < 3; ++mb) {
+                acc[mb] = floatx4{0.F, 0.F, 0.F, 0.F};
+                cor[mb] = acc[mb];
+              }
+#pragma unroll
+              for (int kb = 0; kb < kH / 32; ++kb) {
+#pragma unroll
+                for (int mb = 0; mb < 3; ++mb) {
+                  const int at = (mb * 16 + r) * kLdH + 32 * kb + 8 * g;
+                  if constexpr (BF) {
+                    const bf16x8 ab = *reinterpret_cast<const bf16x8*>(Gh + at);
+                    acc[mb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ab, bb[kb], acc[mb], 0, 0, 0);
+                  } else if constexpr (HF) {
+                    const half8 ah = *reinterpret_cast<const half8*>(Gh + at);
+                    acc[mb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, bh[kb], acc[mb], 0, 0, 0);
+                  } else {
+                    const half8 ah = *reinterpret_cast<const half8*>(Gh + at);
+                    const half8 al = *reinterpret_cast<const half8*>(Gl + at);
+                    acc[mb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, bh[kb], acc[mb], 0, 0, 0);
+                    cor[mb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, bl[kb], cor[mb], 0, 0, 0);
+                    cor[mb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al, bh[kb], cor[mb], 0, 0, 0);
+                  }
+                }
+              }
+              if constexpr (PREC == kPrecFp32) {
+#pragma unroll
+                for (int mb = 0; mb < 3; ++mb)
+#pragma unroll
+                  for (int e = 0; e < 4; ++e) acc[mb][e] += cor[mb][e] * (1.0F / 2048.0F);
+              }
+              // x[i][col] = sum over the member's K rows of GELU(acc + b2)
+              float sum = 0.0F;
 #pragma unroll
               for (int mb = 0; mb < 3; ++mb)
 #pragma unroll
-                for (int e = 0; e < 4; ++e) acc[mb][e] += cor[mb][e] * (1.0F / 2048.0F);
+                for (int e = 0; e < 4; ++e) {
+                  const int row = mb * 16 + 4 * g + e;
+                  const float gv = gelu_poly(acc[mb][e] + b2, gtab);
+                  sum += row < K ? gv : 0.0F;
+                }
+              sum += __shfl_xor(sum, 16, 64);
+              sum += __shfl_xor(sum, 32, 64);
+              if (lane < 16) x[i * kH + col] = sum;
             }
-            // x[i][col] = sum over the member's K rows of GELU(acc + b2)
-            float sum = 0.0F;
-#pragma unroll
-            for (int mb = 0; mb < 3; ++mb)
-#pragma unroll
-              for (int e = 0; e < 4; ++e) {
-                const int row = mb * 16 + 4 * g + e;
-                const float gv = gelu_poly(acc[mb][e] + b2, gtab);
-                sum += row < K ? gv : 0.0F;
-              }
-            sum += __shfl_xor(sum, 16, 64);
-            sum += __shfl_xor(sum, 32, 64);
-            if (lane < 16) x[i * kH + col] = sum;
+            __syncthreads();
           }
-          __syncthreads();
         }
         // upd = (W3 s + K b3) / 30 ; h1 = LN1(h + upd): wave i owns member i
         float4 acc[kGroup];
@@ -622,7 +669,7 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(ModelDev m, DecodeArgs
         if (lp_out && lane < kV) lp_out[(size_t)t * kV + lane] = lpv;
         if (lane == tok) store_dev(chosen + t, lpv);
         if (lane == 0) {
-          tokens[t] = tok;
+          store_dev(tokens + t, tok);
           tok_s[i] = tok;
         }
       }
@@ -652,6 +699,130 @@ finish:
       msum += static_cast<double>(act);
     }
     a.scores[b] = msum > 0.0 ? static_cast<float>(loss / msum) : 0.0F;
+  }
+}
+
+// Layer-0 message table (launch_layer0_table): workgroup (t, y) writes the
+// rows of slots [kTabSlots y, kTabSlots y + kTabSlots) of residue t, all
+// classes, 48 rows at a time. Each row repeats the decode loop's fp32 steps
+// for a slot whose neighbour is in that class (decode_kernel, PREC = fp32):
+// the pre-activation hA + (E1 + z) with z = Q^0_j + T_0[c] for a neighbour
+// decoded with token c (the R^0_j row its writer stores), z = Q^0_j
+// otherwise and e = z = 0 for an empty slot; GELU and the hi/lo split into
+// the same LDS layout; the same MFMA operands and order; GELU(acc + b2).
+constexpr int kTabSlots = 24;
+__global__ __launch_bounds__(kThreads, 4) void layer0_table_kernel(ModelDev m, const float* __restrict__ E1,
+                                                                  const float* __restrict__ Q,
+                                                                  const int32_t* __restrict__ idx, int L, int K,
+                                                                  float* __restrict__ tab) {
+  __shared__ __attribute__((aligned(16))) _Float16 G16[2 * kKmax * kLdH];  // hi rows, then lo rows
+  __shared__ __attribute__((aligned(16))) float es[kTabSlots * kH];          // E1_tk
+  __shared__ __attribute__((aligned(16))) float qs[kTabSlots * kH];          // Q^0_j
+  __shared__ __attribute__((aligned(16))) float ts[kV * kH];                 // T_0
+  __shared__ __attribute__((aligned(16))) float hA[kH];
+  __shared__ __attribute__((aligned(16))) float gtab[kGeluPolyRows * 8];
+  __shared__ int js[kTabSlots];
+  const int t = blockIdx.x;
+  const int k0 = blockIdx.y * kTabSlots;
+  const int nk = min(kTabSlots, K - k0);
+  if (t >= L || nk <= 0) return;
+  const DecLayerDev& w = m.dec[0];
+  for (int i = threadIdx.x; i < kGeluPolyRows * 8; i += kThreads) gtab[i] = kGeluPoly[i];
+  for (int i = threadIdx.x; i < kH; i += kThreads) hA[i] = Q[((size_t)3 * L + t) * kH + i] + w.b1[i];
+  if (threadIdx.x < nk) {
+    const int jj = idx[(size_t)t * K + k0 + threadIdx.x];
+    js[threadIdx.x] = (jj >= 0 && jj < L) ? jj : -1;
+  }
+  for (int i = threadIdx.x; i < kV * kH; i += kThreads) ts[i] = w.T[i];
+  __syncthreads();
+  for (int task = threadIdx.x; task < nk * (kH / 4); task += kThreads) {
+    const int s = task / (kH / 4), c = 4 * (task % (kH / 4));
+    const int j = js[s];
+    float4 e = make_float4(0.F, 0.F, 0.F, 0.F), z = e;
+    if (j >= 0) {
+      e = *reinterpret_cast<const float4*>(E1 + ((size_t)t * K + k0 + s) * kH + c);
+      z = *reinterpret_cast<const float4*>(Q + (size_t)j * kH + c);
+    }
+    *reinterpret_cast<float4*>(es + s * kH + c) = e;
+    *reinterpret_cast<float4*>(qs + s * kH + c) = z;
+  }
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int r = lane & 15, g = lane >> 4;
+  const int col = wave * 16 + r;
+  half8 bh[kH / 32], bl[kH / 32];
+#pragma unroll
+  for (int kb = 0; kb < kH / 32; ++kb) {
+    const size_t at = ((size_t)(4 * kb + g) * kH + col) * 4;
+    bh[kb] = __builtin_bit_cast(half8, *reinterpret_cast<const float4*>(w.W2h + at));
+    bl[kb] = __builtin_bit_cast(half8, *reinterpret_cast<const float4*>(w.W2l + at));
+  }
+  const float b2 = w.b2[col];
+  const int rows = nk * kL0Classes;
+  float* out = tab + ((size_t)t * K + k0) * kL0Classes * kH;
+  __syncthreads();
+  for (int r0 = 0; r0 < rows; r0 += kKmax) {
+    for (int task = threadIdx.x; task < kKmax * (kH / 4); task += kThreads) {
+      const int row = task / (kH / 4), c = 4 * (task % (kH / 4));
+      float vv[4] = {0.F, 0.F, 0.F, 0.F};
+      if (r0 + row < rows) {
+        const int s = (r0 + row) / kL0Classes, cl = (r0 + row) % kL0Classes;
+        const float4 e = *reinterpret_cast<const float4*>(es + s * kH + c);
+        float4 z = *reinterpret_cast<const float4*>(qs + s * kH + c);
+        if (js[s] >= 0 && cl < kV) {
+          const float4 tv = *reinterpret_cast<const float4*>(ts + cl * kH + c);
+          z.x = z.x + tv.x;
+          z.y = z.y + tv.y;
+          z.z = z.z + tv.z;
+          z.w = z.w + tv.w;
+        }
+        float4 xv = *reinterpret_cast<const float4*>(hA + c);
+        xv.x += e.x + z.x;
+        xv.y += e.y + z.y;
+        xv.z += e.z + z.z;
+        xv.w += e.w + z.w;
+        vv[0] = gelu_poly(xv.x, gtab);
+        vv[1] = gelu_poly(xv.y, gtab);
+        vv[2] = gelu_poly(xv.z, gtab);
+        vv[3] = gelu_poly(xv.w, gtab);
+      }
+      half4 hv, lv;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const float cl = __builtin_amdgcn_fmed3f(vv[e], -65504.0F, 65504.0F);
+        hv[e] = static_cast<_Float16>(cl);
+        lv[e] = static_cast<_Float16>((vv[e] - static_cast<float>(hv[e])) * 2048.0F);
+      }
+      *reinterpret_cast<half4*>(G16 + row * kLdH + c) = hv;
+      *reinterpret_cast<half4*>(G16 + (kKmax + row) * kLdH + c) = lv;
+    }
+    __syncthreads();
+    floatx4 acc[3], cor[3];
+#pragma unroll
+    for (int mb = 0; mb < 3; ++mb) {
+      acc[mb] = floatx4{0.F, 0.F, 0.F, 0.F};
+      cor[mb] = acc[mb];
+    }
+#pragma unroll
+    for (int kb = 0; kb < kH / 32; ++kb) {
+#pragma unroll
+      for (int mb = 0; mb < 3; ++mb) {
+        const int at = (mb * 16 + r) * kLdH + 32 * kb + 8 * g;
+        const half8 ah = *reinterpret_cast<const half8*>(G16 + at);
+        const half8 al = *reinterpret_cast<const half8*>(G16 + kKmax * kLdH + at);
+        acc[mb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, bh[kb], acc[mb], 0, 0, 0);
+        cor[mb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, bl[kb], cor[mb], 0, 0, 0);
+        cor[mb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al, bh[kb], cor[mb], 0, 0, 0);
+      }
+    }
+#pragma unroll
+    for (int mb = 0; mb < 3; ++mb)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int row = r0 + mb * 16 + 4 * g + e;
+        const float v = acc[mb][e] + cor[mb][e] * (1.0F / 2048.0F);
+        if (row < rows) out[(size_t)row * kH + col] = gelu_poly(v + b2, gtab);
+      }
+    __syncthreads();
   }
 }
 
@@ -1153,6 +1324,15 @@ hipError_t launch_q_precompute(const ModelDev& m, const float* h_v, int L, float
   if (L <= 0) return hipSuccess;
   rows_gemm_kernel<<<dim3((unsigned)((L + kGemmRows - 1) / kGemmRows), kLayers + 1), 256, 0, stream>>>(
       h_v, (size_t)L, m.W1d_dec_p, (kLayers + 1) * kH, Q);
+  return hipGetLastError();
+}
+
+hipError_t launch_layer0_table(const ModelDev& m, const float* E1, const float* Q, const int32_t* idx, int L, int K,
+                               float* tab, hipStream_t stream) {
+  if (L <= 0 || K <= 0) return hipSuccess;
+  if (K > kKmax) return hipErrorInvalidValue;
+  layer0_table_kernel<<<dim3((unsigned)L, (unsigned)((K + kTabSlots - 1) / kTabSlots)), kThreads, 0, stream>>>(
+      m, E1, Q, idx, L, K, tab);
   return hipGetLastError();
 }
 

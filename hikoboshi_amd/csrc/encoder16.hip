@@ -39,21 +39,18 @@
 //                  (valid slots).
 #include "device_math.hpp"
 #include "edge_chunk.hpp"
+#include "mfma_tile.hpp"
 #include "pmpnn_internal.hpp"
 
 namespace hkbs {
 namespace {
 
-typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 
 constexpr int kLdF = kFF + 4;      // floats per row of the FFN hidden layer
 constexpr int kLdH = kH + 4;       // floats per row of a 128-wide activation
 static_assert(kKmax == 48, "edge_msg16 covers a residue's slots with 3 waves of 16 rows");
 static_assert(kEdgeIn % 32 == 0, "MFMA k-steps");
 
-__device__ inline floatx4 mfma_f16(f16x8 a, f16x8 b, floatx4 c) {
-  return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
-}
 
 // acc[nt] = A[16 rows][K] . W[K][n0 + 16 nt + (0..15)] for nt < NT. A is the
 // wave's fp32 slab (lda floats per row); Wp the split weights, hi as
@@ -138,95 +135,6 @@ __device__ inline float sum16(float v) {
   v += __shfl_xor(v, 4, 64);
   v += __shfl_xor(v, 8, 64);
   return v;
-}
-
-// ------------------------------------------------------------ edge tiles ----
-// A tile holds 16 RB edge rows. Its operands live in LDS split into fp16
-// halves, hi [rows][ld] then lo [rows][ld] (v = hi + lo / 2048); a row stride
-// of K + 8 halves steps 4 banks per row, so the 16-byte fragment reads of 8
-// consecutive rows cover all banks once. Wave w produces output columns
-// [32 w, 32 w + 32) as two 16-column MFMA tiles per row block, computed
-// transposed (weights as the MFMA's A operand, rows as its B operand): lane
-// (r, g) then holds row 16 rb + r, columns 32 w + 16 nt + 4 g + (0..3).
-constexpr int kTileThreads = 256;
-constexpr int kLdS2 = 2 * kH + 8;  // halves per row of a K = 256 operand ([e_ij | h_j])
-constexpr int kLdS1 = kH + 8;      // halves per row of a K = 128 operand
-typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
-
-// Four consecutive floats into the split slab at (row, col).
-__device__ inline void put_split4(_Float16* S, int rows, int ld, int row, int col, float4 v) {
-  const float f[4] = {v.x, v.y, v.z, v.w};
-  f16x4 h, l;
-#pragma unroll
-  for (int e = 0; e < 4; ++e) {
-    const _Float16 hi = static_cast<_Float16>(__builtin_amdgcn_fmed3f(f[e], -65504.0F, 65504.0F));
-    h[e] = hi;
-    l[e] = static_cast<_Float16>((f[e] - static_cast<float>(hi)) * 2048.0F);
-  }
-  *reinterpret_cast<f16x4*>(S + row * ld + col) = h;
-  *reinterpret_cast<f16x4*>(S + (rows + row) * ld + col) = l;
-}
-
-// acc[rb][nt][i] = sum_k A[16 rb + r][k] W[n0 + 16 nt + 4 g + i][k] over K
-// inputs (added to acc when accumulate), A the split slab (rows = 16 RB,
-// stride ld), W (128 outputs) split as hi [K / 8][128][8] halves with lo at
-// Wp + lo_off. Weight fragments stream through a ring of PF k-steps, so each
-// load is issued PF - 1 k-steps before its use.
-template <int RB, int K, int PF = 4>
-__device__ inline void tile_gemm(const _Float16* S, int ld, const uint16_t* __restrict__ Wp, int n0, size_t lo_off,
-                                 floatx4 (&acc)[RB][2], bool accumulate = false) {
-  constexpr int NKB = K / 32;
-  constexpr size_t kstep = (size_t)4 * kH * 8;  // halves per 32 inputs
-  static_assert(K % 32 == 0 && PF >= 2, "k-steps");
-  const int lane = threadIdx.x & 63, r = lane & 15, g = lane >> 4;
-  const _Float16* Sh = S + r * ld + 8 * g;
-  const _Float16* Sl = Sh + 16 * RB * ld;
-  const uint16_t* wh = Wp + ((size_t)g * kH + n0 + r) * 8;
-  const uint16_t* wl = wh + lo_off;
-  floatx4 cor[RB][2];
-#pragma unroll
-  for (int rb = 0; rb < RB; ++rb)
-#pragma unroll
-    for (int nt = 0; nt < 2; ++nt) {
-      cor[rb][nt] = floatx4{0.F, 0.F, 0.F, 0.F};
-      if (!accumulate) acc[rb][nt] = cor[rb][nt];
-    }
-  f16x8 bh[PF][2], bl[PF][2];
-#pragma unroll
-  for (int kb = 0; kb < PF - 1 && kb < NKB; ++kb)
-#pragma unroll
-    for (int nt = 0; nt < 2; ++nt) {
-      bh[kb][nt] = *reinterpret_cast<const f16x8*>(wh + kb * kstep + (size_t)nt * 16 * 8);
-      bl[kb][nt] = *reinterpret_cast<const f16x8*>(wl + kb * kstep + (size_t)nt * 16 * 8);
-    }
-#pragma unroll
-  for (int kb = 0; kb < NKB; ++kb) {
-    const int kn = kb + PF - 1;
-    if (kn < NKB) {
-#pragma unroll
-      for (int nt = 0; nt < 2; ++nt) {
-        bh[kn % PF][nt] = *reinterpret_cast<const f16x8*>(wh + kn * kstep + (size_t)nt * 16 * 8);
-        bl[kn % PF][nt] = *reinterpret_cast<const f16x8*>(wl + kn * kstep + (size_t)nt * 16 * 8);
-      }
-    }
-#pragma unroll
-    for (int rb = 0; rb < RB; ++rb) {
-      const f16x8 ah = *reinterpret_cast<const f16x8*>(Sh + 16 * rb * ld + 32 * kb);
-      const f16x8 al = *reinterpret_cast<const f16x8*>(Sl + 16 * rb * ld + 32 * kb);
-#pragma unroll
-      for (int nt = 0; nt < 2; ++nt) {
-        acc[rb][nt] = mfma_f16(bh[kb % PF][nt], ah, acc[rb][nt]);
-        cor[rb][nt] = mfma_f16(bh[kb % PF][nt], al, cor[rb][nt]);
-        cor[rb][nt] = mfma_f16(bl[kb % PF][nt], ah, cor[rb][nt]);
-      }
-    }
-  }
-#pragma unroll
-  for (int rb = 0; rb < RB; ++rb)
-#pragma unroll
-    for (int nt = 0; nt < 2; ++nt)
-#pragma unroll
-      for (int i = 0; i < 4; ++i) acc[rb][nt][i] += cor[rb][nt][i] * (1.0F / 2048.0F);
 }
 
 // The tile's rows [e_ij | h_j] (slot = slot_of(row); negative: a zero row;

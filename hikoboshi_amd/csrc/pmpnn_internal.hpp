@@ -166,6 +166,7 @@ struct DecodeArgs {
   int precision;          // 0 fp32, 1 bf16, 2 fp16 weights and message rows (see decode_kernel)
   int max_members;        // most steps one pass decodes (<= kDecodeGroup * team size)
   int pass_granule;       // team size the schedule balances passes for (<= 1: none)
+  const float* l0tab;     // [L][K][kL0Classes][128] layer-0 message rows (fp32 decode), or null
 };
 constexpr int kDecodeGroup = 4;  // steps one workgroup decodes in a pass
 // int32 words of DecodeArgs.sched_tmp for nq orders of length L with K neighbours.
@@ -185,6 +186,17 @@ int decode_team_size(int precision, int B, int max_team);
 hipError_t launch_decode(const ModelDev& m, const DecodeArgs& a, hipStream_t stream, int max_team = 8);
 // Q[l] = W1d_l h^0 (l < 3), Q[3] = W1a_0 h^0, without the E1 edge products.
 hipError_t launch_q_precompute(const ModelDev& m, const float* h_v, int L, float* Q, hipStream_t stream);
+// Layer-0 message table of the fp32 decode. Slot k of residue t sees its
+// neighbour j = idx[t][k] in one of kL0Classes states: decoded before t with
+// token c (c < kV), or not yet decoded / an empty slot (c = kV). Row
+// ((t K + k) kL0Classes + c) holds GELU(W2 GELU(A_t + E1_tk + z) + b2) for
+// that state's z, computed with the decode loop's own operations, so the
+// decode sums K rows instead of computing them. E1, Q as written by
+// launch_decoder_precompute.
+constexpr int kL0Classes = kV + 1;
+inline size_t l0_table_floats(size_t L, size_t K) { return L * K * kL0Classes * kH; }
+hipError_t launch_layer0_table(const ModelDev& m, const float* E1, const float* Q, const int32_t* idx, int L, int K,
+                               float* tab, hipStream_t stream);
 struct TfArgs {
   const int32_t* idx;     // [L][K] global neighbour indices
   const int32_t* pos;     // [L] position of each residue in its protein's decoding order

@@ -295,6 +295,33 @@ def test_design_dependency_schedule_long_chain(gpu_ctx, monkeypatch):
         np.testing.assert_array_equal(out["dependency"][key], out["sequential"][key], err_msg=key)
 
 
+@pytest.mark.parametrize("L,B,shared", [(120, 9, False), (300, 16, True), (30, 3, False)])
+def test_design_layer0_table_is_exact(gpu_ctx, oracle, L, B, shared, monkeypatch):
+    """The fp32 decode reading its layer-0 message rows from the precomputed table gives the bits of
+    computing them in the decode loop (HKBS_DECODE_L0TABLE=off): inactive residues (decoded before or
+    after their neighbours), a chain mask with true tokens, per-sequence and shared orders, K < 48."""
+    bb = backbone.single_chain(L, 6)
+    src = bb.atom_sources.copy()
+    src[[1, L // 2, L - 2], 1] = 0
+    bb = backbone.Backbone(bb.coords, src)
+    cm = np.ones(L, np.float32)
+    cm[L // 3:L // 3 + 5] = 0.0
+    tt = (np.arange(L) * 11 % 20).astype(np.int32)
+    seeds = (np.arange(B) + 41).astype(np.uint64)
+    kw = dict(order_mode=_lib.ORDER_INPUT_SHARED, orders=_lib.decode_order(bb.atom_sources, 41)) if shared else \
+        dict(order_seeds=seeds)
+    out = {}
+    for mode in ("off", "on"):
+        monkeypatch.setenv("HKBS_DECODE_L0TABLE", mode)
+        _say(f"design layer-0 table={mode} L={L} B={B}")
+        out[mode] = gpu_ctx.design(bb.coords, bb.atom_sources, B, seeds, temperature=0.1, chain_mask=cm,
+                                   true_tokens=tt, **kw)
+    for key in ("tokens", "log_probs", "scores", "orders"):
+        np.testing.assert_array_equal(out["on"][key], out["off"][key], err_msg=key)
+    check_design(oracle, bb, {k: v[:2] for k, v in out["on"].items()}, seeds[:2], 0.1, chain_mask=cm,
+                 true_tokens=tt)
+
+
 def test_design_team_barrier_timeout_reruns(gpu_ctx, monkeypatch):
     """A team barrier that gives up (forced here by a one-poll wait limit) leaves
     the kernel early with the fault word raised; the design call then decodes
