@@ -796,7 +796,8 @@ size_t decode_bytes(int L, int K, int B, bool l0table) {
          aligned_bytes<float>((size_t)B * kLayers * L * kH) + aligned_bytes<int32_t>((size_t)B * L) +
          aligned_bytes<float>((size_t)B * L * kV) + aligned_bytes<float>((size_t)B * L) + aligned_bytes<float>(B) +
          aligned_bytes<uint32_t>((size_t)B + 1) + 2 * aligned_bytes<int32_t>((size_t)B * L * K) +
-         schedule_bytes(L, K, B) + (l0table ? aligned_bytes<float>(l0_table_floats(L, K)) : 0);
+         schedule_bytes(L, K, B) + (l0table ? aligned_bytes<float>(l0_table_floats(L, K)) : 0) +
+         aligned_bytes<float4>((size_t)B * L * kRecFloat4);
 }
 
 hkbs_status enter(hkbs_pmpnn* ctx) {
@@ -821,7 +822,7 @@ size_t design_scratch_bytes(int L, int B, bool shared, bool l0table) {
          aligned_bytes<float>((size_t)B * kLayers * L * kH) + aligned_bytes<uint32_t>((size_t)B + 1) +
          2 * aligned_bytes<int32_t>(nq * L * K) + aligned_bytes<int32_t>(nq * L) + aligned_bytes<int32_t>(nq * (L + 2)) +
          aligned_bytes<int32_t>(nq) + aligned_bytes<int32_t>(nq * L) + aligned_bytes<int32_t>(sched_scratch_words(L, K, nq)) +
-         (l0table ? aligned_bytes<float>(l0_table_floats(L, K)) : 0);
+         (l0table ? aligned_bytes<float>(l0_table_floats(L, K)) : 0) + aligned_bytes<float4>(nq * L * kRecFloat4);
 }
 
 // Shared implementation of the device design path. All pointers device.
@@ -851,6 +852,7 @@ hkbs_status design_on_device(hkbs_pmpnn* ctx, const float* coords, const uint8_t
   int32_t* draw = ar.take<int32_t>(nq * L);
   int32_t* sched_tmp = ar.take<int32_t>(sched_scratch_words(L, K, nq));
   float* l0tab = l0table ? ar.take<float>(l0_table_floats(L, K)) : nullptr;
+  float4* rec = ar.take<float4>(nq * L * kRecFloat4);
   if (ar.used > ar.cap) return fail(HKBS_INTERNAL_ERROR, "design workspace exceeds its reservation");
   ctx->fault = sync + B;
   DecodeArgs a{};
@@ -886,6 +888,7 @@ hkbs_status design_on_device(hkbs_pmpnn* ctx, const float* coords, const uint8_t
   a.sched_tmp = sched_tmp;
   a.precision = ctx->precision;
   a.l0tab = l0tab;
+  a.rec = rec;
   const int team = decode_team_size(a.precision, B, 8);
   a.max_members = kDecodeGroup * team;
   a.pass_granule = team;
@@ -909,6 +912,7 @@ hkbs_status design_on_device(hkbs_pmpnn* ctx, const float* coords, const uint8_t
   if (l0tab) HK_CHECK(launch_layer0_table(ctx->model, E1, Q, e.idx, L, K, l0tab, ctx->stream), "layer-0 table failed");
   HK_CHECK(launch_zero(reinterpret_cast<float*>(sync), (size_t)B + 1, ctx->stream), "workspace clear failed");
   HK_CHECK(hipStreamWaitEvent(ctx->stream, ctx->join, 0), "stream wait failed");
+  HK_CHECK(launch_step_records(ctx->model, a, rec, ctx->stream), "step records launch failed");
   if (ctx->timing) HK_CHECK(hipEventRecord(ctx->ev[2], ctx->stream), "event record failed");
   HK_CHECK(launch_decode(ctx->model, a, ctx->stream, team), "decode launch failed");
   if (ctx->timing) {
@@ -1114,6 +1118,7 @@ hkbs_status hkbs_pmpnn_design(hkbs_pmpnn* ctx, const float* coords, const uint8_
     one.max_members = kDecodeGroup;  // steps one workgroup can hold
     one.pass_granule = 1;
     HK_CHECK(launch_decode_schedule(one, s), "decode schedule launch failed");
+    HK_CHECK(launch_step_records(ctx->model, one, const_cast<float4*>(one.rec), s), "step records launch failed");
     HK_CHECK(launch_decode(ctx->model, one, s, 1), "decode launch failed");
     HK_CHECK(hipMemcpyAsync(tokens, d_tokens, (size_t)B * L * 4, hipMemcpyDeviceToHost, s), "D2H failed");
     if (log_probs) HK_CHECK(hipMemcpyAsync(log_probs, d_lp, (size_t)B * L * kV * 4, hipMemcpyDeviceToHost, s), "D2H failed");

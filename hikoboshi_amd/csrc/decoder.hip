@@ -198,21 +198,25 @@ __device__ inline float4 load4_dev(const float* p) {
 
 constexpr uint32_t kSpinLimit = 1u << 20;  // default polls (~1 s) before a team gives up
 
-// Barrier over the P workgroups of a team. Every wave first waits for its own
-// memory operations (so its device-scope stores of exchanged state have
-// completed at the device coherence point) and the workgroup meets at a
-// barrier; thread 0 then counts the workgroup in with a device-scope atomic
-// and polls the count with device-scope loads until all P have arrived
-// `target / P` times, and the workgroup meets again. Exchanged state is read
-// only after that, and only with device-scope loads (load_dev, load4_dev), so
-// a member sees every store the others made before they arrived, wherever
-// the members run on the device. Returns false (and raises the fault word) if
-// the wait does not end; the caller then stops so that every wave exits.
-__device__ inline bool team_sync(uint32_t* counter, uint32_t target, uint32_t spin_limit, uint32_t* fault, int* bad) {
+// Split-phase barrier over the P workgroups of a team. team_arrive: every
+// wave first waits for its own memory operations (so its device-scope stores
+// of exchanged state have completed at the device coherence point) and the
+// workgroup meets at a barrier; thread 0 then counts the workgroup in with a
+// device-scope atomic. Work that reads no exchanged state may run between
+// arrive and wait. team_wait: thread 0 polls the count with device-scope
+// loads until all P have arrived `target / P` times, and the workgroup meets
+// again. Exchanged state is read only after that, and only with device-scope
+// loads (load_dev, load4_dev), so a member sees every store the others made
+// before they arrived, wherever the members run on the device. team_wait
+// returns false (and raises the fault word) if the wait does not end; the
+// caller then stops so that every wave exits.
+__device__ inline void team_arrive(uint32_t* counter) {
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
+  if (threadIdx.x == 0) __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ inline bool team_wait(uint32_t* counter, uint32_t target, uint32_t spin_limit, uint32_t* fault, int* bad) {
   if (threadIdx.x == 0) {
-    __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     uint32_t n = 0;
     while (__hip_atomic_load(counter, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < target) {
       __builtin_amdgcn_s_sleep(1);
@@ -271,8 +275,11 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(ModelDev m, DecodeArgs
   __shared__ int nbr[kGroup * kKmax];
   __shared__ int bwf[kGroup * kKmax];
   __shared__ int cls[kGroup * kKmax];  // layer-0 table class of each slot (with a.l0tab)
+  __shared__ __attribute__((aligned(16))) float q0s[kGroup * kH];  // Q^0 rows of the members (R^0 base)
   __shared__ int tres[kGroup];
-  __shared__ int ures[kGroup];
+  __shared__ int sdraw[kGroup];  // sampler draw index of each member
+  __shared__ float sdes[kGroup];  // design weight chain_mask * mask (0: keep the true token)
+  __shared__ int stt[kGroup];     // true token, or the fallback token
   __shared__ int tok_s[kGroup];
   __shared__ int bad;
 
@@ -348,43 +355,76 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(ModelDev m, DecodeArgs
           store_dev(R + ((size_t)l * L + t) * kH + c, base + m.dec[l].T[tok * kH + c]);
         }
       }
-      if (P > 1 && !team_sync(counter, ++passes * P, a.spin_limit, a.fault, &bad)) goto finish;
-      __syncthreads();
+      if (P > 1) team_arrive(counter);
     }
   }
+  // Inputs of a pass that no other workgroup writes come from its step
+  // records: one 16-byte slice per thread, loaded during the previous pass's
+  // logits and written to LDS once that pass is done with its copies (between
+  // the team barrier's arrive and wait).
+  const float4* rec = a.rec + qo * (size_t)L * kRecFloat4;
+  auto members = [&](int ps, int& s0) -> int {  // members of this rank in pass ps: rank + P i
+    s0 = pstart[ps];
+    const int mg = pstart[ps + 1] - s0;
+    return mg > rank ? (mg - rank + P - 1) / P : 0;
+  };
+  auto rec_load = [&](int s0, int mlp) -> float4 {
+    const int i = threadIdx.x / kRecFloat4;
+    if (mlp > kGroup || i >= mlp) return make_float4(0.F, 0.F, 0.F, 0.F);
+    return rec[(size_t)(s0 + rank + P * i) * kRecFloat4 + threadIdx.x % kRecFloat4];
+  };
+  auto rec_store = [&](int mlp, const float4& v) {
+    const int i = threadIdx.x / kRecFloat4, w = threadIdx.x % kRecFloat4;
+    if (mlp > kGroup || i >= mlp) return;
+    if (w < kKmax / 4) {
+      const int wd[4] = {__float_as_int(v.x), __float_as_int(v.y), __float_as_int(v.z), __float_as_int(v.w)};
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        nbr[i * kKmax + 4 * w + e] = wd[e] < 0 ? -1 : (wd[e] & 0x3FFFFFFF);
+        bwf[i * kKmax + 4 * w + e] = wd[e] >= 0 && (wd[e] & 0x40000000) != 0;
+      }
+    } else if (w == kKmax / 4) {
+      tres[i] = __float_as_int(v.x);
+      sdraw[i] = __float_as_int(v.y);
+      sdes[i] = v.z;
+      stt[i] = __float_as_int(v.w);
+    } else if (w >= 16) {
+      const int blk = (w - 16) / (kH / 4), c = 4 * ((w - 16) % (kH / 4));
+      float* dst = blk == 0 ? h : (blk == 1 ? hA : q0s);
+      *reinterpret_cast<float4*>(dst + i * kH + c) = v;
+    }
+  };
+  static_assert(kKmax % 4 == 0 && kRecFloat4 == 16 + 3 * kH / 4 && kRecFloat4 * kGroup <= kThreads, "record layout");
+  int ml = 0;
+  if (npass >= 1) {
+    int s0 = 0;
+    ml = members(1, s0);
+    rec_store(ml, rec_load(s0, ml));
+  }
+  if (P > 1 && pstart[1] > pstart[0]) {  // the pass-0 barrier
+    if (!team_wait(counter, ++passes * P, a.spin_limit, a.fault, &bad)) goto finish;
+  }
+  __syncthreads();
   for (int pass = 1; pass <= npass; ++pass) {
-    const int s0 = pstart[pass];
-    const int mg = pstart[pass + 1] - s0;
-    const int ml = mg > rank ? (mg - rank + P - 1) / P : 0;  // members of this rank: rank + P i
     if (ml > kGroup) {  // a schedule built for a larger team: refuse rather than overrun LDS
       if (threadIdx.x == 0) __hip_atomic_store(a.fault, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       bad = 1;
       break;
     }
+    int s0n = 0, mln = 0;  // the next pass
+    if (pass < npass) mln = members(pass + 1, s0n);
+    float4 rv = make_float4(0.F, 0.F, 0.F, 0.F);
+    bool staged = false;
     if (ml > 0) {
-      if (threadIdx.x < ml * K) {
-        const int i = threadIdx.x / K, k = threadIdx.x % K;
-        const int u = sched[s0 + rank + P * i];
-        const size_t at = (size_t)u * K + k;
-        const int j = nbj[at];
-        const bool bw = nbp[at] < u;  // empty slots hold position L
-        nbr[i * kKmax + k] = j;
-        bwf[i * kKmax + k] = bw;
-        if (PREC == kPrecFp32 && a.l0tab) cls[i * kKmax + k] = (j >= 0 && bw) ? load_dev(tokens + j) : kV;
-        if (k == 0) {
-          tres[i] = order[u];
-          ures[i] = u;
-        }
-      }
-      for (int task = threadIdx.x; task < ml * kH; task += kThreads) {
-        const int i = task / kH, c = task % kH;
-        const int t = order[sched[s0 + rank + P * i]];
-        h[i * kH + c] = a.h_v[(size_t)t * kH + c];
-        // layer-0 W1a h^0_t comes from the precompute (Q block 3)
-        hA[i * kH + c] = a.Q[((size_t)3 * L + t) * kH + c] + prm[kPrmB1 + c];
-      }
-      __syncthreads();
       if (PREC == kPrecFp32 && a.l0tab) {
+        // layer-0 table class of each slot: the token of a neighbour decoded before
+        // the step (written by the team before the last barrier), else kV
+        if (threadIdx.x < ml * K) {
+          const int i = threadIdx.x / K, k = threadIdx.x % K;
+          const int j = nbr[i * kKmax + k];
+          cls[i * kKmax + k] = (j >= 0 && bwf[i * kKmax + k]) ? load_dev(tokens + j) : kV;
+        }
+        __syncthreads();
         // x[i] = sum over slots of table rows, in the order of the MFMA path
         // below: lane group g (rows 16 mb + 4 g + e, mb outer) sums its rows,
         // then the four groups add as (g0 + g1) + (g2 + g3).
@@ -643,6 +683,8 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(ModelDev m, DecodeArgs
           __syncthreads();
         }
       }
+      rv = rec_load(s0n, mln);  // the next pass's records, in flight during logits and sampling
+      staged = true;
       // logits = W_out h + b (padded to 32 outputs), then one draw per member.
       {
         float4 acc[kGroup];
@@ -660,12 +702,9 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(ModelDev m, DecodeArgs
         const int i = wave;
         const int t = tres[i];
         float lpv;
-        const uint64_t state = seed + (uint64_t)draw[ures[i]] * 0x9E3779B97F4A7C15ull;
+        const uint64_t state = seed + (uint64_t)sdraw[i] * 0x9E3779B97F4A7C15ull;
         const int s_tok = sample_wave(logits + i * 32, T, greedy, state, &lpv);
-        const float design = (a.chain_mask ? a.chain_mask[t] : 1.0F) * a.mask[t];
-        int tok = s_tok;
-        if (design == 0.0F)
-          tok = (a.true_tokens && a.true_tokens[t] >= 0 && a.true_tokens[t] < kV) ? a.true_tokens[t] : kV - 1;
+        const int tok = sdes[i] == 0.0F ? stt[i] : s_tok;
         if (lp_out && lane < kV) lp_out[(size_t)t * kV + lane] = lpv;
         if (lane == tok) store_dev(chosen + t, lpv);
         if (lane == 0) {
@@ -677,11 +716,19 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(ModelDev m, DecodeArgs
       for (int task = threadIdx.x; task < ml * kLayers * kH; task += kThreads) {
         const int i = task / (kLayers * kH), l = (task / kH) % kLayers, c = task % kH;
         const int t = tres[i];
-        const float base = (l == 0) ? a.Q[(size_t)t * kH + c] : Pd[(i * 2 + l - 1) * kH + c];
+        const float base = (l == 0) ? q0s[i * kH + c] : Pd[(i * 2 + l - 1) * kH + c];
         store_dev(R + ((size_t)l * L + t) * kH + c, base + m.dec[l].T[tok_s[i] * kH + c]);
       }
     }
-    if (P > 1 && !team_sync(counter, ++passes * P, a.spin_limit, a.fault, &bad)) break;
+    if (!staged) rv = rec_load(s0n, mln);
+    // this pass's LDS state is consumed (team_arrive starts with a barrier)
+    if (P > 1)
+      team_arrive(counter);
+    else
+      __syncthreads();
+    rec_store(mln, rv);
+    ml = mln;
+    if (P > 1 && !team_wait(counter, ++passes * P, a.spin_limit, a.fault, &bad)) break;
     __syncthreads();
   }
 finish:
@@ -824,6 +871,49 @@ __global__ __launch_bounds__(kThreads, 4) void layer0_table_kernel(ModelDev m, c
       }
     __syncthreads();
   }
+}
+
+// Step records (launch_step_records): block (s, q) writes record s of order q.
+__global__ __launch_bounds__(128) void step_records_kernel(ModelDev m, DecodeArgs a, float4* __restrict__ rec) {
+  const int s = blockIdx.x, q = blockIdx.y, w = threadIdx.x;
+  if (w >= kRecFloat4) return;
+  const int L = a.L, K = a.K;
+  const int32_t* order = a.shared_order ? a.orders : a.orders + (size_t)q * L;
+  const int u = a.sched[(size_t)q * L + s];
+  const int t = (u >= 0 && u < L) ? order[u] : -1;
+  float4 v = make_float4(0.F, 0.F, 0.F, 0.F);
+  if (t >= 0 && t < L) {
+    if (w < kKmax / 4) {
+      int wd[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int k = 4 * w + e;
+        wd[e] = -1;
+        if (k < K) {
+          const size_t at = ((size_t)q * L + u) * K + k;
+          const int j = a.nbj[at];
+          if (j >= 0) wd[e] = j | (a.nbp[at] < u ? 0x40000000 : 0);
+        }
+      }
+      v = make_float4(__int_as_float(wd[0]), __int_as_float(wd[1]), __int_as_float(wd[2]), __int_as_float(wd[3]));
+    } else if (w == kKmax / 4) {
+      const int tt = (a.true_tokens && a.true_tokens[t] >= 0 && a.true_tokens[t] < kV) ? a.true_tokens[t] : kV - 1;
+      v = make_float4(__int_as_float(t), __int_as_float(a.draw[(size_t)q * L + u]),
+                      (a.chain_mask ? a.chain_mask[t] : 1.0F) * a.mask[t], __int_as_float(tt));
+    } else if (w >= 16) {
+      const int blk = (w - 16) / (kH / 4), c = 4 * ((w - 16) % (kH / 4));
+      if (blk == 0) {
+        v = *reinterpret_cast<const float4*>(a.h_v + (size_t)t * kH + c);
+      } else if (blk == 1) {  // W1a_0 h^0_t + b1_0 (Q block 3)
+        const float4 qv = *reinterpret_cast<const float4*>(a.Q + ((size_t)3 * L + t) * kH + c);
+        const float* b1 = m.dec[0].b1 + c;
+        v = make_float4(qv.x + b1[0], qv.y + b1[1], qv.z + b1[2], qv.w + b1[3]);
+      } else {
+        v = *reinterpret_cast<const float4*>(a.Q + (size_t)t * kH + c);
+      }
+    }
+  }
+  rec[((size_t)q * L + s) * kRecFloat4 + w] = v;
 }
 
 // out[c][row][:] = A[row] . Wp(cols 128c..128c+127) for a [M,128] input.
@@ -1324,6 +1414,14 @@ hipError_t launch_q_precompute(const ModelDev& m, const float* h_v, int L, float
   if (L <= 0) return hipSuccess;
   rows_gemm_kernel<<<dim3((unsigned)((L + kGemmRows - 1) / kGemmRows), kLayers + 1), 256, 0, stream>>>(
       h_v, (size_t)L, m.W1d_dec_p, (kLayers + 1) * kH, Q);
+  return hipGetLastError();
+}
+
+hipError_t launch_step_records(const ModelDev& m, const DecodeArgs& a, float4* rec, hipStream_t stream) {
+  if (a.L <= 0 || a.B <= 0) return hipSuccess;
+  if (a.K > kKmax) return hipErrorInvalidValue;
+  const int nq = a.shared_order ? 1 : a.B;
+  step_records_kernel<<<dim3((unsigned)a.L, (unsigned)nq), 128, 0, stream>>>(m, a, rec);
   return hipGetLastError();
 }
 

@@ -167,6 +167,7 @@ struct DecodeArgs {
   int max_members;        // most steps one pass decodes (<= kDecodeGroup * team size)
   int pass_granule;       // team size the schedule balances passes for (<= 1: none)
   const float* l0tab;     // [L][K][kL0Classes][128] layer-0 message rows (fp32 decode), or null
+  const float4* rec;      // [nq][L][kRecFloat4] per-step inputs in schedule order (launch_step_records)
 };
 constexpr int kDecodeGroup = 4;  // steps one workgroup decodes in a pass
 // int32 words of DecodeArgs.sched_tmp for nq orders of length L with K neighbours.
@@ -175,6 +176,16 @@ inline size_t sched_scratch_words(size_t L, size_t K, size_t nq) { return nq * (
 // a.pstart, a.npass, a.draw) from the orders, positions, mask and kNN graph;
 // launch_decode reads them.
 hipError_t launch_decode_schedule(const DecodeArgs& a, hipStream_t stream);
+// Per-step inputs of the decode in schedule order (after launch_decode_schedule
+// and the decoder precompute): record s of order q describes step
+// u = sched[q][s] (residue t = order[u]) as 112 float4: words 0..47 the
+// neighbour slots (j | 2^30 if j is decoded before the step, -1 for an empty
+// slot), word 48 t, 49 the draw index, 50 the design weight chain_mask[t]
+// mask[t] (float bits), 51 the true token or the fallback token, 52..63 zero,
+// then the rows h^0_t, W1a_0 h^0_t + b1_0 and W1d_0 h^0_t (128 floats each).
+// The decode stages a pass's members with one 16-byte load per thread.
+constexpr int kRecFloat4 = 112;
+hipError_t launch_step_records(const ModelDev& m, const DecodeArgs& a, float4* rec, hipStream_t stream);
 // Workgroups per sequence the decode will use for B sequences (1..min(8, max_team)).
 int decode_team_size(int precision, int B, int max_team);
 // Decodes with up to min(8, max_team) workgroups per sequence when the whole
