@@ -447,7 +447,7 @@ hkbs_status build_model(hkbs_pmpnn* ctx, const float* const* t) {
     size_t pos_w, pos_b, edge_t, ne_g, ne_b, We_t, We_b, Ws;
     size_t W1b_dec_p, W1d_dec_p, Wlog_t, blog, Wlog_h, Wlog_f;
     size_t enc[kLayers][22];
-    size_t dec[kLayers][22];
+    size_t dec[kLayers][23];
     size_t dec_h[kLayers][4];  // bf16 copies of W3_t, Win_t, Wout_t, W1da_t
     size_t dec_f[kLayers][4];  // fp16 copies of the same
     size_t enc16[2 + 8 * kLayers];  // split-fp16 encoder weights: W_edge, W_e, then per layer
@@ -544,6 +544,12 @@ hkbs_status build_model(hkbs_pmpnn* ctx, const float* const* t) {
       q[6] = copy_raw(ar, T.data(), T.size());
     }
     q[20] = pack_f16_split(ar, d[2], 128, 128);       // W2 hi, lo (fp16)
+    {
+      std::vector<float> w1b(128 * 128);  // W1b (inputs 128..255 of W1)
+      for (int n = 0; n < 128; ++n)
+        for (int k = 0; k < 128; ++k) w1b[(size_t)n * 128 + k] = d[0][(size_t)n * 512 + 128 + k];
+      q[22] = pack_f16_split(ar, w1b.data(), 128, 128);  // W1b hi, lo (fp16)
+    }
     q[21] = pack_bf16_k8(ar, d[2], 128, 128);         // W2 (bf16)
     q[16] = pack_k16(ar, {d[4]}, 128, 128, 0, 128);   // W3_p
     q[17] = pack_k16(ar, {d[10]}, 512, 128, 0, 128);  // Win_p
@@ -626,6 +632,7 @@ hkbs_status build_model(hkbs_pmpnn* ctx, const float* const* t) {
     w.W2_p = B + q[1];
     w.W2h = B + q[20];
     w.W2l = B + q[20] + 128 * 128 / 2;
+    w.W1b_s = reinterpret_cast<const uint16_t*>(B + q[22]);
     w.W2_b = reinterpret_cast<const uint16_t*>(B + q[21]);
     w.W3_h = reinterpret_cast<const uint16_t*>(B + o.dec_h[l][0]);
     w.Win_h = reinterpret_cast<const uint16_t*>(B + o.dec_h[l][1]);

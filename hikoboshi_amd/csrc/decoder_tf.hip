@@ -8,17 +8,20 @@
 //   bw (j before t): [h_E_tj, W_s[tok_j], h^l_j],  fw: [h_E_tj, 0, h^0_j],
 // both scaled by the row mask. As in the autoregressive kernel the W1 product
 // is split into A_t = W1a h^l_t + b1, E1 = W1b h_E (here computed in the edge
-// kernel on MFMA, every edge is used once per layer), R^l_j = W1d h^l_j +
+// kernel, every edge is used once per layer), R^l_j = W1d h^l_j +
 // W1c W_s[tok_j] and Q^l_j = W1d h^0_j; and sum_k (W3 g_k + b3) = W3 sum_k g_k + K b3.
 // Per layer:
-//   tf_edge_kernel  tiles of whole residues (<= 96 edge rows): W1b and W2 on
-//                   fp32 MFMA, GELU, neighbour sum (all K slots, no attention mask).
+//   tf_edge_kernel  tiles of whole residues (<= 96 edge rows): W1b and W2 on the
+//                   fp16 MFMA with split operands (hi + lo / 2048 for weights and
+//                   rows, about 22 significant bits), GELU, neighbour sum (all K
+//                   slots, no attention mask).
 //   tf_node_kernel  tiles of 16 residues: W3, LN1, FFN, LN2, row-mask gate,
 //                   then the next layer's [A | R] terms, or for the last layer
 //                   logits and log_softmax in the reference's order.
 // Rows may belong to different proteins of a ragged batch: every neighbour
 // index is global, so the kernels never look at protein boundaries.
 #include "device_math.hpp"
+#include "mfma_tile.hpp"
 #include "pmpnn_internal.hpp"
 
 namespace hkbs {
@@ -39,43 +42,22 @@ __global__ void tf_init_kernel(ModelDev m, const float* __restrict__ Q, const in
   NB[r * 256 + kH + c] = Q[r * kH + c] + m.dec[0].T[tokens[r] * kH + c];
 }
 
-// acc[mb][nb][i] = sum_k A[16 mb + r][k] W[n0 + 16 nb + 4 g + i][k] on the fp32
-// MFMA: mfma_tile with the operands exchanged (weights as the MFMA's A
-// operand), so that lane (r, g) holds row 16 mb + r and four consecutive
-// output columns.
-template <int MB, int NB>
-__device__ inline void mfma_tile_rows(const float* __restrict__ A, int lda, const float* __restrict__ Wp, int N,
-                                      int n0, int kdim, floatx4 (&acc)[MB][NB]) {
-  const int lane = threadIdx.x & 63;
-  const int r = lane & 15;
-  const int g = lane >> 4;
-  for (int kb = 0; kb < kdim / 16; ++kb) {
-    float4 a[MB];
-    float4 b[NB];
-#pragma unroll
-    for (int nb = 0; nb < NB; ++nb)
-      b[nb] = *reinterpret_cast<const float4*>(Wp + ((size_t)kb * N + n0 + nb * 16 + r) * 16 + 4 * g);
-#pragma unroll
-    for (int mb = 0; mb < MB; ++mb)
-      a[mb] = *reinterpret_cast<const float4*>(A + (mb * 16 + r) * lda + kb * 16 + 4 * g);
-#pragma unroll
-    for (int mb = 0; mb < MB; ++mb)
-#pragma unroll
-      for (int nb = 0; nb < NB; ++nb) {
-        acc[mb][nb] = mfma16(b[nb].x, a[mb].x, acc[mb][nb]);
-        acc[mb][nb] = mfma16(b[nb].y, a[mb].y, acc[mb][nb]);
-        acc[mb][nb] = mfma16(b[nb].z, a[mb].z, acc[mb][nb]);
-        acc[mb][nb] = mfma16(b[nb].w, a[mb].w, acc[mb][nb]);
-      }
-  }
-}
+// Edge rows of a tile as split fp16 operands: two half-tiles of 48 rows, each
+// hi [48][kLdS1] then lo [48][kLdS1] (the layout of tile_gemm).
+constexpr int kHalfRows = kRows / 2;
+constexpr int kHalfRB = kHalfRows / 16;
+constexpr int kHalfSlab = 2 * kHalfRows * kLdS1;  // halves
 
-__global__ __launch_bounds__(256, 2) void tf_edge_kernel(DecLayerDev w, const float* __restrict__ W1b_p, int layer,
-                                                      const float* __restrict__ h_e, const int32_t* __restrict__ idx,
-                                                      const int32_t* __restrict__ pos, const float* __restrict__ mask,
-                                                      const float* __restrict__ NB, const float* __restrict__ Ql, int L,
-                                                      int K, float* __restrict__ msg_sum) {
-  __shared__ __attribute__((aligned(16))) float A[kRows * kLd];
+__global__ __launch_bounds__(256, 2) void tf_edge_kernel(DecLayerDev w, const float* __restrict__ h_e,
+                                                      const int32_t* __restrict__ idx, const int32_t* __restrict__ pos,
+                                                      const float* __restrict__ mask, const float* __restrict__ NB,
+                                                      const float* __restrict__ Ql, int L, int K,
+                                                      float* __restrict__ msg_sum) {
+  // The two half-tile slabs; once the W2 product has read them, the same bytes
+  // hold the fp32 message rows [kRows][kLd] for the neighbour sums.
+  __shared__ __attribute__((aligned(16))) _Float16 S[2 * kHalfSlab];
+  float* A = reinterpret_cast<float*>(S);
+  static_assert(kRows * kLd * sizeof(float) <= sizeof(S), "fp32 rows alias the slabs");
   __shared__ __attribute__((aligned(16))) float gtab[kGeluPolyRows * 8];
   // per edge row, formed once: its residue t, and its neighbour j with the
   // backward flag (pos[j] < pos[t]) in bit 31, or -1 when the slot adds nothing
@@ -96,8 +78,8 @@ __global__ __launch_bounds__(256, 2) void tf_edge_kernel(DecLayerDev w, const fl
     row_j[row] = (j >= 0 && j < L && mask[t] != 0.0F) ? (j | (pos[j] < pos[t] ? (int)0x80000000u : 0)) : -1;
   }
   {
-    // the tile's h_E rows: thread (wave w, lane c) loads float4 column c % 32 of rows 2 w + c / 32 + 8 i,
-    // all loads issued before the first store
+    // the tile's h_E rows, split: thread (wave w, lane c) loads float4 column c % 32 of rows
+    // 2 w + c / 32 + 8 i, all loads issued before the first store
     constexpr int N = kRows * (kH / 4) / 256;
     float4 v[N];
 #pragma unroll
@@ -107,69 +89,79 @@ __global__ __launch_bounds__(256, 2) void tf_edge_kernel(DecLayerDev w, const fl
                           : make_float4(0.F, 0.F, 0.F, 0.F);
     }
 #pragma unroll
-    for (int i = 0; i < N; ++i)
-      *reinterpret_cast<float4*>(A + (2 * wave + (lane >> 5) + 8 * i) * kLd + 4 * (lane & 31)) = v[i];
-  }
-  __syncthreads();
-  // x = A_t + (E1 + (bw ? R_j : Q_j)) for a slot that adds something, else A_t; its GELU into A.
-  // The A and R|Q rows load before the E1 product.
-  float4 base[6][2], nbr[6][2];
-#pragma unroll
-  for (int mb = 0; mb < 6; ++mb) {
-    const int row = mb * 16 + r;
-    const int t = row < n_rows ? row_t[row] : 0;
-    const int jb = row < n_rows ? row_j[row] : -1;
-    const int j = jb & 0x7FFFFFFF;
-#pragma unroll
-    for (int nb = 0; nb < 2; ++nb) {
-      const int c0 = wave * 32 + nb * 16 + 4 * g;
-      base[mb][nb] = row < n_rows ? *reinterpret_cast<const float4*>(NB + (size_t)t * 256 + c0)
-                                  : make_float4(0.F, 0.F, 0.F, 0.F);
-      nbr[mb][nb] = jb == -1 ? make_float4(0.F, 0.F, 0.F, 0.F)
-                             : *reinterpret_cast<const float4*>(jb < 0 ? NB + (size_t)j * 256 + kH + c0
-                                                                       : Ql + (size_t)j * kH + c0);
+    for (int i = 0; i < N; ++i) {
+      const int row = 2 * wave + (lane >> 5) + 8 * i;
+      put_split4(S + (row / kHalfRows) * kHalfSlab, kHalfRows, kLdS1, row % kHalfRows, 4 * (lane & 31), v[i]);
     }
   }
-  floatx4 acc[6][2];
-  zero_acc(acc);
-  mfma_tile_rows<6, 2>(A, kLd, W1b_p, kLayers * kH, layer * kH + wave * 32, kH, acc);
   __syncthreads();
+  // Per half-tile: x = A_t + (E1 + (bw ? R_j : Q_j)) for a slot that adds something, else A_t, with
+  // E1 = W1b h_E; GELU(x) replaces the half's h_E rows. The A and R|Q rows load before the E1 product.
+#pragma unroll 1
+  for (int hf = 0; hf < 2; ++hf) {
+    _Float16* Sh = S + hf * kHalfSlab;
+    float4 base[kHalfRB][2], nbr[kHalfRB][2];
 #pragma unroll
-  for (int mb = 0; mb < 6; ++mb) {
-    const int row = mb * 16 + r;
-    const bool adds = row < n_rows && row_j[row] != -1;
+    for (int mb = 0; mb < kHalfRB; ++mb) {
+      const int row = hf * kHalfRows + mb * 16 + r;
+      const int t = row < n_rows ? row_t[row] : 0;
+      const int jb = row < n_rows ? row_j[row] : -1;
+      const int j = jb & 0x7FFFFFFF;
 #pragma unroll
-    for (int nb = 0; nb < 2; ++nb) {
-      const int c0 = wave * 32 + nb * 16 + 4 * g;
-      float4 o = make_float4(0.F, 0.F, 0.F, 0.F);
-      if (row < n_rows) {
-        const float4 x = base[mb][nb], e = nbr[mb][nb];
-        const floatx4 y = acc[mb][nb];
-        o = adds ? make_float4(gelu_poly(x.x + (y[0] + e.x), gtab), gelu_poly(x.y + (y[1] + e.y), gtab),
-                               gelu_poly(x.z + (y[2] + e.z), gtab), gelu_poly(x.w + (y[3] + e.w), gtab))
-                 : make_float4(gelu_poly(x.x, gtab), gelu_poly(x.y, gtab), gelu_poly(x.z, gtab),
-                               gelu_poly(x.w, gtab));
+      for (int nb = 0; nb < 2; ++nb) {
+        const int c0 = wave * 32 + nb * 16 + 4 * g;
+        base[mb][nb] = row < n_rows ? *reinterpret_cast<const float4*>(NB + (size_t)t * 256 + c0)
+                                    : make_float4(0.F, 0.F, 0.F, 0.F);
+        nbr[mb][nb] = jb == -1 ? make_float4(0.F, 0.F, 0.F, 0.F)
+                               : *reinterpret_cast<const float4*>(jb < 0 ? NB + (size_t)j * 256 + kH + c0
+                                                                         : Ql + (size_t)j * kH + c0);
       }
-      *reinterpret_cast<float4*>(A + row * kLd + c0) = o;
+    }
+    floatx4 acc[kHalfRB][2];
+    tile_gemm<kHalfRB, kH>(Sh, kLdS1, w.W1b_s, wave * 32, (size_t)kH * kH, acc);
+    __syncthreads();  // every wave is done with this half's h_E rows
+#pragma unroll
+    for (int mb = 0; mb < kHalfRB; ++mb) {
+      const int row = hf * kHalfRows + mb * 16 + r;
+      const bool adds = row < n_rows && row_j[row] != -1;
+#pragma unroll
+      for (int nb = 0; nb < 2; ++nb) {
+        const int c0 = wave * 32 + nb * 16 + 4 * g;
+        float4 o = make_float4(0.F, 0.F, 0.F, 0.F);
+        if (row < n_rows) {
+          const float4 x = base[mb][nb], e = nbr[mb][nb];
+          const floatx4 y = acc[mb][nb];
+          o = adds ? make_float4(gelu_poly(x.x + (y[0] + e.x), gtab), gelu_poly(x.y + (y[1] + e.y), gtab),
+                                 gelu_poly(x.z + (y[2] + e.z), gtab), gelu_poly(x.w + (y[3] + e.w), gtab))
+                   : make_float4(gelu_poly(x.x, gtab), gelu_poly(x.y, gtab), gelu_poly(x.z, gtab),
+                                 gelu_poly(x.w, gtab));
+        }
+        put_split4(Sh, kHalfRows, kLdS1, mb * 16 + r, c0, o);
+      }
     }
   }
   __syncthreads();
-  zero_acc(acc);
-  mfma_tile_rows<6, 2>(A, kLd, w.W2_p, kH, wave * 32, kH, acc);
-  __syncthreads();
+  floatx4 acc2[2][kHalfRB][2];
+#pragma unroll
+  for (int hf = 0; hf < 2; ++hf)
+    tile_gemm<kHalfRB, kH>(S + hf * kHalfSlab, kLdS1, reinterpret_cast<const uint16_t*>(w.W2h), wave * 32,
+                           (size_t)kH * kH, acc2[hf]);
+  __syncthreads();  // the slabs are consumed; A reuses their bytes
 #pragma unroll
   for (int nb = 0; nb < 2; ++nb) {
     const int c0 = wave * 32 + nb * 16 + 4 * g;
     const float4 bv = *reinterpret_cast<const float4*>(w.b2 + c0);
 #pragma unroll
-    for (int mb = 0; mb < 6; ++mb) {
-      const int row = mb * 16 + r;
-      const floatx4 y = acc[mb][nb];
-      *reinterpret_cast<float4*>(A + row * kLd + c0) =
-          row < n_rows ? make_float4(gelu_poly(y[0] + bv.x, gtab), gelu_poly(y[1] + bv.y, gtab),
-                                     gelu_poly(y[2] + bv.z, gtab), gelu_poly(y[3] + bv.w, gtab))
-                       : make_float4(0.F, 0.F, 0.F, 0.F);
-    }
+    for (int hf = 0; hf < 2; ++hf)
+#pragma unroll
+      for (int mb = 0; mb < kHalfRB; ++mb) {
+        const int row = hf * kHalfRows + mb * 16 + r;
+        const floatx4 y = acc2[hf][mb][nb];
+        *reinterpret_cast<float4*>(A + row * kLd + c0) =
+            row < n_rows ? make_float4(gelu_poly(y[0] + bv.x, gtab), gelu_poly(y[1] + bv.y, gtab),
+                                       gelu_poly(y[2] + bv.z, gtab), gelu_poly(y[3] + bv.w, gtab))
+                         : make_float4(0.F, 0.F, 0.F, 0.F);
+      }
   }
   __syncthreads();
   for (int task = threadIdx.x; task < nr * kH; task += blockDim.x) {
@@ -312,7 +304,7 @@ hipError_t launch_teacher_forced(const ModelDev& m, const TfArgs& a, hipStream_t
   const unsigned edge_tiles = (unsigned)((L + nres - 1) / nres);
   const unsigned node_tiles = (unsigned)((L + 15) / 16);
   for (int l = 0; l < kLayers; ++l) {
-    tf_edge_kernel<<<edge_tiles, 256, 0, stream>>>(m.dec[l], m.W1b_dec_p, l, a.h_e, a.idx, a.pos, a.mask, a.NB,
+    tf_edge_kernel<<<edge_tiles, 256, 0, stream>>>(m.dec[l], a.h_e, a.idx, a.pos, a.mask, a.NB,
                                                    a.Q + (size_t)l * L * kH, L, K, a.msg_sum);
     tf_node_kernel<<<node_tiles, 256, 0, stream>>>(m, l, a.msg_sum, a.mask, a.tokens, L, K, a.h, a.NB, a.log_probs);
   }

@@ -58,6 +58,7 @@ struct DecLayerDev {
   const float* W2_p;   // kpack16 128 -> 128
   const float* W2h;    // [16][128][8] fp16: W2 = W2h + W2l / 2048 (decode loop)
   const float* W2l;
+  const uint16_t* W1b_s;  // W1b [16][128][8] fp16 hi, then lo (lo follows 128 * 128 halves later): teacher forcing
   // bf16 copies for the bf16 decode (round to nearest even; same layouts as
   // the fp32 t-layouts, W2 as [16][128][8] like W2h)
   const uint16_t *W2_b, *W3_h, *Win_h, *Wout_h, *W1da_h;
