@@ -1010,7 +1010,7 @@ __global__ void neighbour_schedule_kernel(const int32_t* __restrict__ orders, co
 // balanced passes) and the pass loop, with the pending counts as bytes in LDS.
 constexpr int kSchedThreads = 512;
 constexpr int kSchedMaxL = 60000;  // pending counts as L bytes of LDS
-constexpr int kSchedPrioMaxL = 8192;  // balanced passes up to this length (heights as 2 L bytes of LDS)
+constexpr int kSchedPrioMaxL = 8192;  // balanced passes up to this length (heights, counts, frontier: 2 L bytes of LDS each)
 constexpr int kSchedCand = 1024;      // ready steps a balanced pass chooses from
 
 // Active step u of order q: valid residue with mask != 0.
@@ -1137,16 +1137,34 @@ __global__ void dep_fill_kernel(const int32_t* __restrict__ orders, const float*
 // inactive or dropped.
 __device__ inline int sched_pending(const uint32_t* w, int u) { return (w[u >> 2] >> (8 * (u & 3))) & 0xFF; }
 
+// Ready steps (pending count 0) among the 8 steps 8 i .. 8 i + 7 as a bit mask
+// (bit b: step 8 i + b); words words .. of the count array read as all placed.
+__device__ inline uint32_t sched_ready8(const uint32_t* w, int words, int i) {
+  const uint32_t a = 2 * i < words ? w[2 * i] : 0xFFFFFFFFu;
+  const uint32_t b = 2 * i + 1 < words ? w[2 * i + 1] : 0xFFFFFFFFu;
+  uint32_t m = 0;
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    m |= (((a >> (8 * k)) & 0xFFu) == 0u ? 1u : 0u) << k;
+    m |= (((b >> (8 * k)) & 0xFFu) == 0u ? 1u : 0u) << (4 + k);
+  }
+  return m;
+}
+
 // Height of every active step of one order: 1 + the largest height among the
 // later steps that wait for it, 1 when none does (the longest chain of
-// dependent steps it starts). Computed in rounds: round r gives height r to
-// the steps whose dependents all have heights, then takes them off their own
-// earlier neighbours' counts of dependents still without one. ht[u] = 0xFFFF
-// for an inactive step; outw holds those counts as 16-bit halves. Returns the
-// number of rounds, the longest chain. Every round places at least one step
-// (dependencies run from smaller to larger u), so the loop ends.
+// dependent steps it starts). Computed in rounds over a frontier list: round r
+// gives height r to the steps in its frontier (all of whose dependents have
+// heights), then takes them off their own earlier neighbours' counts of
+// dependents still without one; a neighbour whose count reaches zero joins the
+// next frontier. Round 1's frontier is every active step no step waits for.
+// ht[u] = 0xFFFF for an inactive step; outw holds the counts as 16-bit halves;
+// list (nact 16-bit entries, L <= kSchedPrioMaxL) receives the frontiers one
+// after another. Returns the
+// number of rounds, the longest chain. The work is proportional to the
+// dependency pairs, not to L per round.
 __device__ int sched_heights(const int32_t* order, const float* mask, const int32_t* np, const int32_t* oq,
-                             int L, int K, int nact, uint16_t* ht, uint32_t* outw, int* list, int* tmp) {
+                             int L, int K, uint16_t* ht, uint32_t* outw, uint16_t* list, int* tmp, int* tail) {
   uint16_t* outc = reinterpret_cast<uint16_t*>(outw);
   for (int u = threadIdx.x; u < L; u += kSchedThreads) {
     const bool a = sched_active(order, mask, L, u);
@@ -1154,37 +1172,37 @@ __device__ int sched_heights(const int32_t* order, const float* mask, const int3
     outc[u] = (uint16_t)(a ? oq[u + 1] - oq[u] : 0);  // < L <= kSchedPrioMaxL
   }
   __syncthreads();
+  int n = 0;
+  for (int c0 = 0; c0 < L; c0 += kSchedThreads) {
+    const int u = c0 + threadIdx.x;
+    const bool sink = u < L && ht[u] == 0 && outc[u] == 0;
+    int tot;
+    const int r = block_scan(sink ? 1 : 0, tmp, &tot);
+    if (sink) list[n + r] = (uint16_t)u;
+    n += tot;
+  }
+  if (threadIdx.x == 0) *tail = n;
+  __syncthreads();
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  int rounds = 0, left = nact;
-  while (left > 0) {
+  int start = 0, end = n, rounds = 0;
+  while (start < end) {
     ++rounds;
-    int got = 0;
-    // Blocks of kSchedThreads steps in increasing u. A step placed here only
-    // lowers the counts of smaller steps, whose blocks this round has already
-    // examined, so no step gets the height of a dependent placed this round.
-    for (int c0 = 0; c0 < L; c0 += kSchedThreads) {
-      const int u = c0 + threadIdx.x;
-      const bool now = u < L && ht[u] == 0 && outc[u] == 0;
-      int tot;
-      const int r = block_scan(now ? 1 : 0, tmp, &tot);
-      if (now) {
-        ht[u] = (uint16_t)rounds;
-        list[r] = u;
-      }
-      __syncthreads();
-      // wave w takes the placed steps w, w + 8, ...; lane k their slot k (K <= 64)
-      for (int i = wave; i < tot; i += kSchedThreads / 64) {
-        const int v = list[i];
-        if (lane < K) {
-          const int p = np[(size_t)v * K + lane];
-          if (p >= 0 && p < v && ht[p] != 0xFFFF) atomicSub(outw + (p >> 1), 1u << (16 * (p & 1)));
+    for (int i = start + threadIdx.x; i < end; i += kSchedThreads) ht[list[i]] = (uint16_t)rounds;
+    // wave w takes the frontier's steps w, w + 8, ...; lane k their slot k (K <= 64)
+    for (int i = start + wave; i < end; i += kSchedThreads / 64) {
+      const int v = list[i];
+      if (lane < K) {
+        const int p = np[(size_t)v * K + lane];
+        if (p >= 0 && p < v && ht[p] != 0xFFFF) {
+          const uint32_t old = atomicSub(outw + (p >> 1), 1u << (16 * (p & 1)));
+          if (((old >> (16 * (p & 1))) & 0xFFFFu) == 1u) list[atomicAdd(tail, 1)] = (uint16_t)p;
         }
       }
-      __syncthreads();
-      got += tot;
     }
-    left -= got;
-    if (got == 0) break;
+    __syncthreads();
+    start = end;
+    end = *tail;
+    __syncthreads();  // every thread has read the tail before the next round appends to it
   }
   return rounds;
 }
@@ -1206,12 +1224,13 @@ __global__ __launch_bounds__(kSchedThreads) void ready_schedule_kernel(
     const int32_t* __restrict__ dlist, const int32_t* __restrict__ draw, const int32_t* __restrict__ meta,
     int32_t* __restrict__ sched, int32_t* __restrict__ pstart, int32_t* __restrict__ npass) {
   // ceil(L / 4) words of pending counts, then (balanced passes) 16-bit heights
-  // and dependents' counts, ceil(L / 2) words each
+  // and dependents' counts, and the 16-bit frontier list of sched_heights,
+  // ceil(L / 2) words each
   extern __shared__ __attribute__((aligned(16))) uint32_t pend[];
   __shared__ int tmp[kSchedThreads / 64];
   __shared__ int chosen[256];
   __shared__ int cand[kSchedCand];
-  __shared__ int low_s, found_s;
+  __shared__ int low_s, found_s, tail_s, thr_s, above_s;
   const int q = blockIdx.x;
   const int32_t* order = orders + (size_t)q * L;
   const int32_t* ig = indeg + (size_t)q * L;
@@ -1241,8 +1260,8 @@ __global__ __launch_bounds__(kSchedThreads) void ready_schedule_kernel(
   uint16_t* ht = reinterpret_cast<uint16_t*>(pend + words);
   int height = 0;
   if (balance)
-    height = sched_heights(order, mask, nbp + (size_t)q * L * K, oq, L, K, nact, ht, pend + words + (L + 1) / 2,
-                           cand, tmp);
+    height = sched_heights(order, mask, nbp + (size_t)q * L * K, oq, L, K, ht, pend + words + (L + 1) / 2,
+                           reinterpret_cast<uint16_t*>(pend + words + 2 * ((L + 1) / 2)), tmp, &tail_s);
   for (int w = threadIdx.x; w < words; w += kSchedThreads) {
     uint32_t v = 0;
     for (int b = 0; b < 4; ++b) {
@@ -1259,26 +1278,32 @@ __global__ __launch_bounds__(kSchedThreads) void ready_schedule_kernel(
   while (placed < nact) {
     ++pass;
     int found = 0;
+    // Ready steps are found 8 per thread (two words of pending counts), from
+    // the first unplaced step on, in order of u.
     if (!balance) {
-      for (int cursor = low_s; found < cap && cursor < L; cursor += kSchedThreads) {
-        const int u = cursor + threadIdx.x;
-        const bool rdy = u < L && sched_pending(pend, u) == 0;
+      for (int c8 = low_s / 8; found < cap && 8 * c8 < L; c8 += kSchedThreads) {
+        const int i = c8 + threadIdx.x;
+        const uint32_t rdy = sched_ready8(pend, words, i);
         int tot;
-        const int rank = block_scan(rdy ? 1 : 0, tmp, &tot);
-        if (rdy && found + rank < cap) chosen[found + rank] = u;
+        int rank = found + block_scan(__popc(rdy), tmp, &tot);
+        for (uint32_t m = rdy; m; m &= m - 1, ++rank)
+          if (rank < cap) chosen[rank] = 8 * i + __ffs(m) - 1;
         found = min(cap, found + tot);
       }
     } else {
       // candidates: the first kSchedCand ready steps, in order of u
       const int remaining = height - pass + 1;
       int n = 0, myf = 0, tot;
-      for (int cursor = low_s; n < kSchedCand && cursor < L; cursor += kSchedThreads) {
-        const int u = cursor + threadIdx.x;
-        const bool rdy = u < L && sched_pending(pend, u) == 0;
-        const int rank = block_scan(rdy ? 1 : 0, tmp, &tot);
-        if (rdy && n + rank < kSchedCand) {
-          cand[n + rank] = u;
-          myf += (int)ht[u] >= remaining;
+      for (int c8 = low_s / 8; n < kSchedCand && 8 * c8 < L; c8 += kSchedThreads) {
+        const int i = c8 + threadIdx.x;
+        const uint32_t rdy = sched_ready8(pend, words, i);
+        int rank = n + block_scan(__popc(rdy), tmp, &tot);
+        for (uint32_t m = rdy; m; m &= m - 1, ++rank) {
+          const int u = 8 * i + __ffs(m) - 1;
+          if (rank < kSchedCand) {
+            cand[rank] = u;
+            myf += (int)ht[u] >= remaining;
+          }
         }
         n = min(kSchedCand, n + tot);
       }
@@ -1314,32 +1339,46 @@ __global__ __launch_bounds__(kSchedThreads) void ready_schedule_kernel(
         int k = max(max(G * (n / G), G * ((f + G - 1) / G)), min(n, G));
         k = min(k, min(n, cap));
         if (k < n) {
-          // threshold height thr: the largest with at least k candidates at or above it
-          int lo = 1, hi = height;
-          while (lo < hi) {
-            const int mid = (lo + hi + 1) >> 1;
-            int c = 0;
-            for (int i = threadIdx.x; i < n; i += kSchedThreads) c += (int)ht[cand[i]] >= mid;
-            block_scan(c, tmp, &tot);
-            if (tot >= k) lo = mid;
-            else hi = mid - 1;
+          // Threshold height thr: the largest with at least k candidates at or above it, from a
+          // histogram of the candidates' heights (in the dependents' counts of sched_heights, free
+          // now); thread t holds heights [1 + t C, 1 + (t + 1) C) and finds the crossing in its range.
+          uint32_t* histw = pend + words + (L + 1) / 2;
+          const uint16_t* hist = reinterpret_cast<const uint16_t*>(histw);  // hist[h - 1]
+          for (int i = threadIdx.x; i < (height + 1) / 2; i += kSchedThreads) histw[i] = 0;
+          __syncthreads();
+          for (int i = threadIdx.x; i < n; i += kSchedThreads) {
+            const int h = (int)ht[cand[i]] - 1;
+            atomicAdd(histw + (h >> 1), 1u << (16 * (h & 1)));
           }
-          const int thr = lo;
-          int c = 0;
-          for (int i = threadIdx.x; i < n; i += kSchedThreads) c += (int)ht[cand[i]] > thr;
-          block_scan(c, tmp, &tot);
-          const int need = k - tot;  // candidates at height thr to take, the smallest u first
-          int eq = 0;
-          for (int c0 = 0; c0 < n; c0 += kSchedThreads) {
-            const int i = c0 + threadIdx.x;
-            const int h = i < n ? (int)ht[cand[i]] : 0;
-            const int er = block_scan(i < n && h == thr ? 1 : 0, tmp, &tot);
-            const bool sel = i < n && (h > thr || (h == thr && eq + er < need));
-            eq += tot;
-            const int r = block_scan(sel ? 1 : 0, tmp, &tot);
-            if (sel) chosen[found + r] = cand[i];
-            found += tot;
+          __syncthreads();
+          const int C = (height + kSchedThreads - 1) / kSchedThreads;
+          const int a0 = threadIdx.x * C, a1 = min(a0 + C, height);
+          int local = 0;
+          for (int i = a0; i < a1; ++i) local += hist[i];
+          const int before = block_scan(local, tmp, &tot);
+          int above = n - before - local;  // candidates with a histogram index >= a1
+          for (int i = a1 - 1; i >= a0; --i) {
+            const int higher = above;
+            above += hist[i];
+            if (above >= k && higher < k) {
+              thr_s = i + 1;
+              above_s = higher;
+            }
           }
+          __syncthreads();
+          const int thr = thr_s, need = k - above_s;  // candidates at height thr to take, the smallest u first
+          // thread t: candidates 2 t and 2 t + 1, so that the scans keep the order of u
+          static_assert(kSchedCand <= 2 * kSchedThreads, "two candidates per thread");
+          const int i0 = 2 * threadIdx.x;
+          const int h0 = i0 < n ? (int)ht[cand[i0]] : 0, h1 = i0 + 1 < n ? (int)ht[cand[i0 + 1]] : 0;
+          const int e0 = i0 < n && h0 == thr, e1 = i0 + 1 < n && h1 == thr;
+          const int er = block_scan(e0 + e1, tmp, &tot);
+          const int s0 = i0 < n && (h0 > thr || (e0 && er < need));
+          const int s1 = i0 + 1 < n && (h1 > thr || (e1 && er + e0 < need));
+          const int r = block_scan(s0 + s1, tmp, &tot);
+          if (s0) chosen[r] = cand[i0];
+          if (s1) chosen[r + s0] = cand[i0 + 1];
+          found = tot;
         } else {
           for (int i = threadIdx.x; i < k; i += kSchedThreads) chosen[i] = cand[i];
           found = k;
@@ -1457,7 +1496,7 @@ hipError_t launch_decode_schedule(const DecodeArgs& a, hipStream_t stream) {
                                                      a.pstart, meta);
   dep_fill_kernel<<<dim3(blocks, nq), 256, 0, stream>>>(a.orders, a.mask, a.nbp, a.L, a.K, off, cur, dlist);
   const bool balance = a.pass_granule > 1 && a.L <= kSchedPrioMaxL;
-  const size_t lds_words = (L + 3) / 4 + (balance ? 2 * ((L + 1) / 2) : 0);
+  const size_t lds_words = (L + 3) / 4 + (balance ? 3 * ((L + 1) / 2) : 0);
   ready_schedule_kernel<<<nq, kSchedThreads, sizeof(uint32_t) * lds_words, stream>>>(
       a.orders, a.mask, a.nbp, a.L, a.K, a.max_members, a.pass_granule, indeg, off, dlist, a.draw, meta, a.sched,
       a.pstart, a.npass);
