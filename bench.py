@@ -41,16 +41,19 @@ from hikoboshi_amd import backbone  # noqa: E402  (numpy only; no GPU)
 
 METRIC = "sampled residues/sec at L=300×64 seqs; µs per decode step"
 F_RES = 29_103_360        # FLOP per sampled residue, reference arithmetic at K=48
-# FLOP per sampled residue the restructured decode loop executes, split by unit: per layer the
-# W2 product over the 48 message rows (on the fp16 MFMA as three products of split operands,
-# hi.hi + hi.lo + lo.hi), and on the VALU the row sums A + E1 + R|Q and column sums, W3 on the
-# summed rows, W_in and W_out, plus the fused next-layer [W1d | W1a] of layers 0 and 1 and logits.
-F_W2 = 3 * (2 * 48 * 128 * 128)
-F_VALU = 3 * (2 * 48 * 128 + 48 * 128 + 2 * 128 * 128 + 2 * 2 * 128 * 512) + 2 * (2 * 128 * 256) + 2 * 128 * 21
-F_EXEC = F_W2 + F_VALU
+# FLOP per sampled residue the restructured decode loop executes, split by unit: per message layer
+# the W2 product over the 48 message rows (fp32 mode: on the fp16 MFMA as three products of split
+# operands, hi.hi + hi.lo + lo.hi; bf16 mode: one bf16 product) and on the VALU the row sums
+# A + E1 + R|Q and the column sums; on every layer W3 on the summed rows, W_in and W_out; the fused
+# next-layer [W1d | W1a] of layers 0 and 1 and the logits. In fp32 mode layer 0's message rows come
+# from the precomputed table (the decode then only sums 48 rows of it), so two layers are message layers.
+F_W2_LAYER = 2 * 48 * 128 * 128
+F_MSG_VALU_LAYER = 2 * 48 * 128 + 48 * 128
+F_VALU_REST = 3 * (2 * 128 * 128 + 2 * 2 * 128 * 512) + 2 * (2 * 128 * 256) + 2 * 128 * 21
+L0_TABLE_MAX_BYTES = 4 << 30  # the library's limit for the layer-0 table (22 rows of 128 floats per slot)
 W_DEC = 698_133           # decoder + W_out + W_s floats
 PEAK_FP32_TFLOPS = 157.3  # MI355X dense fp32 (vector and matrix)
-PEAK_FP16_TFLOPS = 2500.0 # MI355X dense fp16 MFMA
+PEAK_FP16_TFLOPS = 2500.0 # MI355X dense fp16 / bf16 MFMA
 PEAK_HBM_GBPS = 8000.0    # MI355X HBM3E
 H, V = 128, 21
 C4_CPU_PROTEINS = 32      # proteins of the ragged batch the CPU baseline scores
@@ -107,7 +110,7 @@ def workloads(args):
                        seeds=(seed + np.arange(256)).astype(np.uint64), precision="fp32",
                        cpu_seqs=[int(b) for b in np.linspace(0, 255, 16).round()])
         c5 = backbone.single_chain(4000, seed)
-        W["C5"] = dict(name="long_L4000_B32_bf16", bb=c5, B=32, T=0.1, order=shared_order(c5),
+        W["C5"] = dict(name="design_L4000_B32_bf16", bb=c5, B=32, T=0.1, order=shared_order(c5),
                        seeds=(seed + np.arange(32)).astype(np.uint64), precision="bf16", cpu_seqs=[0])
         coords, src, tok, off = backbone.ragged_batch(4096, seed)
         pick = np.sort(np.random.default_rng(seed).choice(4096, C4_CPU_PROTEINS, replace=False))
@@ -303,11 +306,23 @@ def measured_traffic(workload: str):
     return None, None
 
 
+def l0_table_used(precision: str, L: int) -> bool:
+    """Whether the library builds the layer-0 message table for this request (fp32 only)."""
+    K = min(48, L)
+    return precision == "fp32" and os.environ.get("HKBS_DECODE_L0TABLE") != "off" and \
+        L * K * 22 * 128 * 4 <= L0_TABLE_MAX_BYTES
+
+
 def decode_roofline(ctx, w, order, decode_ms):
     """The decode kernel against HBM bandwidth (algorithmic bytes) and its executed FLOP against the
-    VALU fp32 and MFMA fp16 peaks."""
+    VALU fp32 and MFMA peaks."""
     bb, B, L = w["bb"], w["B"], w["bb"].L
     K = min(48, L)
+    bf16 = w["precision"] == "bf16"
+    table = l0_table_used(w["precision"], L)
+    msg_layers = 2 if table else 3
+    f_valu = msg_layers * F_MSG_VALU_LAYER + (48 * 128 if table else 0) + F_VALU_REST
+    f_mfma = (1 if bf16 else 3) * msg_layers * F_W2_LAYER
     idx, _ = ctx.knn(bb.coords, bb.atom_sources)
     pos = np.empty(L, np.int64)
     pos[order] = np.arange(L)
@@ -316,8 +331,12 @@ def decode_roofline(ctx, w, order, decode_ms):
     t = decode_ms * 1e-3
     achieved = launch_bytes / t / 1e9
     traffic, traffic_src = measured_traffic(w["name"])
-    valu = B * L * F_VALU / t / 1e12
-    mfma = B * L * 3 * F_W2 / t / 1e12
+    valu = B * L * f_valu / t / 1e12
+    mfma = B * L * f_mfma / t / 1e12
+    mfma_key = "mfma_bf16" if bf16 else "mfma_fp16"
+    mfma_note = ("W2 of all three layers as one bf16 product" if bf16 else
+                 f"W2 of {msg_layers} layers as three fp16 products of split operands (hi.hi + hi.lo + lo.hi)"
+                 + ("; layer 0's rows come from the layer-0 table kernel, outside this launch" if table else ""))
     return {
         "kernel": "decode_kernel",
         "bound": "hbm",
@@ -333,11 +352,10 @@ def decode_roofline(ctx, w, order, decode_ms):
         "traffic_source": (f"{traffic_src}: rocprofv3 FETCH_SIZE x2.0 + WRITE_SIZE x1.0 (copy-kernel "
                            "calibrated), bytes per launch") if traffic else None,
         "executed": {
-            "valu_fp32": {"flop_per_residue": F_VALU, "achieved_tflops": round(valu, 3), "peak": PEAK_FP32_TFLOPS,
+            "valu_fp32": {"flop_per_residue": f_valu, "achieved_tflops": round(valu, 3), "peak": PEAK_FP32_TFLOPS,
                           "frac": round(valu / PEAK_FP32_TFLOPS, 4)},
-            "mfma_fp16": {"flop_per_residue": 3 * F_W2, "achieved_tflops": round(mfma, 3), "peak": PEAK_FP16_TFLOPS,
-                          "frac": round(mfma / PEAK_FP16_TFLOPS, 4),
-                          "note": "W2 as three fp16 products of split operands (hi.hi + hi.lo + lo.hi)"},
+            mfma_key: {"flop_per_residue": f_mfma, "achieved_tflops": round(mfma, 3), "peak": PEAK_FP16_TFLOPS,
+                       "frac": round(mfma / PEAK_FP16_TFLOPS, 4), "note": mfma_note},
             "reference_flop_per_residue": F_RES,
         },
         "limiter": ("latency: neither HBM nor the arithmetic units are near their peaks; the SQ counters in "
@@ -437,7 +455,8 @@ def run_configs(ctx, cpu, workers, model, wall, steps, warmup):
                     "value": round(w["B"] * w["bb"].L / (ms * 1e-3), 1), "unit": "residues/s",
                     "phase_ms": {"featurise_encode": round(float(ph[0]), 4),
                                  "decoder_precompute": round(float(ph[1]), 4), "decode_loop": round(float(ph[2]), 4)},
-                    "us_per_decode_step": round(float(ph[2]) * 1e3 / w["bb"].L, 3)})
+                    "us_per_decode_step": round(float(ph[2]) * 1e3 / w["bb"].L, 3),
+                    "roofline": decode_roofline(ctx, w, order, float(ph[2]))})
         if cfg == "C5":
             # bf16 against the fp32 path on the bf16 run's own trajectory at the config's T (contract 2e-2)
             worst = 0.0

@@ -896,6 +896,15 @@ hkbs_status design_on_device(hkbs_pmpnn* ctx, const float* coords, const uint8_t
   a.precision = ctx->precision;
   a.l0tab = l0tab;
   a.rec = rec;
+  if (a.precision != HKBS_PRECISION_FP32) {
+    // 16-bit modes read the message rows' inputs in fp16: E1 and the Q blocks 0..2 share E1's space
+    // (3 S + 3 L halves <= 3 S floats), R rows take half of R's.
+    _Float16* E1h = reinterpret_cast<_Float16*>(E1);
+    a.E1h = E1h;
+    a.Qh = E1h + (size_t)kLayers * S * kH;
+    a.Rh = reinterpret_cast<_Float16*>(R);
+    a.E1 = nullptr;
+  }
   const int team = decode_team_size(a.precision, B, 8);
   a.max_members = kDecodeGroup * team;
   a.pass_granule = team;
@@ -915,7 +924,9 @@ hkbs_status design_on_device(hkbs_pmpnn* ctx, const float* coords, const uint8_t
   HK_CHECK(launch_decode_schedule(a, ctx->side), "decode schedule launch failed");
   HK_CHECK(hipEventRecord(ctx->join, ctx->side), "event record failed");
   if (ctx->timing) HK_CHECK(hipEventRecord(ctx->ev[1], ctx->stream), "event record failed");
-  HK_CHECK(launch_decoder_precompute(ctx->model, e.h_v, e.h_e, L, K, E1, Q, ctx->stream), "decoder precompute failed");
+  HK_CHECK(launch_decoder_precompute(ctx->model, e.h_v, e.h_e, L, K, E1, Q, ctx->stream, const_cast<_Float16*>(a.E1h),
+                                     const_cast<_Float16*>(a.Qh)),
+           "decoder precompute failed");
   if (l0tab) HK_CHECK(launch_layer0_table(ctx->model, E1, Q, e.idx, L, K, l0tab, ctx->stream), "layer-0 table failed");
   HK_CHECK(launch_zero(reinterpret_cast<float*>(sync), (size_t)B + 1, ctx->stream), "workspace clear failed");
   HK_CHECK(hipStreamWaitEvent(ctx->stream, ctx->join, 0), "stream wait failed");

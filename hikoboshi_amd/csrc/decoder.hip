@@ -196,6 +196,24 @@ __device__ inline float4 load4_dev(const float* p) {
                      __uint_as_float((uint32_t)(b >> 32)));
 }
 
+// Four fp16 values (8 bytes) widened to fp32.
+__device__ inline float4 widen_h4(uint64_t v) {
+  const auto h = [](uint64_t x, int i) {
+    return static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(x >> (16 * i))));
+  };
+  return make_float4(h(v, 0), h(v, 1), h(v, 2), h(v, 3));
+}
+__device__ inline uint64_t load8_dev(const _Float16* p) {
+  return __hip_atomic_load(reinterpret_cast<uint64_t*>(const_cast<_Float16*>(p)), __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_AGENT);
+}
+// Two fp32 values as fp16 (clamped to its range) packed into one 32-bit word, the lower address first.
+__device__ inline int32_t pack_h2(float a, float b) {
+  const uint32_t lo = __builtin_bit_cast(uint16_t, static_cast<_Float16>(__builtin_amdgcn_fmed3f(a, -65504.0F, 65504.0F)));
+  const uint32_t hi = __builtin_bit_cast(uint16_t, static_cast<_Float16>(__builtin_amdgcn_fmed3f(b, -65504.0F, 65504.0F)));
+  return static_cast<int32_t>(lo | (hi << 16));
+}
+
 constexpr uint32_t kSpinLimit = 1u << 20;  // default polls (~1 s) before a team gives up
 
 // Split-phase barrier over the P workgroups of a team. team_arrive: every
@@ -304,6 +322,7 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(ModelDev m, DecodeArgs
   const int32_t* draw = a.draw + qo * L;
   const int npass = a.npass[qo];
   float* R = a.R + (size_t)b * kLayers * L * kH;
+  _Float16* Rh = (BF || HF) ? a.Rh + (size_t)b * kLayers * L * kH : nullptr;  // 16-bit modes: R in fp16
   int32_t* tokens = a.tokens + (size_t)b * L;
   float* lp_out = a.log_probs ? a.log_probs + (size_t)b * L * kV : nullptr;
   float* chosen = a.chosen_lp + (size_t)b * L;
@@ -347,12 +366,24 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(ModelDev m, DecodeArgs
         if (lp_out)
           for (int task = threadIdx.x; task < n0 * kV; task += kThreads)
             lp_out[(size_t)order[sched[s0 + task / kV]] * kV + task % kV] = 0.0F;
-        for (int task = threadIdx.x; task < n0 * kLayers * kH; task += kThreads) {
-          const int i = task / (kLayers * kH), l = (task / kH) % kLayers, c = task % kH;
-          const int t = order[sched[s0 + i]];
-          const int tok = (a.true_tokens && a.true_tokens[t] >= 0 && a.true_tokens[t] < kV) ? a.true_tokens[t] : kV - 1;
-          const float base = (l == 0) ? a.Q[(size_t)t * kH + c] : 0.0F;
-          store_dev(R + ((size_t)l * L + t) * kH + c, base + m.dec[l].T[tok * kH + c]);
+        if constexpr (BF || HF) {  // fp16 rows, two columns per device-scope store
+          for (int task = threadIdx.x; task < n0 * kLayers * (kH / 2); task += kThreads) {
+            const int i = task / (kLayers * kH / 2), l = (task / (kH / 2)) % kLayers, c = 2 * (task % (kH / 2));
+            const int t = order[sched[s0 + i]];
+            const int tok = (a.true_tokens && a.true_tokens[t] >= 0 && a.true_tokens[t] < kV) ? a.true_tokens[t] : kV - 1;
+            const float* q = a.Q + (size_t)t * kH + c;
+            const float* tv = m.dec[l].T + tok * kH + c;
+            const float v0 = ((l == 0) ? q[0] : 0.0F) + tv[0], v1 = ((l == 0) ? q[1] : 0.0F) + tv[1];
+            store_dev(reinterpret_cast<int32_t*>(Rh + ((size_t)l * L + t) * kH + c), pack_h2(v0, v1));
+          }
+        } else {
+          for (int task = threadIdx.x; task < n0 * kLayers * kH; task += kThreads) {
+            const int i = task / (kLayers * kH), l = (task / kH) % kLayers, c = task % kH;
+            const int t = order[sched[s0 + i]];
+            const int tok = (a.true_tokens && a.true_tokens[t] >= 0 && a.true_tokens[t] < kV) ? a.true_tokens[t] : kV - 1;
+            const float base = (l == 0) ? a.Q[(size_t)t * kH + c] : 0.0F;
+            store_dev(R + ((size_t)l * L + t) * kH + c, base + m.dec[l].T[tok * kH + c]);
+          }
         }
       }
       if (P > 1) team_arrive(counter);
@@ -497,18 +528,27 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(ModelDev m, DecodeArgs
               static_assert(kKmax == 48 && kThreads == 512, "row mapping");
               const int c = 4 * (threadIdx.x & 31);
               const int r0 = threadIdx.x >> 5;
-              float4 e[kS], z[kS];
+              // 16-bit modes: fp16 inputs, held raw (four per 8 bytes) until all loads are issued
+              using Raw = typename std::conditional<BF || HF, uint64_t, float4>::type;
+              Raw e[kS], z[kS];
 #pragma unroll
               for (int s = 0; s < kS; ++s) {
                 const int i = i0 + s / 3, k = 16 * (s % 3) + r0;
-                e[s] = make_float4(0.F, 0.F, 0.F, 0.F);
+                e[s] = Raw{};
                 z[s] = e[s];
                 if (i < ml && k < K) {
                   const int j = nbr[i * kKmax + k];
                   if (j >= 0) {
-                    e[s] = *reinterpret_cast<const float4*>(a.E1 + ((size_t)l * S + (size_t)tres[i] * K + k) * kH + c);
-                    z[s] = bwf[i * kKmax + k] ? load4_dev(Rl + (size_t)j * kH + c)  // R: written by the team
-                                                  : *reinterpret_cast<const float4*>(Ql + (size_t)j * kH + c);
+                    if constexpr (BF || HF) {
+                      e[s] = *reinterpret_cast<const uint64_t*>(a.E1h + ((size_t)l * S + (size_t)tres[i] * K + k) * kH + c);
+                      z[s] = bwf[i * kKmax + k]
+                                 ? load8_dev(Rh + ((size_t)l * L + j) * kH + c)  // R: written by the team
+                                 : *reinterpret_cast<const uint64_t*>(a.Qh + ((size_t)l * L + j) * kH + c);
+                    } else {
+                      e[s] = *reinterpret_cast<const float4*>(a.E1 + ((size_t)l * S + (size_t)tres[i] * K + k) * kH + c);
+                      z[s] = bwf[i * kKmax + k] ? load4_dev(Rl + (size_t)j * kH + c)  // R: written by the team
+                                                    : *reinterpret_cast<const float4*>(Ql + (size_t)j * kH + c);
+                    }
                   }
                 }
               }
@@ -516,11 +556,19 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(ModelDev m, DecodeArgs
               for (int s = 0; s < kS; ++s) {
                 const int i = i0 + s / 3, k = 16 * (s % 3) + r0;
                 if (i < ml) {
+                  float4 ev, zv;
+                  if constexpr (BF || HF) {
+                    ev = widen_h4(e[s]);
+                    zv = widen_h4(z[s]);
+                  } else {
+                    ev = e[s];
+                    zv = z[s];
+                  }
                   float4 xv = *reinterpret_cast<const float4*>(hA + i * kH + c);
-                  xv.x += e[s].x + z[s].x;
-                  xv.y += e[s].y + z[s].y;
-                  xv.z += e[s].z + z[s].z;
-                  xv.w += e[s].w + z[s].w;
+                  xv.x += ev.x + zv.x;
+                  xv.y += ev.y + zv.y;
+                  xv.z += ev.z + zv.z;
+                  xv.w += ev.w + zv.w;
                   float4 v = make_float4(gelu_poly(xv.x, gtab), gelu_poly(xv.y, gtab), gelu_poly(xv.z, gtab),
                                          gelu_poly(xv.w, gtab));
                   if (k >= K) v = make_float4(0.F, 0.F, 0.F, 0.F);
@@ -713,11 +761,21 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(ModelDev m, DecodeArgs
         }
       }
       __syncthreads();
-      for (int task = threadIdx.x; task < ml * kLayers * kH; task += kThreads) {
-        const int i = task / (kLayers * kH), l = (task / kH) % kLayers, c = task % kH;
-        const int t = tres[i];
-        const float base = (l == 0) ? q0s[i * kH + c] : Pd[(i * 2 + l - 1) * kH + c];
-        store_dev(R + ((size_t)l * L + t) * kH + c, base + m.dec[l].T[tok_s[i] * kH + c]);
+      if constexpr (BF || HF) {  // fp16 rows, two columns per device-scope store
+        for (int task = threadIdx.x; task < ml * kLayers * (kH / 2); task += kThreads) {
+          const int i = task / (kLayers * kH / 2), l = (task / (kH / 2)) % kLayers, c = 2 * (task % (kH / 2));
+          const int t = tres[i];
+          const float* base = (l == 0) ? q0s + i * kH + c : Pd + (i * 2 + l - 1) * kH + c;
+          const float* tv = m.dec[l].T + tok_s[i] * kH + c;
+          store_dev(reinterpret_cast<int32_t*>(Rh + ((size_t)l * L + t) * kH + c), pack_h2(base[0] + tv[0], base[1] + tv[1]));
+        }
+      } else {
+        for (int task = threadIdx.x; task < ml * kLayers * kH; task += kThreads) {
+          const int i = task / (kLayers * kH), l = (task / kH) % kLayers, c = task % kH;
+          const int t = tres[i];
+          const float base = (l == 0) ? q0s[i * kH + c] : Pd[(i * 2 + l - 1) * kH + c];
+          store_dev(R + ((size_t)l * L + t) * kH + c, base + m.dec[l].T[tok_s[i] * kH + c]);
+        }
       }
     }
     if (!staged) rv = rec_load(s0n, mln);
@@ -916,11 +974,14 @@ __global__ __launch_bounds__(128) void step_records_kernel(ModelDev m, DecodeArg
   rec[((size_t)q * L + s) * kRecFloat4 + w] = v;
 }
 
-// out[c][row][:] = A[row] . Wp(cols 128c..128c+127) for a [M,128] input.
+// out[c][row][:] = A[row] . Wp(cols 128c..128c+127) for a [M,128] input;
+// out_h (if not null) receives blocks c < nh in fp16 (clamped to its range),
+// out (if not null) every block in fp32.
 constexpr int kGemmRows = 64;
 __global__ __launch_bounds__(256) void rows_gemm_kernel(const float* __restrict__ Ain, size_t M,
                                                         const float* __restrict__ Wp, int N,
-                                                        float* __restrict__ out) {
+                                                        float* __restrict__ out, _Float16* __restrict__ out_h,
+                                                        int nh) {
   __shared__ __attribute__((aligned(16))) float A[kGemmRows * kLd];
   const size_t row0 = (size_t)blockIdx.x * kGemmRows;
   const int cblk = blockIdx.y;
@@ -937,7 +998,8 @@ __global__ __launch_bounds__(256) void rows_gemm_kernel(const float* __restrict_
   floatx4 acc[4][2];
   zero_acc(acc);
   mfma_tile<4, 2>(A, kLd, Wp, N, cblk * kH + wave * 32, kH, acc);
-  float* o = out + (size_t)cblk * M * kH;
+  float* o = out ? out + (size_t)cblk * M * kH : nullptr;
+  _Float16* oh = (out_h && cblk < nh) ? out_h + (size_t)cblk * M * kH : nullptr;
 #pragma unroll
   for (int mb = 0; mb < 4; ++mb)
 #pragma unroll
@@ -946,7 +1008,9 @@ __global__ __launch_bounds__(256) void rows_gemm_kernel(const float* __restrict_
       for (int i = 0; i < 4; ++i) {
         const size_t row = row0 + mb * 16 + 4 * (lane >> 4) + i;
         const int col = wave * 32 + nb * 16 + (lane & 15);
-        if (row < M) o[row * kH + col] = acc[mb][nb][i];
+        if (row >= M) continue;
+        if (o) o[row * kH + col] = acc[mb][nb][i];
+        if (oh) oh[row * kH + col] = static_cast<_Float16>(__builtin_amdgcn_fmed3f(acc[mb][nb][i], -65504.0F, 65504.0F));
       }
 }
 
@@ -1439,20 +1503,20 @@ hipError_t launch_positions(const int32_t* orders, int L, int n_orders, int shar
 }
 
 hipError_t launch_decoder_precompute(const ModelDev& m, const float* h_v, const float* h_e, int L, int K,
-                                     float* E1, float* Q, hipStream_t stream) {
+                                     float* E1, float* Q, hipStream_t stream, _Float16* E1h, _Float16* Qh) {
   const size_t S = (size_t)L * K;
   if (S == 0) return hipSuccess;
   rows_gemm_kernel<<<dim3((unsigned)((S + kGemmRows - 1) / kGemmRows), kLayers), 256, 0, stream>>>(
-      h_e, S, m.W1b_dec_p, kLayers * kH, E1);
+      h_e, S, m.W1b_dec_p, kLayers * kH, E1h ? nullptr : E1, E1h, kLayers);
   rows_gemm_kernel<<<dim3((unsigned)((L + kGemmRows - 1) / kGemmRows), kLayers + 1), 256, 0, stream>>>(
-      h_v, (size_t)L, m.W1d_dec_p, (kLayers + 1) * kH, Q);
+      h_v, (size_t)L, m.W1d_dec_p, (kLayers + 1) * kH, Q, Qh, kLayers);
   return hipGetLastError();
 }
 
 hipError_t launch_q_precompute(const ModelDev& m, const float* h_v, int L, float* Q, hipStream_t stream) {
   if (L <= 0) return hipSuccess;
   rows_gemm_kernel<<<dim3((unsigned)((L + kGemmRows - 1) / kGemmRows), kLayers + 1), 256, 0, stream>>>(
-      h_v, (size_t)L, m.W1d_dec_p, (kLayers + 1) * kH, Q);
+      h_v, (size_t)L, m.W1d_dec_p, (kLayers + 1) * kH, Q, nullptr, 0);
   return hipGetLastError();
 }
 

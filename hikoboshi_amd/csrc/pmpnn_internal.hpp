@@ -128,8 +128,12 @@ hipError_t launch_encoder(const ModelDev& m, const int32_t* idx, const float* ma
 hipError_t launch_encoder16(const ModelDev& m, const float* coords, const uint8_t* atom_src,
                             const int32_t* resid, const int32_t* chain, const int32_t* idx, const float* mask,
                             int L, int K, float* h_v, float* h_e, const EncoderScratch& ws, hipStream_t stream);
+// E1 = W1b h_E [3][L*K][128] and Q [4][L][128]. With E1h (the 16-bit decode
+// modes) E1 is written only in fp16 to E1h (E1 may be null) and Qh receives an
+// fp16 copy of Q blocks 0..2; values are clamped to the fp16 range.
 hipError_t launch_decoder_precompute(const ModelDev& m, const float* h_v, const float* h_e, int L,
-                                     int K, float* E1, float* Q, hipStream_t stream);
+                                     int K, float* E1, float* Q, hipStream_t stream, _Float16* E1h = nullptr,
+                                     _Float16* Qh = nullptr);
 struct DecodeArgs {
   const int32_t* idx;     // [L][K]
   const float* mask;      // [L]
@@ -169,6 +173,10 @@ struct DecodeArgs {
   int pass_granule;       // team size the schedule balances passes for (<= 1: none)
   const float* l0tab;     // [L][K][kL0Classes][128] layer-0 message rows (fp32 decode), or null
   const float4* rec;      // [nq][L][kRecFloat4] per-step inputs in schedule order (launch_step_records)
+  // 16-bit decode modes: the message rows' inputs in fp16 (E1 and R unused then)
+  const _Float16* E1h;    // [3][L*K][128]
+  const _Float16* Qh;     // [3][L][128]: Q blocks 0..2
+  _Float16* Rh;           // [B][3][L][128]
 };
 constexpr int kDecodeGroup = 4;  // steps one workgroup decodes in a pass
 // int32 words of DecodeArgs.sched_tmp for nq orders of length L with K neighbours.
