@@ -489,8 +489,6 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(ModelDev m, DecodeArgs
         __syncthreads();
       }
 
-      typename GLog::Part lg;  // logits weights in flight for the whole pass
-      GLog::load(lg, (BF ? static_cast<const void*>(m.Wlog_h) : HF ? static_cast<const void*>(m.Wlog_f) : m.Wlog_t), 0);
       for (int l = 0; l < kLayers; ++l) {
         const DecLayerDev& w = m.dec[l];
         const float* Ql = a.Q + (size_t)l * L * kH;
@@ -498,8 +496,6 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(ModelDev m, DecodeArgs
         // Layer 0 of the fp32 decode reads its message rows from the table.
         const bool from_tab = PREC == kPrecFp32 && l == 0 && a.l0tab != nullptr;
         const float* pl = prm + l * kPrmLayer;
-        typename G3::Part g3;  // W3 in flight during the message rows and their product
-        G3::load(g3, (BF ? static_cast<const void*>(w.W3_h) : HF ? static_cast<const void*>(w.W3_f) : w.W3_t), 0);
         if (!from_tab) {  // else x holds the layer-0 message sums (table, above)
           // W2 fragments of this wave's 16 columns stay in registers for all members.
           const int r = lane & 15, g = lane >> 4;
@@ -655,6 +651,9 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(ModelDev m, DecodeArgs
           }
         }
         // upd = (W3 s + K b3) / 30 ; h1 = LN1(h + upd): wave i owns member i
+        // (W3 loads here: issued during the message rows they competed with the gathers and cost spills)
+        typename G3::Part g3;
+        G3::load(g3, (BF ? static_cast<const void*>(w.W3_h) : HF ? static_cast<const void*>(w.W3_f) : w.W3_t), 0);
         float4 acc[kGroup];
         zero4(acc);
         G3::fma(g3, 0, x, ml, acc);
@@ -735,6 +734,8 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(ModelDev m, DecodeArgs
       staged = true;
       // logits = W_out h + b (padded to 32 outputs), then one draw per member.
       {
+        typename GLog::Part lg;  // loaded here: held through the pass it cost more in spills than its latency
+        GLog::load(lg, (BF ? static_cast<const void*>(m.Wlog_h) : HF ? static_cast<const void*>(m.Wlog_f) : m.Wlog_t), 0);
         float4 acc[kGroup];
         zero4(acc);
         GLog::fma(lg, 0, h, ml, acc);
