@@ -137,12 +137,14 @@ hkbs_status hkbs_pmpnn_design_device(hkbs_pmpnn* ctx, const float* coords,
  * std::vector workspaces per call); it is for callers that cannot allocate
  * device memory: code under HIP graph capture, tight serving loops, harnesses
  * that forbid hipMalloc. Its scratch (encoder states, decoder precompute,
- * per-sequence decoder state, decode schedule, team barrier counters) lives in
- * one static device array of 128 MiB per GPU, which each GPU the library runs
- * on holds until the process ends; the call makes no hipMalloc or hipFree.
- * A request whose scratch exceeds 128 MiB returns HKBS_INVALID_ARGUMENT (at
- * L = 300: up to 206 sequences with a shared order, 149 with one order per
- * sequence; L = 4,000 does not fit). Every call on one
+ * per-sequence decoder state, decode schedule and step records, team barrier
+ * counters, and the fp32 layer-0 message table when it fits beside the rest)
+ * lives in one static device array of 128 MiB per GPU, which each GPU the
+ * library runs on holds until the process ends; the call makes no hipMalloc or
+ * hipFree. A request whose scratch exceeds 128 MiB returns
+ * HKBS_INVALID_ARGUMENT (at L = 300: up to 205 sequences with a shared order,
+ * 81 with one order per sequence; L = 4,000 does not fit). Results equal
+ * hkbs_pmpnn_design_device's with or without the table. Every call on one
  * GPU shares that GPU's array and leaves its contents behind (what must start
  * at zero is cleared by a kernel in the call): calls that overlap on one GPU,
  * from any context or stream, race and must be serialised by the caller. */
