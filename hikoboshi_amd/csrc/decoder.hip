@@ -514,19 +514,21 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(ModelDev m, DecodeArgs
             }
           }
           const float b2 = pl[kPrmB2 + col];
-          for (int i0 = 0; i0 < ml; i0 += 2) {
-            {
-              // Message rows g1 = GELU(A + E1_tk + (bw ? R : Q)_j) of members i0, i0 + 1;
-              // rows >= K are zero. Thread owns columns c..c+3 of rows r0 + 16 s
-              // (member i0 + s / 3, slot 16 (s % 3) + r0); all gathers are issued
-              // before the first use.
-              constexpr int kS = 2 * kKmax / 16;
-              static_assert(kKmax == 48 && kThreads == 512, "row mapping");
-              const int c = 4 * (threadIdx.x & 31);
-              const int r0 = threadIdx.x >> 5;
-              // 16-bit modes: fp16 inputs, held raw (four per 8 bytes) until all loads are issued
-              using Raw = typename std::conditional<BF || HF, uint64_t, float4>::type;
-              Raw e[kS], z[kS];
+          // Message rows g1 = GELU(A + E1_tk + (bw ? R : Q)_j), two members at a time;
+          // rows >= K are zero. Thread owns columns c..c+3 of rows r0 + 16 s
+          // (member i0 + s / 3, slot 16 (s % 3) + r0); all gathers of a pair are
+          // issued before the first use. In the 16-bit modes the rows of all four
+          // members fit in G16 (one 16-bit copy each), so the next pair's gathers
+          // are issued before this pair's product and their latency overlaps it.
+          constexpr bool kPipe = BF || HF;
+          constexpr int kS = 2 * kKmax / 16;
+          static_assert(kKmax == 48 && kThreads == 512, "row mapping");
+          const int c = 4 * (threadIdx.x & 31);
+          const int r0 = threadIdx.x >> 5;
+          // 16-bit modes: fp16 inputs, held raw (four per 8 bytes) until all loads are issued
+          using Raw = typename std::conditional<BF || HF, uint64_t, float4>::type;
+          Raw e[kS], z[kS];
+          auto gather = [&](int i0) {
 #pragma unroll
               for (int s = 0; s < kS; ++s) {
                 const int i = i0 + s / 3, k = 16 * (s % 3) + r0;
@@ -548,6 +550,11 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(ModelDev m, DecodeArgs
                   }
                 }
               }
+          };
+          if constexpr (kPipe) gather(0);
+          for (int i0 = 0; i0 < ml; i0 += 2) {
+            {
+              if constexpr (!kPipe) gather(i0);
 #pragma unroll
               for (int s = 0; s < kS; ++s) {
                 const int i = i0 + s / 3, k = 16 * (s % 3) + r0;
@@ -568,7 +575,7 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(ModelDev m, DecodeArgs
                   float4 v = make_float4(gelu_poly(xv.x, gtab), gelu_poly(xv.y, gtab), gelu_poly(xv.z, gtab),
                                          gelu_poly(xv.w, gtab));
                   if (k >= K) v = make_float4(0.F, 0.F, 0.F, 0.F);
-                  _Float16* gh = G16 + (((s / 3) * 2) * kKmax + k) * kLdH + c;
+                  _Float16* gh = G16 + ((kPipe ? i : (s / 3) * 2) * kKmax + k) * kLdH + c;  // 16-bit: slot = member
                   const float vv[4] = {v.x, v.y, v.z, v.w};
                   if constexpr (BF) {
                     bf16x4 bv;
@@ -597,8 +604,11 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(ModelDev m, DecodeArgs
               }
             }
             __syncthreads();
+            if constexpr (kPipe) {
+              if (i0 + 2 < ml) gather(i0 + 2);
+            }
             for (int i = i0; i < ml && i < i0 + 2; ++i) {
-              const _Float16* Gh = G16 + (i - i0) * 2 * kKmax * kLdH;
+              const _Float16* Gh = kPipe ? G16 + i * kKmax * kLdH : G16 + (i - i0) * 2 * kKmax * kLdH;
               const _Float16* Gl = Gh + kKmax * kLdH;
               // W2 product: hi.hi + (hi.lo + lo.hi) / 2048 on the fp16 MFMA, or bf16 x bf16
               floatx4 acc[3], cor[3];
@@ -647,8 +657,9 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(ModelDev m, DecodeArgs
               sum += __shfl_xor(sum, 32, 64);
               if (lane < 16) x[i * kH + col] = sum;
             }
-            __syncthreads();
+            if constexpr (!kPipe) __syncthreads();
           }
+          if constexpr (kPipe) __syncthreads();
         }
         // upd = (W3 s + K b3) / 30 ; h1 = LN1(h + upd): wave i owns member i
         // (W3 loads here: issued during the message rows they competed with the gathers and cost spills)
