@@ -70,17 +70,18 @@ struct Gemv {
     W4 w[PP];
   };
 
-  static __device__ inline void load(Part& P, const void* __restrict__ Wt, int k) {
+  // spread = 0: every lane loads the first slice (a placeholder load that costs no L2 traffic)
+  static __device__ inline void load(Part& P, const void* __restrict__ Wt, int k, size_t spread = 1) {
     const int q = threadIdx.x % Q4, grp = threadIdx.x / Q4;
-    const size_t at = (size_t)(grp * PER + k * PP) * OUT + 4 * q;
+    const size_t at = ((size_t)(grp * PER + k * PP) * OUT + 4 * q) * spread;
     if constexpr (WT != kPrecFp32) {
       const uint16_t* p = static_cast<const uint16_t*>(Wt) + at;
 #pragma unroll
-      for (int i = 0; i < PP; ++i) P.w[i] = *reinterpret_cast<const uint2*>(p + (size_t)i * OUT);
+      for (int i = 0; i < PP; ++i) P.w[i] = *reinterpret_cast<const uint2*>(p + (size_t)i * OUT * spread);
     } else {
       const float* p = static_cast<const float*>(Wt) + at;
 #pragma unroll
-      for (int i = 0; i < PP; ++i) P.w[i] = *reinterpret_cast<const float4*>(p + (size_t)i * OUT);
+      for (int i = 0; i < PP; ++i) P.w[i] = *reinterpret_cast<const float4*>(p + (size_t)i * OUT * spread);
     }
   }
   static __device__ inline float half_lo(uint32_t v) {
@@ -140,10 +141,10 @@ __device__ inline void zero4(float4 (&acc)[kGroup]) {
 // (returned in *lp); the sum of exponentials and the double-precision CDF
 // walk run over the tokens in order, identically in every lane. Returns the
 // drawn token, the same in every lane.
-__device__ inline int sample_wave(const float* logits, float T, bool greedy, uint64_t state, float* lp) {
+__device__ inline int sample_wave(float logit, float T, bool greedy, uint64_t state, float* lp) {
   const int lane = threadIdx.x & 63;
   const bool tok_lane = lane < kV;
-  const float z = tok_lane ? logits[lane] / T : -__builtin_inff();
+  const float z = tok_lane ? logit / T : -__builtin_inff();
   const float row_max = wave_max(z);
   const float e = tok_lane ? expf(z - row_max) : 0.0F;
   float row_sum = 0.0F;
@@ -277,7 +278,6 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(ModelDev m, DecodeArgs
   using GIn = Gemv<kH, kFF, 2, PREC>;
   using GOut = Gemv<kFF, kH, 2, PREC>;
   using GDa = Gemv<kH, 2 * kH, 1, PREC>;
-  using GLog = Gemv<kH, 32, 1, PREC>;
   // message rows of two members as fp16 pairs: [member][hi, lo][row][kLdH]
   __shared__ __attribute__((aligned(16))) _Float16 G16[2 * 2 * kKmax * kLdH];
   __shared__ __attribute__((aligned(16))) float part[8192];
@@ -287,17 +287,17 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(ModelDev m, DecodeArgs
   __shared__ __attribute__((aligned(16))) float x[kGroup * kH];
   __shared__ __attribute__((aligned(16))) float h1[kGroup * kH];
   __shared__ __attribute__((aligned(16))) float Pd[kGroup * 2 * kH];  // W1d h^l of layers 1, 2
-  __shared__ float logits[kGroup * 32];
+  // logits weights (32 outputs, 21 used) as fp32, [k / 4][v][k % 4]: lane v reads four k of its column at once
+  __shared__ __attribute__((aligned(16))) float wlg[kH * 32];
   __shared__ __attribute__((aligned(16))) float prm[kPrmSize];
   __shared__ __attribute__((aligned(16))) float gtab[kGeluPolyRows * 8];  // GELU polynomials
-  __shared__ int nbr[kGroup * kKmax];
-  __shared__ int bwf[kGroup * kKmax];
+  // neighbour words of the step records: -1 for an empty slot, else j | 2^30 if j is decoded before the step
+  __shared__ __attribute__((aligned(16))) int nbw[kGroup * kKmax];
   __shared__ int cls[kGroup * kKmax];  // layer-0 table class of each slot (with a.l0tab)
   __shared__ __attribute__((aligned(16))) float q0s[kGroup * kH];  // Q^0 rows of the members (R^0 base)
-  __shared__ int tres[kGroup];
-  __shared__ int sdraw[kGroup];  // sampler draw index of each member
-  __shared__ float sdes[kGroup];  // design weight chain_mask * mask (0: keep the true token)
-  __shared__ int stt[kGroup];     // true token, or the fallback token
+  // per member: residue, sampler draw index, design weight chain_mask * mask as float bits (0: keep the
+  // true token), true token or the fallback token
+  __shared__ int4 meta[kGroup];
   __shared__ int tok_s[kGroup];
   __shared__ int bad;
 
@@ -349,6 +349,18 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(ModelDev m, DecodeArgs
     for (int i = threadIdx.x; i < kFF; i += kThreads) p[kPrmBin + i] = w.bin[i];
   }
   if (threadIdx.x < 32) prm[kPrmLog + threadIdx.x] = m.blog[threadIdx.x];
+  for (int e = threadIdx.x; e < kH * 32; e += kThreads) {
+    const int k = e / 32, v = e % 32;
+    float wv;
+    if constexpr (BF) {
+      wv = __uint_as_float(static_cast<uint32_t>(m.Wlog_h[e]) << 16);
+    } else if constexpr (HF) {
+      wv = static_cast<float>(__builtin_bit_cast(_Float16, m.Wlog_f[e]));
+    } else {
+      wv = m.Wlog_t[e];
+    }
+    wlg[((k >> 2) * 32 + v) * 4 + (k & 3)] = wv;
+  }
   __syncthreads();
 
   // Pass 0: inactive residues (inverse_fold_scalar.cpp:804-813): fallback
@@ -405,25 +417,23 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(ModelDev m, DecodeArgs
     return rec[(size_t)(s0 + rank + P * i) * kRecFloat4 + threadIdx.x % kRecFloat4];
   };
   auto rec_store = [&](int mlp, const float4& v) {
-    const int i = threadIdx.x / kRecFloat4, w = threadIdx.x % kRecFloat4;
-    if (mlp > kGroup || i >= mlp) return;
+    // The destination is recomputed here on purpose: a copy hoisted out of the
+    // pass loop would be spilled, and reloading it put memory latency in the
+    // pass hand-over.
+    int tid = threadIdx.x;
+    asm volatile("" : "+v"(tid));
+    const int i = tid / kRecFloat4, w = tid % kRecFloat4;
+    if (mlp > kGroup || i >= mlp || (w > kKmax / 4 && w < 16)) return;
+    float4* dst;
     if (w < kKmax / 4) {
-      const int wd[4] = {__float_as_int(v.x), __float_as_int(v.y), __float_as_int(v.z), __float_as_int(v.w)};
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        nbr[i * kKmax + 4 * w + e] = wd[e] < 0 ? -1 : (wd[e] & 0x3FFFFFFF);
-        bwf[i * kKmax + 4 * w + e] = wd[e] >= 0 && (wd[e] & 0x40000000) != 0;
-      }
+      dst = reinterpret_cast<float4*>(nbw + i * kKmax) + w;
     } else if (w == kKmax / 4) {
-      tres[i] = __float_as_int(v.x);
-      sdraw[i] = __float_as_int(v.y);
-      sdes[i] = v.z;
-      stt[i] = __float_as_int(v.w);
-    } else if (w >= 16) {
+      dst = reinterpret_cast<float4*>(meta + i);
+    } else {
       const int blk = (w - 16) / (kH / 4), c = 4 * ((w - 16) % (kH / 4));
-      float* dst = blk == 0 ? h : (blk == 1 ? hA : q0s);
-      *reinterpret_cast<float4*>(dst + i * kH + c) = v;
+      dst = reinterpret_cast<float4*>((blk == 0 ? h : (blk == 1 ? hA : q0s)) + i * kH + c);
     }
+    *dst = v;
   };
   static_assert(kKmax % 4 == 0 && kRecFloat4 == 16 + 3 * kH / 4 && kRecFloat4 * kGroup <= kThreads, "record layout");
   int ml = 0;
@@ -450,25 +460,40 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(ModelDev m, DecodeArgs
       if (PREC == kPrecFp32 && a.l0tab) {
         // layer-0 table class of each slot: the token of a neighbour decoded before
         // the step (written by the team before the last barrier), else kV
-        if (threadIdx.x < ml * K) {
-          const int i = threadIdx.x / K, k = threadIdx.x % K;
-          const int j = nbr[i * kKmax + k];
-          cls[i * kKmax + k] = (j >= 0 && bwf[i * kKmax + k]) ? load_dev(tokens + j) : kV;
+        int tid = threadIdx.x;
+        asm volatile("" : "+v"(tid));  // keeps these addresses out of loop-invariant (spilled) registers
+        static_assert(kGroup * kKmax <= kThreads, "one slot per thread");
+        if (tid < ml * kKmax && tid % kKmax < K) {
+          const int wd = nbw[tid];
+          cls[tid] = (wd >= 0 && (wd & 0x40000000) != 0) ? load_dev(tokens + (wd & 0x3FFFFFFF)) : kV;
         }
         __syncthreads();
         // x[i] = sum over slots of table rows, in the order of the MFMA path
         // below: lane group g (rows 16 mb + 4 g + e, mb outer) sums its rows,
         // then the four groups add as (g0 + g1) + (g2 + g3).
-        const int i = threadIdx.x >> 7, gq = (threadIdx.x >> 5) & 3, q = threadIdx.x & 31;
+        // The twelve class reads, then the twelve row loads, are issued before
+        // the first use of each. Rows >= K (short chains) load row K - 1 and are
+        // masked to +0 (an AND rather than a select, which the compiler would
+        // turn into a branch around each load). Indices fit 32 bits (the table
+        // is at most 4 GiB).
+        const int i = tid >> 7, gq = (tid >> 5) & 3, q = tid & 31;
         static_assert(kThreads == 128 * kGroup, "table sum mapping");
         if (i < ml) {
-          const float* tb = a.l0tab + (size_t)tres[i] * K * kL0Classes * kH + 4 * q;
+          const float* tb = a.l0tab + ((uint32_t)meta[i].x * (uint32_t)(K * kL0Classes * kH) + 4u * q);
+          int cl[12];
+#pragma unroll
+          for (int n = 0; n < 12; ++n) cl[n] = cls[i * kKmax + min((n / 4) * 16 + 4 * gq + (n % 4), K - 1)];
           float4 v[12];
 #pragma unroll
           for (int n = 0; n < 12; ++n) {
-            const int row = (n / 4) * 16 + 4 * gq + (n % 4);
-            v[n] = row < K ? *reinterpret_cast<const float4*>(tb + ((size_t)row * kL0Classes + cls[i * kKmax + row]) * kH)
-                           : make_float4(0.F, 0.F, 0.F, 0.F);
+            const int rr = min((n / 4) * 16 + 4 * gq + (n % 4), K - 1);
+            v[n] = *reinterpret_cast<const float4*>(tb + (uint32_t)((rr * kL0Classes + cl[n]) * kH));
+          }
+#pragma unroll
+          for (int n = 0; n < 12; ++n) {
+            const uint32_t keep = (n / 4) * 16 + 4 * gq + (n % 4) < K ? ~0u : 0u;
+            v[n] = make_float4(__uint_as_float(__float_as_uint(v[n].x) & keep), __uint_as_float(__float_as_uint(v[n].y) & keep),
+                               __uint_as_float(__float_as_uint(v[n].z) & keep), __uint_as_float(__float_as_uint(v[n].w) & keep));
           }
           float4 sum = make_float4(0.F, 0.F, 0.F, 0.F);
 #pragma unroll
@@ -489,14 +514,71 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(ModelDev m, DecodeArgs
         __syncthreads();
       }
 
+      // Message-row gathers of members i0, i0 + 1 in layer ll (E1_tk and the R or Q
+      // row of each slot's neighbour). Every row is known when the pass starts (R
+      // rows of earlier passes), so the first pair of layer l + 1 is gathered
+      // during layer l's LayerNorm and fused product, and its latency is hidden.
+      constexpr bool kPipe = BF || HF;
+      constexpr int kS = 2 * kKmax / 16;
+      static_assert(kKmax == 48 && kThreads == 512, "row mapping");
+      const int c = 4 * (threadIdx.x & 31);
+      const int r0 = threadIdx.x >> 5;
+      // 16-bit modes: fp16 inputs, held raw (four per 8 bytes) until all loads are issued
+      using Raw = typename std::conditional<BF || HF, uint64_t, float4>::type;
+      Raw e[kS], z[kS];
+      auto gather = [&](int ll, int i0) {
+          // The slots' neighbour words and the two residues are read from LDS
+          // first, so that the row loads below issue back to back (read one
+          // slot at a time, every load waited for its own LDS reads).
+          int wd[kS];
+          const int t0 = meta[min(i0, kGroup - 1)].x, t1 = meta[min(i0 + 1, kGroup - 1)].x;
+#pragma unroll
+          for (int s = 0; s < kS; ++s) {
+            const int i = i0 + s / 3, k = 16 * (s % 3) + r0;  // k < kKmax
+            wd[s] = nbw[min(i, kGroup - 1) * kKmax + k] | ((i < ml && k < K) ? 0 : -1);
+          }
+#pragma unroll
+          for (int s = 0; s < kS; ++s) {
+            const int k = 16 * (s % 3) + r0;
+            const size_t tk = (size_t)(s < 3 ? t0 : t1) * K + k;
+            e[s] = Raw{};
+            z[s] = e[s];
+            if (wd[s] >= 0) {
+              const int j = wd[s] & 0x3FFFFFFF;
+              const bool bw = (wd[s] & 0x40000000) != 0;
+              // z: the R row (written by the team) or the Q row, both read with a
+              // device-scope load; one load per slot (two exec-masked loads into
+              // one register set were issued one after the other)
+              if constexpr (BF || HF) {
+                e[s] = *reinterpret_cast<const uint64_t*>(a.E1h + ((size_t)ll * S + tk) * kH + c);
+                z[s] = load8_dev((bw ? Rh : a.Qh) + ((size_t)ll * L + j) * kH + c);
+              } else {
+                e[s] = *reinterpret_cast<const float4*>(a.E1 + ((size_t)ll * S + tk) * kH + c);
+                z[s] = load4_dev((bw ? R : a.Q) + ((size_t)ll * L + j) * kH + c);
+              }
+            }
+          }
+      };
+      // The first pair of layer l + 1 is gathered during layer l (kPrefetch); in
+      // the fp32 kernel its registers would be spilled, so there it is gathered
+      // where it is used.
+      constexpr bool kPrefetch = BF || HF;
+      if (kPrefetch) gather(0, 0);
       for (int l = 0; l < kLayers; ++l) {
         const DecLayerDev& w = m.dec[l];
-        const float* Ql = a.Q + (size_t)l * L * kH;
-        const float* Rl = R + (size_t)l * L * kH;
         // Layer 0 of the fp32 decode reads its message rows from the table.
         const bool from_tab = PREC == kPrecFp32 && l == 0 && a.l0tab != nullptr;
         const float* pl = prm + l * kPrmLayer;
         if (!from_tab) {  // else x holds the layer-0 message sums (table, above)
+          // Message rows g1 = GELU(A + E1_tk + (bw ? R : Q)_j), two members at a time;
+          // rows >= K are zero. Thread owns columns c..c+3 of rows r0 + 16 s
+          // (member i0 + s / 3, slot 16 (s % 3) + r0); all gathers of a pair are
+          // issued before the first use. In the 16-bit modes the rows of all four
+          // members fit in G16 (one 16-bit copy each), so the next pair's gathers
+          // are issued before this pair's product and their latency overlaps it.
+          // With kPrefetch the first pair's gathers are in flight already (issued
+          // before the loop for layer 0, during the previous layer otherwise).
+          if (!kPrefetch) gather(l, 0);
           // W2 fragments of this wave's 16 columns stay in registers for all members.
           const int r = lane & 15, g = lane >> 4;
           const int col = wave * 16 + r;
@@ -514,47 +596,11 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(ModelDev m, DecodeArgs
             }
           }
           const float b2 = pl[kPrmB2 + col];
-          // Message rows g1 = GELU(A + E1_tk + (bw ? R : Q)_j), two members at a time;
-          // rows >= K are zero. Thread owns columns c..c+3 of rows r0 + 16 s
-          // (member i0 + s / 3, slot 16 (s % 3) + r0); all gathers of a pair are
-          // issued before the first use. In the 16-bit modes the rows of all four
-          // members fit in G16 (one 16-bit copy each), so the next pair's gathers
-          // are issued before this pair's product and their latency overlaps it.
-          constexpr bool kPipe = BF || HF;
-          constexpr int kS = 2 * kKmax / 16;
-          static_assert(kKmax == 48 && kThreads == 512, "row mapping");
-          const int c = 4 * (threadIdx.x & 31);
-          const int r0 = threadIdx.x >> 5;
-          // 16-bit modes: fp16 inputs, held raw (four per 8 bytes) until all loads are issued
-          using Raw = typename std::conditional<BF || HF, uint64_t, float4>::type;
-          Raw e[kS], z[kS];
-          auto gather = [&](int i0) {
-#pragma unroll
-              for (int s = 0; s < kS; ++s) {
-                const int i = i0 + s / 3, k = 16 * (s % 3) + r0;
-                e[s] = Raw{};
-                z[s] = e[s];
-                if (i < ml && k < K) {
-                  const int j = nbr[i * kKmax + k];
-                  if (j >= 0) {
-                    if constexpr (BF || HF) {
-                      e[s] = *reinterpret_cast<const uint64_t*>(a.E1h + ((size_t)l * S + (size_t)tres[i] * K + k) * kH + c);
-                      z[s] = bwf[i * kKmax + k]
-                                 ? load8_dev(Rh + ((size_t)l * L + j) * kH + c)  // R: written by the team
-                                 : *reinterpret_cast<const uint64_t*>(a.Qh + ((size_t)l * L + j) * kH + c);
-                    } else {
-                      e[s] = *reinterpret_cast<const float4*>(a.E1 + ((size_t)l * S + (size_t)tres[i] * K + k) * kH + c);
-                      z[s] = bwf[i * kKmax + k] ? load4_dev(Rl + (size_t)j * kH + c)  // R: written by the team
-                                                    : *reinterpret_cast<const float4*>(Ql + (size_t)j * kH + c);
-                    }
-                  }
-                }
-              }
-          };
-          if constexpr (kPipe) gather(0);
           for (int i0 = 0; i0 < ml; i0 += 2) {
             {
-              if constexpr (!kPipe) gather(i0);
+              if constexpr (!kPipe) {
+                if (i0 > 0) gather(l, i0);
+              }
 #pragma unroll
               for (int s = 0; s < kS; ++s) {
                 const int i = i0 + s / 3, k = 16 * (s % 3) + r0;
@@ -605,7 +651,7 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(ModelDev m, DecodeArgs
             }
             __syncthreads();
             if constexpr (kPipe) {
-              if (i0 + 2 < ml) gather(i0 + 2);
+              if (i0 + 2 < ml) gather(l, i0 + 2);
             }
             for (int i = i0; i < ml && i < i0 + 2; ++i) {
               const _Float16* Gh = kPipe ? G16 + i * kKmax * kLdH : G16 + (i - i0) * 2 * kKmax * kLdH;
@@ -708,13 +754,18 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(ModelDev m, DecodeArgs
           GOut::fma(out1, 1, ff, ml, acc);
         }
         GOut::store(acc, ml, part);
-        // The next layer's fused weights load during LN2. The last layer loads its
-        // own (unused) instead: an unconditional load keeps the register budget.
+        // The next layer's fused weights load during LN2. The last layer issues
+        // the same loads with every lane on one 16-byte slice (unused; an L1 hit):
+        // an unconditional load keeps the register budget, and a full-size one
+        // would hold the logits behind its 128 KB of L2 traffic.
         typename GDa::Part da;
         {
-          const DecLayerDev& nx = m.dec[l + 1 < kLayers ? l + 1 : l];
-          GDa::load(da, (BF ? static_cast<const void*>(nx.W1da_h) : HF ? static_cast<const void*>(nx.W1da_f) : nx.W1da_t), 0);
+          const bool nxt = l + 1 < kLayers;
+          const DecLayerDev& nx = m.dec[nxt ? l + 1 : l];
+          GDa::load(da, (BF ? static_cast<const void*>(nx.W1da_h) : HF ? static_cast<const void*>(nx.W1da_f) : nx.W1da_t), 0,
+                    nxt ? 1 : 0);
         }
+        if (kPrefetch && l + 1 < kLayers) gather(l + 1, 0);  // the next layer's first pair
         __syncthreads();
         if (wave < ml) {
           float v[2];
@@ -743,28 +794,43 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(ModelDev m, DecodeArgs
       }
       rv = rec_load(s0n, mln);  // the next pass's records, in flight during logits and sampling
       staged = true;
-      // logits = W_out h + b (padded to 32 outputs), then one draw per member.
-      {
-        typename GLog::Part lg;  // loaded here: held through the pass it cost more in spills than its latency
-        GLog::load(lg, (BF ? static_cast<const void*>(m.Wlog_h) : HF ? static_cast<const void*>(m.Wlog_f) : m.Wlog_t), 0);
-        float4 acc[kGroup];
-        zero4(acc);
-        GLog::fma(lg, 0, h, ml, acc);
-        GLog::store(acc, ml, part);
-      }
-      __syncthreads();
-      for (int task = threadIdx.x; task < ml * 32; task += kThreads) {
-        const int i = task / 32, o = task % 32;
-        logits[task] = GLog::sum(part, i, o) + prm[kPrmLog + o];
-      }
-      __syncthreads();
-      if (wave < ml) {  // wave i draws member i
+      // Wave i computes member i's logits = W_out h + b and draws its token:
+      // lane v + 32 kh sums inputs [64 kh, 64 kh + 64) of output v (weights
+      // from LDS), and the two halves add across the wave.
+      if (wave < ml) {
         const int i = wave;
-        const int t = tres[i];
+        const int v = lane & 31, kh = lane >> 5;
+        const float4* wr = reinterpret_cast<const float4*>(wlg) + kh * 16 * 32 + v;
+        const float4* hr = reinterpret_cast<const float4*>(h + i * kH) + kh * 16;
+        float4 s4 = make_float4(0.F, 0.F, 0.F, 0.F);
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb) {
+          // eight reads of each operand in flight before their FMAs (the
+          // scheduler otherwise waits for every read)
+          float4 wv[8], hv[8];
+#pragma unroll
+          for (int u = 0; u < 8; ++u) {
+            wv[u] = wr[(8 * kb + u) * 32];
+            hv[u] = hr[8 * kb + u];
+          }
+          __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+          for (int u = 0; u < 8; ++u) {
+            s4.x += hv[u].x * wv[u].x;
+            s4.y += hv[u].y * wv[u].y;
+            s4.z += hv[u].z * wv[u].z;
+            s4.w += hv[u].w * wv[u].w;
+          }
+        }
+        float lsum = (s4.x + s4.y) + (s4.z + s4.w);
+        lsum += __shfl_xor(lsum, 32, 64);
+        const float logit = lsum + prm[kPrmLog + v];
+        const int4 mt = meta[i];  // residue, draw index, design weight bits, true token
+        const int t = mt.x;
         float lpv;
-        const uint64_t state = seed + (uint64_t)sdraw[i] * 0x9E3779B97F4A7C15ull;
-        const int s_tok = sample_wave(logits + i * 32, T, greedy, state, &lpv);
-        const int tok = sdes[i] == 0.0F ? stt[i] : s_tok;
+        const uint64_t state = seed + (uint64_t)mt.y * 0x9E3779B97F4A7C15ull;
+        const int s_tok = sample_wave(logit, T, greedy, state, &lpv);
+        const int tok = __int_as_float(mt.z) == 0.0F ? mt.w : s_tok;
         if (lp_out && lane < kV) lp_out[(size_t)t * kV + lane] = lpv;
         if (lane == tok) store_dev(chosen + t, lpv);
         if (lane == 0) {
@@ -776,7 +842,7 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(ModelDev m, DecodeArgs
       if constexpr (BF || HF) {  // fp16 rows, two columns per device-scope store
         for (int task = threadIdx.x; task < ml * kLayers * (kH / 2); task += kThreads) {
           const int i = task / (kLayers * kH / 2), l = (task / (kH / 2)) % kLayers, c = 2 * (task % (kH / 2));
-          const int t = tres[i];
+          const int t = meta[i].x;
           const float* base = (l == 0) ? q0s + i * kH + c : Pd + (i * 2 + l - 1) * kH + c;
           const float* tv = m.dec[l].T + tok_s[i] * kH + c;
           store_dev(reinterpret_cast<int32_t*>(Rh + ((size_t)l * L + t) * kH + c), pack_h2(base[0] + tv[0], base[1] + tv[1]));
@@ -784,7 +850,7 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(ModelDev m, DecodeArgs
       } else {
         for (int task = threadIdx.x; task < ml * kLayers * kH; task += kThreads) {
           const int i = task / (kLayers * kH), l = (task / kH) % kLayers, c = task % kH;
-          const int t = tres[i];
+          const int t = meta[i].x;
           const float base = (l == 0) ? q0s[i * kH + c] : Pd[(i * 2 + l - 1) * kH + c];
           store_dev(R + ((size_t)l * L + t) * kH + c, base + m.dec[l].T[tok_s[i] * kH + c]);
         }
