@@ -730,10 +730,11 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(ModelDev m, DecodeArgs
         __syncthreads();
         // f = GELU(W_in h1 + b)
         zero4(acc);
-        GIn::fma(in0, 0, h1, ml, acc);
         {
+          // second half in flight during the first half's FMAs
           typename GIn::Part in1;
           GIn::load(in1, (BF ? static_cast<const void*>(w.Win_h) : HF ? static_cast<const void*>(w.Win_f) : w.Win_t), 1);
+          GIn::fma(in0, 0, h1, ml, acc);
           GIn::fma(in1, 1, h1, ml, acc);
         }
         GIn::store(acc, ml, part);
@@ -747,10 +748,10 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(ModelDev m, DecodeArgs
         __syncthreads();
         // h^{l+1} = LN2(h1 + (W_out f + b)) (the mask gate is 1 for an active residue)
         zero4(acc);
-        GOut::fma(out0, 0, ff, ml, acc);
         {
-          typename GOut::Part out1;
+          typename GOut::Part out1;  // second half in flight during the first half's FMAs
           GOut::load(out1, (BF ? static_cast<const void*>(w.Wout_h) : HF ? static_cast<const void*>(w.Wout_f) : w.Wout_t), 1);
+          GOut::fma(out0, 0, ff, ml, acc);
           GOut::fma(out1, 1, ff, ml, acc);
         }
         GOut::store(acc, ml, part);
