@@ -663,23 +663,34 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(ModelDev m, DecodeArgs
                 acc[mb] = floatx4{0.F, 0.F, 0.F, 0.F};
                 cor[mb] = acc[mb];
               }
-#pragma unroll
-              for (int kb = 0; kb < kH / 32; ++kb) {
+              // A operands of k-block kb for the three row blocks, double buffered:
+              // the next block's LDS reads are issued before this block's products.
+              using AOp = typename std::conditional<BF, bf16x8, half8>::type;
+              AOp ah[2][3], al[2][3];
+              auto aload = [&](int kb, int buf) {
 #pragma unroll
                 for (int mb = 0; mb < 3; ++mb) {
                   const int at = (mb * 16 + r) * kLdH + 32 * kb + 8 * g;
+                  ah[buf][mb] = *reinterpret_cast<const AOp*>(Gh + at);
+                  if constexpr (PREC == kPrecFp32) al[buf][mb] = *reinterpret_cast<const AOp*>(Gl + at);
+                }
+              };
+              aload(0, 0);
+#pragma unroll
+              for (int kb = 0; kb < kH / 32; ++kb) {
+                if (kb + 1 < kH / 32) aload(kb + 1, (kb + 1) & 1);
+                __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+                for (int mb = 0; mb < 3; ++mb) {
+                  const AOp& a0 = ah[kb & 1][mb];
                   if constexpr (BF) {
-                    const bf16x8 ab = *reinterpret_cast<const bf16x8*>(Gh + at);
-                    acc[mb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ab, bb[kb], acc[mb], 0, 0, 0);
+                    acc[mb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a0, bb[kb], acc[mb], 0, 0, 0);
                   } else if constexpr (HF) {
-                    const half8 ah = *reinterpret_cast<const half8*>(Gh + at);
-                    acc[mb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, bh[kb], acc[mb], 0, 0, 0);
+                    acc[mb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a0, bh[kb], acc[mb], 0, 0, 0);
                   } else {
-                    const half8 ah = *reinterpret_cast<const half8*>(Gh + at);
-                    const half8 al = *reinterpret_cast<const half8*>(Gl + at);
-                    acc[mb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, bh[kb], acc[mb], 0, 0, 0);
-                    cor[mb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, bl[kb], cor[mb], 0, 0, 0);
-                    cor[mb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al, bh[kb], cor[mb], 0, 0, 0);
+                    acc[mb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a0, bh[kb], acc[mb], 0, 0, 0);
+                    cor[mb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a0, bl[kb], cor[mb], 0, 0, 0);
+                    cor[mb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al[kb & 1][mb], bh[kb], cor[mb], 0, 0, 0);
                   }
                 }
               }
