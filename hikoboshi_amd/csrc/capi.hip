@@ -303,6 +303,21 @@ size_t pack_bf16_k8(HostArena& ar, const float* W, int N, int kin) {
   return off;
 }
 
+// 16-bit copy (bf16, or fp16 if !bf16) of a t-layout matrix already packed at float offset
+// src ([kin][ldo], inputs outer, the first N columns used) as [kin / 8][N][8]: the B
+// fragments of the 16x16x32 MFMA, 8 consecutive inputs of one output per 16 bytes.
+size_t pack_k8_t(HostArena& ar, size_t src, int kin, int N, int ldo, bool bf16) {
+  const size_t off = ar.add((size_t)N * kin / 2);
+  auto* dst = reinterpret_cast<uint16_t*>(ar.data.data() + off);
+  const float* s = ar.data.data() + src;
+  for (int k = 0; k < kin; ++k)
+    for (int n = 0; n < N; ++n) {
+      const float w = s[(size_t)k * ldo + n];
+      dst[((size_t)(k / 8) * N + n) * 8 + k % 8] = bf16 ? to_bf16(w) : __builtin_bit_cast(uint16_t, static_cast<_Float16>(w));
+    }
+  return off;
+}
+
 // Transposed: W [N][kin] columns [c0, c0 + kd) -> [kd][ldo] (first N columns used).
 size_t pack_t(HostArena& ar, const float* W, int N, int kin, int c0, int kd, int ldo) {
   const size_t off = ar.add((size_t)kd * ldo);
@@ -448,8 +463,8 @@ hkbs_status build_model(hkbs_pmpnn* ctx, const float* const* t) {
     size_t W1b_dec_p, W1d_dec_p, Wlog_t, blog, Wlog_h, Wlog_f;
     size_t enc[kLayers][22];
     size_t dec[kLayers][23];
-    size_t dec_h[kLayers][4];  // bf16 copies of W3_t, Win_t, Wout_t, W1da_t
-    size_t dec_f[kLayers][4];  // fp16 copies of the same
+    size_t dec_h[kLayers][4];  // bf16 of W3_t, Win_t, Wout_t, W1da_t as MFMA B fragments (pack_k8_t)
+    size_t dec_f[kLayers][4];  // fp16 of the same
     size_t enc16[2 + 8 * kLayers];  // split-fp16 encoder weights: W_edge, W_e, then per layer
                                     // W1 W2 W3 W11 W12 W13 W_in W_out
   } o{};
@@ -566,14 +581,13 @@ hkbs_status build_model(hkbs_pmpnn* ctx, const float* const* t) {
     } else {
       q[19] = 0;
     }
-    o.dec_h[l][0] = copy_bf16(ar, q[2], 128 * 128);  // W3_t
-    o.dec_h[l][1] = copy_bf16(ar, q[3], 128 * 512);  // Win_t
-    o.dec_h[l][2] = copy_bf16(ar, q[4], 512 * 128);  // Wout_t
-    o.dec_h[l][3] = copy_bf16(ar, q[5], 128 * 256);  // W1da_t
-    o.dec_f[l][0] = copy_f16(ar, q[2], 128 * 128);
-    o.dec_f[l][1] = copy_f16(ar, q[3], 128 * 512);
-    o.dec_f[l][2] = copy_f16(ar, q[4], 512 * 128);
-    o.dec_f[l][3] = copy_f16(ar, q[5], 128 * 256);
+    for (int h = 0; h < 2; ++h) {
+      size_t* dst = h == 0 ? o.dec_h[l] : o.dec_f[l];
+      dst[0] = pack_k8_t(ar, q[2], 128, 128, 128, h == 0);  // W3_t
+      dst[1] = pack_k8_t(ar, q[3], 128, 512, 512, h == 0);  // Win_t
+      dst[2] = pack_k8_t(ar, q[4], 512, 128, 128, h == 0);  // Wout_t
+      dst[3] = pack_k8_t(ar, q[5], 128, 256, 256, h == 0);  // W1da_t
+    }
     q[7] = copy_raw(ar, d[1], 128);    // b1
     q[8] = copy_raw(ar, d[3], 128);    // b2
     q[9] = copy_raw(ar, d[5], 128);    // b3

@@ -130,6 +130,104 @@ struct Gemv {
   }
 };
 
+// Products of the 16-bit decode modes on the MFMA: y[m][n] = sum_k x[m][k] W[k][n]
+// for the members m < ml (rows of the 16-row A operand; the other rows are zero),
+// so that the arithmetic does not grow with the members a workgroup holds. W is
+// stored as B fragments [IN / 8][OUT][8] (bf16 or fp16, pack_k8_t). The
+// activations come from a split 16-bit copy in LDS (put_split16: x = hi + lo
+// with bf16 parts, x = hi + lo / 2048 with fp16 parts), so that, as with the
+// fp32 activations of the VALU products, only the weights are rounded to 16
+// bits; the products accumulate in fp32. Wave w owns output columns [16 CPW w,
+// 16 CPW (w + 1)) over the whole input range (no partial sums), which part p
+// of NP splits into k-ranges loaded separately.
+template <int IN, int OUT, int NP, int PREC>
+struct MGemv {
+  static constexpr bool BF = PREC == kPrecBf16;
+  static constexpr int KB = IN / 32 / NP;                 // k-blocks of 32 inputs per part
+  static constexpr int CPW = OUT / 16 / (kThreads / 64);  // 16-column blocks per wave
+  static_assert(PREC != kPrecFp32 && KB * 32 * NP == IN && CPW * 16 * (kThreads / 64) == OUT, "MFMA product shape");
+  using Op = typename std::conditional<BF, bf16x8, half8>::type;
+  struct Part {
+    Op b[CPW][KB];
+  };
+  struct Acc {
+    floatx4 a[CPW], c[CPW];  // c: the fp16 lo products (scaled by 2048)
+  };
+  // spread = 0: every lane loads the first fragment (a placeholder load that costs no L2 traffic)
+  static __device__ inline void load(Part& P, const uint16_t* __restrict__ W, int part, size_t spread = 1) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+#pragma unroll
+    for (int cb = 0; cb < CPW; ++cb)
+#pragma unroll
+      for (int kb = 0; kb < KB; ++kb) {
+        const size_t at = ((size_t)(4 * (part * KB + kb) + (lane >> 4)) * OUT + (wave * CPW + cb) * 16 + (lane & 15)) * 8;
+        P.b[cb][kb] = *reinterpret_cast<const Op*>(W + at * spread);
+      }
+  }
+  static __device__ inline void zero(Acc& A) {
+#pragma unroll
+    for (int cb = 0; cb < CPW; ++cb) {
+      A.a[cb] = floatx4{0.F, 0.F, 0.F, 0.F};
+      A.c[cb] = A.a[cb];
+    }
+  }
+  // xs: the split copy, hi plane [kGroup][IN] then lo plane
+  static __device__ inline void run(const Part& P, int part, const uint16_t* xs, int ml, Acc& A) {
+    const int lane = threadIdx.x & 63, row = lane & 15;
+#pragma unroll
+    for (int kb = 0; kb < KB; ++kb) {
+      Op ah{}, al{};
+      if (row < ml) {
+        const int at = row * IN + 32 * (part * KB + kb) + 8 * (lane >> 4);
+        ah = *reinterpret_cast<const Op*>(xs + at);
+        al = *reinterpret_cast<const Op*>(xs + kGroup * IN + at);
+      }
+#pragma unroll
+      for (int cb = 0; cb < CPW; ++cb) {
+        if constexpr (BF) {
+          A.a[cb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, P.b[cb][kb], A.a[cb], 0, 0, 0);
+          A.a[cb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al, P.b[cb][kb], A.a[cb], 0, 0, 0);
+        } else {
+          A.a[cb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, P.b[cb][kb], A.a[cb], 0, 0, 0);
+          A.c[cb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al, P.b[cb][kb], A.c[cb], 0, 0, 0);
+        }
+      }
+    }
+  }
+  // y[m][n] into ys [kGroup][OUT]: lane j < 16 holds column j of rows (members) 0..3
+  static __device__ inline void store(const Acc& A, int ml, float* ys) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    if (lane >= 16) return;
+#pragma unroll
+    for (int cb = 0; cb < CPW; ++cb) {
+      const int col = (wave * CPW + cb) * 16 + lane;
+#pragma unroll
+      for (int e = 0; e < kGroup; ++e) {
+        if (e >= ml) break;
+        ys[e * OUT + col] = BF ? A.a[cb][e] : A.a[cb][e] + A.c[cb][e] * (1.0F / 2048.0F);
+      }
+    }
+  }
+};
+static_assert(kGroup == 4, "MGemv::store: members are rows 0..3 of a lane's accumulator");
+
+// Split 16-bit copy of one activation for MGemv: plane 0 = hi, plane 1 (lo_at
+// elements later) = lo; bf16: x = hi + lo, fp16: x = hi + lo / 2048 (|x| clamped
+// to the fp16 range).
+template <int PREC>
+__device__ inline void put_split16(uint16_t* hi, int lo_at, float v) {
+  if constexpr (PREC == kPrecBf16) {
+    const __bf16 h = static_cast<__bf16>(v);
+    hi[0] = __builtin_bit_cast(uint16_t, h);
+    hi[lo_at] = __builtin_bit_cast(uint16_t, static_cast<__bf16>(v - static_cast<float>(h)));
+  } else {
+    const float c = __builtin_amdgcn_fmed3f(v, -65504.0F, 65504.0F);
+    const _Float16 h = static_cast<_Float16>(c);
+    hi[0] = __builtin_bit_cast(uint16_t, h);
+    hi[lo_at] = __builtin_bit_cast(uint16_t, static_cast<_Float16>((c - static_cast<float>(h)) * 2048.0F));
+  }
+}
+
 __device__ inline void zero4(float4 (&acc)[kGroup]) {
 #pragma unroll
   for (int i = 0; i < kGroup; ++i) acc[i] = make_float4(0.F, 0.F, 0.F, 0.F);
@@ -301,6 +399,15 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(ModelDev m, DecodeArgs
   __shared__ int tok_s[kGroup];
   __shared__ int bad;
 
+  // 16-bit modes: the MFMA products' outputs and the split 16-bit copies of
+  // their inputs (put_split16), in `part`, which only the fp32 products use
+  float* ys = part;  // [kGroup][up to kFF]
+  uint16_t* const s16 = reinterpret_cast<uint16_t*>(part + kGroup * kFF);
+  uint16_t* const xs16 = s16;                    // message sums, [hi, lo][kGroup][kH]
+  uint16_t* const h1s16 = s16 + 2 * kGroup * kH;  // h1
+  uint16_t* const hs16 = s16 + 4 * kGroup * kH;   // h
+  uint16_t* const ffs16 = s16 + 6 * kGroup * kH;  // ff, [hi, lo][kGroup][kFF]
+  static_assert(kGroup * kFF + (6 * kGroup * kH + 2 * kGroup * kFF) / 2 <= 8192, "16-bit staging fits part");
   const int P = a.team;
   int b = blockIdx.x, rank = 0;
   if (P > 1) {
@@ -712,96 +819,202 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(ModelDev m, DecodeArgs
                 }
               sum += __shfl_xor(sum, 16, 64);
               sum += __shfl_xor(sum, 32, 64);
-              if (lane < 16) x[i * kH + col] = sum;
+              if (lane < 16) {
+                x[i * kH + col] = sum;
+                if constexpr (BF || HF) put_split16<PREC>(xs16 + i * kH + col, kGroup * kH, sum);
+              }
             }
             if constexpr (!kPipe) __syncthreads();
           }
           if constexpr (kPipe) __syncthreads();
         }
-        // upd = (W3 s + K b3) / 30 ; h1 = LN1(h + upd): wave i owns member i
-        // (W3 loads here: issued during the message rows they competed with the gathers and cost spills)
-        typename G3::Part g3;
-        G3::load(g3, (BF ? static_cast<const void*>(w.W3_h) : HF ? static_cast<const void*>(w.W3_f) : w.W3_t), 0);
-        float4 acc[kGroup];
-        zero4(acc);
-        G3::fma(g3, 0, x, ml, acc);
-        G3::store(acc, ml, part);
-        typename GIn::Part in0;  // first half of W_in in flight during the reduction and LN1
-        GIn::load(in0, (BF ? static_cast<const void*>(w.Win_h) : HF ? static_cast<const void*>(w.Win_f) : w.Win_t), 0);
-        __syncthreads();
-        if (wave < ml) {
-          float v[2];
-#pragma unroll
-          for (int hh = 0; hh < 2; ++hh) {
-            const int c = lane + 64 * hh;
-            v[hh] = h[wave * kH + c] + (G3::sum(part, wave, c) + static_cast<float>(K) * pl[kPrmB3 + c]) * (1.0F / 30.0F);
+        if constexpr (BF || HF) {
+          // 16-bit modes: the four products on the MFMA (MGemv), inputs from the
+          // split copies, outputs in ys.
+          using M3 = MGemv<kH, kH, 1, PREC>;
+          using MIn = MGemv<kH, kFF, 1, PREC>;
+          using MOut = MGemv<kFF, kH, 2, PREC>;
+          using MDa = MGemv<kH, 2 * kH, 1, PREC>;
+          // upd = (W3 s + K b3) / 30 ; h1 = LN1(h + upd): wave i owns member i
+          {
+            typename M3::Part g3;
+            M3::load(g3, BF ? w.W3_h : w.W3_f, 0);
+            typename M3::Acc a3;
+            M3::zero(a3);
+            M3::run(g3, 0, xs16, ml, a3);
+            M3::store(a3, ml, ys);
           }
-          ln_regs_wave(v[0], v[1], pl + kPrmN1g, pl + kPrmN1b, h1 + wave * kH);
-        }
-        __syncthreads();
-        // f = GELU(W_in h1 + b)
-        zero4(acc);
-        {
-          // second half in flight during the first half's FMAs
-          typename GIn::Part in1;
-          GIn::load(in1, (BF ? static_cast<const void*>(w.Win_h) : HF ? static_cast<const void*>(w.Win_f) : w.Win_t), 1);
-          GIn::fma(in0, 0, h1, ml, acc);
-          GIn::fma(in1, 1, h1, ml, acc);
-        }
-        GIn::store(acc, ml, part);
-        typename GOut::Part out0;  // first half of W_out in flight during the reduction and GELU
-        GOut::load(out0, (BF ? static_cast<const void*>(w.Wout_h) : HF ? static_cast<const void*>(w.Wout_f) : w.Wout_t), 0);
-        __syncthreads();
-        for (int task = threadIdx.x; task < ml * kFF; task += kThreads) {
-          const int i = task / kFF, o = task % kFF;
-          ff[task] = gelu_poly(GIn::sum(part, i, o) + pl[kPrmBin + o], gtab);
-        }
-        __syncthreads();
-        // h^{l+1} = LN2(h1 + (W_out f + b)) (the mask gate is 1 for an active residue)
-        zero4(acc);
-        {
-          typename GOut::Part out1;  // second half in flight during the first half's FMAs
-          GOut::load(out1, (BF ? static_cast<const void*>(w.Wout_h) : HF ? static_cast<const void*>(w.Wout_f) : w.Wout_t), 1);
-          GOut::fma(out0, 0, ff, ml, acc);
-          GOut::fma(out1, 1, ff, ml, acc);
-        }
-        GOut::store(acc, ml, part);
-        // The next layer's fused weights load during LN2. The last layer issues
-        // the same loads with every lane on one 16-byte slice (unused; an L1 hit):
-        // an unconditional load keeps the register budget, and a full-size one
-        // would hold the logits behind its 128 KB of L2 traffic.
-        typename GDa::Part da;
-        {
-          const bool nxt = l + 1 < kLayers;
-          const DecLayerDev& nx = m.dec[nxt ? l + 1 : l];
-          GDa::load(da, (BF ? static_cast<const void*>(nx.W1da_h) : HF ? static_cast<const void*>(nx.W1da_f) : nx.W1da_t), 0,
-                    nxt ? 1 : 0);
-        }
-        if (kPrefetch && l + 1 < kLayers) gather(l + 1, 0);  // the next layer's first pair
-        __syncthreads();
-        if (wave < ml) {
-          float v[2];
+          typename MIn::Part pin;  // W_in in flight during LN1
+          MIn::load(pin, BF ? w.Win_h : w.Win_f, 0);
+          __syncthreads();
+          if (wave < ml) {
+            float v[2];
 #pragma unroll
-          for (int hh = 0; hh < 2; ++hh) {
-            const int c = lane + 64 * hh;
-            v[hh] = h1[wave * kH + c] + (GOut::sum(part, wave, c) + pl[kPrmBout + c]);
+            for (int hh = 0; hh < 2; ++hh) {
+              const int c = lane + 64 * hh;
+              v[hh] = h[wave * kH + c] + (ys[wave * kH + c] + static_cast<float>(K) * pl[kPrmB3 + c]) * (1.0F / 30.0F);
+            }
+            ln_regs_wave(v[0], v[1], pl + kPrmN1g, pl + kPrmN1b, h1 + wave * kH);
+#pragma unroll
+            for (int hh = 0; hh < 2; ++hh) {
+              const int c = lane + 64 * hh;
+              put_split16<PREC>(h1s16 + wave * kH + c, kGroup * kH, h1[wave * kH + c]);
+            }
           }
-          ln_regs_wave(v[0], v[1], pl + kPrmN2g, pl + kPrmN2b, h + wave * kH);
-        }
-        __syncthreads();
-        if (l + 1 < kLayers) {
-          // fused [W1d | W1a] of the next layer: W1d h is kept for R (completed with
-          // T[tok] after sampling), W1a h + b1 is the next A.
+          __syncthreads();
+          // f = GELU(W_in h1 + b)
+          typename MOut::Part po0;  // first half of W_out in flight during W_in and the GELU
+          MOut::load(po0, BF ? w.Wout_h : w.Wout_f, 0);
+          {
+            typename MIn::Acc ai;
+            MIn::zero(ai);
+            MIn::run(pin, 0, h1s16, ml, ai);
+            MIn::store(ai, ml, ys);
+          }
+          __syncthreads();
+          for (int task = threadIdx.x; task < ml * kFF; task += kThreads) {
+            const int o = task % kFF;
+            const float f = gelu_poly(ys[task] + pl[kPrmBin + o], gtab);
+            ff[task] = f;
+            put_split16<PREC>(ffs16 + task, kGroup * kFF, f);
+          }
+          __syncthreads();
+          // h^{l+1} = LN2(h1 + (W_out f + b))
+          {
+            typename MOut::Part po1;  // second half in flight during the first half's products
+            MOut::load(po1, BF ? w.Wout_h : w.Wout_f, 1);
+            typename MOut::Acc ao;
+            MOut::zero(ao);
+            MOut::run(po0, 0, ffs16, ml, ao);
+            MOut::run(po1, 1, ffs16, ml, ao);
+            MOut::store(ao, ml, ys);
+          }
+          // the next layer's fused weights during LN2 (a placeholder load in the last layer)
+          typename MDa::Part pda;
+          {
+            const bool nxt = l + 1 < kLayers;
+            const DecLayerDev& nx = m.dec[nxt ? l + 1 : l];
+            MDa::load(pda, BF ? nx.W1da_h : nx.W1da_f, 0, nxt ? 1 : 0);
+          }
+          if (kPrefetch && l + 1 < kLayers) gather(l + 1, 0);  // the next layer's first pair
+          __syncthreads();
+          if (wave < ml) {
+            float v[2];
+#pragma unroll
+            for (int hh = 0; hh < 2; ++hh) {
+              const int c = lane + 64 * hh;
+              v[hh] = h1[wave * kH + c] + (ys[wave * kH + c] + pl[kPrmBout + c]);
+            }
+            ln_regs_wave(v[0], v[1], pl + kPrmN2g, pl + kPrmN2b, h + wave * kH);
+#pragma unroll
+            for (int hh = 0; hh < 2; ++hh) {
+              const int c = lane + 64 * hh;
+              put_split16<PREC>(hs16 + wave * kH + c, kGroup * kH, h[wave * kH + c]);
+            }
+          }
+          __syncthreads();
+          if (l + 1 < kLayers) {
+            // fused [W1d | W1a] of the next layer (see the fp32 branch)
+            {
+              typename MDa::Acc ad;
+              MDa::zero(ad);
+              MDa::run(pda, 0, hs16, ml, ad);
+              MDa::store(ad, ml, ys);
+            }
+            __syncthreads();
+            for (int task = threadIdx.x; task < ml * kH; task += kThreads) {
+              const int i = task / kH, c = task % kH;
+              Pd[(i * 2 + l) * kH + c] = ys[i * 2 * kH + c];
+              hA[task] = ys[i * 2 * kH + kH + c] + pl[kPrmLayer + kPrmB1 + c];
+            }
+            __syncthreads();
+          }
+        } else {
+          // upd = (W3 s + K b3) / 30 ; h1 = LN1(h + upd): wave i owns member i
+          // (W3 loads here: issued during the message rows they competed with the gathers and cost spills)
+          typename G3::Part g3;
+          G3::load(g3, (BF ? static_cast<const void*>(w.W3_h) : HF ? static_cast<const void*>(w.W3_f) : w.W3_t), 0);
+          float4 acc[kGroup];
           zero4(acc);
-          GDa::fma(da, 0, h, ml, acc);
-          GDa::store(acc, ml, part);
+          G3::fma(g3, 0, x, ml, acc);
+          G3::store(acc, ml, part);
+          typename GIn::Part in0;  // first half of W_in in flight during the reduction and LN1
+          GIn::load(in0, (BF ? static_cast<const void*>(w.Win_h) : HF ? static_cast<const void*>(w.Win_f) : w.Win_t), 0);
           __syncthreads();
-          for (int task = threadIdx.x; task < ml * kH; task += kThreads) {
-            const int i = task / kH, c = task % kH;
-            Pd[(i * 2 + l) * kH + c] = GDa::sum(part, i, c);
-            hA[task] = GDa::sum(part, i, kH + c) + pl[kPrmLayer + kPrmB1 + c];
+          if (wave < ml) {
+            float v[2];
+  #pragma unroll
+            for (int hh = 0; hh < 2; ++hh) {
+              const int c = lane + 64 * hh;
+              v[hh] = h[wave * kH + c] + (G3::sum(part, wave, c) + static_cast<float>(K) * pl[kPrmB3 + c]) * (1.0F / 30.0F);
+            }
+            ln_regs_wave(v[0], v[1], pl + kPrmN1g, pl + kPrmN1b, h1 + wave * kH);
           }
           __syncthreads();
+          // f = GELU(W_in h1 + b)
+          zero4(acc);
+          {
+            // second half in flight during the first half's FMAs
+            typename GIn::Part in1;
+            GIn::load(in1, (BF ? static_cast<const void*>(w.Win_h) : HF ? static_cast<const void*>(w.Win_f) : w.Win_t), 1);
+            GIn::fma(in0, 0, h1, ml, acc);
+            GIn::fma(in1, 1, h1, ml, acc);
+          }
+          GIn::store(acc, ml, part);
+          typename GOut::Part out0;  // first half of W_out in flight during the reduction and GELU
+          GOut::load(out0, (BF ? static_cast<const void*>(w.Wout_h) : HF ? static_cast<const void*>(w.Wout_f) : w.Wout_t), 0);
+          __syncthreads();
+          for (int task = threadIdx.x; task < ml * kFF; task += kThreads) {
+            const int i = task / kFF, o = task % kFF;
+            ff[task] = gelu_poly(GIn::sum(part, i, o) + pl[kPrmBin + o], gtab);
+          }
+          __syncthreads();
+          // h^{l+1} = LN2(h1 + (W_out f + b)) (the mask gate is 1 for an active residue)
+          zero4(acc);
+          {
+            typename GOut::Part out1;  // second half in flight during the first half's FMAs
+            GOut::load(out1, (BF ? static_cast<const void*>(w.Wout_h) : HF ? static_cast<const void*>(w.Wout_f) : w.Wout_t), 1);
+            GOut::fma(out0, 0, ff, ml, acc);
+            GOut::fma(out1, 1, ff, ml, acc);
+          }
+          GOut::store(acc, ml, part);
+          // The next layer's fused weights load during LN2. The last layer issues
+          // the same loads with every lane on one 16-byte slice (unused; an L1 hit):
+          // an unconditional load keeps the register budget, and a full-size one
+          // would hold the logits behind its 128 KB of L2 traffic.
+          typename GDa::Part da;
+          {
+            const bool nxt = l + 1 < kLayers;
+            const DecLayerDev& nx = m.dec[nxt ? l + 1 : l];
+            GDa::load(da, (BF ? static_cast<const void*>(nx.W1da_h) : HF ? static_cast<const void*>(nx.W1da_f) : nx.W1da_t), 0,
+                      nxt ? 1 : 0);
+          }
+          if (kPrefetch && l + 1 < kLayers) gather(l + 1, 0);  // the next layer's first pair
+          __syncthreads();
+          if (wave < ml) {
+            float v[2];
+  #pragma unroll
+            for (int hh = 0; hh < 2; ++hh) {
+              const int c = lane + 64 * hh;
+              v[hh] = h1[wave * kH + c] + (GOut::sum(part, wave, c) + pl[kPrmBout + c]);
+            }
+            ln_regs_wave(v[0], v[1], pl + kPrmN2g, pl + kPrmN2b, h + wave * kH);
+          }
+          __syncthreads();
+          if (l + 1 < kLayers) {
+            // fused [W1d | W1a] of the next layer: W1d h is kept for R (completed with
+            // T[tok] after sampling), W1a h + b1 is the next A.
+            zero4(acc);
+            GDa::fma(da, 0, h, ml, acc);
+            GDa::store(acc, ml, part);
+            __syncthreads();
+            for (int task = threadIdx.x; task < ml * kH; task += kThreads) {
+              const int i = task / kH, c = task % kH;
+              Pd[(i * 2 + l) * kH + c] = GDa::sum(part, i, c);
+              hA[task] = GDa::sum(part, i, kH + c) + pl[kPrmLayer + kPrmB1 + c];
+            }
+            __syncthreads();
+          }
         }
       }
       rv = rec_load(s0n, mln);  // the next pass's records, in flight during logits and sampling

@@ -59,8 +59,9 @@ struct DecLayerDev {
   const float* W2h;    // [16][128][8] fp16: W2 = W2h + W2l / 2048 (decode loop)
   const float* W2l;
   const uint16_t* W1b_s;  // W1b [16][128][8] fp16 hi, then lo (lo follows 128 * 128 halves later): teacher forcing
-  // bf16 copies for the bf16 decode (round to nearest even; same layouts as
-  // the fp32 t-layouts, W2 as [16][128][8] like W2h)
+  // bf16 copies for the bf16 decode (round to nearest even), all as MFMA B
+  // fragments [inputs / 8][outputs][8] (W2 like W2h; W3, Win, Wout, W1da from
+  // their t-layouts)
   const uint16_t *W2_b, *W3_h, *Win_h, *Wout_h, *W1da_h;
   const uint16_t *W3_f, *Win_f, *Wout_f, *W1da_f;  // fp16 copies (W2 in fp16 is W2h)
   const float* W3_t;   // [128][128]
