@@ -817,7 +817,8 @@ size_t decode_bytes(int L, int K, int B, bool l0table) {
          aligned_bytes<float>((size_t)B * kLayers * L * kH) + aligned_bytes<int32_t>((size_t)B * L) +
          aligned_bytes<float>((size_t)B * L * kV) + aligned_bytes<float>((size_t)B * L) + aligned_bytes<float>(B) +
          aligned_bytes<uint32_t>((size_t)B + 1) + 2 * aligned_bytes<int32_t>((size_t)B * L * K) +
-         schedule_bytes(L, K, B) + (l0table ? aligned_bytes<float>(l0_table_floats(L, K)) : 0) +
+         schedule_bytes(L, K, B) +
+         (l0table ? aligned_bytes<float>(l0_table_floats(L, K)) + aligned_bytes<int32_t>((size_t)L + 1) : 0) +
          aligned_bytes<float4>((size_t)B * L * kRecFloat4);
 }
 
@@ -843,7 +844,8 @@ size_t design_scratch_bytes(int L, int B, bool shared, bool l0table) {
          aligned_bytes<float>((size_t)B * kLayers * L * kH) + aligned_bytes<uint32_t>((size_t)B + 1) +
          2 * aligned_bytes<int32_t>(nq * L * K) + aligned_bytes<int32_t>(nq * L) + aligned_bytes<int32_t>(nq * (L + 2)) +
          aligned_bytes<int32_t>(nq) + aligned_bytes<int32_t>(nq * L) + aligned_bytes<int32_t>(sched_scratch_words(L, K, nq)) +
-         (l0table ? aligned_bytes<float>(l0_table_floats(L, K)) : 0) + aligned_bytes<float4>(nq * L * kRecFloat4);
+         (l0table ? aligned_bytes<float>(l0_table_floats(L, K)) + aligned_bytes<int32_t>((size_t)L + 1) : 0) +
+         aligned_bytes<float4>(nq * L * kRecFloat4);
 }
 
 // Shared implementation of the device design path. All pointers device.
@@ -873,6 +875,8 @@ hkbs_status design_on_device(hkbs_pmpnn* ctx, const float* coords, const uint8_t
   int32_t* draw = ar.take<int32_t>(nq * L);
   int32_t* sched_tmp = ar.take<int32_t>(sched_scratch_words(L, K, nq));
   float* l0tab = l0table ? ar.take<float>(l0_table_floats(L, K)) : nullptr;
+  // one shared order: the compact table (rows a slot can use in that order)
+  int32_t* l0base = l0table && shared ? ar.take<int32_t>((size_t)L + 1) : nullptr;
   float4* rec = ar.take<float4>(nq * L * kRecFloat4);
   if (ar.used > ar.cap) return fail(HKBS_INTERNAL_ERROR, "design workspace exceeds its reservation");
   ctx->fault = sync + B;
@@ -909,6 +913,7 @@ hkbs_status design_on_device(hkbs_pmpnn* ctx, const float* coords, const uint8_t
   a.sched_tmp = sched_tmp;
   a.precision = ctx->precision;
   a.l0tab = l0tab;
+  a.l0base = l0base;
   a.rec = rec;
   if (a.precision != HKBS_PRECISION_FP32) {
     // 16-bit modes read the message rows' inputs in fp16: E1 and the Q blocks 0..2 share E1's space
@@ -935,15 +940,18 @@ hkbs_status design_on_device(hkbs_pmpnn* ctx, const float* coords, const uint8_t
   HK_CHECK(launch_featurise_encode(ctx, coords, src, resid, chain, L, K, e), "encoder launch failed");
   HK_CHECK(hipStreamWaitEvent(ctx->side, ctx->fork, 0), "stream wait failed");
   HK_CHECK(launch_positions(orders, L, shared ? 1 : B, shared, pos, ctx->side), "position kernel failed");
+  if (l0base) HK_CHECK(launch_l0_rows(e.idx, pos, L, K, l0base, ctx->side), "layer-0 table rows failed");
   HK_CHECK(launch_decode_schedule(a, ctx->side), "decode schedule launch failed");
   HK_CHECK(hipEventRecord(ctx->join, ctx->side), "event record failed");
   if (ctx->timing) HK_CHECK(hipEventRecord(ctx->ev[1], ctx->stream), "event record failed");
   HK_CHECK(launch_decoder_precompute(ctx->model, e.h_v, e.h_e, L, K, E1, Q, ctx->stream, const_cast<_Float16*>(a.E1h),
                                      const_cast<_Float16*>(a.Qh)),
            "decoder precompute failed");
-  if (l0tab) HK_CHECK(launch_layer0_table(ctx->model, E1, Q, e.idx, L, K, l0tab, ctx->stream), "layer-0 table failed");
   HK_CHECK(launch_zero(reinterpret_cast<float*>(sync), (size_t)B + 1, ctx->stream), "workspace clear failed");
+  // the schedule (built under the encoder) and the compact table's row offsets
   HK_CHECK(hipStreamWaitEvent(ctx->stream, ctx->join, 0), "stream wait failed");
+  if (l0tab)
+    HK_CHECK(launch_layer0_table(ctx->model, E1, Q, e.idx, pos, l0base, L, K, l0tab, ctx->stream), "layer-0 table failed");
   HK_CHECK(launch_step_records(ctx->model, a, rec, ctx->stream), "step records launch failed");
   if (ctx->timing) HK_CHECK(hipEventRecord(ctx->ev[2], ctx->stream), "event record failed");
   HK_CHECK(launch_decode(ctx->model, a, ctx->stream, team), "decode launch failed");

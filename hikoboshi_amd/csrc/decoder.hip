@@ -391,11 +391,13 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(ModelDev m, DecodeArgs
   __shared__ __attribute__((aligned(16))) float gtab[kGeluPolyRows * 8];  // GELU polynomials
   // neighbour words of the step records: -1 for an empty slot, else j | 2^30 if j is decoded before the step
   __shared__ __attribute__((aligned(16))) int nbw[kGroup * kKmax];
-  __shared__ int cls[kGroup * kKmax];  // layer-0 table class of each slot (with a.l0tab)
+  __shared__ int cls[kGroup * kKmax];  // layer-0 table row of each slot (with a.l0tab)
   __shared__ __attribute__((aligned(16))) float q0s[kGroup * kH];  // Q^0 rows of the members (R^0 base)
   // per member: residue, sampler draw index, design weight chain_mask * mask as float bits (0: keep the
   // true token), true token or the fallback token
   __shared__ int4 meta[kGroup];
+  // per member: mask of the slots decoded before the step (lo, hi words), first layer-0 table row
+  __shared__ int4 meta2[kGroup];
   __shared__ int tok_s[kGroup];
   __shared__ int bad;
 
@@ -530,12 +532,14 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(ModelDev m, DecodeArgs
     int tid = threadIdx.x;
     asm volatile("" : "+v"(tid));
     const int i = tid / kRecFloat4, w = tid % kRecFloat4;
-    if (mlp > kGroup || i >= mlp || (w > kKmax / 4 && w < 16)) return;
+    if (mlp > kGroup || i >= mlp || (w > kKmax / 4 + 1 && w < 16)) return;
     float4* dst;
     if (w < kKmax / 4) {
       dst = reinterpret_cast<float4*>(nbw + i * kKmax) + w;
     } else if (w == kKmax / 4) {
       dst = reinterpret_cast<float4*>(meta + i);
+    } else if (w == kKmax / 4 + 1) {
+      dst = reinterpret_cast<float4*>(meta2 + i);
     } else {
       const int blk = (w - 16) / (kH / 4), c = 4 * ((w - 16) % (kH / 4));
       dst = reinterpret_cast<float4*>((blk == 0 ? h : (blk == 1 ? hA : q0s)) + i * kH + c);
@@ -565,20 +569,29 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(ModelDev m, DecodeArgs
     bool staged = false;
     if (ml > 0) {
       if (PREC == kPrecFp32 && a.l0tab) {
-        // layer-0 table class of each slot: the token of a neighbour decoded before
-        // the step (written by the team before the last barrier), else kV
+        // layer-0 table row of each slot, from the token of a neighbour decoded
+        // before the step (written by the team before the last barrier)
         int tid = threadIdx.x;
         asm volatile("" : "+v"(tid));  // keeps these addresses out of loop-invariant (spilled) registers
         static_assert(kGroup * kKmax <= kThreads, "one slot per thread");
         if (tid < ml * kKmax && tid % kKmax < K) {
+          const int i = tid / kKmax, k = tid % kKmax;
           const int wd = nbw[tid];
-          cls[tid] = (wd >= 0 && (wd & 0x40000000) != 0) ? load_dev(tokens + (wd & 0x3FFFFFFF)) : kV;
+          const bool bw = wd >= 0 && (wd & 0x40000000) != 0;
+          const int tok = bw ? load_dev(tokens + (wd & 0x3FFFFFFF)) : kV;
+          const int4 m2 = meta2[i];
+          if (a.l0base) {  // compact: kV rows for each earlier backward slot, one for any other
+            const uint64_t before = ((uint64_t)(uint32_t)m2.x | ((uint64_t)(uint32_t)m2.y << 32)) & ((1ull << k) - 1);
+            cls[tid] = m2.z + k + (kV - 1) * __popcll(before) + (bw ? tok : 0);
+          } else {
+            cls[tid] = m2.z + k * kL0Classes + tok;
+          }
         }
         __syncthreads();
         // x[i] = sum over slots of table rows, in the order of the MFMA path
         // below: lane group g (rows 16 mb + 4 g + e, mb outer) sums its rows,
         // then the four groups add as (g0 + g1) + (g2 + g3).
-        // The twelve class reads, then the twelve row loads, are issued before
+        // The twelve row-index reads, then the twelve row loads, are issued before
         // the first use of each. Rows >= K (short chains) load row K - 1 and are
         // masked to +0 (an AND rather than a select, which the compiler would
         // turn into a branch around each load). Indices fit 32 bits (the table
@@ -586,16 +599,13 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(ModelDev m, DecodeArgs
         const int i = tid >> 7, gq = (tid >> 5) & 3, q = tid & 31;
         static_assert(kThreads == 128 * kGroup, "table sum mapping");
         if (i < ml) {
-          const float* tb = a.l0tab + ((uint32_t)meta[i].x * (uint32_t)(K * kL0Classes * kH) + 4u * q);
-          int cl[12];
+          const float* tb = a.l0tab + 4u * q;
+          int cl[12];  // table rows
 #pragma unroll
           for (int n = 0; n < 12; ++n) cl[n] = cls[i * kKmax + min((n / 4) * 16 + 4 * gq + (n % 4), K - 1)];
           float4 v[12];
 #pragma unroll
-          for (int n = 0; n < 12; ++n) {
-            const int rr = min((n / 4) * 16 + 4 * gq + (n % 4), K - 1);
-            v[n] = *reinterpret_cast<const float4*>(tb + (uint32_t)((rr * kL0Classes + cl[n]) * kH));
-          }
+          for (int n = 0; n < 12; ++n) v[n] = *reinterpret_cast<const float4*>(tb + (uint32_t)cl[n] * (uint32_t)kH);
 #pragma unroll
           for (int n = 0; n < 12; ++n) {
             const uint32_t keep = (n / 4) * 16 + 4 * gq + (n % 4) < K ? ~0u : 0u;
@@ -1119,9 +1129,47 @@ finish:
 // otherwise and e = z = 0 for an empty slot; GELU and the hi/lo split into
 // the same LDS layout; the same MFMA operands and order; GELU(acc + b2).
 constexpr int kTabSlots = 24;
+// Rows of slot k of residue t in the compact table: the kV token states when its
+// neighbour is decoded before t in the shared order, else its one state.
+__device__ inline int l0_slot_rows(const int32_t* __restrict__ idx, const int32_t* __restrict__ pos, int L, int K,
+                                   int t, int k) {
+  const int j = idx[(size_t)t * K + k];
+  return (j >= 0 && j < L && pos[j] < pos[t]) ? kV : 1;
+}
+
+// Compact-table row offsets (launch_l0_rows): one workgroup; thread i sums the
+// rows of a contiguous run of residues, a block scan gives each run's start.
+constexpr int kL0RowsThreads = 1024;
+__global__ __launch_bounds__(kL0RowsThreads) void l0_rows_kernel(const int32_t* __restrict__ idx,
+                                                                 const int32_t* __restrict__ pos, int L, int K,
+                                                                 int32_t* __restrict__ base) {
+  __shared__ int run[kL0RowsThreads];
+  const int per = (L + kL0RowsThreads - 1) / kL0RowsThreads;
+  const int t0 = min(L, (int)threadIdx.x * per), t1 = min(L, t0 + per);
+  int sum = 0;
+  for (int t = t0; t < t1; ++t)
+    for (int k = 0; k < K; ++k) sum += l0_slot_rows(idx, pos, L, K, t, k);
+  run[threadIdx.x] = sum;
+  __syncthreads();
+  for (int d = 1; d < kL0RowsThreads; d <<= 1) {  // inclusive scan
+    const int v = threadIdx.x >= (unsigned)d ? run[threadIdx.x - d] : 0;
+    __syncthreads();
+    run[threadIdx.x] += v;
+    __syncthreads();
+  }
+  int at = run[threadIdx.x] - sum;
+  for (int t = t0; t < t1; ++t) {
+    base[t] = at;
+    for (int k = 0; k < K; ++k) at += l0_slot_rows(idx, pos, L, K, t, k);
+  }
+  if (threadIdx.x == kL0RowsThreads - 1) base[L] = run[threadIdx.x];
+}
+
 __global__ __launch_bounds__(kThreads, 4) void layer0_table_kernel(ModelDev m, const float* __restrict__ E1,
                                                                   const float* __restrict__ Q,
-                                                                  const int32_t* __restrict__ idx, int L, int K,
+                                                                  const int32_t* __restrict__ idx,
+                                                                  const int32_t* __restrict__ pos,
+                                                                  const int32_t* __restrict__ base, int L, int K,
                                                                   float* __restrict__ tab) {
   __shared__ __attribute__((aligned(16))) _Float16 G16[2 * kKmax * kLdH];  // hi rows, then lo rows
   __shared__ __attribute__((aligned(16))) float es[kTabSlots * kH];          // E1_tk
@@ -1130,6 +1178,8 @@ __global__ __launch_bounds__(kThreads, 4) void layer0_table_kernel(ModelDev m, c
   __shared__ __attribute__((aligned(16))) float hA[kH];
   __shared__ __attribute__((aligned(16))) float gtab[kGeluPolyRows * 8];
   __shared__ int js[kTabSlots];
+  __shared__ int srows[kKmax + 1];  // rows of each slot of t, then (thread 0) their running start
+  __shared__ int16_t rslot[kTabSlots * kL0Classes], rcls[kTabSlots * kL0Classes];  // row -> (slot, state)
   const int t = blockIdx.x;
   const int k0 = blockIdx.y * kTabSlots;
   const int nk = min(kTabSlots, K - k0);
@@ -1141,8 +1191,27 @@ __global__ __launch_bounds__(kThreads, 4) void layer0_table_kernel(ModelDev m, c
     const int jj = idx[(size_t)t * K + k0 + threadIdx.x];
     js[threadIdx.x] = (jj >= 0 && jj < L) ? jj : -1;
   }
+  if (threadIdx.x < K) srows[threadIdx.x] = base ? l0_slot_rows(idx, pos, L, K, t, threadIdx.x) : kL0Classes;
   for (int i = threadIdx.x; i < kV * kH; i += kThreads) ts[i] = w.T[i];
   __syncthreads();
+  if (threadIdx.x == 0) {  // exclusive running start of every slot (srows[K] = the residue's row count)
+    int at = 0;
+    for (int k = 0; k < K; ++k) {
+      const int n = srows[k];
+      srows[k] = at;
+      at += n;
+    }
+    srows[K] = at;
+  }
+  __syncthreads();
+  // this block's rows: slot k0 + s owns rows [srows[k0 + s], srows[k0 + s + 1]) of the residue
+  if (threadIdx.x < nk) {
+    const int s = threadIdx.x, r0 = srows[k0 + s] - srows[k0], n = srows[k0 + s + 1] - srows[k0 + s];
+    for (int r = 0; r < n; ++r) {
+      rslot[r0 + r] = static_cast<int16_t>(s);
+      rcls[r0 + r] = static_cast<int16_t>(n == 1 ? kV : r);  // one row: not decoded before t, or empty
+    }
+  }
   for (int task = threadIdx.x; task < nk * (kH / 4); task += kThreads) {
     const int s = task / (kH / 4), c = 4 * (task % (kH / 4));
     const int j = js[s];
@@ -1165,15 +1234,15 @@ __global__ __launch_bounds__(kThreads, 4) void layer0_table_kernel(ModelDev m, c
     bl[kb] = __builtin_bit_cast(half8, *reinterpret_cast<const float4*>(w.W2l + at));
   }
   const float b2 = w.b2[col];
-  const int rows = nk * kL0Classes;
-  float* out = tab + ((size_t)t * K + k0) * kL0Classes * kH;
+  const int rows = srows[k0 + nk] - srows[k0];
+  float* out = tab + ((size_t)(base ? base[t] : t * K * kL0Classes) + srows[k0]) * kH;
   __syncthreads();
   for (int r0 = 0; r0 < rows; r0 += kKmax) {
     for (int task = threadIdx.x; task < kKmax * (kH / 4); task += kThreads) {
       const int row = task / (kH / 4), c = 4 * (task % (kH / 4));
       float vv[4] = {0.F, 0.F, 0.F, 0.F};
       if (r0 + row < rows) {
-        const int s = (r0 + row) / kL0Classes, cl = (r0 + row) % kL0Classes;
+        const int s = rslot[r0 + row], cl = rcls[r0 + row];
         const float4 e = *reinterpret_cast<const float4*>(es + s * kH + c);
         float4 z = *reinterpret_cast<const float4*>(qs + s * kH + c);
         if (js[s] >= 0 && cl < kV) {
@@ -1261,6 +1330,19 @@ __global__ __launch_bounds__(128) void step_records_kernel(ModelDev m, DecodeArg
       const int tt = (a.true_tokens && a.true_tokens[t] >= 0 && a.true_tokens[t] < kV) ? a.true_tokens[t] : kV - 1;
       v = make_float4(__int_as_float(t), __int_as_float(a.draw[(size_t)q * L + u]),
                       (a.chain_mask ? a.chain_mask[t] : 1.0F) * a.mask[t], __int_as_float(tt));
+    } else if (w == kKmax / 4 + 1) {  // slots decoded before the step (bit k), first layer-0 table row
+      uint32_t lo = 0, hi = 0;
+      for (int k = 0; k < K; ++k) {
+        const size_t at = ((size_t)q * L + u) * K + k;
+        if (a.nbj[at] >= 0 && a.nbp[at] < u) {
+          if (k < 32)
+            lo |= 1u << k;
+          else
+            hi |= 1u << (k - 32);
+        }
+      }
+      const int row0 = a.l0base ? a.l0base[t] : t * K * kL0Classes;
+      v = make_float4(__uint_as_float(lo), __uint_as_float(hi), __int_as_float(row0), 0.F);
     } else if (w >= 16) {
       const int blk = (w - 16) / (kH / 4), c = 4 * ((w - 16) % (kH / 4));
       if (blk == 0) {
@@ -1831,12 +1913,19 @@ hipError_t launch_step_records(const ModelDev& m, const DecodeArgs& a, float4* r
   return hipGetLastError();
 }
 
-hipError_t launch_layer0_table(const ModelDev& m, const float* E1, const float* Q, const int32_t* idx, int L, int K,
-                               float* tab, hipStream_t stream) {
+hipError_t launch_layer0_table(const ModelDev& m, const float* E1, const float* Q, const int32_t* idx,
+                               const int32_t* pos, const int32_t* base, int L, int K, float* tab, hipStream_t stream) {
+  if (L <= 0 || K <= 0) return hipSuccess;
+  if (K > kKmax || (base && !pos)) return hipErrorInvalidValue;
+  layer0_table_kernel<<<dim3((unsigned)L, (unsigned)((K + kTabSlots - 1) / kTabSlots)), kThreads, 0, stream>>>(
+      m, E1, Q, idx, pos, base, L, K, tab);
+  return hipGetLastError();
+}
+
+hipError_t launch_l0_rows(const int32_t* idx, const int32_t* pos, int L, int K, int32_t* base, hipStream_t stream) {
   if (L <= 0 || K <= 0) return hipSuccess;
   if (K > kKmax) return hipErrorInvalidValue;
-  layer0_table_kernel<<<dim3((unsigned)L, (unsigned)((K + kTabSlots - 1) / kTabSlots)), kThreads, 0, stream>>>(
-      m, E1, Q, idx, L, K, tab);
+  l0_rows_kernel<<<1, kL0RowsThreads, 0, stream>>>(idx, pos, L, K, base);
   return hipGetLastError();
 }
 

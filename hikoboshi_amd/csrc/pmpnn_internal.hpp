@@ -172,7 +172,8 @@ struct DecodeArgs {
   int precision;          // 0 fp32, 1 bf16, 2 fp16 weights and message rows (see decode_kernel)
   int max_members;        // most steps one pass decodes (<= kDecodeGroup * team size)
   int pass_granule;       // team size the schedule balances passes for (<= 1: none)
-  const float* l0tab;     // [L][K][kL0Classes][128] layer-0 message rows (fp32 decode), or null
+  const float* l0tab;     // layer-0 message rows (fp32 decode; launch_layer0_table), or null
+  const int32_t* l0base;  // [L + 1] first table row of each residue (compact table of one shared order), or null
   const float4* rec;      // [nq][L][kRecFloat4] per-step inputs in schedule order (launch_step_records)
   // 16-bit decode modes: the message rows' inputs in fp16 (E1 and R unused then)
   const _Float16* E1h;    // [3][L*K][128]
@@ -191,8 +192,10 @@ hipError_t launch_decode_schedule(const DecodeArgs& a, hipStream_t stream);
 // u = sched[q][s] (residue t = order[u]) as 112 float4: words 0..47 the
 // neighbour slots (j | 2^30 if j is decoded before the step, -1 for an empty
 // slot), word 48 t, 49 the draw index, 50 the design weight chain_mask[t]
-// mask[t] (float bits), 51 the true token or the fallback token, 52..63 zero,
-// then the rows h^0_t, W1a_0 h^0_t + b1_0 and W1d_0 h^0_t (128 floats each).
+// mask[t] (float bits), 51 the true token or the fallback token, 52 and 53 the
+// mask of slots decoded before the step (bit k), 54 the residue's first row in
+// the layer-0 table, 55..63 zero, then the rows h^0_t, W1a_0 h^0_t + b1_0 and
+// W1d_0 h^0_t (128 floats each).
 // The decode stages a pass's members with one 16-byte load per thread.
 constexpr int kRecFloat4 = 112;
 hipError_t launch_step_records(const ModelDev& m, const DecodeArgs& a, float4* rec, hipStream_t stream);
@@ -209,15 +212,22 @@ hipError_t launch_decode(const ModelDev& m, const DecodeArgs& a, hipStream_t str
 hipError_t launch_q_precompute(const ModelDev& m, const float* h_v, int L, float* Q, hipStream_t stream);
 // Layer-0 message table of the fp32 decode. Slot k of residue t sees its
 // neighbour j = idx[t][k] in one of kL0Classes states: decoded before t with
-// token c (c < kV), or not yet decoded / an empty slot (c = kV). Row
-// ((t K + k) kL0Classes + c) holds GELU(W2 GELU(A_t + E1_tk + z) + b2) for
-// that state's z, computed with the decode loop's own operations, so the
-// decode sums K rows instead of computing them. E1, Q as written by
-// launch_decoder_precompute.
+// token c (c < kV), or not yet decoded / an empty slot (c = kV). A row holds
+// GELU(W2 GELU(A_t + E1_tk + z) + b2) for that state's z, computed with the
+// decode loop's own operations, so the decode sums K rows instead of computing
+// them. Full table (base null): row (t K + k) kL0Classes + c, every state of
+// every slot. Compact table of one shared order (base from launch_l0_rows): a
+// slot whose neighbour is decoded before t has the kV token rows, any other
+// slot only its one state; residue t's rows start at base[t], its slots in
+// order. E1, Q as written by launch_decoder_precompute; pos = the order's
+// positions (launch_positions).
 constexpr int kL0Classes = kV + 1;
 inline size_t l0_table_floats(size_t L, size_t K) { return L * K * kL0Classes * kH; }
-hipError_t launch_layer0_table(const ModelDev& m, const float* E1, const float* Q, const int32_t* idx, int L, int K,
-                               float* tab, hipStream_t stream);
+hipError_t launch_layer0_table(const ModelDev& m, const float* E1, const float* Q, const int32_t* idx,
+                               const int32_t* pos, const int32_t* base, int L, int K, float* tab, hipStream_t stream);
+// Row offsets of the compact layer-0 table of one shared order: base[t] = the
+// first row of residue t, base[L] = the row count (at most L K kV).
+hipError_t launch_l0_rows(const int32_t* idx, const int32_t* pos, int L, int K, int32_t* base, hipStream_t stream);
 struct TfArgs {
   const int32_t* idx;     // [L][K] global neighbour indices
   const int32_t* pos;     // [L] position of each residue in its protein's decoding order
