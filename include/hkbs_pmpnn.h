@@ -67,11 +67,12 @@ enum {
 enum {
   HKBS_PRECISION_FP32 = 0, /* default: featurisation and encoder in the reference's fp32 rounding,
                               log-probs within 1e-4 of the reference */
-  HKBS_PRECISION_BF16 = 1, /* decoder in bf16: bf16 weights of every decoder product and bf16
-                              message rows into the W2 MFMA, fp32 accumulation, GELU, LayerNorm
-                              and softmax. Featurisation and encoder run on the fp16 MFMA with
-                              each operand split into two fp16 halves (fp32-level accuracy,
-                              not the reference's rounding sequence) */
+  HKBS_PRECISION_BF16 = 1, /* decoder in bf16: bf16 weights of every decoder product, bf16
+                              message rows into the W2 MFMA, the other products on the MFMA with
+                              their fp32 inputs split into two bf16 halves; fp32 accumulation,
+                              GELU, LayerNorm and softmax. Featurisation and encoder run on the
+                              fp16 MFMA with each operand split into two fp16 halves (fp32-level
+                              accuracy, not the reference's rounding sequence) */
   HKBS_PRECISION_FP16 = 2  /* the same with an fp16 decoder (three more significant bits than
                               bf16) */
 };
