@@ -295,11 +295,12 @@ def test_design_dependency_schedule_long_chain(gpu_ctx, monkeypatch):
         np.testing.assert_array_equal(out["dependency"][key], out["sequential"][key], err_msg=key)
 
 
-@pytest.mark.parametrize("L,B,shared", [(120, 9, False), (300, 16, True), (30, 3, False)])
+@pytest.mark.parametrize("L,B,shared", [(120, 9, False), (300, 16, True), (30, 3, False), (40, 5, True)])
 def test_design_layer0_table_is_exact(gpu_ctx, oracle, L, B, shared, monkeypatch):
     """The fp32 decode reading its layer-0 message rows from the precomputed table gives the bits of
     computing them in the decode loop (HKBS_DECODE_L0TABLE=off): inactive residues (decoded before or
-    after their neighbours), a chain mask with true tokens, per-sequence and shared orders, K < 48."""
+    after their neighbours), a chain mask with true tokens, per-sequence orders (full table) and shared
+    orders (compact table: only the states the order allows), K < 48."""
     bb = backbone.single_chain(L, 6)
     src = bb.atom_sources.copy()
     src[[1, L // 2, L - 2], 1] = 0
