@@ -1137,18 +1137,26 @@ __device__ inline int l0_slot_rows(const int32_t* __restrict__ idx, const int32_
   return (j >= 0 && j < L && pos[j] < pos[t]) ? kV : 1;
 }
 
-// Compact-table row offsets (launch_l0_rows): one workgroup; thread i sums the
-// rows of a contiguous run of residues, a block scan gives each run's start.
+// Compact-table row offsets (launch_l0_rows): one workgroup; every residue's
+// row count goes to LDS (residues strided over the threads), then thread i
+// scans a contiguous run of residues and a block scan gives each run's start.
 constexpr int kL0RowsThreads = 1024;
+constexpr int kL0RowsMaxL = 8192;  // the table is used while it takes <= 4 GiB: L <= 7,943
 __global__ __launch_bounds__(kL0RowsThreads) void l0_rows_kernel(const int32_t* __restrict__ idx,
                                                                  const int32_t* __restrict__ pos, int L, int K,
                                                                  int32_t* __restrict__ base) {
+  __shared__ int cnt[kL0RowsMaxL];
   __shared__ int run[kL0RowsThreads];
+  for (int t = threadIdx.x; t < L; t += kL0RowsThreads) {
+    int n = 0;
+    for (int k = 0; k < K; ++k) n += l0_slot_rows(idx, pos, L, K, t, k);
+    cnt[t] = n;
+  }
+  __syncthreads();
   const int per = (L + kL0RowsThreads - 1) / kL0RowsThreads;
   const int t0 = min(L, (int)threadIdx.x * per), t1 = min(L, t0 + per);
   int sum = 0;
-  for (int t = t0; t < t1; ++t)
-    for (int k = 0; k < K; ++k) sum += l0_slot_rows(idx, pos, L, K, t, k);
+  for (int t = t0; t < t1; ++t) sum += cnt[t];
   run[threadIdx.x] = sum;
   __syncthreads();
   for (int d = 1; d < kL0RowsThreads; d <<= 1) {  // inclusive scan
@@ -1160,7 +1168,7 @@ __global__ __launch_bounds__(kL0RowsThreads) void l0_rows_kernel(const int32_t* 
   int at = run[threadIdx.x] - sum;
   for (int t = t0; t < t1; ++t) {
     base[t] = at;
-    for (int k = 0; k < K; ++k) at += l0_slot_rows(idx, pos, L, K, t, k);
+    at += cnt[t];
   }
   if (threadIdx.x == kL0RowsThreads - 1) base[L] = run[threadIdx.x];
 }
@@ -1924,7 +1932,7 @@ hipError_t launch_layer0_table(const ModelDev& m, const float* E1, const float* 
 
 hipError_t launch_l0_rows(const int32_t* idx, const int32_t* pos, int L, int K, int32_t* base, hipStream_t stream) {
   if (L <= 0 || K <= 0) return hipSuccess;
-  if (K > kKmax) return hipErrorInvalidValue;
+  if (K > kKmax || L > kL0RowsMaxL) return hipErrorInvalidValue;
   l0_rows_kernel<<<1, kL0RowsThreads, 0, stream>>>(idx, pos, L, K, base);
   return hipGetLastError();
 }
