@@ -364,11 +364,13 @@ __device__ inline bool team_wait(uint32_t* counter, uint32_t target, uint32_t sp
 // sequence b runs as workgroup 8 (P (b / 8) + r) + b % 8, so that a team
 // shares one XCD when workgroups are dealt round-robin over the 8 XCDs; the
 // whole grid fits the device at once.
-// PREC = kPrecFp32: fp32 weights, W2 product on the fp16 MFMA with hi/lo
-// operands (fp32-level accuracy). kPrecBf16 / kPrecFp16: 16-bit weights for
-// every product (GEMVs widen them to fp32 and accumulate in fp32), message rows
-// rounded to 16 bits for one 16x16x32 MFMA per k-block; activations,
-// LayerNorm and the sampler stay fp32.
+// PREC = kPrecFp32: fp32 weights; W2 product on the fp16 MFMA with hi/lo
+// operands (fp32-level accuracy), the layer products (Gemv) on the VALU in
+// fp32. kPrecBf16 / kPrecFp16: 16-bit weights for every product; message rows
+// rounded to 16 bits for one 16x16x32 MFMA per k-block; the layer products
+// (MGemv) on the MFMA with the fp32 activations split into two 16-bit parts,
+// accumulated in fp32. In every mode activations, LayerNorm, the logits (one
+// wave per member, weights in LDS) and the sampler are fp32.
 template <int PREC>
 __global__ __launch_bounds__(kThreads) void decode_kernel(ModelDev m, DecodeArgs a) {
   constexpr bool BF = PREC == kPrecBf16, HF = PREC == kPrecFp16;
