@@ -302,11 +302,9 @@ __device__ inline void seq_gemm(float (&acc)[RM][CN], const float* A, int lda, i
   }
 }
 
-// Welford LayerNorm of one 128-wide row read from a k-major LDS column
-// (x[d * ld]), written to out[d * ld] (may alias). Reference order of
-// cpp/primitives/compute/layer_norm_scalar.cpp:8-40, eps 1e-5.
-// Welford mean and 1 / sqrt(var + eps) of 128 values x[d * ld] in the
-// reference's order (the statistics half of welford_ln_col).
+// Welford mean and 1 / sqrt(var + eps) of 128 values x[d * ld] (a k-major
+// LDS column) in the reference's order
+// (cpp/primitives/compute/layer_norm_scalar.cpp:8-40, eps 1e-5).
 __device__ inline void welford_stats_col(const float* x, int ld, float* mean_out, float* inv_out) {
 #pragma clang fp contract(off)
   float mean = 0.0F, m2 = 0.0F;
@@ -342,26 +340,6 @@ __device__ inline void ln_cols_block(const float* x, float* out, int ld, int row
     out[d * ld + r] = (x[d * ld + r] - stat[r]) * stat[rows + r] * g[d] + b[d];
   }
   __syncthreads();
-}
-
-__device__ inline void welford_ln_col(const float* x, float* out, int ld, const float* __restrict__ g,
-                                      const float* __restrict__ b) {
-#pragma clang fp contract(off)
-  float mean = 0.0F, m2 = 0.0F;
-  for (int d = 0; d < 128; ++d) {
-    const float v = x[d * ld];
-    const float count = static_cast<float>(d + 1);
-    const float delta = v - mean;
-    mean += delta / count;
-    const float delta2 = v - mean;
-    m2 += delta * delta2;
-  }
-  const float var = m2 / 128.0F;
-  const float inv_std = 1.0F / sqrtf(var + 1.0e-5F);
-  for (int d = 0; d < 128; ++d) {
-    const float normalized = (x[d * ld] - mean) * inv_std;
-    out[d * ld] = normalized * g[d] + b[d];
-  }
 }
 
 // Two-pass LayerNorm statistics of a 128-float row held as 2 floats per lane

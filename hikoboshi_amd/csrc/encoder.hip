@@ -18,13 +18,15 @@
 //
 // Kernels per layer:
 //   edge_msg_kernel    tile of 32 edge rows: W1 (e, h_j terms), W2, W3 -> m_ij.
-//   node_kernel        tile of 4 residues: the masked neighbour sum of m_ij in
-//                      slot order, LN1, FFN, LN2, mask, and the W11 and
-//                      next-layer W1 prefixes.
+//   node_kernel        tile of 2 to 16 residues: the masked neighbour sum of
+//                      m_ij in slot order, LN1, FFN, LN2, mask, and the W11
+//                      and next-layer W1 prefixes, its weights streamed
+//                      through a ring of register stages and LDS.
 //   edge_update_kernel tile of 32 edge rows: W11, W12, W13, residual, LN3.
 // Small tiles keep several workgroups on every CU; the weights stream through
 // LDS in double-buffered chunks.
 #include <cstdlib>
+#include <utility>
 
 #include "device_math.hpp"
 #include "pmpnn_internal.hpp"
@@ -114,82 +116,127 @@ __global__ __launch_bounds__(256) void edge_msg_kernel(EncLayerDev w, const floa
       for (int j = 0; j < kEdgeCN; ++j) msg[(slot0 + row0 + i) * kH + col0 + j] = acc[i][j] + w.b3[col0 + j];
 }
 
-// acc[j][r] += A[k][row0 + r] * Wt[k][c0 + j * CS] for k = k0 .. k0 + KB - 1 in
-// order (A k-major with leading dimension lda, one rounding per product and
-// per sum); w holds the KB weight rows of the thread's columns.
-template <int KB, int CPT, int RPT>
-__device__ inline void use_rows(const float (&w)[KB][CPT], const float* A, int lda, int row0, int k0,
-                                float (&acc)[CPT][RPT]) {
-#pragma clang fp contract(off)
-#pragma unroll
-  for (int kk = 0; kk < KB; ++kk) {
-    float a[RPT];
-#pragma unroll
-    for (int r = 0; r < RPT; ++r) a[r] = A[(k0 + kk) * lda + row0 + r];
-#pragma unroll
-    for (int j = 0; j < CPT; ++j)
-#pragma unroll
-      for (int r = 0; r < RPT; ++r) acc[j][r] = acc[j][r] + a[r] * w[kk][j];
+// The weights of the node update stream through the workgroup as 40 chunks
+// of 4096 floats (16 KB), in the order they are used:
+//   chunks  0..15  W_in rows 8 c .. 8 c + 7, all 512 columns;
+//   chunks 16..31  W_out rows 32 (c - 16) .. + 31, all 128 columns;
+//   chunks 32..39  rows 16 (c - 32) .. + 15 of the h_i block (first 128
+//                  rows) of W11, then the same rows of the next layer's W1.
+// Each chunk is contiguous in memory (two 8 KB halves for chunks 32..39) and
+// lands in LDS in the same order, so thread t loads 16-byte vectors t and
+// t + 512 from a workgroup-uniform base. Chunk c is loaded kNodeDepth chunks
+// before it is used, so 128 KB are in flight while earlier chunks are
+// multiplied: the node update is a few short dependency chains per thread,
+// and without deep prefetch it waits on every weight row. Two waves per SIMD
+// hide the LDS latency of one another's chains.
+constexpr int kNodeThreads = 512;
+constexpr int kNodeChunks = 40;
+constexpr int kNodeDepth = 8;
+constexpr int kNodePT = 4096 / 4 / kNodeThreads;  // 16-byte vectors per thread per chunk
+
+__device__ __forceinline__ void node_chunk_load(floatx4 (&dst)[kNodePT], const EncLayerDev& w,
+                                                const float* __restrict__ Wn, int c) {
+  static_assert(kNodePT == 2, "chunk mapping");
+  const int t = threadIdx.x;
+  if (c < 32) {
+    const floatx4* base = reinterpret_cast<const floatx4*>(c < 16 ? w.Win_t + (size_t)4096 * c
+                                                                  : w.Wout_t + (size_t)4096 * (c - 16));
+    dst[0] = base[t];
+    dst[1] = base[t + kNodeThreads];
+  } else {
+    dst[0] = reinterpret_cast<const floatx4*>(w.W11_t + (size_t)2048 * (c - 32))[t];
+    dst[1] = reinterpret_cast<const floatx4*>(Wn + (size_t)2048 * (c - 32))[t];
   }
 }
 
-template <int KB, int N, int CPT, int CS>
-__device__ inline void load_rows(float (&w)[KB][CPT], const float* __restrict__ Wt, int k0, int c0) {
+// One step of the chunk ring (S = ring slot = c % kNodeDepth, compile-time so
+// that the ring stays in registers): chunk c to LDS half c & 1, barrier,
+// refill the slot with chunk c + kNodeDepth, then use(chunk in LDS, c). The
+// LDS half that chunk c overwrites was last read while using chunk c - 2,
+// which every thread finished before the barrier of chunk c - 1.
+template <int S, typename Use>
+__device__ __forceinline__ void node_step(floatx4 (&ring)[kNodeDepth][kNodePT], float* Wl, const EncLayerDev& w,
+                                          const float* __restrict__ Wn, int c, Use& use) {
+  float* buf = Wl + (S & 1) * 4096;
 #pragma unroll
-  for (int kk = 0; kk < KB; ++kk)
-#pragma unroll
-    for (int j = 0; j < CPT; ++j) w[kk][j] = Wt[(size_t)(k0 + kk) * N + c0 + j * CS];
+  for (int p = 0; p < kNodePT; ++p) reinterpret_cast<floatx4*>(buf)[threadIdx.x + kNodeThreads * p] = ring[S][p];
+  __syncthreads();
+  if (c + kNodeDepth < kNodeChunks) node_chunk_load(ring[S], w, Wn, c + kNodeDepth);
+  use(static_cast<const float*>(buf), c);
 }
 
-// Sequential-k product of a few rows with the thread's columns c0 + j * CS of
-// Wt [K][N] (t-layout). Weights stream from global memory KB k-rows at a time
-// with the next KB in flight while the current ones are used.
-template <int K, int N, int CPT, int CS, int RPT, int KB>
-__device__ inline void col_gemm(const float* __restrict__ Wt, const float* A, int lda, int row0, int c0,
-                                float (&acc)[CPT][RPT]) {
-  static_assert(K % (2 * KB) == 0, "k chunking");
-  float wa[KB][CPT], wb[KB][CPT];
-  load_rows<KB, N, CPT, CS>(wa, Wt, 0, c0);
-  for (int k0 = 0; k0 < K; k0 += 2 * KB) {
-    load_rows<KB, N, CPT, CS>(wb, Wt, k0 + KB, c0);
-    use_rows<KB, CPT, RPT>(wa, A, lda, row0, k0, acc);
-    if (k0 + 2 * KB < K) load_rows<KB, N, CPT, CS>(wa, Wt, k0 + 2 * KB, c0);
-    use_rows<KB, CPT, RPT>(wb, A, lda, row0, k0 + KB, acc);
-  }
+template <typename Use, int... S>
+__device__ __forceinline__ void node_steps(floatx4 (&ring)[kNodeDepth][kNodePT], float* Wl, const EncLayerDev& w,
+                                           const float* __restrict__ Wn, int cb, Use& use,
+                                           std::integer_sequence<int, S...>) {
+  (node_step<S>(ring, Wl, w, Wn, cb + S, use), ...);
+}
+
+// Uses chunks [c_begin, c_end) (multiples of kNodeDepth) in order.
+template <typename Use>
+__device__ __forceinline__ void node_run(floatx4 (&ring)[kNodeDepth][kNodePT], float* Wl, const EncLayerDev& w,
+                                         const float* __restrict__ Wn, int c_begin, int c_end, Use&& use) {
+  for (int cb = c_begin; cb < c_end; cb += kNodeDepth)
+    node_steps(ring, Wl, w, Wn, cb, use, std::make_integer_sequence<int, kNodeDepth>{});
+}
+
+template <int... S>
+__device__ __forceinline__ void node_fill(floatx4 (&ring)[kNodeDepth][kNodePT], const EncLayerDev& w,
+                                          const float* __restrict__ Wn, std::integer_sequence<int, S...>) {
+  (node_chunk_load(ring[S], w, Wn, S), ...);
 }
 
 // Node update for NR residues: LN1(h + upd), FFN, LN2, mask; then the W11
 // prefix of this layer's edge update and (when Wnext_t is given) the next
 // layer's W1 prefix. Every thread owns whole output columns, so each dot
-// product runs over k in order. Each weight element read from L2 serves NR
-// rows: few rows keep the grid wide when L is small, more rows cut the weight
-// traffic when L is large.
+// product runs over k in order with one rounding per product and per sum.
+// Each weight element read serves NR rows: few rows keep the grid wide when
+// L is small, more rows cut the weight traffic when L is large.
 template <int NR>
-__global__ __launch_bounds__(256) void node_kernel(EncLayerDev w, const float* __restrict__ Wnext_t,
-                                                   const float* __restrict__ msg, const int32_t* __restrict__ idx,
-                                                   const float* __restrict__ mask, int L, int K,
-                                                   float* __restrict__ h_v, float* __restrict__ prefix) {
+__global__ __launch_bounds__(kNodeThreads) void node_kernel(EncLayerDev w, const float* __restrict__ Wnext_t,
+                                                            const float* __restrict__ msg,
+                                                            const int32_t* __restrict__ idx,
+                                                            const float* __restrict__ mask, int L, int K,
+                                                            float* __restrict__ h_v, float* __restrict__ prefix) {
 #pragma clang fp contract(off)
   static_assert(NR % 2 == 0 && NR <= 16, "thread mapping");
-  constexpr int NH = NR / 2;  // rows per thread in the column-per-thread phases
-  constexpr int KB = NR <= 4 ? 32 : 64 / NR;  // weight rows in flight per half-step
+  static_assert(kNodeChunks % kNodeDepth == 0 && 16 % kNodeDepth == 0, "phases start on a ring boundary");
+  constexpr int RQ = NR >= 4 ? NR / 4 : 1;  // rows per thread in the message sum and W_out (4 row groups)
+  constexpr int RP = NR / 2;                // rows per thread in the prefix products (2 row groups)
   __shared__ __attribute__((aligned(16))) float X[kH * NR];   // k-major [d][row]
   __shared__ __attribute__((aligned(16))) float H1[kH * NR];
   __shared__ __attribute__((aligned(16))) float F[kFF * NR];
   __shared__ __attribute__((aligned(16))) float H2[kH * NR];
+  __shared__ __attribute__((aligned(16))) float Wl[2 * 4096];
+  // bias and LayerNorm vectors: bin [512], bout, n1g, n1b, n2g, n2b [128 each]
+  __shared__ float par[kFF + 5 * kH];
+  __shared__ float alpha_s[NR * kKmax];
+  __shared__ float mask_s[NR];
   __shared__ float tbl[17];
-  if (threadIdx.x < 17) tbl[threadIdx.x] = kExpNegTable[threadIdx.x];
   const int r0 = blockIdx.x * NR;
   const int nr = min(NR, L - r0);
   const int t = threadIdx.x;
+  const float* Wn = Wnext_t ? Wnext_t : w.W11_t;  // loaded either way; its prefix is stored only if given
 
+  floatx4 ring[kNodeDepth][kNodePT];
+  node_fill(ring, w, Wn, std::make_integer_sequence<int, kNodeDepth>{});
+
+  if (t < 17) tbl[t] = kExpNegTable[t];
+  par[t] = w.bin[t];
+  if (t < kH) {
+    par[kFF + t] = w.bout[t];
+    par[kFF + kH + t] = w.n1g[t];
+    par[kFF + 2 * kH + t] = w.n1b[t];
+    par[kFF + 3 * kH + t] = w.n2g[t];
+    par[kFF + 4 * kH + t] = w.n2b[t];
+  }
+  if (t < NR) mask_s[t] = t < nr ? mask[r0 + t] : 0.0F;
   // upd = sum over valid slots, in order, of (1/30) mask_i mask_j m_ij; then
   // X = h + upd (axpy order: 1 * residual + input). The weight of each
   // (row, slot) is computed once into LDS (0 for an invalid slot); thread t
-  // owns column t % 128 of rows NH (t / 128) + q, q < NH, issues all of a
+  // owns column t % 128 of rows RQ (t / 128) + q, q < RQ, issues all of a
   // row's message loads at once and sums them in slot order.
-  __shared__ float alpha_s[NR * kKmax];
-  for (int i = t; i < NR * kKmax; i += blockDim.x) {
+  for (int i = t; i < NR * kKmax; i += kNodeThreads) {
     const int row = i / kKmax, k = i % kKmax;
     float alpha = 0.0F;
     if (row < nr && k < K) {
@@ -204,9 +251,10 @@ __global__ __launch_bounds__(256) void node_kernel(EncLayerDev w, const float* _
   }
   __syncthreads();
   {
-    const int d = t % kH, rb = NH * (t / kH);
-    for (int q = 0; q < NH; ++q) {
+    const int d = t % kH, rb = RQ * (t / kH);
+    for (int q = 0; q < RQ; ++q) {
       const int row = rb + q;
+      if (row >= NR) break;
       float v = 0.0F;
       if (row < nr) {
         const int r = r0 + row;
@@ -231,53 +279,83 @@ __global__ __launch_bounds__(256) void node_kernel(EncLayerDev w, const float* _
   __shared__ float ln_mean[NR], ln_inv[NR];
   if (t < NR) welford_stats_col(X + t, NR, ln_mean + t, ln_inv + t);
   __syncthreads();
-  for (int i = t; i < NR * kH; i += blockDim.x) {
+  for (int i = t; i < NR * kH; i += kNodeThreads) {
     const int row = i % NR, d = i / NR;
-    H1[i] = (X[i] - ln_mean[row]) * ln_inv[row] * w.n1g[d] + w.n1b[d];
+    H1[i] = (X[i] - ln_mean[row]) * ln_inv[row] * par[kFF + kH + d] + par[kFF + 2 * kH + d];
   }
-  __syncthreads();
+  // (the barrier of the first chunk orders these writes before their use)
   {
-    // W_in: columns t and t + 256 of all rows, then GELU
-    float acc[2][NR] = {};
-    col_gemm<kH, kFF, 2, 256, NR, KB>(w.Win_t, H1, NR, 0, t, acc);
+    // W_in: column t of all rows, then GELU into F
+    float acc[NR] = {};
+    node_run(ring, Wl, w, Wn, 0, 16, [&](const float* Wc, int c) {
 #pragma unroll
-    for (int j = 0; j < 2; ++j)
+      for (int kk = 0; kk < 8; ++kk) {
+        const int k = 8 * c + kk;
+        const float wv = Wc[kk * kFF + t];
 #pragma unroll
-      for (int r = 0; r < NR; ++r) F[(t + 256 * j) * NR + r] = gelu(acc[j][r] + w.bin[t + 256 * j], tbl);
+        for (int r = 0; r < NR; ++r) acc[r] = acc[r] + H1[k * NR + r] * wv;
+      }
+    });
+#pragma unroll
+    for (int r = 0; r < NR; ++r) F[t * NR + r] = gelu(acc[r] + par[t], tbl);
   }
-  __syncthreads();
   {
-    // W_out: column t % 128 of rows NH (t / 128) + r, r < NH; X = h1 + (W_out f + b)
-    const int c = t % kH, rr = NH * (t / kH);
-    float acc[1][NH] = {};
-    col_gemm<kFF, kH, 1, 0, NH, KB>(w.Wout_t, F, NR, rr, c, acc);
+    // W_out: column t % 128 of rows RQ (t / 128) + r, r < RQ; X = h1 + (W_out f + b).
+    // Row groups past NR (NR = 2) have no rows: those waves only stream.
+    const int c = t % kH, rr = RQ * (t / kH);
+    const bool active = rr < NR;
+    float acc[RQ] = {};
+    node_run(ring, Wl, w, Wn, 16, 32, [&](const float* Wc, int ch) {
+      if (!active) return;
+#pragma unroll 8
+      for (int kk = 0; kk < 32; ++kk) {
+        const int k = 32 * (ch - 16) + kk;
+        const float wv = Wc[kk * kH + c];
 #pragma unroll
-    for (int r = 0; r < NH; ++r) X[c * NR + rr + r] = H1[c * NR + rr + r] + (acc[0][r] + w.bout[c]);
+        for (int r = 0; r < RQ; ++r) acc[r] = acc[r] + F[k * NR + rr + r] * wv;
+      }
+    });
+    if (active) {
+#pragma unroll
+      for (int r = 0; r < RQ; ++r) X[c * NR + rr + r] = H1[c * NR + rr + r] + (acc[r] + par[kFF + c]);
+    }
   }
   __syncthreads();
   if (t < NR) welford_stats_col(X + t, NR, ln_mean + t, ln_inv + t);
   __syncthreads();
-  for (int i = t; i < NR * kH; i += blockDim.x) {
+  for (int i = t; i < NR * kH; i += kNodeThreads) {
     const int row = i % NR, d = i / NR;
-    float v = (X[i] - ln_mean[row]) * ln_inv[row] * w.n2g[d] + w.n2b[d];
-    v *= row < nr ? mask[r0 + row] : 0.0F;
+    float v = (X[i] - ln_mean[row]) * ln_inv[row] * par[kFF + 3 * kH + d] + par[kFF + 4 * kH + d];
+    v *= mask_s[row];
     H2[i] = v;
   }
   __syncthreads();
-  for (int i = t; i < nr * kH; i += blockDim.x) {
+  for (int i = t; i < nr * kH; i += kNodeThreads) {
     const int row = i / kH, d = i % kH;
     h_v[(size_t)(r0 + row) * kH + d] = H2[d * NR + row];
   }
-  // prefixes: [0,128) of W11 (threads 0..127) and of the next layer's W1 (128..255) over h'
+  // prefixes over h': column q = t % 256 of [W11 h-block | next layer's W1 h-block]
+  // (q < 128: W11), rows RP (t / 256) + r, r < RP
   {
-    const int part = t / kH, c = t % kH;
-    const float* Wt = part == 0 ? w.W11_t : Wnext_t;
-    if (Wt) {
-      float acc[1][NR] = {};
-      col_gemm<kH, kH, 1, 0, NR, KB>(Wt, H2, NR, 0, c, acc);
+    const int q = t % 256, part = q / kH, c = q % kH, rr = RP * (t / 256);
+    float acc[RP] = {};
+    node_run(ring, Wl, w, Wn, 32, kNodeChunks, [&](const float* Wc, int ch) {
 #pragma unroll
-      for (int r = 0; r < NR; ++r)
-        if (r < nr) prefix[(size_t)(r0 + r) * 256 + part * 128 + c] = acc[0][r];
+      for (int kk = 0; kk < 16; ++kk) {
+        const int k = 16 * (ch - 32) + kk;
+        const float wv = Wc[part * 2048 + kk * kH + c];
+#pragma unroll
+        for (int r = 0; r < RP; ++r) acc[r] = acc[r] + H2[k * NR + rr + r] * wv;
+      }
+    });
+    // the sums are complete here: without this the compiler sinks each row's
+    // products into its conditional store below and holds every operand
+#pragma unroll
+    for (int r = 0; r < RP; ++r) asm volatile("" : "+v"(acc[r]));
+    if (part == 0 || Wnext_t) {
+#pragma unroll
+      for (int r = 0; r < RP; ++r)
+        if (rr + r < nr) prefix[(size_t)(r0 + rr + r) * 256 + part * 128 + c] = acc[r];
     }
   }
 }
@@ -367,7 +445,10 @@ static int encoder_node_rows(int L) {
     const int n = std::atoi(env);
     if (n == 2 || n == 4 || n == 8 || n == 16) return n;
   }
-  return L >= 1500 ? 8 : 4;  // measured: 4 is fastest up to L = 1000, 8 from L = 2000
+  // measured on single chains: 2 rows are fastest at L = 300, 4 at L = 1000,
+  // 8 from L = 2000 (16 is within noise of 8 at L = 4000)
+  if (L < 700) return 2;
+  return L < 1500 ? 4 : 8;
 }
 
 hipError_t launch_zero(float* p, size_t n, hipStream_t stream) {
@@ -391,13 +472,13 @@ hipError_t launch_encoder(const ModelDev& m, const int32_t* idx, const float* ma
     edge_msg_kernel<<<edge_tiles, 256, 0, stream>>>(m.enc[l], h_e, h_v, idx, ws.prefix, L, K, ws.msg);
     const float* Wnext = l + 1 < kLayers ? m.enc[l + 1].W1_t : nullptr;
     if (node_rows == 16)
-      node_kernel<16><<<node_tiles, 256, 0, stream>>>(m.enc[l], Wnext, ws.msg, idx, mask, L, K, h_v, ws.prefix);
+      node_kernel<16><<<node_tiles, kNodeThreads, 0, stream>>>(m.enc[l], Wnext, ws.msg, idx, mask, L, K, h_v, ws.prefix);
     else if (node_rows == 8)
-      node_kernel<8><<<node_tiles, 256, 0, stream>>>(m.enc[l], Wnext, ws.msg, idx, mask, L, K, h_v, ws.prefix);
+      node_kernel<8><<<node_tiles, kNodeThreads, 0, stream>>>(m.enc[l], Wnext, ws.msg, idx, mask, L, K, h_v, ws.prefix);
     else if (node_rows == 4)
-      node_kernel<4><<<node_tiles, 256, 0, stream>>>(m.enc[l], Wnext, ws.msg, idx, mask, L, K, h_v, ws.prefix);
+      node_kernel<4><<<node_tiles, kNodeThreads, 0, stream>>>(m.enc[l], Wnext, ws.msg, idx, mask, L, K, h_v, ws.prefix);
     else
-      node_kernel<2><<<node_tiles, 256, 0, stream>>>(m.enc[l], Wnext, ws.msg, idx, mask, L, K, h_v, ws.prefix);
+      node_kernel<2><<<node_tiles, kNodeThreads, 0, stream>>>(m.enc[l], Wnext, ws.msg, idx, mask, L, K, h_v, ws.prefix);
     edge_update_kernel<<<edge_tiles, 256, 0, stream>>>(m.enc[l], h_e, h_v, idx, ws.prefix, L, K);
   }
   return hipGetLastError();
