@@ -1130,7 +1130,7 @@ finish:
 // decoded with token c (the R^0_j row its writer stores), z = Q^0_j
 // otherwise and e = z = 0 for an empty slot; GELU and the hi/lo split into
 // the same LDS layout; the same MFMA operands and order; GELU(acc + b2).
-constexpr int kTabSlots = 24;
+constexpr int kTabSlots = 12;  // 4 workgroups per residue: 73 us against 79 us with 24 slots at L = 300
 // Rows of slot k of residue t in the compact table: the kV token states when its
 // neighbour is decoded before t in the shared order, else its one state.
 __device__ inline int l0_slot_rows(const int32_t* __restrict__ idx, const int32_t* __restrict__ pos, int L, int K,
