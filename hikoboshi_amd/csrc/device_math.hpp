@@ -93,7 +93,8 @@ __device__ inline float gelu(float x, const float* tbl = kExpNegTable) {  // tbl
 }
 
 // The same GELU formula for code held to a tolerance rather than to bit
-// identity (the 16-bit encoder; the decode loop uses gelu_poly below): the exp table is read from LDS (tbl = 17
+// identity (the 16-bit encoder's node kernel; the decode loop and the 16-bit
+// edge kernels use gelu_poly below): the exp table is read from LDS (tbl = 17
 // floats, kExpNegTable), 1/(1 + p v) is the hardware reciprocal (1 ulp) and
 // contraction is allowed. No v > 4 case is needed: there q is clamped to 16
 // and poly(t) exp(-16) < 2^-25, so mag rounds to exactly 1. The sign is copied

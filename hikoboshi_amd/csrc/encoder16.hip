@@ -7,9 +7,9 @@
 // fp16(v), lo = fp16((v - hi) * 2048)): hi.hi + (hi.lo + lo.hi) / 2048 in fp32
 // carries about 22 significant bits, so the encoder is fp32-accurate (not
 // the reference's rounding sequence, which encoder.hip reproduces). Features,
-// biases, GELU (gelu_fast), LayerNorm (two-pass), residuals and the neighbour
-// sum are fp32, and h_V, h_E are stored in fp32. The kNN graph comes from the
-// exact fp32 kernel.
+// biases, GELU (gelu_poly in the edge kernels, gelu_fast in the node kernel),
+// LayerNorm (two-pass), residuals and the neighbour sum are fp32, and h_V, h_E
+// are stored in fp32. The kNN graph comes from the exact fp32 kernel.
 //
 // Edge products (the bulk of the work) run as workgroup tiles of 48 or 64 edge
 // rows and four waves: the tile's operand sits in LDS already split into fp16
