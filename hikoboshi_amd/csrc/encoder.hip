@@ -200,6 +200,7 @@ __global__ __launch_bounds__(kNodeThreads) void node_kernel(EncLayerDev w, const
                                                             float* __restrict__ h_v, float* __restrict__ prefix) {
 #pragma clang fp contract(off)
   static_assert(NR % 2 == 0 && NR <= 16, "thread mapping");
+  static_assert(kNodeThreads == kFF && kNodeThreads == 4 * kH, "one W_in column and bias per thread; four row groups");
   static_assert(kNodeChunks % kNodeDepth == 0 && 16 % kNodeDepth == 0, "phases start on a ring boundary");
   constexpr int RQ = NR >= 4 ? NR / 4 : 1;  // rows per thread in the message sum and W_out (4 row groups)
   constexpr int RP = NR / 2;                // rows per thread in the prefix products (2 row groups)
