@@ -1616,7 +1616,7 @@ __device__ inline uint32_t sched_ready8(const uint32_t* w, int words, int i) {
 // gives height r to the steps in its frontier (all of whose dependents have
 // heights), then takes them off their own earlier neighbours' counts of
 // dependents still without one; a neighbour whose count reaches zero joins the
-// next frontier. Round 1's frontier is every active step no step waits for.
+// next frontier. The first frontier is every active step no step waits for.
 // ht[u] = 0xFFFF for an inactive step; outw holds the counts as 16-bit halves;
 // list (nact 16-bit entries, L <= kSchedPrioMaxL) receives the frontiers one
 // after another. Returns the
