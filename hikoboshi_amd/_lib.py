@@ -18,7 +18,7 @@ STATUS_NAMES = {
     0: "Ok", 1: "InvalidArgument", 2: "FailedPrecondition", 3: "Unavailable", 4: "Unimplemented", 5: "InternalError",
 }
 ORDER_RANDOM, ORDER_INPUT_PER_SEQUENCE, ORDER_INPUT_SHARED, ORDER_N_TO_C = range(4)
-PRECISION_FP32, PRECISION_BF16, PRECISION_FP16 = range(3)
+PRECISION_FP32, PRECISION_BF16, PRECISION_FP16, PRECISION_BF16X3 = range(4)
 
 #: Symbols declared in include/*.h.
 EXPORTS = (
@@ -272,7 +272,7 @@ class Context:
             int(bool(greedy)), tokens_ptr, log_probs_ptr, scores_ptr, stream_ptr))
 
     def set_precision(self, precision: int) -> None:
-        """PRECISION_FP32 (default), PRECISION_BF16 or PRECISION_FP16 for later design calls."""
+        """PRECISION_FP32 (default), PRECISION_BF16, PRECISION_FP16 or PRECISION_BF16X3 for later design calls."""
         check(self._lib.hkbs_pmpnn_set_precision(self._h, int(precision)))
 
     def set_timing(self, enable: bool) -> None:

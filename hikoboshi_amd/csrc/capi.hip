@@ -294,27 +294,46 @@ size_t copy_f16(HostArena& ar, size_t src, size_t n) {
   return off;
 }
 
-// bf16 of W [N][kin] as [kin / 8][N][8] (the B fragments of the 16x16x32 MFMA).
-size_t pack_bf16_k8(HostArena& ar, const float* W, int N, int kin) {
+float from_bf16(uint16_t h) {
+  const uint32_t u = static_cast<uint32_t>(h) << 16;
+  float f = 0.0F;
+  std::memcpy(&f, &u, 4);
+  return f;
+}
+
+// The 16-bit forms of one weight: kHalfBf16 = bf16(w), kHalfBf16Lo = bf16(w - bf16(w))
+// (the remainder of the split bf16 decode: w ~ hi + lo to about 16 significant bits,
+// and hi + lo is exact in fp32), kHalfFp16 = fp16(w).
+enum HalfForm { kHalfFp16 = 0, kHalfBf16 = 1, kHalfBf16Lo = 2 };
+uint16_t to_half_form(float w, HalfForm form) {
+  switch (form) {
+    case kHalfBf16:
+      return to_bf16(w);
+    case kHalfBf16Lo:
+      return to_bf16(w - from_bf16(to_bf16(w)));
+    default:
+      return __builtin_bit_cast(uint16_t, static_cast<_Float16>(w));
+  }
+}
+
+// A 16-bit form of W [N][kin] as [kin / 8][N][8] (the B fragments of the 16x16x32 MFMA).
+size_t pack_bf16_k8(HostArena& ar, const float* W, int N, int kin, HalfForm form = kHalfBf16) {
   const size_t off = ar.add((size_t)N * kin / 2);
   auto* dst = reinterpret_cast<uint16_t*>(ar.data.data() + off);
   for (int n = 0; n < N; ++n)
-    for (int k = 0; k < kin; ++k) dst[((size_t)(k / 8) * N + n) * 8 + k % 8] = to_bf16(W[(size_t)n * kin + k]);
+    for (int k = 0; k < kin; ++k) dst[((size_t)(k / 8) * N + n) * 8 + k % 8] = to_half_form(W[(size_t)n * kin + k], form);
   return off;
 }
 
-// 16-bit copy (bf16, or fp16 if !bf16) of a t-layout matrix already packed at float offset
-// src ([kin][ldo], inputs outer, the first N columns used) as [kin / 8][N][8]: the B
-// fragments of the 16x16x32 MFMA, 8 consecutive inputs of one output per 16 bytes.
-size_t pack_k8_t(HostArena& ar, size_t src, int kin, int N, int ldo, bool bf16) {
+// A 16-bit form of a t-layout matrix already packed at float offset src ([kin][ldo],
+// inputs outer, the first N columns used) as [kin / 8][N][8]: the B fragments of the
+// 16x16x32 MFMA, 8 consecutive inputs of one output per 16 bytes.
+size_t pack_k8_t(HostArena& ar, size_t src, int kin, int N, int ldo, HalfForm form) {
   const size_t off = ar.add((size_t)N * kin / 2);
   auto* dst = reinterpret_cast<uint16_t*>(ar.data.data() + off);
   const float* s = ar.data.data() + src;
   for (int k = 0; k < kin; ++k)
-    for (int n = 0; n < N; ++n) {
-      const float w = s[(size_t)k * ldo + n];
-      dst[((size_t)(k / 8) * N + n) * 8 + k % 8] = bf16 ? to_bf16(w) : __builtin_bit_cast(uint16_t, static_cast<_Float16>(w));
-    }
+    for (int n = 0; n < N; ++n) dst[((size_t)(k / 8) * N + n) * 8 + k % 8] = to_half_form(s[(size_t)k * ldo + n], form);
   return off;
 }
 
@@ -462,9 +481,10 @@ hkbs_status build_model(hkbs_pmpnn* ctx, const float* const* t) {
     size_t pos_w, pos_b, edge_t, ne_g, ne_b, We_t, We_b, Ws;
     size_t W1b_dec_p, W1d_dec_p, Wlog_t, blog, Wlog_h, Wlog_f;
     size_t enc[kLayers][22];
-    size_t dec[kLayers][23];
+    size_t dec[kLayers][24];
     size_t dec_h[kLayers][4];  // bf16 of W3_t, Win_t, Wout_t, W1da_t as MFMA B fragments (pack_k8_t)
     size_t dec_f[kLayers][4];  // fp16 of the same
+    size_t dec_hl[kLayers][4];  // bf16 remainders of the same (split bf16 decode)
     size_t enc16[2 + 8 * kLayers];  // split-fp16 encoder weights: W_edge, W_e, then per layer
                                     // W1 W2 W3 W11 W12 W13 W_in W_out
   } o{};
@@ -566,6 +586,7 @@ hkbs_status build_model(hkbs_pmpnn* ctx, const float* const* t) {
       q[22] = pack_f16_split(ar, w1b.data(), 128, 128);  // W1b hi, lo (fp16)
     }
     q[21] = pack_bf16_k8(ar, d[2], 128, 128);         // W2 (bf16)
+    q[23] = pack_bf16_k8(ar, d[2], 128, 128, kHalfBf16Lo);  // W2 bf16 remainder
     q[16] = pack_k16(ar, {d[4]}, 128, 128, 0, 128);   // W3_p
     q[17] = pack_k16(ar, {d[10]}, 512, 128, 0, 128);  // Win_p
     q[18] = pack_k16(ar, {d[12]}, 128, 512, 0, 512);  // Wout_p
@@ -581,12 +602,12 @@ hkbs_status build_model(hkbs_pmpnn* ctx, const float* const* t) {
     } else {
       q[19] = 0;
     }
-    for (int h = 0; h < 2; ++h) {
-      size_t* dst = h == 0 ? o.dec_h[l] : o.dec_f[l];
-      dst[0] = pack_k8_t(ar, q[2], 128, 128, 128, h == 0);  // W3_t
-      dst[1] = pack_k8_t(ar, q[3], 128, 512, 512, h == 0);  // Win_t
-      dst[2] = pack_k8_t(ar, q[4], 512, 128, 128, h == 0);  // Wout_t
-      dst[3] = pack_k8_t(ar, q[5], 128, 256, 256, h == 0);  // W1da_t
+    for (HalfForm form : {kHalfBf16, kHalfFp16, kHalfBf16Lo}) {
+      size_t* dst = form == kHalfBf16 ? o.dec_h[l] : form == kHalfFp16 ? o.dec_f[l] : o.dec_hl[l];
+      dst[0] = pack_k8_t(ar, q[2], 128, 128, 128, form);  // W3_t
+      dst[1] = pack_k8_t(ar, q[3], 128, 512, 512, form);  // Win_t
+      dst[2] = pack_k8_t(ar, q[4], 512, 128, 128, form);  // Wout_t
+      dst[3] = pack_k8_t(ar, q[5], 128, 256, 256, form);  // W1da_t
     }
     q[7] = copy_raw(ar, d[1], 128);    // b1
     q[8] = copy_raw(ar, d[3], 128);    // b2
@@ -656,6 +677,11 @@ hkbs_status build_model(hkbs_pmpnn* ctx, const float* const* t) {
     w.Win_f = reinterpret_cast<const uint16_t*>(B + o.dec_f[l][1]);
     w.Wout_f = reinterpret_cast<const uint16_t*>(B + o.dec_f[l][2]);
     w.W1da_f = reinterpret_cast<const uint16_t*>(B + o.dec_f[l][3]);
+    w.W2_bl = reinterpret_cast<const uint16_t*>(B + q[23]);
+    w.W3_hl = reinterpret_cast<const uint16_t*>(B + o.dec_hl[l][0]);
+    w.Win_hl = reinterpret_cast<const uint16_t*>(B + o.dec_hl[l][1]);
+    w.Wout_hl = reinterpret_cast<const uint16_t*>(B + o.dec_hl[l][2]);
+    w.W1da_hl = reinterpret_cast<const uint16_t*>(B + o.dec_hl[l][3]);
     w.W3_t = B + q[2];
     w.Win_t = B + q[3];
     w.Wout_t = B + q[4];
@@ -915,8 +941,8 @@ hkbs_status design_on_device(hkbs_pmpnn* ctx, const float* coords, const uint8_t
   a.l0tab = l0tab;
   a.l0base = l0base;
   a.rec = rec;
-  if (a.precision != HKBS_PRECISION_FP32) {
-    // 16-bit modes read the message rows' inputs in fp16: E1 and the Q blocks 0..2 share E1's space
+  if (a.precision == HKBS_PRECISION_BF16 || a.precision == HKBS_PRECISION_FP16) {
+    // bf16 and fp16 modes read the message rows' inputs in fp16: E1 and the Q blocks 0..2 share E1's space
     // (3 S + 3 L halves <= 3 S floats), R rows take half of R's.
     _Float16* E1h = reinterpret_cast<_Float16*>(E1);
     a.E1h = E1h;
@@ -1247,7 +1273,8 @@ hkbs_status hkbs_pmpnn_design_device_noalloc(hkbs_pmpnn* ctx, const float* coord
 hkbs_status hkbs_pmpnn_set_precision(hkbs_pmpnn* ctx, int32_t precision) {
   hkbs_status st = enter(ctx);
   if (st != HKBS_OK) return st;
-  if (precision != HKBS_PRECISION_FP32 && precision != HKBS_PRECISION_BF16 && precision != HKBS_PRECISION_FP16)
+  if (precision != HKBS_PRECISION_FP32 && precision != HKBS_PRECISION_BF16 && precision != HKBS_PRECISION_FP16 &&
+      precision != HKBS_PRECISION_BF16X3)
     return fail(HKBS_INVALID_ARGUMENT, "unknown precision");
   ctx->precision = precision;
   return HKBS_OK;

@@ -55,7 +55,8 @@ constexpr int kGroup = kDecodeGroup;  // steps one workgroup decodes in a pass (
 // step's reduction) is still running. fma() accumulates one part in input
 // order, store() leaves per-group partial sums in LDS (part >= 8192 floats),
 // and after a barrier sum() adds the groups of one output in a fixed order.
-constexpr int kPrecFp32 = 0, kPrecBf16 = 1, kPrecFp16 = 2;  // decode arithmetic (DecodeArgs.precision)
+// decode arithmetic (DecodeArgs.precision): fp32, bf16, fp16, split bf16 (two bf16 terms per operand)
+constexpr int kPrecFp32 = 0, kPrecBf16 = 1, kPrecFp16 = 2, kPrecBf16x3 = 3;
 
 template <int IN, int OUT, int NP = 1, int WT = kPrecFp32>
 struct Gemv {
@@ -140,21 +141,28 @@ struct Gemv {
 // bits; the products accumulate in fp32. Wave w owns output columns [16 CPW w,
 // 16 CPW (w + 1)) over the whole input range (no partial sums), which part p
 // of NP splits into k-ranges loaded separately.
+// PREC = kPrecBf16x3 (split bf16): the weights too are two bf16 terms (W and its
+// remainder Wl, pack_k8_t kHalfBf16Lo), and each k-block takes three MFMAs,
+// x_hi W + (x_hi Wl + x_lo W); the dropped x_lo Wl is below 2^-16 of the product.
 template <int IN, int OUT, int NP, int PREC>
 struct MGemv {
-  static constexpr bool BF = PREC == kPrecBf16;
+  static constexpr bool X3 = PREC == kPrecBf16x3;
+  static constexpr bool BF = PREC == kPrecBf16 || X3;     // bf16 operands
   static constexpr int KB = IN / 32 / NP;                 // k-blocks of 32 inputs per part
   static constexpr int CPW = OUT / 16 / (kThreads / 64);  // 16-column blocks per wave
   static_assert(PREC != kPrecFp32 && KB * 32 * NP == IN && CPW * 16 * (kThreads / 64) == OUT, "MFMA product shape");
   using Op = typename std::conditional<BF, bf16x8, half8>::type;
   struct Part {
     Op b[CPW][KB];
+    Op bl[X3 ? CPW : 1][X3 ? KB : 1];  // split bf16: the weights' remainders
   };
   struct Acc {
-    floatx4 a[CPW], c[CPW];  // c: the fp16 lo products (scaled by 2048)
+    floatx4 a[CPW], c[CPW];  // c: the fp16 lo products (scaled by 2048), or the split bf16 remainder products
   };
-  // spread = 0: every lane loads the first fragment (a placeholder load that costs no L2 traffic)
-  static __device__ inline void load(Part& P, const uint16_t* __restrict__ W, int part, size_t spread = 1) {
+  // spread = 0: every lane loads the first fragment (a placeholder load that costs no L2 traffic).
+  // Wl (the remainders) is read only in the split bf16 mode.
+  static __device__ inline void load(Part& P, const uint16_t* __restrict__ W, const uint16_t* __restrict__ Wl, int part,
+                                     size_t spread = 1) {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
 #pragma unroll
     for (int cb = 0; cb < CPW; ++cb)
@@ -162,6 +170,7 @@ struct MGemv {
       for (int kb = 0; kb < KB; ++kb) {
         const size_t at = ((size_t)(4 * (part * KB + kb) + (lane >> 4)) * OUT + (wave * CPW + cb) * 16 + (lane & 15)) * 8;
         P.b[cb][kb] = *reinterpret_cast<const Op*>(W + at * spread);
+        if constexpr (X3) P.bl[cb][kb] = *reinterpret_cast<const Op*>(Wl + at * spread);
       }
   }
   static __device__ inline void zero(Acc& A) {
@@ -184,7 +193,11 @@ struct MGemv {
       }
 #pragma unroll
       for (int cb = 0; cb < CPW; ++cb) {
-        if constexpr (BF) {
+        if constexpr (X3) {
+          A.a[cb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, P.b[cb][kb], A.a[cb], 0, 0, 0);
+          A.c[cb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, P.bl[cb][kb], A.c[cb], 0, 0, 0);
+          A.c[cb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al, P.b[cb][kb], A.c[cb], 0, 0, 0);
+        } else if constexpr (BF) {
           A.a[cb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, P.b[cb][kb], A.a[cb], 0, 0, 0);
           A.a[cb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al, P.b[cb][kb], A.a[cb], 0, 0, 0);
         } else {
@@ -204,7 +217,7 @@ struct MGemv {
 #pragma unroll
       for (int e = 0; e < kGroup; ++e) {
         if (e >= ml) break;
-        ys[e * OUT + col] = BF ? A.a[cb][e] : A.a[cb][e] + A.c[cb][e] * (1.0F / 2048.0F);
+        ys[e * OUT + col] = X3 ? A.a[cb][e] + A.c[cb][e] : BF ? A.a[cb][e] : A.a[cb][e] + A.c[cb][e] * (1.0F / 2048.0F);
       }
     }
   }
@@ -212,11 +225,11 @@ struct MGemv {
 static_assert(kGroup == 4, "MGemv::store: members are rows 0..3 of a lane's accumulator");
 
 // Split 16-bit copy of one activation for MGemv: plane 0 = hi, plane 1 (lo_at
-// elements later) = lo; bf16: x = hi + lo, fp16: x = hi + lo / 2048 (|x| clamped
-// to the fp16 range).
+// elements later) = lo; bf16 and split bf16: x = hi + lo, fp16: x = hi + lo / 2048
+// (|x| clamped to the fp16 range).
 template <int PREC>
 __device__ inline void put_split16(uint16_t* hi, int lo_at, float v) {
-  if constexpr (PREC == kPrecBf16) {
+  if constexpr (PREC == kPrecBf16 || PREC == kPrecBf16x3) {
     const __bf16 h = static_cast<__bf16>(v);
     hi[0] = __builtin_bit_cast(uint16_t, h);
     hi[lo_at] = __builtin_bit_cast(uint16_t, static_cast<__bf16>(v - static_cast<float>(h)));
@@ -369,11 +382,18 @@ __device__ inline bool team_wait(uint32_t* counter, uint32_t target, uint32_t sp
 // fp32. kPrecBf16 / kPrecFp16: 16-bit weights for every product; message rows
 // rounded to 16 bits for one 16x16x32 MFMA per k-block; the layer products
 // (MGemv) on the MFMA with the fp32 activations split into two 16-bit parts,
-// accumulated in fp32. In every mode activations, LayerNorm, the logits (one
-// wave per member, weights in LDS) and the sampler are fp32.
+// accumulated in fp32. kPrecBf16x3 (split bf16): every product on the bf16 MFMA
+// with both operands as two bf16 terms (hi + lo) and three MFMAs per k-block
+// (hi.hi + hi.lo + lo.hi): the message rows into W2 and the weights of W2 and
+// of the layer products (MGemv); the message rows' inputs (E1, Q, R) stay
+// fp32, and so do the logit weights (hi + lo, exact in fp32). In every mode
+// activations, LayerNorm, the logits (one wave per member, weights in LDS) and
+// the sampler are fp32.
 template <int PREC>
 __global__ __launch_bounds__(kThreads) void decode_kernel(ModelDev m, DecodeArgs a) {
-  constexpr bool BF = PREC == kPrecBf16, HF = PREC == kPrecFp16;
+  constexpr bool BF = PREC == kPrecBf16, HF = PREC == kPrecFp16, X3 = PREC == kPrecBf16x3;
+  constexpr bool H16 = BF || HF;        // message rows' inputs (E1, Q, R) in fp16
+  constexpr bool M16 = BF || HF || X3;  // layer products on the MFMA (MGemv)
   using G3 = Gemv<kH, kH, 1, PREC>;
   using GIn = Gemv<kH, kFF, 2, PREC>;
   using GOut = Gemv<kFF, kH, 2, PREC>;
@@ -433,7 +453,7 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(ModelDev m, DecodeArgs
   const int32_t* draw = a.draw + qo * L;
   const int npass = a.npass[qo];
   float* R = a.R + (size_t)b * kLayers * L * kH;
-  _Float16* Rh = (BF || HF) ? a.Rh + (size_t)b * kLayers * L * kH : nullptr;  // 16-bit modes: R in fp16
+  _Float16* Rh = H16 ? a.Rh + (size_t)b * kLayers * L * kH : nullptr;  // bf16 / fp16 modes: R in fp16
   int32_t* tokens = a.tokens + (size_t)b * L;
   float* lp_out = a.log_probs ? a.log_probs + (size_t)b * L * kV : nullptr;
   float* chosen = a.chosen_lp + (size_t)b * L;
@@ -465,6 +485,10 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(ModelDev m, DecodeArgs
     float wv;
     if constexpr (BF) {
       wv = __uint_as_float(static_cast<uint32_t>(m.Wlog_h[e]) << 16);
+    } else if constexpr (X3) {  // hi + lo, exact in fp32
+      const float w0 = m.Wlog_t[e];
+      const float hi = static_cast<float>(static_cast<__bf16>(w0));
+      wv = hi + static_cast<float>(static_cast<__bf16>(w0 - hi));
     } else if constexpr (HF) {
       wv = static_cast<float>(__builtin_bit_cast(_Float16, m.Wlog_f[e]));
     } else {
@@ -489,7 +513,7 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(ModelDev m, DecodeArgs
         if (lp_out)
           for (int task = threadIdx.x; task < n0 * kV; task += kThreads)
             lp_out[(size_t)order[sched[s0 + task / kV]] * kV + task % kV] = 0.0F;
-        if constexpr (BF || HF) {  // fp16 rows, two columns per device-scope store
+        if constexpr (H16) {  // fp16 rows, two columns per device-scope store
           for (int task = threadIdx.x; task < n0 * kLayers * (kH / 2); task += kThreads) {
             const int i = task / (kLayers * kH / 2), l = (task / (kH / 2)) % kLayers, c = 2 * (task % (kH / 2));
             const int t = order[sched[s0 + i]];
@@ -637,13 +661,13 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(ModelDev m, DecodeArgs
       // row of each slot's neighbour). Every row is known when the pass starts (R
       // rows of earlier passes), so the first pair of layer l + 1 is gathered
       // during layer l's LayerNorm and fused product, and its latency is hidden.
-      constexpr bool kPipe = BF || HF;
+      constexpr bool kPipe = H16;
       constexpr int kS = 2 * kKmax / 16;
       static_assert(kKmax == 48 && kThreads == 512, "row mapping");
       const int c = 4 * (threadIdx.x & 31);
       const int r0 = threadIdx.x >> 5;
       // 16-bit modes: fp16 inputs, held raw (four per 8 bytes) until all loads are issued
-      using Raw = typename std::conditional<BF || HF, uint64_t, float4>::type;
+      using Raw = typename std::conditional<H16, uint64_t, float4>::type;
       Raw e[kS], z[kS];
       auto gather = [&](int ll, int i0) {
           // The slots' neighbour words and the two residues are read from LDS
@@ -668,7 +692,7 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(ModelDev m, DecodeArgs
               // z: the R row (written by the team) or the Q row, both read with a
               // device-scope load; one load per slot (two exec-masked loads into
               // one register set were issued one after the other)
-              if constexpr (BF || HF) {
+              if constexpr (H16) {
                 e[s] = *reinterpret_cast<const uint64_t*>(a.E1h + ((size_t)ll * S + tk) * kH + c);
                 z[s] = load8_dev((bw ? Rh : a.Qh) + ((size_t)ll * L + j) * kH + c);
               } else {
@@ -681,7 +705,7 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(ModelDev m, DecodeArgs
       // The first pair of layer l + 1 is gathered during layer l (kPrefetch); in
       // the fp32 kernel its registers would be spilled, so there it is gathered
       // where it is used.
-      constexpr bool kPrefetch = BF || HF;
+      constexpr bool kPrefetch = H16;
       if (kPrefetch) gather(0, 0);
       for (int l = 0; l < kLayers; ++l) {
         const DecLayerDev& w = m.dec[l];
@@ -703,12 +727,13 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(ModelDev m, DecodeArgs
           const int col = wave * 16 + r;
           // B fragments of the 16x16x32 MFMA: column col, k = 32 kb + 8 g + 0..7
           half8 bh[kH / 32], bl[kH / 32];
-          bf16x8 bb[kH / 32];
+          bf16x8 bb[kH / 32], bbl[kH / 32];
 #pragma unroll
           for (int kb = 0; kb < kH / 32; ++kb) {
             const size_t at = ((size_t)(4 * kb + g) * kH + col) * 4;  // float slots of 8 halves
-            if constexpr (BF) {
+            if constexpr (BF || X3) {
               bb[kb] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const float4*>(w.W2_b + 2 * at));
+              if constexpr (X3) bbl[kb] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const float4*>(w.W2_bl + 2 * at));
             } else {
               bh[kb] = __builtin_bit_cast(half8, *reinterpret_cast<const float4*>(w.W2h + at));
               if constexpr (!HF) bl[kb] = __builtin_bit_cast(half8, *reinterpret_cast<const float4*>(w.W2l + at));
@@ -725,7 +750,7 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(ModelDev m, DecodeArgs
                 const int i = i0 + s / 3, k = 16 * (s % 3) + r0;
                 if (i < ml) {
                   float4 ev, zv;
-                  if constexpr (BF || HF) {
+                  if constexpr (H16) {
                     ev = widen_h4(e[s]);
                     zv = widen_h4(z[s]);
                   } else {
@@ -752,6 +777,16 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(ModelDev m, DecodeArgs
 #pragma unroll
                     for (int e = 0; e < 4; ++e) hv[e] = static_cast<_Float16>(__builtin_amdgcn_fmed3f(vv[e], -65504.0F, 65504.0F));
                     *reinterpret_cast<half4*>(gh) = hv;
+                  } else if constexpr (X3) {
+                    // split for the bf16 MFMA: v = hi + lo, lo = bf16(v - hi), to about 2^-16 relative
+                    bf16x4 hv, lv;
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                      hv[e] = static_cast<__bf16>(vv[e]);
+                      lv[e] = static_cast<__bf16>(vv[e] - static_cast<float>(hv[e]));
+                    }
+                    *reinterpret_cast<bf16x4*>(gh) = hv;
+                    *reinterpret_cast<bf16x4*>(gh + kKmax * kLdH) = lv;
                   } else {
                     // split for the fp16 MFMA: v = hi + lo / 2048 to about 2^-22 relative
                     _Float16* gl = gh + kKmax * kLdH;
@@ -784,14 +819,14 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(ModelDev m, DecodeArgs
               }
               // A operands of k-block kb for the three row blocks, double buffered:
               // the next block's LDS reads are issued before this block's products.
-              using AOp = typename std::conditional<BF, bf16x8, half8>::type;
+              using AOp = typename std::conditional<BF || X3, bf16x8, half8>::type;
               AOp ah[2][3], al[2][3];
               auto aload = [&](int kb, int buf) {
 #pragma unroll
                 for (int mb = 0; mb < 3; ++mb) {
                   const int at = (mb * 16 + r) * kLdH + 32 * kb + 8 * g;
                   ah[buf][mb] = *reinterpret_cast<const AOp*>(Gh + at);
-                  if constexpr (PREC == kPrecFp32) al[buf][mb] = *reinterpret_cast<const AOp*>(Gl + at);
+                  if constexpr (PREC == kPrecFp32 || X3) al[buf][mb] = *reinterpret_cast<const AOp*>(Gl + at);
                 }
               };
               aload(0, 0);
@@ -804,6 +839,10 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(ModelDev m, DecodeArgs
                   const AOp& a0 = ah[kb & 1][mb];
                   if constexpr (BF) {
                     acc[mb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a0, bb[kb], acc[mb], 0, 0, 0);
+                  } else if constexpr (X3) {
+                    acc[mb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a0, bb[kb], acc[mb], 0, 0, 0);
+                    cor[mb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a0, bbl[kb], cor[mb], 0, 0, 0);
+                    cor[mb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al[kb & 1][mb], bb[kb], cor[mb], 0, 0, 0);
                   } else if constexpr (HF) {
                     acc[mb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a0, bh[kb], acc[mb], 0, 0, 0);
                   } else {
@@ -818,6 +857,11 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(ModelDev m, DecodeArgs
                 for (int mb = 0; mb < 3; ++mb)
 #pragma unroll
                   for (int e = 0; e < 4; ++e) acc[mb][e] += cor[mb][e] * (1.0F / 2048.0F);
+              } else if constexpr (X3) {
+#pragma unroll
+                for (int mb = 0; mb < 3; ++mb)
+#pragma unroll
+                  for (int e = 0; e < 4; ++e) acc[mb][e] += cor[mb][e];
               }
               // x[i][col] = sum over the member's K rows of GELU(acc + b2)
               float sum = 0.0F;
@@ -833,31 +877,36 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(ModelDev m, DecodeArgs
               sum += __shfl_xor(sum, 32, 64);
               if (lane < 16) {
                 x[i * kH + col] = sum;
-                if constexpr (BF || HF) put_split16<PREC>(xs16 + i * kH + col, kGroup * kH, sum);
+                if constexpr (M16) put_split16<PREC>(xs16 + i * kH + col, kGroup * kH, sum);
               }
             }
             if constexpr (!kPipe) __syncthreads();
           }
           if constexpr (kPipe) __syncthreads();
         }
-        if constexpr (BF || HF) {
+        if constexpr (M16) {
           // 16-bit modes: the four products on the MFMA (MGemv), inputs from the
-          // split copies, outputs in ys.
+          // split copies, outputs in ys. Weights in bf16 (bf16 and split bf16,
+          // with the remainders of the latter) or fp16. The split bf16 mode holds
+          // twice the fragments per k-block, so its products take more, smaller
+          // parts, each loaded while the part before it runs.
+          constexpr int kNpIn = X3 ? 4 : 1, kNpOut = X3 ? 4 : 2, kNpDa = X3 ? 2 : 1;
           using M3 = MGemv<kH, kH, 1, PREC>;
-          using MIn = MGemv<kH, kFF, 1, PREC>;
-          using MOut = MGemv<kFF, kH, 2, PREC>;
-          using MDa = MGemv<kH, 2 * kH, 1, PREC>;
+          using MIn = MGemv<kH, kFF, kNpIn, PREC>;
+          using MOut = MGemv<kFF, kH, kNpOut, PREC>;
+          using MDa = MGemv<kH, 2 * kH, kNpDa, PREC>;
+          const auto wsel = [](const uint16_t* h16, const uint16_t* f16) { return HF ? f16 : h16; };
           // upd = (W3 s + K b3) / 30 ; h1 = LN1(h + upd): wave i owns member i
           {
             typename M3::Part g3;
-            M3::load(g3, BF ? w.W3_h : w.W3_f, 0);
+            M3::load(g3, wsel(w.W3_h, w.W3_f), w.W3_hl, 0);
             typename M3::Acc a3;
             M3::zero(a3);
             M3::run(g3, 0, xs16, ml, a3);
             M3::store(a3, ml, ys);
           }
-          typename MIn::Part pin;  // W_in in flight during LN1
-          MIn::load(pin, BF ? w.Win_h : w.Win_f, 0);
+          typename MIn::Part pin[2];  // first part of W_in in flight during LN1
+          MIn::load(pin[0], wsel(w.Win_h, w.Win_f), w.Win_hl, 0);
           __syncthreads();
           if (wave < ml) {
             float v[2];
@@ -875,12 +924,16 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(ModelDev m, DecodeArgs
           }
           __syncthreads();
           // f = GELU(W_in h1 + b)
-          typename MOut::Part po0;  // first half of W_out in flight during W_in and the GELU
-          MOut::load(po0, BF ? w.Wout_h : w.Wout_f, 0);
+          typename MOut::Part po[2];  // first part of W_out in flight during W_in and the GELU
+          MOut::load(po[0], wsel(w.Wout_h, w.Wout_f), w.Wout_hl, 0);
           {
             typename MIn::Acc ai;
             MIn::zero(ai);
-            MIn::run(pin, 0, h1s16, ml, ai);
+#pragma unroll
+            for (int pp = 0; pp < kNpIn; ++pp) {
+              if (pp + 1 < kNpIn) MIn::load(pin[(pp + 1) & 1], wsel(w.Win_h, w.Win_f), w.Win_hl, pp + 1);
+              MIn::run(pin[pp & 1], pp, h1s16, ml, ai);
+            }
             MIn::store(ai, ml, ys);
           }
           __syncthreads();
@@ -891,23 +944,22 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(ModelDev m, DecodeArgs
             put_split16<PREC>(ffs16 + task, kGroup * kFF, f);
           }
           __syncthreads();
-          // h^{l+1} = LN2(h1 + (W_out f + b))
+          // h^{l+1} = LN2(h1 + (W_out f + b)); each next part in flight during the current part's products
           {
-            typename MOut::Part po1;  // second half in flight during the first half's products
-            MOut::load(po1, BF ? w.Wout_h : w.Wout_f, 1);
             typename MOut::Acc ao;
             MOut::zero(ao);
-            MOut::run(po0, 0, ffs16, ml, ao);
-            MOut::run(po1, 1, ffs16, ml, ao);
+#pragma unroll
+            for (int pp = 0; pp < kNpOut; ++pp) {
+              if (pp + 1 < kNpOut) MOut::load(po[(pp + 1) & 1], wsel(w.Wout_h, w.Wout_f), w.Wout_hl, pp + 1);
+              MOut::run(po[pp & 1], pp, ffs16, ml, ao);
+            }
             MOut::store(ao, ml, ys);
           }
           // the next layer's fused weights during LN2 (a placeholder load in the last layer)
-          typename MDa::Part pda;
-          {
-            const bool nxt = l + 1 < kLayers;
-            const DecLayerDev& nx = m.dec[nxt ? l + 1 : l];
-            MDa::load(pda, BF ? nx.W1da_h : nx.W1da_f, 0, nxt ? 1 : 0);
-          }
+          typename MDa::Part pda[2];
+          const bool nxt = l + 1 < kLayers;
+          const DecLayerDev& nx = m.dec[nxt ? l + 1 : l];
+          MDa::load(pda[0], wsel(nx.W1da_h, nx.W1da_f), nx.W1da_hl, 0, nxt ? 1 : 0);
           if (kPrefetch && l + 1 < kLayers) gather(l + 1, 0);  // the next layer's first pair
           __syncthreads();
           if (wave < ml) {
@@ -930,7 +982,11 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(ModelDev m, DecodeArgs
             {
               typename MDa::Acc ad;
               MDa::zero(ad);
-              MDa::run(pda, 0, hs16, ml, ad);
+#pragma unroll
+              for (int pp = 0; pp < kNpDa; ++pp) {
+                if (pp + 1 < kNpDa) MDa::load(pda[(pp + 1) & 1], wsel(nx.W1da_h, nx.W1da_f), nx.W1da_hl, pp + 1);
+                MDa::run(pda[pp & 1], pp, hs16, ml, ad);
+              }
               MDa::store(ad, ml, ys);
             }
             __syncthreads();
@@ -1076,7 +1132,7 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(ModelDev m, DecodeArgs
         }
       }
       __syncthreads();
-      if constexpr (BF || HF) {  // fp16 rows, two columns per device-scope store
+      if constexpr (H16) {  // fp16 rows, two columns per device-scope store
         for (int task = threadIdx.x; task < ml * kLayers * (kH / 2); task += kThreads) {
           const int i = task / (kLayers * kH / 2), l = (task / (kH / 2)) % kLayers, c = 2 * (task % (kH / 2));
           const int t = meta[i].x;
@@ -2019,6 +2075,8 @@ hipError_t launch_decode_as(const ModelDev& m, const DecodeArgs& args, hipStream
 
 int decode_team_size(int precision, int B, int max_team) {
   switch (precision) {
+    case kPrecBf16x3:
+      return team_size_as<kPrecBf16x3>(B, max_team);
     case kPrecBf16:
       return team_size_as<kPrecBf16>(B, max_team);
     case kPrecFp16:
@@ -2030,6 +2088,8 @@ int decode_team_size(int precision, int B, int max_team) {
 
 hipError_t launch_decode(const ModelDev& m, const DecodeArgs& args, hipStream_t stream, int max_team) {
   switch (args.precision) {
+    case kPrecBf16x3:
+      return launch_decode_as<kPrecBf16x3>(m, args, stream, max_team);
     case kPrecBf16:
       return launch_decode_as<kPrecBf16>(m, args, stream, max_team);
     case kPrecFp16:

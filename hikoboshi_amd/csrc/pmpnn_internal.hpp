@@ -63,6 +63,9 @@ struct DecLayerDev {
   // fragments [inputs / 8][outputs][8] (W2 like W2h; W3, Win, Wout, W1da from
   // their t-layouts)
   const uint16_t *W2_b, *W3_h, *Win_h, *Wout_h, *W1da_h;
+  // the bf16 remainders lo = bf16(w - hi) of the same, for the split bf16 decode
+  // (w = hi + lo to about 16 significant bits)
+  const uint16_t *W2_bl, *W3_hl, *Win_hl, *Wout_hl, *W1da_hl;
   const uint16_t *W3_f, *Win_f, *Wout_f, *W1da_f;  // fp16 copies (W2 in fp16 is W2h)
   const float* W3_t;   // [128][128]
   const float* Win_t;  // [128][512]
@@ -169,7 +172,7 @@ struct DecodeArgs {
   uint32_t* fault;        // [1] set when a team barrier times out, zero at launch
   int team;               // workgroups per sequence (set by launch_decode)
   uint32_t spin_limit;    // polls before a team barrier gives up (set by launch_decode)
-  int precision;          // 0 fp32, 1 bf16, 2 fp16 weights and message rows (see decode_kernel)
+  int precision;          // 0 fp32, 1 bf16, 2 fp16, 3 split bf16 (see decode_kernel)
   int max_members;        // most steps one pass decodes (<= kDecodeGroup * team size)
   int pass_granule;       // team size the schedule balances passes for (<= 1: none)
   const float* l0tab;     // layer-0 message rows (fp32 decode; launch_layer0_table), or null
