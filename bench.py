@@ -21,8 +21,10 @@ The JSON line also carries
                       same workload, timed on this host's cores before the GPU is touched;
   configs             the other workloads: L = 120 x 8 with per-sequence random orders, the
                       4 x 256 complex x 256 sequences, the 4,096-protein teacher-forced ragged
-                      batch and L = 4,000 x 32 in bf16, each with its time, throughput, a spot
-                      check against the CPU reference and a CPU baseline of its own.
+                      batch and L = 4,000 x 32 in split bf16 (every decoder product on the bf16
+                      MFMA with both operands as two bf16 terms; plain bf16 and fp32 timed beside
+                      it), each with its time, throughput, a spot check against the CPU reference
+                      and a CPU baseline of its own.
 """
 from __future__ import annotations
 
@@ -49,7 +51,14 @@ F_RES = 29_103_360        # FLOP per sampled residue, reference arithmetic at K=
 # from the precomputed table (the decode then only sums 48 rows of it), so two layers are message layers.
 F_W2_LAYER = 2 * 48 * 128 * 128
 F_MSG_VALU_LAYER = 2 * 48 * 128 + 48 * 128
-F_VALU_REST = 3 * (2 * 128 * 128 + 2 * 2 * 128 * 512) + 2 * (2 * 128 * 256) + 2 * 128 * 21
+F_LOGITS = 2 * 128 * 21
+F_LAYER_PRODUCTS = 3 * (2 * 128 * 128 + 2 * 2 * 128 * 512) + 2 * (2 * 128 * 256)  # W3, W_in, W_out, next [W1d | W1a]
+F_VALU_REST = F_LAYER_PRODUCTS + F_LOGITS
+# MFMA products per product of the 16-bit modes: bf16 / fp16 multiply the two halves of the split
+# activations by one 16-bit weight; split bf16 takes hi.hi + hi.lo + lo.hi. W2's message rows are one
+# bf16 / fp16 operand in those modes, two bf16 terms in split bf16.
+SPLIT_PRODUCTS = {"bf16": (1, 2), "fp16": (1, 2), "bf16x3": (3, 3)}  # (W2, layer products)
+PRECISION_CODES = {"fp32": 0, "bf16": 1, "fp16": 2, "bf16x3": 3}
 L0_TABLE_MAX_BYTES = 4 << 30  # the library's limit for the layer-0 table (22 rows of 128 floats per slot)
 W_DEC = 698_133           # decoder + W_out + W_s floats
 PEAK_FP32_TFLOPS = 157.3  # MI355X dense fp32 (vector and matrix)
@@ -68,8 +77,9 @@ def parse_args():
     p.add_argument("--num-seqs", type=int, default=64)
     p.add_argument("--temperature", type=float, default=0.1)
     p.add_argument("--seed", type=int, default=7)
-    p.add_argument("--precision", choices=("fp32", "bf16"), default="fp32",
-                   help="design arithmetic of the headline workload (bf16: bf16 decoder)")
+    p.add_argument("--precision", choices=("fp32", "bf16", "bf16x3"), default="fp32",
+                   help="design arithmetic of the headline workload (bf16: bf16 decoder; bf16x3: split bf16 "
+                        "decoder, both operands of every product as two bf16 terms)")
     p.add_argument("--workers", type=int, default=0, help="CPU worker processes (default: min(16, host CPUs))")
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baselines")
     p.add_argument("--no-configs", action="store_true", help="headline workload only")
@@ -97,7 +107,7 @@ def workloads(args):
 
     L, B = args.L, args.num_seqs
     bb = backbone.single_chain(L, seed)
-    suffix = "" if args.precision == "fp32" else "_bf16"
+    suffix = "" if args.precision == "fp32" else "_" + args.precision
     W = {"C2": dict(name=f"design_L{L}_B{B}{suffix}", bb=bb, B=B, T=args.temperature, order=shared_order(bb),
                     seeds=(seed + np.arange(B)).astype(np.uint64), precision=args.precision,
                     cpu_seqs=list(range(min(B, 16))))}
@@ -110,8 +120,8 @@ def workloads(args):
                        seeds=(seed + np.arange(256)).astype(np.uint64), precision="fp32",
                        cpu_seqs=[int(b) for b in np.linspace(0, 255, 16).round()])
         c5 = backbone.single_chain(4000, seed)
-        W["C5"] = dict(name="design_L4000_B32_bf16", bb=c5, B=32, T=0.1, order=shared_order(c5),
-                       seeds=(seed + np.arange(32)).astype(np.uint64), precision="bf16", cpu_seqs=[0])
+        W["C5"] = dict(name="design_L4000_B32_bf16x3", bb=c5, B=32, T=0.1, order=shared_order(c5),
+                       seeds=(seed + np.arange(32)).astype(np.uint64), precision="bf16x3", cpu_seqs=[0])
         coords, src, tok, off = backbone.ragged_batch(4096, seed)
         pick = np.sort(np.random.default_rng(seed).choice(4096, C4_CPU_PROTEINS, replace=False))
         W["C4"] = dict(name="score_ragged4096", batch=(coords, src, tok, off), cpu_proteins=[int(i) for i in pick])
@@ -313,16 +323,28 @@ def l0_table_used(precision: str, L: int) -> bool:
         L * K * 22 * 128 * 4 <= L0_TABLE_MAX_BYTES
 
 
-def decode_roofline(ctx, w, order, decode_ms):
+def decode_roofline(ctx, w, order, decode_ms, precision=None, name=None):
     """The decode kernel against HBM bandwidth (algorithmic bytes) and its executed FLOP against the
     VALU fp32 and MFMA peaks."""
     bb, B, L = w["bb"], w["B"], w["bb"].L
     K = min(48, L)
-    bf16 = w["precision"] == "bf16"
-    table = l0_table_used(w["precision"], L)
+    prec = precision or w["precision"]
+    table = l0_table_used(prec, L)
     msg_layers = 2 if table else 3
-    f_valu = msg_layers * F_MSG_VALU_LAYER + (48 * 128 if table else 0) + F_VALU_REST
-    f_mfma = (1 if bf16 else 3) * msg_layers * F_W2_LAYER
+    if prec == "fp32":  # W2 on the fp16 MFMA (split operands), the layer products on the VALU
+        f_valu = msg_layers * F_MSG_VALU_LAYER + (48 * 128 if table else 0) + F_VALU_REST
+        f_mfma = 3 * msg_layers * F_W2_LAYER
+        mfma_key = "mfma_fp16"
+        mfma_note = (f"W2 of {msg_layers} layers as three fp16 products of split operands (hi.hi + hi.lo + lo.hi)"
+                     + ("; layer 0's rows come from the layer-0 table kernel, outside this launch" if table else ""))
+    else:  # W2 and the layer products on the MFMA
+        w2x, lpx = SPLIT_PRODUCTS[prec]
+        f_valu = 3 * F_MSG_VALU_LAYER + F_LOGITS
+        f_mfma = w2x * 3 * F_W2_LAYER + lpx * F_LAYER_PRODUCTS
+        mfma_key = "mfma_fp16" if prec == "fp16" else "mfma_bf16"
+        mfma_note = (f"W2 of all three layers as {w2x} and W3, W_in, W_out and the fused next-layer product as "
+                     f"{lpx} {'fp16' if prec == 'fp16' else 'bf16'} products each, useful rows only (members "
+                     "of a pass fill rows of the 16-row tiles)")
     idx, _ = ctx.knn(bb.coords, bb.atom_sources)
     pos = np.empty(L, np.int64)
     pos[order] = np.arange(L)
@@ -330,13 +352,9 @@ def decode_roofline(ctx, w, order, decode_ms):
     launch_bytes = 4.0 * (B * (3 * H * e_bw + L * (2 * H + V + 1)) + L * (2 * K + 1) * H + W_DEC)
     t = decode_ms * 1e-3
     achieved = launch_bytes / t / 1e9
-    traffic, traffic_src = measured_traffic(w["name"])
+    traffic, traffic_src = measured_traffic(name or w["name"])
     valu = B * L * f_valu / t / 1e12
     mfma = B * L * f_mfma / t / 1e12
-    mfma_key = "mfma_bf16" if bf16 else "mfma_fp16"
-    mfma_note = ("W2 of all three layers as one bf16 product" if bf16 else
-                 f"W2 of {msg_layers} layers as three fp16 products of split operands (hi.hi + hi.lo + lo.hi)"
-                 + ("; layer 0's rows come from the layer-0 table kernel, outside this launch" if table else ""))
     return {
         "kernel": "decode_kernel",
         "bound": "hbm",
@@ -401,6 +419,22 @@ def calibrate_copy(mib: int) -> int:
     return 0
 
 
+def trajectory_deviation(ctx, w, order, run, n):
+    """max |d log p| of the last run's first n sequences against the fp32 path on the same trajectory:
+    fp32 teacher-forced log-probs of the run's tokens and order, rescaled to the run's T (contract 2e-2)."""
+    worst = 0.0
+    bb = w["bb"]
+    for b in range(n):
+        tok = run.h_tokens.array[b].copy()
+        lp1, _ = ctx.score(bb.coords, bb.atom_sources, tok, order=order)
+        z = lp1.astype(np.float64) / w["T"]
+        z -= z.max(1, keepdims=True)
+        ref = z - np.log(np.exp(z).sum(1, keepdims=True))
+        worst = max(worst, float(np.abs(run.h_lp.array[b] - ref).max()))
+    return {"max_abs_dlogp": round(worst, 6), "sequences": n, "contract": 2e-2,
+            "note": "fp32 teacher-forced log-probs of the run's tokens and order, at T"}
+
+
 def run_configs(ctx, cpu, workers, model, wall, steps, warmup):
     """C1, C3, C4 and C5 on the GPU, each with its CPU baseline and spot check."""
     from hikoboshi_amd import _lib
@@ -442,11 +476,23 @@ def run_configs(ctx, cpu, workers, model, wall, steps, warmup):
                "decode_order": "shared random permutation (reference routine, seed 7)",
                "inputs": "device buffers, outputs copied to pinned host memory"}
         if cfg == "C5":
+            # fp32 first (the tolerance reference and the CPU spot check), then plain bf16 (kept beside
+            # the result: it misses the contract), then the configuration's mode, split bf16.
             ms32, ph32 = run.run(steps, warmup)
             fp32_tokens, fp32_lp = run.h_tokens.array.copy(), run.h_lp.array.copy()
             res["fp32"] = {"ms": round(ms32, 4), "value": round(w["B"] * w["bb"].L / (ms32 * 1e-3), 1),
                            "decode_ms": round(float(ph32[2]), 4)}
             ctx.set_precision(_lib.PRECISION_BF16)
+            try:
+                msb, phb = run.run(steps, warmup)
+            finally:
+                ctx.set_precision(_lib.PRECISION_FP32)
+            res["plain_bf16"] = {
+                "mode": "HKBS_PRECISION_BF16: bf16 weights, bf16 message rows into W2, fp16 E1/Q/R rows",
+                "ms": round(msb, 4), "value": round(w["B"] * w["bb"].L / (msb * 1e-3), 1),
+                "decode_ms": round(float(phb[2]), 4),
+                "bf16_vs_fp32": trajectory_deviation(ctx, w, order, run, 2)}
+            ctx.set_precision(PRECISION_CODES[w["precision"]])
         try:
             ms, ph = run.run(steps, warmup)
         finally:
@@ -458,18 +504,11 @@ def run_configs(ctx, cpu, workers, model, wall, steps, warmup):
                     "us_per_decode_step": round(float(ph[2]) * 1e3 / w["bb"].L, 3),
                     "roofline": decode_roofline(ctx, w, order, float(ph[2]))})
         if cfg == "C5":
-            # bf16 against the fp32 path on the bf16 run's own trajectory at the config's T (contract 2e-2)
-            worst = 0.0
-            bb = w["bb"]
-            for b in range(2):
-                tok = run.h_tokens.array[b].copy()
-                lp1, _ = ctx.score(bb.coords, bb.atom_sources, tok, order=order)
-                z = lp1.astype(np.float64) / w["T"]
-                z -= z.max(1, keepdims=True)
-                ref = z - np.log(np.exp(z).sum(1, keepdims=True))
-                worst = max(worst, float(np.abs(run.h_lp.array[b] - ref).max()))
-            res["bf16_vs_fp32"] = {"max_abs_dlogp": round(worst, 5), "sequences": 2, "contract": 2e-2,
-                                   "note": "fp32 teacher-forced log-probs of the bf16 run's tokens and order, at T"}
+            res["mode"] = ("HKBS_PRECISION_BF16X3 (split bf16): every decoder product on the bf16 MFMA with "
+                           "weights and inputs each as two bf16 terms (hi + lo), three MFMAs per product, fp32 "
+                           "accumulation, GELU, LayerNorm and softmax; E1/Q/R rows fp32; encoder on the fp16 "
+                           "MFMA with split operands")
+            res["bf16_vs_fp32"] = trajectory_deviation(ctx, w, order, run, w["B"])
             tokens, lps = fp32_tokens, fp32_lp
         else:
             tokens, lps = run.h_tokens.array, run.h_lp.array
@@ -531,8 +570,8 @@ def main() -> int:
     if not np.array_equal(order, w["order"]):
         raise RuntimeError("decode order differs between the library and the oracle")
     ctx = _lib.Context(weights.read_package_bytes(), device=0)
-    if args.precision == "bf16":
-        ctx.set_precision(_lib.PRECISION_BF16)
+    if args.precision != "fp32":
+        ctx.set_precision(PRECISION_CODES[args.precision])
     run = DeviceDesign(ctx, w, order)
     ms_per_step, ph = run.run(args.steps, args.warmup)
     decode_ms = float(ph[2])
@@ -548,7 +587,7 @@ def main() -> int:
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "f32" if args.precision == "fp32" else "bf16",
+        "dtype": "f32" if args.precision == "fp32" else "bf16" if args.precision.startswith("bf16") else "f16",
         "data": "synthetic",
         "config": {
             "workload": w["name"],

@@ -219,6 +219,8 @@ WORKLOADS = {
     "design_L120_B8": dict(L=120, B=8, temperature=0.1, seed=7, order="random_per_seq"),
     "design_L300_B64": dict(L=300, B=64, temperature=0.1, seed=7, order="shared_random"),
     "complex_4x256_B256": dict(L=1024, B=256, temperature=0.2, seed=7, order="shared_random"),
+    "design_L4000_B32_bf16x3": dict(L=4000, B=32, temperature=0.1, seed=7, order="shared_random",
+                                    precision="bf16x3"),
     "design_L4000_B32_bf16": dict(L=4000, B=32, temperature=0.1, seed=7, order="shared_random", precision="bf16"),
 }
 

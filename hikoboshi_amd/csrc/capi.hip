@@ -362,7 +362,11 @@ struct DeviceArena {
     base = nullptr;
     cap = 0;
     hipError_t e = hipMalloc(&base, bytes);
-    if (e != hipSuccess) return e;
+    if (e != hipSuccess) {
+      (void)hipGetLastError();  // a failed allocation's error must not surface from a later launch check
+      base = nullptr;
+      return e;
+    }
     cap = bytes;
     return hipSuccess;
   }
@@ -763,10 +767,17 @@ EncodeBuffers take_encode(DeviceArena& ar, int L, int K) {
 }
 
 // Featurisation and encoder: the reference's fp32 rounding sequence, or in the
-// 16-bit modes the split-operand fp16 MFMA (fp32-level accuracy).
+// 16-bit modes the split-operand fp16 MFMA (fp32-level accuracy). In fp32 mode
+// HKBS_ENCODER=mfma selects the MFMA encoder too (fp32-accurate, not the
+// reference's rounding sequence).
+bool mfma_encoder_forced() {
+  const char* env = std::getenv("HKBS_ENCODER");
+  return env && std::strcmp(env, "mfma") == 0;
+}
+
 hipError_t launch_featurise_encode(hkbs_pmpnn* ctx, const float* coords, const uint8_t* src, const int32_t* resid,
                                    const int32_t* chain, int L, int K, const EncodeBuffers& e) {
-  if (ctx->precision != HKBS_PRECISION_FP32)
+  if (ctx->precision != HKBS_PRECISION_FP32 || mfma_encoder_forced())
     return launch_encoder16(ctx->model, coords, src, resid, chain, e.idx, e.mask, L, K, e.h_v, e.h_e, e.scratch,
                             ctx->stream);
   hipError_t err = launch_edge_embed(ctx->model, coords, src, resid, chain, e.idx, L, K, e.h_e, ctx->stream);
@@ -872,6 +883,34 @@ size_t design_scratch_bytes(int L, int B, bool shared, bool l0table) {
          aligned_bytes<int32_t>(nq) + aligned_bytes<int32_t>(nq * L) + aligned_bytes<int32_t>(sched_scratch_words(L, K, nq)) +
          (l0table ? aligned_bytes<float>(l0_table_floats(L, K)) + aligned_bytes<int32_t>((size_t)L + 1) : 0) +
          aligned_bytes<float4>(nq * L * kRecFloat4);
+}
+
+// Reserves the context's workspace for need(l0table) bytes. The layer-0 table
+// only saves time (the results are the same without it), so when that
+// reservation fails the table is dropped (l0table = false) and the smaller
+// reservation is tried before the call fails.
+template <typename Need>
+hkbs_status reserve_workspace(DeviceArena& ar, const Need& need, bool& l0table) {
+  if (ar.reserve(need(l0table)) == hipSuccess) return HKBS_OK;
+  if (l0table) {
+    l0table = false;
+    if (ar.reserve(need(false)) == hipSuccess) return HKBS_OK;
+  }
+  return fail(HKBS_INTERNAL_ERROR, "device workspace allocation failed");
+}
+
+// A device entry point called with the caller's stream runs its work there. It
+// first waits for anything still pending on the context's own stream (earlier
+// calls may use the same workspace), except while the caller's stream is being
+// captured into a HIP graph: a capture must not synchronise other streams, and
+// the caller orders the captured work after earlier calls.
+hkbs_status adopt_caller_stream(hkbs_pmpnn* ctx, void* stream) {
+  hipStream_t user = static_cast<hipStream_t>(stream);
+  hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+  HK_CHECK(hipStreamIsCapturing(user, &cs), "stream capture query failed");
+  if (cs == hipStreamCaptureStatusNone) HK_CHECK(hipStreamSynchronize(ctx->stream), "context stream failed");
+  ctx->stream = user;
+  return HKBS_OK;
 }
 
 // Shared implementation of the device design path. All pointers device.
@@ -1147,13 +1186,14 @@ hkbs_status hkbs_pmpnn_design(hkbs_pmpnn* ctx, const float* coords, const uint8_
 
   const int K = std::min(kKmax, L);
   const size_t norders = shared ? (size_t)L : (size_t)B * L;
-  const bool l0table = l0_table_wanted(ctx->precision, L);
-  const size_t need = input_bytes(L) + encode_bytes(L, K) + decode_bytes(L, K, B, l0table) + aligned_bytes<int32_t>(norders) +
-                      aligned_bytes<uint64_t>(B) + aligned_bytes<int32_t>((size_t)B * L) +
-                      aligned_bytes<float>((size_t)B * L * kV) + aligned_bytes<float>(B) + aligned_bytes<float>((size_t)B * L) +
-                      (64u << 10);
+  bool l0table = l0_table_wanted(ctx->precision, L);
+  const auto need = [&](bool tab) {
+    return input_bytes(L) + encode_bytes(L, K) + decode_bytes(L, K, B, tab) + aligned_bytes<int32_t>(norders) +
+           aligned_bytes<uint64_t>(B) + aligned_bytes<int32_t>((size_t)B * L) + aligned_bytes<float>((size_t)B * L * kV) +
+           aligned_bytes<float>(B) + aligned_bytes<float>((size_t)B * L) + (64u << 10);
+  };
   DeviceArena& ar = ctx->arena;
-  if (ar.reserve(need) != hipSuccess) return fail(HKBS_INTERNAL_ERROR, "device workspace allocation failed");
+  if ((st = reserve_workspace(ar, need, l0table)) != HKBS_OK) return st;
   ar.reset();
   Inputs in{};
   if ((st = upload_inputs(ctx, ar, coords, atom_sources, residue_indices, chain_labels, chain_mask, true_tokens, L, in)) != HKBS_OK)
@@ -1212,18 +1252,18 @@ hkbs_status hkbs_pmpnn_design_device(hkbs_pmpnn* ctx, const float* coords, const
   if (!coords || !atom_sources || !orders || !sampler_seeds || !tokens)
     return fail(HKBS_INVALID_ARGUMENT, "device design pointers must be non-null");
   const int K = std::min(kKmax, L);
-  const bool l0table = l0_table_wanted(ctx->precision, L);
-  const size_t need = encode_bytes(L, K) + decode_bytes(L, K, B, l0table) + aligned_bytes<float>((size_t)B * L) + (64u << 10);
+  bool l0table = l0_table_wanted(ctx->precision, L);
+  const auto need = [&](bool tab) {
+    return encode_bytes(L, K) + decode_bytes(L, K, B, tab) + aligned_bytes<float>((size_t)B * L) + (64u << 10);
+  };
   DeviceArena& ar = ctx->arena;
   hipStream_t saved = ctx->stream;
   if (stream) {
-    // Work on the caller's stream: wait for anything pending on ours first.
-    HK_CHECK(hipStreamSynchronize(saved), "context stream failed");
-    ctx->stream = static_cast<hipStream_t>(stream);
+    if ((st = adopt_caller_stream(ctx, stream)) != HKBS_OK) return st;
   }
-  if (ar.reserve(need) != hipSuccess) {
+  if ((st = reserve_workspace(ar, need, l0table)) != HKBS_OK) {
     ctx->stream = saved;
-    return fail(HKBS_INTERNAL_ERROR, "device workspace allocation failed");
+    return st;
   }
   ar.reset();
   float* chosen = ar.take<float>((size_t)B * L);
@@ -1259,8 +1299,7 @@ hkbs_status hkbs_pmpnn_design_device_noalloc(hkbs_pmpnn* ctx, const float* coord
   ar.cap = kNoAllocScratchBytes;
   hipStream_t saved = ctx->stream;
   if (stream) {
-    HK_CHECK(hipStreamSynchronize(saved), "context stream failed");
-    ctx->stream = static_cast<hipStream_t>(stream);
+    if ((st = adopt_caller_stream(ctx, stream)) != HKBS_OK) return st;
   }
   float* chosen = ar.take<float>((size_t)B * L);
   st = design_on_device(ctx, coords, atom_sources, residue_indices, chain_labels, chain_mask, true_tokens, L, B, orders,

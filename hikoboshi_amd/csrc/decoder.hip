@@ -451,6 +451,15 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(ModelDev m, DecodeArgs
   const int32_t* sched = a.sched + qo * L;
   const int32_t* pstart = a.pstart + qo * (L + 2);
   const int32_t* draw = a.draw + qo * L;
+  // An order that is not a permutation of 0..L-1 is not decoded (the reference
+  // rejects it, decode_order_scalar.cpp:67-79; the host entry points check
+  // orders before any GPU work, the device entry points cannot): the sequence
+  // keeps a NaN score and its tokens and log-probs are not written. Every rank
+  // of a team reads the same flag, so the team leaves together.
+  if (sched_meta(a.sched_tmp, L, a.shared_order ? 1 : a.B)[qo * 4 + 3] == 0) {
+    if (a.scores && rank == 0 && threadIdx.x == 0) a.scores[b] = __builtin_nanf("");
+    return;
+  }
   const int npass = a.npass[qo];
   float* R = a.R + (size_t)b * kLayers * L * kH;
   _Float16* Rh = H16 ? a.Rh + (size_t)b * kLayers * L * kH : nullptr;  // bf16 / fp16 modes: R in fp16
@@ -1513,12 +1522,14 @@ __global__ void neighbour_schedule_kernel(const int32_t* __restrict__ orders, co
 // ready_schedule_kernel). Inactive residues
 // (mask 0) read nothing and form pass 0, which runs before all others; entries
 // outside 0..L-1 are dropped. If the order is not a permutation (a residue
-// repeated), every active step gets a pass of its own, in order: sequential
-// decoding (also selected by HKBS_DECODE_SCHEDULE=sequential).
+// repeated), every active step gets a pass of its own, in order, as with
+// HKBS_DECODE_SCHEDULE=sequential, and the decode kernel refuses the order.
 // Outputs per order: sched [L] (steps grouped by pass, increasing u within a
 // pass), pstart [L + 2] (pass p holds sched[pstart[p] .. pstart[p + 1])),
-// npass (passes after pass 0) and draw [L] (index of the step's sampler draw
-// among the active steps: the sampler stream is consumed in order of u).
+// npass (passes after pass 0), draw [L] (index of the step's sampler draw
+// among the active steps: the sampler stream is consumed in order of u) and
+// the order's four sched_meta words (word 3 = permutation flag: the decode
+// kernel does not decode an order that is not a permutation).
 // Four kernels: pending-dependency and dependent counts over all (step, slot)
 // pairs; per order the permutation check, draw indices, pass 0 and the
 // dependents' offsets; the dependents lists; per order the step heights (for
@@ -1595,12 +1606,14 @@ __global__ __launch_bounds__(kSchedThreads) void sched_prep_kernel(const int32_t
   int32_t* oq = off + (size_t)q * (L + 1);
   int32_t* dq = draw + (size_t)q * L;
   int32_t* sq = sched + (size_t)q * L;
-  if (threadIdx.x == 0) bad = sequential;
+  if (threadIdx.x == 0) bad = 0;
   __syncthreads();
   for (int u = threadIdx.x; u < L; u += kSchedThreads) {
     const int t = order[u];
     if (t < 0 || t >= L || pq[t] != u) bad = 1;
   }
+  __syncthreads();
+  const int not_perm = bad;
   int act = 0, inact = 0, deps = 0;
   for (int u0 = 0; u0 < L; u0 += kSchedThreads) {
     const int u = u0 + threadIdx.x;
@@ -1624,9 +1637,10 @@ __global__ __launch_bounds__(kSchedThreads) void sched_prep_kernel(const int32_t
     int32_t* ps = pstart + (size_t)q * (L + 2);
     ps[0] = 0;
     ps[1] = inact;
-    meta[(size_t)q * 4 + 0] = !bad;
+    meta[(size_t)q * 4 + 0] = !(not_perm || sequential);
     meta[(size_t)q * 4 + 1] = act;
     meta[(size_t)q * 4 + 2] = inact;
+    meta[(size_t)q * 4 + 3] = !not_perm;
   }
 }
 
@@ -2008,7 +2022,7 @@ hipError_t launch_decode_schedule(const DecodeArgs& a, hipStream_t stream) {
   int32_t* indeg = a.sched_tmp;            // [nq][L]
   int32_t* off = indeg + nq * L;           // [nq][L + 1]: counts, then offsets
   int32_t* cur = off + nq * (L + 1);       // [nq][L]
-  int32_t* meta = cur + nq * L;            // [nq][4]
+  int32_t* meta = cur + nq * L;            // [nq][4] (= sched_meta(a.sched_tmp, L, nq))
   int32_t* dlist = meta + nq * 4;          // [nq][L K]
   hipError_t err = launch_zero(reinterpret_cast<float*>(indeg), nq * (3 * L + 1), stream);
   if (err != hipSuccess) return err;

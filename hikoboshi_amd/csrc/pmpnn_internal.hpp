@@ -186,6 +186,11 @@ struct DecodeArgs {
 constexpr int kDecodeGroup = 4;  // steps one workgroup decodes in a pass
 // int32 words of DecodeArgs.sched_tmp for nq orders of length L with K neighbours.
 inline size_t sched_scratch_words(size_t L, size_t K, size_t nq) { return nq * (3 * L + 1 + 4 + L * K); }
+// Four words per order inside sched_tmp, written by the schedule: {decoded in dependency
+// passes, active steps, inactive steps, the order is a permutation of 0..L-1}.
+__host__ __device__ inline int32_t* sched_meta(int32_t* sched_tmp, size_t L, size_t nq) {
+  return sched_tmp + nq * (3 * L + 1);
+}
 // Per-step neighbour lists (a.nbj, a.nbp) and the pass schedule (a.sched,
 // a.pstart, a.npass, a.draw) from the orders, positions, mask and kNN graph;
 // launch_decode reads them.

@@ -64,8 +64,8 @@ def test_design_complex_4x256_b256(gpu_ctx, oracle):
     idx = enc[1]
     assert idx.shape == (L, 48)
     assert (cx.chain_labels[idx] != cx.chain_labels[:, None]).any(), "no cross-chain kNN edges"
-    which = sorted({int(b) for b in np.linspace(0, B - 1, 16).round()} | {1, 130})
-    assert replay_many(oracle, enc, order, seeds, T, res, which) <= LP_TOL
+    # every sequence; positions above the bar are arbitrated by the float64 decoder
+    assert replay_many(oracle, enc, order, seeds, T, res, list(range(B)), arbitrate=True, bb=cx) <= LP_TOL
 
 
 @pytest.fixture(scope="module")
@@ -86,7 +86,7 @@ def test_design_long_chain_fp32(gpu_ctx, oracle, long_chain):
     _design_properties(res, L, B)
     _say("  oracle encode L=4000")
     enc = oracle.encode(bb)
-    assert replay_many(oracle, enc, order, seeds, T, res, [0, 1, 16, B - 1]) <= LP_TOL
+    assert replay_many(oracle, enc, order, seeds, T, res, [0, 1, 16, B - 1], arbitrate=True, bb=bb) <= LP_TOL
 
 
 BF16_TOL = 2e-2  # bf16 per-position log-probs against the fp32 path of the same inputs

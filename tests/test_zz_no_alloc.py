@@ -5,7 +5,9 @@ with its scratch in one static device array per GPU, so its outputs must be
 bit-identical to that entry point's on the same inputs. Two calls in a row (the
 second smaller, with per-sequence orders, chain labels and residue offsets)
 check that what the first call leaves in the shared array does not leak into
-the second; an oversized request is refused before any GPU work.
+the second; an oversized request is refused before any GPU work. A call leaves
+the device's free memory unchanged, and the call captured on a caller's stream
+into a HIP graph replays to the same bits, with other work between replays.
 """
 import ctypes as C
 
@@ -79,3 +81,75 @@ def test_noalloc_design_refuses_oversized_request(gpu_ctx):
                                               out[2].ptr, None)
     assert st == _lib.INVALID_ARGUMENT
     assert "128 MiB" in lib.hkbs_last_error().decode()
+
+
+def _mem_free():
+    free, total = C.c_size_t(), C.c_size_t()
+    hip.check(hip.rt().hipMemGetInfo(C.byref(free), C.byref(total)), "hipMemGetInfo")
+    return free.value
+
+
+def test_noalloc_design_allocates_nothing_and_replays_in_a_graph(gpu_ctx):
+    lib = _lib.load()
+    rt = hip.rt()
+    bb = backbone.single_chain(120, 5)
+    L, B, T = bb.L, 8, 0.1
+    order = _lib.decode_order(bb.atom_sources, 5)
+    seeds = (5 + np.arange(B)).astype(np.uint64)
+    c, s, od, sd = _dev(bb.coords), _dev(bb.atom_sources), _dev(order), _dev(seeds)
+    outs = [hip.DeviceBuffer(B * L * 4), hip.DeviceBuffer(B * L * 21 * 4), hip.DeviceBuffer(B * 4)]
+
+    def call(stream):
+        return lib.hkbs_pmpnn_design_device_noalloc(gpu_ctx._h, c.ptr, s.ptr, None, None, None, None, L, B, od.ptr, 1,
+                                                    sd.ptr, C.c_float(T), 0, outs[0].ptr, outs[1].ptr, outs[2].ptr,
+                                                    stream)
+
+    def results():
+        return (_host(outs[0], (B, L), np.int32), _host(outs[1], (B, L, 21), np.float32),
+                _host(outs[2], (B,), np.float32))
+
+    def clear():
+        for o in outs:
+            hip.check(rt.hipMemset(o.ptr, 0xFF, C.c_size_t(o.nbytes)), "memset")
+
+    _say("noalloc design L=120 B=8 eager (reference bits; loads every kernel)")
+    _lib.check(call(None))
+    hip.device_synchronize()
+    want = results()
+    assert np.isfinite(want[2]).all()
+    _say("noalloc design: device free memory before and after a call")
+    free0 = _mem_free()
+    clear()
+    _lib.check(call(None))
+    hip.device_synchronize()
+    assert _mem_free() == free0
+    for g, w in zip(results(), want):
+        np.testing.assert_array_equal(g, w)
+
+    _say("noalloc design captured on a caller stream into a HIP graph")
+    st = hip.Stream()
+    graph, exe = C.c_void_p(), C.c_void_p()
+    hip.check(rt.hipStreamBeginCapture(st.h, C.c_int(0)), "hipStreamBeginCapture")  # hipStreamCaptureModeGlobal
+    rc = call(st.h)
+    end = rt.hipStreamEndCapture(st.h, C.byref(graph))
+    _lib.check(rc)
+    hip.check(end, "hipStreamEndCapture")
+    try:
+        hip.check(rt.hipGraphInstantiate(C.byref(exe), graph, None, None, C.c_size_t(0)), "hipGraphInstantiate")
+        other = backbone.single_chain(64, 9)
+        oseeds = np.array([3, 4], np.uint64)
+        for rep in range(3):
+            clear()
+            # the program's own eager work on the context's stream between replays
+            gpu_ctx.design(other.coords, other.atom_sources, 2, oseeds, order_seeds=oseeds, temperature=0.2)
+            _say(f"  graph replay {rep}")
+            hip.check(rt.hipGraphLaunch(exe, st.h), "hipGraphLaunch")
+            st.sync()
+            for g, w in zip(results(), want):
+                np.testing.assert_array_equal(g, w, err_msg=f"replay {rep}")
+    finally:
+        if exe:
+            rt.hipGraphExecDestroy(exe)
+        if graph:
+            rt.hipGraphDestroy(graph)
+        st.destroy()
