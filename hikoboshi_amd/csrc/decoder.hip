@@ -340,12 +340,26 @@ constexpr uint32_t kSpinLimit = 1u << 20;  // default polls (~1 s) before a team
 // before they arrived, wherever the members run on the device. team_wait
 // returns false (and raises the fault word) if the wait does not end; the
 // caller then stops so that every wave exits.
-__device__ inline void team_arrive(uint32_t* counter) {
+// With fences != 0 the barrier also carries the ordering of the HIP memory
+// model: an agent-scope release fence before the count's add and an
+// agent-scope acquire fence once the poll loop has seen the count (once per
+// barrier, not per poll), so that the stores made before a member's arrival
+// happen before the loads made after another member's wait. The relaxed form
+// (fences == 0) gives the same bits in every test and is the default: on
+// gfx950 those two fences write back and invalidate the XCD's L2
+// (buffer_wbl2 / buffer_inv), which costs about 3 us per barrier.
+// A team's members are dealt onto one XCD (round-robin dispatch) only for the
+// barrier's latency; neither form depends on it for its results.
+__device__ inline void team_arrive(uint32_t* counter, int fences) {
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
-  if (threadIdx.x == 0) __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  if (threadIdx.x == 0) {
+    if (fences) __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+    __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
 }
-__device__ inline bool team_wait(uint32_t* counter, uint32_t target, uint32_t spin_limit, uint32_t* fault, int* bad) {
+__device__ inline bool team_wait(uint32_t* counter, uint32_t target, uint32_t spin_limit, uint32_t* fault, int* bad,
+                                 int fences) {
   if (threadIdx.x == 0) {
     uint32_t n = 0;
     while (__hip_atomic_load(counter, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < target) {
@@ -356,6 +370,7 @@ __device__ inline bool team_wait(uint32_t* counter, uint32_t target, uint32_t sp
         break;
       }
     }
+    if (fences) __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
   }
   __syncthreads();
   return *bad == 0;
@@ -542,7 +557,7 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(ModelDev m, DecodeArgs
           }
         }
       }
-      if (P > 1) team_arrive(counter);
+      if (P > 1) team_arrive(counter, a.fences);
     }
   }
   // Inputs of a pass that no other workgroup writes come from its step
@@ -589,7 +604,7 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(ModelDev m, DecodeArgs
     rec_store(ml, rec_load(s0, ml));
   }
   if (P > 1 && pstart[1] > pstart[0]) {  // the pass-0 barrier
-    if (!team_wait(counter, ++passes * P, a.spin_limit, a.fault, &bad)) goto finish;
+    if (!team_wait(counter, ++passes * P, a.spin_limit, a.fault, &bad, a.fences)) goto finish;
   }
   __syncthreads();
   for (int pass = 1; pass <= npass; ++pass) {
@@ -1161,12 +1176,12 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(ModelDev m, DecodeArgs
     if (!staged) rv = rec_load(s0n, mln);
     // this pass's LDS state is consumed (team_arrive starts with a barrier)
     if (P > 1)
-      team_arrive(counter);
+      team_arrive(counter, a.fences);
     else
       __syncthreads();
     rec_store(mln, rv);
     ml = mln;
-    if (P > 1 && !team_wait(counter, ++passes * P, a.spin_limit, a.fault, &bad)) break;
+    if (P > 1 && !team_wait(counter, ++passes * P, a.spin_limit, a.fault, &bad, a.fences)) break;
     __syncthreads();
   }
 finish:
@@ -2069,6 +2084,10 @@ hipError_t launch_decode_as(const ModelDev& m, const DecodeArgs& args, hipStream
   if (a.max_members < 1 || a.max_members > kGroup * P) return hipErrorInvalidValue;  // the schedule assumed a larger team
   a.spin_limit = kSpinLimit;
   if (const char* env = std::getenv("HKBS_DECODE_SPIN_LIMIT")) a.spin_limit = (uint32_t)std::max(1, std::atoi(env));
+  {
+    const char* env = std::getenv("HKBS_DECODE_FENCES");
+    a.fences = env && std::strcmp(env, "1") == 0;
+  }
   if (P > 1) {
     a.team = P;
     const dim3 grid((unsigned)(8 * teams_per_xcd * P));

@@ -172,6 +172,7 @@ struct DecodeArgs {
   uint32_t* fault;        // [1] set when a team barrier times out, zero at launch
   int team;               // workgroups per sequence (set by launch_decode)
   uint32_t spin_limit;    // polls before a team barrier gives up (set by launch_decode)
+  int fences;             // team barrier with release/acquire fences (set by launch_decode, HKBS_DECODE_FENCES=1)
   int precision;          // 0 fp32, 1 bf16, 2 fp16, 3 split bf16 (see decode_kernel)
   int max_members;        // most steps one pass decodes (<= kDecodeGroup * team size)
   int pass_granule;       // team size the schedule balances passes for (<= 1: none)

@@ -331,7 +331,8 @@ def test_design_device_refuses_non_permutation_order(gpu_ctx):
 
 @pytest.mark.parametrize("B", [9, 64])
 def test_design_team_split_is_exact(gpu_ctx, oracle, B, monkeypatch):
-    """Several workgroups per sequence give the same bits as one workgroup per sequence."""
+    """Several workgroups per sequence give the same bits as one workgroup per sequence, with the team
+    barrier in either form (relaxed, or with release/acquire fences: HKBS_DECODE_FENCES=1)."""
     bb = backbone.single_chain(120, 4)
     src = bb.atom_sources.copy()
     src[[3, 60, 61], 0] = 0  # inactive residues take the one-residue path
@@ -341,12 +342,13 @@ def test_design_team_split_is_exact(gpu_ctx, oracle, B, monkeypatch):
     tt = (np.arange(120) * 5 % 20).astype(np.int32)
     seeds = (np.arange(B) + 31).astype(np.uint64)
     out = {}
-    for team in ("1", "2", "4"):
-        monkeypatch.setenv("HKBS_DECODE_TEAM", team)
+    for team in ("1", "2", "4", "4f"):
+        monkeypatch.setenv("HKBS_DECODE_TEAM", team[0])
+        monkeypatch.setenv("HKBS_DECODE_FENCES", "1" if team.endswith("f") else "0")  # 4f: fenced barrier
         _say(f"design team={team} B={B}")
         out[team] = gpu_ctx.design(bb.coords, bb.atom_sources, B, seeds, order_seeds=seeds, temperature=0.1,
                                    chain_mask=cm, true_tokens=tt)
-    for team in ("2", "4"):
+    for team in ("2", "4", "4f"):
         for key in ("tokens", "log_probs", "scores"):
             np.testing.assert_array_equal(out[team][key], out["1"][key], err_msg=f"team {team} {key}")
     check_design(oracle, bb, {k: v[:2] for k, v in out["4"].items()}, seeds[:2], 0.1, chain_mask=cm,
@@ -423,17 +425,19 @@ def test_design_layer0_table_is_exact(gpu_ctx, oracle, L, B, shared, monkeypatch
                  true_tokens=tt)
 
 
-def test_design_team_barrier_timeout_reruns(gpu_ctx, monkeypatch):
+@pytest.mark.parametrize("fences", ["0", "1"])
+def test_design_team_barrier_timeout_reruns(gpu_ctx, monkeypatch, fences):
     """A team barrier that gives up (forced here by a one-poll wait limit) leaves
     the kernel early with the fault word raised; the design call then decodes
     again with one workgroup per sequence and returns the same bits."""
     bb = backbone.single_chain(90, 6)
     seeds = (np.arange(5) + 3).astype(np.uint64)
+    monkeypatch.setenv("HKBS_DECODE_FENCES", fences)
     monkeypatch.setenv("HKBS_DECODE_TEAM", "1")
     ref = gpu_ctx.design(bb.coords, bb.atom_sources, 5, seeds, order_seeds=seeds, temperature=0.1)
     monkeypatch.setenv("HKBS_DECODE_TEAM", "4")
     monkeypatch.setenv("HKBS_DECODE_SPIN_LIMIT", "1")
-    _say("design with a one-poll team barrier")
+    _say(f"design with a one-poll team barrier (fences={fences})")
     out = gpu_ctx.design(bb.coords, bb.atom_sources, 5, seeds, order_seeds=seeds, temperature=0.1)
     for key in ("tokens", "log_probs", "scores"):
         np.testing.assert_array_equal(out[key], ref[key], err_msg=key)
