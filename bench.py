@@ -80,6 +80,9 @@ def parse_args():
     p.add_argument("--precision", choices=("fp32", "bf16", "bf16x3"), default="fp32",
                    help="design arithmetic of the headline workload (bf16: bf16 decoder; bf16x3: split bf16 "
                         "decoder, both operands of every product as two bf16 terms)")
+    p.add_argument("--complex", action="store_true",
+                   help="the main workload is the tetrahedral complex of 4 chains of --L residues (with --num-seqs "
+                        "256 --temperature 0.2 and --L 256: the 4 x 256 configuration)")
     p.add_argument("--workers", type=int, default=0, help="CPU worker processes (default: min(16, host CPUs))")
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baselines")
     p.add_argument("--no-configs", action="store_true", help="headline workload only")
@@ -106,9 +109,10 @@ def workloads(args):
         return orc.decode_order(bb.L, seed, residue_mask=valid)
 
     L, B = args.L, args.num_seqs
-    bb = backbone.single_chain(L, seed)
+    bb = backbone.tetrahedral_complex(L, seed) if args.complex else backbone.single_chain(L, seed)
     suffix = "" if args.precision == "fp32" else "_" + args.precision
-    W = {"C2": dict(name=f"design_L{L}_B{B}{suffix}", bb=bb, B=B, T=args.temperature, order=shared_order(bb),
+    name = f"complex_4x{L}_B{B}{suffix}" if args.complex else f"design_L{L}_B{B}{suffix}"
+    W = {"C2": dict(name=name, bb=bb, B=B, T=args.temperature, order=shared_order(bb),
                     seeds=(seed + np.arange(B)).astype(np.uint64), precision=args.precision,
                     cpu_seqs=list(range(min(B, 16))))}
     if not args.no_configs:
@@ -592,7 +596,9 @@ def main() -> int:
         "config": {
             "workload": w["name"],
             "L": L, "num_seqs": B, "k_neighbors": K, "temperature": T,
-            "backbone": f"NeRF ideal-geometry single chain, helix/strand segments, seed {args.seed}",
+            "backbone": (f"4 NeRF chains of {args.L} residues on a tetrahedron, 25 A apart, seed {args.seed}"
+                         if args.complex else
+                         f"NeRF ideal-geometry single chain, helix/strand segments, seed {args.seed}"),
             "decode_order": f"shared random permutation (reference routine, seed {args.seed})",
             "sampler_seeds": f"{args.seed}+b (splitmix64 counter streams)",
             "weights": "ProteinMPNN v_48_020 (bundled package)",

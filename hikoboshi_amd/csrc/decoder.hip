@@ -914,7 +914,7 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(ModelDev m, DecodeArgs
           // with the remainders of the latter) or fp16. The split bf16 mode holds
           // twice the fragments per k-block, so its products take more, smaller
           // parts, each loaded while the part before it runs.
-          constexpr int kNpIn = X3 ? 4 : 1, kNpOut = X3 ? 4 : 2, kNpDa = X3 ? 2 : 1;
+          constexpr int kNpIn = X3 ? 4 : 1, kNpOut = X3 ? 8 : 2, kNpDa = X3 ? 2 : 1;
           using M3 = MGemv<kH, kH, 1, PREC>;
           using MIn = MGemv<kH, kFF, kNpIn, PREC>;
           using MOut = MGemv<kFF, kH, kNpOut, PREC>;

@@ -131,7 +131,12 @@ hkbs_status hkbs_pmpnn_design(hkbs_pmpnn* ctx, const float* coords, const uint8_
  * work a team can fail to assemble, and then that sequence's score is NaN
  * (the synchronous hkbs_pmpnn_design detects this and decodes again with one
  * workgroup per sequence). HKBS_DECODE_TEAM=1 in the environment disables
- * teams. */
+ * teams. An order that is not a permutation of 0..L-1 is not decoded: that
+ * sequence's score is NaN and its tokens and log-probs are not written (the
+ * reference rejects such an order, cpp/modules/mpnn/decode_order_scalar.cpp:67-79;
+ * hkbs_pmpnn_design returns HKBS_INVALID_ARGUMENT for it). With a stream that
+ * is not being captured the call first waits for work pending on the context's
+ * own stream. */
 hkbs_status hkbs_pmpnn_design_device(hkbs_pmpnn* ctx, const float* coords,
                                      const uint8_t* atom_sources, const int32_t* residue_indices,
                                      const int32_t* chain_labels, const float* chain_mask,
@@ -156,7 +161,10 @@ hkbs_status hkbs_pmpnn_design_device(hkbs_pmpnn* ctx, const float* coords,
  * hkbs_pmpnn_design_device's with or without the table. Every call on one
  * GPU shares that GPU's array and leaves its contents behind (what must start
  * at zero is cleared by a kernel in the call): calls that overlap on one GPU,
- * from any context or stream, race and must be serialised by the caller. */
+ * from any context or stream, race and must be serialised by the caller. On a
+ * stream that is being captured into a HIP graph the call records its kernels
+ * (no memset nodes) without synchronising any stream; the caller then orders
+ * the graph after earlier calls on the context. */
 hkbs_status hkbs_pmpnn_design_device_noalloc(hkbs_pmpnn* ctx, const float* coords,
                                              const uint8_t* atom_sources,
                                              const int32_t* residue_indices,

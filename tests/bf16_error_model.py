@@ -139,6 +139,11 @@ def variants():
         "w_W2": bf16, "a_W2": bf16, "w_W3": bf16, "w_in": bf16, "w_out": bf16, "w_log": bf16}
     out["fp16 weights and activations of every product"] = {f"{k}_{p}": fp16 for p in PRODUCTS for k in "wa"}
     out["bf16 pairs (hi + lo) for every weight, exact activations"] = {f"w_{p}": bf16x2 for p in PRODUCTS}
+    # the split bf16 mode (HKBS_PRECISION_BF16X3): weights and inputs of every product as bf16 pairs
+    # (the logits' inputs stay fp32), then the same with the W1 inputs (the E1, Q and R rows) in fp16
+    split = {**{f"w_{p}": bf16x2 for p in PRODUCTS}, **{f"a_{p}": bf16x2 for p in PRODUCTS if p != "log"}}
+    out["split bf16: bf16 pairs for the weights and inputs of every product"] = split
+    out["split bf16 with fp16 message-row inputs (E1, Q, R)"] = {**split, "a_W1": fp16}
     return out
 
 

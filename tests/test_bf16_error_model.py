@@ -5,7 +5,8 @@ T = 1 within 1e-4 on the same backbone, order and tokens). Then, on an oracle
 design trajectory at T = 0.1: rounding any single group of decoder operands to
 bf16 (the weights or the inputs of one product) moves the log-probs by more
 than the 2e-2 that the long-chain bf16 configuration asks for, while weights
-carried as two bf16 terms (about 16 significant bits) stay far inside it.
+(and, as the split bf16 mode carries them, inputs too) carried as two bf16
+terms (about 16 significant bits) stay far inside it.
 """
 import numpy as np
 
@@ -34,3 +35,4 @@ def test_bf16_rounding_of_any_product_exceeds_the_bound():
     assert len(single) == 2 * len(bm.PRODUCTS)
     assert min(single.values()) > 2e-2, single
     assert dev["bf16 pairs (hi + lo) for every weight, exact activations"] < 2e-3
+    assert dev["split bf16: bf16 pairs for the weights and inputs of every product"] < 2e-3
