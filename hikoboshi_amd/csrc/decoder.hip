@@ -425,7 +425,7 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(ModelDev m, DecodeArgs
   // logits weights (32 outputs, 21 used) as fp32, [k / 4][v][k % 4]: lane v reads four k of its column at once
   __shared__ __attribute__((aligned(16))) float wlg[kH * 32];
   __shared__ __attribute__((aligned(16))) float prm[kPrmSize];
-  __shared__ __attribute__((aligned(16))) float gtab[kGeluPolyRows * 8];  // GELU polynomials
+  __shared__ __attribute__((aligned(16))) float gtab[kGeluPolyLds];  // GELU polynomials
   // neighbour words of the step records: -1 for an empty slot, else j | 2^30 if j is decoded before the step
   __shared__ __attribute__((aligned(16))) int nbw[kGroup * kKmax];
   __shared__ int cls[kGroup * kKmax];  // layer-0 table row of each slot (with a.l0tab)
@@ -486,7 +486,7 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(ModelDev m, DecodeArgs
   const uint64_t seed = a.seeds[b];
   const float T = (a.temperature > 0.0F && isfinite(a.temperature)) ? a.temperature : 1.0F;
   const bool greedy = a.greedy || a.temperature <= 0.0F;
-  for (int i = threadIdx.x; i < kGeluPolyRows * 8; i += kThreads) gtab[i] = kGeluPoly[i];
+  load_gelu_poly(gtab, threadIdx.x, kThreads);
   if (threadIdx.x == 0) bad = 0;
   for (int l = 0; l < kLayers; ++l) {
     const DecLayerDev& w = m.dec[l];
@@ -1266,7 +1266,7 @@ __global__ __launch_bounds__(kThreads, 4) void layer0_table_kernel(ModelDev m, c
   __shared__ __attribute__((aligned(16))) float qs[kTabSlots * kH];          // Q^0_j
   __shared__ __attribute__((aligned(16))) float ts[kV * kH];                 // T_0
   __shared__ __attribute__((aligned(16))) float hA[kH];
-  __shared__ __attribute__((aligned(16))) float gtab[kGeluPolyRows * 8];
+  __shared__ __attribute__((aligned(16))) float gtab[kGeluPolyLds];
   __shared__ int js[kTabSlots];
   __shared__ int srows[kKmax + 1];  // rows of each slot of t, then (thread 0) their running start
   __shared__ int16_t rslot[kTabSlots * kL0Classes], rcls[kTabSlots * kL0Classes];  // row -> (slot, state)
@@ -1275,7 +1275,7 @@ __global__ __launch_bounds__(kThreads, 4) void layer0_table_kernel(ModelDev m, c
   const int nk = min(kTabSlots, K - k0);
   if (t >= L || nk <= 0) return;
   const DecLayerDev& w = m.dec[0];
-  for (int i = threadIdx.x; i < kGeluPolyRows * 8; i += kThreads) gtab[i] = kGeluPoly[i];
+  load_gelu_poly(gtab, threadIdx.x, kThreads);
   for (int i = threadIdx.x; i < kH; i += kThreads) hA[i] = Q[((size_t)3 * L + t) * kH + i] + w.b1[i];
   if (threadIdx.x < nk) {
     const int jj = idx[(size_t)t * K + k0 + threadIdx.x];

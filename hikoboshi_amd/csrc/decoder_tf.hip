@@ -58,7 +58,7 @@ __global__ __launch_bounds__(256, 2) void tf_edge_kernel(DecLayerDev w, const fl
   __shared__ __attribute__((aligned(16))) _Float16 S[2 * kHalfSlab];
   float* A = reinterpret_cast<float*>(S);
   static_assert(kRows * kLd * sizeof(float) <= sizeof(S), "fp32 rows alias the slabs");
-  __shared__ __attribute__((aligned(16))) float gtab[kGeluPolyRows * 8];
+  __shared__ __attribute__((aligned(16))) float gtab[kGeluPolyLds];
   // per edge row, formed once: its residue t, and its neighbour j with the
   // backward flag (pos[j] < pos[t]) in bit 31, or -1 when the slot adds nothing
   __shared__ int row_t[kRows], row_j[kRows];
@@ -69,7 +69,7 @@ __global__ __launch_bounds__(256, 2) void tf_edge_kernel(DecLayerDev w, const fl
   const size_t slot0 = (size_t)r0 * K;
   const int wave = threadIdx.x >> 6;
   const int lane = threadIdx.x & 63, r = lane & 15, g = lane >> 4;
-  for (int i = threadIdx.x; i < kGeluPolyRows * 8; i += blockDim.x) gtab[i] = kGeluPoly[i];
+  load_gelu_poly(gtab, threadIdx.x, blockDim.x);
   if (threadIdx.x < n_rows) {
     const int row = threadIdx.x;
     const int t = r0 + row / K;

@@ -122,20 +122,30 @@ __device__ inline float gelu_fast(float x, const float* tbl) {
 // exp Taylor polynomial (gelu_poly_gen.py fits the table to the reference
 // expression, within 7.4e-8 absolute; the segments keep the reference's exp
 // table breakpoints, and row 17, v >= sqrt(15.5), is zero since the
-// reference's 1 - P rounds to 1 there). tab = the kGeluPolyRows x 8 table in
-// LDS (16-byte aligned). The tail keeps the reference's rounding of
+// reference's 1 - P rounds to 1 there). tab = the table in LDS as load_gelu_poly
+// lays it out (16-byte aligned). The tail keeps the reference's rounding of
 // mag = 1 - P and 0.5 x (1 + copysign(mag, x)). About 20 VALU slots against
 // the 31 of gelu_fast. Over all 2^32 inputs it is closer to the reference
 // expression than gelu_fast (5.1 against 7.5 units of ulp(result) + |x| 2^-25)
 // and equal to it on infinities and NaN.
+// LDS row stride of the table (floats): a lane reads the row of its own value,
+// and 12 floats (48 bytes) put the rows of up to 8-16 distinct segments on
+// distinct banks, where 8 floats let rows 4 or 8 apart share them.
+constexpr int kGeluPolyStride = 12;
+constexpr int kGeluPolyLds = kGeluPolyRows * kGeluPolyStride;  // floats of the LDS copy
+// Copies the table into LDS rows of kGeluPolyStride floats (tab: kGeluPolyLds floats,
+// 16-byte aligned); thread tid of n.
+__device__ inline void load_gelu_poly(float* tab, int tid, int n) {
+  for (int i = tid; i < kGeluPolyRows * 8; i += n) tab[(i / 8) * kGeluPolyStride + i % 8] = kGeluPoly[i];
+}
 __device__ inline float gelu_poly(float x, const float* tab) {
   // v > 4 takes row 17 (zero) as the reference's v > 4 case does; clamping v
   // rather than q keeps u finite for x = +-inf and NaN
   const float v = fminf(fabsf(x) * 0.7071067811865475F, 4.0F);
   const float q = v * v;
   const int row = static_cast<int>(q + 0.5F) + (v >= kGeluPolySplit ? 1 : 0);
-  const float4 c0 = *reinterpret_cast<const float4*>(tab + 8 * row);
-  const float4 c1 = *reinterpret_cast<const float4*>(tab + 8 * row + 4);
+  const float4 c0 = *reinterpret_cast<const float4*>(tab + kGeluPolyStride * row);
+  const float4 c1 = *reinterpret_cast<const float4*>(tab + kGeluPolyStride * row + 4);
   const float u = v - c0.x;
   float p = c1.w * u + c1.z;
   p = p * u + c1.y;

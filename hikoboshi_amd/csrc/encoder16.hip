@@ -283,7 +283,8 @@ __global__ __launch_bounds__(kTileThreads, 2) void edge_embed16_kernel(ModelDev 
   // neighbour j (n), their presence bits (q: bits 0-4, n: bits 8-12; bit 16:
   // j is a residue) and the positional class. Waves 0, 1 and 2 load the three
   // parts for the row of their lane.
-  __shared__ float xq[R][16], xn[R][16];
+  // 17 floats per row: lane = row reads one column of 64 rows, so an odd stride keeps them in distinct banks
+  __shared__ float xq[R][17], xn[R][17];
   __shared__ int info[R][2];
   __shared__ float tbl[17];
   if (threadIdx.x < 17) tbl[threadIdx.x] = kExpNegTable[threadIdx.x];
@@ -334,10 +335,20 @@ __global__ __launch_bounds__(kTileThreads, 2) void edge_embed16_kernel(ModelDev 
           rbf_chunk(&xq[row][3 * qa], &xn[row][3 * na], out, tbl);
         }
       }
+      // hi and lo halves 8 at a time (16-byte stores: 16 lanes, 16 rows 4 banks apart, fill all banks once)
 #pragma unroll
-      for (int q = 0; q < 4; ++q)
-        put_split4(S, R, kLdE, row, 16 * (c - c0) + 4 * q,
-                   make_float4(out[4 * q], out[4 * q + 1], out[4 * q + 2], out[4 * q + 3]));
+      for (int q = 0; q < 2; ++q) {
+        f16x8 h, l;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const float f = out[8 * q + e];
+          const _Float16 hi = static_cast<_Float16>(__builtin_amdgcn_fmed3f(f, -65504.0F, 65504.0F));
+          h[e] = hi;
+          l[e] = static_cast<_Float16>((f - static_cast<float>(hi)) * 2048.0F);
+        }
+        *reinterpret_cast<f16x8*>(S + row * kLdE + 16 * (c - c0) + 8 * q) = h;
+        *reinterpret_cast<f16x8*>(S + (R + row) * kLdE + 16 * (c - c0) + 8 * q) = l;
+      }
     }
     __syncthreads();
   };
@@ -381,11 +392,11 @@ __global__ __launch_bounds__(kTileThreads, 3) void edge_msg16_kernel(EncLayerDev
                                                                   float* __restrict__ upd) {
   constexpr int RB = 3;
   __shared__ __attribute__((aligned(16))) _Float16 S[2 * 16 * RB * kLdS2];
-  __shared__ __attribute__((aligned(16))) float gtab[kGeluPolyRows * 8];
+  __shared__ __attribute__((aligned(16))) float gtab[kGeluPolyLds];
   const int res = blockIdx.x;
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, r = lane & 15, g = lane >> 4;
   const int n0 = 32 * wave;
-  for (int i = threadIdx.x; i < kGeluPolyRows * 8; i += kTileThreads) gtab[i] = kGeluPoly[i];
+  load_gelu_poly(gtab, threadIdx.x, kTileThreads);
   tile_rows<RB>(S, h_v, h_e, idx, L, [&](int row) -> long long { return row < K ? (long long)res * K + row : -1; });
   // weight of slot 16 rb + r in the neighbour sum: mask_i mask_j / 30 for a valid slot
   float alpha[RB];
@@ -530,10 +541,10 @@ __global__ __launch_bounds__(kTileThreads, 2) void edge_update16_kernel(EncLayer
   constexpr int RB = 4;
   __shared__ __attribute__((aligned(16))) _Float16 S[2 * 16 * RB * kLdS2];
   __shared__ float stat[4][16 * RB];
-  __shared__ __attribute__((aligned(16))) float gtab[kGeluPolyRows * 8];
+  __shared__ __attribute__((aligned(16))) float gtab[kGeluPolyLds];
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, r = lane & 15, g = lane >> 4;
   const int n0 = 32 * wave;
-  for (int i = threadIdx.x; i < kGeluPolyRows * 8; i += kTileThreads) gtab[i] = kGeluPoly[i];
+  load_gelu_poly(gtab, threadIdx.x, kTileThreads);
   const long long S_ = (long long)L * K;
   const long long base = (long long)blockIdx.x * 16 * RB;
   tile_rows<RB>(S, h_v, h_e, idx, L, [&](int row) -> long long { return base + row < S_ ? base + row : -1; });

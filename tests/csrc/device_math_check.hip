@@ -101,9 +101,9 @@ __device__ inline float dev_units(float a, float b, float x) {
 // worst[2]: the input of worst[0].
 __global__ void check_kernel(unsigned long long* counts, unsigned int* first, unsigned int* worst) {
   __shared__ float tbl[17];
-  __shared__ __attribute__((aligned(16))) float gtab[hkbs::kGeluPolyRows * 8];
+  __shared__ __attribute__((aligned(16))) float gtab[hkbs::kGeluPolyLds];
   if (threadIdx.x < 17) tbl[threadIdx.x] = kExpNegTable[threadIdx.x];
-  for (int i = threadIdx.x; i < hkbs::kGeluPolyRows * 8; i += blockDim.x) gtab[i] = hkbs::kGeluPoly[i];
+  hkbs::load_gelu_poly(gtab, threadIdx.x, blockDim.x);
   __syncthreads();
   float w_poly = 0.0F, w_fast = 0.0F;
   unsigned int w_at = 0xFFFFFFFFu;
