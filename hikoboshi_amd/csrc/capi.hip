@@ -17,6 +17,7 @@
 #include <cstdlib>
 #include <cstring>
 #include <map>
+#include <type_traits>
 #include <numeric>
 #include <string>
 #include <vector>
@@ -464,6 +465,13 @@ struct hkbs_pmpnn {
   uint32_t* fault = nullptr;  // device word raised by the last decode if a team barrier timed out
   DecodeArgs last_decode{};   // arguments of the last decode launch (for a one-workgroup rerun)
   int precision = HKBS_PRECISION_FP32;
+  // Ragged scoring pipeline: chunk inputs go up on `side` and results come down on `down`, through two
+  // staging slots of pinned host memory; per slot, events for inputs uploaded, chunk computed and results
+  // copied down.
+  hipStream_t down = nullptr;
+  hipEvent_t score_ev[3][2] = {};
+  char* pinned = nullptr;
+  size_t pinned_cap = 0;
 };
 
 namespace {
@@ -747,8 +755,8 @@ struct EncodeBuffers {
 size_t encode_bytes(int L, int K) {
   const size_t S = (size_t)L * K;
   return aligned_bytes<float>(L) + aligned_bytes<float4>(L) + aligned_bytes<int32_t>(S) + aligned_bytes<float>(S) +
-         aligned_bytes<float>((size_t)L * kH) + aligned_bytes<float>(S * kH) + aligned_bytes<float>((size_t)L * 256) +
-         aligned_bytes<float>(S * kH) + aligned_bytes<float>((size_t)L * kH);
+         aligned_bytes<float>((size_t)L * kH) + aligned_bytes<float>(S * kH) + aligned_bytes<float>((size_t)L * kPrefix) +
+         aligned_bytes<float>(S * kH + L) + aligned_bytes<float>((size_t)L * kH);
 }
 
 EncodeBuffers take_encode(DeviceArena& ar, int L, int K) {
@@ -760,8 +768,8 @@ EncodeBuffers take_encode(DeviceArena& ar, int L, int K) {
   e.d2 = ar.take<float>(S);
   e.h_v = ar.take<float>((size_t)L * kH);
   e.h_e = ar.take<float>(S * kH);
-  e.scratch.prefix = ar.take<float>((size_t)L * 256);
-  e.scratch.msg = ar.take<float>(S * kH);
+  e.scratch.prefix = ar.take<float>((size_t)L * kPrefix);
+  e.scratch.msg = ar.take<float>(S * kH + L);
   e.msg_sum = ar.take<float>((size_t)L * kH);
   return e;
 }
@@ -1106,8 +1114,14 @@ void hkbs_pmpnn_destroy(hkbs_pmpnn* ctx) {
   (void)hipSetDevice(ctx->device);
   if (ctx->stream) (void)hipStreamSynchronize(ctx->stream);
   if (ctx->side) (void)hipStreamSynchronize(ctx->side);
+  if (ctx->down) (void)hipStreamSynchronize(ctx->down);
   for (hipEvent_t& ev : ctx->ev)
     if (ev) (void)hipEventDestroy(ev);
+  for (auto& evs : ctx->score_ev)
+    for (hipEvent_t& ev : evs)
+      if (ev) (void)hipEventDestroy(ev);
+  if (ctx->pinned) (void)hipHostFree(ctx->pinned);
+  if (ctx->down) (void)hipStreamDestroy(ctx->down);
   if (ctx->fork) (void)hipEventDestroy(ctx->fork);
   if (ctx->join) (void)hipEventDestroy(ctx->join);
   if (ctx->side) (void)hipStreamDestroy(ctx->side);
@@ -1496,49 +1510,132 @@ hkbs_status hkbs_pmpnn_score_batch(hkbs_pmpnn* ctx, int32_t n, const int64_t* of
     chunks.push_back({i, j, offsets[i], offsets[j], K});
     i = j;
   }
-  size_t need = 0;
+  // Two staging slots: chunk c uses slot c % 2 (pinned host buffers and device input / log-prob buffers),
+  // so that chunk c + 1's inputs go up while chunk c computes and chunk c's log-probs come down while
+  // chunk c + 1 computes. The encoder and decoder workspace after the slots is shared (one compute stream).
+  int maxL = 0, maxP = 0;
+  size_t work = 0;
   for (const Chunk& ch : chunks) {
     const int L = (int)(ch.r1 - ch.r0);
-    need = std::max(need, input_bytes(L) + tf_bytes(L, ch.K) + 2 * aligned_bytes<int32_t>(L) +
-                              aligned_bytes<int32_t>(L) + aligned_bytes<int64_t>(ch.last - ch.first + 1) +
-                              aligned_bytes<float>((size_t)L * kV));
+    maxL = std::max(maxL, L);
+    maxP = std::max(maxP, ch.last - ch.first);
+    work = std::max(work, tf_bytes(L, ch.K));
   }
+  const size_t Lm = (size_t)maxL;
+  const size_t slot_dev = aligned_bytes<float>(Lm * 15) + aligned_bytes<uint8_t>(Lm * 5) + 3 * aligned_bytes<int32_t>(Lm) +
+                          aligned_bytes<int64_t>((size_t)maxP + 1) + aligned_bytes<float>(Lm * kV);
   DeviceArena& ar = ctx->arena;
-  if (ar.reserve(need + (64u << 10)) != hipSuccess) return fail(HKBS_INTERNAL_ERROR, "device workspace allocation failed");
+  if (ar.reserve(2 * slot_dev + work + (64u << 10)) != hipSuccess)
+    return fail(HKBS_INTERNAL_ERROR, "device workspace allocation failed");
+  struct Slot {
+    float* coords;
+    uint8_t* src;
+    int32_t *tok, *pos, *seg;
+    int64_t* off;
+    float* lp;
+  };
+  auto take_slot = [&](auto&& take) {
+    Slot sl{};
+    sl.coords = take(sl.coords, Lm * 15);
+    sl.src = take(sl.src, Lm * 5);
+    sl.tok = take(sl.tok, Lm);
+    sl.pos = take(sl.pos, Lm);
+    sl.seg = take(sl.seg, Lm);
+    sl.off = take(sl.off, (size_t)maxP + 1);
+    sl.lp = take(sl.lp, Lm * kV);
+    return sl;
+  };
+  ar.reset();
+  Slot dev[2];
+  for (Slot& sl : dev) sl = take_slot([&](auto* p, size_t n) { return ar.take<std::remove_pointer_t<decltype(p)>>(n); });
+  const size_t mark = ar.used;
   hipStream_t s = ctx->stream;
-  std::vector<int32_t> seg;
-  std::vector<int64_t> loc;
-  for (const Chunk& ch : chunks) {
+  for (hipStream_t st2 : {s, ctx->side})
+    HK_CHECK(hipStreamSynchronize(st2), "an earlier call's kernels failed");
+  if (ctx->pinned_cap < 2 * slot_dev) {
+    if (ctx->pinned) (void)hipHostFree(ctx->pinned);
+    ctx->pinned = nullptr;
+    ctx->pinned_cap = 0;
+    if (hipHostMalloc(reinterpret_cast<void**>(&ctx->pinned), 2 * slot_dev, hipHostMallocDefault) != hipSuccess) {
+      (void)hipGetLastError();
+      ctx->pinned = nullptr;
+      return fail(HKBS_INTERNAL_ERROR, "pinned staging allocation failed");
+    }
+    ctx->pinned_cap = 2 * slot_dev;
+  }
+  if (!ctx->down && hipStreamCreateWithFlags(&ctx->down, hipStreamNonBlocking) != hipSuccess) {
+    ctx->down = nullptr;
+    return fail(HKBS_INTERNAL_ERROR, "HIP stream creation failed");
+  }
+  for (auto& evs : ctx->score_ev)
+    for (hipEvent_t& ev : evs)
+      if (!ev && hipEventCreateWithFlags(&ev, hipEventDisableTiming) != hipSuccess) {
+        ev = nullptr;
+        return fail(HKBS_INTERNAL_ERROR, "HIP event creation failed");
+      }
+  Slot pin[2];
+  {
+    size_t at = 0;
+    for (Slot& sl : pin)
+      sl = take_slot([&](auto* p, size_t n) {
+        auto* q = reinterpret_cast<decltype(p)>(ctx->pinned + at);
+        at += aligned_bytes<std::remove_pointer_t<decltype(p)>>(n);
+        return q;
+      });
+  }
+  hipEvent_t* uploaded = ctx->score_ev[0];
+  hipEvent_t* computed = ctx->score_ev[1];
+  hipEvent_t* copied = ctx->score_ev[2];
+  // chunk c's log-probs from its slot's pinned buffer to the caller's (its copy has been waited for)
+  auto deliver = [&](int c) {
+    const Chunk& ch = chunks[c];
+    std::memcpy(log_probs + ch.r0 * kV, pin[c & 1].lp, (size_t)(ch.r1 - ch.r0) * kV * sizeof(float));
+  };
+  const int nch = static_cast<int>(chunks.size());
+  for (int c = 0; c < nch; ++c) {
+    const Chunk& ch = chunks[c];
     const int L = (int)(ch.r1 - ch.r0);
     const int np = ch.last - ch.first;
-    // The arena and the host staging vectors are reused per chunk: finish the
-    // previous chunk's kernels and copies (which read seg and loc) first.
-    HK_CHECK(hipStreamSynchronize(s), "teacher-forced kernels failed");
-    seg.resize(L);
-    loc.resize(np + 1);
-    for (int p = 0; p < np; ++p) {
-      loc[p] = offsets[ch.first + p] - ch.r0;
-      for (int64_t r = offsets[ch.first + p]; r < offsets[ch.first + p + 1]; ++r) seg[r - ch.r0] = p;
+    const int k = c & 1;
+    Slot& hp = pin[k];
+    Slot& dp = dev[k];
+    if (c >= 2) {
+      // chunk c - 2 (same slot): its results are down, so its pinned and device buffers are free
+      HK_CHECK(hipEventSynchronize(copied[k]), "teacher-forced kernels failed");
+      deliver(c - 2);
     }
-    loc[np] = L;
-    ar.reset();
-    Inputs in{};
-    if ((st = upload_inputs(ctx, ar, coords + ch.r0 * 15, atom_sources + ch.r0 * 5, nullptr, nullptr, nullptr, nullptr, L,
-                            in)) != HKBS_OK)
+    std::memcpy(hp.coords, coords + ch.r0 * 15, (size_t)L * 15 * sizeof(float));
+    std::memcpy(hp.src, atom_sources + ch.r0 * 5, (size_t)L * 5);
+    std::memcpy(hp.tok, tokens + ch.r0, (size_t)L * 4);
+    std::memcpy(hp.pos, pos.data() + ch.r0, (size_t)L * 4);
+    for (int p = 0; p < np; ++p) {
+      hp.off[p] = offsets[ch.first + p] - ch.r0;
+      for (int64_t r = offsets[ch.first + p]; r < offsets[ch.first + p + 1]; ++r) hp.seg[r - ch.r0] = p;
+    }
+    hp.off[np] = L;
+    hipStream_t up = ctx->side;
+    HK_CHECK(hipMemcpyAsync(dp.coords, hp.coords, (size_t)L * 15 * sizeof(float), hipMemcpyHostToDevice, up), "H2D failed");
+    HK_CHECK(hipMemcpyAsync(dp.src, hp.src, (size_t)L * 5, hipMemcpyHostToDevice, up), "H2D failed");
+    HK_CHECK(hipMemcpyAsync(dp.tok, hp.tok, (size_t)L * 4, hipMemcpyHostToDevice, up), "H2D failed");
+    HK_CHECK(hipMemcpyAsync(dp.pos, hp.pos, (size_t)L * 4, hipMemcpyHostToDevice, up), "H2D failed");
+    HK_CHECK(hipMemcpyAsync(dp.seg, hp.seg, (size_t)L * 4, hipMemcpyHostToDevice, up), "H2D failed");
+    HK_CHECK(hipMemcpyAsync(dp.off, hp.off, (size_t)(np + 1) * 8, hipMemcpyHostToDevice, up), "H2D failed");
+    HK_CHECK(hipEventRecord(uploaded[k], up), "event record failed");
+    HK_CHECK(hipStreamWaitEvent(s, uploaded[k], 0), "stream wait failed");
+    ar.used = mark;
+    if ((st = teacher_forced_chunk(ctx, dp.coords, dp.src, nullptr, nullptr, dp.tok, dp.pos, L, ch.K, dp.seg, dp.off,
+                                   dp.lp, ar)) != HKBS_OK)
       return st;
-    int32_t* d_tok = ar.take<int32_t>(L);
-    int32_t* d_pos = ar.take<int32_t>(L);
-    int32_t* d_seg = ar.take<int32_t>(L);
-    int64_t* d_off = ar.take<int64_t>(np + 1);
-    float* d_lp = ar.take<float>((size_t)L * kV);
-    HK_CHECK(hipMemcpyAsync(d_tok, tokens + ch.r0, (size_t)L * 4, hipMemcpyHostToDevice, s), "H2D failed");
-    HK_CHECK(hipMemcpyAsync(d_pos, pos.data() + ch.r0, (size_t)L * 4, hipMemcpyHostToDevice, s), "H2D failed");
-    HK_CHECK(hipMemcpyAsync(d_seg, seg.data(), (size_t)L * 4, hipMemcpyHostToDevice, s), "H2D failed");
-    HK_CHECK(hipMemcpyAsync(d_off, loc.data(), (size_t)(np + 1) * 8, hipMemcpyHostToDevice, s), "H2D failed");
-    if ((st = teacher_forced_chunk(ctx, in.coords, in.src, nullptr, nullptr, d_tok, d_pos, L, ch.K, d_seg, d_off, d_lp,
-                                   ar)) != HKBS_OK)
-      return st;
-    HK_CHECK(hipMemcpyAsync(log_probs + ch.r0 * kV, d_lp, (size_t)L * kV * 4, hipMemcpyDeviceToHost, s), "D2H failed");
+    HK_CHECK(hipEventRecord(computed[k], s), "event record failed");
+    HK_CHECK(hipStreamWaitEvent(ctx->down, computed[k], 0), "stream wait failed");
+    HK_CHECK(hipMemcpyAsync(hp.lp, dp.lp, (size_t)L * kV * sizeof(float), hipMemcpyDeviceToHost, ctx->down), "D2H failed");
+    HK_CHECK(hipEventRecord(copied[k], ctx->down), "event record failed");
+    // The next upload into this slot's device inputs (chunk c + 2) comes after this chunk's results are down,
+    // which follow its kernels, so the kernels have read the inputs by then.
+  }
+  for (int c = std::max(0, nch - 2); c < nch; ++c) {
+    HK_CHECK(hipEventSynchronize(copied[c & 1]), "teacher-forced kernels failed");
+    deliver(c);
   }
   HK_CHECK(hipStreamSynchronize(s), "teacher-forced kernels failed");
   if (scores) {

@@ -27,7 +27,7 @@
 namespace hkbs {
 namespace {
 
-constexpr int kRows = 96;
+constexpr int kRows = 48;
 constexpr int kLd = kH + 4;
 constexpr int kLdF = kFF + 4;
 
@@ -42,26 +42,23 @@ __global__ void tf_init_kernel(ModelDev m, const float* __restrict__ Q, const in
   NB[r * 256 + kH + c] = Q[r * kH + c] + m.dec[0].T[tokens[r] * kH + c];
 }
 
-// Edge rows of a tile as split fp16 operands: two half-tiles of 48 rows, each
-// hi [48][kLdS1] then lo [48][kLdS1] (the layout of tile_gemm).
-constexpr int kHalfRows = kRows / 2;
-constexpr int kHalfRB = kHalfRows / 16;
-constexpr int kHalfSlab = 2 * kHalfRows * kLdS1;  // halves
+// One tile of kRows edge rows per workgroup: the K slots of kRows / K
+// consecutive residues (one residue when K = 48), their h_E rows split into
+// fp16 halves in LDS (hi [kRows][kLdS1] then lo, the layout of tile_gemm).
+constexpr int kRB = kRows / 16;
+static_assert(kRows % 16 == 0 && kRows >= kKmax, "a tile holds whole residues");
 
-__global__ __launch_bounds__(256, 2) void tf_edge_kernel(DecLayerDev w, const float* __restrict__ h_e,
+__global__ __launch_bounds__(256, 4) void tf_edge_kernel(DecLayerDev w, const float* __restrict__ h_e,
                                                       const int32_t* __restrict__ idx, const int32_t* __restrict__ pos,
                                                       const float* __restrict__ mask, const float* __restrict__ NB,
                                                       const float* __restrict__ Ql, int L, int K,
                                                       float* __restrict__ msg_sum) {
-  // The two half-tile slabs; once the W2 product has read them, the same bytes
-  // hold the fp32 message rows [kRows][kLd] for the neighbour sums.
-  __shared__ __attribute__((aligned(16))) _Float16 S[2 * kHalfSlab];
+  // The split h_E slab; once the W2 product has read it, the same bytes hold
+  // the fp32 message rows [kRows][kLd] for the neighbour sums (K < 48).
+  __shared__ __attribute__((aligned(16))) _Float16 S[2 * kRows * kLdS1];
   float* A = reinterpret_cast<float*>(S);
-  static_assert(kRows * kLd * sizeof(float) <= sizeof(S), "fp32 rows alias the slabs");
+  static_assert(kRows * kLd * sizeof(float) <= sizeof(S), "fp32 rows alias the slab");
   __shared__ __attribute__((aligned(16))) float gtab[kGeluPolyLds];
-  // per edge row, formed once: its residue t, and its neighbour j with the
-  // backward flag (pos[j] < pos[t]) in bit 31, or -1 when the slot adds nothing
-  __shared__ int row_t[kRows], row_j[kRows];
   const int nres = kRows / K;
   const int r0 = blockIdx.x * nres;
   const int nr = min(nres, L - r0);
@@ -69,99 +66,102 @@ __global__ __launch_bounds__(256, 2) void tf_edge_kernel(DecLayerDev w, const fl
   const size_t slot0 = (size_t)r0 * K;
   const int wave = threadIdx.x >> 6;
   const int lane = threadIdx.x & 63, r = lane & 15, g = lane >> 4;
+  const int n0 = 32 * wave;
   load_gelu_poly(gtab, threadIdx.x, blockDim.x);
-  if (threadIdx.x < n_rows) {
-    const int row = threadIdx.x;
-    const int t = r0 + row / K;
-    const int j = idx[slot0 + row];
-    row_t[row] = t;
-    row_j[row] = (j >= 0 && j < L && mask[t] != 0.0F) ? (j | (pos[j] < pos[t] ? (int)0x80000000u : 0)) : -1;
-  }
   {
-    // the tile's h_E rows, split: thread (wave w, lane c) loads float4 column c % 32 of rows
-    // 2 w + c / 32 + 8 i, all loads issued before the first store
+    // the tile's h_E rows, split: thread t loads float4 column t % 32 of rows t / 32 + 8 i, all loads
+    // issued before the first store
     constexpr int N = kRows * (kH / 4) / 256;
+    const int col = 4 * (threadIdx.x & 31), row0 = threadIdx.x >> 5;
     float4 v[N];
 #pragma unroll
     for (int i = 0; i < N; ++i) {
-      const int row = 2 * wave + (lane >> 5) + 8 * i;
-      v[i] = row < n_rows ? *reinterpret_cast<const float4*>(h_e + (slot0 + row) * kH + 4 * (lane & 31))
+      const int row = row0 + 8 * i;
+      v[i] = row < n_rows ? *reinterpret_cast<const float4*>(h_e + (slot0 + row) * kH + col)
                           : make_float4(0.F, 0.F, 0.F, 0.F);
     }
 #pragma unroll
-    for (int i = 0; i < N; ++i) {
-      const int row = 2 * wave + (lane >> 5) + 8 * i;
-      put_split4(S + (row / kHalfRows) * kHalfSlab, kHalfRows, kLdS1, row % kHalfRows, 4 * (lane & 31), v[i]);
+    for (int i = 0; i < N; ++i) put_split4(S, kRows, kLdS1, row0 + 8 * i, col, v[i]);
+  }
+  // Row 16 rb + r: its residue t and whether the slot adds a context (j a residue, t not masked). Then
+  // x = A_t + (bw ? R_j : Q_j) + E1 with E1 = W1b h_E for a slot that adds one, else x = A_t: the
+  // accumulators start at A_t + (R_j or Q_j) and the W1b product adds E1.
+  int row_t[kRB];
+  bool adds[kRB];
+  floatx4 acc[kRB][2];
+#pragma unroll
+  for (int rb = 0; rb < kRB; ++rb) {
+    const int row = 16 * rb + r;
+    const bool valid = row < n_rows;
+    const int t = r0 + (valid ? row / K : 0);
+    const int j = valid ? idx[slot0 + row] : -1;
+    adds[rb] = valid && j >= 0 && j < L && mask[t] != 0.0F;
+    const bool bw = adds[rb] && pos[j] < pos[t];
+    row_t[rb] = valid ? t : -1;
+#pragma unroll
+    for (int nt = 0; nt < 2; ++nt) {
+      const int c0 = n0 + 16 * nt + 4 * g;
+      const float4 x = valid ? *reinterpret_cast<const float4*>(NB + (size_t)t * 256 + c0) : make_float4(0.F, 0.F, 0.F, 0.F);
+      const float4 e = !adds[rb] ? make_float4(0.F, 0.F, 0.F, 0.F)
+                                 : *reinterpret_cast<const float4*>(bw ? NB + (size_t)j * 256 + kH + c0
+                                                                       : Ql + (size_t)j * kH + c0);
+      acc[rb][nt] = floatx4{x.x + e.x, x.y + e.y, x.z + e.z, x.w + e.w};
     }
   }
   __syncthreads();
-  // Per half-tile: x = A_t + (E1 + (bw ? R_j : Q_j)) for a slot that adds something, else A_t, with
-  // E1 = W1b h_E; GELU(x) replaces the half's h_E rows. The A and R|Q rows load before the E1 product.
-#pragma unroll 1
-  for (int hf = 0; hf < 2; ++hf) {
-    _Float16* Sh = S + hf * kHalfSlab;
-    float4 base[kHalfRB][2], nbr[kHalfRB][2];
+  tile_gemm<kRB, kH, 3>(S, kLdS1, w.W1b_s, n0, (size_t)kH * kH, acc, true);
+  __syncthreads();  // every wave is done with the h_E rows
 #pragma unroll
-    for (int mb = 0; mb < kHalfRB; ++mb) {
-      const int row = hf * kHalfRows + mb * 16 + r;
-      const int t = row < n_rows ? row_t[row] : 0;
-      const int jb = row < n_rows ? row_j[row] : -1;
-      const int j = jb & 0x7FFFFFFF;
+  for (int rb = 0; rb < kRB; ++rb) {
 #pragma unroll
-      for (int nb = 0; nb < 2; ++nb) {
-        const int c0 = wave * 32 + nb * 16 + 4 * g;
-        base[mb][nb] = row < n_rows ? *reinterpret_cast<const float4*>(NB + (size_t)t * 256 + c0)
-                                    : make_float4(0.F, 0.F, 0.F, 0.F);
-        nbr[mb][nb] = jb == -1 ? make_float4(0.F, 0.F, 0.F, 0.F)
-                               : *reinterpret_cast<const float4*>(jb < 0 ? NB + (size_t)j * 256 + kH + c0
-                                                                         : Ql + (size_t)j * kH + c0);
+    for (int nt = 0; nt < 2; ++nt) {
+      const int c0 = n0 + 16 * nt + 4 * g;
+      floatx4 x = acc[rb][nt];
+      if (!adds[rb]) {  // A_t alone (zero for a row past the tile's residues)
+        const float4 a = row_t[rb] >= 0 ? *reinterpret_cast<const float4*>(NB + (size_t)row_t[rb] * 256 + c0)
+                                        : make_float4(0.F, 0.F, 0.F, 0.F);
+        x = floatx4{a.x, a.y, a.z, a.w};
       }
-    }
-    floatx4 acc[kHalfRB][2];
-    tile_gemm<kHalfRB, kH>(Sh, kLdS1, w.W1b_s, wave * 32, (size_t)kH * kH, acc);
-    __syncthreads();  // every wave is done with this half's h_E rows
-#pragma unroll
-    for (int mb = 0; mb < kHalfRB; ++mb) {
-      const int row = hf * kHalfRows + mb * 16 + r;
-      const bool adds = row < n_rows && row_j[row] != -1;
-#pragma unroll
-      for (int nb = 0; nb < 2; ++nb) {
-        const int c0 = wave * 32 + nb * 16 + 4 * g;
-        float4 o = make_float4(0.F, 0.F, 0.F, 0.F);
-        if (row < n_rows) {
-          const float4 x = base[mb][nb], e = nbr[mb][nb];
-          const floatx4 y = acc[mb][nb];
-          o = adds ? make_float4(gelu_poly(x.x + (y[0] + e.x), gtab), gelu_poly(x.y + (y[1] + e.y), gtab),
-                                 gelu_poly(x.z + (y[2] + e.z), gtab), gelu_poly(x.w + (y[3] + e.w), gtab))
-                   : make_float4(gelu_poly(x.x, gtab), gelu_poly(x.y, gtab), gelu_poly(x.z, gtab),
-                                 gelu_poly(x.w, gtab));
-        }
-        put_split4(Sh, kHalfRows, kLdS1, mb * 16 + r, c0, o);
-      }
+      const float4 o = row_t[rb] >= 0 ? make_float4(gelu_poly(x[0], gtab), gelu_poly(x[1], gtab),
+                                                    gelu_poly(x[2], gtab), gelu_poly(x[3], gtab))
+                                      : make_float4(0.F, 0.F, 0.F, 0.F);
+      put_split4(S, kRows, kLdS1, 16 * rb + r, c0, o);
     }
   }
   __syncthreads();
-  floatx4 acc2[2][kHalfRB][2];
+  tile_gemm<kRB, kH, 3>(S, kLdS1, reinterpret_cast<const uint16_t*>(w.W2h), n0, (size_t)kH * kH, acc);
+  // g = GELU(W2 x + b2) per valid row; msg_sum[t] = the sum over the residue's K slots
+  if (nres == 1) {
 #pragma unroll
-  for (int hf = 0; hf < 2; ++hf)
-    tile_gemm<kHalfRB, kH>(S + hf * kHalfSlab, kLdS1, reinterpret_cast<const uint16_t*>(w.W2h), wave * 32,
-                           (size_t)kH * kH, acc2[hf]);
-  __syncthreads();  // the slabs are consumed; A reuses their bytes
+    for (int nt = 0; nt < 2; ++nt) {
+      const int c0 = n0 + 16 * nt + 4 * g;
+      const float4 bv = *reinterpret_cast<const float4*>(w.b2 + c0);
+      float sv[4];
 #pragma unroll
-  for (int nb = 0; nb < 2; ++nb) {
-    const int c0 = wave * 32 + nb * 16 + 4 * g;
+      for (int i = 0; i < 4; ++i) {
+        const float b = i == 0 ? bv.x : i == 1 ? bv.y : i == 2 ? bv.z : bv.w;
+        float v = 0.0F;
+#pragma unroll
+        for (int rb = 0; rb < kRB; ++rb) v += row_t[rb] >= 0 ? gelu_poly(acc[rb][nt][i] + b, gtab) : 0.0F;
+        sv[i] = sum16(v);
+      }
+      if (r == 0) *reinterpret_cast<float4*>(msg_sum + (size_t)r0 * kH + c0) = make_float4(sv[0], sv[1], sv[2], sv[3]);
+    }
+    return;
+  }
+  __syncthreads();  // the slab is consumed; A reuses its bytes
+#pragma unroll
+  for (int nt = 0; nt < 2; ++nt) {
+    const int c0 = n0 + 16 * nt + 4 * g;
     const float4 bv = *reinterpret_cast<const float4*>(w.b2 + c0);
 #pragma unroll
-    for (int hf = 0; hf < 2; ++hf)
-#pragma unroll
-      for (int mb = 0; mb < kHalfRB; ++mb) {
-        const int row = hf * kHalfRows + mb * 16 + r;
-        const floatx4 y = acc2[hf][mb][nb];
-        *reinterpret_cast<float4*>(A + row * kLd + c0) =
-            row < n_rows ? make_float4(gelu_poly(y[0] + bv.x, gtab), gelu_poly(y[1] + bv.y, gtab),
+    for (int rb = 0; rb < kRB; ++rb) {
+      const floatx4 y = acc[rb][nt];
+      *reinterpret_cast<float4*>(A + (16 * rb + r) * kLd + c0) =
+          row_t[rb] >= 0 ? make_float4(gelu_poly(y[0] + bv.x, gtab), gelu_poly(y[1] + bv.y, gtab),
                                        gelu_poly(y[2] + bv.z, gtab), gelu_poly(y[3] + bv.w, gtab))
                          : make_float4(0.F, 0.F, 0.F, 0.F);
-      }
+    }
   }
   __syncthreads();
   for (int task = threadIdx.x; task < nr * kH; task += blockDim.x) {

@@ -1,6 +1,7 @@
 // Edge features of one 16-feature chunk of an edge slot, shared by the
 // fp32 and the 16-bit edge embeddings (features.hip, encoder16.hip). The
-// float operations follow the reference order with contraction disabled.
+// float operations of rbf_chunk follow the reference order with contraction
+// disabled; rbf_chunk_fma is the 16-bit encoder's shorter form.
 #pragma once
 
 #include "device_math.hpp"
@@ -53,6 +54,45 @@ __device__ inline void rbf_chunk(const float* qx, const float* nx, float* out, c
     const float center = 2.0F + static_cast<float>(f) * center_step;
     const float delta = dist - center;
     out[f] = fast_exp_neg(-(delta * delta) / two_sigma_sq, tbl);
+  }
+}
+
+// The 16 RBF features of rbf_chunk in fewer operations, for the 16-bit
+// encoder (fp32-accurate, not the reference's rounding sequence): the same
+// distance, centres, width and exp form (table value times the degree-6
+// Taylor series of exp(r), |r| <= 1/2), with fused multiply-adds, a multiplication by
+// 1 / (2 sigma^2) in place of the division, and no checks for inputs that
+// cannot occur (the argument is never NaN or positive). A feature differs
+// from rbf_chunk's by a few float ulps, or, where t lies within rounding of a
+// half-integer and the two take neighbouring table entries, by up to the
+// difference of the Taylor remainders at r = +1/2 and -1/2 (3.4e-6 of the
+// value).
+__device__ inline void rbf_chunk_fma(const float* qx, const float* nx, float* out, const float* tbl) {
+#pragma clang fp contract(off)
+  float sq = 0.0F;  // the distance as rbf_chunk rounds it: the far features are sensitive to its last bits
+#pragma unroll
+  for (int ax = 0; ax < 3; ++ax) {
+    const float delta = nx[ax] - qx[ax];
+    sq += delta * delta;
+  }
+  const float dist = sqrtf(sq + 1.0e-6F);
+  const float center_step = (22.0F - 2.0F) / static_cast<float>(kRbf - 1);
+  const float sigma = (22.0F - 2.0F) / (static_cast<float>(kRbf) / 0.7071067811865475F);
+  const float inv_two_sigma_sq = 1.0F / (2.0F * sigma * sigma);
+#pragma unroll
+  for (int f = 0; f < 16; ++f) {
+    const float center = 2.0F + static_cast<float>(f) * center_step;
+    const float delta = dist - center;
+    const float t = delta * delta * inv_two_sigma_sq;  // exp(-t), t >= 0
+    const int n = static_cast<int>(fminf(t, 16.0F) + 0.5F);  // nearest integer, at most 16
+    const float r = static_cast<float>(n) - t;
+    float e = __builtin_fmaf(r, 1.0F / 720.0F, 1.0F / 120.0F);
+    e = __builtin_fmaf(r, e, 1.0F / 24.0F);
+    e = __builtin_fmaf(r, e, 1.0F / 6.0F);
+    e = __builtin_fmaf(r, e, 0.5F);
+    e = __builtin_fmaf(r, e, 1.0F);
+    e = __builtin_fmaf(r, e, 1.0F);
+    out[f] = t > 16.0F ? 0.0F : tbl[n] * e;
   }
 }
 

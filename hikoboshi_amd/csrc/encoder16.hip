@@ -18,25 +18,26 @@
 // blocks. The edge embedding and the node kernel keep 16 rows per wave with
 // the fp32 operand split as it is read (wave_gemm).
 //
-// The h_i block of W1 [h_i | e_ij | h_j] (and of W11) is the same for all K
-// slots of residue i, so node16 computes it once per residue into a prefix
-// buffer [L][256] (W11 part for this layer's edge update, W1 part for the
-// next layer's messages; zero for layer 0, where h = 0) and the edge kernels
-// run K = 256 over [e_ij | h_j], starting from the prefix.
+// W1 [h_i | e_ij | h_j] x (and W11) is W1a h_i + W1b e_ij + W1c h_j: node16
+// forms the W1a and W1c products of every residue once per layer into four
+// planes [L][128] (W11 h_i and W11 h_j for this layer's edge update, W1 h_i
+// and W1 h_j for the next layer's messages; zero for layer 0, where h = 0),
+// and the edge kernels run the K = 128 product over e_ij, starting from
+// P[i] + P[j] (no h_j block for an empty slot).
 //
 // Kernels:
-//   edge_embed16   32 edge slots per workgroup (2 waves): 416 features ->
+//   edge_embed16   64 edge slots per workgroup (4 waves): 416 features ->
 //                  W_edge -> LN -> W_e -> h_E.
 //   per layer:
-//   edge_msg16     one residue per workgroup (48 slots, 4 waves):
-//                  prefix + W1 [e_ij | h_j], GELU, W2, GELU, W3 -> the masked
-//                  sum over the residue's slots / 30 -> upd[i].
-//   node16         16 residues per workgroup (4 waves, a quarter of the FFN
-//                  each): LN1(h + upd), the FFN on the MFMA, LN2, mask; then
-//                  the W11 and next-layer W1 prefixes of the new h.
-//   edge_update16  64 edge slots per workgroup (4 waves): prefix + W11
-//                  [e_ij | h_j], GELU, W12, GELU, W13, residual, LN3 -> h_E
-//                  (valid slots).
+//   edge_msg16     one residue per workgroup (48 slots, 4 waves): W1 e_ij +
+//                  P, GELU, W2, GELU -> the sum over the residue's slots
+//                  weighted by mask_i mask_j / 30, and the sum of the weights.
+//   node16         16 residues per workgroup (4 waves): upd = W3 sum + (sum of
+//                  weights) b3, LN1(h + upd), the FFN on the MFMA (a quarter
+//                  of it per wave), LN2, mask; then the four W1 / W11 blocks
+//                  of the new h.
+//   edge_update16  64 edge slots per workgroup (4 waves): W11 e_ij + P, GELU,
+//                  W12, GELU, W13, residual, LN3 -> h_E (valid slots).
 #include "device_math.hpp"
 #include "edge_chunk.hpp"
 #include "mfma_tile.hpp"
@@ -128,59 +129,53 @@ __device__ inline void store_gelu(const floatx4 (&acc)[NT], const float* __restr
   }
 }
 
-// Sum over the 16 lanes that hold one row (lanes 16 g .. 16 g + 15).
-__device__ inline float sum16(float v) {
-  v += __shfl_xor(v, 1, 64);
-  v += __shfl_xor(v, 2, 64);
-  v += __shfl_xor(v, 4, 64);
-  v += __shfl_xor(v, 8, 64);
-  return v;
-}
-
-// The tile's rows [e_ij | h_j] (slot = slot_of(row); negative: a zero row;
-// j = idx[slot] outside [0, L): a zero h_j block) into the split slab. Thread
-// (wave w, lane c) fills float4 column c of rows w, w + 4, ...; all of its
-// index loads, then all of its row loads, are issued before the first use.
+// The tile's h_E rows (slot = slot_of(row); negative: a zero row) into the
+// split slab (K = 128). Thread t fills float4 column t % 32 of rows t / 32,
+// t / 32 + 8, ...; all of its row loads are issued before the first store.
 template <int RB, typename SlotOf>
-__device__ inline void tile_rows(_Float16* S, const float* __restrict__ h_v, const float* __restrict__ h_e,
-                                 const int32_t* __restrict__ idx, int L, SlotOf slot_of) {
-  constexpr int R = 16 * RB, N = R * 64 / kTileThreads;
-  const int c4 = threadIdx.x & 63, part = c4 >> 5, col = 4 * (c4 & 31), row0 = threadIdx.x >> 6;
-  long long src[N];
-#pragma unroll
-  for (int i = 0; i < N; ++i) src[i] = slot_of(row0 + 4 * i);
-  if (part) {
-#pragma unroll
-    for (int i = 0; i < N; ++i) {
-      const int j = src[i] >= 0 ? idx[src[i]] : -1;
-      src[i] = (j >= 0 && j < L) ? j : -1;
-    }
-  }
-  const float* base = part ? h_v : h_e;
+__device__ inline void tile_rows(_Float16* S, const float* __restrict__ h_e, SlotOf slot_of) {
+  constexpr int R = 16 * RB, N = R * 32 / kTileThreads;
+  const int col = 4 * (threadIdx.x & 31), row0 = threadIdx.x >> 5;
   float4 v[N];
 #pragma unroll
-  for (int i = 0; i < N; ++i)
-    v[i] = src[i] >= 0 ? *reinterpret_cast<const float4*>(base + (size_t)src[i] * kH + col)
-                       : make_float4(0.F, 0.F, 0.F, 0.F);
+  for (int i = 0; i < N; ++i) {
+    const long long slot = slot_of(row0 + 8 * i);
+    v[i] = slot >= 0 ? *reinterpret_cast<const float4*>(h_e + (size_t)slot * kH + col) : make_float4(0.F, 0.F, 0.F, 0.F);
+  }
 #pragma unroll
-  for (int i = 0; i < N; ++i) put_split4(S, R, kLdS2, row0 + 4 * i, part * kH + col, v[i]);
+  for (int i = 0; i < N; ++i) put_split4(S, R, kLdS1, row0 + 8 * i, col, v[i]);
 }
 
-// GELU(acc + add + bias) of the wave's columns into the split slab (K = 128
-// operand of the next product); add[rb] is a per-row base (the h_i prefix).
+// Starting value of the first product of an edge row of residue i with
+// neighbour j: P[pi][i][c] + P[pj][j][c] + b[c] for columns c0 .. c0 + 3 (P:
+// planes of [L][128] floats holding the W1 h_i and h_j blocks of
+// [h_i | e_ij | h_j], formed per residue by node16); an empty slot (j outside
+// [0, L)) has no h_j term.
+__device__ inline floatx4 edge_base(const float* __restrict__ P, size_t i, int j, int L, int pi, int pj,
+                                    const float* __restrict__ b, int c0) {
+  float4 a = *reinterpret_cast<const float4*>(P + ((size_t)pi * L + i) * kH + c0);
+  if (j >= 0 && j < L) {
+    const float4 q = *reinterpret_cast<const float4*>(P + ((size_t)pj * L + j) * kH + c0);
+    a = make_float4(a.x + q.x, a.y + q.y, a.z + q.z, a.w + q.w);
+  }
+  const float4 bv = *reinterpret_cast<const float4*>(b + c0);
+  return floatx4{a.x + bv.x, a.y + bv.y, a.z + bv.z, a.w + bv.w};
+}
+
+// GELU(acc + bias) of the wave's columns into the split slab (K = 128 operand
+// of the next product); no bias when bias is null.
 template <int RB>
-__device__ inline void tile_store_gelu(const floatx4 (&acc)[RB][2], const float* __restrict__ bias,
-                                       const float4 (&add)[RB][2], _Float16* S, const float* gtab) {
+__device__ inline void tile_store_gelu(const floatx4 (&acc)[RB][2], const float* __restrict__ bias, _Float16* S,
+                                       const float* gtab) {
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, r = lane & 15, g = lane >> 4;
 #pragma unroll
   for (int nt = 0; nt < 2; ++nt) {
     const int c0 = 32 * wave + 16 * nt + 4 * g;
-    const float4 bv = *reinterpret_cast<const float4*>(bias + c0);
+    const float4 bv = bias ? *reinterpret_cast<const float4*>(bias + c0) : make_float4(0.F, 0.F, 0.F, 0.F);
 #pragma unroll
     for (int rb = 0; rb < RB; ++rb) {
-      const float4 a = add[rb][nt];
-      const float4 v = make_float4(gelu_poly(acc[rb][nt][0] + a.x + bv.x, gtab), gelu_poly(acc[rb][nt][1] + a.y + bv.y, gtab),
-                                   gelu_poly(acc[rb][nt][2] + a.z + bv.z, gtab), gelu_poly(acc[rb][nt][3] + a.w + bv.w, gtab));
+      const float4 v = make_float4(gelu_poly(acc[rb][nt][0] + bv.x, gtab), gelu_poly(acc[rb][nt][1] + bv.y, gtab),
+                                   gelu_poly(acc[rb][nt][2] + bv.z, gtab), gelu_poly(acc[rb][nt][3] + bv.w, gtab));
       put_split4(S, 16 * RB, kLdS1, 16 * rb + r, c0, v);
     }
   }
@@ -332,7 +327,7 @@ __global__ __launch_bounds__(kTileThreads, 2) void edge_embed16_kernel(ModelDev 
 #pragma unroll
           for (int f = 0; f < 16; ++f) out[f] = 0.0F;
         } else {
-          rbf_chunk(&xq[row][3 * qa], &xn[row][3 * na], out, tbl);
+          rbf_chunk_fma(&xq[row][3 * qa], &xn[row][3 * na], out, tbl);
         }
       }
       // hi and lo halves 8 at a time (16-byte stores: 16 lanes, 16 rows 4 banks apart, fill all banks once)
@@ -382,78 +377,76 @@ __global__ __launch_bounds__(kTileThreads, 2) void edge_embed16_kernel(ModelDev 
   }
 }
 
-// One residue per workgroup: its 48 slots as one tile of 3 row blocks.
-__global__ __launch_bounds__(kTileThreads, 3) void edge_msg16_kernel(EncLayerDev w, Enc16LayerDev w16,
+// One residue per workgroup: its 48 slots as one tile of 3 row blocks. The
+// message of slot k is m_k = W3 g_k + b3 with g_k = GELU(W2 GELU(W1 x_k + b1) +
+// b2), and upd_i = sum_k alpha_k m_k = W3 (sum_k alpha_k g_k) + (sum_k alpha_k)
+// b3, so this kernel stops at s_i = sum_k alpha_k g_k and a_i = sum_k alpha_k
+// (gsum[i][0 .. 127] and gsum[128 L + i]); node16 applies W3 to 16 residues
+// at a time.
+__global__ __launch_bounds__(kTileThreads, 4) void edge_msg16_kernel(EncLayerDev w, Enc16LayerDev w16,
                                                                   const float* __restrict__ h_e,
-                                                                  const float* __restrict__ h_v,
                                                                   const int32_t* __restrict__ idx,
                                                                   const float* __restrict__ mask,
                                                                   const float* __restrict__ prefix, int L, int K,
-                                                                  float* __restrict__ upd) {
+                                                                  float* __restrict__ gsum) {
   constexpr int RB = 3;
-  __shared__ __attribute__((aligned(16))) _Float16 S[2 * 16 * RB * kLdS2];
+  __shared__ __attribute__((aligned(16))) _Float16 S[2 * 16 * RB * kLdS1];
   __shared__ __attribute__((aligned(16))) float gtab[kGeluPolyLds];
   const int res = blockIdx.x;
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, r = lane & 15, g = lane >> 4;
   const int n0 = 32 * wave;
   load_gelu_poly(gtab, threadIdx.x, kTileThreads);
-  tile_rows<RB>(S, h_v, h_e, idx, L, [&](int row) -> long long { return row < K ? (long long)res * K + row : -1; });
+  tile_rows<RB>(S, h_e, [&](int row) -> long long { return row < K ? (long long)res * K + row : -1; });
   // weight of slot 16 rb + r in the neighbour sum: mask_i mask_j / 30 for a valid slot
   float alpha[RB];
+  floatx4 acc[RB][2];
 #pragma unroll
   for (int rb = 0; rb < RB; ++rb) {
     const int k = 16 * rb + r;
     const int j = k < K ? idx[(size_t)res * K + k] : -1;
     alpha[rb] = (j >= 0 && j < L) ? mask[res] * mask[j] * (1.0F / 30.0F) : 0.0F;
-  }
-  float4 add[RB][2];
 #pragma unroll
-  for (int nt = 0; nt < 2; ++nt) {
-    const float4 pv = *reinterpret_cast<const float4*>(prefix + (size_t)res * 256 + kH + n0 + 16 * nt + 4 * g);
-#pragma unroll
-    for (int rb = 0; rb < RB; ++rb) add[rb][nt] = pv;
+    for (int nt = 0; nt < 2; ++nt) acc[rb][nt] = edge_base(prefix, res, j, L, 2, 3, w.b1, n0 + 16 * nt + 4 * g);
   }
   __syncthreads();
-  floatx4 acc[RB][2];
-  // rows 128 .. 383 of W1 (packed k-blocks 16 ..) over [e_ij | h_j], plus the h_i prefix
-  tile_gemm<RB, 2 * kH>(S, kLdS2, w16.W1 + (size_t)16 * kH * 8, n0, (size_t)3 * kH * kH, acc);
-  __syncthreads();  // every wave is done with [e_ij | h_j]
-  tile_store_gelu<RB>(acc, w.b1, add, S, gtab);
+  // rows 128 .. 255 of W1 (packed k-blocks 16 .. 31) over e_ij, added to the h_i, h_j blocks and b1
+  tile_gemm<RB, kH, 3>(S, kLdS1, w16.W1 + (size_t)16 * kH * 8, n0, (size_t)3 * kH * kH, acc, true);
+  __syncthreads();  // every wave is done with e_ij
+  tile_store_gelu<RB>(acc, nullptr, S, gtab);
   __syncthreads();
-  tile_gemm<RB, kH>(S, kLdS1, w16.W2, n0, (size_t)kH * kH, acc);
-#pragma unroll
-  for (int nt = 0; nt < 2; ++nt)
-#pragma unroll
-    for (int rb = 0; rb < RB; ++rb) add[rb][nt] = make_float4(0.F, 0.F, 0.F, 0.F);
-  __syncthreads();
-  tile_store_gelu<RB>(acc, w.b2, add, S, gtab);
-  __syncthreads();
-  tile_gemm<RB, kH>(S, kLdS1, w16.W3, n0, (size_t)kH * kH, acc);
-  // upd[col] = sum over the residue's valid slots of (mask_i mask_j / 30) (W3 g + b3)
+  tile_gemm<RB, kH, 3>(S, kLdS1, w16.W2, n0, (size_t)kH * kH, acc);
 #pragma unroll
   for (int nt = 0; nt < 2; ++nt) {
     const int c0 = n0 + 16 * nt + 4 * g;
-    const float4 bv = *reinterpret_cast<const float4*>(w.b3 + c0);
+    const float4 bv = *reinterpret_cast<const float4*>(w.b2 + c0);
     float sv[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const float b = i == 0 ? bv.x : i == 1 ? bv.y : i == 2 ? bv.z : bv.w;
       float v = 0.0F;
 #pragma unroll
-      for (int rb = 0; rb < RB; ++rb) v += alpha[rb] * (acc[rb][nt][i] + b);
+      for (int rb = 0; rb < RB; ++rb) v += alpha[rb] * gelu_poly(acc[rb][nt][i] + b, gtab);
       sv[i] = sum16(v);
     }
-    if (r == 0) *reinterpret_cast<float4*>(upd + (size_t)res * kH + c0) = make_float4(sv[0], sv[1], sv[2], sv[3]);
+    if (r == 0) *reinterpret_cast<float4*>(gsum + (size_t)res * kH + c0) = make_float4(sv[0], sv[1], sv[2], sv[3]);
+  }
+  if (wave == 0) {
+    float a = 0.0F;
+#pragma unroll
+    for (int rb = 0; rb < RB; ++rb) a += alpha[rb];
+    a = sum16(a);
+    if (lane == 0) gsum[(size_t)L * kH + res] = a;
   }
 }
 
 // 16 residues per workgroup of four waves; lane (r, g) of a wave holds rows
 // 4 g + i, columns 16 nt + r of a 128-wide block (the MFMA output layout).
-// Wave 0 forms h1 = LN1(h + upd) for all 16 rows; wave w computes the FFN
-// hidden columns [128 w, 128 w + 128) and the W_out partial sum over those
-// inputs; wave 0 adds the four partials in order, the residual, LN2 and the
-// mask.
-__global__ __launch_bounds__(256) void node16_kernel(EncLayerDev w, Enc16LayerDev w16, const float* __restrict__ upd,
+// Wave w first forms columns [32 w, 32 w + 32) of the neighbour update
+// upd = W3 s + a b3 from edge_msg16's sums; wave 0 forms h1 = LN1(h + upd)
+// for all 16 rows; wave w computes the FFN hidden columns [128 w, 128 w + 128)
+// and the W_out partial sum over those inputs; wave 0 adds the four partials
+// in order, the residual, LN2 and the mask.
+__global__ __launch_bounds__(256) void node16_kernel(EncLayerDev w, Enc16LayerDev w16, const float* __restrict__ gsum,
                                                      const float* __restrict__ mask, int L, float* __restrict__ h_v,
                                                      const uint16_t* __restrict__ W1_next, float* __restrict__ prefix) {
   __shared__ __attribute__((aligned(16))) float A[16 * kLdH];
@@ -463,6 +456,31 @@ __global__ __launch_bounds__(256) void node16_kernel(EncLayerDev w, Enc16LayerDe
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, r = lane & 15, g = lane >> 4;
   const int r0 = blockIdx.x * 16;
   if (threadIdx.x < 17) tbl[threadIdx.x] = kExpNegTable[threadIdx.x];
+  // the 16 rows of s into A (float4 column t % 32 of rows t / 32 and t / 32 + 8)
+#pragma unroll
+  for (int q = 0; q < 2; ++q) {
+    const int row = (threadIdx.x >> 5) + 8 * q, c = 4 * (threadIdx.x & 31);
+    const int res = r0 + row;
+    *reinterpret_cast<float4*>(A + row * kLdH + c) =
+        res < L ? *reinterpret_cast<const float4*>(gsum + (size_t)res * kH + c) : make_float4(0.F, 0.F, 0.F, 0.F);
+  }
+  __syncthreads();
+  {
+    floatx4 u[2];
+    wave_gemm<2>(A, kLdH, w16.W3, kH, 32 * wave, kH, u);
+#pragma unroll
+    for (int nt = 0; nt < 2; ++nt) {
+      const int col = 32 * wave + 16 * nt + r;
+      const float bv = w.b3[col];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int res = r0 + 4 * g + i;
+        const float a = res < L ? gsum[(size_t)L * kH + res] : 0.0F;
+        Pt[0][(4 * g + i) * kLdH + col] = u[nt][i] + a * bv;
+      }
+    }
+  }
+  __syncthreads();
   floatx4 x[8];
   if (wave == 0) {
 #pragma unroll
@@ -470,11 +488,11 @@ __global__ __launch_bounds__(256) void node16_kernel(EncLayerDev w, Enc16LayerDe
       const int res = r0 + 4 * g + i;
 #pragma unroll
       for (int nt = 0; nt < 8; ++nt) {
-        const size_t at = (size_t)res * kH + 16 * nt + r;
-        x[nt][i] = res < L ? h_v[at] + upd[at] : 0.0F;
+        const int col = 16 * nt + r;
+        x[nt][i] = res < L ? h_v[(size_t)res * kH + col] + Pt[0][(4 * g + i) * kLdH + col] : 0.0F;
       }
     }
-    ln_acc(x, w.n1g, w.n1b);
+  ln_acc(x, w.n1g, w.n1b);
 #pragma unroll
     for (int nt = 0; nt < 8; ++nt)
 #pragma unroll
@@ -517,29 +535,29 @@ __global__ __launch_bounds__(256) void node16_kernel(EncLayerDev w, Enc16LayerDe
   }
   }
   __syncthreads();
-  // prefixes of the new h: wave 0 the h_i rows of this layer's W11, wave 1
-  // those of the next layer's W1 (packed k-blocks 0 .. 15 of the K = 384
-  // matrices; lo 384 x 128 halves after hi)
-  if (wave >= 2 || (wave == 1 && !W1_next)) return;
+  // products of the new h into the planes [W11 h_i | W11 h_j | next W1 h_i | next W1 h_j] of prefix
+  // ([4][L][128]): wave w takes plane w (packed k-blocks 0 .. 15 for the h_i rows, 32 .. 47 for the h_j rows of the K = 384 matrices;
+  // lo 384 x 128 halves after hi)
+  if (wave >= 2 && !W1_next) return;
   floatx4 pacc[8];
-  wave_gemm<8>(A, kLdH, wave == 0 ? w16.W11 : W1_next, kH, 0, kH, pacc, (size_t)3 * kH * kH);
+  wave_gemm<8>(A, kLdH, (wave < 2 ? w16.W11 : W1_next) + (size_t)(wave & 1) * 32 * kH * 8, kH, 0, kH, pacc,
+               (size_t)3 * kH * kH);
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const int res = r0 + 4 * g + i;
     if (res >= L) continue;
 #pragma unroll
-    for (int nt = 0; nt < 8; ++nt) prefix[(size_t)res * 256 + kH * wave + 16 * nt + r] = pacc[nt][i];
+    for (int nt = 0; nt < 8; ++nt) prefix[((size_t)wave * L + res) * kH + 16 * nt + r] = pacc[nt][i];
   }
 }
 
 // 64 consecutive edge slots per workgroup: one tile of 4 row blocks.
-__global__ __launch_bounds__(kTileThreads, 2) void edge_update16_kernel(EncLayerDev w, Enc16LayerDev w16,
+__global__ __launch_bounds__(kTileThreads, 3) void edge_update16_kernel(EncLayerDev w, Enc16LayerDev w16,
                                                                      float* __restrict__ h_e,
-                                                                     const float* __restrict__ h_v,
                                                                      const int32_t* __restrict__ idx,
                                                                      const float* __restrict__ prefix, int L, int K) {
   constexpr int RB = 4;
-  __shared__ __attribute__((aligned(16))) _Float16 S[2 * 16 * RB * kLdS2];
+  __shared__ __attribute__((aligned(16))) _Float16 S[2 * 16 * RB * kLdS1];
   __shared__ float stat[4][16 * RB];
   __shared__ __attribute__((aligned(16))) float gtab[kGeluPolyLds];
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, r = lane & 15, g = lane >> 4;
@@ -547,51 +565,41 @@ __global__ __launch_bounds__(kTileThreads, 2) void edge_update16_kernel(EncLayer
   load_gelu_poly(gtab, threadIdx.x, kTileThreads);
   const long long S_ = (long long)L * K;
   const long long base = (long long)blockIdx.x * 16 * RB;
-  tile_rows<RB>(S, h_v, h_e, idx, L, [&](int row) -> long long { return base + row < S_ ? base + row : -1; });
-  float4 add[RB][2];
+  tile_rows<RB>(S, h_e, [&](int row) -> long long { return base + row < S_ ? base + row : -1; });
+  floatx4 acc[RB][2];
 #pragma unroll
   for (int rb = 0; rb < RB; ++rb) {
     const long long slot = base + 16 * rb + r;
     const size_t res = slot < S_ ? (size_t)(slot / K) : 0;
+    const int j = slot < S_ ? idx[slot] : -1;
 #pragma unroll
-    for (int nt = 0; nt < 2; ++nt)
-      add[rb][nt] = *reinterpret_cast<const float4*>(prefix + res * 256 + n0 + 16 * nt + 4 * g);
+    for (int nt = 0; nt < 2; ++nt) acc[rb][nt] = edge_base(prefix, res, j, L, 0, 1, w.b11, n0 + 16 * nt + 4 * g);
   }
   __syncthreads();
-  floatx4 acc[RB][2];
-  tile_gemm<RB, 2 * kH>(S, kLdS2, w16.W11 + (size_t)16 * kH * 8, n0, (size_t)3 * kH * kH, acc);
+  // rows 128 .. 255 of W11 (packed k-blocks 16 .. 31) over e_ij, added to the h_i, h_j blocks and b11
+  tile_gemm<RB, kH, 3>(S, kLdS1, w16.W11 + (size_t)16 * kH * 8, n0, (size_t)3 * kH * kH, acc, true);
   __syncthreads();
-  tile_store_gelu<RB>(acc, w.b11, add, S, gtab);
+  tile_store_gelu<RB>(acc, nullptr, S, gtab);
   __syncthreads();
-  tile_gemm<RB, kH>(S, kLdS1, w16.W12, n0, (size_t)kH * kH, acc);
-  // the residual e rows load during the last two products
-#pragma unroll
-  for (int rb = 0; rb < RB; ++rb) {
-    const long long slot = base + 16 * rb + r;
-#pragma unroll
-    for (int nt = 0; nt < 2; ++nt)
-      add[rb][nt] = slot < S_ ? *reinterpret_cast<const float4*>(h_e + (size_t)slot * kH + n0 + 16 * nt + 4 * g)
-                              : make_float4(0.F, 0.F, 0.F, 0.F);
-  }
-  const float4 zero[RB][2] = {};
+  tile_gemm<RB, kH, 3>(S, kLdS1, w16.W12, n0, (size_t)kH * kH, acc);
   __syncthreads();
-  tile_store_gelu<RB>(acc, w.b12, zero, S, gtab);
-  __syncthreads();
-  tile_gemm<RB, kH>(S, kLdS1, w16.W13, n0, (size_t)kH * kH, acc);
-  // x = e + (W13 g + b13), then LN3 over each row's 128 columns (four waves)
+  tile_store_gelu<RB>(acc, w.b12, S, gtab);
+  // x = (e + b13) + W13 g: the residual rows start the last product's accumulators
 #pragma unroll
   for (int nt = 0; nt < 2; ++nt) {
     const int c0 = n0 + 16 * nt + 4 * g;
     const float4 bv = *reinterpret_cast<const float4*>(w.b13 + c0);
 #pragma unroll
     for (int rb = 0; rb < RB; ++rb) {
-      const float4 e = add[rb][nt];
-      acc[rb][nt][0] = e.x + (acc[rb][nt][0] + bv.x);
-      acc[rb][nt][1] = e.y + (acc[rb][nt][1] + bv.y);
-      acc[rb][nt][2] = e.z + (acc[rb][nt][2] + bv.z);
-      acc[rb][nt][3] = e.w + (acc[rb][nt][3] + bv.w);
+      const long long slot = base + 16 * rb + r;
+      const float4 e = slot < S_ ? *reinterpret_cast<const float4*>(h_e + (size_t)slot * kH + c0)
+                                 : make_float4(0.F, 0.F, 0.F, 0.F);
+      acc[rb][nt] = floatx4{e.x + bv.x, e.y + bv.y, e.z + bv.z, e.w + bv.w};
     }
   }
+  __syncthreads();
+  tile_gemm<RB, kH, 3>(S, kLdS1, w16.W13, n0, (size_t)kH * kH, acc, true);
+  // LN3 over each row's 128 columns (four waves)
   tile_layer_norm<RB>(acc, w.n3g, w.n3b, stat);
 #pragma unroll
   for (int rb = 0; rb < RB; ++rb) {
@@ -620,17 +628,19 @@ hipError_t launch_encoder16(const ModelDev& m, const float* coords, const uint8_
   hipError_t e = launch_zero(h_v, (size_t)L * kH, stream);
   if (e != hipSuccess) return e;
   edge_embed16_kernel<<<tiles64, kTileThreads, 0, stream>>>(m, coords, atom_src, resid, chain, idx, L, K, h_e);
-  e = launch_zero(ws.prefix, (size_t)L * 256, stream);  // layer 0: h = 0, so its W1 prefix is 0
+  e = launch_zero(ws.prefix, (size_t)L * kPrefix, stream);  // layer 0: h = 0, so its W1 blocks are 0
   if (e != hipSuccess) return e;
-  float* upd = ws.msg;  // [L][128] neighbour sums (the [S][128] message buffer is otherwise unused here)
+  // [L][128] weighted GELU sums and [L] weight sums of edge_msg16 (the [S][128] + L message buffer is
+  // otherwise unused here)
+  float* gsum = ws.msg;
   for (int l = 0; l < kLayers; ++l) {
     const Enc16LayerDev& w16 = m.enc16.layer[l];
     const uint16_t* W1_next = l + 1 < kLayers ? m.enc16.layer[l + 1].W1 : nullptr;
-    edge_msg16_kernel<<<(unsigned)L, kTileThreads, 0, stream>>>(m.enc[l], w16, h_e, h_v, idx, mask, ws.prefix, L, K,
-                                                                 upd);
-    node16_kernel<<<(unsigned)((L + 15) / 16), 256, 0, stream>>>(m.enc[l], w16, upd, mask, L, h_v, W1_next,
+    edge_msg16_kernel<<<(unsigned)L, kTileThreads, 0, stream>>>(m.enc[l], w16, h_e, idx, mask, ws.prefix, L, K,
+                                                                 gsum);
+    node16_kernel<<<(unsigned)((L + 15) / 16), 256, 0, stream>>>(m.enc[l], w16, gsum, mask, L, h_v, W1_next,
                                                                 ws.prefix);
-    edge_update16_kernel<<<tiles64, kTileThreads, 0, stream>>>(m.enc[l], w16, h_e, h_v, idx, ws.prefix, L, K);
+    edge_update16_kernel<<<tiles64, kTileThreads, 0, stream>>>(m.enc[l], w16, h_e, idx, ws.prefix, L, K);
   }
   return hipGetLastError();
 }

@@ -19,6 +19,16 @@ __device__ inline floatx4 mfma_f16(f16x8 a, f16x8 b, floatx4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
 }
 
+// Sum over the 16 lanes 16 g .. 16 g + 15 of a wave (a row of a wave_gemm
+// output, or a column block of a tile_gemm output summed over its rows).
+__device__ inline float sum16(float v) {
+  v += __shfl_xor(v, 1, 64);
+  v += __shfl_xor(v, 2, 64);
+  v += __shfl_xor(v, 4, 64);
+  v += __shfl_xor(v, 8, 64);
+  return v;
+}
+
 // ------------------------------------------------------------ edge tiles ----
 // A tile holds 16 RB edge rows. Its operands live in LDS split into fp16
 // halves, hi [rows][ld] then lo [rows][ld] (v = hi + lo / 2048); a row stride
@@ -28,7 +38,6 @@ __device__ inline floatx4 mfma_f16(f16x8 a, f16x8 b, floatx4 c) {
 // transposed (weights as the MFMA's A operand, rows as its B operand): lane
 // (r, g) then holds row 16 rb + r, columns 32 w + 16 nt + 4 g + (0..3).
 constexpr int kTileThreads = 256;
-constexpr int kLdS2 = 2 * kH + 8;  // halves per row of a K = 256 operand ([e_ij | h_j])
 constexpr int kLdS1 = kH + 8;      // halves per row of a K = 128 operand
 
 // Four consecutive floats into the split slab at (row, col).

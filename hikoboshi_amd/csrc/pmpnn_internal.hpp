@@ -114,9 +114,12 @@ hipError_t launch_edge_features(const ModelDev& m, const float* coords, const ui
 hipError_t launch_edge_embed(const ModelDev& m, const float* coords, const uint8_t* atom_src,
                              const int32_t* resid, const int32_t* chain, const int32_t* idx, int L,
                              int K, float* h_e, hipStream_t stream);
+// Floats per residue of EncoderScratch::prefix.
+constexpr int kPrefix = 4 * kH;
 struct EncoderScratch {
-  float* prefix;   // [L][256]: sequential partial sums over the h_i inputs of [W11 | next W1]
-  float* msg;      // [L * K][128] edge messages of the current layer
+  float* prefix;   // L x kPrefix floats, per-residue products of h (fp32 encoder: [L][256], the [W11 | next W1]
+                   // h_i blocks; 16-bit encoder: planes [4][L][128], W11 h_i, W11 h_j, next W1 h_i, next W1 h_j)
+  float* msg;      // [L * K][128] edge messages of the current layer, plus L floats
 };
 // Fills n floats with zero (a kernel, so it can sit inside a captured graph).
 hipError_t launch_zero(float* p, size_t n, hipStream_t stream);

@@ -23,6 +23,7 @@
 #include <cstdint>
 
 #include "../../hikoboshi_amd/csrc/device_math.hpp"
+#include "../../hikoboshi_amd/csrc/edge_chunk.hpp"
 
 namespace {
 
@@ -167,5 +168,57 @@ extern "C" int hkbs_check_device_gelu(unsigned long long* counts_out, unsigned i
   if (counts) (void)hipFree(counts);
   if (first) (void)hipFree(first);
   if (worst) (void)hipFree(worst);
+  return static_cast<int>(e);
+}
+
+namespace {
+
+// rbf_chunk_fma (16-bit encoder) against rbf_chunk (the reference's operation
+// order) for n atom-pair offsets: offset i has length 30 i / n Angstrom along
+// a direction that turns with i. out[0] = the largest |fma - ref| / ref over
+// features with ref >= 1e-30 (float bits), out[1] = the largest |fma - ref|
+// (float bits), out[2] = the number of features where exactly one of the two
+// is zero (the exp(-16) cut-off).
+__global__ void rbf_kernel(unsigned int n, unsigned int* out) {
+  __shared__ float tbl[17];
+  if (threadIdx.x < 17) tbl[threadIdx.x] = kExpNegTable[threadIdx.x];
+  __syncthreads();
+  float w_rel = 0.0F, w_abs = 0.0F;
+  unsigned int cut = 0;
+  for (unsigned int i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x) {
+    const float len = 30.0F * static_cast<float>(i) / static_cast<float>(n);
+    const float a = 0.6180339F * static_cast<float>(i % 4096), b = 0.4142135F * static_cast<float>(i % 2048);
+    const float q[3] = {1.25F, -3.5F, 7.0F};
+    const float nx[3] = {q[0] + len * cosf(a) * sinf(b), q[1] + len * sinf(a) * sinf(b), q[2] + len * cosf(b)};
+    float ref[16], fma[16];
+    hkbs::rbf_chunk(q, nx, ref, tbl);
+    hkbs::rbf_chunk_fma(q, nx, fma, tbl);
+#pragma unroll
+    for (int f = 0; f < 16; ++f) {
+      const float d = fabsf(fma[f] - ref[f]);
+      w_abs = fmaxf(w_abs, d != d ? 3.0e38F : d);
+      if ((ref[f] == 0.0F) != (fma[f] == 0.0F)) ++cut;
+      else if (ref[f] >= 1.0e-30F) w_rel = fmaxf(w_rel, d / ref[f]);
+    }
+  }
+  atomicMax(&out[0], __float_as_uint(w_rel));
+  atomicMax(&out[1], __float_as_uint(w_abs));
+  atomicAdd(&out[2], cut);
+}
+
+}  // namespace
+
+// Runs rbf_kernel over n offsets on the current device; out[3] as there.
+extern "C" int hkbs_check_device_rbf(unsigned int n, unsigned int* out_host) {
+  unsigned int* out = nullptr;
+  hipError_t e = hipMalloc(&out, 3 * sizeof(unsigned int));
+  if (e == hipSuccess) e = hipMemset(out, 0, 3 * sizeof(unsigned int));
+  if (e == hipSuccess) {
+    rbf_kernel<<<1024, 256>>>(n, out);
+    e = hipGetLastError();
+  }
+  if (e == hipSuccess) e = hipDeviceSynchronize();
+  if (e == hipSuccess) e = hipMemcpy(out_host, out, 3 * sizeof(unsigned int), hipMemcpyDeviceToHost);
+  if (out) (void)hipFree(out);
   return static_cast<int>(e);
 }

@@ -41,3 +41,25 @@ def test_device_gelu_all_inputs():
     assert counts[1] == 0, f"gelu_fast differs from the select form on {counts[1]} inputs (first {first[1]:#010x})"
     assert counts[2] == 0, f"gelu_poly differs on {counts[2]} non-finite inputs (first {first[2]:#010x})"
     assert w_poly <= POLY_UNITS, f"gelu_poly deviates by {w_poly} units at x = {at!r}"
+
+
+def test_device_rbf_fused_form():
+    """rbf_chunk_fma (the 16-bit encoder's RBF features) against rbf_chunk (the reference's operation order,
+    bit-exact with the oracle through the fp32 encoder tests) over 2^22 atom-pair offsets of 0 .. 30 A. The two
+    may take neighbouring exp-table entries where t = d^2 / (2 sigma^2) lies within rounding of a half-integer;
+    there the degree-6 Taylor series are cut at r = +1/2 and -1/2, whose remainders are -1.0e-6 and +2.4e-6 of
+    exp(r), so the bound is 5e-6 of the feature; where one of them falls under the exp(-16) cut-off the other
+    is at most 1.2e-7."""
+    if not LIB.exists():
+        pytest.fail(f"{LIB} is not built (run __graft_entry__.build())")
+    lib = C.CDLL(str(LIB))
+    lib.hkbs_check_device_rbf.restype = C.c_int
+    out = (C.c_uint * 3)()
+    print("device rbf: 2^22 offsets", flush=True)
+    assert lib.hkbs_check_device_rbf(1 << 22, out) == 0
+    as_float = lambda u: struct.unpack("<f", struct.pack("<I", u))[0]
+    rel, dabs = as_float(out[0]), as_float(out[1])
+    print(f"rbf_chunk_fma: largest relative deviation {rel:.3g}, absolute {dabs:.3g}, cut-off disagreements {out[2]}",
+          flush=True)
+    assert rel <= 5e-6
+    assert dabs <= 5e-6
