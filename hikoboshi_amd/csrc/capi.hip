@@ -456,6 +456,7 @@ struct hkbs_pmpnn {
   hipStream_t side = nullptr;   // builds the decode schedule while the encoder runs
   hipEvent_t fork = nullptr;    // kNN graph ready (recorded on stream)
   hipEvent_t join = nullptr;    // schedule ready (recorded on side)
+  hipEvent_t rows = nullptr;    // decode positions and the compact layer-0 table's row offsets ready (on side)
   float* weights = nullptr;
   ModelDev model{};
   DeviceArena arena;
@@ -844,12 +845,13 @@ size_t schedule_bytes(int L, int K, int B) {
          aligned_bytes<int32_t>(sched_scratch_words(L, K, nq));
 }
 
-// The fp32 decode reads its layer-0 message rows from a table
-// (launch_layer0_table) unless HKBS_DECODE_L0TABLE=off or the table would
-// exceed kL0TableMaxBytes; the results are the same either way.
+// The fp32 and split bf16 decodes read their layer-0 message rows from a table
+// (launch_layer0_table, fp32-accurate) unless HKBS_DECODE_L0TABLE=off or the
+// table would exceed kL0TableMaxBytes; in fp32 the results are the same either
+// way, in split bf16 layer 0 is then fp32-accurate rather than split bf16.
 constexpr size_t kL0TableMaxBytes = (size_t)4 << 30;
 bool l0_table_wanted(int precision, int L) {
-  if (precision != HKBS_PRECISION_FP32) return false;
+  if (precision != HKBS_PRECISION_FP32 && precision != HKBS_PRECISION_BF16X3) return false;
   if (const char* env = std::getenv("HKBS_DECODE_L0TABLE"); env && std::strcmp(env, "off") == 0) return false;
   const int K = std::min(kKmax, L);
   return l0_table_floats((size_t)L, (size_t)K) * sizeof(float) <= kL0TableMaxBytes;
@@ -1014,6 +1016,7 @@ hkbs_status design_on_device(hkbs_pmpnn* ctx, const float* coords, const uint8_t
   HK_CHECK(hipStreamWaitEvent(ctx->side, ctx->fork, 0), "stream wait failed");
   HK_CHECK(launch_positions(orders, L, shared ? 1 : B, shared, pos, ctx->side), "position kernel failed");
   if (l0base) HK_CHECK(launch_l0_rows(e.idx, pos, L, K, l0base, ctx->side), "layer-0 table rows failed");
+  HK_CHECK(hipEventRecord(ctx->rows, ctx->side), "event record failed");
   HK_CHECK(launch_decode_schedule(a, ctx->side), "decode schedule launch failed");
   HK_CHECK(hipEventRecord(ctx->join, ctx->side), "event record failed");
   if (ctx->timing) HK_CHECK(hipEventRecord(ctx->ev[1], ctx->stream), "event record failed");
@@ -1021,10 +1024,12 @@ hkbs_status design_on_device(hkbs_pmpnn* ctx, const float* coords, const uint8_t
                                      const_cast<_Float16*>(a.Qh)),
            "decoder precompute failed");
   HK_CHECK(launch_zero(reinterpret_cast<float*>(sync), (size_t)B + 1, ctx->stream), "workspace clear failed");
-  // the schedule (built under the encoder) and the compact table's row offsets
-  HK_CHECK(hipStreamWaitEvent(ctx->stream, ctx->join, 0), "stream wait failed");
+  // The table needs the positions and its row offsets; it is built while the
+  // schedule (a few workgroups on the side stream) may still run.
+  HK_CHECK(hipStreamWaitEvent(ctx->stream, ctx->rows, 0), "stream wait failed");
   if (l0tab)
     HK_CHECK(launch_layer0_table(ctx->model, E1, Q, e.idx, pos, l0base, L, K, l0tab, ctx->stream), "layer-0 table failed");
+  HK_CHECK(hipStreamWaitEvent(ctx->stream, ctx->join, 0), "stream wait failed");  // the schedule
   HK_CHECK(launch_step_records(ctx->model, a, rec, ctx->stream), "step records launch failed");
   if (ctx->timing) HK_CHECK(hipEventRecord(ctx->ev[2], ctx->stream), "event record failed");
   HK_CHECK(launch_decode(ctx->model, a, ctx->stream, team), "decode launch failed");
@@ -1090,7 +1095,8 @@ hkbs_status hkbs_pmpnn_create(const uint8_t* data, size_t nbytes, int32_t device
   if (hipStreamCreateWithFlags(&ctx->stream, hipStreamNonBlocking) != hipSuccess ||
       hipStreamCreateWithFlags(&ctx->side, hipStreamNonBlocking) != hipSuccess ||
       hipEventCreateWithFlags(&ctx->fork, hipEventDisableTiming) != hipSuccess ||
-      hipEventCreateWithFlags(&ctx->join, hipEventDisableTiming) != hipSuccess) {
+      hipEventCreateWithFlags(&ctx->join, hipEventDisableTiming) != hipSuccess ||
+      hipEventCreateWithFlags(&ctx->rows, hipEventDisableTiming) != hipSuccess) {
     hkbs_pmpnn_destroy(ctx);
     return fail(HKBS_UNAVAILABLE, "HIP stream creation failed");
   }
@@ -1124,6 +1130,7 @@ void hkbs_pmpnn_destroy(hkbs_pmpnn* ctx) {
   if (ctx->down) (void)hipStreamDestroy(ctx->down);
   if (ctx->fork) (void)hipEventDestroy(ctx->fork);
   if (ctx->join) (void)hipEventDestroy(ctx->join);
+  if (ctx->rows) (void)hipEventDestroy(ctx->rows);
   if (ctx->side) (void)hipStreamDestroy(ctx->side);
   if (ctx->arena.base) (void)hipFree(ctx->arena.base);
   if (ctx->weights) (void)hipFree(ctx->weights);

@@ -618,7 +618,7 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(ModelDev m, DecodeArgs
     float4 rv = make_float4(0.F, 0.F, 0.F, 0.F);
     bool staged = false;
     if (ml > 0) {
-      if (PREC == kPrecFp32 && a.l0tab) {
+      if ((PREC == kPrecFp32 || X3) && a.l0tab) {
         // layer-0 table row of each slot, from the token of a neighbour decoded
         // before the step (written by the team before the last barrier)
         int tid = threadIdx.x;
@@ -677,6 +677,7 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(ModelDev m, DecodeArgs
           const int im = task / kH, c = task % kH;
           const float* f = ff + im * 4 * kH + c;
           x[task] = (f[0] + f[kH]) + (f[2 * kH] + f[3 * kH]);
+          if constexpr (X3) put_split16<PREC>(xs16 + task, kGroup * kH, x[task]);  // W3's input on the MFMA
         }
         __syncthreads();
       }
@@ -733,8 +734,8 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(ModelDev m, DecodeArgs
       if (kPrefetch) gather(0, 0);
       for (int l = 0; l < kLayers; ++l) {
         const DecLayerDev& w = m.dec[l];
-        // Layer 0 of the fp32 decode reads its message rows from the table.
-        const bool from_tab = PREC == kPrecFp32 && l == 0 && a.l0tab != nullptr;
+        // Layer 0 of the fp32 and split bf16 decodes reads its message rows from the table.
+        const bool from_tab = (PREC == kPrecFp32 || X3) && l == 0 && a.l0tab != nullptr;
         const float* pl = prm + l * kPrmLayer;
         if (!from_tab) {  // else x holds the layer-0 message sums (table, above)
           // Message rows g1 = GELU(A + E1_tk + (bw ? R : Q)_j), two members at a time;

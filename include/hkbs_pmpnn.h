@@ -80,8 +80,10 @@ enum {
                               (x = hi + lo, hi = bf16(x), lo = bf16(x - hi): about 16
                               significant bits) and three MFMA products per product
                               (hi.hi + hi.lo + lo.hi); fp32 accumulation, GELU, LayerNorm and
-                              softmax; the message rows' inputs (E1, Q, R) in fp32.
-                              Featurisation and encoder as in HKBS_PRECISION_BF16. Log-probs
+                              softmax; the message rows' inputs (E1, Q, R) in fp32, and layer
+                              0's message rows from the fp32 path's per-backbone table while
+                              it fits 4 GiB. Featurisation and encoder as in
+                              HKBS_PRECISION_BF16. Log-probs
                               within 2e-2 of the fp32 path at T = 0.1 (plain bf16 is not) */
 };
 
