@@ -14,8 +14,11 @@ The JSON line also carries
                       achieved = algorithmic bytes per launch / kernel time, the compulsory
                       bytes of one decode being 4 [B (3 H E_bw + L (2H + V + 1)) + L (2K + 1) H
                       + W_dec] (E_bw = kNN edges to earlier positions); traffic = HBM bytes per
-                      launch from the committed rocprofv3 counters; and the FLOP the launch
-                      executes against the VALU fp32 and MFMA fp16 peaks;
+                      launch from the committed rocprofv3 counters; the FLOP the launch
+                      executes against the VALU fp32 and MFMA fp16 peaks; and l2_stream, the
+                      bytes its L1 caches request from L2 (committed counters) over the kernel
+                      time against the L2-to-L1 peak (the decoder weights are streamed from L2
+                      by every workgroup in every dependency pass);
   encoder             featurise + encode against the fp32 peak;
   cpu_baseline        the reference's own scalar code (oracle/_ref) on a bounded sample of the
                       same workload, timed on this host's cores before the GPU is touched;
@@ -64,6 +67,9 @@ W_DEC = 698_133           # decoder + W_out + W_s floats
 PEAK_FP32_TFLOPS = 157.3  # MI355X dense fp32 (vector and matrix)
 PEAK_FP16_TFLOPS = 2500.0 # MI355X dense fp16 / bf16 MFMA
 PEAK_HBM_GBPS = 8000.0    # MI355X HBM3E
+# L2 to L1 (the port the decode streams its weights through): 16 channels x 128 bytes a clock per XCD (the
+# CDNA3 L2 design), 8 XCDs, 2.4 GHz peak engine clock; 64 bytes a clock for each of the 256 CUs.
+PEAK_L2_GBPS = 16 * 128 * 8 * 2.4
 H, V = 128, 21
 C4_CPU_PROTEINS = 32      # proteins of the ragged batch the CPU baseline scores
 
@@ -320,10 +326,25 @@ def measured_traffic(workload: str):
     return None, None
 
 
+def measured_l2_reads(workload: str):
+    """decode_kernel's L1-to-L2 read bytes per launch from the committed rocprofv3 summary, if it covers this
+    workload."""
+    path = os.path.join(ROOT, "profiles", f"decode_kernel_{workload}.md")
+    key = f"decode_kernel L1-to-L2 read bytes per launch ({workload}):"
+    try:
+        with open(path, encoding="utf-8") as f:
+            for line in f:
+                if line.startswith(key):
+                    return int(line.split(":")[1].strip()), os.path.relpath(path, ROOT)
+    except OSError:
+        pass
+    return None, None
+
+
 def l0_table_used(precision: str, L: int) -> bool:
-    """Whether the library builds the layer-0 message table for this request (fp32 only)."""
+    """Whether the library builds the layer-0 message table for this request (fp32 and split bf16)."""
     K = min(48, L)
-    return precision == "fp32" and os.environ.get("HKBS_DECODE_L0TABLE") != "off" and \
+    return precision in ("fp32", "bf16x3") and os.environ.get("HKBS_DECODE_L0TABLE") != "off" and \
         L * K * 22 * 128 * 4 <= L0_TABLE_MAX_BYTES
 
 
@@ -343,12 +364,13 @@ def decode_roofline(ctx, w, order, decode_ms, precision=None, name=None):
                      + ("; layer 0's rows come from the layer-0 table kernel, outside this launch" if table else ""))
     else:  # W2 and the layer products on the MFMA
         w2x, lpx = SPLIT_PRODUCTS[prec]
-        f_valu = 3 * F_MSG_VALU_LAYER + F_LOGITS
-        f_mfma = w2x * 3 * F_W2_LAYER + lpx * F_LAYER_PRODUCTS
+        f_valu = msg_layers * F_MSG_VALU_LAYER + (48 * 128 if table else 0) + F_LOGITS
+        f_mfma = w2x * msg_layers * F_W2_LAYER + lpx * F_LAYER_PRODUCTS
         mfma_key = "mfma_fp16" if prec == "fp16" else "mfma_bf16"
-        mfma_note = (f"W2 of all three layers as {w2x} and W3, W_in, W_out and the fused next-layer product as "
-                     f"{lpx} {'fp16' if prec == 'fp16' else 'bf16'} products each, useful rows only (members "
-                     "of a pass fill rows of the 16-row tiles)")
+        mfma_note = (f"W2 of {'layers 1 and 2' if table else 'all three layers'} as {w2x} and W3, W_in, W_out and "
+                     f"the fused next-layer product as {lpx} {'fp16' if prec == 'fp16' else 'bf16'} products each, "
+                     "useful rows only (members of a pass fill rows of the 16-row tiles)"
+                     + ("; layer 0's rows come from the layer-0 table kernel, outside this launch" if table else ""))
     idx, _ = ctx.knn(bb.coords, bb.atom_sources)
     pos = np.empty(L, np.int64)
     pos[order] = np.arange(L)
@@ -357,6 +379,7 @@ def decode_roofline(ctx, w, order, decode_ms, precision=None, name=None):
     t = decode_ms * 1e-3
     achieved = launch_bytes / t / 1e9
     traffic, traffic_src = measured_traffic(name or w["name"])
+    l2_bytes, l2_src = measured_l2_reads(name or w["name"])
     valu = B * L * f_valu / t / 1e12
     mfma = B * L * f_mfma / t / 1e12
     return {
@@ -380,6 +403,12 @@ def decode_roofline(ctx, w, order, decode_ms, precision=None, name=None):
                        "frac": round(mfma / PEAK_FP16_TFLOPS, 4), "note": mfma_note},
             "reference_flop_per_residue": F_RES,
         },
+        # every workgroup streams the decoder weights from L2 in every dependency pass: the bytes its L1s
+        # request from L2 (committed counters of the same workload) over this launch's time
+        "l2_stream": None if not l2_bytes else {
+            "bytes": l2_bytes, "achieved": round(l2_bytes / t / 1e9, 1), "peak": round(PEAK_L2_GBPS, 1), "unit": "GB/s",
+            "frac": round(l2_bytes / t / 1e9 / PEAK_L2_GBPS, 4),
+            "source": f"{l2_src}: rocprofv3 TCP_TCC_READ_REQ_sum x 128 bytes, per launch"},
         "limiter": ("latency: neither HBM nor the arithmetic units are near their peaks; the SQ counters in "
                     "profiles/ show waves waiting most of their cycles on L2 weight streaming and barriers"),
     }
