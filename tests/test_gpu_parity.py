@@ -710,6 +710,29 @@ def test_design_half_precision_against_fp32(gpu_ctx, prec, L, B):
         assert np.isfinite(res["scores"]).all()
 
 
+@pytest.mark.parametrize("L,B", [(300, 4), (1000, 2)])
+def test_design_split_bf16_without_layer0_table(gpu_ctx, monkeypatch, L, B):
+    """Split bf16 with its layer 0 computed in split bf16 (HKBS_DECODE_L0TABLE=off, as for chains whose
+    table would exceed 4 GiB) against the fp32 path on the run's own trajectory, at T = 1 and 0.1."""
+    monkeypatch.setenv("HKBS_DECODE_L0TABLE", "off")
+    bb = backbone.single_chain(L, 23)
+    order = _lib.decode_order(bb.atom_sources, 23)
+    seeds = (np.arange(B) + 9).astype(np.uint64)
+    for T in (1.0, 0.1):
+        _say(f"design bf16x3 without the layer-0 table L={L} B={B} T={T}")
+        gpu_ctx.set_precision(_lib.PRECISION_BF16X3)
+        try:
+            res = gpu_ctx.design(bb.coords, bb.atom_sources, B, seeds, order_mode=_lib.ORDER_INPUT_SHARED,
+                                 orders=order, temperature=T)
+        finally:
+            gpu_ctx.set_precision(_lib.PRECISION_FP32)
+        worst = max(float(np.abs(res["log_probs"][b] - _fp32_on_trajectory(gpu_ctx, bb, res["tokens"][b], order, T)).max())
+                    for b in range(B))
+        _say(f"  bf16x3 (no table) vs fp32 max|dlogp|={worst:.3g} at T={T}")
+        assert worst <= HALF_TOL["bf16x3"]
+        assert np.isfinite(res["scores"]).all()
+
+
 @pytest.mark.parametrize("prec", ["fp16", "bf16", "bf16x3"])
 @pytest.mark.parametrize("case", ["L30_masks", "L120_B9"])
 def test_design_half_precision_orders_and_masks(gpu_ctx, prec, case):
