@@ -193,7 +193,11 @@ hkbs_status hkbs_pmpnn_score(hkbs_pmpnn* ctx, const float* coords, const uint8_t
  * [offsets[i], offsets[i+1]) of coords [sum L,5,3], atom_sources [sum L,5] and
  * tokens [sum L]; orders (or NULL = N-to-C) holds each protein's permutation
  * of 0..L_i-1 at the same offsets. Outputs log_probs [sum L,21] and scores [n].
- * Proteins are processed in chunks that share K = min(48, L). Host memory. */
+ * Proteins are processed in chunks that share K = min(48, L). Host memory;
+ * synchronous. Chunks go up and results come back through two staging slots
+ * of pinned host memory that the context keeps (each a chunk's inputs and
+ * log-probs, about 14 MB for chunks of K = 48) while the neighbouring chunks
+ * compute. */
 hkbs_status hkbs_pmpnn_score_batch(hkbs_pmpnn* ctx, int32_t n, const int64_t* offsets, const float* coords,
                                    const uint8_t* atom_sources, const int32_t* tokens,
                                    const int32_t* orders, float* log_probs, float* scores);
