@@ -741,9 +741,10 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(ModelDev m, DecodeArgs
           // Message rows g1 = GELU(A + E1_tk + (bw ? R : Q)_j), two members at a time;
           // rows >= K are zero. Thread owns columns c..c+3 of rows r0 + 16 s
           // (member i0 + s / 3, slot 16 (s % 3) + r0); all gathers of a pair are
-          // issued before the first use. In the 16-bit modes the rows of all four
-          // members fit in G16 (one 16-bit copy each), so the next pair's gathers
-          // are issued before this pair's product and their latency overlaps it.
+          // issued before the first use, and the next pair's once this pair's rows
+          // are in G16, so that their latency overlaps this pair's product. In the
+          // 16-bit modes the rows of all four members fit in G16 (one 16-bit copy
+          // each); otherwise G16 holds one pair (hi and lo rows) at a time.
           // With kPrefetch the first pair's gathers are in flight already (issued
           // before the loop for layer 0, during the previous layer otherwise).
           if (!kPrefetch) gather(l, 0);
@@ -767,9 +768,6 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(ModelDev m, DecodeArgs
           const float b2 = pl[kPrmB2 + col];
           for (int i0 = 0; i0 < ml; i0 += 2) {
             {
-              if constexpr (!kPipe) {
-                if (i0 > 0) gather(l, i0);
-              }
 #pragma unroll
               for (int s = 0; s < kS; ++s) {
                 const int i = i0 + s / 3, k = 16 * (s % 3) + r0;
@@ -829,9 +827,7 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(ModelDev m, DecodeArgs
               }
             }
             __syncthreads();
-            if constexpr (kPipe) {
-              if (i0 + 2 < ml) gather(l, i0 + 2);
-            }
+            if (i0 + 2 < ml) gather(l, i0 + 2);
             for (int i = i0; i < ml && i < i0 + 2; ++i) {
               const _Float16* Gh = kPipe ? G16 + i * kKmax * kLdH : G16 + (i - i0) * 2 * kKmax * kLdH;
               const _Float16* Gl = Gh + kKmax * kLdH;
