@@ -11,7 +11,7 @@
 // kernel, every edge is used once per layer), R^l_j = W1d h^l_j +
 // W1c W_s[tok_j] and Q^l_j = W1d h^0_j; and sum_k (W3 g_k + b3) = W3 sum_k g_k + K b3.
 // Per layer:
-//   tf_edge_kernel  tiles of whole residues (<= 96 edge rows): W1b and W2 on the
+//   tf_edge_kernel  tiles of whole residues (<= 48 edge rows): W1b and W2 on the
 //                   fp16 MFMA with split operands (hi + lo / 2048 for weights and
 //                   rows, about 22 significant bits), GELU, neighbour sum (all K
 //                   slots, no attention mask).

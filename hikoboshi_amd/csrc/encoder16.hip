@@ -15,8 +15,9 @@
 // rows and four waves: the tile's operand sits in LDS already split into fp16
 // hi / lo halves, every wave reads all of its rows and produces 32 of the 128
 // output columns, so each weight fragment streamed from L2 feeds 3 or 4 row
-// blocks. The edge embedding and the node kernel keep 16 rows per wave with
-// the fp32 operand split as it is read (wave_gemm).
+// blocks (the edge embedding builds its features into such a tile in two
+// parts). The node kernel keeps 16 rows per wave with the fp32 operand split
+// as it is read (wave_gemm).
 //
 // W1 [h_i | e_ij | h_j] x (and W11) is W1a h_i + W1b e_ij + W1c h_j: node16
 // forms the W1a and W1c products of every residue once per layer into four
