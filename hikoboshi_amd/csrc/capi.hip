@@ -1531,6 +1531,11 @@ hkbs_status hkbs_pmpnn_score_batch(hkbs_pmpnn* ctx, int32_t n, const int64_t* of
   const size_t Lm = (size_t)maxL;
   const size_t slot_dev = aligned_bytes<float>(Lm * 15) + aligned_bytes<uint8_t>(Lm * 5) + 3 * aligned_bytes<int32_t>(Lm) +
                           aligned_bytes<int64_t>((size_t)maxP + 1) + aligned_bytes<float>(Lm * kV);
+  // Nothing of an earlier call (one that returned early included) may still
+  // use the staging slots or the workspace.
+  hipStream_t s = ctx->stream;
+  for (hipStream_t st2 : {s, ctx->side, ctx->down})
+    if (st2) HK_CHECK(hipStreamSynchronize(st2), "an earlier call's kernels failed");
   DeviceArena& ar = ctx->arena;
   if (ar.reserve(2 * slot_dev + work + (64u << 10)) != hipSuccess)
     return fail(HKBS_INTERNAL_ERROR, "device workspace allocation failed");
@@ -1556,9 +1561,6 @@ hkbs_status hkbs_pmpnn_score_batch(hkbs_pmpnn* ctx, int32_t n, const int64_t* of
   Slot dev[2];
   for (Slot& sl : dev) sl = take_slot([&](auto* p, size_t n) { return ar.take<std::remove_pointer_t<decltype(p)>>(n); });
   const size_t mark = ar.used;
-  hipStream_t s = ctx->stream;
-  for (hipStream_t st2 : {s, ctx->side})
-    HK_CHECK(hipStreamSynchronize(st2), "an earlier call's kernels failed");
   if (ctx->pinned_cap < 2 * slot_dev) {
     if (ctx->pinned) (void)hipHostFree(ctx->pinned);
     ctx->pinned = nullptr;
