@@ -266,6 +266,42 @@ def test_design_chain_mask_missing_atoms_greedy(gpu_ctx, oracle):
     check_design(oracle, bb, g, seeds[:1], 0.0, greedy=True)
 
 
+@pytest.mark.parametrize("case", ["no_active_residue", "nothing_designed", "one_active_residue"])
+def test_design_degenerate_masks(gpu_ctx, oracle, case):
+    """Chains where the decode has nothing or almost nothing to do: every residue without its CA (every
+    step is the inactive pass: true or fallback tokens, zero log-probs, score 0), a chain mask of zeros
+    (every residue keeps its true token with computed log-probs, score 0), and one active residue among
+    inactive ones. Tokens, log-probs and scores against the oracle."""
+    L = 40
+    bb = backbone.single_chain(L, 31)
+    src = bb.atom_sources.copy()
+    cm, tt = None, (np.arange(L) * 3 % 20).astype(np.int32)
+    if case == "no_active_residue":
+        src[:, 1] = 0
+        tt[5] = -1  # no true token: the fallback token
+    elif case == "nothing_designed":
+        cm = np.zeros(L, np.float32)
+    else:
+        src[:, 1] = 0
+        src[17, 1] = 1
+    bb = backbone.Backbone(bb.coords, src)
+    seeds = np.array([3, 4], dtype=np.uint64)
+    _say(f"design {case}")
+    res = gpu_ctx.design(bb.coords, bb.atom_sources, 2, seeds, order_seeds=seeds, temperature=0.1, chain_mask=cm,
+                         true_tokens=tt)
+    check_design(oracle, bb, res, seeds, 0.1, chain_mask=cm, true_tokens=tt)
+    assert np.isfinite(res["scores"]).all()
+    if case == "no_active_residue":
+        np.testing.assert_array_equal(res["log_probs"], 0.0)
+        np.testing.assert_array_equal(res["scores"], 0.0)
+        exp = tt.copy()
+        exp[5] = 20
+        np.testing.assert_array_equal(res["tokens"], np.broadcast_to(exp, (2, L)))
+    elif case == "nothing_designed":
+        np.testing.assert_array_equal(res["tokens"], np.broadcast_to(tt, (2, L)))
+        np.testing.assert_array_equal(res["scores"], 0.0)
+
+
 @pytest.mark.parametrize("L", [1, 7, 47, 49])
 def test_design_small_lengths(gpu_ctx, oracle, L):
     bb = backbone.single_chain(L, L)
