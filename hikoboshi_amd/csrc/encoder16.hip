@@ -257,11 +257,12 @@ __device__ inline void ln_acc(floatx4 (&acc)[8], const float* __restrict__ gam, 
 }
 
 // 64 consecutive edge slots per workgroup: one tile of 4 row blocks. The 416
-// features are built in two parts (feature chunks 0 .. 13, then 14 .. 25, 16
-// features each) so that the split slab holds 224 inputs at a time.
-constexpr int kEmbedChunks0 = 14;
-constexpr int kLdE = 16 * kEmbedChunks0 + 8;  // halves per slab row of the first part
-__global__ __launch_bounds__(kTileThreads, 2) void edge_embed16_kernel(ModelDev m, const float* __restrict__ coords,
+// features are built in four parts (feature chunks 0 .. 7, 8 .. 13, 14 .. 19
+// and 20 .. 25, 16 features each), so that the split slab holds 128 inputs at
+// a time and three workgroups fit a CU.
+constexpr int kEmbedChunks0 = 8;  // chunks of the first part; the other three take 6 each
+constexpr int kLdE = 16 * kEmbedChunks0 + 8;  // halves per slab row
+__global__ __launch_bounds__(kTileThreads, 3) void edge_embed16_kernel(ModelDev m, const float* __restrict__ coords,
                                                                        const uint8_t* __restrict__ src,
                                                                        const int32_t* __restrict__ resid,
                                                                        const int32_t* __restrict__ chain,
@@ -348,13 +349,17 @@ __global__ __launch_bounds__(kTileThreads, 2) void edge_embed16_kernel(ModelDev 
     }
     __syncthreads();
   };
-  constexpr int kC1 = 26 - kEmbedChunks0;
+  constexpr int kC1 = 6;
+  static_assert(kEmbedChunks0 + 3 * kC1 == 26, "feature parts");
   build(0, kEmbedChunks0);
   tile_gemm<RB, 16 * kEmbedChunks0>(S, kLdE, m.enc16.Wedge, n0, (size_t)kEdgeIn * kH, acc);
-  __syncthreads();  // every wave is done with the first part
-  build(kEmbedChunks0, kC1);
-  tile_gemm<RB, 16 * kC1>(S, kLdE, m.enc16.Wedge + (size_t)(2 * kEmbedChunks0) * kH * 8, n0, (size_t)kEdgeIn * kH,
-                          acc, true);
+#pragma unroll
+  for (int part = 0; part < 3; ++part) {
+    const int c0 = kEmbedChunks0 + kC1 * part;
+    __syncthreads();  // every wave is done with the previous part
+    build(c0, kC1);
+    tile_gemm<RB, 16 * kC1>(S, kLdE, m.enc16.Wedge + (size_t)(2 * c0) * kH * 8, n0, (size_t)kEdgeIn * kH, acc, true);
+  }
   tile_layer_norm<RB>(acc, m.ne_g, m.ne_b, stat);
 #pragma unroll
   for (int nt = 0; nt < 2; ++nt)
