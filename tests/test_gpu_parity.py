@@ -311,7 +311,7 @@ def test_design_small_lengths(gpu_ctx, oracle, L):
     check_design(oracle, bb, res, seeds, 0.1)
 
 
-@pytest.mark.parametrize("case", golden_cases()[:2], ids=lambda c: c["fixture_id"])
+@pytest.mark.parametrize("case", golden_cases(), ids=lambda c: c["fixture_id"])
 def test_design_golden_structures(gpu_ctx, oracle, case):
     bb, _ = structure.read_backbone(FIXTURES / case["pdb"])
     seeds = np.array([case["seed"]], dtype=np.uint64)
