@@ -600,9 +600,9 @@ hkbs_status build_model(hkbs_pmpnn* ctx, const float* const* t) {
     }
     q[21] = pack_bf16_k8(ar, d[2], 128, 128);         // W2 (bf16)
     q[23] = pack_bf16_k8(ar, d[2], 128, 128, kHalfBf16Lo);  // W2 bf16 remainder
-    q[16] = pack_k16(ar, {d[4]}, 128, 128, 0, 128);   // W3_p
-    q[17] = pack_k16(ar, {d[10]}, 512, 128, 0, 128);  // Win_p
-    q[18] = pack_k16(ar, {d[12]}, 128, 512, 0, 512);  // Wout_p
+    q[16] = pack_f16_split(ar, d[4], 128, 128);   // W3 hi, lo (fp16; teacher forcing)
+    q[17] = pack_f16_split(ar, d[10], 512, 128);  // W_in
+    q[18] = pack_f16_split(ar, d[12], 128, 512);  // W_out
     if (l + 1 < kLayers) {
       const float* Wn = t[74 + 14 * (l + 1)];
       std::vector<float> nx(256 * 128);
@@ -611,7 +611,7 @@ hkbs_status build_model(hkbs_pmpnn* ctx, const float* const* t) {
           nx[(size_t)n * 128 + k] = Wn[(size_t)n * 512 + k];                // W1a of layer l+1
           nx[(size_t)(128 + n) * 128 + k] = Wn[(size_t)n * 512 + 384 + k];  // W1d of layer l+1
         }
-      q[19] = pack_k16(ar, {nx.data()}, 256, 128, 0, 128);
+      q[19] = pack_f16_split(ar, nx.data(), 256, 128);
     } else {
       q[19] = 0;
     }
@@ -709,10 +709,10 @@ hkbs_status build_model(hkbs_pmpnn* ctx, const float* const* t) {
     w.n1b = B + q[13];
     w.n2g = B + q[14];
     w.n2b = B + q[15];
-    w.W3_p = B + q[16];
-    w.Win_p = B + q[17];
-    w.Wout_p = B + q[18];
-    w.Wnext_p = (l + 1 < kLayers) ? B + q[19] : nullptr;
+    w.W3_s = reinterpret_cast<const uint16_t*>(B + q[16]);
+    w.Win_s = reinterpret_cast<const uint16_t*>(B + q[17]);
+    w.Wout_s = reinterpret_cast<const uint16_t*>(B + q[18]);
+    w.Wnext_s = (l + 1 < kLayers) ? reinterpret_cast<const uint16_t*>(B + q[19]) : nullptr;
   }
   m.W1b_dec_p = B + o.W1b_dec_p;
   m.W1d_dec_p = B + o.W1d_dec_p;

@@ -16,7 +16,8 @@
 //                   rows, about 22 significant bits), GELU, neighbour sum (all K
 //                   slots, no attention mask).
 //   tf_node_kernel  tiles of 16 residues: W3, LN1, FFN, LN2, row-mask gate,
-//                   then the next layer's [A | R] terms, or for the last layer
+//                   then the next layer's [A | R] terms (the products on the
+//                   same split-operand fp16 MFMA), or for the last layer
 //                   logits and log_softmax in the reference's order.
 // Rows may belong to different proteins of a ragged batch: every neighbour
 // index is global, so the kernels never look at protein boundaries.
@@ -172,7 +173,7 @@ __global__ __launch_bounds__(256, 4) void tf_edge_kernel(DecLayerDev w, const fl
   }
 }
 
-__global__ __launch_bounds__(256) void tf_node_kernel(ModelDev m, int layer, const float* __restrict__ msg_sum,
+__global__ __launch_bounds__(256, 3) void tf_node_kernel(ModelDev m, int layer, const float* __restrict__ msg_sum,
                                                       const float* __restrict__ mask, const int32_t* __restrict__ tokens,
                                                       int L, int K, float* __restrict__ h, float* __restrict__ NB,
                                                       float* __restrict__ log_probs) {
@@ -194,9 +195,8 @@ __global__ __launch_bounds__(256) void tf_node_kernel(ModelDev m, int layer, con
   }
   __syncthreads();
   {
-    floatx4 acc[1][2];
-    zero_acc(acc);
-    mfma_tile<1, 2>(A, kLd, w.W3_p, kH, wave * 32, kH, acc);
+    floatx4 acc[2];
+    wave_gemm<2>(A, kLd, w.W3_s, kH, wave * 32, kH, acc);
 #pragma unroll
     for (int nb = 0; nb < 2; ++nb)
 #pragma unroll
@@ -205,7 +205,7 @@ __global__ __launch_bounds__(256) void tf_node_kernel(ModelDev m, int layer, con
         const int col = wave * 32 + nb * 16 + (lane & 15);
         float v = 0.0F;
         if (r0 + row < L)
-          v = h[(size_t)(r0 + row) * kH + col] + (acc[0][nb][i] + static_cast<float>(K) * w.b3[col]) * (1.0F / 30.0F);
+          v = h[(size_t)(r0 + row) * kH + col] + (acc[nb][i] + static_cast<float>(K) * w.b3[col]) * (1.0F / 30.0F);
         X[row * kLd + col] = v;
       }
   }
@@ -213,30 +213,28 @@ __global__ __launch_bounds__(256) void tf_node_kernel(ModelDev m, int layer, con
   for (int row = wave; row < 16; row += 4) ln_row_wave(X + row * kLd, w.n1g, w.n1b, A + row * kLd);  // h1
   __syncthreads();
   {
-    floatx4 acc[1][8];
-    zero_acc(acc);
-    mfma_tile<1, 8>(A, kLd, w.Win_p, kFF, wave * 128, kH, acc);
+    floatx4 acc[8];
+    wave_gemm<8>(A, kLd, w.Win_s, kFF, wave * 128, kH, acc);
 #pragma unroll
     for (int nb = 0; nb < 8; ++nb)
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const int row = 4 * (lane >> 4) + i;
         const int col = wave * 128 + nb * 16 + (lane & 15);
-        F[row * kLdF + col] = gelu(acc[0][nb][i] + w.bin[col], tbl);
+        F[row * kLdF + col] = gelu(acc[nb][i] + w.bin[col], tbl);
       }
   }
   __syncthreads();
   {
-    floatx4 acc[1][2];
-    zero_acc(acc);
-    mfma_tile<1, 2>(F, kLdF, w.Wout_p, kH, wave * 32, kFF, acc);
+    floatx4 acc[2];
+    wave_gemm<2>(F, kLdF, w.Wout_s, kH, wave * 32, kFF, acc);
 #pragma unroll
     for (int nb = 0; nb < 2; ++nb)
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const int row = 4 * (lane >> 4) + i;
         const int col = wave * 32 + nb * 16 + (lane & 15);
-        X[row * kLd + col] = A[row * kLd + col] + (acc[0][nb][i] + w.bout[col]);
+        X[row * kLd + col] = A[row * kLd + col] + (acc[nb][i] + w.bout[col]);
       }
   }
   __syncthreads();
@@ -256,9 +254,8 @@ __global__ __launch_bounds__(256) void tf_node_kernel(ModelDev m, int layer, con
   __syncthreads();
   if (layer + 1 < kLayers) {
     const DecLayerDev& wn = m.dec[layer + 1];
-    floatx4 acc[1][4];
-    zero_acc(acc);
-    mfma_tile<1, 4>(A, kLd, w.Wnext_p, 2 * kH, wave * 64, kH, acc);
+    floatx4 acc[4];
+    wave_gemm<4>(A, kLd, w.Wnext_s, 2 * kH, wave * 64, kH, acc);
 #pragma unroll
     for (int nb = 0; nb < 4; ++nb)
 #pragma unroll
@@ -267,8 +264,8 @@ __global__ __launch_bounds__(256) void tf_node_kernel(ModelDev m, int layer, con
         const int col = wave * 64 + nb * 16 + (lane & 15);  // [0,128): A, [128,256): R
         if (r0 + row >= L) continue;
         const size_t r = r0 + row;
-        NB[r * 256 + col] = col < kH ? acc[0][nb][i] + wn.b1[col]
-                                     : acc[0][nb][i] + wn.T[tokens[r] * kH + (col - kH)];
+        NB[r * 256 + col] = col < kH ? acc[nb][i] + wn.b1[col]
+                                     : acc[nb][i] + wn.T[tokens[r] * kH + (col - kH)];
       }
     return;
   }

@@ -29,6 +29,69 @@ __device__ inline float sum16(float v) {
   return v;
 }
 
+// --------------------------------------------------------------- row blocks ----
+// acc[nt] = A[16 rows][K] . W[K][n0 + 16 nt + (0..15)] for nt < NT. A is the
+// wave's fp32 slab (lda floats per row); Wp the split weights, hi as
+// [K / 8][N][8] halves and lo at Wp + K * N (or Wp + lo_off when Wp starts
+// inside a larger matrix). With lane = 16 g + r, acc[nt][i]
+// is row 4 g + i, column n0 + 16 nt + r. The next k-step's weight fragments
+// load while the current ones are used.
+template <int NT>
+__device__ inline void wave_gemm(const float* A, int lda, const uint16_t* __restrict__ Wp, int N, int n0, int K,
+                                 floatx4 (&acc)[NT], size_t lo_off = 0) {
+  const int lane = threadIdx.x & 63, r = lane & 15, g = lane >> 4;
+  const uint16_t* wh = Wp + ((size_t)g * N + n0 + r) * 8;
+  const uint16_t* wl = wh + (lo_off ? lo_off : (size_t)K * N);
+  const size_t kstep = (size_t)4 * N * 8;  // halves per 32 inputs
+  floatx4 cor[NT];
+#pragma unroll
+  for (int nt = 0; nt < NT; ++nt) {
+    acc[nt] = floatx4{0.F, 0.F, 0.F, 0.F};
+    cor[nt] = acc[nt];
+  }
+  const int nkb = K / 32;
+  f16x8 bh[NT], bl[NT];
+#pragma unroll
+  for (int nt = 0; nt < NT; ++nt) {
+    bh[nt] = *reinterpret_cast<const f16x8*>(wh + (size_t)nt * 16 * 8);
+    bl[nt] = *reinterpret_cast<const f16x8*>(wl + (size_t)nt * 16 * 8);
+  }
+  for (int kb = 0; kb < nkb; ++kb) {
+    const int kn = kb + 1 < nkb ? kb + 1 : kb;
+    f16x8 nh[NT], nl[NT];
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) {
+      nh[nt] = *reinterpret_cast<const f16x8*>(wh + (size_t)kn * kstep + (size_t)nt * 16 * 8);
+      nl[nt] = *reinterpret_cast<const f16x8*>(wl + (size_t)kn * kstep + (size_t)nt * 16 * 8);
+    }
+    const float4* ap = reinterpret_cast<const float4*>(A + r * lda + 32 * kb + 8 * g);
+    const float4 a0 = ap[0], a1 = ap[1];
+    const float av[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
+    f16x8 ah, al;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const float v = __builtin_amdgcn_fmed3f(av[e], -65504.0F, 65504.0F);
+      ah[e] = static_cast<_Float16>(v);
+      al[e] = static_cast<_Float16>((av[e] - static_cast<float>(ah[e])) * 2048.0F);
+    }
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) {
+      acc[nt] = mfma_f16(ah, bh[nt], acc[nt]);
+      cor[nt] = mfma_f16(ah, bl[nt], cor[nt]);
+      cor[nt] = mfma_f16(al, bh[nt], cor[nt]);
+    }
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) {
+      bh[nt] = nh[nt];
+      bl[nt] = nl[nt];
+    }
+  }
+#pragma unroll
+  for (int nt = 0; nt < NT; ++nt)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) acc[nt][i] += cor[nt][i] * (1.0F / 2048.0F);
+}
+
 // ------------------------------------------------------------ edge tiles ----
 // A tile holds 16 RB edge rows. Its operands live in LDS split into fp16
 // halves, hi [rows][ld] then lo [rows][ld] (v = hi + lo / 2048); a row stride

@@ -71,10 +71,11 @@ struct DecLayerDev {
   const float* Win_t;  // [128][512]
   const float* Wout_t; // [512][128]
   const float* W1da_t; // [128][256]: columns [W1d | W1a] (layers 1, 2)
-  const float* W3_p;   // kpack16 128 -> 128 (teacher forcing)
-  const float* Win_p;  // kpack16 128 -> 512
-  const float* Wout_p; // kpack16 512 -> 128
-  const float* Wnext_p; // kpack16 128 -> 256: rows [W1a; W1d] of the next layer (layers 0, 1)
+  // teacher forcing, split fp16 [K / 8][N][8] hi then lo (lo K * N halves later), for wave_gemm
+  const uint16_t* W3_s;    // 128 -> 128
+  const uint16_t* Win_s;   // 128 -> 512
+  const uint16_t* Wout_s;  // 512 -> 128
+  const uint16_t* Wnext_s; // 128 -> 256: outputs [W1a; W1d] of the next layer (layers 0, 1)
   const float* T;      // [21][128]: W1c . W_s[v]
   const float *b1, *b2, *b3, *bin, *bout;
   const float *n1g, *n1b, *n2g, *n2b;
