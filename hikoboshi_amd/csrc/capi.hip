@@ -357,8 +357,11 @@ struct DeviceArena {
   char* base = nullptr;
   size_t cap = 0;
   size_t used = 0;
-  hipError_t reserve(size_t bytes) {
+  // busy: an event that follows every kernel still using the workspace (or
+  // null); a workspace that has to grow is freed only after it.
+  hipError_t reserve(size_t bytes, hipEvent_t busy) {
     if (bytes <= cap) return hipSuccess;
+    if (busy) (void)hipEventSynchronize(busy);
     if (base) (void)hipFree(base);
     base = nullptr;
     cap = 0;
@@ -473,6 +476,11 @@ struct hkbs_pmpnn {
   hipEvent_t score_ev[3][2] = {};
   char* pinned = nullptr;
   size_t pinned_cap = 0;
+  // End of the last device entry point's work: those calls return while their
+  // kernels may still run (on the caller's stream), and every later call on the
+  // context waits for this event before it uses the workspace.
+  hipEvent_t done = nullptr;
+  bool done_recorded = false;
 };
 
 namespace {
@@ -487,6 +495,25 @@ hkbs_status hip_fail(hipError_t e, const char* what) {
     hipError_t _e = (expr);                       \
     if (_e != hipSuccess) return hip_fail(_e, what); \
   } while (0)
+
+// Calls on one context share its workspace. A device entry point returns while
+// its kernels may still run on the caller's stream, so every call makes the
+// stream it enqueues on wait, on the device, for the end of the previous device
+// entry point's work before its first enqueue, and a device entry point records
+// that end (ctx->done). A stream being captured into a HIP graph does neither:
+// the caller orders the graph after earlier calls on the context.
+hipEvent_t busy_event(const hkbs_pmpnn* ctx) { return ctx->done_recorded ? ctx->done : nullptr; }
+
+hkbs_status after_previous_call(hkbs_pmpnn* ctx, hipStream_t s) {
+  if (ctx->done_recorded) HK_CHECK(hipStreamWaitEvent(s, ctx->done, 0), "stream wait failed");
+  return HKBS_OK;
+}
+
+hkbs_status record_call_end(hkbs_pmpnn* ctx, hipStream_t s) {
+  HK_CHECK(hipEventRecord(ctx->done, s), "event record failed");
+  ctx->done_recorded = true;
+  return HKBS_OK;
+}
 
 hkbs_status build_model(hkbs_pmpnn* ctx, const float* const* t) {
   HostArena ar;
@@ -900,26 +927,25 @@ size_t design_scratch_bytes(int L, int B, bool shared, bool l0table) {
 // reservation fails the table is dropped (l0table = false) and the smaller
 // reservation is tried before the call fails.
 template <typename Need>
-hkbs_status reserve_workspace(DeviceArena& ar, const Need& need, bool& l0table) {
-  if (ar.reserve(need(l0table)) == hipSuccess) return HKBS_OK;
+hkbs_status reserve_workspace(hkbs_pmpnn* ctx, const Need& need, bool& l0table) {
+  DeviceArena& ar = ctx->arena;
+  if (ar.reserve(need(l0table), busy_event(ctx)) == hipSuccess) return HKBS_OK;
   if (l0table) {
     l0table = false;
-    if (ar.reserve(need(false)) == hipSuccess) return HKBS_OK;
+    if (ar.reserve(need(false), busy_event(ctx)) == hipSuccess) return HKBS_OK;
   }
   return fail(HKBS_INTERNAL_ERROR, "device workspace allocation failed");
 }
 
-// A device entry point called with the caller's stream runs its work there. It
-// first waits for anything still pending on the context's own stream (earlier
-// calls may use the same workspace), except while the caller's stream is being
-// captured into a HIP graph: a capture must not synchronise other streams, and
-// the caller orders the captured work after earlier calls.
-hkbs_status adopt_caller_stream(hkbs_pmpnn* ctx, void* stream) {
-  hipStream_t user = static_cast<hipStream_t>(stream);
+// A device entry point runs its work on the caller's stream (the context's own
+// when none is given). *capturing tells whether that stream is being captured
+// into a HIP graph: a captured call neither waits for nor records the end of
+// other calls (after_previous_call, record_call_end).
+hkbs_status adopt_caller_stream(hkbs_pmpnn* ctx, void* stream, bool* capturing) {
+  if (stream) ctx->stream = static_cast<hipStream_t>(stream);
   hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
-  HK_CHECK(hipStreamIsCapturing(user, &cs), "stream capture query failed");
-  if (cs == hipStreamCaptureStatusNone) HK_CHECK(hipStreamSynchronize(ctx->stream), "context stream failed");
-  ctx->stream = user;
+  HK_CHECK(hipStreamIsCapturing(ctx->stream, &cs), "stream capture query failed");
+  *capturing = cs != hipStreamCaptureStatusNone;
   return HKBS_OK;
 }
 
@@ -1096,7 +1122,8 @@ hkbs_status hkbs_pmpnn_create(const uint8_t* data, size_t nbytes, int32_t device
       hipStreamCreateWithFlags(&ctx->side, hipStreamNonBlocking) != hipSuccess ||
       hipEventCreateWithFlags(&ctx->fork, hipEventDisableTiming) != hipSuccess ||
       hipEventCreateWithFlags(&ctx->join, hipEventDisableTiming) != hipSuccess ||
-      hipEventCreateWithFlags(&ctx->rows, hipEventDisableTiming) != hipSuccess) {
+      hipEventCreateWithFlags(&ctx->rows, hipEventDisableTiming) != hipSuccess ||
+      hipEventCreateWithFlags(&ctx->done, hipEventDisableTiming) != hipSuccess) {
     hkbs_pmpnn_destroy(ctx);
     return fail(HKBS_UNAVAILABLE, "HIP stream creation failed");
   }
@@ -1121,6 +1148,8 @@ void hkbs_pmpnn_destroy(hkbs_pmpnn* ctx) {
   if (ctx->stream) (void)hipStreamSynchronize(ctx->stream);
   if (ctx->side) (void)hipStreamSynchronize(ctx->side);
   if (ctx->down) (void)hipStreamSynchronize(ctx->down);
+  // a device entry point's kernels may still run on the caller's stream
+  if (ctx->done_recorded) (void)hipEventSynchronize(ctx->done);
   for (hipEvent_t& ev : ctx->ev)
     if (ev) (void)hipEventDestroy(ev);
   for (auto& evs : ctx->score_ev)
@@ -1131,6 +1160,7 @@ void hkbs_pmpnn_destroy(hkbs_pmpnn* ctx) {
   if (ctx->fork) (void)hipEventDestroy(ctx->fork);
   if (ctx->join) (void)hipEventDestroy(ctx->join);
   if (ctx->rows) (void)hipEventDestroy(ctx->rows);
+  if (ctx->done) (void)hipEventDestroy(ctx->done);
   if (ctx->side) (void)hipStreamDestroy(ctx->side);
   if (ctx->arena.base) (void)hipFree(ctx->arena.base);
   if (ctx->weights) (void)hipFree(ctx->weights);
@@ -1214,7 +1244,8 @@ hkbs_status hkbs_pmpnn_design(hkbs_pmpnn* ctx, const float* coords, const uint8_
            aligned_bytes<float>(B) + aligned_bytes<float>((size_t)B * L) + (64u << 10);
   };
   DeviceArena& ar = ctx->arena;
-  if ((st = reserve_workspace(ar, need, l0table)) != HKBS_OK) return st;
+  if ((st = reserve_workspace(ctx, need, l0table)) != HKBS_OK) return st;
+  if ((st = after_previous_call(ctx, ctx->stream)) != HKBS_OK) return st;
   ar.reset();
   Inputs in{};
   if ((st = upload_inputs(ctx, ar, coords, atom_sources, residue_indices, chain_labels, chain_mask, true_tokens, L, in)) != HKBS_OK)
@@ -1279,10 +1310,10 @@ hkbs_status hkbs_pmpnn_design_device(hkbs_pmpnn* ctx, const float* coords, const
   };
   DeviceArena& ar = ctx->arena;
   hipStream_t saved = ctx->stream;
-  if (stream) {
-    if ((st = adopt_caller_stream(ctx, stream)) != HKBS_OK) return st;
-  }
-  if ((st = reserve_workspace(ar, need, l0table)) != HKBS_OK) {
+  bool capturing = false;
+  if ((st = adopt_caller_stream(ctx, stream, &capturing)) != HKBS_OK ||
+      (st = reserve_workspace(ctx, need, l0table)) != HKBS_OK ||
+      (!capturing && (st = after_previous_call(ctx, ctx->stream)) != HKBS_OK)) {
     ctx->stream = saved;
     return st;
   }
@@ -1291,6 +1322,10 @@ hkbs_status hkbs_pmpnn_design_device(hkbs_pmpnn* ctx, const float* coords, const
   st = design_on_device(ctx, coords, atom_sources, residue_indices, chain_labels, chain_mask, true_tokens, L, B, orders,
                         shared_order != 0, sampler_seeds, temperature, greedy, tokens, log_probs, scores, ar, chosen,
                         l0table);
+  if (!capturing) {  // recorded also after a failure: part of the work may have been enqueued
+    const hkbs_status end = record_call_end(ctx, ctx->stream);
+    if (st == HKBS_OK) st = end;
+  }
   ctx->stream = saved;
   return st;
 }
@@ -1319,13 +1354,20 @@ hkbs_status hkbs_pmpnn_design_device_noalloc(hkbs_pmpnn* ctx, const float* coord
   ar.base = ctx->scratch;
   ar.cap = kNoAllocScratchBytes;
   hipStream_t saved = ctx->stream;
-  if (stream) {
-    if ((st = adopt_caller_stream(ctx, stream)) != HKBS_OK) return st;
+  bool capturing = false;
+  if ((st = adopt_caller_stream(ctx, stream, &capturing)) != HKBS_OK ||
+      (!capturing && (st = after_previous_call(ctx, ctx->stream)) != HKBS_OK)) {
+    ctx->stream = saved;
+    return st;
   }
   float* chosen = ar.take<float>((size_t)B * L);
   st = design_on_device(ctx, coords, atom_sources, residue_indices, chain_labels, chain_mask, true_tokens, L, B, orders,
                         shared_order != 0, sampler_seeds, temperature, greedy, tokens, log_probs, scores, ar, chosen,
                         l0table);
+  if (!capturing) {
+    const hkbs_status end = record_call_end(ctx, ctx->stream);
+    if (st == HKBS_OK) st = end;
+  }
   ctx->stream = saved;
   return st;
 }
@@ -1450,8 +1492,9 @@ hkbs_status hkbs_pmpnn_score(hkbs_pmpnn* ctx, const float* coords, const uint8_t
   const int K = std::min(kKmax, L);
   DeviceArena& ar = ctx->arena;
   if (ar.reserve(input_bytes(L) + tf_bytes(L, K) + 2 * aligned_bytes<int32_t>(L) + aligned_bytes<float>((size_t)L * kV) +
-                 (64u << 10)) != hipSuccess)
+                 (64u << 10), busy_event(ctx)) != hipSuccess)
     return fail(HKBS_INTERNAL_ERROR, "device workspace allocation failed");
+  if ((st = after_previous_call(ctx, ctx->stream)) != HKBS_OK) return st;
   ar.reset();
   Inputs in{};
   if ((st = upload_inputs(ctx, ar, coords, atom_sources, residue_indices, chain_labels, nullptr, nullptr, L, in)) != HKBS_OK)
@@ -1536,8 +1579,9 @@ hkbs_status hkbs_pmpnn_score_batch(hkbs_pmpnn* ctx, int32_t n, const int64_t* of
   hipStream_t s = ctx->stream;
   for (hipStream_t st2 : {s, ctx->side, ctx->down})
     if (st2) HK_CHECK(hipStreamSynchronize(st2), "an earlier call's kernels failed");
+  if (ctx->done_recorded) HK_CHECK(hipEventSynchronize(ctx->done), "an earlier call's kernels failed");
   DeviceArena& ar = ctx->arena;
-  if (ar.reserve(2 * slot_dev + work + (64u << 10)) != hipSuccess)
+  if (ar.reserve(2 * slot_dev + work + (64u << 10), nullptr) != hipSuccess)
     return fail(HKBS_INTERNAL_ERROR, "device workspace allocation failed");
   struct Slot {
     float* coords;
@@ -1669,8 +1713,9 @@ hkbs_status hkbs_pmpnn_knn(hkbs_pmpnn* ctx, const float* coords, const uint8_t* 
   const int K = std::min(kKmax, L);
   const size_t S = (size_t)L * K;
   DeviceArena& ar = ctx->arena;
-  if (ar.reserve(input_bytes(L) + encode_bytes(L, K) + (64u << 10)) != hipSuccess)
+  if (ar.reserve(input_bytes(L) + encode_bytes(L, K) + (64u << 10), busy_event(ctx)) != hipSuccess)
     return fail(HKBS_INTERNAL_ERROR, "device workspace allocation failed");
+  if ((st = after_previous_call(ctx, ctx->stream)) != HKBS_OK) return st;
   ar.reset();
   Inputs in{};
   if ((st = upload_inputs(ctx, ar, coords, atom_sources, nullptr, nullptr, nullptr, nullptr, L, in)) != HKBS_OK) return st;
@@ -1693,8 +1738,9 @@ hkbs_status hkbs_pmpnn_encode(hkbs_pmpnn* ctx, const float* coords, const uint8_
   const int K = std::min(kKmax, L);
   const size_t S = (size_t)L * K;
   DeviceArena& ar = ctx->arena;
-  if (ar.reserve(input_bytes(L) + encode_bytes(L, K) + (64u << 10)) != hipSuccess)
+  if (ar.reserve(input_bytes(L) + encode_bytes(L, K) + (64u << 10), busy_event(ctx)) != hipSuccess)
     return fail(HKBS_INTERNAL_ERROR, "device workspace allocation failed");
+  if ((st = after_previous_call(ctx, ctx->stream)) != HKBS_OK) return st;
   ar.reset();
   Inputs in{};
   if ((st = upload_inputs(ctx, ar, coords, atom_sources, residue_indices, chain_labels, nullptr, nullptr, L, in)) != HKBS_OK)
@@ -1721,8 +1767,9 @@ hkbs_status hkbs_pmpnn_edge_features(hkbs_pmpnn* ctx, const float* coords, const
   const int K = std::min(kKmax, L);
   const size_t S = (size_t)L * K;
   DeviceArena& ar = ctx->arena;
-  if (ar.reserve(input_bytes(L) + encode_bytes(L, K) + aligned_bytes<float>(S * kEdgeIn) + (64u << 10)) != hipSuccess)
+  if (ar.reserve(input_bytes(L) + encode_bytes(L, K) + aligned_bytes<float>(S * kEdgeIn) + (64u << 10), busy_event(ctx)) != hipSuccess)
     return fail(HKBS_INTERNAL_ERROR, "device workspace allocation failed");
+  if ((st = after_previous_call(ctx, ctx->stream)) != HKBS_OK) return st;
   ar.reset();
   Inputs in{};
   if ((st = upload_inputs(ctx, ar, coords, atom_sources, residue_indices, chain_labels, nullptr, nullptr, L, in)) != HKBS_OK)

@@ -25,8 +25,13 @@
  *  - Optional inputs may be NULL: residue_indices (default 0..L-1),
  *    chain_labels (default one chain), chain_mask (default ones),
  *    true_tokens (default: fallback token 20 for residues not designed).
- *  - Calls on one context are serialised by the caller (a context owns one
- *    HIP stream and its workspace). Distinct contexts are independent.
+ *  - Calls on one context are made from one host thread at a time (a context
+ *    owns one HIP stream and its workspace). Their GPU work is ordered by the
+ *    library: a call's work starts after that of the previous device design
+ *    call on the context has ended, on whatever stream it ran (the new call's
+ *    stream waits on the device, the host does not block), except on a stream
+ *    that is being captured into a HIP graph. Distinct contexts are
+ *    independent.
  */
 #ifndef HKBS_PMPNN_H
 #define HKBS_PMPNN_H
@@ -136,9 +141,9 @@ hkbs_status hkbs_pmpnn_design(hkbs_pmpnn* ctx, const float* coords, const uint8_
  * teams. An order that is not a permutation of 0..L-1 is not decoded: that
  * sequence's score is NaN and its tokens and log-probs are not written (the
  * reference rejects such an order, cpp/modules/mpnn/decode_order_scalar.cpp:67-79;
- * hkbs_pmpnn_design returns HKBS_INVALID_ARGUMENT for it). With a stream that
- * is not being captured the call first waits for work pending on the context's
- * own stream. */
+ * hkbs_pmpnn_design returns HKBS_INVALID_ARGUMENT for it). On a stream that is
+ * not being captured the call's work waits, on the device, for the end of the
+ * previous calls on the context, and the next call waits for its own end. */
 hkbs_status hkbs_pmpnn_design_device(hkbs_pmpnn* ctx, const float* coords,
                                      const uint8_t* atom_sources, const int32_t* residue_indices,
                                      const int32_t* chain_labels, const float* chain_mask,
@@ -165,8 +170,8 @@ hkbs_status hkbs_pmpnn_design_device(hkbs_pmpnn* ctx, const float* coords,
  * at zero is cleared by a kernel in the call): calls that overlap on one GPU,
  * from any context or stream, race and must be serialised by the caller. On a
  * stream that is being captured into a HIP graph the call records its kernels
- * (no memset nodes) without synchronising any stream; the caller then orders
- * the graph after earlier calls on the context. */
+ * (no memset nodes) and neither waits for nor marks the end of other calls on
+ * the context; the caller then orders the graph after earlier calls. */
 hkbs_status hkbs_pmpnn_design_device_noalloc(hkbs_pmpnn* ctx, const float* coords,
                                              const uint8_t* atom_sources,
                                              const int32_t* residue_indices,

@@ -365,6 +365,80 @@ def test_design_device_refuses_non_permutation_order(gpu_ctx):
     assert scores[0] == one["scores"][0]
 
 
+def test_device_design_calls_on_other_streams_are_ordered(gpu_ctx):
+    """A device design call returns while its kernels run on the caller's stream. Calls that follow it on
+    the same context, on another stream (device entry point) or on the context's own stream (synchronous
+    entry point), without the caller synchronising in between, share its workspace and must wait for it:
+    every output equals that of the same call made alone."""
+    import ctypes as C
+
+    from hikoboshi_amd import hip
+
+    lib = _lib.load()
+    bbs = [backbone.single_chain(300, 7), backbone.single_chain(300, 8)]
+    B = 64
+    bufs = []
+    for i, bb in enumerate(bbs):
+        order = _lib.decode_order(bb.atom_sources, 7 + i)
+        seeds = (7 + 100 * i + np.arange(B)).astype(np.uint64)
+        ins = [hip.DeviceBuffer.from_array(a) for a in (bb.coords, bb.atom_sources, order, seeds)]
+        outs = [hip.DeviceBuffer(B * bb.L * 4), hip.DeviceBuffer(B * bb.L * 21 * 4), hip.DeviceBuffer(B * 4)]
+        bufs.append((bb, ins, outs))
+
+    def launch(i, stream):
+        bb, (c, s, o, sd), (tk, lp, sc) = bufs[i]
+        _lib.check(lib.hkbs_pmpnn_design_device(gpu_ctx._h, c.ptr, s.ptr, None, None, None, None, bb.L, B, o.ptr, 1,
+                                                sd.ptr, C.c_float(0.1), 0, tk.ptr, lp.ptr, sc.ptr,
+                                                stream.h if stream else None))
+
+    def read(i):
+        bb, _, outs = bufs[i]
+        got = []
+        for buf, shape, dt in zip(outs, [(B, bb.L), (B, bb.L, 21), (B,)], [np.int32, np.float32, np.float32]):
+            a = np.empty(shape, dt)
+            hip.check(hip.rt().hipMemcpy(a.ctypes.data_as(C.c_void_p), buf.ptr, C.c_size_t(a.nbytes), hip.D2H), "D2H")
+            got.append(a)
+        return got
+
+    def clear():
+        for _, _, outs in bufs:
+            for o in outs:
+                hip.check(hip.rt().hipMemset(o.ptr, 0xFF, C.c_size_t(o.nbytes)), "memset")
+        hip.device_synchronize()
+
+    alone = []
+    for i in range(2):
+        clear()
+        launch(i, None)
+        hip.device_synchronize()
+        alone.append(read(i))
+    s1, s2 = hip.Stream(), hip.Stream()
+    try:
+        _say("two device design calls on two streams, no synchronisation between them")
+        clear()
+        launch(0, s1)
+        launch(1, s2)
+        hip.device_synchronize()
+        for i in range(2):
+            for g, a in zip(read(i), alone[i]):
+                np.testing.assert_array_equal(g, a)
+        _say("a device design call followed by a synchronous design call")
+        clear()
+        launch(0, s1)
+        bb1 = bbs[1]
+        sync_res = gpu_ctx.design(bb1.coords, bb1.atom_sources, B, (7 + 100 + np.arange(B)).astype(np.uint64),
+                                  order_mode=_lib.ORDER_INPUT_SHARED, orders=_lib.decode_order(bb1.atom_sources, 8),
+                                  temperature=0.1)
+        hip.device_synchronize()
+        for g, a in zip(read(0), alone[0]):
+            np.testing.assert_array_equal(g, a)
+        np.testing.assert_array_equal(sync_res["tokens"], alone[1][0])
+        np.testing.assert_array_equal(sync_res["scores"], alone[1][2])
+    finally:
+        s1.destroy()
+        s2.destroy()
+
+
 @pytest.mark.parametrize("B", [9, 64])
 def test_design_team_split_is_exact(gpu_ctx, oracle, B, monkeypatch):
     """Several workgroups per sequence give the same bits as one workgroup per sequence, with the team
