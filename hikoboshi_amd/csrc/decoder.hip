@@ -46,7 +46,7 @@ typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
 constexpr int kThreads = 512;
 
-constexpr int kGroup = kDecodeGroup;  // steps one workgroup decodes in a pass (sizes its LDS)
+constexpr int kGroup = 4;  // members of the fp32 products' accumulators (Gemv)
 
 // Y[i][o] = sum_p X[i][p] Wt[p][o] for i < m rows (m <= kGroup), OUT outputs
 // and IN inputs on all threads. Thread (q, grp) owns float4 column q and
@@ -150,6 +150,7 @@ struct MGemv {
   static constexpr bool BF = PREC == kPrecBf16 || X3;     // bf16 operands
   static constexpr int KB = IN / 32 / NP;                 // k-blocks of 32 inputs per part
   static constexpr int CPW = OUT / 16 / (kThreads / 64);  // 16-column blocks per wave
+  static constexpr int GR = decode_group(PREC);           // member rows of the split copies
   static_assert(PREC != kPrecFp32 && KB * 32 * NP == IN && CPW * 16 * (kThreads / 64) == OUT, "MFMA product shape");
   using Op = typename std::conditional<BF, bf16x8, half8>::type;
   struct Part {
@@ -180,7 +181,7 @@ struct MGemv {
       A.c[cb] = A.a[cb];
     }
   }
-  // xs: the split copy, hi plane [kGroup][IN] then lo plane
+  // xs: the split copy, hi plane [GR][IN] then lo plane
   static __device__ inline void run(const Part& P, int part, const uint16_t* xs, int ml, Acc& A) {
     const int lane = threadIdx.x & 63, row = lane & 15;
 #pragma unroll
@@ -189,7 +190,7 @@ struct MGemv {
       if (row < ml) {
         const int at = row * IN + 32 * (part * KB + kb) + 8 * (lane >> 4);
         ah = *reinterpret_cast<const Op*>(xs + at);
-        al = *reinterpret_cast<const Op*>(xs + kGroup * IN + at);
+        al = *reinterpret_cast<const Op*>(xs + GR * IN + at);
       }
 #pragma unroll
       for (int cb = 0; cb < CPW; ++cb) {
@@ -207,22 +208,23 @@ struct MGemv {
       }
     }
   }
-  // y[m][n] into ys [kGroup][OUT]: lane j < 16 holds column j of rows (members) 0..3
+  // y[m][n] into ys [GR][OUT]: lane j holds column j % 16 of rows (members) 4 (j / 16) + 0..3
   static __device__ inline void store(const Acc& A, int ml, float* ys) {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    if (lane >= 16) return;
+    const int r0 = 4 * (lane >> 4);
+    if (r0 >= ml) return;
 #pragma unroll
     for (int cb = 0; cb < CPW; ++cb) {
-      const int col = (wave * CPW + cb) * 16 + lane;
+      const int col = (wave * CPW + cb) * 16 + (lane & 15);
 #pragma unroll
-      for (int e = 0; e < kGroup; ++e) {
-        if (e >= ml) break;
-        ys[e * OUT + col] = X3 ? A.a[cb][e] + A.c[cb][e] : BF ? A.a[cb][e] : A.a[cb][e] + A.c[cb][e] * (1.0F / 2048.0F);
+      for (int e = 0; e < 4; ++e) {
+        if (r0 + e >= ml) break;
+        ys[(r0 + e) * OUT + col] =
+            X3 ? A.a[cb][e] + A.c[cb][e] : BF ? A.a[cb][e] : A.a[cb][e] + A.c[cb][e] * (1.0F / 2048.0F);
       }
     }
   }
 };
-static_assert(kGroup == 4, "MGemv::store: members are rows 0..3 of a lane's accumulator");
 
 // Split 16-bit copy of one activation for MGemv: plane 0 = hi, plane 1 (lo_at
 // elements later) = lo; bf16 and split bf16: x = hi + lo, fp16: x = hi + lo / 2048
@@ -413,40 +415,44 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(ModelDev m, DecodeArgs
   using GIn = Gemv<kH, kFF, 2, PREC>;
   using GOut = Gemv<kFF, kH, 2, PREC>;
   using GDa = Gemv<kH, 2 * kH, 1, PREC>;
+  constexpr int G = decode_group(PREC);  // steps this workgroup can hold in a pass
+  static_assert(G == kGroup || M16, "the fp32 products (Gemv) hold kGroup members");
+  // 16-bit staging of the MFMA products (below) in `part`, which the fp32 products use for partial sums
+  constexpr int kPart = std::max(8192, G * kFF + (6 * G * kH + 2 * G * kFF) / 2);
   // message rows of two members as fp16 pairs: [member][hi, lo][row][kLdH]
   __shared__ __attribute__((aligned(16))) _Float16 G16[2 * 2 * kKmax * kLdH];
-  __shared__ __attribute__((aligned(16))) float part[8192];
-  __shared__ __attribute__((aligned(16))) float ff[kGroup * kFF];  // also [m][256] scratch
-  __shared__ __attribute__((aligned(16))) float h[kGroup * kH];
-  __shared__ __attribute__((aligned(16))) float hA[kGroup * kH];
-  __shared__ __attribute__((aligned(16))) float x[kGroup * kH];
-  __shared__ __attribute__((aligned(16))) float h1[kGroup * kH];
-  __shared__ __attribute__((aligned(16))) float Pd[kGroup * 2 * kH];  // W1d h^l of layers 1, 2
+  __shared__ __attribute__((aligned(16))) float part[kPart];
+  __shared__ __attribute__((aligned(16))) float ff[G * kFF];  // also [m][256] scratch
+  __shared__ __attribute__((aligned(16))) float h[G * kH];
+  __shared__ __attribute__((aligned(16))) float hA[G * kH];
+  __shared__ __attribute__((aligned(16))) float x[G * kH];
+  __shared__ __attribute__((aligned(16))) float h1[G * kH];
+  __shared__ __attribute__((aligned(16))) float Pd[G * 2 * kH];  // W1d h^l of layers 1, 2
   // logits weights (32 outputs, 21 used) as fp32, [k / 4][v][k % 4]: lane v reads four k of its column at once
   __shared__ __attribute__((aligned(16))) float wlg[kH * 32];
   __shared__ __attribute__((aligned(16))) float prm[kPrmSize];
   __shared__ __attribute__((aligned(16))) float gtab[kGeluPolyLds];  // GELU polynomials
   // neighbour words of the step records: -1 for an empty slot, else j | 2^30 if j is decoded before the step
-  __shared__ __attribute__((aligned(16))) int nbw[kGroup * kKmax];
-  __shared__ int cls[kGroup * kKmax];  // layer-0 table row of each slot (with a.l0tab)
-  __shared__ __attribute__((aligned(16))) float q0s[kGroup * kH];  // Q^0 rows of the members (R^0 base)
+  __shared__ __attribute__((aligned(16))) int nbw[G * kKmax];
+  __shared__ int cls[G * kKmax];  // layer-0 table row of each slot (with a.l0tab)
+  __shared__ __attribute__((aligned(16))) float q0s[G * kH];  // Q^0 rows of the members (R^0 base)
   // per member: residue, sampler draw index, design weight chain_mask * mask as float bits (0: keep the
   // true token), true token or the fallback token
-  __shared__ int4 meta[kGroup];
+  __shared__ int4 meta[G];
   // per member: mask of the slots decoded before the step (lo, hi words), first layer-0 table row
-  __shared__ int4 meta2[kGroup];
-  __shared__ int tok_s[kGroup];
+  __shared__ int4 meta2[G];
+  __shared__ int tok_s[G];
   __shared__ int bad;
 
   // 16-bit modes: the MFMA products' outputs and the split 16-bit copies of
   // their inputs (put_split16), in `part`, which only the fp32 products use
-  float* ys = part;  // [kGroup][up to kFF]
-  uint16_t* const s16 = reinterpret_cast<uint16_t*>(part + kGroup * kFF);
-  uint16_t* const xs16 = s16;                    // message sums, [hi, lo][kGroup][kH]
-  uint16_t* const h1s16 = s16 + 2 * kGroup * kH;  // h1
-  uint16_t* const hs16 = s16 + 4 * kGroup * kH;   // h
-  uint16_t* const ffs16 = s16 + 6 * kGroup * kH;  // ff, [hi, lo][kGroup][kFF]
-  static_assert(kGroup * kFF + (6 * kGroup * kH + 2 * kGroup * kFF) / 2 <= 8192, "16-bit staging fits part");
+  float* ys = part;  // [G][up to kFF]
+  uint16_t* const s16 = reinterpret_cast<uint16_t*>(part + G * kFF);
+  uint16_t* const xs16 = s16;                    // message sums, [hi, lo][G][kH]
+  uint16_t* const h1s16 = s16 + 2 * G * kH;  // h1
+  uint16_t* const hs16 = s16 + 4 * G * kH;   // h
+  uint16_t* const ffs16 = s16 + 6 * G * kH;  // ff, [hi, lo][G][kFF]
+  static_assert(G * kFF + (6 * G * kH + 2 * G * kFF) / 2 <= kPart, "16-bit staging fits part");
   const int P = a.team;
   int b = blockIdx.x, rank = 0;
   if (P > 1) {
@@ -570,19 +576,23 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(ModelDev m, DecodeArgs
     const int mg = pstart[ps + 1] - s0;
     return mg > rank ? (mg - rank + P - 1) / P : 0;
   };
-  auto rec_load = [&](int s0, int mlp) -> float4 {
-    const int i = threadIdx.x / kRecFloat4;
-    if (mlp > kGroup || i >= mlp) return make_float4(0.F, 0.F, 0.F, 0.F);
-    return rec[(size_t)(s0 + rank + P * i) * kRecFloat4 + threadIdx.x % kRecFloat4];
+  // Slice e = threadIdx.x + kThreads q of the members' records is thread
+  // threadIdx.x's slice of round q (kRecRounds rounds cover G members).
+  constexpr int kRecRounds = (G * kRecFloat4 + kThreads - 1) / kThreads;
+  auto rec_load = [&](int s0, int mlp, int q) -> float4 {
+    const int e = threadIdx.x + kThreads * q, i = e / kRecFloat4;
+    if (mlp > G || i >= mlp) return make_float4(0.F, 0.F, 0.F, 0.F);
+    return rec[(size_t)(s0 + rank + P * i) * kRecFloat4 + e % kRecFloat4];
   };
-  auto rec_store = [&](int mlp, const float4& v) {
+  auto rec_store = [&](int mlp, const float4& v, int q) {
     // The destination is recomputed here on purpose: a copy hoisted out of the
     // pass loop would be spilled, and reloading it put memory latency in the
     // pass hand-over.
     int tid = threadIdx.x;
     asm volatile("" : "+v"(tid));
-    const int i = tid / kRecFloat4, w = tid % kRecFloat4;
-    if (mlp > kGroup || i >= mlp || (w > kKmax / 4 + 1 && w < 16)) return;
+    const int e = tid + kThreads * q;
+    const int i = e / kRecFloat4, w = e % kRecFloat4;
+    if (mlp > G || i >= mlp || (w > kKmax / 4 + 1 && w < 16)) return;
     float4* dst;
     if (w < kKmax / 4) {
       dst = reinterpret_cast<float4*>(nbw + i * kKmax) + w;
@@ -596,26 +606,29 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(ModelDev m, DecodeArgs
     }
     *dst = v;
   };
-  static_assert(kKmax % 4 == 0 && kRecFloat4 == 16 + 3 * kH / 4 && kRecFloat4 * kGroup <= kThreads, "record layout");
+  static_assert(kKmax % 4 == 0 && kRecFloat4 == 16 + 3 * kH / 4 && kRecRounds <= 2, "record layout");
   int ml = 0;
   if (npass >= 1) {
     int s0 = 0;
     ml = members(1, s0);
-    rec_store(ml, rec_load(s0, ml));
+#pragma unroll
+    for (int q = 0; q < kRecRounds; ++q) rec_store(ml, rec_load(s0, ml, q), q);
   }
   if (P > 1 && pstart[1] > pstart[0]) {  // the pass-0 barrier
     if (!team_wait(counter, ++passes * P, a.spin_limit, a.fault, &bad, a.fences)) goto finish;
   }
   __syncthreads();
   for (int pass = 1; pass <= npass; ++pass) {
-    if (ml > kGroup) {  // a schedule built for a larger team: refuse rather than overrun LDS
+    if (ml > G) {  // a schedule built for a larger team: refuse rather than overrun LDS
       if (threadIdx.x == 0) __hip_atomic_store(a.fault, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       bad = 1;
       break;
     }
     int s0n = 0, mln = 0;  // the next pass
     if (pass < npass) mln = members(pass + 1, s0n);
-    float4 rv = make_float4(0.F, 0.F, 0.F, 0.F);
+    float4 rv[kRecRounds];
+#pragma unroll
+    for (int q = 0; q < kRecRounds; ++q) rv[q] = make_float4(0.F, 0.F, 0.F, 0.F);
     bool staged = false;
     if (ml > 0) {
       if ((PREC == kPrecFp32 || X3) && a.l0tab) {
@@ -623,7 +636,7 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(ModelDev m, DecodeArgs
         // before the step (written by the team before the last barrier)
         int tid = threadIdx.x;
         asm volatile("" : "+v"(tid));  // keeps these addresses out of loop-invariant (spilled) registers
-        static_assert(kGroup * kKmax <= kThreads, "one slot per thread");
+        static_assert(G * kKmax <= kThreads, "one slot per thread");
         if (tid < ml * kKmax && tid % kKmax < K) {
           const int i = tid / kKmax, k = tid % kKmax;
           const int wd = nbw[tid];
@@ -646,9 +659,11 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(ModelDev m, DecodeArgs
         // masked to +0 (an AND rather than a select, which the compiler would
         // turn into a branch around each load). Indices fit 32 bits (the table
         // is at most 4 GiB).
-        const int i = tid >> 7, gq = (tid >> 5) & 3, q = tid & 31;
-        static_assert(kThreads == 128 * kGroup, "table sum mapping");
-        if (i < ml) {
+        // Members in rounds of four (128 threads each).
+        static_assert(kThreads == 512, "table sum mapping");
+        const int gq = (tid >> 5) & 3, q = tid & 31;
+#pragma unroll 1
+        for (int i = tid >> 7; i < ml; i += 4) {
           const float* tb = a.l0tab + 4u * q;
           int cl[12];  // table rows
 #pragma unroll
@@ -671,13 +686,14 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(ModelDev m, DecodeArgs
             sum.w += v[n].w;
           }
           *reinterpret_cast<float4*>(ff + (i * 4 + gq) * kH + 4 * q) = sum;
+          if constexpr (G <= 4) break;  // one round
         }
         __syncthreads();
         for (int task = threadIdx.x; task < ml * kH; task += kThreads) {
           const int im = task / kH, c = task % kH;
           const float* f = ff + im * 4 * kH + c;
           x[task] = (f[0] + f[kH]) + (f[2 * kH] + f[3 * kH]);
-          if constexpr (X3) put_split16<PREC>(xs16 + task, kGroup * kH, x[task]);  // W3's input on the MFMA
+          if constexpr (X3) put_split16<PREC>(xs16 + task, G * kH, x[task]);  // W3's input on the MFMA
         }
         __syncthreads();
       }
@@ -699,11 +715,11 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(ModelDev m, DecodeArgs
           // first, so that the row loads below issue back to back (read one
           // slot at a time, every load waited for its own LDS reads).
           int wd[kS];
-          const int t0 = meta[min(i0, kGroup - 1)].x, t1 = meta[min(i0 + 1, kGroup - 1)].x;
+          const int t0 = meta[min(i0, G - 1)].x, t1 = meta[min(i0 + 1, G - 1)].x;
 #pragma unroll
           for (int s = 0; s < kS; ++s) {
             const int i = i0 + s / 3, k = 16 * (s % 3) + r0;  // k < kKmax
-            wd[s] = nbw[min(i, kGroup - 1) * kKmax + k] | ((i < ml && k < K) ? 0 : -1);
+            wd[s] = nbw[min(i, G - 1) * kKmax + k] | ((i < ml && k < K) ? 0 : -1);
           }
 #pragma unroll
           for (int s = 0; s < kS; ++s) {
@@ -898,7 +914,7 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(ModelDev m, DecodeArgs
               sum += __shfl_xor(sum, 32, 64);
               if (lane < 16) {
                 x[i * kH + col] = sum;
-                if constexpr (M16) put_split16<PREC>(xs16 + i * kH + col, kGroup * kH, sum);
+                if constexpr (M16) put_split16<PREC>(xs16 + i * kH + col, G * kH, sum);
               }
             }
             if constexpr (!kPipe) __syncthreads();
@@ -940,7 +956,7 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(ModelDev m, DecodeArgs
 #pragma unroll
             for (int hh = 0; hh < 2; ++hh) {
               const int c = lane + 64 * hh;
-              put_split16<PREC>(h1s16 + wave * kH + c, kGroup * kH, h1[wave * kH + c]);
+              put_split16<PREC>(h1s16 + wave * kH + c, G * kH, h1[wave * kH + c]);
             }
           }
           __syncthreads();
@@ -962,7 +978,7 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(ModelDev m, DecodeArgs
             const int o = task % kFF;
             const float f = gelu_poly(ys[task] + pl[kPrmBin + o], gtab);
             ff[task] = f;
-            put_split16<PREC>(ffs16 + task, kGroup * kFF, f);
+            put_split16<PREC>(ffs16 + task, G * kFF, f);
           }
           __syncthreads();
           // h^{l+1} = LN2(h1 + (W_out f + b)); each next part in flight during the current part's products
@@ -994,7 +1010,7 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(ModelDev m, DecodeArgs
 #pragma unroll
             for (int hh = 0; hh < 2; ++hh) {
               const int c = lane + 64 * hh;
-              put_split16<PREC>(hs16 + wave * kH + c, kGroup * kH, h[wave * kH + c]);
+              put_split16<PREC>(hs16 + wave * kH + c, G * kH, h[wave * kH + c]);
             }
           }
           __syncthreads();
@@ -1106,7 +1122,8 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(ModelDev m, DecodeArgs
           }
         }
       }
-      rv = rec_load(s0n, mln);  // the next pass's records, in flight during logits and sampling
+#pragma unroll
+      for (int q = 0; q < kRecRounds; ++q) rv[q] = rec_load(s0n, mln, q);  // in flight during logits and sampling
       staged = true;
       // Wave i computes member i's logits = W_out h + b and draws its token:
       // lane v + 32 kh sums inputs [64 kh, 64 kh + 64) of output v (weights
@@ -1170,13 +1187,16 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(ModelDev m, DecodeArgs
         }
       }
     }
-    if (!staged) rv = rec_load(s0n, mln);
+    if (!staged)
+#pragma unroll
+      for (int q = 0; q < kRecRounds; ++q) rv[q] = rec_load(s0n, mln, q);
     // this pass's LDS state is consumed (team_arrive starts with a barrier)
     if (P > 1)
       team_arrive(counter, a.fences);
     else
       __syncthreads();
-    rec_store(mln, rv);
+#pragma unroll
+    for (int q = 0; q < kRecRounds; ++q) rec_store(mln, rv[q], q);
     ml = mln;
     if (P > 1 && !team_wait(counter, ++passes * P, a.spin_limit, a.fault, &bad, a.fences)) break;
     __syncthreads();
@@ -2078,7 +2098,8 @@ hipError_t launch_decode_as(const ModelDev& m, const DecodeArgs& args, hipStream
   const long teams_per_xcd = (a.B + 7) / 8;
   int P = team_size_as<PREC>(a.B, max_team);
   if (!a.sync || !a.fault) P = 1;
-  if (a.max_members < 1 || a.max_members > kGroup * P) return hipErrorInvalidValue;  // the schedule assumed a larger team
+  if (a.max_members < 1 || a.max_members > decode_group(PREC) * P)
+    return hipErrorInvalidValue;  // the schedule assumed a larger team
   a.spin_limit = kSpinLimit;
   if (const char* env = std::getenv("HKBS_DECODE_SPIN_LIMIT")) a.spin_limit = (uint32_t)std::max(1, std::atoi(env));
   {

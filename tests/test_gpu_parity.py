@@ -439,10 +439,13 @@ def test_device_design_calls_on_other_streams_are_ordered(gpu_ctx):
         s2.destroy()
 
 
+@pytest.mark.parametrize("prec", ["fp32", "bf16x3"])
 @pytest.mark.parametrize("B", [9, 64])
-def test_design_team_split_is_exact(gpu_ctx, oracle, B, monkeypatch):
+def test_design_team_split_is_exact(gpu_ctx, oracle, B, prec, monkeypatch):
     """Several workgroups per sequence give the same bits as one workgroup per sequence, with the team
-    barrier in either form (relaxed, or with release/acquire fences: HKBS_DECODE_FENCES=1)."""
+    barrier in either form (relaxed, or with release/acquire fences: HKBS_DECODE_FENCES=1). In split bf16 a
+    workgroup holds up to six steps of a pass (rows of the MFMA products' operand), four in fp32: how the
+    steps are grouped does not change any step's arithmetic."""
     bb = backbone.single_chain(120, 4)
     src = bb.atom_sources.copy()
     src[[3, 60, 61], 0] = 0  # inactive residues take the one-residue path
@@ -452,17 +455,22 @@ def test_design_team_split_is_exact(gpu_ctx, oracle, B, monkeypatch):
     tt = (np.arange(120) * 5 % 20).astype(np.int32)
     seeds = (np.arange(B) + 31).astype(np.uint64)
     out = {}
-    for team in ("1", "2", "4", "4f"):
-        monkeypatch.setenv("HKBS_DECODE_TEAM", team[0])
-        monkeypatch.setenv("HKBS_DECODE_FENCES", "1" if team.endswith("f") else "0")  # 4f: fenced barrier
-        _say(f"design team={team} B={B}")
-        out[team] = gpu_ctx.design(bb.coords, bb.atom_sources, B, seeds, order_seeds=seeds, temperature=0.1,
-                                   chain_mask=cm, true_tokens=tt)
+    gpu_ctx.set_precision(PRECISIONS.get(prec, _lib.PRECISION_FP32))
+    try:
+        for team in ("1", "2", "4", "4f"):
+            monkeypatch.setenv("HKBS_DECODE_TEAM", team[0])
+            monkeypatch.setenv("HKBS_DECODE_FENCES", "1" if team.endswith("f") else "0")  # 4f: fenced barrier
+            _say(f"design {prec} team={team} B={B}")
+            out[team] = gpu_ctx.design(bb.coords, bb.atom_sources, B, seeds, order_seeds=seeds, temperature=0.1,
+                                       chain_mask=cm, true_tokens=tt)
+    finally:
+        gpu_ctx.set_precision(_lib.PRECISION_FP32)
     for team in ("2", "4", "4f"):
         for key in ("tokens", "log_probs", "scores"):
             np.testing.assert_array_equal(out[team][key], out["1"][key], err_msg=f"team {team} {key}")
-    check_design(oracle, bb, {k: v[:2] for k, v in out["4"].items()}, seeds[:2], 0.1, chain_mask=cm,
-                 true_tokens=tt)
+    if prec == "fp32":
+        check_design(oracle, bb, {k: v[:2] for k, v in out["4"].items()}, seeds[:2], 0.1, chain_mask=cm,
+                     true_tokens=tt)
 
 
 @pytest.mark.parametrize("L,B,shared", [(120, 5, False), (300, 64, True)])
