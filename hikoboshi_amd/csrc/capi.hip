@@ -1026,7 +1026,7 @@ hkbs_status design_on_device(hkbs_pmpnn* ctx, const float* coords, const uint8_t
     a.E1 = nullptr;
   }
   const int team = decode_team_size(a.precision, B, 8);
-  a.max_members = decode_group(a.precision) * team;
+  a.max_members = decode_group(a.precision, team) * team;
   a.pass_granule = team;
   if (const char* env = std::getenv("HKBS_DECODE_MAX_MEMBERS"))
     a.max_members = std::max(1, std::min(a.max_members, std::atoi(env)));
@@ -1273,7 +1273,7 @@ hkbs_status hkbs_pmpnn_design(hkbs_pmpnn* ctx, const float* coords, const uint8_
     // A team of workgroups could not run together (the device was busy with
     // other work): decode again with one workgroup per sequence.
     DecodeArgs one = ctx->last_decode;
-    one.max_members = decode_group(one.precision);  // steps one workgroup can hold
+    one.max_members = decode_group(one.precision, 1);  // steps one workgroup can hold
     one.pass_granule = 1;
     HK_CHECK(launch_decode_schedule(one, s), "decode schedule launch failed");
     HK_CHECK(launch_step_records(ctx->model, one, const_cast<float4*>(one.rec), s), "step records launch failed");

@@ -64,7 +64,7 @@ struct Gemv {
   static constexpr int GROUPS = kThreads / Q4;  // input groups
   static constexpr int PER = IN / GROUPS;       // inputs per group
   static constexpr int PP = PER / NP;           // inputs per part
-  static_assert(GROUPS * OUT * kGroup <= 8192 && PP * NP == PER, "partial buffer");
+  static_assert(PP * NP == PER, "parts");
   // fp32 weights: one float4 per input; bf16 / fp16 weights: four 16-bit values (8 bytes) per input
   using W4 = typename std::conditional<WT == kPrecFp32, float4, uint2>::type;
   struct Part {
@@ -150,7 +150,7 @@ struct MGemv {
   static constexpr bool BF = PREC == kPrecBf16 || X3;     // bf16 operands
   static constexpr int KB = IN / 32 / NP;                 // k-blocks of 32 inputs per part
   static constexpr int CPW = OUT / 16 / (kThreads / 64);  // 16-column blocks per wave
-  static constexpr int GR = decode_group(PREC);           // member rows of the split copies
+  static constexpr int GR = decode_group(PREC, 1);        // member rows of the split copies
   static_assert(PREC != kPrecFp32 && KB * 32 * NP == IN && CPW * 16 * (kThreads / 64) == OUT, "MFMA product shape");
   using Op = typename std::conditional<BF, bf16x8, half8>::type;
   struct Part {
@@ -406,7 +406,7 @@ __device__ inline bool team_wait(uint32_t* counter, uint32_t target, uint32_t sp
 // fp32, and so do the logit weights (hi + lo, exact in fp32). In every mode
 // activations, LayerNorm, the logits (one wave per member, weights in LDS) and
 // the sampler are fp32.
-template <int PREC>
+template <int PREC, int G>
 __global__ __launch_bounds__(kThreads) void decode_kernel(ModelDev m, DecodeArgs a) {
   constexpr bool BF = PREC == kPrecBf16, HF = PREC == kPrecFp16, X3 = PREC == kPrecBf16x3;
   constexpr bool H16 = BF || HF;        // message rows' inputs (E1, Q, R) in fp16
@@ -415,13 +415,23 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(ModelDev m, DecodeArgs
   using GIn = Gemv<kH, kFF, 2, PREC>;
   using GOut = Gemv<kFF, kH, 2, PREC>;
   using GDa = Gemv<kH, 2 * kH, 1, PREC>;
-  constexpr int G = decode_group(PREC);  // steps this workgroup can hold in a pass
-  static_assert(G == kGroup || M16, "the fp32 products (Gemv) hold kGroup members");
-  // 16-bit staging of the MFMA products (below) in `part`, which the fp32 products use for partial sums
-  constexpr int kPart = std::max(8192, G * kFF + (6 * G * kH + 2 * G * kFF) / 2);
+  // G: steps this workgroup can hold in a pass (decode_group(PREC, team size))
+  static_assert(G == decode_group(PREC, 1) || G == decode_group(PREC, 2), "group size of this mode");
   // message rows of two members as fp16 pairs: [member][hi, lo][row][kLdH]
   __shared__ __attribute__((aligned(16))) _Float16 G16[2 * 2 * kKmax * kLdH];
-  __shared__ __attribute__((aligned(16))) float part[kPart];
+  // 16-bit modes: staging of the MFMA products (below). fp32: the products'
+  // partial sums [member][group][output] (2048 floats per member); with more
+  // members than kGroup they share G16's space: the message rows and the partial
+  // sums are never live together (barriers separate a layer's last W2 product
+  // from its W3 partial sums, and the fused next-layer sums from the next
+  // layer's message rows).
+  constexpr bool kPartInG16 = !M16 && G > kGroup;
+  constexpr int kPart = M16 ? G * kFF + (6 * G * kH + 2 * G * kFF) / 2 : kPartInG16 ? 1 : 2048 * G;
+  __shared__ __attribute__((aligned(16))) float part16[kPart];
+  float* const part = kPartInG16 ? reinterpret_cast<float*>(G16) : part16;
+  static_assert(M16 || (G3::GROUPS * kH == 2048 && GIn::GROUPS * kFF == 2048 && GOut::GROUPS * kH == 2048 &&
+                        GDa::GROUPS * 2 * kH == 2048 && (!kPartInG16 || 2048 * G * sizeof(float) <= sizeof(G16))),
+                "fp32 partial sums fit");
   __shared__ __attribute__((aligned(16))) float ff[G * kFF];  // also [m][256] scratch
   __shared__ __attribute__((aligned(16))) float h[G * kH];
   __shared__ __attribute__((aligned(16))) float hA[G * kH];
@@ -452,7 +462,7 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(ModelDev m, DecodeArgs
   uint16_t* const h1s16 = s16 + 2 * G * kH;  // h1
   uint16_t* const hs16 = s16 + 4 * G * kH;   // h
   uint16_t* const ffs16 = s16 + 6 * G * kH;  // ff, [hi, lo][G][kFF]
-  static_assert(G * kFF + (6 * G * kH + 2 * G * kFF) / 2 <= kPart, "16-bit staging fits part");
+  static_assert(!M16 || G * kFF + (6 * G * kH + 2 * G * kFF) / 2 <= kPart, "16-bit staging fits part");
   const int P = a.team;
   int b = blockIdx.x, rank = 0;
   if (P > 1) {
@@ -1039,10 +1049,17 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(ModelDev m, DecodeArgs
           // (W3 loads here: issued during the message rows they competed with the gathers and cost spills)
           typename G3::Part g3;
           G3::load(g3, (BF ? static_cast<const void*>(w.W3_h) : HF ? static_cast<const void*>(w.W3_f) : w.W3_t), 0);
+          // The products accumulate kGroup members at a time: chunk i0 holds members
+          // i0 .. i0 + n - 1 (each member's sums are the same whatever the chunk; one
+          // chunk when G <= kGroup).
           float4 acc[kGroup];
-          zero4(acc);
-          G3::fma(g3, 0, x, ml, acc);
-          G3::store(acc, ml, part);
+          const int chunk_end = G <= kGroup ? 1 : ml;
+          for (int i0 = 0; i0 < chunk_end; i0 += kGroup) {
+            const int n = G <= kGroup ? ml : min(kGroup, ml - i0);
+            zero4(acc);
+            G3::fma(g3, 0, x + i0 * kH, n, acc);
+            G3::store(acc, n, part + i0 * G3::GROUPS * kH);
+          }
           typename GIn::Part in0;  // first half of W_in in flight during the reduction and LN1
           GIn::load(in0, (BF ? static_cast<const void*>(w.Win_h) : HF ? static_cast<const void*>(w.Win_f) : w.Win_t), 0);
           __syncthreads();
@@ -1057,15 +1074,18 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(ModelDev m, DecodeArgs
           }
           __syncthreads();
           // f = GELU(W_in h1 + b)
-          zero4(acc);
           {
             // second half in flight during the first half's FMAs
             typename GIn::Part in1;
             GIn::load(in1, (BF ? static_cast<const void*>(w.Win_h) : HF ? static_cast<const void*>(w.Win_f) : w.Win_t), 1);
-            GIn::fma(in0, 0, h1, ml, acc);
-            GIn::fma(in1, 1, h1, ml, acc);
+            for (int i0 = 0; i0 < chunk_end; i0 += kGroup) {
+              const int n = G <= kGroup ? ml : min(kGroup, ml - i0);
+              zero4(acc);
+              GIn::fma(in0, 0, h1 + i0 * kH, n, acc);
+              GIn::fma(in1, 1, h1 + i0 * kH, n, acc);
+              GIn::store(acc, n, part + i0 * GIn::GROUPS * kFF);
+            }
           }
-          GIn::store(acc, ml, part);
           typename GOut::Part out0;  // first half of W_out in flight during the reduction and GELU
           GOut::load(out0, (BF ? static_cast<const void*>(w.Wout_h) : HF ? static_cast<const void*>(w.Wout_f) : w.Wout_t), 0);
           __syncthreads();
@@ -1075,14 +1095,17 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(ModelDev m, DecodeArgs
           }
           __syncthreads();
           // h^{l+1} = LN2(h1 + (W_out f + b)) (the mask gate is 1 for an active residue)
-          zero4(acc);
           {
             typename GOut::Part out1;  // second half in flight during the first half's FMAs
             GOut::load(out1, (BF ? static_cast<const void*>(w.Wout_h) : HF ? static_cast<const void*>(w.Wout_f) : w.Wout_t), 1);
-            GOut::fma(out0, 0, ff, ml, acc);
-            GOut::fma(out1, 1, ff, ml, acc);
+            for (int i0 = 0; i0 < chunk_end; i0 += kGroup) {
+              const int n = G <= kGroup ? ml : min(kGroup, ml - i0);
+              zero4(acc);
+              GOut::fma(out0, 0, ff + i0 * kFF, n, acc);
+              GOut::fma(out1, 1, ff + i0 * kFF, n, acc);
+              GOut::store(acc, n, part + i0 * GOut::GROUPS * kH);
+            }
           }
-          GOut::store(acc, ml, part);
           // The next layer's fused weights load during LN2. The last layer issues
           // the same loads with every lane on one 16-byte slice (unused; an L1 hit):
           // an unconditional load keeps the register budget, and a full-size one
@@ -1109,9 +1132,12 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(ModelDev m, DecodeArgs
           if (l + 1 < kLayers) {
             // fused [W1d | W1a] of the next layer: W1d h is kept for R (completed with
             // T[tok] after sampling), W1a h + b1 is the next A.
-            zero4(acc);
-            GDa::fma(da, 0, h, ml, acc);
-            GDa::store(acc, ml, part);
+            for (int i0 = 0; i0 < chunk_end; i0 += kGroup) {
+              const int n = G <= kGroup ? ml : min(kGroup, ml - i0);
+              zero4(acc);
+              GDa::fma(da, 0, h + i0 * kH, n, acc);
+              GDa::store(acc, n, part + i0 * GDa::GROUPS * 2 * kH);
+            }
             __syncthreads();
             for (int task = threadIdx.x; task < ml * kH; task += kThreads) {
               const int i = task / kH, c = task % kH;
@@ -2080,7 +2106,8 @@ int team_size_as(int B, int max_team) {
   int dev = 0, cus = 0, per_cu = 0;
   if (hipGetDevice(&dev) != hipSuccess ||
       hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
-      hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, decode_kernel<PREC>, kThreads, 0) != hipSuccess)
+      hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, decode_kernel<PREC, decode_group(PREC, 2)>, kThreads, 0) !=
+          hipSuccess)
     return 1;
   const long resident = (long)cus * per_cu;
   const long teams_per_xcd = (B + 7) / 8;
@@ -2098,7 +2125,7 @@ hipError_t launch_decode_as(const ModelDev& m, const DecodeArgs& args, hipStream
   const long teams_per_xcd = (a.B + 7) / 8;
   int P = team_size_as<PREC>(a.B, max_team);
   if (!a.sync || !a.fault) P = 1;
-  if (a.max_members < 1 || a.max_members > decode_group(PREC) * P)
+  if (a.max_members < 1 || a.max_members > decode_group(PREC, P) * P)
     return hipErrorInvalidValue;  // the schedule assumed a larger team
   a.spin_limit = kSpinLimit;
   if (const char* env = std::getenv("HKBS_DECODE_SPIN_LIMIT")) a.spin_limit = (uint32_t)std::max(1, std::atoi(env));
@@ -2114,11 +2141,11 @@ hipError_t launch_decode_as(const ModelDev& m, const DecodeArgs& args, hipStream
     // running nothing else every team is resident. Every team barrier wait is
     // bounded: a member that is not resident ends the wait with the fault
     // word raised instead of hanging.
-    decode_kernel<PREC><<<grid, kThreads, 0, stream>>>(mm, a);
+    decode_kernel<PREC, decode_group(PREC, 2)><<<grid, kThreads, 0, stream>>>(mm, a);
     return hipGetLastError();
   }
   a.team = 1;
-  decode_kernel<PREC><<<a.B, kThreads, 0, stream>>>(mm, a);
+  decode_kernel<PREC, decode_group(PREC, 1)><<<a.B, kThreads, 0, stream>>>(mm, a);
   return hipGetLastError();
 }
 

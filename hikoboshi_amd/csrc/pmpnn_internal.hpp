@@ -178,7 +178,7 @@ struct DecodeArgs {
   uint32_t spin_limit;    // polls before a team barrier gives up (set by launch_decode)
   int fences;             // team barrier with release/acquire fences (set by launch_decode, HKBS_DECODE_FENCES=1)
   int precision;          // 0 fp32, 1 bf16, 2 fp16, 3 split bf16 (see decode_kernel)
-  int max_members;        // most steps one pass decodes (<= decode_group(precision) * team size)
+  int max_members;        // most steps one pass decodes (<= decode_group(precision, team) * team)
   int pass_granule;       // team size the schedule balances passes for (<= 1: none)
   const float* l0tab;     // layer-0 message rows (fp32 decode; launch_layer0_table), or null
   const int32_t* l0base;  // [L + 1] first table row of each residue (compact table of one shared order), or null
@@ -188,11 +188,13 @@ struct DecodeArgs {
   const _Float16* Qh;     // [3][L][128]: Q blocks 0..2
   _Float16* Rh;           // [B][3][L][128]
 };
-// Steps one workgroup decodes in a pass: 6 in the split bf16 mode (DecodeArgs.precision 3), whose layer
-// products run on the MFMA with the members as rows of a 16-row operand, so that more members cost no
-// more product time; 4 in the other modes (the fp32 products on the VALU grow with the members).
-constexpr int decode_group(int precision) { return precision == 3 ? 6 : 4; }
-constexpr int kDecodeGroupMax = 6;
+// Steps one workgroup decodes in a pass, for DecodeArgs.precision and the team
+// size (workgroups per sequence): 6 in the split bf16 mode (3), whose layer
+// products run on the MFMA with the members as rows of a 16-row operand, so that
+// more members cost no more product time, and in fp32 (0) with one workgroup per
+// sequence, where this capacity rather than the depth of the step graph bounds
+// the passes; 4 otherwise. Team size 1 gives the largest value of a mode.
+constexpr int decode_group(int precision, int team) { return precision == 3 || (precision == 0 && team == 1) ? 6 : 4; }
 // int32 words of DecodeArgs.sched_tmp for nq orders of length L with K neighbours.
 inline size_t sched_scratch_words(size_t L, size_t K, size_t nq) { return nq * (3 * L + 1 + 4 + L * K); }
 // Four words per order inside sched_tmp, written by the schedule: {decoded in dependency
@@ -220,9 +222,9 @@ hipError_t launch_step_records(const ModelDev& m, const DecodeArgs& a, float4* r
 int decode_team_size(int precision, int B, int max_team);
 // Decodes with up to min(8, max_team) workgroups per sequence when the whole
 // grid fits the device at once, else one per sequence; a.max_members must not
-// exceed decode_group(a.precision) x that team size (the schedule has to be built for it).
+// exceed decode_group(a.precision, team) x that team size (the schedule has to be built for it).
 // A team launch that could not run its members together raises *a.fault (and
-// leaves NaN scores); rebuild the schedule with max_members = decode_group(a.precision) and
+// leaves NaN scores); rebuild the schedule with max_members = decode_group(a.precision, 1) and
 // run it again with max_team = 1.
 hipError_t launch_decode(const ModelDev& m, const DecodeArgs& a, hipStream_t stream, int max_team = 8);
 // Q[l] = W1d_l h^0 (l < 3), Q[3] = W1a_0 h^0, without the E1 edge products.
