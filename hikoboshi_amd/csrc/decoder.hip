@@ -378,6 +378,33 @@ __device__ inline bool team_wait(uint32_t* counter, uint32_t target, uint32_t sp
   return *bad == 0;
 }
 
+// Token of a residue whose step another workgroup of the team (or this one)
+// decodes: tokens start the decode at -1 and a step's token is stored only
+// after the R rows of that step have completed at the device coherence point,
+// so once a device-scope load returns the token, device-scope loads of the
+// step's R rows return the rows. Polls at most spin_limit times; a wait that
+// runs out raises the fault word and *bad and returns 0 (the caller then
+// stops). With fences != 0 an agent-scope acquire fence follows the poll
+// (the writer puts a release fence before the token store).
+__device__ inline int await_token(const int32_t* tok, uint32_t spin_limit, uint32_t* fault, int* bad, int fences) {
+  int v = load_dev(tok);
+  uint32_t n = 0;
+  while (v < 0) {
+    if (++n >= spin_limit) {
+      *bad = 1;
+      __hip_atomic_store(fault, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      return 0;
+    }
+    __builtin_amdgcn_s_sleep(1);
+    v = load_dev(tok);
+  }
+  if (fences) __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+  return v;
+}
+// Added to the team counter by a workgroup that stopped early (a wait ran out):
+// the final count then tells rank 0 that the sequence was not decoded.
+constexpr uint32_t kTeamAbort = 1u << 24;
+
 // Decodes one sequence per team of P workgroups (P = a.team, 1..8) in the
 // passes of the dependency schedule (dag_schedule_kernel): a pass holds up to
 // a.max_members (<= kGroup * P) steps whose earlier kNN neighbours were all
@@ -498,7 +525,6 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(ModelDev m, DecodeArgs
   float* lp_out = a.log_probs ? a.log_probs + (size_t)b * L * kV : nullptr;
   float* chosen = a.chosen_lp + (size_t)b * L;
   uint32_t* counter = a.sync + b;
-  uint32_t passes = 0;
   const uint64_t seed = a.seeds[b];
   const float T = (a.temperature > 0.0F && isfinite(a.temperature)) ? a.temperature : 1.0F;
   const bool greedy = a.greedy || a.temperature <= 0.0F;
@@ -536,6 +562,11 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(ModelDev m, DecodeArgs
     }
     wlg[((k >> 2) * 32 + v) * 4 + (k & 3)] = wv;
   }
+  // Every token starts at -1 (not decoded yet); later passes wait for the
+  // tokens of their steps' earlier neighbours (await_token) instead of for
+  // the whole team.
+  if (rank == 0)
+    for (int i = threadIdx.x; i < L; i += kThreads) store_dev(tokens + i, -1);
   __syncthreads();
 
   // Pass 0: inactive residues (inverse_fold_scalar.cpp:804-813): fallback
@@ -573,13 +604,12 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(ModelDev m, DecodeArgs
           }
         }
       }
-      if (P > 1) team_arrive(counter, a.fences);
     }
   }
+  if (P > 1) team_arrive(counter, a.fences);  // the -1 tokens and pass 0 are in place before any wait
   // Inputs of a pass that no other workgroup writes come from its step
   // records: one 16-byte slice per thread, loaded during the previous pass's
-  // logits and written to LDS once that pass is done with its copies (between
-  // the team barrier's arrive and wait).
+  // logits and written to LDS once that pass is done with its copies.
   const float4* rec = a.rec + qo * (size_t)L * kRecFloat4;
   auto members = [&](int ps, int& s0) -> int {  // members of this rank in pass ps: rank + P i
     s0 = pstart[ps];
@@ -624,9 +654,8 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(ModelDev m, DecodeArgs
 #pragma unroll
     for (int q = 0; q < kRecRounds; ++q) rec_store(ml, rec_load(s0, ml, q), q);
   }
-  if (P > 1 && pstart[1] > pstart[0]) {  // the pass-0 barrier
-    if (!team_wait(counter, ++passes * P, a.spin_limit, a.fault, &bad, a.fences)) goto finish;
-  }
+  if (P > 1 && !team_wait(counter, P, a.spin_limit, a.fault, &bad, a.fences)) goto finish;  // pass 0
+  __builtin_amdgcn_s_waitcnt(0);  // one workgroup per sequence: its own pass-0 stores are complete
   __syncthreads();
   for (int pass = 1; pass <= npass; ++pass) {
     if (ml > G) {  // a schedule built for a larger team: refuse rather than overrun LDS
@@ -641,17 +670,20 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(ModelDev m, DecodeArgs
     for (int q = 0; q < kRecRounds; ++q) rv[q] = make_float4(0.F, 0.F, 0.F, 0.F);
     bool staged = false;
     if (ml > 0) {
-      if ((PREC == kPrecFp32 || X3) && a.l0tab) {
-        // layer-0 table row of each slot, from the token of a neighbour decoded
-        // before the step (written by the team before the last barrier)
-        int tid = threadIdx.x;
-        asm volatile("" : "+v"(tid));  // keeps these addresses out of loop-invariant (spilled) registers
-        static_assert(G * kKmax <= kThreads, "one slot per thread");
-        if (tid < ml * kKmax && tid % kKmax < K) {
-          const int i = tid / kKmax, k = tid % kKmax;
-          const int wd = nbw[tid];
-          const bool bw = wd >= 0 && (wd & 0x40000000) != 0;
-          const int tok = bw ? load_dev(tokens + (wd & 0x3FFFFFFF)) : kV;
+      // Wait for the tokens of the members' earlier neighbours (their steps ran
+      // in earlier passes, on any workgroup of the team; their R rows are then
+      // complete), and with the layer-0 table pick each slot's table row from
+      // the neighbour's token.
+      constexpr bool kTab = PREC == kPrecFp32 || X3;
+      int tid = threadIdx.x;
+      asm volatile("" : "+v"(tid));  // keeps these addresses out of loop-invariant (spilled) registers
+      static_assert(G * kKmax <= kThreads, "one slot per thread");
+      if (tid < ml * kKmax && tid % kKmax < K) {
+        const int i = tid / kKmax, k = tid % kKmax;
+        const int wd = nbw[tid];
+        const bool bw = wd >= 0 && (wd & 0x40000000) != 0;
+        const int tok = bw ? await_token(tokens + (wd & 0x3FFFFFFF), a.spin_limit, a.fault, &bad, a.fences) : kV;
+        if (kTab && a.l0tab) {
           const int4 m2 = meta2[i];
           if (a.l0base) {  // compact: kV rows for each earlier backward slot, one for any other
             const uint64_t before = ((uint64_t)(uint32_t)m2.x | ((uint64_t)(uint32_t)m2.y << 32)) & ((1ull << k) - 1);
@@ -660,7 +692,10 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(ModelDev m, DecodeArgs
             cls[tid] = m2.z + k * kL0Classes + tok;
           }
         }
-        __syncthreads();
+      }
+      __syncthreads();
+      if (bad) break;
+      if (kTab && a.l0tab) {
         // x[i] = sum over slots of table rows, in the order of the MFMA path
         // below: lane group g (rows 16 mb + 4 g + e, mb outer) sums its rows,
         // then the four groups add as (g0 + g1) + (g2 + g3).
@@ -1190,10 +1225,7 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(ModelDev m, DecodeArgs
         const int tok = __int_as_float(mt.z) == 0.0F ? mt.w : s_tok;
         if (lp_out && lane < kV) lp_out[(size_t)t * kV + lane] = lpv;
         if (lane == tok) store_dev(chosen + t, lpv);
-        if (lane == 0) {
-          store_dev(tokens + t, tok);
-          tok_s[i] = tok;
-        }
+        if (lane == 0) tok_s[i] = tok;
       }
       __syncthreads();
       if constexpr (H16) {  // fp16 rows, two columns per device-scope store
@@ -1212,20 +1244,38 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(ModelDev m, DecodeArgs
           store_dev(R + ((size_t)l * L + t) * kH + c, base + m.dec[l].T[tok_s[i] * kH + c]);
         }
       }
+      // The tokens last: every wave's R-row stores have completed at the device
+      // coherence point before a member's token is stored (await_token).
+      __builtin_amdgcn_s_waitcnt(0);
+      __syncthreads();
+      if (threadIdx.x < ml) {
+        if (a.fences) __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+        store_dev(tokens + meta[threadIdx.x].x, tok_s[threadIdx.x]);
+      }
     }
     if (!staged)
 #pragma unroll
       for (int q = 0; q < kRecRounds; ++q) rv[q] = rec_load(s0n, mln, q);
-    // this pass's LDS state is consumed (team_arrive starts with a barrier)
-    if (P > 1)
-      team_arrive(counter, a.fences);
-    else
-      __syncthreads();
+    __syncthreads();  // this pass's LDS state is consumed
 #pragma unroll
     for (int q = 0; q < kRecRounds; ++q) rec_store(mln, rv[q], q);
     ml = mln;
-    if (P > 1 && !team_wait(counter, ++passes * P, a.spin_limit, a.fault, &bad, a.fences)) break;
     __syncthreads();
+  }
+  // The chosen log-probs of every member are in place before rank 0 sums them;
+  // a workgroup that stopped early marks the count so that rank 0 leaves a NaN score.
+  if (P > 1) {
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    if (threadIdx.x == 0) {
+      if (a.fences) __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+      __hip_atomic_fetch_add(counter, bad ? 1u + kTeamAbort : 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    if (rank == 0 && !bad) {
+      if (!team_wait(counter, 2 * P, a.spin_limit, a.fault, &bad, a.fences)) goto finish;
+      if (threadIdx.x == 0 && __hip_atomic_load(counter, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) >= kTeamAbort) bad = 1;
+      __syncthreads();
+    }
   }
 finish:
   // Mean NLL over designed residues in residue order (inverse_fold_scalar.cpp:471-493).
