@@ -406,16 +406,18 @@ __device__ inline int await_token(const int32_t* tok, uint32_t spin_limit, uint3
 constexpr uint32_t kTeamAbort = 1u << 24;
 
 // Decodes one sequence per team of P workgroups (P = a.team, 1..8) in the
-// passes of the dependency schedule (dag_schedule_kernel): a pass holds up to
-// a.max_members (<= kGroup * P) steps whose earlier kNN neighbours were all
+// passes of the dependency schedule (ready_schedule_kernel): a pass holds up to
+// a.max_members (<= G * P) steps whose earlier kNN neighbours were all
 // decoded in earlier passes, so each step sees the inputs of sequential
 // decoding (bw = the neighbour's position is before the step's own). Member i
 // of a pass runs on team rank i % P; a rank with several members shares each
-// weight load and barrier between them. A step's token comes from draw
-// a.draw[u] of the sequence's counter stream, i.e. draws are consumed in order
-// of u whatever pass decodes the step. The state a later pass reads (R rows,
-// chosen log-probs) is written with device-scope stores and published by a
-// team barrier at the end of each pass. Pass 0 (inactive residues: fallback
+// weight load and workgroup barrier between them. A step's token comes from
+// draw a.draw[u] of the sequence's counter stream, i.e. draws are consumed in
+// order of u whatever pass decodes the step. The state a later pass reads (R
+// rows, tokens) is written with device-scope stores; a step's token is stored
+// after its R rows have completed, and a pass starts by waiting for the tokens
+// of its steps' earlier neighbours (await_token), so the ranks of a team meet
+// only after pass 0 and before the score. Pass 0 (inactive residues: fallback
 // token, zero log-probs, no draw) runs first, on rank 0.
 // With P > 1 the grid is 8 * ceil(B / 8) * P workgroups and rank r of
 // sequence b runs as workgroup 8 (P (b / 8) + r) + b % 8, so that a team
