@@ -28,7 +28,14 @@ HOST_FLAGS = ["-ffp-contract=off"]
 # The decode kernel keeps many loop-invariant values across its pass loop; sinking
 # them back into the loop where that avoids spills leaves registers for the weight
 # loads in flight.
-DEVICE_FLAGS = {"decoder.hip": ["-mllvm", "-sink-insts-to-avoid-spills"]}
+# The reference-order encoder adds matrix-core products to its accumulators on
+# the VALU; the products have to land in ordinary VGPRs (not AGPRs, which would
+# cost a copy per product).
+DEVICE_FLAGS = {
+    "decoder.hip": ["-mllvm", "-sink-insts-to-avoid-spills"],
+    "encoder.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"],
+    "features.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"],
+}
 
 
 def source_flags(src: str) -> list:

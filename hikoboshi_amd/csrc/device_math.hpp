@@ -224,24 +224,48 @@ __device__ inline void store_acc(const floatx4 (&acc)[MB][NB], float* C, int ldc
 // before the add (no FMA), then adds the bias
 // (cpp/primitives/linalg/gemm_scalar_fast.cpp:107-176,249-314;
 // cpp/include/hikoboshi/modules/mpnn/detail/mpnn_inner_inline.hpp:319-339).
-// seq_gemm reproduces that rounding bit for bit: each thread owns an RM x CN
-// block of outputs and walks k in order; parallelism comes from the outputs.
+// seq_gemm_mfma reproduces that rounding bit for bit with the products on the
+// matrix cores: for each k, v_mfma_f32_16x16x1_4b_f32 forms the outer product
+// of a column of A (16 rows) and a row of W (64 columns) with a zero addend,
+// i.e. every product rounded once to fp32 as the VALU multiply rounds it, and
+// the VALU adds it to the accumulators in k order, so each output is one
+// sequential float sum of rounded products (one VALU add per product instead
+// of a multiply and an add). The matrix cores flush products below 2^-126 to
+// zero where the VALU keeps IEEE subnormals: such a term could change a sum
+// only if all of the sum's terms were below about 2^-100. In the encoder every
+// product has a weight of at least 3.7e-8 in magnitude or zero (the v_48_020
+// package's smallest) and an input that is zero or at least about 1e-9 (GELU
+// outputs, LayerNorm outputs, RBF features of at least exp(-16)), so no
+// product is subnormal.
 //   A   : LDS, k-major: A[k * lda + row].
-//   W   : global, transposed weights W[k * ldw + col] (col < NC).
+//   W   : global, transposed weights W[k * ldw + col] (col < NC); kd (the rows
+//         used) a multiple of 4.
 //   Wbuf: LDS staging, 2 x KC x NC floats: chunk c + 1 of the weights is
 //         loaded into registers while chunk c is used, then stored to the
 //         other half.
-// The thread's block is rows [r0, r0 + RM), cols [c0, c0 + CN). Every thread
-// of the 256-thread block must call it (it contains barriers); it starts and
-// ends with a barrier, so LDS writes made before the call are visible and A
-// may be overwritten after it.
-template <int RM, int CN, int NC, int KC>
-__device__ inline void seq_gemm(float (&acc)[RM][CN], const float* A, int lda, int r0,
-                                const float* __restrict__ W, int ldw, int kd, float* Wbuf, int c0) {
+// Every wave owns a 16 x 64 block of outputs at rows [rb, rb + 16), columns
+// [cb, cb + 64); accumulator v of lane l is output row mfma_row(rb, v),
+// column mfma_col(cb, v) (the instruction's lane layout on gfx950: block
+// v / 4, row 4 (l / 16) + v % 4, column l % 16 of that block). The k loop runs
+// in groups of four: a group's four products are issued before the next
+// group's LDS operands are read, and both are in flight while the group's 64
+// adds run. Every thread of the 256-thread block must call it (it contains
+// barriers); it starts and ends with a barrier, so LDS writes made before the
+// call are visible and A may be overwritten after it.
+typedef float floatx16 __attribute__((ext_vector_type(16)));
+__device__ inline int mfma_row(int rb, int v) { return rb + 4 * ((threadIdx.x & 63) >> 4) + (v & 3); }
+__device__ inline int mfma_col(int cb, int v) { return cb + 16 * (v >> 2) + (threadIdx.x & 15); }
+
+template <int NC, int KC>
+__device__ inline void seq_gemm_mfma(float (&acc)[16], const float* A, int lda, int rb,
+                                     const float* __restrict__ W, int ldw, int kd, float* Wbuf, int cb) {
 #pragma clang fp contract(off)
   constexpr int kBlock = 256;
   constexpr int V = KC * (NC / 4);  // float4 per chunk
   constexpr int PT = (V + kBlock - 1) / kBlock;
+  static_assert(NC % 64 == 0 && KC % 4 == 0, "64-column wave blocks, k groups of four");
+  __builtin_assume(kd % 4 == 0 && kd > 0);
+  const int lane = threadIdx.x & 63;
   float4 stage[PT];
   const int nchunks = (kd + KC - 1) / KC;
 #pragma unroll
@@ -258,6 +282,7 @@ __device__ inline void seq_gemm(float (&acc)[RM][CN], const float* A, int lda, i
     if (i < V) *reinterpret_cast<float4*>(Wbuf + i * 4) = stage[p];
   }
   __syncthreads();
+  const floatx16 zero = {};
   for (int c = 0; c < nchunks; ++c) {
     const int k0 = c * KC;
     const bool more = c + 1 < nchunks;
@@ -273,33 +298,31 @@ __device__ inline void seq_gemm(float (&acc)[RM][CN], const float* A, int lda, i
     }
     const float* Wc = Wbuf + (c & 1) * (KC * NC);
     const int kn = (kd - k0) < KC ? (kd - k0) : KC;
-    for (int kk = 0; kk < kn; ++kk) {
-      float a[RM];
-      float w[CN];
-      const float* ap = A + (size_t)(k0 + kk) * lda + r0;
-      if constexpr (RM % 4 == 0) {
+    const float* ap = A + (size_t)k0 * lda + rb + (lane & 15);
+    const float* wp = Wc + cb + lane;
+    // kd is a multiple of 4 (every caller's), so every group of four k is whole
+    float a[4], b[4];
 #pragma unroll
-        for (int i = 0; i < RM; i += 4) {
-          const float4 v = *reinterpret_cast<const float4*>(ap + i);
-          a[i] = v.x; a[i + 1] = v.y; a[i + 2] = v.z; a[i + 3] = v.w;
-        }
-      } else {
+    for (int j = 0; j < 4; ++j) {
+      a[j] = ap[(size_t)j * lda];
+      b[j] = wp[j * NC];
+    }
+#pragma unroll 1
+    for (int kk = 0; kk < kn; kk += 4) {
+      floatx16 p[4];
 #pragma unroll
-        for (int i = 0; i < RM; i += 2) {
-          const float2 v = *reinterpret_cast<const float2*>(ap + i);
-          a[i] = v.x; a[i + 1] = v.y;
+      for (int j = 0; j < 4; ++j) p[j] = __builtin_amdgcn_mfma_f32_16x16x1f32(a[j], b[j], zero, 0, 0, 0);
+      if (kk + 4 < kn) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          a[j] = ap[(size_t)(kk + 4 + j) * lda];
+          b[j] = wp[(kk + 4 + j) * NC];
         }
       }
-      const float* wp = Wc + kk * NC + c0;
 #pragma unroll
-      for (int j = 0; j < CN; j += 4) {
-        const float4 v = *reinterpret_cast<const float4*>(wp + j);
-        w[j] = v.x; w[j + 1] = v.y; w[j + 2] = v.z; w[j + 3] = v.w;
-      }
+      for (int j = 0; j < 4; ++j)
 #pragma unroll
-      for (int i = 0; i < RM; ++i)
-#pragma unroll
-        for (int j = 0; j < CN; ++j) acc[i][j] = acc[i][j] + a[i] * w[j];
+        for (int v = 0; v < 16; ++v) acc[v] = acc[v] + p[j][v];
     }
     if (more) {
       float* Wn = Wbuf + ((c + 1) & 1) * (KC * NC);

@@ -10,7 +10,7 @@
 // The encoder runs once per backbone and its outputs feed every sequence,
 // and its rounding dominates the log-prob deviation at design temperatures,
 // so every product here reproduces the reference bit for bit: sequential
-// k-order sums without FMA (seq_gemm), Welford LayerNorm, the same
+// k-order sums of rounded products (seq_gemm_mfma), Welford LayerNorm, the same
 // elementwise order. The only reuse is exact: the first 128 terms of the
 // W1 / W11 sums ([h_i] part) are the same prefix for all K edges of residue
 // i, so the node kernel computes that prefix once per residue and the edge
@@ -36,8 +36,6 @@ namespace {
 
 constexpr int kRows = 32;    // edge rows per tile (any rows of the [L * K] edge list)
 constexpr int kLdE = 36;     // k-major leading dimension of edge tiles
-constexpr int kEdgeRM = 4;   // rows per thread (8 row groups)
-constexpr int kEdgeCN = 4;   // cols per thread (32 col groups)
 constexpr int kKC = 32;      // weight rows staged per chunk
 
 // Loads rows of a [*, 128] row-major matrix into a k-major LDS tile
@@ -59,7 +57,8 @@ __device__ inline void load_kmajor(float* A, int lda, int n_tile_rows, RowFn row
 
 // Edge messages m_ij = W3 GELU(W2 GELU(W1 [h_i, e_ij, h_j] + b1) + b2) + b3 for
 // a tile of kRows consecutive edge rows; the neighbour sum is taken in order
-// by node_kernel.
+// by node_kernel. The products run on the matrix cores (seq_gemm_mfma): wave w
+// owns rows [16 (w % 2), + 16) and columns [64 (w / 2), + 64) of the tile.
 __global__ __launch_bounds__(256) void edge_msg_kernel(EncLayerDev w, const float* __restrict__ h_e,
                                                        const float* __restrict__ h_v, const int32_t* __restrict__ idx,
                                                        const float* __restrict__ prefix, int L, int K,
@@ -72,48 +71,44 @@ __global__ __launch_bounds__(256) void edge_msg_kernel(EncLayerDev w, const floa
   const size_t S = (size_t)L * K;
   const size_t slot0 = (size_t)blockIdx.x * kRows;
   const int n_rows = (int)min((size_t)kRows, S - slot0);
-  const int rg = threadIdx.x / 32, cg = threadIdx.x % 32;
-  const int row0 = rg * kEdgeRM, col0 = cg * kEdgeCN;
+  const int wave = threadIdx.x >> 6;
+  const int rb = 16 * (wave & 1), cb = 64 * (wave >> 1);
 
-  float acc[kEdgeRM][kEdgeCN];
+  float acc[16];
 #pragma unroll
-  for (int i = 0; i < kEdgeRM; ++i) {
-    const int row = row0 + i;
-    const float* pre = row < n_rows ? prefix + ((slot0 + row) / K) * 256 + 128 : nullptr;
-#pragma unroll
-    for (int j = 0; j < kEdgeCN; ++j) acc[i][j] = pre ? pre[col0 + j] : 0.0F;
+  for (int v = 0; v < 16; ++v) {
+    const int row = mfma_row(rb, v);
+    acc[v] = row < n_rows ? prefix[((slot0 + row) / K) * 256 + 128 + mfma_col(cb, v)] : 0.0F;
   }
   load_kmajor(A, kLdE, kRows, [&](int row) -> const float* {
     return row < n_rows ? h_e + (slot0 + row) * kH : nullptr;
   });
-  seq_gemm<kEdgeRM, kEdgeCN, kH, kKC>(acc, A, kLdE, row0, w.W1_t + 128 * kH, kH, kH, Wbuf, col0);
+  seq_gemm_mfma<kH, kKC>(acc, A, kLdE, rb, w.W1_t + 128 * kH, kH, kH, Wbuf, cb);
   load_kmajor(A, kLdE, kRows, [&](int row) -> const float* {
     if (row >= n_rows) return nullptr;
     const int j = idx[slot0 + row];
     return (j >= 0 && j < L) ? h_v + (size_t)j * kH : nullptr;
   });
-  seq_gemm<kEdgeRM, kEdgeCN, kH, kKC>(acc, A, kLdE, row0, w.W1_t + 256 * kH, kH, kH, Wbuf, col0);
+  seq_gemm_mfma<kH, kKC>(acc, A, kLdE, rb, w.W1_t + 256 * kH, kH, kH, Wbuf, cb);
 #pragma unroll
-  for (int i = 0; i < kEdgeRM; ++i)
+  for (int v = 0; v < 16; ++v) {
+    const int row = mfma_row(rb, v), c = mfma_col(cb, v);
+    A[c * kLdE + row] = row < n_rows ? gelu(acc[v] + w.b1[c], tbl) : 0.0F;
+    acc[v] = 0.0F;
+  }
+  seq_gemm_mfma<kH, kKC>(acc, A, kLdE, rb, w.W2_t, kH, kH, Wbuf, cb);
 #pragma unroll
-    for (int j = 0; j < kEdgeCN; ++j) {
-      A[(col0 + j) * kLdE + row0 + i] = (row0 + i < n_rows) ? gelu(acc[i][j] + w.b1[col0 + j], tbl) : 0.0F;
-      acc[i][j] = 0.0F;
-    }
-  seq_gemm<kEdgeRM, kEdgeCN, kH, kKC>(acc, A, kLdE, row0, w.W2_t, kH, kH, Wbuf, col0);
+  for (int v = 0; v < 16; ++v) {
+    const int row = mfma_row(rb, v), c = mfma_col(cb, v);
+    A[c * kLdE + row] = row < n_rows ? gelu(acc[v] + w.b2[c], tbl) : 0.0F;
+    acc[v] = 0.0F;
+  }
+  seq_gemm_mfma<kH, kKC>(acc, A, kLdE, rb, w.W3_t, kH, kH, Wbuf, cb);
 #pragma unroll
-  for (int i = 0; i < kEdgeRM; ++i)
-#pragma unroll
-    for (int j = 0; j < kEdgeCN; ++j) {
-      A[(col0 + j) * kLdE + row0 + i] = (row0 + i < n_rows) ? gelu(acc[i][j] + w.b2[col0 + j], tbl) : 0.0F;
-      acc[i][j] = 0.0F;
-    }
-  seq_gemm<kEdgeRM, kEdgeCN, kH, kKC>(acc, A, kLdE, row0, w.W3_t, kH, kH, Wbuf, col0);
-#pragma unroll
-  for (int i = 0; i < kEdgeRM; ++i)
-    if (row0 + i < n_rows)
-#pragma unroll
-      for (int j = 0; j < kEdgeCN; ++j) msg[(slot0 + row0 + i) * kH + col0 + j] = acc[i][j] + w.b3[col0 + j];
+  for (int v = 0; v < 16; ++v) {
+    const int row = mfma_row(rb, v), c = mfma_col(cb, v);
+    if (row < n_rows) msg[(slot0 + row) * kH + c] = acc[v] + w.b3[c];
+  }
 }
 
 // The weights of the node update stream through the workgroup as 40 chunks
@@ -373,51 +368,45 @@ __global__ __launch_bounds__(256) void edge_update_kernel(EncLayerDev w, float* 
   const size_t S = (size_t)L * K;
   const size_t slot0 = (size_t)blockIdx.x * kRows;
   const int n_rows = (int)min((size_t)kRows, S - slot0);
-  const int rg = threadIdx.x / 32, cg = threadIdx.x % 32;
-  const int row0 = rg * kEdgeRM, col0 = cg * kEdgeCN;
+  const int wave = threadIdx.x >> 6;
+  const int rb = 16 * (wave & 1), cb = 64 * (wave >> 1);  // this wave's block (seq_gemm_mfma)
 
-  float acc[kEdgeRM][kEdgeCN];
+  float acc[16];
 #pragma unroll
-  for (int i = 0; i < kEdgeRM; ++i) {
-    const int row = row0 + i;
-    const float* pre = row < n_rows ? prefix + ((slot0 + row) / K) * 256 : nullptr;
-#pragma unroll
-    for (int j = 0; j < kEdgeCN; ++j) acc[i][j] = pre ? pre[col0 + j] : 0.0F;
+  for (int v = 0; v < 16; ++v) {
+    const int row = mfma_row(rb, v);
+    acc[v] = row < n_rows ? prefix[((slot0 + row) / K) * 256 + mfma_col(cb, v)] : 0.0F;
   }
   load_kmajor(A, kLdE, kRows, [&](int row) -> const float* {
     return row < n_rows ? h_e + (slot0 + row) * kH : nullptr;
   });
-  seq_gemm<kEdgeRM, kEdgeCN, kH, kKC>(acc, A, kLdE, row0, w.W11_t + 128 * kH, kH, kH, Wbuf, col0);
+  seq_gemm_mfma<kH, kKC>(acc, A, kLdE, rb, w.W11_t + 128 * kH, kH, kH, Wbuf, cb);
   load_kmajor(A, kLdE, kRows, [&](int row) -> const float* {
     if (row >= n_rows) return nullptr;
     const int j = idx[slot0 + row];
     return (j >= 0 && j < L) ? h_v + (size_t)j * kH : nullptr;
   });
-  seq_gemm<kEdgeRM, kEdgeCN, kH, kKC>(acc, A, kLdE, row0, w.W11_t + 256 * kH, kH, kH, Wbuf, col0);
+  seq_gemm_mfma<kH, kKC>(acc, A, kLdE, rb, w.W11_t + 256 * kH, kH, kH, Wbuf, cb);
 #pragma unroll
-  for (int i = 0; i < kEdgeRM; ++i)
+  for (int v = 0; v < 16; ++v) {
+    const int row = mfma_row(rb, v), c = mfma_col(cb, v);
+    A[c * kLdE + row] = row < n_rows ? gelu(acc[v] + w.b11[c], tbl) : 0.0F;
+    acc[v] = 0.0F;
+  }
+  seq_gemm_mfma<kH, kKC>(acc, A, kLdE, rb, w.W12_t, kH, kH, Wbuf, cb);
 #pragma unroll
-    for (int j = 0; j < kEdgeCN; ++j) {
-      A[(col0 + j) * kLdE + row0 + i] = (row0 + i < n_rows) ? gelu(acc[i][j] + w.b11[col0 + j], tbl) : 0.0F;
-      acc[i][j] = 0.0F;
-    }
-  seq_gemm<kEdgeRM, kEdgeCN, kH, kKC>(acc, A, kLdE, row0, w.W12_t, kH, kH, Wbuf, col0);
-#pragma unroll
-  for (int i = 0; i < kEdgeRM; ++i)
-#pragma unroll
-    for (int j = 0; j < kEdgeCN; ++j) {
-      A[(col0 + j) * kLdE + row0 + i] = (row0 + i < n_rows) ? gelu(acc[i][j] + w.b12[col0 + j], tbl) : 0.0F;
-      acc[i][j] = 0.0F;
-    }
-  seq_gemm<kEdgeRM, kEdgeCN, kH, kKC>(acc, A, kLdE, row0, w.W13_t, kH, kH, Wbuf, col0);
+  for (int v = 0; v < 16; ++v) {
+    const int row = mfma_row(rb, v), c = mfma_col(cb, v);
+    A[c * kLdE + row] = row < n_rows ? gelu(acc[v] + w.b12[c], tbl) : 0.0F;
+    acc[v] = 0.0F;
+  }
+  seq_gemm_mfma<kH, kKC>(acc, A, kLdE, rb, w.W13_t, kH, kH, Wbuf, cb);
   // x = 1 * e + m  (axpy order), then LN3 per valid row
 #pragma unroll
-  for (int i = 0; i < kEdgeRM; ++i)
-#pragma unroll
-    for (int j = 0; j < kEdgeCN; ++j) {
-      const int row = row0 + i, c = col0 + j;
-      A[c * kLdE + row] = (row < n_rows) ? h_e[(slot0 + row) * kH + c] + (acc[i][j] + w.b13[c]) : 0.0F;
-    }
+  for (int v = 0; v < 16; ++v) {
+    const int row = mfma_row(rb, v), c = mfma_col(cb, v);
+    A[c * kLdE + row] = (row < n_rows) ? h_e[(slot0 + row) * kH + c] + (acc[v] + w.b13[c]) : 0.0F;
+  }
   __shared__ float ln_stat[2 * kRows];
   __shared__ int row_ok[kRows];
   if (threadIdx.x < kRows) {

@@ -69,52 +69,40 @@ __global__ __launch_bounds__(256) void edge_embed_kernel(ModelDev m, const float
   __syncthreads();
   const size_t S = (size_t)L * K;
   const size_t slot0 = (size_t)blockIdx.x * kTile;
-  const int rg = threadIdx.x / 32, cg = threadIdx.x % 32;
-  const int row0 = rg * 4, col0 = cg * 4;
+  const int wave = threadIdx.x >> 6;
+  const int rb = 16 * (wave & 1), cb = 64 * (wave >> 1);  // this wave's block (seq_gemm_mfma)
   const int frow = threadIdx.x % kTile, fchunk = threadIdx.x / kTile;
   const size_t fslot = slot0 + frow;
   const int fr = fslot < S ? static_cast<int>(fslot / K) : 0;
   const int fj = fslot < S ? idx[fslot] : -1;
 
-  float acc[4][4];
+  float acc[16];
 #pragma unroll
-  for (int i = 0; i < 4; ++i)
-#pragma unroll
-    for (int j = 0; j < 4; ++j) acc[i][j] = 0.0F;
+  for (int v = 0; v < 16; ++v) acc[v] = 0.0F;
   for (int c0 = 0; c0 < 26; c0 += kGroupChunks) {
     const int nc = min(kGroupChunks, 26 - c0);
-    // A is free here: seq_gemm ends with a barrier
+    // A is free here: seq_gemm_mfma ends with a barrier
     if (fchunk < nc) {
       float out[16];
       edge_chunk(m, coords, src, resid, chain, L, fr, fj, c0 + fchunk, out, tbl);  // zeros when fj is not a residue
 #pragma unroll
       for (int f = 0; f < 16; ++f) A[(fchunk * 16 + f) * kLdT + frow] = out[f];
     }
-    seq_gemm<4, 4, kH, 32>(acc, A, kLdT, row0, m.edge_t + (size_t)c0 * 16 * kH, kH, nc * 16, Wbuf, col0);
+    seq_gemm_mfma<kH, 32>(acc, A, kLdT, rb, m.edge_t + (size_t)c0 * 16 * kH, kH, nc * 16, Wbuf, cb);
   }
   float* X = A;
 #pragma unroll
-  for (int i = 0; i < 4; ++i)
-#pragma unroll
-    for (int j = 0; j < 4; ++j) X[(col0 + j) * kLdT + row0 + i] = acc[i][j];
+  for (int v = 0; v < 16; ++v) X[mfma_col(cb, v) * kLdT + mfma_row(rb, v)] = acc[v];
   __shared__ float ln_stat[2 * kTile];
   ln_cols_block(X, A, kLdT, kTile, m.ne_g, m.ne_b, ln_stat, [](int) { return true; });
 #pragma unroll
-  for (int i = 0; i < 4; ++i)
+  for (int v = 0; v < 16; ++v) acc[v] = 0.0F;
+  seq_gemm_mfma<kH, 32>(acc, A, kLdT, rb, m.We_t, kH, kH, Wbuf, cb);
 #pragma unroll
-    for (int j = 0; j < 4; ++j) acc[i][j] = 0.0F;
-  seq_gemm<4, 4, kH, 32>(acc, A, kLdT, row0, m.We_t, kH, kH, Wbuf, col0);
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const size_t slot = slot0 + row0 + i;
-    if (slot < S) {
-      float4 v;
-      v.x = acc[i][0] + m.We_b[col0 + 0];
-      v.y = acc[i][1] + m.We_b[col0 + 1];
-      v.z = acc[i][2] + m.We_b[col0 + 2];
-      v.w = acc[i][3] + m.We_b[col0 + 3];
-      *reinterpret_cast<float4*>(h_e + slot * kH + col0) = v;
-    }
+  for (int v = 0; v < 16; ++v) {
+    const size_t slot = slot0 + mfma_row(rb, v);
+    const int c = mfma_col(cb, v);
+    if (slot < S) h_e[slot * kH + c] = acc[v] + m.We_b[c];
   }
 }
 

@@ -15,9 +15,11 @@
 //   ulp(gelu(x)) + |x| 2^-25  (one ulp of the result plus half an x-scaled step
 //                              of the float grid under 1 that mag = 1 - P is
 //                              rounded to)
-// is reported, with the same figure for gelu_fast for comparison. Test
-// infrastructure only: built into tests/libdevice_math_check.so and called by
-// tests/test_gpu_device_math.py.
+// is reported, with the same figure for gelu_fast for comparison. A further
+// kernel checks seq_gemm_mfma (the encoder's reference-order sums with the
+// products on the matrix cores) against the same sums formed on the VALU, bit
+// for bit. Test infrastructure only: built into tests/libdevice_math_check.so
+// and called by tests/test_gpu_device_math.py.
 #include <hip/hip_runtime.h>
 
 #include <cstdint>
@@ -206,7 +208,79 @@ __global__ void rbf_kernel(unsigned int n, unsigned int* out) {
   atomicAdd(&out[2], cut);
 }
 
+// seq_gemm_mfma against the reference's sequential sums on the VALU (a product
+// rounded, then added, k in order, starting from the initial accumulator): one
+// 32 x 128 output tile with kd = 128 per workgroup, random operands from a
+// counter hash. Operand magnitudes span 2^-40 .. 2^12 (A) and 2^-30 .. 2^2 (W)
+// with random signs and about 1/16 exact zeros, so every product is a normal
+// float or zero, as in the encoder; the initial accumulators are random too.
+// out[0] counts outputs whose bits differ, out[1..3] = the first one's block,
+// row * 128 + col and (MFMA bits) for the report.
+__device__ inline uint32_t mix32(uint64_t x) {
+  x += 0x9E3779B97F4A7C15ull;
+  x = (x ^ (x >> 30)) * 0xBF58476D1CE4E5B9ull;
+  x = (x ^ (x >> 27)) * 0x94D049BB133111EBull;
+  return static_cast<uint32_t>(x ^ (x >> 31));
+}
+__device__ inline float rand_operand(uint64_t key, int lo_exp, int span) {
+  const uint32_t r = mix32(key);
+  if ((r & 15u) == 0u) return 0.0F;
+  const uint32_t e = static_cast<uint32_t>(127 + lo_exp + (int)((r >> 4) % (uint32_t)span));
+  return __uint_as_float(((r >> 31) << 31) | (e << 23) | (mix32(key ^ 0x5555ull) & 0x7FFFFFu));
+}
+constexpr int kGemmLd = 36;
+__global__ __launch_bounds__(256) void seq_gemm_check_kernel(float* __restrict__ W, unsigned int* out) {
+#pragma clang fp contract(off)
+  __shared__ __attribute__((aligned(16))) float A[128 * kGemmLd];
+  __shared__ __attribute__((aligned(16))) float Wbuf[2 * 32 * 128];
+  const uint64_t base = static_cast<uint64_t>(blockIdx.x) << 32;
+  float* Wb = W + static_cast<size_t>(blockIdx.x) * 128 * 128;
+  for (int i = threadIdx.x; i < 128 * 32; i += 256) A[(i / 32) * kGemmLd + i % 32] = rand_operand(base + i, -40, 52);
+  for (int i = threadIdx.x; i < 128 * 128; i += 256) Wb[i] = rand_operand(base + 0x10000 + i, -30, 32);
+  __threadfence();
+  __syncthreads();
+  const int wave = threadIdx.x >> 6;
+  const int rb = 16 * (wave & 1), cb = 64 * (wave >> 1);
+  float acc[16], ref[16];
+#pragma unroll
+  for (int v = 0; v < 16; ++v) {
+    acc[v] = rand_operand(base + 0x20000 + hkbs::mfma_row(rb, v) * 128 + hkbs::mfma_col(cb, v), -10, 14);
+    ref[v] = acc[v];
+  }
+  hkbs::seq_gemm_mfma<128, 32>(acc, A, kGemmLd, rb, Wb, 128, 128, Wbuf, cb);
+#pragma unroll
+  for (int v = 0; v < 16; ++v) {
+    const int row = hkbs::mfma_row(rb, v), col = hkbs::mfma_col(cb, v);
+    for (int k = 0; k < 128; ++k) ref[v] = ref[v] + A[k * kGemmLd + row] * Wb[k * 128 + col];
+    if (__float_as_uint(ref[v]) != __float_as_uint(acc[v])) {
+      if (atomicAdd(&out[0], 1u) == 0u) {
+        out[1] = blockIdx.x;
+        out[2] = static_cast<unsigned int>(row * 128 + col);
+        out[3] = __float_as_uint(acc[v]);
+      }
+    }
+  }
+}
+
 }  // namespace
+
+// Runs seq_gemm_check_kernel on `blocks` tiles on the current device; out[4] as there.
+extern "C" int hkbs_check_device_seq_gemm(unsigned int blocks, unsigned int* out_host) {
+  unsigned int* out = nullptr;
+  float* W = nullptr;
+  hipError_t e = hipMalloc(&out, 4 * sizeof(unsigned int));
+  if (e == hipSuccess) e = hipMalloc(&W, static_cast<size_t>(blocks) * 128 * 128 * sizeof(float));
+  if (e == hipSuccess) e = hipMemset(out, 0, 4 * sizeof(unsigned int));
+  if (e == hipSuccess) {
+    seq_gemm_check_kernel<<<blocks, 256>>>(W, out);
+    e = hipGetLastError();
+  }
+  if (e == hipSuccess) e = hipDeviceSynchronize();
+  if (e == hipSuccess) e = hipMemcpy(out_host, out, 4 * sizeof(unsigned int), hipMemcpyDeviceToHost);
+  if (W) (void)hipFree(W);
+  if (out) (void)hipFree(out);
+  return static_cast<int>(e);
+}
 
 // Runs rbf_kernel over n offsets on the current device; out[3] as there.
 extern "C" int hkbs_check_device_rbf(unsigned int n, unsigned int* out_host) {

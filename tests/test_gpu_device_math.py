@@ -9,7 +9,9 @@ the 2^32 float inputs; the encoder tests then pin the straightforward form
 against the oracle. The decode loop's gelu_poly takes the A&S term from
 per-segment polynomials: on every finite input it must stay within
 POLY_UNITS units of ulp(gelu(x)) + |x| 2^-25 of gelu (the bit-exact reference
-form), and agree bit for bit on infinities and NaNs.
+form), and agree bit for bit on infinities and NaNs. The encoder's sums with the products
+on the matrix cores (seq_gemm_mfma) must equal the same sums on the VALU bit
+for bit.
 """
 import ctypes as C
 import struct
@@ -63,3 +65,18 @@ def test_device_rbf_fused_form():
           flush=True)
     assert rel <= 5e-6
     assert dabs <= 5e-6
+
+
+def test_device_matrix_core_products_are_sequential_sums():
+    """seq_gemm_mfma (the encoder's reference-order sums, products from v_mfma_f32_16x16x1_4b_f32 with a zero
+    addend) against the same sums on the VALU (product rounded, added in k order) over 4096 tiles of 32 x 128
+    outputs with 128 terms each: operands of random sign with exponents over 52 and 32 binades, about 1/16
+    zeros, every product a normal float or zero. Bit-exact: a failure names the first differing output."""
+    if not LIB.exists():
+        pytest.fail(f"{LIB} is not built (run __graft_entry__.build())")
+    lib = C.CDLL(str(LIB))
+    lib.hkbs_check_device_seq_gemm.restype = C.c_int
+    out = (C.c_uint * 4)()
+    print("device seq_gemm_mfma: 4096 tiles of 32 x 128 x 128", flush=True)
+    assert lib.hkbs_check_device_seq_gemm(4096, out) == 0
+    assert out[0] == 0, f"{out[0]} sums differ (first: tile {out[1]}, row {out[2] // 128}, col {out[2] % 128})"
