@@ -645,8 +645,9 @@ def main() -> int:
             "unit": "TFLOP/s",
             "frac": round(f_enc / (float(ph[0]) * 1e-3) / 1e12 / PEAK_FP32_TFLOPS, 4),
             "note": ("featurise + encode, F_enc = S*128*8768 + 786432*L FLOP per backbone; in fp32 the "
-                     "encoder keeps the reference's rounding sequence (separate multiply and add on the "
-                     "VALU, ceiling peak/4) and in the 16-bit modes runs on the fp16 MFMA"),
+                     "encoder keeps the reference's rounding sequence (each product rounded once on the "
+                     "fp32 MFMA with a zero addend, then one VALU add per product in k order) and in the "
+                     "16-bit modes runs on the fp16 MFMA"),
         },
     }
     if "C2" in cpu:
