@@ -446,8 +446,6 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(ModelDev m, DecodeArgs
   using GDa = Gemv<kH, 2 * kH, 1, PREC>;
   // G: steps this workgroup can hold in a pass (decode_group(PREC, team size))
   static_assert(G == decode_group(PREC, 1) || G == decode_group(PREC, 2), "group size of this mode");
-  // message rows of two members as fp16 pairs: [member][hi, lo][row][kLdH]
-  __shared__ __attribute__((aligned(16))) _Float16 G16[2 * 2 * kKmax * kLdH];
   // 16-bit modes: staging of the MFMA products (below). fp32: the products'
   // partial sums [member][group][output] (2048 floats per member); with more
   // members than kGroup they share G16's space: the message rows and the partial
@@ -455,6 +453,10 @@ __global__ __launch_bounds__(kThreads) void decode_kernel(ModelDev m, DecodeArgs
   // from its W3 partial sums, and the fused next-layer sums from the next
   // layer's message rows).
   constexpr bool kPartInG16 = !M16 && G > kGroup;
+  // message rows of two members as fp16 pairs: [member][hi, lo][row][kLdH]
+  // (larger when it also holds the partial sums of more members)
+  constexpr int kG16 = kPartInG16 && 2 * 2048 * G > 2 * 2 * kKmax * kLdH ? 2 * 2048 * G : 2 * 2 * kKmax * kLdH;
+  __shared__ __attribute__((aligned(16))) _Float16 G16[kG16];
   constexpr int kPart = M16 ? G * kFF + (6 * G * kH + 2 * G * kFF) / 2 : kPartInG16 ? 1 : 2048 * G;
   __shared__ __attribute__((aligned(16))) float part16[kPart];
   float* const part = kPartInG16 ? reinterpret_cast<float*>(G16) : part16;
