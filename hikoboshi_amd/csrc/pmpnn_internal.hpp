@@ -189,14 +189,15 @@ struct DecodeArgs {
   _Float16* Rh;           // [B][3][L][128]
 };
 // Steps one workgroup decodes in a pass, for DecodeArgs.precision and the team
-// size (workgroups per sequence): 8 in fp32 (0) with one workgroup per sequence,
-// where this capacity rather than the depth of the step graph bounds the passes
-// (one wave per member; the partial sums of 8 members fill the message rows'
-// LDS); 6 in the split bf16 mode (3), whose layer products run on the MFMA with
-// the members as rows of a 16-row operand, so that more members cost no more
-// product time; 4 otherwise. Team size 1 gives the largest value of a mode.
+// size (workgroups per sequence): 8 in fp32 (0), where with one workgroup per
+// sequence, or with long chains, this capacity rather than the depth of the step
+// graph bounds the passes (one wave per member; the partial sums of 8 members
+// fill the message rows' LDS); 6 in the split bf16 mode (3), whose layer
+// products run on the MFMA with the members as rows of a 16-row operand, so that
+// more members cost no more product time; 4 otherwise. Team size 1 gives the
+// largest value of a mode.
 constexpr int decode_group(int precision, int team) {
-  return precision == 0 && team == 1 ? 8 : precision == 3 ? 6 : 4;
+  return precision == 0 ? 8 : precision == 3 ? 6 : 4;
 }
 // int32 words of DecodeArgs.sched_tmp for nq orders of length L with K neighbours.
 inline size_t sched_scratch_words(size_t L, size_t K, size_t nq) { return nq * (3 * L + 1 + 4 + L * K); }
